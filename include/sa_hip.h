@@ -1,0 +1,53 @@
+/*
+ * sa_hip.h - C ABI of libsa_hip.so, the MI355X (gfx950) kernel layer of
+ * selective-attention.
+ *
+ * Conventions (all entry points):
+ *   - plain device pointers, int sizes, no torch types; tensors are dense
+ *     row-major (contiguous) in the shapes documented per function;
+ *   - dtype codes: 0 = float32, 1 = bfloat16 (activations); states, A and
+ *     delta_bias are always float32;
+ *   - `stream` is a hipStream_t (passed as void*); every launch is
+ *     asynchronous on it, nothing synchronises the host;
+ *   - return 0 on success, 1 for an argument error, 2 for a HIP launch
+ *     error; the message is in sa_last_error() (thread-local).  No C++
+ *     exception crosses the ABI;
+ *   - the library allocates no device memory: outputs and workspaces are
+ *     passed in by the caller (the Python layer takes them from torch's
+ *     caching allocator).
+ */
+#ifndef SA_HIP_H_
+#define SA_HIP_H_
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library version (incremented on ABI changes). */
+int sa_version(void);
+
+/* Message of the last failing call on this thread. */
+const char* sa_last_error(void);
+
+/*
+ * Single-step selective state update, in place on the fp32 state.
+ * Replaces ssu_forward (reference triton_kernels/ssu/forward.py:7-63,
+ * kernel ssu/forward_kernel.py:6-79), called by SSUFn.forward
+ * (ops/ssu.py:8-63).
+ *   u (b,H,P), B,C (b,G,N), delta_raw (b,H): dtype `dtype`
+ *   A (H,), delta_bias (H,) or NULL: float32
+ *   h (b,H,P,N) float32, read and overwritten
+ *   y (b,H,P): dtype `dtype`
+ *   dt = clamp(softplus20(delta_raw + bias), delta_min, delta_max)
+ *   h = h*exp(A*dt) + dt*u (x) B ;  y = h . C
+ */
+int sa_ssu_fwd(int dtype, const void* u, const float* A, const void* B, const void* C,
+               const void* delta_raw, const float* delta_bias, float* h, void* y, int batch,
+               int num_heads, int head_dim, int num_groups, int state_dim, int use_softplus,
+               float delta_min, float delta_max, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SA_HIP_H_ */

@@ -1,0 +1,196 @@
+// Shared device helpers for the gfx950 kernels of the selective-attention
+// kernel layer: dtype handling, MFMA wave tiles, wave/block reductions and
+// the reference's softplus.  Written for CDNA4 (wave64, 16x16 MFMA tiles).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sa {
+
+// ---------------------------------------------------------------------------
+// dtypes
+// ---------------------------------------------------------------------------
+enum DType : int { kF32 = 0, kBF16 = 1 };
+
+struct bf16 {  // raw bfloat16 bits; arithmetic always happens in fp32
+  uint16_t x;
+};
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16 v) {
+  return __uint_as_float(static_cast<uint32_t>(v.x) << 16);
+}
+
+// round-to-nearest-even fp32 -> bf16 (NaN stays NaN)
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+template <typename T> struct Conv;
+template <> struct Conv<float> {
+  __device__ __forceinline__ static float from(float v) { return v; }
+};
+template <> struct Conv<bf16> {
+  __device__ __forceinline__ static bf16 from(float v) { return bf16{f32_to_bf16_bits(v)}; }
+};
+template <typename T> __device__ __forceinline__ T from_f32(float v) { return Conv<T>::from(v); }
+
+template <typename T> __device__ __forceinline__ float ld(const T* p) { return to_f32(*p); }
+template <typename T> __device__ __forceinline__ void st(T* p, float v) { *p = from_f32<T>(v); }
+
+// ---------------------------------------------------------------------------
+// reference softplus: log(exp(z) + 1) for z <= 20, identity above
+// (triton_kernels/softplus.py:8, forward_kernel.py:77).  Accurate libm calls:
+// the +1 rounding dominates and must match the fp32 reference bit-for-bit in
+// spirit, so no fast-math intrinsics here.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float softplus20(float z) {
+  return z <= 20.0f ? logf(expf(z) + 1.0f) : z;
+}
+
+__device__ __forceinline__ float sigmoidf_acc(float z) { return 1.0f / (1.0f + expf(-z)); }
+
+// dt = clamp(softplus(z)) -- shared by the chunk cumsum and the state update
+__device__ __forceinline__ float make_dt(float z, bool softplus, float dmin, float dmax) {
+  float d = softplus ? softplus20(z) : z;
+  return fminf(fmaxf(d, dmin), dmax);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA traits.  MT is the matrix-core operand type: float (IEEE fp32 products,
+// v_mfma_f32_16x16x4_f32) or bf16 (v_mfma_f32_16x16x32_bf16, gfx950).
+//
+// Operands live in LDS "k-contiguous": A as [m][k] rows, B as [n][k] rows.
+// Lane l supplies row (l & 15) of A / column (l & 15) of B and KPL
+// consecutive k values starting at KPL * (l >> 4).  A and B use the same
+// (lane, slot) -> k assignment, so the product is exact whatever order the
+// hardware sums k in.  The 16x16 fp32 result: lane l holds rows
+// 4 * (l >> 4) + i (i = 0..3) of column (l & 15).
+// ---------------------------------------------------------------------------
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef uint16_t v8u16 __attribute__((ext_vector_type(8)));
+
+template <typename MT> struct Mfma;
+
+template <> struct Mfma<float> {
+  static constexpr int KSTEP = 16;  // k per call (4 MFMA issues of k=4)
+  __device__ __forceinline__ static v4f mma(const float* A, int lda, const float* B, int ldb,
+                                            v4f c, int lane) {
+    const float* a = A + (lane & 15) * lda + (lane >> 4);
+    const float* b = B + (lane & 15) * ldb + (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[4 * s], b[4 * s], c, 0, 0, 0);
+    return c;
+  }
+};
+
+template <> struct Mfma<bf16> {
+  static constexpr int KSTEP = 32;
+  __device__ __forceinline__ static v4f mma(const bf16* A, int lda, const bf16* B, int ldb, v4f c,
+                                            int lane) {
+    const v8bf a = *reinterpret_cast<const v8bf*>(A + (lane & 15) * lda + 8 * (lane >> 4));
+    const v8bf b = *reinterpret_cast<const v8bf*>(B + (lane & 15) * ldb + 8 * (lane >> 4));
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+// A wave computes a (16*TM) x (16*TN) fp32 tile:
+//   acc[i][j] += A[16i.., 0:K] * B[16j.., 0:K]^T
+// A: LDS [rows][lda], B: LDS [cols][ldb], both k-contiguous; K % KSTEP == 0.
+template <typename MT, int TM, int TN>
+__device__ __forceinline__ void wave_mma(v4f (&acc)[TM][TN], const MT* A, int lda, const MT* B,
+                                         int ldb, int K, int lane) {
+  for (int k = 0; k < K; k += Mfma<MT>::KSTEP) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = Mfma<MT>::mma(A + 16 * i * lda + k, lda, B + 16 * j * ldb + k, ldb, acc[i][j],
+                                  lane);
+  }
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void zero_acc(v4f (&acc)[TM][TN]) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+}
+
+// row / column of element r (0..3) of a 16x16 result fragment held by `lane`
+__device__ __forceinline__ int frag_row(int lane, int r) { return 4 * (lane >> 4) + r; }
+__device__ __forceinline__ int frag_col(int lane) { return lane & 15; }
+
+// padded LDS row length (elements) for a k extent: keeps 16-byte alignment and
+// shifts consecutive rows across banks
+template <typename MT> __host__ __device__ constexpr int lds_ld(int k) {
+  return k + (sizeof(MT) == 2 ? 8 : 4);
+}
+
+// ---------------------------------------------------------------------------
+// wave / block reductions and scans (wave64)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+// inclusive prefix sum across the 64 lanes of a wave
+__device__ __forceinline__ float wave_incl_scan(float v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    float t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// XCD-aware block order.  Workgroups are dealt round-robin over the 8 XCDs;
+// remapping gives each XCD a contiguous range of logical tiles so that tiles
+// sharing operands (e.g. heads of one group) share an L2.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int xcd_swizzle(int bid, int nblocks) {
+  constexpr int kXcd = 8;
+  int per = nblocks / kXcd;
+  int rem = nblocks - per * kXcd;
+  int xcd = bid % kXcd;
+  int slot = bid / kXcd;
+  if (slot >= per) return bid;  // tail blocks keep their id (only when nblocks % 8 != 0)
+  (void)rem;
+  return xcd * per + slot;
+}
+
+}  // namespace sa
+
+// host-side error plumbing shared by every entry point (defined in abi.cpp)
+extern "C" void sa_set_error(const char* fmt, ...);
+
+#define SA_CHECK_ARG(cond, ...)        \
+  do {                                 \
+    if (!(cond)) {                     \
+      sa_set_error(__VA_ARGS__);       \
+      return 1;                        \
+    }                                  \
+  } while (0)
+
+#define SA_CHECK_LAUNCH(what)                                                        \
+  do {                                                                               \
+    hipError_t e_ = hipGetLastError();                                               \
+    if (e_ != hipSuccess) {                                                          \
+      sa_set_error("%s: launch failed: %s", what, hipGetErrorString(e_));            \
+      return 2;                                                                      \
+    }                                                                                \
+  } while (0)

@@ -1,0 +1,143 @@
+// Single-step selective state update (decode), gfx950.
+//
+//   dt = clamp(softplus20(delta_raw + bias))
+//   h  <- h * exp(A * dt) + dt * u (x) B          (in place, fp32 state)
+//   y  = h . C                                     (dtype of u)
+//
+// Replaces ssu_forward / ssu_forward_kernel
+// (triton_kernels/ssu/forward.py:7-63, ssu/forward_kernel.py:6-79).
+//
+// Pure HBM stream: the state (b, H, P, N) fp32 is read and written once.  A
+// row (b, h, p) of N states is owned by ROW_LANES lanes, each holding float4
+// strips; ROWS rows per thread are issued back to back for memory-level
+// parallelism.  y is a segmented lane reduction (xor shuffles inside the row
+// group).
+#include "common.h"
+
+namespace sa {
+
+template <typename T, int ROW_LANES, int ROWS>
+__global__ __launch_bounds__(256) void ssu_fwd_kernel(
+    const T* __restrict__ u, const float* __restrict__ A, const T* __restrict__ Bm,
+    const T* __restrict__ Cm, const T* __restrict__ delta_raw, const float* __restrict__ delta_bias,
+    float* __restrict__ h, T* __restrict__ y, int batch, int H, int P, int G, int N, int softplus,
+    float dmin, float dmax, int vec4) {
+  constexpr int kRowsPerBlock = (256 / ROW_LANES) * ROWS;
+  const int lane_in_row = threadIdx.x % ROW_LANES;
+  const int row_slot = threadIdx.x / ROW_LANES;  // 0 .. 256/ROW_LANES-1
+  const long total_rows = static_cast<long>(batch) * H * P;
+  const int hpg = H / G;
+
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    const long row = static_cast<long>(blockIdx.x) * kRowsPerBlock + r * (256 / ROW_LANES) + row_slot;
+    // rows beyond the end still take part in the shuffles below (with zeros)
+    const bool valid = row < total_rows;
+    const long rr = valid ? row : 0;
+    const int p = static_cast<int>(rr % P);
+    const long bh = rr / P;
+    const int hh = static_cast<int>(bh % H);
+    const int bb = static_cast<int>(bh / H);
+    const int g = hh / hpg;
+
+    float z = ld(delta_raw + static_cast<long>(bb) * H + hh);
+    if (delta_bias) z += delta_bias[hh];
+    const float dt = make_dt(z, softplus != 0, dmin, dmax);
+    const float decay = expf(A[hh] * dt);
+    const float du = dt * ld(u + (static_cast<long>(bb) * H + hh) * P + p);
+
+    const T* Brow = Bm + (static_cast<long>(bb) * G + g) * N;
+    const T* Crow = Cm + (static_cast<long>(bb) * G + g) * N;
+    float* hrow = h + rr * N;
+
+    float part = 0.f;
+    if (vec4) {
+      for (int n = 4 * lane_in_row; n < N; n += 4 * ROW_LANES) {
+        if (!valid) break;
+        float4 hv = *reinterpret_cast<float4*>(hrow + n);
+        float b0 = ld(Brow + n), b1 = ld(Brow + n + 1), b2 = ld(Brow + n + 2), b3 = ld(Brow + n + 3);
+        float c0 = ld(Crow + n), c1 = ld(Crow + n + 1), c2 = ld(Crow + n + 2), c3 = ld(Crow + n + 3);
+        hv.x = hv.x * decay + du * b0;
+        hv.y = hv.y * decay + du * b1;
+        hv.z = hv.z * decay + du * b2;
+        hv.w = hv.w * decay + du * b3;
+        *reinterpret_cast<float4*>(hrow + n) = hv;
+        part += hv.x * c0 + hv.y * c1 + hv.z * c2 + hv.w * c3;
+      }
+    } else {
+      for (int n = lane_in_row; n < N; n += ROW_LANES) {
+        if (!valid) break;
+        float hv = hrow[n] * decay + du * ld(Brow + n);
+        hrow[n] = hv;
+        part += hv * ld(Crow + n);
+      }
+    }
+#pragma unroll
+    for (int o = ROW_LANES / 2; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+    if (valid && lane_in_row == 0) st(y + rr, part);
+  }
+}
+
+template <typename T, int ROW_LANES>
+static int launch_ssu(const void* u, const float* A, const void* B, const void* C,
+                      const void* delta_raw, const float* delta_bias, float* h, void* y, int batch,
+                      int H, int P, int G, int N, int softplus, float dmin, float dmax,
+                      hipStream_t stream) {
+  constexpr int ROWS = 2;
+  constexpr int kRowsPerBlock = (256 / ROW_LANES) * ROWS;
+  const long total_rows = static_cast<long>(batch) * H * P;
+  const long blocks = (total_rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  if (blocks == 0) return 0;
+  hipLaunchKernelGGL((ssu_fwd_kernel<T, ROW_LANES, ROWS>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(256), 0, stream, static_cast<const T*>(u), A, static_cast<const T*>(B),
+                     static_cast<const T*>(C), static_cast<const T*>(delta_raw), delta_bias, h,
+                     static_cast<T*>(y), batch, H, P, G, N, softplus, dmin, dmax,
+                     (N % 4 == 0 && (reinterpret_cast<uintptr_t>(h) & 15) == 0) ? 1 : 0);
+  SA_CHECK_LAUNCH("ssu_fwd");
+  return 0;
+}
+
+template <typename T>
+static int dispatch_ssu(const void* u, const float* A, const void* B, const void* C,
+                        const void* delta_raw, const float* delta_bias, float* h, void* y,
+                        int batch, int H, int P, int G, int N, int softplus, float dmin,
+                        float dmax, hipStream_t stream) {
+  // lanes per state row: enough float4 strips to cover N once, at most 64
+  const bool vec4 = N % 4 == 0 && (reinterpret_cast<uintptr_t>(h) & 15) == 0;
+  const int strips = vec4 ? N / 4 : N;
+  if (strips <= 8)
+    return launch_ssu<T, 8>(u, A, B, C, delta_raw, delta_bias, h, y, batch, H, P, G, N, softplus,
+                            dmin, dmax, stream);
+  if (strips <= 16)
+    return launch_ssu<T, 16>(u, A, B, C, delta_raw, delta_bias, h, y, batch, H, P, G, N, softplus,
+                             dmin, dmax, stream);
+  if (strips <= 32)
+    return launch_ssu<T, 32>(u, A, B, C, delta_raw, delta_bias, h, y, batch, H, P, G, N, softplus,
+                             dmin, dmax, stream);
+  return launch_ssu<T, 64>(u, A, B, C, delta_raw, delta_bias, h, y, batch, H, P, G, N, softplus,
+                           dmin, dmax, stream);
+}
+
+}  // namespace sa
+
+extern "C" int sa_ssu_fwd(int dtype, const void* u, const float* A, const void* B, const void* C,
+                          const void* delta_raw, const float* delta_bias, float* h, void* y,
+                          int batch, int num_heads, int head_dim, int num_groups, int state_dim,
+                          int use_softplus, float delta_min, float delta_max, void* stream) {
+  SA_CHECK_ARG(batch >= 0 && num_heads > 0 && head_dim > 0 && num_groups > 0 && state_dim > 0,
+               "sa_ssu_fwd: bad sizes b=%d H=%d P=%d G=%d N=%d", batch, num_heads, head_dim,
+               num_groups, state_dim);
+  SA_CHECK_ARG(num_heads % num_groups == 0, "sa_ssu_fwd: num_heads %% num_groups != 0");
+  SA_CHECK_ARG(u && A && B && C && delta_raw && h && y, "sa_ssu_fwd: null tensor pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == sa::kF32)
+    return sa::dispatch_ssu<float>(u, A, B, C, delta_raw, delta_bias, h, y, batch, num_heads,
+                                   head_dim, num_groups, state_dim, use_softplus, delta_min,
+                                   delta_max, s);
+  if (dtype == sa::kBF16)
+    return sa::dispatch_ssu<sa::bf16>(u, A, B, C, delta_raw, delta_bias, h, y, batch, num_heads,
+                                      head_dim, num_groups, state_dim, use_softplus, delta_min,
+                                      delta_max, s);
+  sa_set_error("sa_ssu_fwd: unsupported dtype %d", dtype);
+  return 1;
+}
