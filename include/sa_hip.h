@@ -19,6 +19,8 @@
 #ifndef SA_HIP_H_
 #define SA_HIP_H_
 
+#include <stdint.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -45,6 +47,26 @@ int sa_ssu_fwd(int dtype, const void* u, const float* A, const void* B, const vo
                const void* delta_raw, const float* delta_bias, float* h, void* y, int batch,
                int num_heads, int head_dim, int num_groups, int state_dim, int use_softplus,
                float delta_min, float delta_max, void* stream);
+
+/*
+ * SSD chunked scan, forward.  Replaces ssd_scan_forward (reference
+ * triton_kernels/ssd_scan/forward.py:223-276: chunk_cumsum_forward :14,
+ * chunk_state_forward :62, state_passing_forward :102, bmm_chunk_forward
+ * :139, chunk_scan_forward :175), called by SSDScanFn.forward
+ * (ops/ssd_scan.py:70-73).
+ *   u (b,L,H,P), B,C (b,L,G,N), delta_raw (b,L,H): dtype `dtype`
+ *   A (H,), delta_bias (H,) or NULL, h_init (b,H,P,N) or NULL: float32
+ *   length (b,) int64 (clamped to [0, L]); chunk_size in [1, 1024]; N <= 256
+ * Outputs (float32): y (b,L,H,P), h_last (b,H,P,N), and the intermediates the
+ * backward consumes: dt, dc (b,H,nc,Lc) and states (b,nc,H,P,N), which holds
+ * the state entering each chunk on return (nc = ceil(L/Lc)).
+ */
+int sa_ssd_fwd(int dtype, const void* u, const float* A, const void* B, const void* C,
+               const void* delta_raw, const float* delta_bias, const float* h_init,
+               const int64_t* length, int batch, int seqlen, int num_heads, int head_dim,
+               int num_groups, int state_dim, int chunk_size, int use_softplus, float delta_min,
+               float delta_max, float* y, float* h_last, float* dt, float* dc, float* states,
+               void* stream);
 
 #ifdef __cplusplus
 }

@@ -39,7 +39,7 @@ template <> struct Conv<bf16> {
 };
 template <typename T> __device__ __forceinline__ T from_f32(float v) { return Conv<T>::from(v); }
 
-template <typename T> __device__ __forceinline__ float ld(const T* p) { return to_f32(*p); }
+template <typename T> __device__ __forceinline__ float load_f32(const T* p) { return to_f32(*p); }
 template <typename T> __device__ __forceinline__ void st(T* p, float v) { *p = from_f32<T>(v); }
 
 // ---------------------------------------------------------------------------

@@ -1,0 +1,48 @@
+// Shapes and shared launch helpers of the SSD chunked scan kernels.
+#pragma once
+
+#include "common.h"
+#include "tile.h"
+
+namespace sa {
+
+struct SsdDims {
+  int b, L, H, P, G, N, Lc, nc;
+};
+
+// effective sequence length of batch row b: clamp(length[b], 0, L)
+__device__ __forceinline__ int seq_limit(const int64_t* length, int b, int L) {
+  long v = length[b];
+  return static_cast<int>(v < 0 ? 0 : (v > L ? L : v));
+}
+// positions of chunk c inside the length (may be <= 0)
+__device__ __forceinline__ int chunk_limit(int len, int c, int Lc) {
+  return min(Lc, len - c * Lc);
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+inline int make_dims(int b, int L, int H, int P, int G, int N, int Lc, SsdDims* d,
+                     const char* who) {
+  SA_CHECK_ARG(b >= 0 && L >= 0 && H > 0 && P > 0 && G > 0 && N > 0,
+               "%s: bad sizes b=%d L=%d H=%d P=%d G=%d N=%d", who, b, L, H, P, G, N);
+  SA_CHECK_ARG(H % G == 0, "%s: num_heads (%d) %% num_groups (%d) != 0", who, H, G);
+  SA_CHECK_ARG(Lc >= 1 && Lc <= 1024, "%s: chunk_size %d outside [1, 1024]", who, Lc);
+  SA_CHECK_ARG(N <= 256, "%s: state_dim %d > 256 is not supported", who, N);
+  d->b = b; d->L = L; d->H = H; d->P = P; d->G = G; d->N = N; d->Lc = Lc;
+  d->nc = (L + Lc - 1) / Lc;
+  return 0;
+}
+
+// launchers shared between the forward and backward translation units
+template <typename T>
+int launch_chunk_cumsum(const void* delta_raw, const float* A, const float* bias,
+                        const int64_t* length, float* dt, float* dc, const SsdDims& d, int sp,
+                        float lo, float hi, hipStream_t s);
+
+// MODE 0: chunk states from (u, B); MODE 1: dH_intra from (dy, C)
+template <typename MT, typename TA, typename TB, int MODE>
+int launch_chunk_outer(const void* a, const void* b, const float* dt, const float* dc,
+                       const int64_t* length, float* out, const SsdDims& d, hipStream_t s);
+
+}  // namespace sa

@@ -1,0 +1,437 @@
+// SSD chunked scan, forward pass (gfx950).
+//
+// Replaces ssd_scan_forward (reference triton_kernels/ssd_scan/forward.py:223-276)
+// and its five Triton kernels with four HIP kernels:
+//
+//   chunk_cumsum    dt = clamp(softplus20(delta_raw+bias)), 0 at t >= length;
+//                   dc = inclusive cumsum over the chunk of dt*A
+//                   (forward_kernel.py:20-87)
+//   chunk_outer     S_c[p,n] = sum_tau u[tau,p] w_tau B[tau,n],
+//                   w_tau = exp(min(dc_last-dc_tau,0)) dt_tau   (forward_kernel.py:108-185)
+//                   -- the same kernel computes the backward's dH_intra with
+//                   (dy, exp(dc) [tau<lim], C) in place of (u, w, B)
+//   state_passing   H_in[0] = h_init | 0, H_in[c+1] = exp(dc_last[c]) H_in[c] + S_c,
+//                   in place over the chunk-state buffer (forward_kernel.py:203-250)
+//   chunk_scan      y = exp(dc) C.H_in^T + (tril(C.B^T) o decay o dt) . u
+//                   (forward_kernel.py:351-455); the C.B^T tile is recomputed
+//                   per (tau-tile, sigma-tile) on the matrix cores instead of
+//                   materialising CB (bmm_chunk_forward, :271-328) in HBM.
+//
+// Layouts (all row-major, contiguous):
+//   u (b,L,H,P)  B,C (b,L,G,N)  delta_raw (b,L,H)  [activations: fp32 | bf16]
+//   dt, dc (b,H,nc,Lc) fp32   states (b,nc,H,P,N) fp32   y (b,L,H,P) fp32
+#include "ssd_common.h"
+
+namespace sa {
+
+// ---------------------------------------------------------------------------
+// chunk cumsum: one block per (b, c, h); each thread owns up to Lc/256
+// consecutive positions, the block adds the per-thread totals in a scan.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void chunk_cumsum_kernel(
+    const T* __restrict__ delta_raw, const float* __restrict__ A,
+    const float* __restrict__ delta_bias, const int64_t* __restrict__ length,
+    float* __restrict__ dt_out, float* __restrict__ dc_out, SsdDims d, int softplus, float dmin,
+    float dmax) {
+  __shared__ float wave_tot[4];
+  const int h = blockIdx.x % d.H;
+  const int c = (blockIdx.x / d.H) % d.nc;
+  const int b = blockIdx.x / (d.H * d.nc);
+  const int len = seq_limit(length, b, d.L);
+  const int lim = chunk_limit(len, c, d.Lc);
+  const float a = A[h];
+  const float bias = delta_bias ? delta_bias[h] : 0.0f;
+  const int per = (d.Lc + 255) / 256;  // positions per thread (<= 4)
+  const int t0 = threadIdx.x * per;
+  float v[4];
+  float run = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[j] = 0.0f;
+    const int tau = t0 + j;
+    if (j < per && tau < lim) {
+      const long t = static_cast<long>(c) * d.Lc + tau;
+      const float z = load_f32(delta_raw + (static_cast<long>(b) * d.L + t) * d.H + h) + bias;
+      v[j] = make_dt(z, softplus != 0, dmin, dmax);
+    }
+  }
+  float part[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    run += v[j] * a;
+    part[j] = run;
+  }
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  float incl = wave_incl_scan(run, lane);
+  if (lane == 63) wave_tot[wid] = incl;
+  __syncthreads();
+  float base = incl - run;
+  for (int w = 0; w < wid; ++w) base += wave_tot[w];
+  const long row = ((static_cast<long>(b) * d.H + h) * d.nc + c) * d.Lc;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int tau = t0 + j;
+    if (j < per && tau < d.Lc) {
+      dt_out[row + tau] = v[j];
+      dc_out[row + tau] = base + part[j];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// chunk outer product: out[(b,c,h)][p][n] = sum_tau a(tau,p) b(tau,n)
+//   MODE 0 (chunk state):  a = u * exp(min(dc_last-dc,0)) * dt,  b = B,  tau < seq end
+//   MODE 1 (dH_intra):     a = dy * exp(dc) [tau < lim],          b = C,  tau < lim
+// One 64x64 (p, n) tile per block, k = tau in steps of 32 through LDS.
+// ---------------------------------------------------------------------------
+template <typename MT, typename TA, typename TB, int MODE>
+__global__ __launch_bounds__(256) void chunk_outer_kernel(
+    const TA* __restrict__ a_src, const TB* __restrict__ b_src, const float* __restrict__ dt,
+    const float* __restrict__ dc, const int64_t* __restrict__ length, float* __restrict__ out,
+    SsdDims d, int vec_a, int vec_b) {
+  constexpr int KC = 32;
+  constexpr int LD = lds_ld<MT>(KC);
+  __shared__ __align__(16) MT As[64 * LD];
+  __shared__ __align__(16) MT Bs[64 * LD];
+  __shared__ float scl[1024];
+
+  const int ptiles = (d.P + 63) / 64, ntiles = (d.N + 63) / 64;
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int tile = bid % (ptiles * ntiles);
+  int rest = bid / (ptiles * ntiles);
+  const int h = rest % d.H;
+  rest /= d.H;
+  const int c = rest % d.nc;
+  const int b = rest / d.nc;
+  const int p0 = (tile / ntiles) * 64, n0 = (tile % ntiles) * 64;
+  const int g = h / (d.H / d.G);
+
+  const long crow = ((static_cast<long>(b) * d.H + h) * d.nc + c) * d.Lc;
+  const int len = seq_limit(length, b, d.L);
+  const int klim = MODE == 0 ? min(d.Lc, d.L - c * d.Lc) : max(0, chunk_limit(len, c, d.Lc));
+  // per-tau scale for the a operand
+  const float dc_last = dc[crow + d.Lc - 1];
+  for (int t = threadIdx.x; t < d.Lc; t += 256) {
+    float s;
+    if (MODE == 0) s = expf(fminf(dc_last - dc[crow + t], 0.0f)) * dt[crow + t];
+    else s = t < klim ? expf(dc[crow + t]) : 0.0f;
+    scl[t] = s;
+  }
+  __syncthreads();
+
+  const long tok0 = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc;
+  const TA* a_base = a_src + (tok0 * d.H + h) * d.P + p0;
+  const TB* b_base = b_src + (tok0 * d.G + g) * d.N + n0;
+  const long a_rs = static_cast<long>(d.H) * d.P, b_rs = static_cast<long>(d.G) * d.N;
+
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = (wid >> 1) * 32, wn = (wid & 1) * 32;
+  v4f acc[2][2];
+  zero_acc(acc);
+  for (int k0 = 0; k0 < klim; k0 += KC) {
+    const int kv = min(KC, klim - k0);
+    const float* sk = scl + k0;
+    stage_transposed<MT>(As, LD, a_base + k0 * a_rs, a_rs, KC, 64, kv, d.P - p0, vec_a != 0,
+                         [sk](int r, int) { return sk[r]; });
+    stage_transposed<MT>(Bs, LD, b_base + k0 * b_rs, b_rs, KC, 64, kv, d.N - n0, vec_b != 0,
+                         NoScale{});
+    __syncthreads();
+    wave_mma<MT, 2, 2>(acc, As + wm * LD, LD, Bs + wn * LD, LD, KC, lane);
+    __syncthreads();
+  }
+  float* o = out + (((static_cast<long>(b) * d.nc + c) * d.H + h) * d.P) * d.N;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int p = p0 + wm + 16 * i + frag_row(lane, r);
+        const int n = n0 + wn + 16 * j + frag_col(lane);
+        if (p < d.P && n < d.N) o[static_cast<long>(p) * d.N + n] = acc[i][j][r];
+      }
+}
+
+// ---------------------------------------------------------------------------
+// state passing (forward): sequential over chunks, parallel over (b, h, P*N).
+// Loads of a group of chunks are issued together before the dependent math.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void state_passing_fwd_kernel(
+    float* __restrict__ states, const float* __restrict__ h_init, float* __restrict__ h_last,
+    const float* __restrict__ dc, SsdDims d) {
+  const long PN = static_cast<long>(d.P) * d.N;
+  const int per_bh = static_cast<int>((PN + 1023) / 1024);
+  const int bh = blockIdx.x / per_bh;
+  const long e0 = (static_cast<long>(blockIdx.x % per_bh) * 256 + threadIdx.x) * 4;
+  const int h = bh % d.H, b = bh / d.H;
+  if (e0 >= PN) return;
+  const bool full = e0 + 4 <= PN && (PN % 4 == 0);
+  auto load4 = [&](const float* p, float (&v)[4]) {
+    if (full) {
+      float4 t = *reinterpret_cast<const float4*>(p);
+      v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    } else {
+      for (int j = 0; j < 4; ++j) v[j] = (e0 + j < PN) ? p[j] : 0.0f;
+    }
+  };
+  auto store4 = [&](float* p, const float (&v)[4]) {
+    if (full) {
+      *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      for (int j = 0; j < 4; ++j)
+        if (e0 + j < PN) p[j] = v[j];
+    }
+  };
+  float hv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (h_init) load4(h_init + static_cast<long>(bh) * PN + e0, hv);
+  const float* dcl = dc + static_cast<long>(bh) * d.nc * d.Lc + (d.Lc - 1);
+  constexpr int GRP = 8;
+  for (int c0 = 0; c0 < d.nc; c0 += GRP) {
+    float s[GRP][4];
+    const int cn = min(GRP, d.nc - c0);
+#pragma unroll
+    for (int j = 0; j < GRP; ++j)
+      if (j < cn) load4(states + ((static_cast<long>(b) * d.nc + c0 + j) * d.H + h) * PN + e0, s[j]);
+#pragma unroll
+    for (int j = 0; j < GRP; ++j) {
+      if (j < cn) {
+        float* dst = states + ((static_cast<long>(b) * d.nc + c0 + j) * d.H + h) * PN + e0;
+        store4(dst, hv);
+        const float sc = expf(dcl[static_cast<long>(c0 + j) * d.Lc]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) hv[q] = sc * hv[q] + s[j][q];
+      }
+    }
+  }
+  store4(h_last + static_cast<long>(bh) * PN + e0, hv);
+}
+
+// ---------------------------------------------------------------------------
+// chunk scan: one 64 (tau) x 64 (p) tile of y per block.
+//   y  = exp(dc_tau) * sum_n C[tau,n] H_in[p,n]
+//      + sum_{sigma <= tau} CB[tau,sigma] exp(min(dc_tau - dc_sigma, 0)) dt_sigma u[sigma,p]
+// CB tiles come from C (kept in LDS for the whole tau tile) and a staged
+// B sigma-tile.  NP = N rounded up to 32 (<= 256).
+// ---------------------------------------------------------------------------
+template <typename MT, typename T>
+__global__ __launch_bounds__(256) void chunk_scan_fwd_kernel(
+    const T* __restrict__ u, const T* __restrict__ Bm, const T* __restrict__ Cm,
+    const float* __restrict__ dt, const float* __restrict__ dc, const float* __restrict__ states,
+    float* __restrict__ y, SsdDims d, int vec_act, int vec_state) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int NP = round_up(d.N, 32);
+  const int LDN = lds_ld<MT>(NP);
+  constexpr int LD64 = lds_ld<MT>(64);
+  MT* Cs = reinterpret_cast<MT*>(smem_raw);          // [64][LDN]   C tau-tile
+  MT* Xs = Cs + 64 * LDN;                            // [64][LDN]   H_in p-tile, then B sigma-tile
+  MT* Ls = Xs + 64 * LDN;                            // [64][LD64]  masked, scaled CB tile
+  MT* Us = Ls + 64 * LD64;                           // [64][LD64]  u^T sigma-tile
+  float* dts = reinterpret_cast<float*>(Us + 64 * LD64);  // [Lc]
+  float* dcs = dts + d.Lc;                                // [Lc]
+
+  const int ttiles = (d.Lc + 63) / 64, ptiles = (d.P + 63) / 64;
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int tile = bid % (ttiles * ptiles);
+  int rest = bid / (ttiles * ptiles);
+  const int h = rest % d.H;
+  rest /= d.H;
+  const int c = rest % d.nc;
+  const int b = rest / d.nc;
+  const int t0 = (tile / ptiles) * 64, p0 = (tile % ptiles) * 64;
+  const int g = h / (d.H / d.G);
+  const int qlim = min(d.Lc, d.L - c * d.Lc);  // rows of this chunk inside the sequence
+  if (t0 >= qlim) return;
+
+  const long crow = ((static_cast<long>(b) * d.H + h) * d.nc + c) * d.Lc;
+  for (int t = threadIdx.x; t < d.Lc; t += 256) {
+    dts[t] = dt[crow + t];
+    dcs[t] = dc[crow + t];
+  }
+  const long tok0 = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc;
+  const long act_rs = static_cast<long>(d.G) * d.N;
+  const T* Cbase = Cm + (tok0 * d.G + g) * d.N;
+  const T* Bbase = Bm + (tok0 * d.G + g) * d.N;
+  const float* Hbase = states + (((static_cast<long>(b) * d.nc + c) * d.H + h) * d.P + p0) * d.N;
+  stage_rows<MT>(Cs, LDN, Cbase + static_cast<long>(t0) * act_rs, act_rs, 64, NP, qlim - t0, d.N,
+                 vec_act != 0, NoScale{});
+  stage_rows<MT>(Xs, LDN, Hbase, d.N, 64, NP, d.P - p0, d.N, vec_state != 0, NoScale{});
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = (wid >> 1) * 32, wn = (wid & 1) * 32;
+  v4f acc[2][2];
+  zero_acc(acc);
+  wave_mma<MT, 2, 2>(acc, Cs + wm * LDN, LDN, Xs + wn * LDN, LDN, NP, lane);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + wm + 16 * i + frag_row(lane, r);
+      const float e = t < d.Lc ? expf(dcs[t]) : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j][r] *= e;
+    }
+  __syncthreads();
+
+  const long u_rs = static_cast<long>(d.H) * d.P;
+  const T* ubase = u + (tok0 * d.H + h) * d.P + p0;
+  const int s_end = min(t0 + 64, qlim);
+  for (int s0 = 0; s0 < s_end; s0 += 64) {
+    const int sv = min(64, qlim - s0);
+    stage_rows<MT>(Xs, LDN, Bbase + static_cast<long>(s0) * act_rs, act_rs, 64, NP, sv, d.N,
+                   vec_act != 0, NoScale{});
+    stage_transposed<MT>(Us, LD64, ubase + static_cast<long>(s0) * u_rs, u_rs, 64, 64, sv,
+                         d.P - p0, vec_act != 0, NoScale{});
+    __syncthreads();
+    v4f cb[2][2];
+    zero_acc(cb);
+    wave_mma<MT, 2, 2>(cb, Cs + wm * LDN, LDN, Xs + wn * LDN, LDN, NP, lane);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tl = wm + 16 * i + frag_row(lane, r);
+          const int sl = wn + 16 * j + frag_col(lane);
+          const int t = t0 + tl, s = s0 + sl;
+          float v = 0.0f;
+          if (s <= t && s < qlim && t < d.Lc)
+            v = cb[i][j][r] * expf(fminf(dcs[t] - dcs[s], 0.0f)) * dts[s];
+          Ls[tl * LD64 + sl] = from_f32<MT>(v);
+        }
+    __syncthreads();
+    wave_mma<MT, 2, 2>(acc, Ls + wm * LD64, LD64, Us + wn * LD64, LD64, 64, lane);
+    __syncthreads();
+  }
+
+  float* ybase = y + (tok0 * d.H + h) * d.P;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + wm + 16 * i + frag_row(lane, r);
+        const int p = p0 + wn + 16 * j + frag_col(lane);
+        if (t < qlim && p < d.P) ybase[static_cast<long>(t) * u_rs + p] = acc[i][j][r];
+      }
+}
+
+size_t chunk_scan_smem(int N, int Lc, bool bf) {
+  const int NP = round_up(N, 32);
+  const size_t e = bf ? 2 : 4;
+  const int LDN = NP + (bf ? 8 : 4), LD64 = 64 + (bf ? 8 : 4);
+  return e * (2 * 64 * LDN + 2 * 64 * LD64) + 2 * sizeof(float) * Lc;
+}
+
+// ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
+template <typename T>
+int launch_chunk_cumsum(const void* delta_raw, const float* A, const float* bias,
+                        const int64_t* length, float* dt, float* dc, const SsdDims& d, int sp,
+                        float lo, float hi, hipStream_t s) {
+  const long blocks = static_cast<long>(d.b) * d.nc * d.H;
+  hipLaunchKernelGGL(chunk_cumsum_kernel<T>, dim3(blocks), dim3(256), 0, s,
+                     static_cast<const T*>(delta_raw), A, bias, length, dt, dc, d, sp, lo, hi);
+  SA_CHECK_LAUNCH("chunk_cumsum");
+  return 0;
+}
+
+template <typename MT, typename TA, typename TB, int MODE>
+int launch_chunk_outer(const void* a, const void* bsrc, const float* dt, const float* dc,
+                       const int64_t* length, float* out, const SsdDims& d, hipStream_t s) {
+  const long blocks = static_cast<long>((d.P + 63) / 64) * ((d.N + 63) / 64) * d.b * d.nc * d.H;
+  const int vec_a = aligned16(a) && (static_cast<long>(d.H) * d.P) % 8 == 0 && d.P % 8 == 0;
+  const int vec_b = aligned16(bsrc) && (static_cast<long>(d.G) * d.N) % 8 == 0 && d.N % 8 == 0;
+  hipLaunchKernelGGL((chunk_outer_kernel<MT, TA, TB, MODE>), dim3(blocks), dim3(256), 0, s,
+                     static_cast<const TA*>(a), static_cast<const TB*>(bsrc), dt, dc, length, out,
+                     d, vec_a, vec_b);
+  SA_CHECK_LAUNCH("chunk_outer");
+  return 0;
+}
+
+int launch_state_passing_fwd(float* states, const float* h_init, float* h_last, const float* dc,
+                             const SsdDims& d, hipStream_t s) {
+  const long PN = static_cast<long>(d.P) * d.N;
+  const long blocks = static_cast<long>(d.b) * d.H * ((PN + 1023) / 1024);
+  hipLaunchKernelGGL(state_passing_fwd_kernel, dim3(blocks), dim3(256), 0, s, states, h_init,
+                     h_last, dc, d);
+  SA_CHECK_LAUNCH("state_passing_fwd");
+  return 0;
+}
+
+template <typename MT, typename T>
+int launch_chunk_scan(const void* u, const void* B, const void* C, const float* dt,
+                      const float* dc, const float* states, float* y, const SsdDims& d,
+                      hipStream_t s) {
+  const long blocks = static_cast<long>((d.Lc + 63) / 64) * ((d.P + 63) / 64) * d.b * d.nc * d.H;
+  const size_t smem = chunk_scan_smem(d.N, d.Lc, sizeof(MT) == 2);
+  const int vec_act = aligned16(u) && aligned16(B) && aligned16(C) && d.P % 8 == 0 &&
+                      d.N % 8 == 0 && (static_cast<long>(d.H) * d.P) % 8 == 0;
+  const int vec_state = aligned16(states) && d.N % 8 == 0;
+  if (smem > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(chunk_scan_fwd_kernel<MT, T>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(smem));
+    SA_CHECK_ARG(e == hipSuccess, "chunk_scan_fwd: %zu B of LDS refused: %s", smem,
+                 hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL((chunk_scan_fwd_kernel<MT, T>), dim3(blocks), dim3(256), smem, s,
+                     static_cast<const T*>(u), static_cast<const T*>(B), static_cast<const T*>(C),
+                     dt, dc, states, y, d, vec_act, vec_state);
+  SA_CHECK_LAUNCH("chunk_scan_fwd");
+  return 0;
+}
+
+template <typename T, typename MT>
+int ssd_fwd_impl(const void* u, const float* A, const void* B, const void* C,
+                 const void* delta_raw, const float* bias, const float* h_init,
+                 const int64_t* length, const SsdDims& d, int sp, float lo, float hi, float* y,
+                 float* h_last, float* dt, float* dc, float* states, hipStream_t s) {
+  int rc;
+  if ((rc = launch_chunk_cumsum<T>(delta_raw, A, bias, length, dt, dc, d, sp, lo, hi, s))) return rc;
+  if ((rc = launch_chunk_outer<MT, T, T, 0>(u, B, dt, dc, length, states, d, s))) return rc;
+  if ((rc = launch_state_passing_fwd(states, h_init, h_last, dc, d, s))) return rc;
+  return launch_chunk_scan<MT, T>(u, B, C, dt, dc, states, y, d, s);
+}
+
+template int launch_chunk_outer<float, float, float, 1>(const void*, const void*, const float*,
+                                                        const float*, const int64_t*, float*,
+                                                        const SsdDims&, hipStream_t);
+template int launch_chunk_outer<bf16, float, bf16, 1>(const void*, const void*, const float*,
+                                                      const float*, const int64_t*, float*,
+                                                      const SsdDims&, hipStream_t);
+template int launch_chunk_outer<bf16, bf16, bf16, 1>(const void*, const void*, const float*,
+                                                     const float*, const int64_t*, float*,
+                                                     const SsdDims&, hipStream_t);
+
+}  // namespace sa
+
+extern "C" int sa_ssd_fwd(int dtype, const void* u, const float* A, const void* B, const void* C,
+                          const void* delta_raw, const float* delta_bias, const float* h_init,
+                          const int64_t* length, int batch, int seqlen, int num_heads,
+                          int head_dim, int num_groups, int state_dim, int chunk_size,
+                          int use_softplus, float delta_min, float delta_max, float* y,
+                          float* h_last, float* dt, float* dc, float* states, void* stream) {
+  sa::SsdDims d;
+  int rc = sa::make_dims(batch, seqlen, num_heads, head_dim, num_groups, state_dim, chunk_size, &d,
+                         "sa_ssd_fwd");
+  if (rc) return rc;
+  SA_CHECK_ARG(u && A && B && C && delta_raw && length && y && h_last && dt && dc && states,
+               "sa_ssd_fwd: null tensor pointer");
+  if (d.b == 0 || d.L == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == sa::kF32)
+    return sa::ssd_fwd_impl<float, float>(u, A, B, C, delta_raw, delta_bias, h_init, length, d,
+                                          use_softplus, delta_min, delta_max, y, h_last, dt, dc,
+                                          states, s);
+  if (dtype == sa::kBF16)
+    return sa::ssd_fwd_impl<sa::bf16, sa::bf16>(u, A, B, C, delta_raw, delta_bias, h_init, length,
+                                                d, use_softplus, delta_min, delta_max, y, h_last,
+                                                dt, dc, states, s);
+  sa_set_error("sa_ssd_fwd: unsupported dtype %d", dtype);
+  return 1;
+}

@@ -40,11 +40,11 @@ __global__ __launch_bounds__(256) void ssu_fwd_kernel(
     const int bb = static_cast<int>(bh / H);
     const int g = hh / hpg;
 
-    float z = ld(delta_raw + static_cast<long>(bb) * H + hh);
+    float z = load_f32(delta_raw + static_cast<long>(bb) * H + hh);
     if (delta_bias) z += delta_bias[hh];
     const float dt = make_dt(z, softplus != 0, dmin, dmax);
     const float decay = expf(A[hh] * dt);
-    const float du = dt * ld(u + (static_cast<long>(bb) * H + hh) * P + p);
+    const float du = dt * load_f32(u + (static_cast<long>(bb) * H + hh) * P + p);
 
     const T* Brow = Bm + (static_cast<long>(bb) * G + g) * N;
     const T* Crow = Cm + (static_cast<long>(bb) * G + g) * N;
@@ -55,8 +55,8 @@ __global__ __launch_bounds__(256) void ssu_fwd_kernel(
       for (int n = 4 * lane_in_row; n < N; n += 4 * ROW_LANES) {
         if (!valid) break;
         float4 hv = *reinterpret_cast<float4*>(hrow + n);
-        float b0 = ld(Brow + n), b1 = ld(Brow + n + 1), b2 = ld(Brow + n + 2), b3 = ld(Brow + n + 3);
-        float c0 = ld(Crow + n), c1 = ld(Crow + n + 1), c2 = ld(Crow + n + 2), c3 = ld(Crow + n + 3);
+        float b0 = load_f32(Brow + n), b1 = load_f32(Brow + n + 1), b2 = load_f32(Brow + n + 2), b3 = load_f32(Brow + n + 3);
+        float c0 = load_f32(Crow + n), c1 = load_f32(Crow + n + 1), c2 = load_f32(Crow + n + 2), c3 = load_f32(Crow + n + 3);
         hv.x = hv.x * decay + du * b0;
         hv.y = hv.y * decay + du * b1;
         hv.z = hv.z * decay + du * b2;
@@ -67,9 +67,9 @@ __global__ __launch_bounds__(256) void ssu_fwd_kernel(
     } else {
       for (int n = lane_in_row; n < N; n += ROW_LANES) {
         if (!valid) break;
-        float hv = hrow[n] * decay + du * ld(Brow + n);
+        float hv = hrow[n] * decay + du * load_f32(Brow + n);
         hrow[n] = hv;
-        part += hv * ld(Crow + n);
+        part += hv * load_f32(Crow + n);
       }
     }
 #pragma unroll

@@ -25,6 +25,9 @@ SIGNATURES: dict[str, list] = {
     "sa_version": [],
     "sa_last_error": [],
     "sa_ssu_fwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _f, _vp],
+    "sa_ssd_fwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                   _i, _i, _i, _i, _i, _i, _i, _i, _f, _f,
+                   _vp, _vp, _vp, _vp, _vp, _vp],
 }
 
 RESTYPES = {"sa_last_error": ctypes.c_char_p}

@@ -1,3 +1,4 @@
+from .ssd_scan import SSDScanFn
 from .ssu import SSUFn
 
-__all__ = ["SSUFn"]
+__all__ = ["SSDScanFn", "SSUFn"]

@@ -1,0 +1,150 @@
+"""SSD chunked scan forward: HIP kernels vs the fp64 CPU oracle."""
+import math
+
+import pytest
+import torch
+
+from oracle import ssd as ref
+from selective_attention import workloads
+from tests.helpers import assert_parity
+
+F64 = torch.float64
+
+
+def make_inputs(b=2, L=100, H=4, P=24, N=40, G=2, dtype=torch.float32, seed=0, with_h=True,
+                with_bias=True, lens=None):
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(b, L, H, P, generator=g).to(dtype)
+    A = -torch.exp(torch.rand(H, generator=g) * math.log(16.0))
+    B = (torch.randn(b, L, G, N, generator=g) / math.sqrt(N)).to(dtype)
+    C = (torch.randn(b, L, G, N, generator=g) / math.sqrt(N)).to(dtype)
+    dr = (torch.randn(b, L, H, generator=g) - 3.0).to(dtype)
+    bias = torch.randn(H, generator=g) * 0.3 if with_bias else None
+    h0 = torch.randn(b, H, P, N, generator=g) * 0.3 if with_h else None
+    length = None if lens is None else torch.tensor(lens, dtype=torch.int64)
+    return dict(u=u, A=A, B=B, C=C, delta_raw=dr, delta_bias=bias, h_init=h0, length=length)
+
+
+def to_dev(x):
+    return {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in x.items()}
+
+
+def run_fwd(x, chunk, **kw):
+    from selective_attention.ops import SSDScanFn
+    xd = to_dev(x)
+    y, h = SSDScanFn.apply(xd["u"], xd["A"], xd["B"], xd["C"], xd["delta_raw"], xd["delta_bias"],
+                           xd["h_init"], xd["length"], chunk, kw.get("softplus", True),
+                           kw.get("limit", (0.0, float("inf"))), True)
+    torch.cuda.synchronize()
+    return y, h
+
+
+FWD_CASES = [
+    ("aligned", dict(b=2, L=128, H=4, P=64, N=64, G=2), 64),
+    ("ragged", dict(b=2, L=100, H=4, P=24, N=40, G=2), 32),
+    ("lens", dict(b=3, L=150, H=2, P=16, N=16, G=1, lens=[150, 37, 0]), 64),
+    ("noinit", dict(b=1, L=70, H=6, P=32, N=24, G=3, with_h=False, with_bias=False), 16),
+    ("bigP", dict(b=1, L=96, H=2, P=130, N=136, G=1), 48),
+    ("chunk1", dict(b=1, L=9, H=2, P=8, N=8, G=2), 1),
+    ("chunk256", dict(b=1, L=300, H=2, P=64, N=128, G=1, lens=[281]), 256),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("name,shape,chunk", FWD_CASES, ids=[c[0] for c in FWD_CASES])
+def test_ssd_fwd_parity(dtype, name, shape, chunk):
+    print(f"ssd fwd {name} dtype={dtype} chunk={chunk}", flush=True)
+    x = make_inputs(dtype=dtype, **shape)
+    y_ref, h_ref = ref.ssd_scan_forward(**x, chunk_size=chunk)
+    y, h = run_fwd(x, chunk)
+    assert y.dtype == torch.float32 and h.dtype == torch.float32
+    assert_parity(y, y_ref, dtype, "y")
+    assert_parity(h, h_ref, dtype, "h_last")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("softplus,limit", [(False, (0.01, 0.2)), (True, (0.03, 0.08))])
+def test_ssd_fwd_limits(softplus, limit):
+    x = make_inputs(L=80, P=16, N=16, dtype=torch.float32)
+    x["delta_raw"] = x["delta_raw"] + 3.0 if not softplus else x["delta_raw"]
+    y_ref, h_ref = ref.ssd_scan_forward(**x, chunk_size=32, use_delta_softplus=softplus,
+                                        delta_limit=limit)
+    y, h = run_fwd(x, 32, softplus=softplus, limit=limit)
+    assert_parity(y, y_ref, torch.float32, "y")
+    assert_parity(h, h_ref, torch.float32, "h_last")
+
+
+@pytest.mark.gpu
+def test_ssd_fwd_intermediates():
+    """dt, dc and the chunk entry states against the oracle's."""
+    from selective_attention.kernels.ssd_scan import ssd_scan_forward
+    x = make_inputs(b=2, L=100, H=4, P=24, N=40, G=2, lens=[100, 61])
+    _, _, it = ref.ssd_scan_forward(**x, chunk_size=32, return_intermediates=True)
+    xd = to_dev(x)
+    _, _, (dt, dc, states) = ssd_scan_forward(
+        xd["u"], xd["A"], xd["B"], xd["C"], xd["delta_raw"], xd["delta_bias"], xd["h_init"],
+        xd["length"], 32, return_saved=True)
+    assert_parity(dt, it["dt"], torch.float32, "dt")
+    assert_parity(dc, it["dc"], torch.float32, "dc")
+    assert_parity(states, it["H_in"], torch.float32, "states")
+
+
+@pytest.mark.gpu
+def test_ssd_fwd_config0():
+    """BASELINE config 0 (fp32): y + D*x and the final state, rtol 1e-4."""
+    cfg = workloads.SSD_CONFIGS[0]
+    x = workloads.ssd_inputs(**cfg)
+    D = x.pop("D")
+    args = dict(u=x["u"], A=x["A"], B=x["B"], C=x["C"], delta_raw=x["delta_raw"],
+                delta_bias=None, h_init=None, length=None)
+    y_ref, h_ref = ref.ssd_scan_forward(**args, chunk_size=cfg["chunk"])
+    y, h = run_fwd(args, cfg["chunk"])
+    b, L, H, P = x["u"].shape
+    ytot_ref = y_ref.reshape(b, L, H * P) + D.double() * x["u"].double().reshape(b, L, H * P)
+    ytot = y.reshape(b, L, H * P) + D.cuda() * x["u"].cuda().reshape(b, L, H * P)
+    assert_parity(ytot, ytot_ref, torch.float32, "y+D*x")
+    assert_parity(h, h_ref, torch.float32, "h_last")
+
+
+@pytest.mark.gpu
+def test_ssd_fwd_config1_row():
+    """BASELINE config 1 shapes (bf16), first batch row against the fp64 oracle."""
+    cfg = dict(workloads.SSD_CONFIGS[1])
+    cfg["batch"] = 1
+    x = workloads.ssd_inputs(**cfg)
+    x.pop("D")
+    args = dict(u=x["u"], A=x["A"], B=x["B"], C=x["C"], delta_raw=x["delta_raw"],
+                delta_bias=None, h_init=None, length=None)
+    y_ref, h_ref = ref.ssd_scan_forward(**args, chunk_size=cfg["chunk"])
+    y, h = run_fwd(args, cfg["chunk"])
+    assert_parity(y, y_ref, torch.bfloat16, "y")
+    assert_parity(h, h_ref, torch.bfloat16, "h_last")
+
+
+@pytest.mark.gpu
+def test_ssd_fwd_split_chaining_on_device():
+    """scan(x[:k]) -> h; scan(x[k:], h_init=h) == scan(x) on the device."""
+    x = make_inputs(b=2, L=192, H=4, P=32, N=32, G=2, dtype=torch.float32)
+    y, h = run_fwd(x, 64)
+    first = {k: (v[:, :64] if k in ("u", "B", "C", "delta_raw") else v) for k, v in x.items()}
+    second = {k: (v[:, 64:] if k in ("u", "B", "C", "delta_raw") else v) for k, v in x.items()}
+    y1, h1 = run_fwd(first, 64)
+    second["h_init"] = h1.cpu()
+    y2, h2 = run_fwd(second, 64)
+    torch.testing.assert_close(torch.cat([y1, y2], 1), y, rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(h2, h, rtol=1e-4, atol=1e-5)
+
+
+def test_ssd_validation_raises_value_error():
+    from selective_attention.ops import SSDScanFn
+    x = make_inputs()
+    with pytest.raises(ValueError):
+        SSDScanFn.apply(x["u"], x["A"][:3], x["B"], x["C"], x["delta_raw"])
+    with pytest.raises(ValueError):
+        SSDScanFn.apply(x["u"], x["A"], x["B"][:, :5], x["C"], x["delta_raw"])
+    with pytest.raises(ValueError):
+        SSDScanFn.apply(x["u"][0], x["A"], x["B"], x["C"], x["delta_raw"])
+    with pytest.raises(ValueError):
+        SSDScanFn.apply(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], None, None,
+                        torch.tensor([3]))
