@@ -19,6 +19,7 @@
 #ifndef SA_HIP_H_
 #define SA_HIP_H_
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -67,6 +68,35 @@ int sa_ssd_fwd(int dtype, const void* u, const float* A, const void* B, const vo
                int num_groups, int state_dim, int chunk_size, int use_softplus, float delta_min,
                float delta_max, float* y, float* h_last, float* dt, float* dc, float* states,
                void* stream);
+
+/*
+ * Workspace bytes sa_ssd_bwd needs for these sizes (0 on bad arguments).
+ */
+size_t sa_ssd_bwd_workspace_size(int dtype, int batch, int seqlen, int num_heads, int head_dim,
+                                 int num_groups, int state_dim, int chunk_size);
+
+/*
+ * SSD chunked scan, backward.  Replaces ssd_scan_backward (reference
+ * triton_kernels/ssd_scan/backward.py:467-555 and its kernels
+ * backward_kernel.py:23-1039), called by SSDScanFn.backward
+ * (ops/ssd_scan.py:84-96).  Consumes the forward's dt, dc, states.
+ *   dy (b,L,H,P) float32; dh_last (b,H,P,N) float32 or NULL
+ *   outputs: du (dtype, like u), dB, dC (dtype), ddelta_raw (dtype),
+ *            dA (H,) f32, ddelta_bias (H,) f32 or NULL, dh_init (b,H,P,N) f32
+ *            or NULL (written when has_h_init)
+ *   workspace: caller-allocated device memory of at least
+ *              sa_ssd_bwd_workspace_size(...) bytes, 256-byte aligned
+ * Gradients at t >= length are zero and dy there is ignored.  All
+ * reductions are deterministic (no atomics).
+ */
+int sa_ssd_bwd(int dtype, const void* u, const float* A, const void* B, const void* C,
+               const void* delta_raw, const float* delta_bias, const int64_t* length,
+               const float* dy, const float* dh_last, const float* dt, const float* dc,
+               const float* states, int batch, int seqlen, int num_heads, int head_dim,
+               int num_groups, int state_dim, int chunk_size, int use_softplus, float delta_min,
+               float delta_max, int has_h_init, void* du, float* dA, void* dB, void* dC,
+               void* ddelta_raw, float* ddelta_bias, float* dh_init, void* workspace,
+               size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

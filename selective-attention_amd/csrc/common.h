@@ -116,6 +116,30 @@ __device__ __forceinline__ void wave_mma(v4f (&acc)[TM][TN], const MT* A, int ld
   }
 }
 
+// Split-precision variant for operands that originate in fp32 (gradients,
+// states, scaled tiles): such an operand is staged as two bf16 planes,
+// x = hi + lo with hi = bf16(x), lo = bf16(x - hi), the lo plane `plane`
+// elements after the hi plane.  Products keep hi*hi + lo*hi + hi*lo, dropping
+// lo*lo (~2^-16 relative), so the result is close to an fp32 GEMM.
+// SA / SB say which operands carry a lo plane.  For MT = float the split is
+// never used (the fp32 MFMA is exact) and SA = SB = false.
+template <typename MT, int TM, int TN, bool SA, bool SB>
+__device__ __forceinline__ void wave_mma_split(v4f (&acc)[TM][TN], const MT* A, int lda, int aplane,
+                                               const MT* B, int ldb, int bplane, int K, int lane) {
+  for (int k = 0; k < K; k += Mfma<MT>::KSTEP) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const MT* a = A + 16 * i * lda + k;
+        const MT* b = B + 16 * j * ldb + k;
+        acc[i][j] = Mfma<MT>::mma(a, lda, b, ldb, acc[i][j], lane);
+        if (SA) acc[i][j] = Mfma<MT>::mma(a + aplane, lda, b, ldb, acc[i][j], lane);
+        if (SB) acc[i][j] = Mfma<MT>::mma(a, lda, b + bplane, ldb, acc[i][j], lane);
+      }
+  }
+}
+
 template <int TM, int TN>
 __device__ __forceinline__ void zero_acc(v4f (&acc)[TM][TN]) {
 #pragma unroll

@@ -92,7 +92,10 @@ __global__ __launch_bounds__(256) void chunk_outer_kernel(
     SsdDims d, int vec_a, int vec_b) {
   constexpr int KC = 32;
   constexpr int LD = lds_ld<MT>(KC);
-  __shared__ __align__(16) MT As[64 * LD];
+  // the gradient operand of MODE 1 is fp32 in origin: split it on the bf16 path
+  constexpr bool SA = MODE == 1 && sizeof(MT) == 2;
+  constexpr int APLANE = SA ? 64 * LD : 0;
+  __shared__ __align__(16) MT As[(SA ? 2 : 1) * 64 * LD];
   __shared__ __align__(16) MT Bs[64 * LD];
   __shared__ float scl[1024];
 
@@ -133,11 +136,12 @@ __global__ __launch_bounds__(256) void chunk_outer_kernel(
     const int kv = min(KC, klim - k0);
     const float* sk = scl + k0;
     stage_transposed<MT>(As, LD, a_base + k0 * a_rs, a_rs, KC, 64, kv, d.P - p0, vec_a != 0,
-                         [sk](int r, int) { return sk[r]; });
+                         [sk](int r, int) { return sk[r]; }, APLANE);
     stage_transposed<MT>(Bs, LD, b_base + k0 * b_rs, b_rs, KC, 64, kv, d.N - n0, vec_b != 0,
                          NoScale{});
     __syncthreads();
-    wave_mma<MT, 2, 2>(acc, As + wm * LD, LD, Bs + wn * LD, LD, KC, lane);
+    wave_mma_split<MT, 2, 2, SA, false>(acc, As + wm * LD, LD, APLANE, Bs + wn * LD, LD, 0, KC,
+                                        lane);
     __syncthreads();
   }
   float* o = out + (((static_cast<long>(b) * d.nc + c) * d.H + h) * d.P) * d.N;
@@ -422,6 +426,8 @@ extern "C" int sa_ssd_fwd(int dtype, const void* u, const float* A, const void* 
   if (rc) return rc;
   SA_CHECK_ARG(u && A && B && C && delta_raw && length && y && h_last && dt && dc && states,
                "sa_ssd_fwd: null tensor pointer");
+  SA_CHECK_ARG(dtype != sa::kF32 || state_dim <= 128,
+               "sa_ssd_fwd: float32 path supports state_dim <= 128 (got %d)", state_dim);
   if (d.b == 0 || d.L == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == sa::kF32)

@@ -34,23 +34,47 @@ template <> struct Vec8<float> {
   }
 };
 
+// Store 8 values; with plane != 0 (bf16 only) also the rounding residuals
+// lo = bf16(x - hi) into the lo plane `plane` elements further.
 template <typename MT> struct Store8;
 template <> struct Store8<bf16> {
-  __device__ __forceinline__ static void store(bf16* p, const float (&v)[8]) {
+  __device__ __forceinline__ static void store(bf16* p, const float (&v)[8], int plane = 0) {
+    uint16_t hb[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) hb[j] = f32_to_bf16_bits(v[j]);
     uint4 raw;
-    raw.x = f32_to_bf16_bits(v[0]) | (static_cast<uint32_t>(f32_to_bf16_bits(v[1])) << 16);
-    raw.y = f32_to_bf16_bits(v[2]) | (static_cast<uint32_t>(f32_to_bf16_bits(v[3])) << 16);
-    raw.z = f32_to_bf16_bits(v[4]) | (static_cast<uint32_t>(f32_to_bf16_bits(v[5])) << 16);
-    raw.w = f32_to_bf16_bits(v[6]) | (static_cast<uint32_t>(f32_to_bf16_bits(v[7])) << 16);
+    raw.x = hb[0] | (static_cast<uint32_t>(hb[1]) << 16);
+    raw.y = hb[2] | (static_cast<uint32_t>(hb[3]) << 16);
+    raw.z = hb[4] | (static_cast<uint32_t>(hb[5]) << 16);
+    raw.w = hb[6] | (static_cast<uint32_t>(hb[7]) << 16);
     *reinterpret_cast<uint4*>(p) = raw;
+    if (plane) {
+      uint16_t lb[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        lb[j] = f32_to_bf16_bits(v[j] - __uint_as_float(static_cast<uint32_t>(hb[j]) << 16));
+      raw.x = lb[0] | (static_cast<uint32_t>(lb[1]) << 16);
+      raw.y = lb[2] | (static_cast<uint32_t>(lb[3]) << 16);
+      raw.z = lb[4] | (static_cast<uint32_t>(lb[5]) << 16);
+      raw.w = lb[6] | (static_cast<uint32_t>(lb[7]) << 16);
+      *reinterpret_cast<uint4*>(p + plane) = raw;
+    }
   }
 };
 template <> struct Store8<float> {
-  __device__ __forceinline__ static void store(float* p, const float (&v)[8]) {
+  __device__ __forceinline__ static void store(float* p, const float (&v)[8], int = 0) {
     *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
     *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
   }
 };
+
+// one element, optionally split into hi/lo planes (bf16 only)
+__device__ __forceinline__ void store_split(float* p, float v, int) { *p = v; }
+__device__ __forceinline__ void store_split(bf16* p, float v, int plane) {
+  const uint16_t hb = f32_to_bf16_bits(v);
+  p->x = hb;
+  if (plane) p[plane].x = f32_to_bf16_bits(v - __uint_as_float(static_cast<uint32_t>(hb) << 16));
+}
 
 struct NoScale {
   __device__ __forceinline__ float operator()(int, int) const { return 1.0f; }
@@ -61,7 +85,8 @@ struct NoScale {
 // kvalid % 8 == 0 so whole 8-vectors can be read.
 template <typename MT, typename TS, typename Scale>
 __device__ __forceinline__ void stage_rows(MT* lds, int ld, const TS* src, long rs, int R, int K,
-                                           int rvalid, int kvalid, bool vec, Scale scale) {
+                                           int rvalid, int kvalid, bool vec, Scale scale,
+                                           int plane = 0) {
   const int kv = K / 8;
   for (int v = threadIdx.x; v < R * kv; v += blockDim.x) {
     const int r = v / kv;
@@ -76,7 +101,7 @@ __device__ __forceinline__ void stage_rows(MT* lds, int ld, const TS* src, long 
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] *= scale(r, k0 + j);
-    Store8<MT>::store(lds + r * ld + k0, x);
+    Store8<MT>::store(lds + r * ld + k0, x, plane);
   }
 }
 
@@ -85,7 +110,7 @@ __device__ __forceinline__ void stage_rows(MT* lds, int ld, const TS* src, long 
 template <typename MT, typename TS, typename Scale>
 __device__ __forceinline__ void stage_transposed(MT* lds, int ld, const TS* src, long rs, int R,
                                                  int Cn, int rvalid, int cvalid, bool vec,
-                                                 Scale scale) {
+                                                 Scale scale, int plane = 0) {
   const int cv = Cn / 8;
   for (int v = threadIdx.x; v < R * cv; v += blockDim.x) {
     const int r = v / cv;
@@ -99,7 +124,7 @@ __device__ __forceinline__ void stage_transposed(MT* lds, int ld, const TS* src,
         x[j] = (r < rvalid && c0 + j < cvalid) ? load_f32(src + r * rs + c0 + j) : 0.0f;
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) lds[(c0 + j) * ld + r] = from_f32<MT>(x[j] * scale(r, c0 + j));
+    for (int j = 0; j < 8; ++j) store_split(lds + (c0 + j) * ld + r, x[j] * scale(r, c0 + j), plane);
   }
 }
 

@@ -28,9 +28,13 @@ SIGNATURES: dict[str, list] = {
     "sa_ssd_fwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                    _i, _i, _i, _i, _i, _i, _i, _i, _f, _f,
                    _vp, _vp, _vp, _vp, _vp, _vp],
+    "sa_ssd_bwd_workspace_size": [_i, _i, _i, _i, _i, _i, _i, _i],
+    "sa_ssd_bwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                   _i, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i,
+                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
 }
 
-RESTYPES = {"sa_last_error": ctypes.c_char_p}
+RESTYPES = {"sa_last_error": ctypes.c_char_p, "sa_ssd_bwd_workspace_size": ctypes.c_size_t}
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1

@@ -107,4 +107,68 @@ def ssd_scan_forward(
 def ssd_scan_backward(u, A, B, C, delta_raw, delta_bias, h_init, y_grad, h_last_grad, length,
                       chunk_size, use_delta_softplus=True, delta_limit=(0.0, float("inf")),
                       is_causal=True, saved=None):
-    raise NotImplementedError("SSD backward kernels not built yet")
+    """
+    Args: as ssd_scan_forward, plus
+        y_grad: (batch_size, seq_len, num_heads, head_dim) or None
+        h_last_grad: (batch_size, num_heads, head_dim, state_dim) or None
+        saved: (dt, dc, states) returned by ssd_scan_forward(return_saved=True);
+               recomputed when None
+
+    Returns:
+        u_grad, A_grad, B_grad, C_grad, delta_raw_grad, delta_bias_grad, h_init_grad
+        in the dtypes of the corresponding inputs (None for absent optionals).
+        Gradients are zero at t >= length and dy is ignored there
+        (backward_kernel.py:69-70, :245).
+    """
+    dtypes = dict(u=u.dtype, A=A.dtype, B=B.dtype, C=C.dtype, delta_raw=delta_raw.dtype,
+                  bias=None if delta_bias is None else delta_bias.dtype,
+                  h=None if h_init is None else h_init.dtype)
+    if saved is None:
+        _, _, saved = ssd_scan_forward(u, A, B, C, delta_raw, delta_bias, h_init, length,
+                                       chunk_size, use_delta_softplus, delta_limit, is_causal,
+                                       return_saved=True)
+    code, u, A32, B, C, delta_raw, bias32, h0, length = _prep(
+        u, A, B, C, delta_raw, delta_bias, h_init, length)
+    dt, dc, states = saved
+    b, L, H, P = u.shape
+    G, N = B.shape[2], B.shape[3]
+    dev = u.device
+    f32 = torch.float32
+    if y_grad is None:
+        dy = torch.zeros((b, L, H, P), dtype=f32, device=dev)
+    else:
+        dy = _f32_aligned(y_grad)
+    dh_last = _f32_aligned(h_last_grad)
+
+    du = torch.empty_like(u)
+    dB = torch.empty_like(B)
+    dC = torch.empty_like(C)
+    ddr = torch.empty_like(delta_raw)
+    dA = torch.empty((H,), dtype=f32, device=dev)
+    dbias = None if delta_bias is None else torch.empty((H,), dtype=f32, device=dev)
+    dh0 = None if h_init is None else torch.empty((b, H, P, N), dtype=f32, device=dev)
+    if L == 0:
+        du.zero_(); dB.zero_(); dC.zero_(); ddr.zero_(); dA.zero_()
+        if dbias is not None:
+            dbias.zero_()
+        if dh0 is not None:
+            dh0.copy_(dh_last if dh_last is not None else torch.zeros_like(dh0))
+    else:
+        lib = _lib.load()
+        nbytes = lib.sa_ssd_bwd_workspace_size(code, b, L, H, P, G, N, int(chunk_size))
+        if nbytes == 0:
+            raise RuntimeError(f"sa_ssd_bwd_workspace_size: {lib.sa_last_error().decode()}")
+        ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+        lo, hi = limits(delta_limit)
+        _lib.call(
+            "sa_ssd_bwd", code, _lib.ptr(u), _lib.ptr(A32), _lib.ptr(B), _lib.ptr(C),
+            _lib.ptr(delta_raw), _lib.ptr(bias32), _lib.ptr(length), _lib.ptr(dy),
+            _lib.ptr(dh_last), _lib.ptr(dt), _lib.ptr(dc), _lib.ptr(states),
+            b, L, H, P, G, N, int(chunk_size), 1 if use_delta_softplus else 0, lo, hi,
+            0 if h_init is None else 1,
+            _lib.ptr(du), _lib.ptr(dA), _lib.ptr(dB), _lib.ptr(dC), _lib.ptr(ddr),
+            _lib.ptr(dbias), _lib.ptr(dh0), _lib.ptr(ws), nbytes, _lib.stream_of(u))
+    return (as_dtype(du, dtypes["u"]), as_dtype(dA, dtypes["A"]), as_dtype(dB, dtypes["B"]),
+            as_dtype(dC, dtypes["C"]), as_dtype(ddr, dtypes["delta_raw"]),
+            None if dbias is None else as_dtype(dbias, dtypes["bias"]),
+            None if dh0 is None else as_dtype(dh0, dtypes["h"]))

@@ -1,0 +1,117 @@
+"""SSD chunked scan backward: HIP kernels vs the fp64 CPU oracle (manual backward)."""
+import math
+
+import pytest
+import torch
+
+from oracle import ssd as ref
+from selective_attention import workloads
+from tests.helpers import assert_parity
+from tests.test_ssd_fwd import make_inputs, to_dev
+
+NAMES = ["u", "A", "B", "C", "delta_raw", "delta_bias", "h_init"]
+
+
+def gpu_grads(x, dy, dh, chunk, softplus=True, limit=(0.0, float("inf"))):
+    """Gradients through SSDScanFn.apply + autograd on the device."""
+    from selective_attention.ops import SSDScanFn
+    xd = to_dev(x)
+    leaves = {}
+    for k in NAMES:
+        if xd.get(k) is not None:
+            xd[k] = xd[k].detach().clone().requires_grad_(True)
+            leaves[k] = xd[k]
+    y, h = SSDScanFn.apply(xd["u"], xd["A"], xd["B"], xd["C"], xd["delta_raw"], xd["delta_bias"],
+                           xd["h_init"], xd["length"], chunk, softplus, limit, True)
+    outs, grads = [y], [dy.cuda()]
+    if dh is not None:
+        outs.append(h)
+        grads.append(dh.cuda())
+    torch.autograd.backward(outs, grads)
+    torch.cuda.synchronize()
+    return {k: v.grad for k, v in leaves.items()}
+
+
+def ref_grads(x, dy, dh, chunk, softplus=True, limit=(0.0, float("inf"))):
+    g = ref.ssd_scan_backward(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], x["delta_bias"],
+                              x["h_init"], dy, dh, x["length"], chunk, softplus, limit)
+    return dict(zip(NAMES, g))
+
+
+def check(x, chunk, dtype, softplus=True, limit=(0.0, float("inf")), with_dh=True, seed=5):
+    g = torch.Generator().manual_seed(seed)
+    b, L, H, P = x["u"].shape
+    N = x["B"].shape[-1]
+    dy = torch.randn(b, L, H, P, generator=g)
+    dh = torch.randn(b, H, P, N, generator=g) if with_dh else None
+    got = gpu_grads(x, dy, dh, chunk, softplus, limit)
+    exp = ref_grads(x, dy, dh, chunk, softplus, limit)
+    for k, v in got.items():
+        assert v is not None, k
+        assert v.dtype == x[k].dtype, f"{k}: grad dtype {v.dtype} vs input {x[k].dtype}"
+        assert_parity(v, exp[k], dtype if k in ("u", "B", "C", "delta_raw") or dtype == torch.float32
+                      else torch.bfloat16, f"d{k}")
+
+
+BWD_CASES = [
+    ("aligned", dict(b=2, L=128, H=4, P=64, N=64, G=2), 64),
+    ("ragged", dict(b=2, L=100, H=4, P=24, N=40, G=2), 32),
+    ("lens", dict(b=3, L=150, H=2, P=16, N=16, G=1, lens=[150, 37, 0]), 64),
+    ("noinit", dict(b=1, L=70, H=6, P=32, N=24, G=3, with_h=False, with_bias=False), 16),
+    ("bigP", dict(b=1, L=96, H=2, P=130, N=72, G=1, lens=[90]), 48),
+    ("chunk256", dict(b=1, L=300, H=2, P=64, N=128, G=1, lens=[281]), 256),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("name,shape,chunk", BWD_CASES, ids=[c[0] for c in BWD_CASES])
+def test_ssd_bwd_parity(dtype, name, shape, chunk):
+    print(f"ssd bwd {name} dtype={dtype} chunk={chunk}", flush=True)
+    check(make_inputs(dtype=dtype, **shape), chunk, dtype)
+
+
+@pytest.mark.gpu
+def test_ssd_bwd_no_state_grad():
+    check(make_inputs(b=2, L=64, H=2, P=16, N=16, G=1), 32, torch.float32, with_dh=False)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("softplus,limit", [(False, (0.01, 0.2)), (True, (0.03, 0.08))])
+def test_ssd_bwd_limits(softplus, limit):
+    x = make_inputs(b=2, L=80, H=4, P=16, N=16, G=2, dtype=torch.float32)
+    if not softplus:
+        x["delta_raw"] = x["delta_raw"] + 3.0
+    check(x, 32, torch.float32, softplus, limit)
+
+
+@pytest.mark.gpu
+def test_ssd_bwd_config0_shape():
+    """Config 0 shapes (fp32) with dy ~ N(0,1): every gradient at rtol 1e-4."""
+    cfg = workloads.SSD_CONFIGS[0]
+    w = workloads.ssd_inputs(**cfg)
+    x = dict(u=w["u"], A=w["A"], B=w["B"], C=w["C"], delta_raw=w["delta_raw"], delta_bias=None,
+             h_init=None, length=None)
+    check(x, cfg["chunk"], torch.float32)
+
+
+@pytest.mark.gpu
+def test_ssd_bwd_config1_heads():
+    """Config 1 head/state/chunk shapes (bf16) on one row of 2048 tokens."""
+    cfg = dict(workloads.SSD_CONFIGS[1])
+    cfg.update(batch=1, seqlen=2048)
+    w = workloads.ssd_inputs(**cfg)
+    x = dict(u=w["u"], A=w["A"], B=w["B"], C=w["C"], delta_raw=w["delta_raw"], delta_bias=None,
+             h_init=None, length=None)
+    check(x, cfg["chunk"], torch.bfloat16, with_dh=False)
+
+
+@pytest.mark.gpu
+def test_ssd_bwd_deterministic():
+    x = make_inputs(b=2, L=128, H=4, P=32, N=32, G=2, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(1)
+    dy = torch.randn(2, 128, 4, 32, generator=g)
+    a = gpu_grads(x, dy, None, 64)
+    b = gpu_grads(x, dy, None, 64)
+    for k in a:
+        assert torch.equal(a[k], b[k]), f"d{k} differs between runs"

@@ -44,7 +44,7 @@ FWD_CASES = [
     ("ragged", dict(b=2, L=100, H=4, P=24, N=40, G=2), 32),
     ("lens", dict(b=3, L=150, H=2, P=16, N=16, G=1, lens=[150, 37, 0]), 64),
     ("noinit", dict(b=1, L=70, H=6, P=32, N=24, G=3, with_h=False, with_bias=False), 16),
-    ("bigP", dict(b=1, L=96, H=2, P=130, N=136, G=1), 48),
+    ("bigP", dict(b=1, L=96, H=2, P=130, N=120, G=1), 48),
     ("chunk1", dict(b=1, L=9, H=2, P=8, N=8, G=2), 1),
     ("chunk256", dict(b=1, L=300, H=2, P=64, N=128, G=1, lens=[281]), 256),
 ]
@@ -148,3 +148,20 @@ def test_ssd_validation_raises_value_error():
     with pytest.raises(ValueError):
         SSDScanFn.apply(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], None, None,
                         torch.tensor([3]))
+
+
+@pytest.mark.gpu
+def test_ssd_fp32_large_state_dim_is_rejected():
+    """fp32 operands with state_dim > 128 do not fit the LDS tiles: a clear error."""
+    x = make_inputs(b=1, L=64, H=2, P=16, N=136, G=1)
+    with pytest.raises(RuntimeError, match="state_dim <= 128"):
+        run_fwd(x, 32)
+
+
+@pytest.mark.gpu
+def test_ssd_bf16_state_dim_256():
+    x = make_inputs(b=1, L=130, H=2, P=32, N=256, G=1, dtype=torch.bfloat16)
+    y_ref, h_ref = ref.ssd_scan_forward(**x, chunk_size=64)
+    y, h = run_fwd(x, 64)
+    assert_parity(y, y_ref, torch.bfloat16, "y")
+    assert_parity(h, h_ref, torch.bfloat16, "h_last")
