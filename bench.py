@@ -1,0 +1,213 @@
+#!/usr/bin/env python3
+"""Benchmark of the selective-attention kernel layer on one MI355X.
+
+Headline (BASELINE.json metric, configs[1]): SSD chunked scan forward +
+backward, b8 L4096 H32 P64 N128 G8 chunk 256, bf16 activations, fp32 state.
+One step = SSDScanFn forward + backward (torch.autograd.grad for u, A, B, C,
+delta_raw) over one batch of synthetic inputs already resident in HBM.
+value = tokens/s over the whole job (one GPU).
+
+Extra fields on the same JSON line:
+  roofline      op-level HBM roofline of the fwd+bwd step (algorithmic bytes
+                at the dtypes passed / step time), plus live per-kernel
+                durations (HIP events on the launch stream) and the dominant
+                kernel; `traffic` comes from the committed rocprofv3 PMC
+                summary when present.
+  cpu_baseline  the CPU restatement (oracle/ssd.py, fp32 torch) of the same
+                fwd+bwd on a bounded sample (one batch row), on this host.
+  decode        config 3 decode step (paged GQA attention + state update),
+                us/step, when those ops are built.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.join(ROOT, "selective-attention_amd")
+for _p in (ROOT, PKG_ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_DENSE_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+
+
+def ssd_alg_bytes(b, L, H, P, G, N, act_bytes=2, y_bytes=4, dy_bytes=4):
+    """Each input read once and each output written once, forward + backward."""
+    u = b * L * H * P * act_bytes
+    bc = b * L * G * N * act_bytes
+    dr = b * L * H * act_bytes
+    y = b * L * H * P * y_bytes
+    h_last = b * H * P * N * 4
+    dy = b * L * H * P * dy_bytes
+    fwd = u + 2 * bc + dr + y + h_last
+    bwd = (u + 2 * bc + dr + dy) + (u + 2 * bc + dr)
+    return fwd + bwd
+
+
+def ssd_alg_flops(b, L, H, P, G, N, Lc):
+    """MFMA contractions counted causally: fwd per (b,c,h) 2LcPN + 2LcPN + Lc^2 P,
+    per (b,c,g) Lc^2 N; backward = 2x forward."""
+    nc = math.ceil(L / Lc)
+    fwd = b * nc * (H * (4 * Lc * P * N + Lc * Lc * P) + G * Lc * Lc * N)
+    return 3 * fwd
+
+
+def run_ssd(args, torch):
+    from selective_attention import workloads
+    from selective_attention.ops import SSDScanFn
+    from selective_attention.profiling import kernel_timer
+
+    cfg = dict(workloads.SSD_CONFIGS[1])
+    dev = torch.device("cuda:0")
+    x = workloads.ssd_inputs(**cfg, device=dev, with_dy=True)
+    b, L, H, P = x["u"].shape
+    G, N = x["B"].shape[2], x["B"].shape[3]
+    Lc = cfg["chunk"]
+    leaves = [x[k].requires_grad_(True) for k in ("u", "A", "B", "C", "delta_raw")]
+    dy = x["dy"]
+    inf = float("inf")
+
+    def step():
+        y, h = SSDScanFn.apply(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], None, None, None,
+                               Lc, True, (0.0, inf), True)
+        return torch.autograd.grad((y,), leaves, (dy,))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+
+    # profiled pass: same steps, per-kernel HIP events on the launch stream
+    with kernel_timer() as kt:
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+    kernels = {}
+    for name, st in sorted(kt.stats.items(), key=lambda kv: -kv[1]["total_ms"]):
+        kernels[name] = {"avg_us": round(st["avg_us"], 2),
+                         "per_step_us": round(1000.0 * st["total_ms"] / args.steps, 2),
+                         "launches_per_step": st["count"] // args.steps}
+    dominant = next(iter(kernels)) if kernels else None
+    kernel_sum_us = sum(v["per_step_us"] for v in kernels.values())
+
+    alg = ssd_alg_bytes(b, L, H, P, G, N)
+    flops = ssd_alg_flops(b, L, H, P, G, N, Lc)
+    achieved = alg / (ms / 1e3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "ssd_fwd_bwd_config1_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_step")
+    roofline = {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": traffic,
+        "scope": "SSD scan fwd+bwd step (all kernels of one op call)",
+        "algorithmic_bytes": alg,
+        "mfma_tflops": round(flops / (ms / 1e3) / 1e12, 1),
+        "mfma_frac": round(flops / (ms / 1e3) / 1e12 / BF16_DENSE_TFLOPS, 4),
+        "dominant_kernel": dominant,
+        "kernel_sum_us": round(kernel_sum_us, 1),
+        "kernels": kernels,
+    }
+    return dict(ms=ms, tokens=b * L, roofline=roofline,
+                config={"workload": "ssd_scan_fwd_bwd_config1", "batch": b, "seq_len": L,
+                        "nheads": H, "headdim": P, "dstate": N, "ngroups": G, "chunk": Lc,
+                        "activations": "bf16", "state": "fp32", "y_dtype": "fp32"})
+
+
+def cpu_baseline(torch, budget_s):
+    """The fp32 CPU restatement (oracle/ssd.py) of the same fwd+bwd on one
+    batch row of config 1; tokens/s of that row."""
+    from oracle import ssd as ref
+    from selective_attention import workloads
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    cfg = dict(workloads.SSD_CONFIGS[1])
+    cfg["batch"] = 1
+    x = workloads.ssd_inputs(**cfg, with_dy=True)
+    f32 = torch.float32
+
+    def once():
+        ref.ssd_scan_forward(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], None, None, None,
+                             cfg["chunk"], True, (0.0, float("inf")), f32)
+        ref.ssd_scan_backward(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], None, None,
+                              x["dy"], None, None, cfg["chunk"], True, (0.0, float("inf")), f32)
+
+    t0 = time.perf_counter()
+    once()  # warm-up (also sizes the sample)
+    first = time.perf_counter() - t0
+    reps = max(1, min(5, int(budget_s / max(first, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    tok = cfg["seqlen"]
+    return {"value": round(tok / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"1 of 8 batch rows (L={tok}) fwd+bwd, fp32 torch restatement, "
+                      f"median of {reps} after 1 warm-up; {med:.2f} s per row"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget-s", type=float, default=20.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    res = run_ssd(args, torch)
+    ms = res["ms"]
+    out = {
+        "metric": "SSD scan fwd+bwd tokens/s & % roofline; decode attn+state us/step @ batch 64",
+        "value": round(res["tokens"] / (ms / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded BASELINE config 1 recipe, resident in HBM)",
+        "config": res["config"],
+        "roofline": res["roofline"],
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(torch, args.cpu_budget_s)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -33,6 +33,18 @@ int sa_version(void);
 const char* sa_last_error(void);
 
 /*
+ * Per-kernel timing (no counterpart in the reference; a measurement aid).
+ * When enabled, every kernel launch is bracketed by HIP events recorded on
+ * its stream.  sa_profile_collect synchronises them, aggregates by kernel
+ * name (NUL-separated into names_buf), writes total milliseconds and launch
+ * counts, clears the records and returns the number of distinct kernels
+ * (-1 on a HIP error).  Not thread-safe.
+ */
+void sa_profile_enable(int on);
+int sa_profile_collect(char* names_buf, int names_len, float* total_ms, int* counts,
+                       int max_kernels);
+
+/*
  * Single-step selective state update, in place on the fp32 state.
  * Replaces ssu_forward (reference triton_kernels/ssu/forward.py:7-63,
  * kernel ssu/forward_kernel.py:6-79), called by SSUFn.forward

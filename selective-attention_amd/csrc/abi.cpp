@@ -3,6 +3,12 @@
 // 1 for an argument error (message in sa_last_error) and 2 for a HIP error.
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "prof.h"
 
 extern "C" {
 
@@ -18,5 +24,92 @@ void sa_set_error(const char* fmt, ...) {
 const char* sa_last_error(void) { return g_err; }
 
 int sa_version(void) { return 1; }
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// per-kernel event timing (single-threaded use; see prof.h)
+// ---------------------------------------------------------------------------
+namespace {
+struct ProfRec {
+  const char* name;
+  hipEvent_t a, b;
+};
+bool g_prof_on = false;
+std::vector<ProfRec> g_recs;
+std::vector<hipEvent_t> g_free;
+
+hipEvent_t take_event() {
+  if (!g_free.empty()) {
+    hipEvent_t e = g_free.back();
+    g_free.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+}  // namespace
+
+namespace sa {
+int prof_begin(const char* name, hipStream_t s) {
+  if (!g_prof_on) return -1;
+  ProfRec r{name, take_event(), take_event()};
+  if (!r.a || !r.b) return -1;
+  (void)hipEventRecord(r.a, s);
+  g_recs.push_back(r);
+  return static_cast<int>(g_recs.size()) - 1;
+}
+void prof_end(int slot, hipStream_t s) {
+  if (slot < 0) return;
+  (void)hipEventRecord(g_recs[slot].b, s);
+}
+}  // namespace sa
+
+extern "C" {
+
+void sa_profile_enable(int on) { g_prof_on = on != 0; }
+
+// Synchronises the recorded events, aggregates by kernel name and clears the
+// records.  Writes up to max_kernels entries: names (NUL-separated into
+// names_buf), total milliseconds and launch counts.  Returns the number of
+// distinct kernels (or -1 on a HIP error).
+int sa_profile_collect(char* names_buf, int names_len, float* total_ms, int* counts,
+                       int max_kernels) {
+  std::vector<std::string> names;
+  std::vector<float> tot;
+  std::vector<int> cnt;
+  int rc = 0;
+  for (auto& r : g_recs) {
+    float ms = 0.f;
+    if (hipEventSynchronize(r.b) != hipSuccess || hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess)
+      rc = -1;
+    size_t k = 0;
+    while (k < names.size() && names[k] != r.name) ++k;
+    if (k == names.size()) {
+      names.emplace_back(r.name);
+      tot.push_back(0.f);
+      cnt.push_back(0);
+    }
+    tot[k] += ms;
+    cnt[k] += 1;
+    g_free.push_back(r.a);
+    g_free.push_back(r.b);
+  }
+  g_recs.clear();
+  if (rc) return -1;
+  int off = 0;
+  const int n = static_cast<int>(names.size());
+  for (int k = 0; k < n && k < max_kernels; ++k) {
+    const int len = static_cast<int>(names[k].size()) + 1;
+    if (off + len <= names_len) {
+      memcpy(names_buf + off, names[k].c_str(), len);
+      off += len;
+    }
+    total_ms[k] = tot[k];
+    counts[k] = cnt[k];
+  }
+  return n;
+}
 
 }  // extern "C"

@@ -23,6 +23,7 @@
 // computed as the exclusive prefix over k of (colsum(M)[k] - rowsum(M)[k]):
 // T(k+1) - T(k) = sum_{t>k} M[t,k] - sum_{s<k} M[k,s].
 #include "ssd_common.h"
+#include "prof.h"
 
 namespace sa {
 
@@ -857,6 +858,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
   // 2. reverse state passing
   {
     const long blocks = static_cast<long>(d.b) * d.H * w.per_bh;
+    ProfScope prof_("state_passing_bwd", s);
     hipLaunchKernelGGL(state_passing_bwd_kernel, dim3(blocks), dim3(256), 0, s, states, dS,
                        dh_last, dh_init, dc, ddc_part, d);
     SA_CHECK_LAUNCH("state_passing_bwd");
@@ -866,6 +868,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
     const size_t smem = du_smem<MT>(d);
     if ((rc = set_smem(chunk_du_bwd_kernel<MT, T>, smem, "chunk_du_bwd"))) return rc;
     const long blocks = static_cast<long>(w.ttiles) * w.ptiles * bnc * d.H;
+    ProfScope prof_("chunk_du_bwd", s);
     hipLaunchKernelGGL((chunk_du_bwd_kernel<MT, T>), dim3(blocks), dim3(256), smem, s, u, Bm, Cm,
                        dy, dt, dc, dS, length, static_cast<T*>(du_), ddt_part, d, vec_act, vec_dy,
                        vec_f32);
@@ -876,6 +879,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
     const size_t smem = dcb_smem<MT>(d);
     if ((rc = set_smem(chunk_dcb_bwd_kernel<MT, T>, smem, "chunk_dcb_bwd"))) return rc;
     const long blocks = static_cast<long>(w.ttiles) * bnc * d.G;
+    ProfScope prof_("chunk_dcb_bwd", s);
     hipLaunchKernelGGL((chunk_dcb_bwd_kernel<MT, T>), dim3(blocks), dim3(256), smem, s, u, Bm, Cm,
                        dy, dt, dc, length, dCB, rsum, qpart, d, vec_act, vec_dy);
     SA_CHECK_LAUNCH("chunk_dcb_bwd");
@@ -883,6 +887,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
   // 5. dB, dC
   {
     const long blocks = 2L * w.ntiles * w.ttiles * bnc * d.G;
+    ProfScope prof_("chunk_dbdc_bwd", s);
     hipLaunchKernelGGL((chunk_dbdc_bwd_kernel<MT, T>), dim3(blocks), dim3(256), 0, s, u, Bm, Cm, dy,
                        dt, dc, states, dS, dCB, length, static_cast<T*>(dB_), static_cast<T*>(dC_),
                        xB_part, xC_part, d, vec_act, vec_dy, vec_f32, vec_dcb);
@@ -891,6 +896,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
   // 6. decay-gradient assembly, d delta_raw, dA/dbias partials
   {
     const long blocks = bnc * d.H;
+    ProfScope prof_("chunk_cumsum_bwd", s);
     hipLaunchKernelGGL(chunk_cumsum_bwd_kernel<T>, dim3(blocks), dim3(256), 0, s,
                        static_cast<const T*>(delta_raw_), A, bias, length, dt, ddt_part, xB_part,
                        xC_part, rsum, qpart, ddc_part, static_cast<T*>(ddelta_), dA_part, db_part,
@@ -898,9 +904,12 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
     SA_CHECK_LAUNCH("chunk_cumsum_bwd");
   }
   // 7. dA, dbias
-  hipLaunchKernelGGL(param_grad_reduce_kernel, dim3(d.H), dim3(256), 0, s, dA_part, db_part, dA,
-                     dbias, static_cast<int>(bnc), d.H);
-  SA_CHECK_LAUNCH("param_grad_reduce");
+  {
+    ProfScope prof_("param_grad_reduce", s);
+    hipLaunchKernelGGL(param_grad_reduce_kernel, dim3(d.H), dim3(256), 0, s, dA_part, db_part, dA,
+                       dbias, static_cast<int>(bnc), d.H);
+    SA_CHECK_LAUNCH("param_grad_reduce");
+  }
   return 0;
 }
 

@@ -21,6 +21,7 @@
 //   u (b,L,H,P)  B,C (b,L,G,N)  delta_raw (b,L,H)  [activations: fp32 | bf16]
 //   dt, dc (b,H,nc,Lc) fp32   states (b,nc,H,P,N) fp32   y (b,L,H,P) fp32
 #include "ssd_common.h"
+#include "prof.h"
 
 namespace sa {
 
@@ -338,6 +339,7 @@ int launch_chunk_cumsum(const void* delta_raw, const float* A, const float* bias
                         const int64_t* length, float* dt, float* dc, const SsdDims& d, int sp,
                         float lo, float hi, hipStream_t s) {
   const long blocks = static_cast<long>(d.b) * d.nc * d.H;
+  ProfScope prof_("chunk_cumsum_fwd", s);
   hipLaunchKernelGGL(chunk_cumsum_kernel<T>, dim3(blocks), dim3(256), 0, s,
                      static_cast<const T*>(delta_raw), A, bias, length, dt, dc, d, sp, lo, hi);
   SA_CHECK_LAUNCH("chunk_cumsum");
@@ -350,6 +352,7 @@ int launch_chunk_outer(const void* a, const void* bsrc, const float* dt, const f
   const long blocks = static_cast<long>((d.P + 63) / 64) * ((d.N + 63) / 64) * d.b * d.nc * d.H;
   const int vec_a = aligned16(a) && (static_cast<long>(d.H) * d.P) % 8 == 0 && d.P % 8 == 0;
   const int vec_b = aligned16(bsrc) && (static_cast<long>(d.G) * d.N) % 8 == 0 && d.N % 8 == 0;
+  ProfScope prof_(MODE == 0 ? "chunk_state_fwd" : "chunk_dstate_bwd", s);
   hipLaunchKernelGGL((chunk_outer_kernel<MT, TA, TB, MODE>), dim3(blocks), dim3(256), 0, s,
                      static_cast<const TA*>(a), static_cast<const TB*>(bsrc), dt, dc, length, out,
                      d, vec_a, vec_b);
@@ -361,6 +364,7 @@ int launch_state_passing_fwd(float* states, const float* h_init, float* h_last, 
                              const SsdDims& d, hipStream_t s) {
   const long PN = static_cast<long>(d.P) * d.N;
   const long blocks = static_cast<long>(d.b) * d.H * ((PN + 1023) / 1024);
+  ProfScope prof_("state_passing_fwd", s);
   hipLaunchKernelGGL(state_passing_fwd_kernel, dim3(blocks), dim3(256), 0, s, states, h_init,
                      h_last, dc, d);
   SA_CHECK_LAUNCH("state_passing_fwd");
@@ -383,6 +387,7 @@ int launch_chunk_scan(const void* u, const void* B, const void* C, const float* 
     SA_CHECK_ARG(e == hipSuccess, "chunk_scan_fwd: %zu B of LDS refused: %s", smem,
                  hipGetErrorString(e));
   }
+  ProfScope prof_("chunk_scan_fwd", s);
   hipLaunchKernelGGL((chunk_scan_fwd_kernel<MT, T>), dim3(blocks), dim3(256), smem, s,
                      static_cast<const T*>(u), static_cast<const T*>(B), static_cast<const T*>(C),
                      dt, dc, states, y, d, vec_act, vec_state);

@@ -13,6 +13,7 @@
 // parallelism.  y is a segmented lane reduction (xor shuffles inside the row
 // group).
 #include "common.h"
+#include "prof.h"
 
 namespace sa {
 
@@ -88,6 +89,7 @@ static int launch_ssu(const void* u, const float* A, const void* B, const void* 
   const long total_rows = static_cast<long>(batch) * H * P;
   const long blocks = (total_rows + kRowsPerBlock - 1) / kRowsPerBlock;
   if (blocks == 0) return 0;
+  ProfScope prof_("ssu_fwd", stream);
   hipLaunchKernelGGL((ssu_fwd_kernel<T, ROW_LANES, ROWS>), dim3(static_cast<unsigned>(blocks)),
                      dim3(256), 0, stream, static_cast<const T*>(u), A, static_cast<const T*>(B),
                      static_cast<const T*>(C), static_cast<const T*>(delta_raw), delta_bias, h,

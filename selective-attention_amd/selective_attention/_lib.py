@@ -24,6 +24,8 @@ _sz = ctypes.c_size_t
 SIGNATURES: dict[str, list] = {
     "sa_version": [],
     "sa_last_error": [],
+    "sa_profile_enable": [_i],
+    "sa_profile_collect": [ctypes.c_char_p, _i, ctypes.POINTER(_f), ctypes.POINTER(_i), _i],
     "sa_ssu_fwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _f, _vp],
     "sa_ssd_fwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                    _i, _i, _i, _i, _i, _i, _i, _i, _f, _f,
@@ -34,7 +36,7 @@ SIGNATURES: dict[str, list] = {
                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
 }
 
-RESTYPES = {"sa_last_error": ctypes.c_char_p, "sa_ssd_bwd_workspace_size": ctypes.c_size_t}
+RESTYPES = {"sa_last_error": ctypes.c_char_p, "sa_profile_enable": None, "sa_ssd_bwd_workspace_size": ctypes.c_size_t}
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
