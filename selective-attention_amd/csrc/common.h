@@ -22,13 +22,23 @@ __device__ __forceinline__ float to_f32(bf16 v) {
   return __uint_as_float(static_cast<uint32_t>(v.x) << 16);
 }
 
-// round-to-nearest-even fp32 -> bf16 (NaN stays NaN)
+// round-to-nearest-even fp32 -> bf16; lowers to gfx950's v_cvt_pk_bf16_f32
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
+// two floats -> packed bf16x2 (a in the low half)
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const v2bf v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float bf16lo_to_f32(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi_to_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// 2^x on the transcendental unit (v_exp_f32); decay factors exp(d) are
+// evaluated as exp2(d * log2(e)) on pre-scaled cumulative sums
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename T> struct Conv;
 template <> struct Conv<float> {

@@ -228,7 +228,7 @@ __global__ __launch_bounds__(256) void chunk_du_bwd_kernel(
     for (int t = t0 + threadIdx.x; t < min(t0 + 64, d.Lc); t += 256) dpart[t] = 0.f;
     return;
   }
-  for (int t = threadIdx.x; t < d.Lc; t += 256) dcs[t] = dc[crow + t];
+  for (int t = threadIdx.x; t < d.Lc; t += 256) dcs[t] = dc[crow + t] * kLog2e;
   const int rv = min(64, lim - t0);
   stage_rows<MT>(Bt, LDN, Bm + (tok0 + t0) * act_rs + static_cast<long>(g) * d.N, act_rs, 64, NP,
                  rv, d.N, vec_act != 0, NoScale{});
@@ -245,7 +245,7 @@ __global__ __launch_bounds__(256) void chunk_du_bwd_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = t0 + wm + 16 * i + frag_row(lane, r);
-      const float e = t < lim ? expf(fminf(dc_last - dcs[t], 0.0f)) : 0.0f;
+      const float e = t < lim ? fast_exp2(fminf(dc_last - dcs[t], 0.0f)) : 0.0f;
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j][r] *= e;
     }
@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) void chunk_du_bwd_kernel(
           const int sl = wn + 16 * j + frag_col(lane);
           const int t = t0 + tl, s = s0 + sl;
           float v = 0.0f;
-          if (s >= t && s < lim) v = cbt[i][j][r] * expf(fminf(dcs[s] - dcs[t], 0.0f));
+          if (s >= t && s < lim) v = cbt[i][j][r] * fast_exp2(fminf(dcs[s] - dcs[t], 0.0f));
           store_split(Ls + tl * LD64 + sl, v, LPL);
         }
     __syncthreads();
@@ -411,8 +411,8 @@ __global__ __launch_bounds__(256) void chunk_dcb_bwd_kernel(
       __syncthreads();  // previous head's Ys/Us reads and dc/dt uses are done
       if (threadIdx.x < 64) {
         const int t = t0 + threadIdx.x, s = s0 + threadIdx.x;
-        dcI[threadIdx.x] = t < d.Lc ? dc[crow + t] : 0.f;
-        dcJ[threadIdx.x] = s < d.Lc ? dc[crow + s] : 0.f;
+        dcI[threadIdx.x] = t < d.Lc ? dc[crow + t] * kLog2e : 0.f;
+        dcJ[threadIdx.x] = s < d.Lc ? dc[crow + s] * kLog2e : 0.f;
         dtJ[threadIdx.x] = s < d.Lc ? dt[crow + s] : 0.f;
       }
       v4f w[2][2];
@@ -439,7 +439,7 @@ __global__ __launch_bounds__(256) void chunk_dcb_bwd_kernel(
             const int t = t0 + tl, s = s0 + sl;
             float W = 0.f;
             if (t >= s && t < lim && s < lim)
-              W = w[i][j][r] * dtJ[sl] * expf(fminf(dcI[tl] - dcJ[sl], 0.0f));
+              W = w[i][j][r] * dtJ[sl] * fast_exp2(fminf(dcI[tl] - dcJ[sl], 0.0f));
             dcb[i][j][r] += W;
             m[i][j][r] = t > s ? W * cb[i][j][r] : 0.f;
           }

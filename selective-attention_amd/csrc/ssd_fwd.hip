@@ -251,7 +251,7 @@ __global__ __launch_bounds__(256) void chunk_scan_fwd_kernel(
   const long crow = ((static_cast<long>(b) * d.H + h) * d.nc + c) * d.Lc;
   for (int t = threadIdx.x; t < d.Lc; t += 256) {
     dts[t] = dt[crow + t];
-    dcs[t] = dc[crow + t];
+    dcs[t] = dc[crow + t] * kLog2e;  // exp(x) = exp2(x log2 e) below
   }
   const long tok0 = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc;
   const long act_rs = static_cast<long>(d.G) * d.N;
@@ -273,7 +273,7 @@ __global__ __launch_bounds__(256) void chunk_scan_fwd_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = t0 + wm + 16 * i + frag_row(lane, r);
-      const float e = t < d.Lc ? expf(dcs[t]) : 0.0f;
+      const float e = t < d.Lc ? fast_exp2(dcs[t]) : 0.0f;
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j][r] *= e;
     }
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(256) void chunk_scan_fwd_kernel(
           const int t = t0 + tl, s = s0 + sl;
           float v = 0.0f;
           if (s <= t && s < qlim && t < d.Lc)
-            v = cb[i][j][r] * expf(fminf(dcs[t] - dcs[s], 0.0f)) * dts[s];
+            v = cb[i][j][r] * fast_exp2(fminf(dcs[t] - dcs[s], 0.0f)) * dts[s];
           Ls[tl * LD64 + sl] = from_f32<MT>(v);
         }
     __syncthreads();

@@ -36,28 +36,24 @@ template <> struct Vec8<float> {
 
 // Store 8 values; with plane != 0 (bf16 only) also the rounding residuals
 // lo = bf16(x - hi) into the lo plane `plane` elements further.
+// Store 8 values; with plane != 0 (bf16 only) also the rounding residuals
+// lo = bf16(x - hi) into the lo plane `plane` elements further.
 template <typename MT> struct Store8;
 template <> struct Store8<bf16> {
   __device__ __forceinline__ static void store(bf16* p, const float (&v)[8], int plane = 0) {
-    uint16_t hb[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) hb[j] = f32_to_bf16_bits(v[j]);
     uint4 raw;
-    raw.x = hb[0] | (static_cast<uint32_t>(hb[1]) << 16);
-    raw.y = hb[2] | (static_cast<uint32_t>(hb[3]) << 16);
-    raw.z = hb[4] | (static_cast<uint32_t>(hb[5]) << 16);
-    raw.w = hb[6] | (static_cast<uint32_t>(hb[7]) << 16);
+    raw.x = pack_bf16x2(v[0], v[1]);
+    raw.y = pack_bf16x2(v[2], v[3]);
+    raw.z = pack_bf16x2(v[4], v[5]);
+    raw.w = pack_bf16x2(v[6], v[7]);
     *reinterpret_cast<uint4*>(p) = raw;
     if (plane) {
-      uint16_t lb[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        lb[j] = f32_to_bf16_bits(v[j] - __uint_as_float(static_cast<uint32_t>(hb[j]) << 16));
-      raw.x = lb[0] | (static_cast<uint32_t>(lb[1]) << 16);
-      raw.y = lb[2] | (static_cast<uint32_t>(lb[3]) << 16);
-      raw.z = lb[4] | (static_cast<uint32_t>(lb[5]) << 16);
-      raw.w = lb[6] | (static_cast<uint32_t>(lb[7]) << 16);
-      *reinterpret_cast<uint4*>(p + plane) = raw;
+      uint4 lo;
+      lo.x = pack_bf16x2(v[0] - bf16lo_to_f32(raw.x), v[1] - bf16hi_to_f32(raw.x));
+      lo.y = pack_bf16x2(v[2] - bf16lo_to_f32(raw.y), v[3] - bf16hi_to_f32(raw.y));
+      lo.z = pack_bf16x2(v[4] - bf16lo_to_f32(raw.z), v[5] - bf16hi_to_f32(raw.z));
+      lo.w = pack_bf16x2(v[6] - bf16lo_to_f32(raw.w), v[7] - bf16hi_to_f32(raw.w));
+      *reinterpret_cast<uint4*>(p + plane) = lo;
     }
   }
 };
@@ -65,6 +61,29 @@ template <> struct Store8<float> {
   __device__ __forceinline__ static void store(float* p, const float (&v)[8], int = 0) {
     *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
     *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+};
+
+// 4 consecutive k values of one LDS row (8 B for bf16, 16 B for fp32)
+template <typename MT> struct Store4;
+template <> struct Store4<bf16> {
+  __device__ __forceinline__ static void store(bf16* p, float a, float b, float c, float d,
+                                               int plane) {
+    uint2 raw;
+    raw.x = pack_bf16x2(a, b);
+    raw.y = pack_bf16x2(c, d);
+    *reinterpret_cast<uint2*>(p) = raw;
+    if (plane) {
+      uint2 lo;
+      lo.x = pack_bf16x2(a - bf16lo_to_f32(raw.x), b - bf16hi_to_f32(raw.x));
+      lo.y = pack_bf16x2(c - bf16lo_to_f32(raw.y), d - bf16hi_to_f32(raw.y));
+      *reinterpret_cast<uint2*>(p + plane) = lo;
+    }
+  }
+};
+template <> struct Store4<float> {
+  __device__ __forceinline__ static void store(float* p, float a, float b, float c, float d, int) {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
   }
 };
 
@@ -80,51 +99,87 @@ struct NoScale {
   __device__ __forceinline__ float operator()(int, int) const { return 1.0f; }
 };
 
+template <typename A, typename B> struct SameT { static constexpr bool value = false; };
+template <typename A> struct SameT<A, A> { static constexpr bool value = true; };
+
 // LDS[r][k] (r < R, k < K; K % 8 == 0) from src rows of stride rs (elements).
 // Valid region: r < rvalid, k < kvalid.  vec: rows are 16-byte aligned and
-// kvalid % 8 == 0 so whole 8-vectors can be read.
+// kvalid % 8 == 0 so whole 8-vectors can be read.  A bf16 -> bf16 copy
+// without scaling or split moves raw 16-byte vectors.
 template <typename MT, typename TS, typename Scale>
 __device__ __forceinline__ void stage_rows(MT* lds, int ld, const TS* src, long rs, int R, int K,
                                            int rvalid, int kvalid, bool vec, Scale scale,
                                            int plane = 0) {
+  constexpr bool kRaw = SameT<MT, TS>::value && SameT<Scale, NoScale>::value;
   const int kv = K / 8;
   for (int v = threadIdx.x; v < R * kv; v += blockDim.x) {
     const int r = v / kv;
     const int k0 = (v - r * kv) * 8;
+    const bool full = r < rvalid && vec && k0 + 8 <= kvalid;
+    if constexpr (kRaw) {
+      if (full && plane == 0) {
+        if constexpr (sizeof(MT) == 2) {
+          *reinterpret_cast<uint4*>(lds + r * ld + k0) =
+              *reinterpret_cast<const uint4*>(src + r * rs + k0);
+        } else {
+          *reinterpret_cast<float4*>(lds + r * ld + k0) =
+              *reinterpret_cast<const float4*>(src + r * rs + k0);
+          *reinterpret_cast<float4*>(lds + r * ld + k0 + 4) =
+              *reinterpret_cast<const float4*>(src + r * rs + k0 + 4);
+        }
+        continue;
+      }
+    }
     float x[8];
-    if (r < rvalid && vec && k0 + 8 <= kvalid) {
+    if (full) {
       Vec8<TS>::load(src + r * rs + k0, x);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         x[j] = (r < rvalid && k0 + j < kvalid) ? load_f32(src + r * rs + k0 + j) : 0.0f;
     }
+    if constexpr (!SameT<Scale, NoScale>::value) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] *= scale(r, k0 + j);
+      for (int j = 0; j < 8; ++j) x[j] *= scale(r, k0 + j);
+    }
     Store8<MT>::store(lds + r * ld + k0, x, plane);
   }
 }
 
 // LDS[c][r] (c < Cn, r < R) from src[r*rs + c]; valid r < rvalid, c < cvalid.
-// vec: rows 16-byte aligned and cvalid % 8 == 0.  Cn % 8 == 0.
+// vec: rows 16-byte aligned and cvalid % 8 == 0.  R % 4 == 0, Cn % 8 == 0.
+// Each thread reads a 4 (r) x 8 (c) block with 8-wide vector loads and
+// writes it transposed as 8 runs of 4 consecutive k; the 16 lanes of a row
+// group cover 64 consecutive k of one LDS row, so the writes are
+// bank-conflict free.
 template <typename MT, typename TS, typename Scale>
 __device__ __forceinline__ void stage_transposed(MT* lds, int ld, const TS* src, long rs, int R,
                                                  int Cn, int rvalid, int cvalid, bool vec,
                                                  Scale scale, int plane = 0) {
-  const int cv = Cn / 8;
-  for (int v = threadIdx.x; v < R * cv; v += blockDim.x) {
-    const int r = v / cv;
-    const int c0 = (v - r * cv) * 8;
-    float x[8];
-    if (r < rvalid && vec && c0 + 8 <= cvalid) {
-      Vec8<TS>::load(src + r * rs + c0, x);
-    } else {
+  const int rq = R / 4, cv = Cn / 8;
+  for (int v = threadIdx.x; v < rq * cv; v += blockDim.x) {
+    const int a = v % rq;
+    const int r0 = a * 4;
+    const int c0 = (v / rq) * 8;
+    float x[4][8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        x[j] = (r < rvalid && c0 + j < cvalid) ? load_f32(src + r * rs + c0 + j) : 0.0f;
+    for (int i = 0; i < 4; ++i) {
+      const int r = r0 + i;
+      if (r < rvalid && vec && c0 + 8 <= cvalid) {
+        Vec8<TS>::load(src + r * rs + c0, x[i]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          x[i][j] = (r < rvalid && c0 + j < cvalid) ? load_f32(src + r * rs + c0 + j) : 0.0f;
+      }
+      if constexpr (!SameT<Scale, NoScale>::value) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[i][j] *= scale(r, c0 + j);
+      }
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) store_split(lds + (c0 + j) * ld + r, x[j] * scale(r, c0 + j), plane);
+    for (int j = 0; j < 8; ++j)
+      Store4<MT>::store(lds + (c0 + j) * ld + r0, x[0][j], x[1][j], x[2][j], x[3][j], plane);
   }
 }
 
