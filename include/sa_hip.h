@@ -110,6 +110,44 @@ int sa_ssd_bwd(int dtype, const void* u, const float* A, const void* B, const vo
                void* ddelta_raw, float* ddelta_bias, float* dh_init, void* workspace,
                size_t workspace_bytes, void* stream);
 
+/*
+ * Varlen block-sparse causal self-attention (prefill), bfloat16.  No
+ * counterpart kernel in the reference: semantics of SelectiveMHA's gated
+ * softmax (modules/selective_attention.py:27-144, mode "seq") restricted to
+ * selected 64-key blocks of the query's own sequence.
+ *   q, k, v, o: (total_tokens, num_heads, head_dim) bf16, head_dim in {64,128}
+ *   cu_seqlens: (num_seqs+1,) int32; block_idx: (num_heads, n_qblk, max_blocks)
+ *   int32, local key-block ids per 64-query block (-1 unused); key_bias:
+ *   (num_heads, total_tokens) f32 or NULL (not applied on the diagonal);
+ *   softmax_scale <= 0 selects 1/sqrt(head_dim).
+ */
+int sa_sparse_attn_fwd(int dtype, const void* q, const void* k, const void* v,
+                       const int32_t* cu_seqlens, int num_seqs, const int32_t* block_idx,
+                       int n_qblk, int max_blocks, int block_size, const float* key_bias,
+                       int total_tokens, int num_heads, int head_dim, float softmax_scale, void* o,
+                       void* stream);
+
+/* Workspace bytes of sa_paged_decode_fwd (split partials). */
+size_t sa_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                      int max_pages);
+
+/*
+ * Paged GQA decode attention, bfloat16.  No counterpart kernel in the
+ * reference: semantics of SelectiveMHA.step (modules/selective_attention.py:
+ * 392-405, mode "pos") over a paged cache.
+ *   q, o: (batch, Hq, D) bf16; k_pages, v_pages: (num_pages, Hkv, page_size, D)
+ *   bf16, page_size in {64,128}, D in {64,128}, Hq/Hkv <= 16; page_table:
+ *   (batch, max_pages) int32; seq_lens: (batch,) int32; key_bias:
+ *   (num_pages, Hkv, page_size) f32 or NULL (not applied to the newest key).
+ *   Out-of-range page ids are skipped.  Two launches: split-KV partials, then
+ *   a log-sum-exp merge.
+ */
+int sa_paged_decode_fwd(int dtype, const void* q, const void* k_pages, const void* v_pages,
+                        const int32_t* page_table, const int32_t* seq_lens, const float* key_bias,
+                        int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                        int max_pages, int num_pages, float softmax_scale, void* o,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,12 +31,18 @@ SIGNATURES: dict[str, list] = {
                    _i, _i, _i, _i, _i, _i, _i, _i, _f, _f,
                    _vp, _vp, _vp, _vp, _vp, _vp],
     "sa_ssd_bwd_workspace_size": [_i, _i, _i, _i, _i, _i, _i, _i],
+    "sa_paged_decode_workspace_size": [_i, _i, _i, _i, _i],
+    "sa_paged_decode_fwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f,
+                            _vp, _vp, _sz, _vp],
+    "sa_sparse_attn_fwd": [_i, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _vp, _i, _i, _i, _f,
+                           _vp, _vp],
     "sa_ssd_bwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                    _i, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i,
                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
 }
 
-RESTYPES = {"sa_last_error": ctypes.c_char_p, "sa_profile_enable": None, "sa_ssd_bwd_workspace_size": ctypes.c_size_t}
+RESTYPES = {"sa_last_error": ctypes.c_char_p, "sa_profile_enable": None, "sa_ssd_bwd_workspace_size": ctypes.c_size_t,
+            "sa_paged_decode_workspace_size": ctypes.c_size_t}
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1

@@ -1,0 +1,98 @@
+"""Launchers of the attention ops (no counterpart kernel in the reference).
+
+sparse_attn_varlen: varlen block-sparse causal self-attention over packed
+sequences.  paged_decode_attn: split-KV paged GQA decode
+attention.  Semantics follow the reference's gated
+softmax (modules/selective_attention.py:99-144): an optional per-key bias
+(the log-gate) is added to every score except the query's own position
+(prefill) / the newest key (decode).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+from .common import require_device
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.int32 and t.is_contiguous() else t.to(torch.int32).contiguous()
+
+
+def sparse_attn_varlen(q, k, v, cu_seqlens, block_idx, block_size=64, softmax_scale=None,
+                       key_bias=None):
+    """
+    Args:
+        q, k, v: (total_tokens, num_heads, head_dim) bfloat16, sequences packed
+        cu_seqlens: (num_seqs + 1,) int32 offsets of the sequences
+        block_idx: (num_heads, n_qblk, max_blocks) int32.  Query blocks are the
+            64-token blocks of each sequence, numbered sequence by sequence;
+            entries are key-block indices local to the query's sequence
+            (block j = positions [64j, 64j+64)), -1 for unused slots.
+            Blocks after the query block and out-of-range entries are ignored.
+        key_bias: (num_heads, total_tokens) float32 or None: added to the score
+            of key j for every query except j itself.
+
+    Returns:
+        o: (total_tokens, num_heads, head_dim), dtype of q.  A query with no
+        admissible key (its diagonal block not selected, nothing else either)
+        gets zeros.
+    """
+    require_device(q, k, v, cu_seqlens, block_idx, key_bias)
+    T, H, D = q.shape
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise TypeError("sparse_attn_varlen: q, k, v must be bfloat16")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    cu = _i32(cu_seqlens)
+    idx = _i32(block_idx)
+    bias = None if key_bias is None else key_bias.to(torch.float32).contiguous()
+    o = torch.empty_like(q)
+    scale = -1.0 if softmax_scale is None else float(softmax_scale)
+    _lib.call("sa_sparse_attn_fwd", _lib.DTYPE_BF16, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v),
+              _lib.ptr(cu), cu.shape[0] - 1, _lib.ptr(idx), idx.shape[1], idx.shape[2],
+              int(block_size), _lib.ptr(bias), T, H, D, scale, _lib.ptr(o), _lib.stream_of(q))
+    return o
+
+
+def paged_decode_attn(q, k_pages, v_pages, page_table, seq_lens, softmax_scale=None,
+                      key_bias=None):
+    """
+    Args:
+        q: (batch, num_q_heads, head_dim) bfloat16
+        k_pages, v_pages: (num_pages, num_kv_heads, page_size, head_dim) bfloat16
+        page_table: (batch, max_pages) int32, page ids of each row in order
+            (entries past the row's last page are ignored; -1 by convention)
+        seq_lens: (batch,) int32 cached tokens per row
+        key_bias: (num_pages, num_kv_heads, page_size) float32 or None: added to
+            every key's score except the newest (position seq_len - 1)
+
+    Returns:
+        o: (batch, num_q_heads, head_dim) bfloat16; query head h reads kv head
+        h // (num_q_heads // num_kv_heads).
+    """
+    require_device(q, k_pages, v_pages, page_table, seq_lens, key_bias)
+    b, Hq, D = q.shape
+    num_pages, Hkv, ps, D2 = k_pages.shape
+    if D2 != D or tuple(v_pages.shape) != tuple(k_pages.shape):
+        raise ValueError("paged_decode_attn: k_pages / v_pages / q shapes disagree")
+    for t in (q, k_pages, v_pages):
+        if t.dtype != torch.bfloat16:
+            raise TypeError("paged_decode_attn: q, k_pages, v_pages must be bfloat16")
+    q = q.contiguous()
+    k_pages, v_pages = k_pages.contiguous(), v_pages.contiguous()
+    pt = _i32(page_table)
+    sl = _i32(seq_lens)
+    bias = None if key_bias is None else key_bias.to(torch.float32).contiguous()
+    max_pages = pt.shape[1]
+    lib = _lib.load()
+    nbytes = lib.sa_paged_decode_workspace_size(b, Hq, Hkv, D, max_pages)
+    ws = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=q.device)
+    o = torch.empty_like(q)
+    scale = -1.0 if softmax_scale is None else float(softmax_scale)
+    _lib.call("sa_paged_decode_fwd", _lib.DTYPE_BF16, _lib.ptr(q), _lib.ptr(k_pages),
+              _lib.ptr(v_pages), _lib.ptr(pt), _lib.ptr(sl), _lib.ptr(bias), b, Hq, Hkv, D, ps,
+              max_pages, num_pages, scale, _lib.ptr(o), _lib.ptr(ws), ws.numel(),
+              _lib.stream_of(q))
+    return o

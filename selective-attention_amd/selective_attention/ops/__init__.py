@@ -1,4 +1,5 @@
+from .attention import paged_decode_attn, sparse_attn_varlen
 from .ssd_scan import SSDScanFn
 from .ssu import SSUFn
 
-__all__ = ["SSDScanFn", "SSUFn"]
+__all__ = ["SSDScanFn", "SSUFn", "sparse_attn_varlen", "paged_decode_attn"]

@@ -1,0 +1,252 @@
+"""Attention ops: oracle pins (CPU), workload invariants (CPU), HIP parity (GPU)."""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attn as ref
+from selective_attention import workloads
+from tests.helpers import assert_parity
+
+F64 = torch.float64
+
+
+# ------------------------------------------------------------------ helpers
+def full_causal_selection(lens, H, bs=64, M=None):
+    nbs = [math.ceil(n / bs) for n in lens]
+    M = M or max(nbs)
+    rows = []
+    for nb in nbs:
+        for j in range(nb):
+            r = list(range(j + 1)) + [-1] * (M - j - 1)
+            rows.append(r)
+    idx = torch.tensor(rows, dtype=torch.int32)
+    return idx[None].expand(H, -1, -1).contiguous()
+
+
+def packed(lens, H, D, seed=0, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    T = sum(lens)
+    q = torch.randn(T, H, D, generator=g).to(dtype)
+    k = torch.randn(T, H, D, generator=g).to(dtype)
+    v = torch.randn(T, H, D, generator=g).to(dtype)
+    cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens), 0).to(torch.int32)
+    return q, k, v, cu
+
+
+# ------------------------------------------------------------ oracle pins
+def test_oracle_sparse_full_selection_is_causal_sdpa():
+    lens, H, D = [70, 130, 5], 2, 16
+    q, k, v, cu = packed(lens, H, D, dtype=F64)
+    idx = full_causal_selection(lens, H)
+    o = ref.sparse_attn_varlen(q, k, v, cu, idx)
+    for s in range(len(lens)):
+        a, b = int(cu[s]), int(cu[s + 1])
+        exp = F.scaled_dot_product_attention(q[a:b].transpose(0, 1), k[a:b].transpose(0, 1),
+                                             v[a:b].transpose(0, 1), is_causal=True)
+        torch.testing.assert_close(o[a:b], exp.transpose(0, 1), rtol=1e-10, atol=1e-12)
+
+
+def test_oracle_sparse_brute_force_with_bias():
+    lens, H, D, bs = [9, 6], 1, 4, 4
+    q, k, v, cu = packed(lens, H, D, seed=3, dtype=F64)
+    g = torch.Generator().manual_seed(4)
+    bias = torch.randn(H, sum(lens), generator=g, dtype=F64)
+    # query blocks: seq0 -> 3 blocks, seq1 -> 2 blocks; drop block 0 for q-block 2 of seq0
+    idx = torch.tensor([[[0, -1, -1], [0, 1, -1], [1, 2, -1], [0, -1, -1], [0, 1, -1]]],
+                       dtype=torch.int32)
+    o = ref.sparse_attn_varlen(q, k, v, cu, idx, block_size=bs, key_bias=bias)
+    sel = {0: {0}, 1: {0, 1}, 2: {1, 2}}
+    for i in range(9):  # sequence 0 by hand
+        keys = [j for j in range(i + 1) if j // bs in sel[i // bs]]
+        sc = torch.tensor([float(q[i, 0] @ k[j, 0]) / 2.0 + (float(bias[0, j]) if j != i else 0.0)
+                           for j in keys], dtype=F64)
+        p = torch.softmax(sc, 0)
+        exp = sum(p[t] * v[keys[t], 0] for t in range(len(keys)))
+        torch.testing.assert_close(o[i, 0], exp, rtol=1e-10, atol=1e-12)
+
+
+def test_oracle_decode_identity_pages_is_sdpa():
+    b, Hq, Hkv, D, ps = 3, 4, 2, 8, 4
+    g = torch.Generator().manual_seed(0)
+    lens = [5, 12, 1]
+    npg = [math.ceil(n / ps) for n in lens]
+    kp = torch.randn(sum(npg), Hkv, ps, D, generator=g, dtype=F64)
+    vp = torch.randn(sum(npg), Hkv, ps, D, generator=g, dtype=F64)
+    q = torch.randn(b, Hq, D, generator=g, dtype=F64)
+    table = torch.full((b, max(npg)), -1, dtype=torch.int32)
+    o_ = 0
+    for i, n in enumerate(npg):
+        table[i, :n] = torch.arange(o_, o_ + n)
+        o_ += n
+    out = ref.paged_decode_attn(q, kp, vp, table, torch.tensor(lens), None)
+    for i, n in enumerate(lens):
+        rows = table[i, :npg[i]].long()
+        K = kp[rows].permute(1, 0, 2, 3).reshape(Hkv, -1, D)[:, :n].repeat_interleave(2, 0)
+        V = vp[rows].permute(1, 0, 2, 3).reshape(Hkv, -1, D)[:, :n].repeat_interleave(2, 0)
+        exp = F.scaled_dot_product_attention(q[i][:, None], K, V)[:, 0]
+        torch.testing.assert_close(out[i], exp, rtol=1e-10, atol=1e-12)
+
+
+def test_oracle_decode_bias_spares_newest_key():
+    g = torch.Generator().manual_seed(1)
+    kp = torch.randn(2, 1, 4, 4, generator=g, dtype=F64)
+    vp = torch.randn(2, 1, 4, 4, generator=g, dtype=F64)
+    q = torch.randn(1, 1, 4, generator=g, dtype=F64)
+    table = torch.tensor([[1, 0]], dtype=torch.int32)
+    bias = torch.full((2, 1, 4), -1e9, dtype=F64)       # every key gated off ...
+    out = ref.paged_decode_attn(q, kp, vp, table, torch.tensor([6]), None, key_bias=bias)
+    # ... except the newest one (position 5 = page 0, slot 1), which is exempt
+    torch.testing.assert_close(out[0, 0], vp[0, 0, 1], rtol=1e-10, atol=1e-12)
+
+
+# ------------------------------------------------------- workload invariants
+def test_varlen_packing_and_selection_invariants():
+    g = torch.Generator().manual_seed(0)
+    lens = workloads.varlen_lengths(65536, 256, 8192, g)
+    assert sum(lens) == 65536 and all(1 <= n <= 8192 for n in lens)
+    assert all(n >= 256 for n in lens[:-1])
+    idx, seq_of, loc_of = workloads.block_selection(lens, 16, 64, 16, g)
+    assert idx.shape == (16, sum(math.ceil(n / 64) for n in lens), 16)
+    for h in (0, 7, 15):
+        for qb in range(0, idx.shape[1], 37):
+            j = int(loc_of[qb])
+            row = idx[h, qb]
+            used = row[row >= 0].tolist()
+            assert used == sorted(used) and len(set(used)) == len(used)
+            assert j in used and (j == 0 or j - 1 in used)
+            assert all(0 <= x <= j for x in used)
+            assert len(used) == 1 + min(1, j) + min(14, max(j - 1, 0))
+            assert (row[len(used):] == -1).all()
+
+
+def test_workload_generators_are_bit_stable():
+    """Seeded index tensors hash to committed values (bit-exact selection/offsets)."""
+    import hashlib
+    import json
+    import os
+    fx = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "workload_hashes.json")))
+    w = workloads.sparse_attn_inputs(total_tokens=65536, nheads=16, headdim=128)
+    h = lambda t: hashlib.sha256(t.contiguous().numpy().tobytes()).hexdigest()  # noqa: E731
+    assert h(w.cu_seqlens) == fx["config2_cu_seqlens"]
+    assert h(w.block_idx) == fx["config2_block_idx"]
+    d = workloads.decode_inputs(batch=64, nheads_q=2, nheads_kv=1, headdim=8, device="cpu")
+    assert h(d.seq_lens) == fx["config3_seq_lens"]
+    assert h(d.page_table) == fx["config3_page_table"]
+
+
+def test_ops_validate_shapes():
+    from selective_attention.ops import paged_decode_attn, sparse_attn_varlen
+    q, k, v, cu = packed([10], 2, 16)
+    idx = full_causal_selection([10], 2)
+    with pytest.raises(ValueError):
+        sparse_attn_varlen(q, k[:5], v, cu, idx)
+    with pytest.raises(ValueError):
+        sparse_attn_varlen(q, k, v, cu, idx[:1])
+    kp = torch.zeros(3, 1, 64, 16, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        paged_decode_attn(q[:2], kp, kp, torch.zeros(3, 1, dtype=torch.int32),
+                          torch.ones(2, dtype=torch.int32))
+    with pytest.raises(ValueError):
+        paged_decode_attn(q[:2], kp, kp[:1], torch.zeros(2, 1, dtype=torch.int32),
+                          torch.ones(2, dtype=torch.int32))
+
+
+# --------------------------------------------------------------- GPU parity
+def _run_sparse(q, k, v, cu, idx, bias=None):
+    from selective_attention.ops import sparse_attn_varlen
+    o = sparse_attn_varlen(q.cuda(), k.cuda(), v.cuda(), cu.cuda(), idx.cuda(),
+                           key_bias=None if bias is None else bias.cuda())
+    torch.cuda.synchronize()
+    return o
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lens,D", [([64], 128), ([200, 37, 64, 129], 128), ([300, 1, 65], 64),
+                                    ([513], 128)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_sparse_attn_parity_random_selection(lens, D, with_bias):
+    print(f"sparse lens={lens} D={D} bias={with_bias}", flush=True)
+    H = 3
+    g = torch.Generator().manual_seed(11)
+    q, k, v, cu = packed(lens, H, D, seed=5)
+    idx, _, _ = workloads.block_selection(lens, H, 64, 6, g)
+    bias = torch.randn(H, sum(lens), generator=g) if with_bias else None
+    o = _run_sparse(q, k, v, cu, idx, bias)
+    exp = ref.sparse_attn_varlen(q, k, v, cu, idx, key_bias=bias)
+    assert_parity(o, exp, torch.bfloat16, "o")
+
+
+@pytest.mark.gpu
+def test_sparse_attn_full_selection_matches_causal():
+    lens, H, D = [130, 260], 2, 128
+    q, k, v, cu = packed(lens, H, D, seed=2)
+    o = _run_sparse(q, k, v, cu, full_causal_selection(lens, H))
+    exp = ref.sparse_attn_varlen(q, k, v, cu, full_causal_selection(lens, H))
+    assert_parity(o, exp, torch.bfloat16, "o")
+
+
+@pytest.mark.gpu
+def test_sparse_attn_missing_diagonal_gives_zero_rows():
+    lens, H, D = [128], 1, 64
+    q, k, v, cu = packed(lens, H, D)
+    idx = torch.tensor([[[-1, -1], [-1, -1]]], dtype=torch.int32)   # nothing selected
+    o = _run_sparse(q, k, v, cu, idx)
+    assert torch.count_nonzero(o) == 0
+
+
+@pytest.mark.gpu
+def test_sparse_attn_config2_sample():
+    """Config 2 (T=65536, H16, D128) on the device; two heads of the first
+    three sequences against the oracle, every output finite."""
+    w = workloads.sparse_attn_inputs()
+    o = _run_sparse(w.q, w.k, w.v, w.cu_seqlens, w.block_idx)
+    assert torch.isfinite(o.float()).all()
+    cu = w.cu_seqlens
+    T3 = int(cu[3])
+    nq = sum(math.ceil(n / 64) for n in w.lens[:3])
+    for h in (0, 9):
+        exp = ref.sparse_attn_varlen(w.q[:T3, h:h + 1], w.k[:T3, h:h + 1], w.v[:T3, h:h + 1],
+                                     cu[:4], w.block_idx[h:h + 1, :nq])
+        assert_parity(o[:T3, h:h + 1], exp, torch.bfloat16, f"o head {h}")
+
+
+def _run_decode(d, bias=None):
+    from selective_attention.ops import paged_decode_attn
+    o = paged_decode_attn(d.q.cuda(), d.k_pages.cuda(), d.v_pages.cuda(), d.page_table.cuda(),
+                          d.seq_lens.cuda(), key_bias=None if bias is None else bias.cuda())
+    torch.cuda.synchronize()
+    return o
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,Hq,Hkv,D,minl,maxl", [(3, 8, 2, 128, 1, 200), (4, 4, 4, 64, 60, 70),
+                                                   (2, 32, 8, 128, 1000, 3000),
+                                                   (5, 16, 1, 128, 1, 1100)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_paged_decode_parity(b, Hq, Hkv, D, minl, maxl, with_bias):
+    print(f"decode b={b} Hq={Hq} Hkv={Hkv} D={D} len=[{minl},{maxl}] bias={with_bias}", flush=True)
+    d = workloads.decode_inputs(batch=b, nheads_q=Hq, nheads_kv=Hkv, headdim=D, min_len=minl,
+                                max_len=maxl, seed=3)
+    g = torch.Generator().manual_seed(9)
+    bias = torch.randn(d.k_pages.shape[:3], generator=g) if with_bias else None
+    o = _run_decode(d, bias)
+    exp = ref.paged_decode_attn(d.q, d.k_pages, d.v_pages, d.page_table, d.seq_lens,
+                                key_bias=bias)
+    assert_parity(o, exp, torch.bfloat16, "o")
+
+
+@pytest.mark.gpu
+def test_paged_decode_config3_sample():
+    """Config 3 (b64, 32q/8kv, D128, len U[1024,32768], 64-token pages) on the
+    device; four rows checked against the oracle."""
+    d = workloads.decode_inputs(device="cuda")
+    o = _run_decode(d)
+    assert torch.isfinite(o.float()).all()
+    rows = [0, 17, 40, 63]
+    kp, vp = d.k_pages, d.v_pages
+    exp = ref.paged_decode_attn(d.q[rows].cpu(), kp.cpu(), vp.cpu(), d.page_table[rows].cpu(),
+                                d.seq_lens[rows].cpu())
+    assert_parity(o[rows], exp, torch.bfloat16, "o")
