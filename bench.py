@@ -135,6 +135,127 @@ def run_ssd(args, torch):
                         "activations": "bf16", "state": "fp32", "y_dtype": "fp32"})
 
 
+def _time_events(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def run_decode(args, torch):
+    """Config 3 decode step: paged GQA attention (b64, 32q/8kv, D128, 64-token
+    pages, len U[1024,32768]) + selective state update (H32 P64 N128 G8)."""
+    from selective_attention import workloads
+    from selective_attention.ops import SSUFn, paged_decode_attn
+    from selective_attention.profiling import kernel_timer
+
+    dev = torch.device("cuda:0")
+    d = workloads.decode_inputs(device=dev)
+    x = workloads.ssu_inputs(device=dev)
+    h = x["h"]
+
+    def attn():
+        return paged_decode_attn(d.q, d.k_pages, d.v_pages, d.page_table, d.seq_lens)
+
+    def ssu():
+        return SSUFn.forward(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], None, h)
+
+    def step():
+        attn()
+        ssu()
+
+    steps = max(args.steps, 10)
+    ms_step = _time_events(torch, step, steps, args.warmup)
+    ms_attn = _time_events(torch, attn, steps, 2)
+    ms_ssu = _time_events(torch, ssu, steps, 2)
+    with kernel_timer() as kt:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    kernels = {k: round(v["avg_us"], 2) for k, v in kt.stats.items()}
+
+    lens = d.seq_lens.to("cpu", torch.int64)
+    b, Hq, D = d.q.shape
+    Hkv, ps = d.k_pages.shape[1], d.k_pages.shape[2]
+    npg = (lens + ps - 1) // ps
+    kv_bytes = int(lens.sum()) * Hkv * D * 2 * 2
+    attn_bytes = kv_bytes + 2 * b * Hq * D * 2 + int(npg.sum()) * 4
+    Hs, P, N = x["h"].shape[1], x["h"].shape[2], x["h"].shape[3]
+    G = x["B"].shape[1]
+    ssu_bytes = 2 * b * Hs * P * N * 4 + b * Hs * P * 2 * 2 + 2 * b * G * N * 2 + b * Hs * 2
+    total = attn_bytes + ssu_bytes
+    gbs = total / (ms_step / 1e3) / 1e9
+    return {
+        "us_per_step": round(ms_step * 1e3, 1),
+        "attn_us": round(ms_attn * 1e3, 1),
+        "ssu_us": round(ms_ssu * 1e3, 1),
+        "config": {"workload": "decode_config3", "batch": b, "q_heads": Hq, "kv_heads": Hkv,
+                   "headdim": D, "page_size": ps, "kv_tokens": int(lens.sum()),
+                   "ssu": f"H{Hs} P{P} N{N} G{G} fp32 state"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": total,
+                     "attn_frac": round(attn_bytes / (ms_attn / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "ssu_frac": round(ssu_bytes / (ms_ssu / 1e3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "kernels_avg_us": kernels,
+    }
+
+
+def sparse_pairs(lens, block_idx, bs=64):
+    """Admissible (query, key) pairs of the block-sparse causal pattern."""
+    import math
+    idx = block_idx.to("cpu")
+    H = idx.shape[0]
+    total = 0
+    qb = 0
+    for n in lens:
+        nb = math.ceil(n / bs)
+        for j in range(nb):
+            nq = min(bs, n - j * bs)
+            sel = idx[:, qb, :]
+            for h in range(H):
+                for kb in sel[h].tolist():
+                    if kb < 0 or kb > j:
+                        continue
+                    if kb < j:
+                        total += nq * bs
+                    else:
+                        total += nq * (nq + 1) // 2
+            qb += 1
+    return total
+
+
+def run_sparse(args, torch):
+    """Config 2: varlen block-sparse causal attention, T=65536, H16, D128."""
+    from selective_attention import workloads
+    from selective_attention.ops import sparse_attn_varlen
+
+    dev = torch.device("cuda:0")
+    w = workloads.sparse_attn_inputs(device=dev)
+
+    def fn():
+        return sparse_attn_varlen(w.q, w.k, w.v, w.cu_seqlens, w.block_idx)
+
+    ms = _time_events(torch, fn, max(args.steps, 10), args.warmup)
+    T, H, D = w.q.shape
+    pairs = sparse_pairs(w.lens, w.block_idx)
+    flops = 4 * D * pairs
+    tf = flops / (ms / 1e3) / 1e12
+    return {"us": round(ms * 1e3, 1), "tokens_per_s": round(T / (ms / 1e3), 1),
+            "config": {"workload": "sparse_attn_config2", "tokens": T, "heads": H, "headdim": D,
+                       "sequences": len(w.lens), "block": 64, "max_blocks": w.block_idx.shape[2]},
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_DENSE_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / BF16_DENSE_TFLOPS, 4),
+                         "algorithmic_flops": flops, "qk_pairs": pairs}}
+
+
 def cpu_baseline(torch, budget_s):
     """The fp32 CPU restatement (oracle/ssd.py) of the same fwd+bwd on one
     batch row of config 1; tokens/s of that row."""
@@ -177,6 +298,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--ssd-only", action="store_true", help="skip the decode / sparse lines")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -204,6 +326,9 @@ def main():
         "config": res["config"],
         "roofline": res["roofline"],
     }
+    if not args.ssd_only:
+        out["decode"] = run_decode(args, torch)
+        out["sparse_attn"] = run_sparse(args, torch)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, args.cpu_budget_s)
     print(json.dumps(out))
