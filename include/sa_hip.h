@@ -135,8 +135,9 @@ size_t sa_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_hea
  * Paged GQA decode attention, bfloat16.  No counterpart kernel in the
  * reference: semantics of SelectiveMHA.step (modules/selective_attention.py:
  * 392-405, mode "pos") over a paged cache.
- *   q, o: (batch, Hq, D) bf16; k_pages, v_pages: (num_pages, Hkv, page_size, D)
- *   bf16, page_size in {64,128}, D in {64,128}, Hq/Hkv <= 16; page_table:
+ *   q, o: (batch, Hq, D) bf16; k_pages: (num_pages, Hkv, page_size, D) bf16;
+ *   v_pages: (num_pages, Hkv, D, page_size) bf16 (V transposed per page);
+ *   page_size in {64,128}, D in {64,128}, Hq/Hkv <= 16; page_table:
  *   (batch, max_pages) int32; seq_lens: (batch,) int32; key_bias:
  *   (num_pages, Hkv, page_size) f32 or NULL (not applied to the newest key).
  *   Out-of-range page ids are skipped.  Two launches: split-KV partials, then

@@ -68,7 +68,8 @@ def sparse_attn_varlen(q, k, v, cu_seqlens, block_idx, block_size=64, softmax_sc
 
 def paged_decode_attn(q, k_pages, v_pages, page_table, seq_lens, softmax_scale=None,
                       key_bias=None, dtype=torch.float64):
-    """q (b, Hq, D); k_pages, v_pages (num_pages, Hkv, page_size, D);
+    """q (b, Hq, D); k_pages (num_pages, Hkv, page_size, D); v_pages
+    (num_pages, Hkv, D, page_size) (V stored transposed per page);
     page_table (b, max_pages) int; seq_lens (b,) int; key_bias
     (num_pages, Hkv, page_size) or None.  Returns o (b, Hq, D) in `dtype`."""
     b, Hq, D = q.shape
@@ -83,7 +84,7 @@ def paged_decode_attn(q, k_pages, v_pages, page_table, seq_lens, softmax_scale=N
         npg = math.ceil(n / ps)
         pages = page_table[i, :npg].to(torch.int64)
         K = k_pages[pages].to(dtype)                                        # (npg, Hkv, ps, D)
-        V = v_pages[pages].to(dtype)
+        V = v_pages[pages].to(dtype).transpose(-1, -2)                      # (npg, Hkv, ps, D)
         K = K.permute(1, 0, 2, 3).reshape(Hkv, npg * ps, D)[:, :n]
         V = V.permute(1, 0, 2, 3).reshape(Hkv, npg * ps, D)[:, :n]
         K = K.repeat_interleave(grp, dim=0)

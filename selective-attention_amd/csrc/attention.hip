@@ -9,10 +9,15 @@
 // mode "pos" :121-123), softmax, times V.
 //
 // MFMA layout (16x16x32 bf16): scores are computed transposed,
-// S^T[key][q] = K . Q^T, so a lane holds 4 consecutive keys of one query
-// column.  That is already the B-operand fragment of O^T = V^T . P^T: P never
-// goes through LDS, and the running max / sum of query q stay in the lanes
-// holding O^T[:, q].  Only V is transposed through LDS (register 4x8 blocks).
+// S^T[key][q] = K . Q^T, so a lane holds 4 keys of one query column.  That is
+// already the B-operand fragment of O^T = V^T . P^T: P never goes through
+// LDS, and the running max / sum of query q stay in the lanes holding
+// O^T[:, q].  Within a 64-key tile, MFMA row c of score tile kt is mapped to
+// key  32(kt/2) + 8(c/4) + 4(kt%2) + c%4  (key_of_row), so the 8 keys a lane
+// contributes to one 32-key step of V^T . P^T are consecutive and its V^T
+// operand is a single 16-byte read: from LDS for prefill (V transposed on
+// staging) and straight from HBM for decode, whose V pages are stored
+// transposed, (num_pages, Hkv, D, page_size).
 #include "common.h"
 #include "prof.h"
 #include "tile.h"
@@ -26,13 +31,6 @@ __device__ __forceinline__ v8bf zero_v8bf() {
   const uint4 z = {0u, 0u, 0u, 0u};
   return __builtin_bit_cast(v8bf, z);
 }
-// two 4-element runs (8 B each) -> one 8-element operand
-__device__ __forceinline__ v8bf load_2x4bf(const bf16* a, const bf16* b) {
-  const uint2 x = *reinterpret_cast<const uint2*>(a);
-  const uint2 y = *reinterpret_cast<const uint2*>(b);
-  const uint4 r = {x.x, x.y, y.x, y.y};
-  return __builtin_bit_cast(v8bf, r);
-}
 __device__ __forceinline__ v8bf pack_p(const v4f& lo, const v4f& hi) {
   const uint4 r = {pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]), pack_bf16x2(hi[0], hi[1]),
                    pack_bf16x2(hi[2], hi[3])};
@@ -43,6 +41,11 @@ __device__ __forceinline__ v4f mfma_bf16(const v8bf& a, const v8bf& b, const v4f
 }
 
 constexpr float kNegInf = -__builtin_huge_valf();
+
+// key (within a 64-key tile) held by MFMA row c of score tile kt
+__device__ __forceinline__ int key_of_row(int kt, int c) {
+  return 32 * (kt >> 1) + 8 * (c >> 2) + 4 * (kt & 1) + (c & 3);
+}
 
 // Online-softmax update for one block of keys.  s[kt][i]: log2-domain scores
 // of keys 16kt + 4g + i for query column (lane & 15); masked entries are
@@ -75,20 +78,18 @@ __device__ __forceinline__ void softmax_block(v4f (&s)[KT], v4f (&o)[DT], float&
   for (int t = 0; t < DT; ++t) o[t] *= alpha;
 }
 
-// O^T[d][q] += sum_key V^T[d][key] P^T[key][q] over NK keys (multiple of 32);
-// Vt: LDS [D][ldv]; s: probabilities from softmax_block
-template <int KT, int DT>
-__device__ __forceinline__ void pv_block(v4f (&o)[DT], const v4f (&s)[KT], const bf16* Vt, int ldv,
+// O^T[d][q] += sum_key V^T[d][key] P^T[key][q] over 64 keys; Vt points at
+// V^T[0][tile start] with row stride ldv; s: probabilities from softmax_block
+template <int DT>
+__device__ __forceinline__ void pv_block(v4f (&o)[DT], const v4f (&s)[4], const bf16* Vt, int ldv,
                                          int lane) {
   const int c = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int ks = 0; ks < KT / 2; ++ks) {
+  for (int ks = 0; ks < 2; ++ks) {
     const v8bf pb = pack_p(s[2 * ks], s[2 * ks + 1]);
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      const bf16* row = Vt + (16 * t + c) * ldv + 32 * ks + 4 * g;
-      o[t] = mfma_bf16(load_2x4bf(row, row + 16), pb, o[t]);
-    }
+    for (int t = 0; t < DT; ++t)
+      o[t] = mfma_bf16(load_v8bf(Vt + (16 * t + c) * ldv + 32 * ks + 8 * g), pb, o[t]);
   }
 }
 
@@ -160,13 +161,14 @@ __global__ __launch_bounds__(256) void sparse_attn_fwd_kernel(
       sc[kt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        sc[kt] = mfma_bf16(load_v8bf(Ks + (16 * kt + c) * LDK + 32 * ks + 8 * g), qf[ks], sc[kt]);
+        sc[kt] = mfma_bf16(load_v8bf(Ks + key_of_row(kt, c) * LDK + 32 * ks + 8 * g), qf[ks],
+                           sc[kt]);
     }
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int kl = 16 * kt + 4 * g + i;
+        const int kl = key_of_row(kt, 4 * g + i);
         const int key = k0 + kl;
         float val = kNegInf;
         if (kl < nk && key <= qloc && qloc < n) {
@@ -176,7 +178,7 @@ __global__ __launch_bounds__(256) void sparse_attn_fwd_kernel(
         sc[kt][i] = val;
       }
     softmax_block<4, DT>(sc, acc, m, l);
-    pv_block<4, DT>(acc, sc, Vt, LDV, lane);
+    pv_block<DT>(acc, sc, Vt, LDV, lane);
   }
   if (qloc < n) {
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
@@ -194,7 +196,9 @@ __global__ __launch_bounds__(256) void sparse_attn_fwd_kernel(
 // ---------------------------------------------------------------------------
 // paged GQA decode, split over pages.  One wave per (batch row, kv head,
 // split of PPS pages); the query heads of the group sit in the first lanes
-// of each 16-lane column group (columns >= group size are padding).
+// of each 16-lane column group (columns >= group size are padding).  No LDS:
+// K rows and V^T rows go from HBM straight into MFMA operands, and every
+// load of a 64-key tile is issued before its first MFMA.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(64) void paged_decode_kernel(
@@ -204,9 +208,6 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
     int Hq, int Hkv, int ps, int max_pages, int num_pages, int pps, int max_splits,
     float scale_log2) {
   constexpr int DT = D / 16, KS = D / 32;
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* Vt = reinterpret_cast<bf16*>(smem_raw);  // [D][ps + 8]
-  const int ldv = ps + 8;
   const int item = blockIdx.x;
   const int split = item % max_splits;
   const int rest = item / max_splits;
@@ -232,39 +233,64 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
   for (int pg = p_begin; pg < p_end; ++pg) {
     const int page = page_table[static_cast<long>(bi) * max_pages + pg];
     if (page < 0 || page >= num_pages) continue;  // corrupt table entry: skip the page
-    const int nk = min(ps, n - pg * ps);
-    const long pbase = (static_cast<long>(page) * Hkv + kvh) * ps;
-    const bf16* kbase = kp + pbase * D;
-    __syncthreads();  // previous page's V^T reads are done (single-wave block)
-    stage_transposed<bf16>(Vt, ldv, vp + pbase * D, D, ps, D, nk, D, true, NoScale{});
-    for (int k0 = 0; k0 < ps; k0 += 64) {
+    const int nk_page = min(ps, n - pg * ps);
+    const long pbase = (static_cast<long>(page) * Hkv + kvh) * ps;  // key index base
+    for (int k0 = 0; k0 < nk_page; k0 += 64) {
+      const int nk = min(64, nk_page - k0);
+      const bf16* kbase = kp + (pbase + k0) * D;
+      const bf16* vbase = vp + pbase * D + k0;  // V^T page: [D][ps]
+      v8bf kf[4][KS], vf[2][DT];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const int key = key_of_row(kt, c);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          kf[kt][ks] = key < nk ? load_v8bf(kbase + key * D + 32 * ks + 8 * g) : zero_v8bf();
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int kk = 32 * ks + 8 * g;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const bf16* src = vbase + static_cast<long>(16 * t + c) * ps + kk;
+          if (kk + 8 <= nk) {
+            vf[ks][t] = load_v8bf(src);
+          } else {  // ragged tail of the last page: zero the keys past the length
+            uint16_t e[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) e[j] = kk + j < nk ? src[j].x : uint16_t(0);
+            const uint4 r = {e[0] | (uint32_t(e[1]) << 16), e[2] | (uint32_t(e[3]) << 16),
+                             e[4] | (uint32_t(e[5]) << 16), e[6] | (uint32_t(e[7]) << 16)};
+            vf[ks][t] = __builtin_bit_cast(v8bf, r);
+          }
+        }
+      }
       v4f sc[4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         sc[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-        const int key = k0 + 16 * kt + c;
-        const bool ok = key < nk;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          sc[kt] = mfma_bf16(ok ? load_v8bf(kbase + static_cast<long>(key) * D + 32 * ks + 8 * g)
-                                : zero_v8bf(),
-                             qf[ks], sc[kt]);
+        for (int ks = 0; ks < KS; ++ks) sc[kt] = mfma_bf16(kf[kt][ks], qf[ks], sc[kt]);
       }
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int kl = k0 + 16 * kt + 4 * g + i;
+          const int kl = key_of_row(kt, 4 * g + i);
           float val = kNegInf;
           if (kl < nk && c < grp) {
             val = sc[kt][i] * scale_log2;
-            if (key_bias && pg * ps + kl != n - 1) val += key_bias[pbase + kl] * kLog2e;
+            if (key_bias && pg * ps + k0 + kl != n - 1) val += key_bias[pbase + k0 + kl] * kLog2e;
           }
           sc[kt][i] = val;
         }
       softmax_block<4, DT>(sc, acc, m, l);
-      __syncthreads();  // V^T staged (first tile) before the LDS reads
-      pv_block<4, DT>(acc, sc, Vt + k0, ldv, lane);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const v8bf pb = pack_p(sc[2 * ks], sc[2 * ks + 1]);
+#pragma unroll
+        for (int t = 0; t < DT; ++t) acc[t] = mfma_bf16(vf[ks][t], pb, acc[t]);
+      }
     }
   }
   // partial results: O^T[d][q] unnormalised, with m (log2 domain) and l
@@ -312,7 +338,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
   }
 }
 
-constexpr int kDecodePPS = 16;  // pages per split
+constexpr int kDecodePPS = 8;  // pages per split
 
 inline size_t decode_ws_bytes(int b, int Hq, int Hkv, int D, int max_pages) {
   const int max_splits = (max_pages + kDecodePPS - 1) / kDecodePPS;
@@ -356,18 +382,17 @@ extern "C" int sa_paged_decode_fwd(int dtype, const void* q, const void* k_pages
   float* part_ml = part_o + static_cast<size_t>(batch) * num_kv_heads * max_splits * grp * head_dim;
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf(static_cast<float>(head_dim));
   const float sl2 = scale * sa::kLog2e;
-  const size_t smem = static_cast<size_t>(head_dim) * (page_size + 8) * 2;
   const long items = static_cast<long>(batch) * num_kv_heads * max_splits;
   {
     sa::ProfScope prof_("paged_decode", s);
     if (head_dim == 128)
-      hipLaunchKernelGGL(sa::paged_decode_kernel<128>, dim3(items), dim3(64), smem, s,
+      hipLaunchKernelGGL(sa::paged_decode_kernel<128>, dim3(items), dim3(64), 0, s,
                          static_cast<const sa::bf16*>(q), static_cast<const sa::bf16*>(k_pages),
                          static_cast<const sa::bf16*>(v_pages), page_table, seq_lens, key_bias,
                          part_o, part_ml, num_q_heads, num_kv_heads, page_size, max_pages,
                          num_pages, sa::kDecodePPS, max_splits, sl2);
     else
-      hipLaunchKernelGGL(sa::paged_decode_kernel<64>, dim3(items), dim3(64), smem, s,
+      hipLaunchKernelGGL(sa::paged_decode_kernel<64>, dim3(items), dim3(64), 0, s,
                          static_cast<const sa::bf16*>(q), static_cast<const sa::bf16*>(k_pages),
                          static_cast<const sa::bf16*>(v_pages), page_table, seq_lens, key_bias,
                          part_o, part_ml, num_q_heads, num_kv_heads, page_size, max_pages,

@@ -61,7 +61,10 @@ def paged_decode_attn(q, k_pages, v_pages, page_table, seq_lens, softmax_scale=N
     """
     Args:
         q: (batch, num_q_heads, head_dim) bfloat16
-        k_pages, v_pages: (num_pages, num_kv_heads, page_size, head_dim) bfloat16
+        k_pages: (num_pages, num_kv_heads, page_size, head_dim) bfloat16
+        v_pages: (num_pages, num_kv_heads, head_dim, page_size) bfloat16 -- V is
+            kept transposed per page, so its MFMA operand is read straight from
+            HBM (the layout vLLM also uses for its V cache)
         page_table: (batch, max_pages) int32, page ids of each row in order
             (entries past the row's last page are ignored; -1 by convention)
         seq_lens: (batch,) int32 cached tokens per row
@@ -75,7 +78,7 @@ def paged_decode_attn(q, k_pages, v_pages, page_table, seq_lens, softmax_scale=N
     require_device(q, k_pages, v_pages, page_table, seq_lens, key_bias)
     b, Hq, D = q.shape
     num_pages, Hkv, ps, D2 = k_pages.shape
-    if D2 != D or tuple(v_pages.shape) != tuple(k_pages.shape):
+    if D2 != D or tuple(v_pages.shape) != (num_pages, Hkv, D, ps):
         raise ValueError("paged_decode_attn: k_pages / v_pages / q shapes disagree")
     for t in (q, k_pages, v_pages):
         if t.dtype != torch.bfloat16:

@@ -36,7 +36,8 @@ def paged_decode_attn(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Ten
                       key_bias: torch.Tensor | None = None) -> torch.Tensor:
     check_ndim(q, 3, name="q")
     check_ndim(k_pages, 4, name="k_pages")
-    check_shape(v_pages, tuple(k_pages.shape), name="v_pages")
+    npages, hkv, ps, hd = k_pages.shape
+    check_shape(v_pages, (npages, hkv, hd, ps), name="v_pages")
     b = q.shape[0]
     check_ndim(page_table, 2, name="page_table")
     if page_table.shape[0] != b:

@@ -155,7 +155,7 @@ def sparse_attn_inputs(total_tokens=65536, nheads=16, headdim=128, min_len=256, 
 class DecodeWorkload:
     q: torch.Tensor            # (b, Hq, D)
     k_pages: torch.Tensor      # (num_pages, Hkv, page_size, D)
-    v_pages: torch.Tensor
+    v_pages: torch.Tensor      # (num_pages, Hkv, D, page_size): V stored transposed per page
     page_table: torch.Tensor   # (b, max_pages) int32, -1 padded
     seq_lens: torch.Tensor     # (b,) int32
 
@@ -164,7 +164,9 @@ def decode_inputs(batch=64, nheads_q=32, nheads_kv=8, headdim=128, min_len=1024,
                   max_len=32768, page_size=64, dtype=torch.bfloat16, seed=0, device="cpu"):
     """seq_lens ~ U[min_len, max_len]; every sequence owns ceil(len/page_size)
     pages of a shared pool; the page numbers are a random permutation of the
-    pool.  q is drawn on the CPU; the K/V pool on `device` (seeded)."""
+    pool.  K pages are (num_pages, Hkv, page_size, D), V pages are stored
+    transposed, (num_pages, Hkv, D, page_size).  q is drawn on the CPU; the
+    K/V pool on `device` (seeded)."""
     g = torch.Generator().manual_seed(seed)
     seq_lens = torch.randint(min_len, max_len + 1, (batch,), generator=g, dtype=torch.int64)
     npages = [math.ceil(int(n) / page_size) for n in seq_lens]
@@ -181,8 +183,8 @@ def decode_inputs(batch=64, nheads_q=32, nheads_kv=8, headdim=128, min_len=1024,
     if dev.type == "cuda":
         gd = torch.Generator(device=dev).manual_seed(seed)
         kp = torch.randn(total, nheads_kv, page_size, headdim, generator=gd, device=dev, dtype=dtype)
-        vp = torch.randn(total, nheads_kv, page_size, headdim, generator=gd, device=dev, dtype=dtype)
+        vp = torch.randn(total, nheads_kv, headdim, page_size, generator=gd, device=dev, dtype=dtype)
     else:
         kp = torch.randn(total, nheads_kv, page_size, headdim, generator=g).to(dtype)
-        vp = torch.randn(total, nheads_kv, page_size, headdim, generator=g).to(dtype)
+        vp = torch.randn(total, nheads_kv, headdim, page_size, generator=g).to(dtype)
     return DecodeWorkload(q.to(dev), kp, vp, table.to(dev), seq_lens.to(torch.int32).to(dev))

@@ -74,7 +74,7 @@ def test_oracle_decode_identity_pages_is_sdpa():
     lens = [5, 12, 1]
     npg = [math.ceil(n / ps) for n in lens]
     kp = torch.randn(sum(npg), Hkv, ps, D, generator=g, dtype=F64)
-    vp = torch.randn(sum(npg), Hkv, ps, D, generator=g, dtype=F64)
+    vp = torch.randn(sum(npg), Hkv, D, ps, generator=g, dtype=F64)
     q = torch.randn(b, Hq, D, generator=g, dtype=F64)
     table = torch.full((b, max(npg)), -1, dtype=torch.int32)
     o_ = 0
@@ -85,7 +85,7 @@ def test_oracle_decode_identity_pages_is_sdpa():
     for i, n in enumerate(lens):
         rows = table[i, :npg[i]].long()
         K = kp[rows].permute(1, 0, 2, 3).reshape(Hkv, -1, D)[:, :n].repeat_interleave(2, 0)
-        V = vp[rows].permute(1, 0, 2, 3).reshape(Hkv, -1, D)[:, :n].repeat_interleave(2, 0)
+        V = vp[rows].permute(1, 0, 3, 2).reshape(Hkv, -1, D)[:, :n].repeat_interleave(2, 0)
         exp = F.scaled_dot_product_attention(q[i][:, None], K, V)[:, 0]
         torch.testing.assert_close(out[i], exp, rtol=1e-10, atol=1e-12)
 
@@ -99,7 +99,7 @@ def test_oracle_decode_bias_spares_newest_key():
     bias = torch.full((2, 1, 4), -1e9, dtype=F64)       # every key gated off ...
     out = ref.paged_decode_attn(q, kp, vp, table, torch.tensor([6]), None, key_bias=bias)
     # ... except the newest one (position 5 = page 0, slot 1), which is exempt
-    torch.testing.assert_close(out[0, 0], vp[0, 0, 1], rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(out[0, 0], vp[0, 0, :, 1], rtol=1e-10, atol=1e-12)
 
 
 # ------------------------------------------------------- workload invariants
@@ -147,11 +147,11 @@ def test_ops_validate_shapes():
         sparse_attn_varlen(q, k, v, cu, idx[:1])
     kp = torch.zeros(3, 1, 64, 16, dtype=torch.bfloat16)
     with pytest.raises(ValueError):
-        paged_decode_attn(q[:2], kp, kp, torch.zeros(3, 1, dtype=torch.int32),
+        paged_decode_attn(q[:2], kp, kp.transpose(-1, -2), torch.zeros(3, 1, dtype=torch.int32),
                           torch.ones(2, dtype=torch.int32))
     with pytest.raises(ValueError):
-        paged_decode_attn(q[:2], kp, kp[:1], torch.zeros(2, 1, dtype=torch.int32),
-                          torch.ones(2, dtype=torch.int32))
+        paged_decode_attn(q[:2], kp, kp, torch.zeros(2, 1, dtype=torch.int32),
+                          torch.ones(2, dtype=torch.int32))   # V must be (np, Hkv, D, ps)
 
 
 # --------------------------------------------------------------- GPU parity
