@@ -197,9 +197,94 @@ __global__ __launch_bounds__(256) void sparse_attn_fwd_kernel(
 // paged GQA decode, split over pages.  One wave per (batch row, kv head,
 // split of PPS pages); the query heads of the group sit in the first lanes
 // of each 16-lane column group (columns >= group size are padding).  No LDS:
-// K rows and V^T rows go from HBM straight into MFMA operands, and every
-// load of a 64-key tile is issued before its first MFMA.
+// K rows and V^T rows go from HBM straight into MFMA operands; all loads of
+// a 64-key tile are issued before its first MFMA.
 // ---------------------------------------------------------------------------
+template <int D>
+struct DecodeTile {
+  v8bf kf[4][D / 32];
+  v8bf vf[2][D / 16];
+  long kbase;  // key index of the tile's first key in the K pool (per kv head)
+  int nk;      // valid keys (0: skip)
+  int pos0;    // sequence position of the tile's first key
+};
+
+template <int D>
+__device__ __forceinline__ void decode_load(DecodeTile<D>& T, const bf16* __restrict__ kp,
+                                            const bf16* __restrict__ vp, int page, int Hkv,
+                                            int kvh, int ps, int num_pages, int k0, int nk_page,
+                                            int pos0, int c, int g) {
+  constexpr int KS = D / 32, DT = D / 16;
+  T.nk = (page < 0 || page >= num_pages) ? 0 : min(64, nk_page - k0);
+  T.pos0 = pos0;
+  const long pbase = (static_cast<long>(max(page, 0)) * Hkv + kvh) * ps;
+  T.kbase = pbase + k0;
+  const bf16* kbase = kp + (pbase + k0) * D;
+  const bf16* vbase = vp + pbase * D + k0;  // V^T page: [D][ps]
+  const int nk = T.nk;
+  // Every address below stays inside the (clamped) page: keys past nk are
+  // read but never used -- their scores are replaced by -inf and their V
+  // entries are zeroed by a bit mask, so stale pool contents cannot leak in.
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) {
+    const int key = key_of_row(kt, c);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) T.kf[kt][ks] = load_v8bf(kbase + key * D + 32 * ks + 8 * g);
+  }
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int kk = 32 * ks + 8 * g;
+    uint32_t mk[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      mk[w] = (kk + 2 * w < nk ? 0x0000ffffu : 0u) | (kk + 2 * w + 1 < nk ? 0xffff0000u : 0u);
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      uint4 r = *reinterpret_cast<const uint4*>(vbase + static_cast<long>(16 * t + c) * ps + kk);
+      r.x &= mk[0];
+      r.y &= mk[1];
+      r.z &= mk[2];
+      r.w &= mk[3];
+      T.vf[ks][t] = __builtin_bit_cast(v8bf, r);
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void decode_compute(const DecodeTile<D>& T, const v8bf (&qf)[D / 32],
+                                               v4f (&acc)[D / 16], float& m, float& l,
+                                               const float* __restrict__ key_bias, int n,
+                                               int grp, float scale_log2, int c, int g) {
+  constexpr int KS = D / 32, DT = D / 16;
+  if (T.nk <= 0) return;
+  v4f sc[4];
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) {
+    sc[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) sc[kt] = mfma_bf16(T.kf[kt][ks], qf[ks], sc[kt]);
+  }
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kl = key_of_row(kt, 4 * g + i);
+      float val = kNegInf;
+      if (kl < T.nk && c < grp) {
+        val = sc[kt][i] * scale_log2;
+        if (key_bias && T.pos0 + kl != n - 1) val += key_bias[T.kbase + kl] * kLog2e;
+      }
+      sc[kt][i] = val;
+    }
+  softmax_block<4, DT>(sc, acc, m, l);
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const v8bf pb = pack_p(sc[2 * ks], sc[2 * ks + 1]);
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] = mfma_bf16(T.vf[ks][t], pb, acc[t]);
+  }
+}
+
 template <int D>
 __global__ __launch_bounds__(64) void paged_decode_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ kp, const bf16* __restrict__ vp,
@@ -230,68 +315,20 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  for (int pg = p_begin; pg < p_end; ++pg) {
-    const int page = page_table[static_cast<long>(bi) * max_pages + pg];
-    if (page < 0 || page >= num_pages) continue;  // corrupt table entry: skip the page
-    const int nk_page = min(ps, n - pg * ps);
-    const long pbase = (static_cast<long>(page) * Hkv + kvh) * ps;  // key index base
-    for (int k0 = 0; k0 < nk_page; k0 += 64) {
-      const int nk = min(64, nk_page - k0);
-      const bf16* kbase = kp + (pbase + k0) * D;
-      const bf16* vbase = vp + pbase * D + k0;  // V^T page: [D][ps]
-      v8bf kf[4][KS], vf[2][DT];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const int key = key_of_row(kt, c);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          kf[kt][ks] = key < nk ? load_v8bf(kbase + key * D + 32 * ks + 8 * g) : zero_v8bf();
-      }
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int kk = 32 * ks + 8 * g;
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-          const bf16* src = vbase + static_cast<long>(16 * t + c) * ps + kk;
-          if (kk + 8 <= nk) {
-            vf[ks][t] = load_v8bf(src);
-          } else {  // ragged tail of the last page: zero the keys past the length
-            uint16_t e[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) e[j] = kk + j < nk ? src[j].x : uint16_t(0);
-            const uint4 r = {e[0] | (uint32_t(e[1]) << 16), e[2] | (uint32_t(e[3]) << 16),
-                             e[4] | (uint32_t(e[5]) << 16), e[6] | (uint32_t(e[7]) << 16)};
-            vf[ks][t] = __builtin_bit_cast(v8bf, r);
-          }
-        }
-      }
-      v4f sc[4];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        sc[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) sc[kt] = mfma_bf16(kf[kt][ks], qf[ks], sc[kt]);
-      }
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kl = key_of_row(kt, 4 * g + i);
-          float val = kNegInf;
-          if (kl < nk && c < grp) {
-            val = sc[kt][i] * scale_log2;
-            if (key_bias && pg * ps + k0 + kl != n - 1) val += key_bias[pbase + k0 + kl] * kLog2e;
-          }
-          sc[kt][i] = val;
-        }
-      softmax_block<4, DT>(sc, acc, m, l);
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const v8bf pb = pack_p(sc[2 * ks], sc[2 * ks + 1]);
-#pragma unroll
-        for (int t = 0; t < DT; ++t) acc[t] = mfma_bf16(vf[ks][t], pb, acc[t]);
-      }
-    }
+  // 64-key tiles of this split, in order
+  const int tiles_per_page = ps / 64;
+  const int ntiles = (p_end - p_begin) * tiles_per_page;
+  const int32_t* prow = page_table + static_cast<long>(bi) * max_pages;
+  auto load = [&](DecodeTile<D>& T, int t) {
+    const int pg = p_begin + t / tiles_per_page;
+    const int k0 = (t % tiles_per_page) * 64;
+    decode_load<D>(T, kp, vp, prow[pg], Hkv, kvh, ps, num_pages, k0, min(ps, n - pg * ps),
+                   pg * ps + k0, c, g);
+  };
+  DecodeTile<D> A;
+  for (int t = 0; t < ntiles; ++t) {
+    load(A, t);
+    decode_compute<D>(A, qf, acc, m, l, key_bias, n, grp, scale_log2, c, g);
   }
   // partial results: O^T[d][q] unnormalised, with m (log2 domain) and l
   const long slot = (static_cast<long>(bi) * Hkv + kvh) * max_splits + split;
@@ -307,34 +344,56 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
   }
 }
 
-// merge the splits of one (batch row, query head): 64 threads over D
+// merge the splits of one (batch row, query head); one wave, the split
+// weights exp2(m_s - M) computed lane-parallel into LDS
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
     const int32_t* __restrict__ seq_lens, bf16* __restrict__ o, int Hq, int Hkv, int D, int ps,
     int max_pages, int pps, int max_splits) {
+  __shared__ float wsh[1024];
   const int qh = blockIdx.x % Hq;
   const int bi = blockIdx.x / Hq;
   const int grp = Hq / Hkv;
   const int kvh = qh / grp, qi = qh % grp;
   const int n = min(max(seq_lens[bi], 0), max_pages * ps);
   const int npg = (n + ps - 1) / ps;
-  const int nsplit = (npg + pps - 1) / pps;
+  const int nsplit = min((npg + pps - 1) / pps, 1024);
   const long slot0 = (static_cast<long>(bi) * Hkv + kvh) * max_splits;
+  const int lane = threadIdx.x;
   float M = kNegInf;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, part_ml[((slot0 + s) * grp + qi) * 2]);
+  for (int s = lane; s < nsplit; s += 64) M = fmaxf(M, part_ml[((slot0 + s) * grp + qi) * 2]);
+  M = wave_max(M);
   float L = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
+  for (int s = lane; s < nsplit; s += 64) {
     const float ms = part_ml[((slot0 + s) * grp + qi) * 2];
-    if (ms != kNegInf) L += fast_exp2(ms - M) * part_ml[((slot0 + s) * grp + qi) * 2 + 1];
+    const float w = (ms == kNegInf) ? 0.0f : fast_exp2(ms - M);
+    wsh[s] = w;
+    L += w * part_ml[((slot0 + s) * grp + qi) * 2 + 1];
   }
+  L = wave_sum(L);
+  __syncthreads();
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  for (int dd = threadIdx.x; dd < D; dd += 64) {
-    float acc = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float ms = part_ml[((slot0 + s) * grp + qi) * 2];
-      if (ms != kNegInf) acc += fast_exp2(ms - M) * part_o[((slot0 + s) * grp + qi) * D + dd];
+  for (int d0 = 2 * lane; d0 < D; d0 += 128) {
+    float a0 = 0.f, a1 = 0.f;
+    int s = 0;
+    for (; s + 4 <= nsplit; s += 4) {
+      float2 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        v[j] = *reinterpret_cast<const float2*>(part_o + ((slot0 + s + j) * grp + qi) * D + d0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a0 += wsh[s + j] * v[j].x;
+        a1 += wsh[s + j] * v[j].y;
+      }
     }
-    o[(static_cast<long>(bi) * Hq + qh) * D + dd] = from_f32<bf16>(acc * inv);
+    for (; s < nsplit; ++s) {
+      const float2 v = *reinterpret_cast<const float2*>(part_o + ((slot0 + s) * grp + qi) * D + d0);
+      a0 += wsh[s] * v.x;
+      a1 += wsh[s] * v.y;
+    }
+    *reinterpret_cast<uint32_t*>(o + (static_cast<long>(bi) * Hq + qh) * D + d0) =
+        pack_bf16x2(a0 * inv, a1 * inv);
   }
 }
 
