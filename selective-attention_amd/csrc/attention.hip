@@ -24,28 +24,7 @@
 
 namespace sa {
 
-__device__ __forceinline__ v8bf load_v8bf(const bf16* p) {
-  return *reinterpret_cast<const v8bf*>(p);
-}
-__device__ __forceinline__ v8bf zero_v8bf() {
-  const uint4 z = {0u, 0u, 0u, 0u};
-  return __builtin_bit_cast(v8bf, z);
-}
-__device__ __forceinline__ v8bf pack_p(const v4f& lo, const v4f& hi) {
-  const uint4 r = {pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]), pack_bf16x2(hi[0], hi[1]),
-                   pack_bf16x2(hi[2], hi[3])};
-  return __builtin_bit_cast(v8bf, r);
-}
-__device__ __forceinline__ v4f mfma_bf16(const v8bf& a, const v8bf& b, const v4f& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
 constexpr float kNegInf = -__builtin_huge_valf();
-
-// key (within a 64-key tile) held by MFMA row c of score tile kt
-__device__ __forceinline__ int key_of_row(int kt, int c) {
-  return 32 * (kt >> 1) + 8 * (c >> 2) + 4 * (kt & 1) + (c & 3);
-}
 
 // Online-softmax update for one block of keys.  s[kt][i]: log2-domain scores
 // of keys 16kt + 4g + i for query column (lane & 15); masked entries are

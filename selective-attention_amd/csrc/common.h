@@ -150,6 +150,52 @@ __device__ __forceinline__ void wave_mma_split(v4f (&acc)[TM][TN], const MT* A, 
   }
 }
 
+// ---------------------------------------------------------------------------
+// register-resident bf16 MFMA helpers (16x16x32): operand fragments held in
+// registers, and the "transposed score" layout shared by the attention and
+// SSD tile kernels.  A 16x16 result tile computed with A-operand rows mapped
+// through key_of_row leaves every lane holding, for its column, 8 consecutive
+// keys across two tiles (2s, 2s+1) -- exactly the B-operand fragment of the
+// next MFMA that contracts over those keys.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ v8bf load_v8bf(const bf16* p) {
+  return *reinterpret_cast<const v8bf*>(p);
+}
+__device__ __forceinline__ v8bf zero_v8bf() {
+  const uint4 z = {0u, 0u, 0u, 0u};
+  return __builtin_bit_cast(v8bf, z);
+}
+__device__ __forceinline__ v8bf pack_p(const v4f& lo, const v4f& hi) {
+  const uint4 r = {pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]), pack_bf16x2(hi[0], hi[1]),
+                   pack_bf16x2(hi[2], hi[3])};
+  return __builtin_bit_cast(v8bf, r);
+}
+__device__ __forceinline__ v4f mfma_bf16(const v8bf& a, const v8bf& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// 16-byte global load, zero when !ok
+__device__ __forceinline__ uint4 ld16(const void* p, bool ok) {
+  return ok ? *reinterpret_cast<const uint4*>(p) : uint4{0u, 0u, 0u, 0u};
+}
+// From four rows of 8 bf16 (r0..r3, one uint4 each) take column j (0..7) as
+// 4 consecutive bf16: the transposed 4-element run written to LDS.
+__device__ __forceinline__ uint2 col4_bf16(const uint4& r0, const uint4& r1, const uint4& r2,
+                                           const uint4& r3, int j) {
+  const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+  const int w = j >> 1;
+  const uint32_t a0 = w == 0 ? r0.x : w == 1 ? r0.y : w == 2 ? r0.z : r0.w;
+  const uint32_t a1 = w == 0 ? r1.x : w == 1 ? r1.y : w == 2 ? r1.z : r1.w;
+  const uint32_t a2 = w == 0 ? r2.x : w == 1 ? r2.y : w == 2 ? r2.z : r2.w;
+  const uint32_t a3 = w == 0 ? r3.x : w == 1 ? r3.y : w == 2 ? r3.z : r3.w;
+  return uint2{__builtin_amdgcn_perm(a1, a0, sel), __builtin_amdgcn_perm(a3, a2, sel)};
+}
+
+// key (within a 64-key tile) held by MFMA row c of score tile kt
+__device__ __forceinline__ int key_of_row(int kt, int c) {
+  return 32 * (kt >> 1) + 8 * (c >> 2) + 4 * (kt & 1) + (c & 3);
+}
+
 template <int TM, int TN>
 __device__ __forceinline__ void zero_acc(v4f (&acc)[TM][TN]) {
 #pragma unroll

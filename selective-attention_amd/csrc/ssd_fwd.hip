@@ -324,6 +324,209 @@ __global__ __launch_bounds__(256) void chunk_scan_fwd_kernel(
       }
 }
 
+// ---------------------------------------------------------------------------
+// chunk scan, bf16 fast path.  One block per (b, chunk, group, 64-row tau
+// tile, 64-wide p tile, chunk of HC heads); wave w owns tau columns
+// 16w..16w+15.  The raw C.B^T tile of each 64-row sigma tile is computed once
+// (transposed, rows = sigma in key_of_row order, columns = tau) and shared by
+// the HC heads: per head it is decayed/masked in registers and fed as the
+// B operand of Y^T[p][tau] += U^T[p][sigma] S^T[sigma][tau].  C rows stay in
+// registers for the whole block; B rows and U^T tiles go through LDS.
+//   Y^T = U^T . S^T + exp(dc_tau) * H_in . C^T
+// ---------------------------------------------------------------------------
+template <int NK, int HC>
+__global__ __launch_bounds__(256) void chunk_scan_fwd_bf16_kernel(
+    const bf16* __restrict__ u, const bf16* __restrict__ Bm, const bf16* __restrict__ Cm,
+    const float* __restrict__ dt, const float* __restrict__ dc, const float* __restrict__ states,
+    float* __restrict__ y, SsdDims d) {
+  constexpr int N = 32 * NK;
+  constexpr int LDN = N + 8, LDU = 64 + 8;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  bf16* Bs = reinterpret_cast<bf16*>(smem_raw);  // [64][LDN]   B rows of the sigma tile
+  bf16* UT = Bs + 64 * LDN;                      // [HC][64][LDU] U^T per head
+  float* dcJ = reinterpret_cast<float*>(UT + HC * 64 * LDU);  // [HC][64] (log2 domain)
+  float* dtJ = dcJ + HC * 64;                                  // [HC][64]
+
+  const int hpg = d.H / d.G;
+  const int nhc = (hpg + HC - 1) / HC;
+  const int ttiles = (d.Lc + 63) / 64, ptiles = (d.P + 63) / 64;
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  int rest = bid;
+  const int ti = rest % ttiles;
+  rest /= ttiles;
+  const int pti = rest % ptiles;
+  rest /= ptiles;
+  const int hc = rest % nhc;
+  rest /= nhc;
+  const int g = rest % d.G;
+  rest /= d.G;
+  const int c = rest % d.nc;
+  const int b = rest / d.nc;
+  const int t0 = ti * 64, p0 = pti * 64;
+  const int qlim = min(d.Lc, d.L - c * d.Lc);
+  if (t0 >= qlim) return;
+  const int h0 = g * hpg + hc * HC;
+  const int nh = min(HC, hpg - hc * HC);
+
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int cl = lane & 15, lg = lane >> 4;
+  const int tau = t0 + 16 * wid + cl;  // this lane's output column
+  const long tok0 = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc;
+  const long act_rs = static_cast<long>(d.G) * d.N;
+  const long u_rs = static_cast<long>(d.H) * d.P;
+
+  v8bf Cw[NK];
+  {
+    const bf16* crow = Cm + (tok0 + min(tau, qlim - 1)) * act_rs + static_cast<long>(g) * d.N;
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) Cw[ks] = tau < qlim ? load_v8bf(crow + 32 * ks + 8 * lg) : zero_v8bf();
+  }
+  float dct[HC];
+#pragma unroll
+  for (int k = 0; k < HC; ++k) {
+    const long crow = ((static_cast<long>(b) * d.H + h0 + min(k, nh - 1)) * d.nc + c) * d.Lc;
+    dct[k] = tau < d.Lc ? dc[crow + tau] * kLog2e : 0.f;
+  }
+  v4f acc[HC][4];
+#pragma unroll
+  for (int k = 0; k < HC; ++k)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[k][t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  const int s_end = min(t0 + 64, qlim);
+  const int tid = threadIdx.x;
+  for (int s0 = 0; s0 < s_end; s0 += 64) {
+    const int sv = min(64, qlim - s0);
+    // issue every global load of the sigma tile, then commit to LDS
+    uint4 rb[NK];
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const int v = tid + 256 * i;
+      const int r = v / (N / 8), k0 = (v % (N / 8)) * 8;
+      rb[i] = ld16(Bm + (tok0 + s0 + r) * act_rs + static_cast<long>(g) * d.N + k0, r < sv);
+    }
+    uint4 ub[(HC * 128 + 255) / 256][4];
+#pragma unroll
+    for (int j = 0; j < (HC * 128 + 255) / 256; ++j) {
+      const int it = tid + 256 * j;
+      const int k = it / 128, a = it % 16, cg = (it / 16) % 8;
+      const int pcol = p0 + 8 * cg;
+      const bool okc = k < nh && pcol < d.P;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        ub[j][i] = ld16(u + (tok0 + s0 + 4 * a + i) * u_rs + static_cast<long>(h0 + min(k, nh - 1)) * d.P + pcol,
+                        okc && 4 * a + i < sv);
+    }
+    float dcv[(HC * 64 + 255) / 256], dtv[(HC * 64 + 255) / 256];
+#pragma unroll
+    for (int j = 0; j < (HC * 64 + 255) / 256; ++j) {
+      const int e = tid + 256 * j;
+      const int k = e / 64, sl = e % 64;
+      const long crow = ((static_cast<long>(b) * d.H + h0 + min(k, nh - 1)) * d.nc + c) * d.Lc;
+      const bool ok = k < nh && s0 + sl < d.Lc;
+      dcv[j] = ok ? dc[crow + s0 + sl] * kLog2e : 0.f;
+      dtv[j] = ok ? dt[crow + s0 + sl] : 0.f;
+    }
+    __syncthreads();  // the previous tile's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const int v = tid + 256 * i;
+      const int r = v / (N / 8), k0 = (v % (N / 8)) * 8;
+      *reinterpret_cast<uint4*>(Bs + r * LDN + k0) = rb[i];
+    }
+#pragma unroll
+    for (int j = 0; j < (HC * 128 + 255) / 256; ++j) {
+      const int it = tid + 256 * j;
+      const int k = it / 128, a = it % 16, cg = (it / 16) % 8;
+      if (k < HC) {
+        bf16* dst = UT + k * 64 * LDU + (8 * cg) * LDU + 4 * a;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          *reinterpret_cast<uint2*>(dst + jj * LDU) = col4_bf16(ub[j][0], ub[j][1], ub[j][2], ub[j][3], jj);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < (HC * 64 + 255) / 256; ++j) {
+      const int e = tid + 256 * j;
+      if (e < HC * 64) {
+        dcJ[e] = dcv[j];
+        dtJ[e] = dtv[j];
+      }
+    }
+    __syncthreads();
+    v4f cbt[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      cbt[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+      const bf16* brow = Bs + key_of_row(kt, cl) * LDN + 8 * lg;
+#pragma unroll
+      for (int ks = 0; ks < NK; ++ks) cbt[kt] = mfma_bf16(load_v8bf(brow + 32 * ks), Cw[ks], cbt[kt]);
+    }
+#pragma unroll
+    for (int k = 0; k < HC; ++k) {
+      if (k >= nh) break;
+      v4f sk[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int sl = key_of_row(kt, 4 * lg + i);
+          const int sg = s0 + sl;
+          float v = 0.f;
+          if (sg <= tau && sg < qlim)
+            v = cbt[kt][i] * fast_exp2(fminf(dct[k] - dcJ[k * 64 + sl], 0.f)) * dtJ[k * 64 + sl];
+          sk[kt][i] = v;
+        }
+      const bf16* ut = UT + k * 64 * LDU + cl * LDU + 8 * lg;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const v8bf pb = pack_p(sk[2 * ks], sk[2 * ks + 1]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          acc[k][t] = mfma_bf16(load_v8bf(ut + 16 * t * LDU + 32 * ks), pb, acc[k][t]);
+      }
+    }
+  }
+
+  // state contribution exp(dc_tau) * H_in . C^T, then the store
+#pragma unroll
+  for (int k = 0; k < HC; ++k) {
+    if (k >= nh) break;
+    const int h = h0 + k;
+    const float* Hb = states + (((static_cast<long>(b) * d.nc + c) * d.H + h) * d.P) * d.N;
+    const float e = fast_exp2(dct[k]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int p = p0 + 16 * t + cl;
+      v4f st = v4f{0.f, 0.f, 0.f, 0.f};
+      if (p < d.P) {
+        const float* hrow = Hb + static_cast<long>(p) * d.N + 8 * lg;
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) {
+          const float4 a = *reinterpret_cast<const float4*>(hrow + 32 * ks);
+          const float4 bq = *reinterpret_cast<const float4*>(hrow + 32 * ks + 4);
+          const uint4 r = {pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w), pack_bf16x2(bq.x, bq.y),
+                           pack_bf16x2(bq.z, bq.w)};
+          st = mfma_bf16(__builtin_bit_cast(v8bf, r), Cw[ks], st);
+        }
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) st = mfma_bf16(zero_v8bf(), Cw[ks], st);
+      }
+      acc[k][t] += st * e;
+    }
+    if (tau < qlim) {
+      float* yrow = y + (tok0 + tau) * u_rs + static_cast<long>(h) * d.P;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int p = p0 + 16 * t + 4 * lg;
+        if (p < d.P)
+          *reinterpret_cast<float4*>(yrow + p) = make_float4(acc[k][t][0], acc[k][t][1], acc[k][t][2], acc[k][t][3]);
+      }
+    }
+  }
+}
+
 size_t chunk_scan_smem(int N, int Lc, bool bf) {
   const int NP = round_up(N, 32);
   const size_t e = bf ? 2 : 4;
@@ -395,6 +598,52 @@ int launch_chunk_scan(const void* u, const void* B, const void* C, const float* 
   return 0;
 }
 
+// bf16 fast path: N a multiple of 32 (<= 256), P a multiple of 16
+template <int NK>
+int launch_chunk_scan_bf16_nk(const void* u, const void* B, const void* C, const float* dt,
+                              const float* dc, const float* states, float* y, const SsdDims& d,
+                              hipStream_t s) {
+  constexpr int HC = 4;
+  const int hpg = d.H / d.G;
+  const int nhc = (hpg + HC - 1) / HC;
+  const long blocks = static_cast<long>((d.Lc + 63) / 64) * ((d.P + 63) / 64) * nhc * d.G *
+                      d.nc * d.b;
+  const size_t smem = sizeof(bf16) * (64 * (32 * NK + 8) + HC * 64 * 72) + sizeof(float) * HC * 128;
+  if (smem > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(chunk_scan_fwd_bf16_kernel<NK, HC>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
+    SA_CHECK_ARG(e == hipSuccess, "chunk_scan_fwd_bf16: %zu B of LDS refused", smem);
+  }
+  ProfScope prof_("chunk_scan_fwd", s);
+  hipLaunchKernelGGL((chunk_scan_fwd_bf16_kernel<NK, HC>), dim3(blocks), dim3(256), smem, s,
+                     static_cast<const bf16*>(u), static_cast<const bf16*>(B),
+                     static_cast<const bf16*>(C), dt, dc, states, y, d);
+  SA_CHECK_LAUNCH("chunk_scan_fwd_bf16");
+  return 0;
+}
+
+inline bool chunk_scan_bf16_ok(const SsdDims& d, const void* u, const void* B, const void* C,
+                               const float* states) {
+  return d.N % 32 == 0 && d.N <= 256 && d.P % 16 == 0 && aligned16(u) && aligned16(B) &&
+         aligned16(C) && aligned16(states);
+}
+
+int launch_chunk_scan_bf16(const void* u, const void* B, const void* C, const float* dt,
+                           const float* dc, const float* states, float* y, const SsdDims& d,
+                           hipStream_t s) {
+  switch (d.N / 32) {
+    case 1: return launch_chunk_scan_bf16_nk<1>(u, B, C, dt, dc, states, y, d, s);
+    case 2: return launch_chunk_scan_bf16_nk<2>(u, B, C, dt, dc, states, y, d, s);
+    case 3: return launch_chunk_scan_bf16_nk<3>(u, B, C, dt, dc, states, y, d, s);
+    case 4: return launch_chunk_scan_bf16_nk<4>(u, B, C, dt, dc, states, y, d, s);
+    case 5: return launch_chunk_scan_bf16_nk<5>(u, B, C, dt, dc, states, y, d, s);
+    case 6: return launch_chunk_scan_bf16_nk<6>(u, B, C, dt, dc, states, y, d, s);
+    case 7: return launch_chunk_scan_bf16_nk<7>(u, B, C, dt, dc, states, y, d, s);
+    default: return launch_chunk_scan_bf16_nk<8>(u, B, C, dt, dc, states, y, d, s);
+  }
+}
+
 template <typename T, typename MT>
 int ssd_fwd_impl(const void* u, const float* A, const void* B, const void* C,
                  const void* delta_raw, const float* bias, const float* h_init,
@@ -404,6 +653,8 @@ int ssd_fwd_impl(const void* u, const float* A, const void* B, const void* C,
   if ((rc = launch_chunk_cumsum<T>(delta_raw, A, bias, length, dt, dc, d, sp, lo, hi, s))) return rc;
   if ((rc = launch_chunk_outer<MT, T, T, 0>(u, B, dt, dc, length, states, d, s))) return rc;
   if ((rc = launch_state_passing_fwd(states, h_init, h_last, dc, d, s))) return rc;
+  if (sizeof(T) == 2 && chunk_scan_bf16_ok(d, u, B, C, states))
+    return launch_chunk_scan_bf16(u, B, C, dt, dc, states, y, d, s);
   return launch_chunk_scan<MT, T>(u, B, C, dt, dc, states, y, d, s);
 }
 

@@ -165,3 +165,23 @@ def test_ssd_bf16_state_dim_256():
     y, h = run_fwd(x, 64)
     assert_parity(y, y_ref, torch.bfloat16, "y")
     assert_parity(h, h_ref, torch.bfloat16, "h_last")
+
+
+# shapes that take the bf16 register-resident chunk-scan path (N % 32 == 0, P % 16 == 0)
+FAST_CASES = [
+    ("hpg3_P48", dict(b=2, L=200, H=6, P=48, N=96, G=2, lens=[200, 133]), 64),
+    ("hpg8", dict(b=1, L=256, H=8, P=32, N=64, G=1), 128),
+    ("chunk96", dict(b=2, L=300, H=4, P=64, N=128, G=2, lens=[300, 95]), 96),
+    ("chunk32", dict(b=1, L=100, H=2, P=16, N=32, G=2, with_h=False), 32),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,shape,chunk", FAST_CASES, ids=[c[0] for c in FAST_CASES])
+def test_ssd_fwd_bf16_fast_path(name, shape, chunk):
+    print(f"ssd fwd fast {name} chunk={chunk}", flush=True)
+    x = make_inputs(dtype=torch.bfloat16, **shape)
+    y_ref, h_ref = ref.ssd_scan_forward(**x, chunk_size=chunk)
+    y, h = run_fwd(x, chunk)
+    assert_parity(y, y_ref, torch.bfloat16, "y")
+    assert_parity(h, h_ref, torch.bfloat16, "h_last")
