@@ -300,6 +300,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ssd-only", action="store_true", help="skip the decode / sparse lines")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="after the timed work, run 3 plain device copies of this many MiB "
+                         "(the reference kernel for scaling HBM counters read under rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -331,6 +334,14 @@ def main():
         out["sparse_attn"] = run_sparse(args, torch)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, args.cpu_budget_s)
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib << 18   # float32 elements
+        src = torch.ones(n, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        out["copy_probe_bytes"] = 4 * n
     print(json.dumps(out))
 
 

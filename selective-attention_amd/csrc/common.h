@@ -191,6 +191,40 @@ __device__ __forceinline__ uint2 col4_bf16(const uint4& r0, const uint4& r1, con
   return uint2{__builtin_amdgcn_perm(a1, a0, sel), __builtin_amdgcn_perm(a3, a2, sel)};
 }
 
+// fp32 pair (a, b) of 4+4 values as two bf16 fragments: hi = bf16(x) and
+// lo = bf16(x - hi), so that hi + lo carries ~16 mantissa bits into an MFMA
+__device__ __forceinline__ void split_p(const v4f& a, const v4f& b, v8bf& hi, v8bf& lo) {
+  const uint4 h = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]),
+                   pack_bf16x2(b[2], b[3])};
+  const uint4 l = {pack_bf16x2(a[0] - bf16lo_to_f32(h.x), a[1] - bf16hi_to_f32(h.x)),
+                   pack_bf16x2(a[2] - bf16lo_to_f32(h.y), a[3] - bf16hi_to_f32(h.y)),
+                   pack_bf16x2(b[0] - bf16lo_to_f32(h.z), b[1] - bf16hi_to_f32(h.z)),
+                   pack_bf16x2(b[2] - bf16lo_to_f32(h.w), b[3] - bf16hi_to_f32(h.w))};
+  hi = __builtin_bit_cast(v8bf, h);
+  lo = __builtin_bit_cast(v8bf, l);
+}
+// 8 consecutive fp32 (two float4) as hi / lo bf16 fragments
+__device__ __forceinline__ void split8(const float4& a, const float4& b, v8bf& hi, v8bf& lo) {
+  split_p(v4f{a.x, a.y, a.z, a.w}, v4f{b.x, b.y, b.z, b.w}, hi, lo);
+}
+
+// LDS transpose read (ds_read_b64_tr_b16).  `x` points at element [k0][c0]
+// of a row-major bf16 LDS tile with row length ld (elements, ld*2 a multiple
+// of 8 bytes); every lane of a 16-lane group receives the column
+// x[k0 .. k0+7][c0 + (lane & 15)] -- the MFMA operand fragment for a
+// contraction over the tile's rows.  Within a 16-lane group, lane i loads the
+// 4 elements at [k0 + i/4][c0 + 4(i%4)] and the hardware hands lane j the
+// elements [k0 + m][c0 + j], m = 0..3.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v8bf lds_tr8(const bf16* x, int ld, int lane) {
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const int i = lane & 15;
+  const bf16* p = x + (i >> 2) * ld + 4 * (i & 3);
+  const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p));
+  const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + 4 * ld));
+  return __builtin_bit_cast(v8bf, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // key (within a 64-key tile) held by MFMA row c of score tile kt
 __device__ __forceinline__ int key_of_row(int kt, int c) {
   return 32 * (kt >> 1) + 8 * (c >> 2) + 4 * (kt & 1) + (c & 3);

@@ -80,7 +80,7 @@ inline BwdWs bwd_layout(const SsdDims& d, size_t /*mt_bytes*/) {
   w.ddt_part = o;  o = al256(o + bhc * w.ptiles * d.Lc * 4);
   w.xB_part = o;   o = al256(o + bhc * w.ntiles * d.Lc * 4);
   w.xC_part = o;   o = al256(o + bhc * w.ntiles * d.Lc * 4);
-  w.rsum = o;      o = al256(o + bhc * d.Lc * 4);
+  w.rsum = o;      o = al256(o + bhc * w.ttiles * d.Lc * 4);
   w.qpart = o;     o = al256(o + bhc * w.ttiles * d.Lc * 4);
   w.ddc_part = o;  o = al256(o + bhc * w.per_bh * 4);
   w.dA_part = o;   o = al256(o + bhc * 4);
@@ -689,8 +689,8 @@ __global__ __launch_bounds__(256) void chunk_cumsum_bwd_kernel(
     const float* __restrict__ xB_part, const float* __restrict__ xC_part,
     const float* __restrict__ rsum, const float* __restrict__ qpart,
     const float* __restrict__ ddc_part, T* __restrict__ ddelta_raw, float* __restrict__ dA_part,
-    float* __restrict__ db_part, SsdDims d, int ptiles, int ntiles, int ttiles, int per_bh,
-    int has_init, int softplus, float lo, float hi) {
+    float* __restrict__ db_part, SsdDims d, int ptiles, int ntiles, int ttiles, int rtiles,
+    int per_bh, int has_init, int softplus, float lo, float hi) {
   __shared__ float wtot[4];
   const int h = blockIdx.x % d.H;
   const int c = (blockIdx.x / d.H) % d.nc;
@@ -722,7 +722,10 @@ __global__ __launch_bounds__(256) void chunk_cumsum_bwd_kernel(
         x1 += xB_part[(bhc * ntiles + k) * d.Lc + t];
         x2 += xC_part[(bhc * ntiles + k) * d.Lc + t];
       }
-      qr[j] = q - rsum[crow + t];
+      // row sums: partials of the source tiles k <= t / 64 (rtiles == 1: complete)
+      float r = 0.f;
+      for (int k = 0; k < rtiles && 64 * k <= t; ++k) r += rsum[(bhc * rtiles + k) * d.Lc + t];
+      qr[j] = q - r;
       xb[j] = t < lim - 1 ? x1 : 0.f;
       xc[j] = (t < lim ? x2 : 0.f) + (t == d.Lc - 1 ? ddc : 0.f);
     }
@@ -863,6 +866,15 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
                        dh_last, dh_init, dc, ddc_part, d);
     SA_CHECK_LAUNCH("state_passing_bwd");
   }
+  int ptiles = w.ptiles, ntiles = w.ntiles, qtiles = w.ttiles, rtiles = 1;
+  if (sizeof(T) == 2 && ssd_bwd_fused_ok(d, u, Bm, Cm, dy)) {
+    // 3-5 fused: du, dB, dC, decay sums
+    if ((rc = launch_ssd_bwd_fused(u, Bm, Cm, dy, dt, dc, states, dS, length, du_, dB_, dC_, dCB,
+                                   ddt_part, xB_part, xC_part, qpart, rsum, d, s)))
+      return rc;
+    ptiles = ntiles = qtiles = 1;
+    rtiles = d.Lc / 64;
+  } else {
   // 3. du, ddt_direct
   {
     const size_t smem = du_smem<MT>(d);
@@ -893,6 +905,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
                        xB_part, xC_part, d, vec_act, vec_dy, vec_f32, vec_dcb);
     SA_CHECK_LAUNCH("chunk_dbdc_bwd");
   }
+  }
   // 6. decay-gradient assembly, d delta_raw, dA/dbias partials
   {
     const long blocks = bnc * d.H;
@@ -900,7 +913,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
     hipLaunchKernelGGL(chunk_cumsum_bwd_kernel<T>, dim3(blocks), dim3(256), 0, s,
                        static_cast<const T*>(delta_raw_), A, bias, length, dt, ddt_part, xB_part,
                        xC_part, rsum, qpart, ddc_part, static_cast<T*>(ddelta_), dA_part, db_part,
-                       d, w.ptiles, w.ntiles, w.ttiles, w.per_bh, has_init, sp, lo, hi);
+                       d, ptiles, ntiles, qtiles, rtiles, w.per_bh, has_init, sp, lo, hi);
     SA_CHECK_LAUNCH("chunk_cumsum_bwd");
   }
   // 7. dA, dbias

@@ -1,0 +1,817 @@
+// SSD chunked scan backward: fused bf16 path for headdim 64 (gfx950).
+//
+// Replaces, for bf16 activations with headdim 64, state_dim 64 or 128,
+// chunk_size a multiple of 64 and at most 4 heads per group, the reference's
+// intra-chunk backward kernels (triton_kernels/ssd_scan/backward_kernel.py:
+// _chunk_scan_bwd_dx :187-317, _chunk_scan_bwd_dcb :569-668, the dC/dB
+// kernels :337-551 and the decay-gradient sums :689-765, :783-911) with two
+// kernels:
+//
+//   ssd_bwd_col (one block per (b, c, group, 64-wide source tile sigma)):
+//     du, ddt_direct, dB (intra + state), x_B, the column sums q of
+//     M = W o CB and per-tile partial row sums r, and the dCB tiles
+//     (fp32, read by ssd_bwd_row).
+//   ssd_bwd_row (one block per (b, c, group, 64-wide target tile tau)):
+//     dC (state + intra through dCB) and x_C.
+//
+// Wave w of a block owns 16 columns (sigma or tau = 16w + (lane & 15)).  All
+// tile products use the 16x16x32 bf16 MFMA.  A product's result fragment
+// (rows in registers, column on the lane) is fed straight back as the B
+// operand of the next product that contracts over those rows; rows are
+// visited through key_of_row so that each lane's 8 rows are consecutive.
+// Operands that must be read along their rows *and* along their columns
+// (dy, C, dS, H_in, B) are staged once, row-major, in LDS: row reads give one
+// orientation, ds_read_b64_tr_b16 (lds_tr8) the other.
+//
+// fp32-origin operands (dy, dS, H_in, the decayed C.B^T and dCB) are carried
+// as hi + lo bf16 planes, products as hi*hi + lo*hi + hi*lo (or hi*x + lo*x
+// against an exact bf16 operand), as in the generic kernels.
+//
+// Staging is a flat list of "stages" (one 64 x 64 fp32 tile -> hi/lo bf16,
+// plus a bf16 C or B tile on some stages).  The global loads of stage i+1 are
+// issued before the MFMAs of stage i and written to the other LDS slot after
+// them, so one barrier per stage orders the pipeline.
+#include "ssd_common.h"
+#include "prof.h"
+
+namespace sa {
+namespace {
+
+constexpr int kLY = 72;             // row length of a 64 x 64 bf16 staging plane
+constexpr int kPlane = 64 * kLY;    // elements per plane; a slot holds hi then lo
+
+// ---------------------------------------------------------------------------
+// staging helpers (256 threads).  Rows past `rows_valid` read a clamped (valid)
+// row and are zeroed afterwards, so the loads are unconditional.
+// ---------------------------------------------------------------------------
+// 64 x 64 fp32 tile, thread share: row tid/4, 16 columns from 16*(tid%4)
+__device__ __forceinline__ void f32_tile_load(float4 (&r)[4], const float* src, int rs,
+                                              int rows_valid, int tid) {
+  const int row = tid >> 2, c0 = 16 * (tid & 3);
+  const float* p = src + static_cast<unsigned>(min(row, rows_valid - 1) * rs + c0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = *reinterpret_cast<const float4*>(p + 4 * i);
+  if (row >= rows_valid) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+__device__ __forceinline__ void f32_tile_commit(bf16* slot, const float4 (&r)[4], int tid) {
+  const int row = tid >> 2, c0 = 16 * (tid & 3);
+  uint32_t hi[8], lo[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float v[4] = {r[i].x, r[i].y, r[i].z, r[i].w};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t h = pack_bf16x2(v[2 * j], v[2 * j + 1]);
+      hi[2 * i + j] = h;
+      lo[2 * i + j] = pack_bf16x2(v[2 * j] - bf16lo_to_f32(h), v[2 * j + 1] - bf16hi_to_f32(h));
+    }
+  }
+  uint4* ph = reinterpret_cast<uint4*>(slot + row * kLY + c0);
+  uint4* pl = reinterpret_cast<uint4*>(slot + kPlane + row * kLY + c0);
+  ph[0] = uint4{hi[0], hi[1], hi[2], hi[3]};
+  ph[1] = uint4{hi[4], hi[5], hi[6], hi[7]};
+  pl[0] = uint4{lo[0], lo[1], lo[2], lo[3]};
+  pl[1] = uint4{lo[4], lo[5], lo[6], lo[7]};
+}
+// 64 x (32 NK) bf16 tile, raw 16-byte copies
+template <int NK>
+__device__ __forceinline__ void bf_tile_load(uint4 (&r)[NK], const bf16* src, int rs,
+                                             int rows_valid, int tid) {
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    const int v = tid + 256 * i;
+    const int row = v / (4 * NK), c8 = v % (4 * NK);
+    r[i] = *reinterpret_cast<const uint4*>(src + static_cast<unsigned>(min(row, rows_valid - 1) * rs + 8 * c8));
+    if (row >= rows_valid) r[i] = uint4{0u, 0u, 0u, 0u};
+  }
+}
+template <int NK>
+__device__ __forceinline__ void bf_tile_commit(bf16* dst, int ld, const uint4 (&r)[NK], int tid) {
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    const int v = tid + 256 * i;
+    const int row = v / (4 * NK), c8 = v % (4 * NK);
+    *reinterpret_cast<uint4*>(dst + row * ld + 8 * c8) = r[i];
+  }
+}
+// 8 consecutive fp32 at p + 32 ks (ks = 0, 1): two k-steps of an MFMA operand
+__device__ __forceinline__ void f32_frag_load(float4 (&r)[4], const float* p, bool ok) {
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    r[2 * ks] = *reinterpret_cast<const float4*>(p + 32 * ks);
+    r[2 * ks + 1] = *reinterpret_cast<const float4*>(p + 32 * ks + 4);
+  }
+  if (!ok) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+__device__ __forceinline__ uint2 pack4_bf16(const v4f& v) {
+  return uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+}
+__device__ __forceinline__ float dot4_bf16(const v4f& a, const uint2& q) {
+  return a[0] * bf16lo_to_f32(q.x) + a[1] * bf16hi_to_f32(q.x) + a[2] * bf16lo_to_f32(q.y) +
+         a[3] * bf16hi_to_f32(q.y);
+}
+// sum over the 4 lane groups (lanes l, l^16, l^32, l^48)
+__device__ __forceinline__ float group_sum(float v) {
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// DPP lane exchange inside rows of 16 lanes (VALU only, no LDS traffic)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Row sums across the 16 lanes of each lane group: lane li of the group
+// returns sum over the group's lanes of v[li].  Each step pairs lanes that
+// differ in one bit of li (row_mirror: bit 3, row_half_mirror: bit 2,
+// quad_perm 3210: bit 1, quad_perm 1032: bit 0; the partner also holds the
+// same absolute indices because it agrees on the bits already consumed) and
+// keeps the half of the values selected by that bit.
+__device__ __forceinline__ float transpose_reduce16(float (&m)[16], int li) {
+  {
+    const bool up = li & 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float a = m[j] + dpp_f<0x140>(m[j]), b = m[j + 8] + dpp_f<0x140>(m[j + 8]);
+      m[j] = up ? b : a;
+    }
+  }
+  {
+    const bool up = li & 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = m[j] + dpp_f<0x141>(m[j]), b = m[j + 4] + dpp_f<0x141>(m[j + 4]);
+      m[j] = up ? b : a;
+    }
+  }
+  {
+    const bool up = li & 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float a = m[j] + dpp_f<0x1B>(m[j]), b = m[j + 2] + dpp_f<0x1B>(m[j + 2]);
+      m[j] = up ? b : a;
+    }
+  }
+  const bool up = li & 1;
+  const float a = m[0] + dpp_f<0xB1>(m[0]), b = m[1] + dpp_f<0xB1>(m[1]);
+  return up ? b : a;
+}
+
+// ---------------------------------------------------------------------------
+// column kernel
+// ---------------------------------------------------------------------------
+template <int NK, int HPG>
+struct ColSmem {
+  static constexpr int N = 32 * NK, LDC = N + 8;
+  static constexpr size_t kC = 64 * LDC;           // bf16 elements of a C or B tile
+  static constexpr size_t bytes = 2 * kC * 2 + 2 * 2 * kPlane * 2 + 2 * 64 * 4 + 2 * 4 * 64 * 4;
+};
+
+template <int NK, int HPG>
+__global__ __launch_bounds__(256, 2) void ssd_bwd_col_kernel(
+    const bf16* __restrict__ u, const bf16* __restrict__ Bm, const bf16* __restrict__ Cm,
+    const float* __restrict__ dy, const float* __restrict__ dt, const float* __restrict__ dc,
+    const float* __restrict__ dS, const int64_t* __restrict__ length, bf16* __restrict__ du,
+    bf16* __restrict__ dB, float* __restrict__ dCB, float* __restrict__ ddt_part,
+    float* __restrict__ xB_part, float* __restrict__ qpart, float* __restrict__ rpart, SsdDims d) {
+  using SM = ColSmem<NK, HPG>;
+  constexpr int N = SM::N, LDC = SM::LDC;
+  constexpr int NH = N / 64;                 // 64-wide n halves of a dS tile
+  constexpr int NT = N / 16;                 // 16-row n tiles of dB^T
+  constexpr int HP = HPG < 2 ? HPG : 2;      // heads per pass (du accumulators held)
+  constexpr int NPASS = (HPG + HP - 1) / HP;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  bf16* Bs = reinterpret_cast<bf16*>(smem_raw);   // [64][LDC]  B rows of this source tile
+  bf16* Cs = Bs + SM::kC;                         // [64][LDC]  C rows of the current target tile
+  bf16* Yb = Cs + SM::kC;                         // [2 slots][2 planes][64][kLY]
+  float* dcs = reinterpret_cast<float*>(Yb + 2 * 2 * kPlane);  // [2][64] dc (log2) of a stage
+  float* rW = dcs + 2 * 64;                                     // [2][4 waves][64]
+
+  const int stiles = d.Lc / 64;
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int S = bid % stiles;
+  int rest = bid / stiles;
+  const int g = rest % d.G;
+  rest /= d.G;
+  const int c = rest % d.nc;
+  const int b = rest / d.nc;
+  const int s0 = 64 * S;
+  const int qlim = min(d.Lc, d.L - c * d.Lc);
+  const int len = seq_limit(length, b, d.L);
+  const int lim = max(0, chunk_limit(len, c, d.Lc));
+  const long tok0 = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc;
+  const int u_rs = d.H * 64, act_rs = d.G * N;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lg = lane >> 4, li = lane & 15;
+  const int sig = s0 + 16 * w + li;   // this lane's source position
+  const int h0 = g * HPG;
+  const long bhc0 = (static_cast<long>(b) * d.H + h0) * d.nc + c;  // bhc of head k: bhc0 + k nc
+  // block-uniform bases; per-lane offsets below are 32-bit
+  const bf16* uc = u + tok0 * u_rs + h0 * 64;                       // [Lc][H*64] from head h0
+  const bf16* Bc = Bm + tok0 * act_rs + static_cast<long>(g) * N;   // [Lc][G*N]
+  const bf16* Cc = Cm + tok0 * act_rs + static_cast<long>(g) * N;
+  const float* dyc = dy + tok0 * u_rs + h0 * 64;
+  const float* dSc = dS + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (64L * N);  // [HPG][64][N]
+  const float* dcc = dc + bhc0 * d.Lc;   // head k: + k nc Lc
+  const float* dtc = dt + bhc0 * d.Lc;
+  const int hstride = d.nc * d.Lc;       // dc / dt / partial rows between heads
+  bf16* duc = du + tok0 * u_rs + h0 * 64;
+  bf16* dBc = dB + tok0 * act_rs + static_cast<long>(g) * N;
+  float* dcbc = dCB + ((static_cast<long>(b) * d.nc + c) * d.G + g) * d.Lc * d.Lc;
+  float* ddtc = ddt_part + bhc0 * d.Lc;
+  float* xBc = xB_part + bhc0 * d.Lc;
+  float* qc = qpart + bhc0 * d.Lc;
+  float* rc = rpart + (bhc0 * stiles + S) * d.Lc;   // head k: + k nc stiles Lc
+  const int rstride = d.nc * stiles * d.Lc;
+
+  if (s0 >= lim) {  // nothing of this source tile is inside the length: zero outputs / partials
+    for (int e = tid; e < 64 * HPG * 8; e += 256) {
+      const int row = e / (HPG * 8), col8 = e % (HPG * 8);
+      if (s0 + row < qlim)
+        *reinterpret_cast<uint4*>(duc + static_cast<unsigned>((s0 + row) * u_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
+    }
+    for (int e = tid; e < 64 * (N / 8); e += 256) {
+      const int row = e / (N / 8), col8 = e % (N / 8);
+      if (s0 + row < qlim)
+        *reinterpret_cast<uint4*>(dBc + static_cast<unsigned>((s0 + row) * act_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
+    }
+    for (int k = 0; k < HPG; ++k) {
+      for (int e = tid; e < 64; e += 256) {
+        ddtc[k * hstride + s0 + e] = 0.f;
+        xBc[k * hstride + s0 + e] = 0.f;
+        qc[k * hstride + s0 + e] = 0.f;
+      }
+      for (int t = s0 + tid; t < d.Lc; t += 256) rc[k * rstride + t] = 0.f;
+    }
+    return;
+  }
+
+  const bool sv = sig < lim;
+  const int scl = min(sig, lim - 1);                    // clamped source row (valid address)
+  const bf16* Bl = Bs + (16 * w + li) * LDC + 8 * lg;   // this lane's B row (operand fragments)
+  const int tend = (lim + 63) / 64;   // target tiles inside the length
+
+  v4f dBT[NT];      // dB^T (rows n = 16 nt + 4 lg + r, column sig), all heads
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) dBT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // ---- stage prefetch registers ----
+  float4 pf[4];
+  uint4 pc[NK];
+  uint4 pu[2];
+  float pdc = 0.f;
+  v8bf uf[2];
+  const unsigned uoff = static_cast<unsigned>(scl * u_rs + 8 * lg);
+  auto load_u = [&](int k) {
+    const bf16* urow = uc + k * 64;
+    pu[0] = *reinterpret_cast<const uint4*>(urow + uoff);
+    pu[1] = *reinterpret_cast<const uint4*>(urow + uoff + 32);
+    if (!sv) pu[0] = pu[1] = uint4{0u, 0u, 0u, 0u};
+  };
+  auto load_state = [&](int k, int half) {
+    load_u(k);
+    f32_tile_load(pf, dSc + k * (64 * N) + 64 * half, N, 64, tid);
+  };
+  auto load_intra = [&](int T, int k, bool with_c) {
+    load_u(k);
+    const int t0 = 64 * T;
+    const int rv = min(64, lim - t0);
+    f32_tile_load(pf, dyc + t0 * u_rs + k * 64, u_rs, rv, tid);
+    if (with_c) bf_tile_load<NK>(pc, Cc + t0 * act_rs, act_rs, rv, tid);
+    pdc = dcc[k * hstride + t0 + (tid & 63)] * kLog2e;
+  };
+  auto commit = [&](int slot, bool intra, bool with_c) {
+    f32_tile_commit(Yb + slot * 2 * kPlane, pf, tid);
+    if (intra) {
+      if (with_c) bf_tile_commit<NK>(Cs, LDC, pc, tid);
+      if (tid < 64) dcs[slot * 64 + tid] = pdc;
+    }
+  };
+  auto take_u = [&]() {
+    uf[0] = __builtin_bit_cast(v8bf, pu[0]);
+    uf[1] = __builtin_bit_cast(v8bf, pu[1]);
+  };
+  // row partials of an intra stage are summed over the 4 waves one stage later
+  int pend_slot = -1, pend_k = 0, pend_T = 0;
+  auto flush_r = [&]() {
+    if (pend_slot >= 0 && tid < 64) {
+      const float* r = rW + pend_slot * 256;
+      rc[pend_k * rstride + 64 * pend_T + tid] = r[tid] + r[64 + tid] + r[128 + tid] + r[192 + tid];
+    }
+    pend_slot = -1;
+  };
+
+  // B rows of the source tile (kept for the whole block) and the first stage
+  bf_tile_load<NK>(pc, Bc + s0 * act_rs, act_rs, min(64, lim - s0), tid);
+  bf_tile_commit<NK>(Bs, LDC, pc, tid);
+  load_state(0, 0);
+  commit(0, false, false);
+  take_u();
+  __syncthreads();
+  int idx = 0;   // running stage index (LDS slot parity)
+
+#pragma unroll
+  for (int pass = 0; pass < NPASS; ++pass) {
+    const int kb = pass * HP;                       // first head of the pass
+    constexpr int HPmax = HP;
+    const int hp = (HPG - kb) < HP ? (HPG - kb) : HP;   // heads in this pass (compile-time)
+    v4f duT[HPmax][4];  // du^T (rows p = 16 pt + 4 lg + r, column sig), before the dt factor
+    float qacc[HPmax];
+#pragma unroll
+    for (int kk = 0; kk < HPmax; ++kk) {
+      qacc[kk] = 0.f;
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) duT[kk][pt] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // ---- state stages of the pass: (head, n half): du^T += dS B^T ; dB^T += w dS^T u^T ----
+#pragma unroll
+    for (int j = 0; j < NH * HPmax; ++j) {
+      if (j >= NH * hp) break;
+      const int kk = j / NH, half = j % NH, k = kb + kk;
+      if (j + 1 < NH * hp) load_state(k + (j + 1) / NH - kk, (j + 1) % NH);
+      else load_intra(S, kb, true);
+      flush_r();
+      const bf16* Yh = Yb + (idx & 1) * 2 * kPlane;
+      const bf16* Yl = Yh + kPlane;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const v8bf bb = load_v8bf(Bl + 64 * half + 32 * ks);
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) {
+          const int off = (16 * pt + li) * kLY + 32 * ks + 8 * lg;
+          duT[kk][pt] = mfma_bf16(load_v8bf(Yh + off), bb, duT[kk][pt]);
+          duT[kk][pt] = mfma_bf16(load_v8bf(Yl + off), bb, duT[kk][pt]);
+        }
+      }
+      const float dcl = dcc[k * hstride + d.Lc - 1] * kLog2e;
+      const float dck = dcc[k * hstride + scl] * kLog2e;
+      const float dtk = dtc[k * hstride + scl];
+      const float e = sv ? fast_exp2(fminf(dcl - dck, 0.f)) : 0.f;
+      const float wk = e * dtk;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        v4f tmp = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const int off = (32 * ks + 8 * lg) * kLY + 16 * nt;
+          tmp = mfma_bf16(lds_tr8(Yh + off, kLY, lane), uf[ks], tmp);
+          tmp = mfma_bf16(lds_tr8(Yl + off, kLY, lane), uf[ks], tmp);
+        }
+        dBT[4 * half + nt] += tmp * wk;
+      }
+      if (half == NH - 1) {
+        // head k's state part is complete: scale by e^{dc_last - dc_sig}; x_B
+        const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
+        float s = 0.f;
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) {
+          duT[kk][pt] *= e;
+          s += dot4_bf16(duT[kk][pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
+        }
+        s = group_sum(sv ? s : 0.f) * dtk;
+        if (lg == 0) xBc[k * hstride + sig] = s;
+      }
+      commit((idx + 1) & 1, j + 1 >= NH * hp, j + 1 >= NH * hp);
+      ++idx;
+      __syncthreads();
+      take_u();
+    }
+
+    // ---- intra stages of the pass: (target tile T, head) ----
+    for (int T = S; T < tend; ++T) {
+      const int t0 = 64 * T;
+      const bool diag = T == S || t0 + 64 > lim;   // tile needs the causal / length masks
+      v4f CB[4], dCBa[4];
+#pragma unroll
+      for (int kk = 0; kk < HPmax; ++kk) {
+        if (kk >= hp) break;
+        const int k = kb + kk;
+        const bool last_pass = pass == NPASS - 1;
+        const bool last_stage = last_pass && kk == hp - 1 && T + 1 == tend;
+        // prefetch the next stage: next head, next tile, or the next pass's first state stage
+        if (kk + 1 < hp) load_intra(T, k + 1, false);
+        else if (T + 1 < tend) load_intra(T + 1, kb, true);
+        else if (!last_pass) load_state(kb + HP, 0);
+        flush_r();
+        const int slot = idx & 1;
+        const bf16* Yh = Yb + slot * 2 * kPlane;
+        const bf16* Yl = Yh + kPlane;
+        const float* dcT = dcs + slot * 64;
+        if (kk == 0) {
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) {
+            CB[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+            dCBa[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+          }
+#pragma unroll
+          for (int ks = 0; ks < NK; ++ks) {
+            const v8bf bb = load_v8bf(Bl + 32 * ks);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+              CB[kt] = mfma_bf16(load_v8bf(Cs + key_of_row(kt, li) * LDC + 8 * lg + 32 * ks), bb, CB[kt]);
+          }
+        }
+        // W[t, sig] = dy[t] . u[sig]
+        v4f W[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          W[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+          const int off = key_of_row(kt, li) * kLY + 8 * lg;
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            W[kt] = mfma_bf16(load_v8bf(Yh + off + 32 * ks), uf[ks], W[kt]);
+            W[kt] = mfma_bf16(load_v8bf(Yl + off + 32 * ks), uf[ks], W[kt]);
+          }
+        }
+        // decay and masks; dCB += W', M = W' o CB (q: column sums, r: row sums); W <- L
+        const float dck = dcc[k * hstride + scl] * kLog2e;
+        const float dtk = sv ? dtc[k * hstride + scl] : 0.f;
+        float m[16];
+        float qs = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);   // first of 4 consecutive rows
+          const float4 dq = *reinterpret_cast<const float4*>(dcT + tb);
+          const float dv[4] = {dq.x, dq.y, dq.z, dq.w};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float dec = fast_exp2(fminf(dv[r] - dck, 0.f));
+            if (diag) {
+              const int t = t0 + tb + r;
+              dec = (t >= sig && t < lim) ? dec : 0.f;
+            }
+            const float wv = W[kt][r] * dtk * dec;
+            dCBa[kt][r] += wv;
+            float mv = wv * CB[kt][r];
+            if (diag) mv = (t0 + tb + r > sig) ? mv : 0.f;
+            m[4 * kt + r] = mv;
+            qs += mv;
+            W[kt][r] = CB[kt][r] * dec;
+          }
+        }
+        qacc[kk] += qs;
+        rW[slot * 256 + w * 64 + key_of_row(li >> 2, 4 * lg + (li & 3))] = transpose_reduce16(m, li);
+        pend_slot = slot;
+        pend_k = k;
+        pend_T = T;
+        // du^T[p, sig] += sum_t dy[t, p] L[t, sig]
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          v8bf lh, ll;
+          split_p(W[2 * ks], W[2 * ks + 1], lh, ll);
+#pragma unroll
+          for (int pt = 0; pt < 4; ++pt) {
+            const int off = (32 * ks + 8 * lg) * kLY + 16 * pt;
+            const v8bf ah = lds_tr8(Yh + off, kLY, lane);
+            const v8bf al = lds_tr8(Yl + off, kLY, lane);
+            duT[kk][pt] = mfma_bf16(ah, lh, duT[kk][pt]);
+            duT[kk][pt] = mfma_bf16(al, lh, duT[kk][pt]);
+            duT[kk][pt] = mfma_bf16(ah, ll, duT[kk][pt]);
+          }
+        }
+        const bool next_c = kk == hp - 1 && !last_stage;   // the next stage replaces Cs
+        float* dcbt = dcbc + t0 * d.Lc;                      // rows of tile T
+        if (kk == hp - 1) {
+          // this pass's heads are done with tile T: dCB partial; on the last pass the
+          // full dCB feeds dB^T[n, sig] += sum_t C[t, n] dCB[t, sig]
+          if (!last_pass) {
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                dcbt[static_cast<unsigned>(key_of_row(kt, 4 * lg + r) * d.Lc + sig)] = dCBa[kt][r];
+          } else {
+            if (NPASS > 1) {
+#pragma unroll
+              for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  dCBa[kt][r] += dcbt[static_cast<unsigned>(key_of_row(kt, 4 * lg + r) * d.Lc + sig)];
+            }
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+              v8bf dh, dl;
+              split_p(dCBa[2 * ks], dCBa[2 * ks + 1], dh, dl);
+#pragma unroll
+              for (int nt = 0; nt < NT; ++nt) {
+                const v8bf a = lds_tr8(Cs + (32 * ks + 8 * lg) * LDC + 16 * nt, LDC, lane);
+                dBT[nt] = mfma_bf16(a, dh, dBT[nt]);
+                dBT[nt] = mfma_bf16(a, dl, dBT[nt]);
+              }
+            }
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                dcbt[static_cast<unsigned>(key_of_row(kt, 4 * lg + r) * d.Lc + sig)] = dCBa[kt][r];
+          }
+          if (next_c) __syncthreads();   // every wave is done with Cs before the next tile lands
+        }
+        if (!last_stage) {
+          const bool next_intra = kk + 1 < hp || T + 1 < tend;
+          commit((idx + 1) & 1, next_intra, next_c && next_intra);
+        }
+        ++idx;
+        __syncthreads();
+        if (!last_stage) take_u();
+      }
+    }
+
+    // ---- pass epilogue: du, ddt_direct, q of the pass's heads ----
+#pragma unroll
+    for (int kk = 0; kk < HPmax; ++kk) {
+      if (kk >= hp) break;
+      const int k = kb + kk;
+      const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
+      const float dtk = sv ? dtc[k * hstride + scl] : 0.f;
+      float s = 0.f;
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) s += dot4_bf16(duT[kk][pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
+      s = group_sum(sv ? s : 0.f);
+      const float q = group_sum(qacc[kk]);
+      if (sig < qlim) {
+        bf16* durow = duc + k * 64 + static_cast<unsigned>(sig * u_rs + 4 * lg);
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) *reinterpret_cast<uint2*>(durow + 16 * pt) = pack4_bf16(duT[kk][pt] * dtk);
+      }
+      if (lg == 0) {
+        ddtc[k * hstride + sig] = s;
+        qc[k * hstride + sig] = q;
+      }
+      for (int t = 64 * tend + tid; t < d.Lc; t += 256) rc[k * rstride + t] = 0.f;
+    }
+  }
+  flush_r();
+  if (sig < qlim) {
+    bf16* dbrow = dBc + static_cast<unsigned>(sig * act_rs + 4 * lg);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<uint2*>(dbrow + 16 * nt) = pack4_bf16(dBT[nt]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// row kernel: dC and x_C
+// ---------------------------------------------------------------------------
+template <int NK>
+struct RowSmem {
+  static constexpr int N = 32 * NK, LDC = N + 8;
+  static constexpr size_t slot_elems = (2 * kPlane > 64 * LDC) ? 2 * kPlane : 64 * LDC;
+  static constexpr size_t bytes = 2 * slot_elems * 2;
+};
+
+template <int NK, int HPG>
+__global__ __launch_bounds__(256, 2) void ssd_bwd_row_kernel(
+    const bf16* __restrict__ Bm, const bf16* __restrict__ Cm, const float* __restrict__ dy,
+    const float* __restrict__ dc, const float* __restrict__ states, const float* __restrict__ dCB,
+    const int64_t* __restrict__ length, bf16* __restrict__ dC, float* __restrict__ xC_part,
+    SsdDims d) {
+  using SM = RowSmem<NK>;
+  constexpr int N = SM::N, LDC = SM::LDC;
+  constexpr int NH = N / 64, NT = N / 16;
+  constexpr int nS = NH * HPG;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  bf16* slots = reinterpret_cast<bf16*>(smem_raw);  // [2][slot_elems]
+
+  const int ttiles = d.Lc / 64;
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int T = bid % ttiles;
+  int rest = bid / ttiles;
+  const int g = rest % d.G;
+  rest /= d.G;
+  const int c = rest % d.nc;
+  const int b = rest / d.nc;
+  const int t0 = 64 * T;
+  const int qlim = min(d.Lc, d.L - c * d.Lc);
+  const int len = seq_limit(length, b, d.L);
+  const int lim = max(0, chunk_limit(len, c, d.Lc));
+  const long tok0 = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc;
+  const int u_rs = d.H * 64, act_rs = d.G * N;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lg = lane >> 4, li = lane & 15;
+  const int tau = t0 + 16 * w + li;
+  const int h0 = g * HPG;
+  const long bhc0 = (static_cast<long>(b) * d.H + h0) * d.nc + c;
+  const int hstride = d.nc * d.Lc;
+  // block-uniform bases; per-lane offsets below are 32-bit
+  const bf16* Bc = Bm + tok0 * act_rs + static_cast<long>(g) * N;
+  const bf16* Cc = Cm + tok0 * act_rs + static_cast<long>(g) * N;
+  const float* dyc = dy + tok0 * u_rs + h0 * 64;
+  const float* Hc = states + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (64L * N);
+  const float* dcc = dc + bhc0 * d.Lc;
+  const float* dcbc = dCB + ((static_cast<long>(b) * d.nc + c) * d.G + g) * d.Lc * d.Lc;
+  bf16* dCc = dC + tok0 * act_rs + static_cast<long>(g) * N;
+  float* xCc = xC_part + bhc0 * d.Lc;
+
+  if (t0 >= lim) {
+    for (int e = tid; e < 64 * (N / 8); e += 256) {
+      const int row = e / (N / 8), col8 = e % (N / 8);
+      if (t0 + row < qlim)
+        *reinterpret_cast<uint4*>(dCc + static_cast<unsigned>((t0 + row) * act_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
+    }
+    for (int k = 0; k < HPG; ++k)
+      for (int e = tid; e < 64; e += 256) xCc[k * hstride + t0 + e] = 0.f;
+    return;
+  }
+  const bool tv = tau < lim;
+  const int tcl = min(tau, lim - 1);
+  // C[tau, 16 nt + 4 lg + r] for x_C
+  uint2 Cq[NT];
+  {
+    const bf16* crow = Cc + static_cast<unsigned>(tcl * act_rs + 4 * lg);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) Cq[nt] = *reinterpret_cast<const uint2*>(crow + 16 * nt);
+  }
+  v4f dCT[NT], tmp[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) dCT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  float4 pf[4];   // state stage: H_in tile
+  uint4 pc[NK];   // intra stage: B tile
+  float4 pg[4];   // dy[tau] of a head (state) / dCB[tau] row piece (intra)
+  float4 cur[4];
+  const unsigned dcb_off = static_cast<unsigned>(tcl * d.Lc + 8 * lg);
+  const unsigned dy_off = static_cast<unsigned>(tcl * u_rs + 8 * lg);
+  auto load_state = [&](int k, int half) {
+    f32_tile_load(pf, Hc + k * (64 * N) + 64 * half, N, 64, tid);
+    if (half == 0) f32_frag_load(pg, dyc + k * 64 + dy_off, tv);
+  };
+  auto load_intra = [&](int S) {
+    const int s0 = 64 * S;
+    bf_tile_load<NK>(pc, Bc + s0 * act_rs, act_rs, min(64, lim - s0), tid);
+    f32_frag_load(pg, dcbc + s0 + dcb_off, tv);
+  };
+
+  load_state(0, 0);
+  f32_tile_commit(slots, pf, tid);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) cur[i] = pg[i];
+  __syncthreads();
+
+  // ---- state stages: tmp^T[n, tau] = sum_p H[p, n] dy[tau, p] ; dC^T += e tmp^T ; x_C ----
+#pragma unroll
+  for (int j = 0; j < nS; ++j) {
+    const int k = j / NH, half = j % NH;
+    if (j + 1 < nS) load_state((j + 1) / NH, (j + 1) % NH);
+    else load_intra(0);
+    const bf16* Yh = slots + (j & 1) * SM::slot_elems;
+    const bf16* Yl = Yh + kPlane;
+    v8bf fh[2], fl[2];
+    split8(cur[0], cur[1], fh[0], fl[0]);
+    split8(cur[2], cur[3], fh[1], fl[1]);
+    if (half == 0) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) tmp[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int off = (32 * ks + 8 * lg) * kLY + 16 * nt;
+        const v8bf ah = lds_tr8(Yh + off, kLY, lane);
+        const v8bf al = lds_tr8(Yl + off, kLY, lane);
+        tmp[4 * half + nt] = mfma_bf16(ah, fh[ks], tmp[4 * half + nt]);
+        tmp[4 * half + nt] = mfma_bf16(al, fh[ks], tmp[4 * half + nt]);
+        tmp[4 * half + nt] = mfma_bf16(ah, fl[ks], tmp[4 * half + nt]);
+      }
+    if (half == NH - 1) {
+      const float e = tv ? fast_exp2(dcc[k * hstride + tcl] * kLog2e) : 0.f;
+      float s = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        s += dot4_bf16(tmp[nt], Cq[nt]);
+        dCT[nt] += tmp[nt] * e;
+      }
+      s = group_sum(s) * e;
+      if (lg == 0) xCc[k * hstride + tau] = s;
+    }
+    if (j + 1 < nS) f32_tile_commit(slots + ((j + 1) & 1) * SM::slot_elems, pf, tid);
+    else bf_tile_commit<NK>(slots + ((j + 1) & 1) * SM::slot_elems, LDC, pc, tid);
+    if (j + 1 >= nS || (j + 1) % NH == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cur[i] = pg[i];
+    }
+    __syncthreads();
+  }
+
+  // ---- intra stages: dC^T[n, tau] += sum_sig B[sig, n] dCB[tau, sig], sig tiles S <= T ----
+  for (int S = 0; S <= T; ++S) {
+    const int idx = nS + S;
+    const bool has_next = S < T;
+    if (has_next) load_intra(S + 1);
+    const bf16* sl = slots + (idx & 1) * SM::slot_elems;
+    v8bf fh[2], fl[2];
+    split8(cur[0], cur[1], fh[0], fl[0]);
+    split8(cur[2], cur[3], fh[1], fl[1]);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const v8bf a = lds_tr8(sl + (32 * ks + 8 * lg) * LDC + 16 * nt, LDC, lane);
+        dCT[nt] = mfma_bf16(a, fh[ks], dCT[nt]);
+        dCT[nt] = mfma_bf16(a, fl[ks], dCT[nt]);
+      }
+    if (has_next) {
+      bf_tile_commit<NK>(slots + ((idx + 1) & 1) * SM::slot_elems, LDC, pc, tid);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cur[i] = pg[i];
+    }
+    __syncthreads();
+  }
+  if (tau < qlim) {
+    bf16* dcrow = dCc + static_cast<unsigned>(tau * act_rs + 4 * lg);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      *reinterpret_cast<uint2*>(dcrow + 16 * nt) = pack4_bf16(tv ? dCT[nt] : v4f{0.f, 0.f, 0.f, 0.f});
+  }
+}
+
+template <typename K>
+int allow_smem(K kernel, size_t bytes, const char* who) {
+  if (bytes <= 64 * 1024) return 0;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(bytes));
+  SA_CHECK_ARG(e == hipSuccess, "%s: %zu B of LDS refused: %s", who, bytes, hipGetErrorString(e));
+  return 0;
+}
+
+template <int NK, int HPG>
+int launch_fused(const bf16* u, const bf16* Bm, const bf16* Cm, const float* dy, const float* dt,
+                 const float* dc, const float* states, const float* dS, const int64_t* length,
+                 bf16* du, bf16* dB, bf16* dC, float* dCB, float* ddt_part, float* xB_part,
+                 float* xC_part, float* qpart, float* rpart, const SsdDims& d, hipStream_t s) {
+  const long blocks = static_cast<long>(d.b) * d.nc * d.G * (d.Lc / 64);
+  {
+    const size_t smem = ColSmem<NK, HPG>::bytes;
+    if (int rc = allow_smem(ssd_bwd_col_kernel<NK, HPG>, smem, "ssd_bwd_col")) return rc;
+    ProfScope prof_("ssd_bwd_col", s);
+    hipLaunchKernelGGL((ssd_bwd_col_kernel<NK, HPG>), dim3(blocks), dim3(256), smem, s, u, Bm, Cm,
+                       dy, dt, dc, dS, length, du, dB, dCB, ddt_part, xB_part, qpart, rpart, d);
+    SA_CHECK_LAUNCH("ssd_bwd_col");
+  }
+  {
+    const size_t smem = RowSmem<NK>::bytes;
+    if (int rc = allow_smem(ssd_bwd_row_kernel<NK, HPG>, smem, "ssd_bwd_row")) return rc;
+    ProfScope prof_("ssd_bwd_row", s);
+    hipLaunchKernelGGL((ssd_bwd_row_kernel<NK, HPG>), dim3(blocks), dim3(256), smem, s, Bm, Cm,
+                       dy, dc, states, dCB, length, dC, xC_part, d);
+    SA_CHECK_LAUNCH("ssd_bwd_row");
+  }
+  return 0;
+}
+
+template <int NK>
+int launch_fused_nk(int hpg, const bf16* u, const bf16* Bm, const bf16* Cm, const float* dy,
+                    const float* dt, const float* dc, const float* states, const float* dS,
+                    const int64_t* length, bf16* du, bf16* dB, bf16* dC, float* dCB,
+                    float* ddt_part, float* xB_part, float* xC_part, float* qpart, float* rpart,
+                    const SsdDims& d, hipStream_t s) {
+#define SA_FUSED_CASE(H)                                                                       \
+  case H:                                                                                      \
+    return launch_fused<NK, H>(u, Bm, Cm, dy, dt, dc, states, dS, length, du, dB, dC, dCB,     \
+                               ddt_part, xB_part, xC_part, qpart, rpart, d, s);
+  switch (hpg) {
+    SA_FUSED_CASE(1)
+    SA_FUSED_CASE(2)
+    SA_FUSED_CASE(3)
+    SA_FUSED_CASE(4)
+  }
+#undef SA_FUSED_CASE
+  SA_CHECK_ARG(false, "ssd_bwd fused path: %d heads per group unsupported", hpg);
+  return 1;
+}
+
+}  // namespace
+
+bool ssd_bwd_fused_ok(const SsdDims& d, const void* u, const void* B, const void* C,
+                      const void* dy) {
+  const int hpg = d.H / d.G;
+  return d.P == 64 && (d.N == 64 || d.N == 128) && d.Lc % 64 == 0 && hpg >= 1 && hpg <= 4 &&
+         aligned16(u) && aligned16(B) && aligned16(C) && aligned16(dy);
+}
+
+int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const float* dy,
+                         const float* dt, const float* dc, const float* states, const float* dS,
+                         const int64_t* length, void* du, void* dB, void* dC, float* dCB,
+                         float* ddt_part, float* xB_part, float* xC_part, float* qpart,
+                         float* rpart, const SsdDims& d, hipStream_t s) {
+  const int hpg = d.H / d.G;
+  const bf16* u_ = static_cast<const bf16*>(u);
+  const bf16* B_ = static_cast<const bf16*>(B);
+  const bf16* C_ = static_cast<const bf16*>(C);
+  if (d.N == 64)
+    return launch_fused_nk<2>(hpg, u_, B_, C_, dy, dt, dc, states, dS, length,
+                              static_cast<bf16*>(du), static_cast<bf16*>(dB), static_cast<bf16*>(dC),
+                              dCB, ddt_part, xB_part, xC_part, qpart, rpart, d, s);
+  return launch_fused_nk<4>(hpg, u_, B_, C_, dy, dt, dc, states, dS, length,
+                            static_cast<bf16*>(du), static_cast<bf16*>(dB), static_cast<bf16*>(dC),
+                            dCB, ddt_part, xB_part, xC_part, qpart, rpart, d, s);
+}
+
+}  // namespace sa

@@ -45,4 +45,14 @@ template <typename MT, typename TA, typename TB, int MODE>
 int launch_chunk_outer(const void* a, const void* b, const float* dt, const float* dc,
                        const int64_t* length, float* out, const SsdDims& d, hipStream_t s);
 
+// fused bf16 backward (headdim 64): column kernel (du, dB, decay sums, dCB)
+// and row kernel (dC, x_C); defined in ssd_bwd_fused.hip
+bool ssd_bwd_fused_ok(const SsdDims& d, const void* u, const void* B, const void* C,
+                      const void* dy);
+int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const float* dy,
+                         const float* dt, const float* dc, const float* states, const float* dS,
+                         const int64_t* length, void* du, void* dB, void* dC, float* dCB,
+                         float* ddt_part, float* xB_part, float* xC_part, float* qpart,
+                         float* rpart, const SsdDims& d, hipStream_t s);
+
 }  // namespace sa

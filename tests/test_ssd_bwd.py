@@ -71,6 +71,34 @@ def test_ssd_bwd_parity(dtype, name, shape, chunk):
     check(make_inputs(dtype=dtype, **shape), chunk, dtype)
 
 
+# bf16, headdim 64, state 64/128, chunk a multiple of 64, <= 4 heads per group:
+# the fused column / row kernels (every other case runs the generic kernels)
+FUSED_CASES = [
+    ("hpg1_lens", dict(b=2, L=192, H=2, P=64, N=128, G=2, lens=[192, 77]), 64),
+    ("hpg3_ragged", dict(b=1, L=200, H=3, P=64, N=64, G=1, lens=[171]), 128),
+    ("hpg4_partial", dict(b=2, L=320, H=8, P=64, N=128, G=2, lens=[320, 130]), 128),
+    ("zero_len", dict(b=2, L=128, H=4, P=64, N=64, G=1, lens=[0, 65], with_h=False), 64),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,shape,chunk", FUSED_CASES, ids=[c[0] for c in FUSED_CASES])
+def test_ssd_bwd_fused_parity(name, shape, chunk):
+    print(f"ssd bwd fused {name} chunk={chunk}", flush=True)
+    check(make_inputs(dtype=torch.bfloat16, **shape), chunk, torch.bfloat16)
+
+
+@pytest.mark.gpu
+def test_ssd_bwd_fused_deterministic():
+    x = make_inputs(b=2, L=256, H=8, P=64, N=128, G=2, dtype=torch.bfloat16, lens=[256, 190])
+    g = torch.Generator().manual_seed(3)
+    dy = torch.randn(2, 256, 8, 64, generator=g)
+    a = gpu_grads(x, dy, None, 128)
+    b = gpu_grads(x, dy, None, 128)
+    for k in a:
+        assert torch.equal(a[k], b[k]), f"d{k} differs between runs"
+
+
 @pytest.mark.gpu
 def test_ssd_bwd_no_state_grad():
     check(make_inputs(b=2, L=64, H=2, P=16, N=16, G=1), 32, torch.float32, with_dh=False)
