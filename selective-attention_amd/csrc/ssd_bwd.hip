@@ -66,7 +66,7 @@ struct BwdWs {
 
 inline size_t al256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-inline BwdWs bwd_layout(const SsdDims& d, size_t /*mt_bytes*/) {
+inline BwdWs bwd_layout(const SsdDims& d, size_t mt_bytes) {
   BwdWs w;
   w.ptiles = (d.P + 63) / 64;
   w.ntiles = (d.N + 63) / 64;
@@ -76,7 +76,9 @@ inline BwdWs bwd_layout(const SsdDims& d, size_t /*mt_bytes*/) {
   const size_t bhc = static_cast<size_t>(d.b) * d.H * d.nc;
   size_t o = 0;
   w.dS = o;        o = al256(o + bhc * PN * 4);
-  w.dCB = o;       o = al256(o + static_cast<size_t>(d.b) * d.nc * d.G * d.Lc * d.Lc * 4);
+  // the fused bf16 path writes one dCB plane per pair of heads of a group
+  const size_t dcb_planes = mt_bytes == 2 && ssd_bwd_fused_shape_ok(d) ? (d.H / d.G + 1) / 2 : 1;
+  w.dCB = o;       o = al256(o + dcb_planes * d.b * d.nc * d.G * d.Lc * d.Lc * 4);
   w.ddt_part = o;  o = al256(o + bhc * w.ptiles * d.Lc * 4);
   w.xB_part = o;   o = al256(o + bhc * w.ntiles * d.Lc * 4);
   w.xC_part = o;   o = al256(o + bhc * w.ntiles * d.Lc * 4);
@@ -856,6 +858,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
   const long bnc = static_cast<long>(d.b) * d.nc;
   int rc;
 
+  const bool fused = sizeof(T) == 2 && ssd_bwd_fused_ok(d, u, Bm, Cm, dy);
   // 1. dH_intra -> dS buffer
   if ((rc = launch_chunk_outer<MT, float, T, 1>(dy, C_, dt, dc, length, dS, d, s))) return rc;
   // 2. reverse state passing
@@ -867,7 +870,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
     SA_CHECK_LAUNCH("state_passing_bwd");
   }
   int ptiles = w.ptiles, ntiles = w.ntiles, qtiles = w.ttiles, rtiles = 1;
-  if (sizeof(T) == 2 && ssd_bwd_fused_ok(d, u, Bm, Cm, dy)) {
+  if (fused) {
     // 3-5 fused: du, dB, dC, decay sums
     if ((rc = launch_ssd_bwd_fused(u, Bm, Cm, dy, dt, dc, states, dS, length, du_, dB_, dC_, dCB,
                                    ddt_part, xB_part, xC_part, qpart, rsum, d, s)))

@@ -7,15 +7,17 @@
 // kernels :337-551 and the decay-gradient sums :689-765, :783-911) with two
 // kernels:
 //
-//   ssd_bwd_col (one block per (b, c, group, 64-wide source tile sigma)):
+//   ssd_bwd_col (one 512-thread block per (b, c, group, 64-wide source tile)):
 //     du, ddt_direct, dB (intra + state), x_B, the column sums q of
-//     M = W o CB and per-tile partial row sums r, and the dCB tiles
-//     (fp32, read by ssd_bwd_row).
-//   ssd_bwd_row (one block per (b, c, group, 64-wide target tile tau)):
-//     dC (state + intra through dCB) and x_C.
+//     M = W o CB, per-tile partial row sums r, and the dCB tiles (fp32, read
+//     by ssd_bwd_row).  Wave w owns the 16 source columns 16 (w & 3) + lane%16
+//     for head slot w >> 2: the two waves of a column strip work on two heads
+//     of the group at once (heads are taken two per pass) and exchange their
+//     dCB contributions through LDS once per target tile.
+//   ssd_bwd_row (one 256-thread block per (b, c, group, 64-wide target tile)):
+//     dC (state + intra through dCB) and x_C; wave w owns 16 target rows.
 //
-// Wave w of a block owns 16 columns (sigma or tau = 16w + (lane & 15)).  All
-// tile products use the 16x16x32 bf16 MFMA.  A product's result fragment
+// All tile products use the 16x16x32 bf16 MFMA.  A product's result fragment
 // (rows in registers, column on the lane) is fed straight back as the B
 // operand of the next product that contracts over those rows; rows are
 // visited through key_of_row so that each lane's 8 rows are consecutive.
@@ -27,10 +29,10 @@
 // as hi + lo bf16 planes, products as hi*hi + lo*hi + hi*lo (or hi*x + lo*x
 // against an exact bf16 operand), as in the generic kernels.
 //
-// Staging is a flat list of "stages" (one 64 x 64 fp32 tile -> hi/lo bf16,
-// plus a bf16 C or B tile on some stages).  The global loads of stage i+1 are
-// issued before the MFMAs of stage i and written to the other LDS slot after
-// them, so one barrier per stage orders the pipeline.
+// Staging is a list of stages (fp32 tiles converted to hi/lo bf16, plus a
+// bf16 C or B tile on some stages).  The global loads of stage i+1 are issued
+// into registers before the MFMAs of stage i and written to the other LDS
+// slot after them, so one barrier per stage orders the pipeline.
 #include "ssd_common.h"
 #include "prof.h"
 
@@ -38,77 +40,67 @@ namespace sa {
 namespace {
 
 constexpr int kLY = 72;             // row length of a 64 x 64 bf16 staging plane
-constexpr int kPlane = 64 * kLY;    // elements per plane; a slot holds hi then lo
+constexpr int kPlane = 64 * kLY;    // elements per plane; a tile holds hi then lo
 
 // ---------------------------------------------------------------------------
-// staging helpers (256 threads).  Rows past `rows_valid` read a clamped (valid)
-// row and are zeroed afterwards, so the loads are unconditional.
+// staging helpers.  Rows past `rows_valid` read a clamped (valid) row and are
+// zeroed afterwards, so the loads are unconditional.
 // ---------------------------------------------------------------------------
-// 64 x 64 fp32 tile, thread share: row tid/4, 16 columns from 16*(tid%4)
+// 64 x 64 fp32 tile; thread share (i in [0, 256)): row i/4, 16 columns from 16*(i%4)
 __device__ __forceinline__ void f32_tile_load(float4 (&r)[4], const float* src, int rs,
-                                              int rows_valid, int tid) {
-  const int row = tid >> 2, c0 = 16 * (tid & 3);
+                                              int rows_valid, int i) {
+  const int row = i >> 2, c0 = 16 * (i & 3);
   const float* p = src + static_cast<unsigned>(min(row, rows_valid - 1) * rs + c0);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = *reinterpret_cast<const float4*>(p + 4 * i);
+  for (int q = 0; q < 4; ++q) r[q] = *reinterpret_cast<const float4*>(p + 4 * q);
   if (row >= rows_valid) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int q = 0; q < 4; ++q) r[q] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
 }
-__device__ __forceinline__ void f32_tile_commit(bf16* slot, const float4 (&r)[4], int tid) {
-  const int row = tid >> 2, c0 = 16 * (tid & 3);
+__device__ __forceinline__ void f32_tile_commit(bf16* tile, const float4 (&r)[4], int i) {
+  const int row = i >> 2, c0 = 16 * (i & 3);
   uint32_t hi[8], lo[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float v[4] = {r[i].x, r[i].y, r[i].z, r[i].w};
+  for (int q = 0; q < 4; ++q) {
+    const float v[4] = {r[q].x, r[q].y, r[q].z, r[q].w};
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const uint32_t h = pack_bf16x2(v[2 * j], v[2 * j + 1]);
-      hi[2 * i + j] = h;
-      lo[2 * i + j] = pack_bf16x2(v[2 * j] - bf16lo_to_f32(h), v[2 * j + 1] - bf16hi_to_f32(h));
+      hi[2 * q + j] = h;
+      lo[2 * q + j] = pack_bf16x2(v[2 * j] - bf16lo_to_f32(h), v[2 * j + 1] - bf16hi_to_f32(h));
     }
   }
-  uint4* ph = reinterpret_cast<uint4*>(slot + row * kLY + c0);
-  uint4* pl = reinterpret_cast<uint4*>(slot + kPlane + row * kLY + c0);
+  uint4* ph = reinterpret_cast<uint4*>(tile + row * kLY + c0);
+  uint4* pl = reinterpret_cast<uint4*>(tile + kPlane + row * kLY + c0);
   ph[0] = uint4{hi[0], hi[1], hi[2], hi[3]};
   ph[1] = uint4{hi[4], hi[5], hi[6], hi[7]};
   pl[0] = uint4{lo[0], lo[1], lo[2], lo[3]};
   pl[1] = uint4{lo[4], lo[5], lo[6], lo[7]};
 }
-// 64 x (32 NK) bf16 tile, raw 16-byte copies
-template <int NK>
-__device__ __forceinline__ void bf_tile_load(uint4 (&r)[NK], const bf16* src, int rs,
-                                             int rows_valid, int tid) {
+// 64 x (32 NK) bf16 tile, raw 16-byte copies shared by NTHR threads
+template <int NK, int NTHR>
+struct BfTile {
+  static constexpr int PER = 64 * 4 * NK / NTHR;   // uint4 per thread
+  uint4 v[PER];
+  __device__ __forceinline__ void load(const bf16* src, int rs, int rows_valid, int tid) {
 #pragma unroll
-  for (int i = 0; i < NK; ++i) {
-    const int v = tid + 256 * i;
-    const int row = v / (4 * NK), c8 = v % (4 * NK);
-    r[i] = *reinterpret_cast<const uint4*>(src + static_cast<unsigned>(min(row, rows_valid - 1) * rs + 8 * c8));
-    if (row >= rows_valid) r[i] = uint4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + NTHR * i;
+      const int row = e / (4 * NK), c8 = e % (4 * NK);
+      v[i] = *reinterpret_cast<const uint4*>(src + static_cast<unsigned>(min(row, rows_valid - 1) * rs + 8 * c8));
+      if (row >= rows_valid) v[i] = uint4{0u, 0u, 0u, 0u};
+    }
   }
-}
-template <int NK>
-__device__ __forceinline__ void bf_tile_commit(bf16* dst, int ld, const uint4 (&r)[NK], int tid) {
+  __device__ __forceinline__ void commit(bf16* dst, int ld, int tid) const {
 #pragma unroll
-  for (int i = 0; i < NK; ++i) {
-    const int v = tid + 256 * i;
-    const int row = v / (4 * NK), c8 = v % (4 * NK);
-    *reinterpret_cast<uint4*>(dst + row * ld + 8 * c8) = r[i];
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + NTHR * i;
+      const int row = e / (4 * NK), c8 = e % (4 * NK);
+      *reinterpret_cast<uint4*>(dst + row * ld + 8 * c8) = v[i];
+    }
   }
-}
-// 8 consecutive fp32 at p + 32 ks (ks = 0, 1): two k-steps of an MFMA operand
-__device__ __forceinline__ void f32_frag_load(float4 (&r)[4], const float* p, bool ok) {
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    r[2 * ks] = *reinterpret_cast<const float4*>(p + 32 * ks);
-    r[2 * ks + 1] = *reinterpret_cast<const float4*>(p + 32 * ks + 4);
-  }
-  if (!ok) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-}
+};
 __device__ __forceinline__ uint2 pack4_bf16(const v4f& v) {
   return uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
 }
@@ -122,7 +114,6 @@ __device__ __forceinline__ float group_sum(float v) {
   v += __shfl_xor(v, 32, 64);
   return v;
 }
-
 // DPP lane exchange inside rows of 16 lanes (VALU only, no LDS traffic)
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
@@ -170,12 +161,15 @@ __device__ __forceinline__ float transpose_reduce16(float (&m)[16], int li) {
 template <int NK, int HPG>
 struct ColSmem {
   static constexpr int N = 32 * NK, LDC = N + 8;
-  static constexpr size_t kC = 64 * LDC;           // bf16 elements of a C or B tile
-  static constexpr size_t bytes = 2 * kC * 2 + 2 * 2 * kPlane * 2 + 2 * 64 * 4 + 2 * 4 * 64 * 4;
+  static constexpr int HP = HPG < 2 ? HPG : 2;
+  static constexpr size_t kC = 64 * LDC;            // bf16 per C tile
+  static constexpr size_t kY = 2 * 2 * kPlane;      // bf16 per stage (2 head slots, hi + lo)
+  static constexpr size_t bytes = 2 * kC * 2 + 2 * kY * 2 + 2 * 2 * 64 * 4 + 2 * 4 * 4 * 64 * 16 +
+                                  2 * 2 * 4 * 64 * 4 + (2 * HPG * 64 + 4) * 4;
 };
 
 template <int NK, int HPG>
-__global__ __launch_bounds__(256, 2) void ssd_bwd_col_kernel(
+__global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
     const bf16* __restrict__ u, const bf16* __restrict__ Bm, const bf16* __restrict__ Cm,
     const float* __restrict__ dy, const float* __restrict__ dt, const float* __restrict__ dc,
     const float* __restrict__ dS, const int64_t* __restrict__ length, bf16* __restrict__ du,
@@ -185,14 +179,18 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_col_kernel(
   constexpr int N = SM::N, LDC = SM::LDC;
   constexpr int NH = N / 64;                 // 64-wide n halves of a dS tile
   constexpr int NT = N / 16;                 // 16-row n tiles of dB^T
-  constexpr int HP = HPG < 2 ? HPG : 2;      // heads per pass (du accumulators held)
+  constexpr int NTW = NT / 2;                // n tiles owned by one head slot
+  constexpr int HP = SM::HP;                 // heads per pass (one per head slot)
   constexpr int NPASS = (HPG + HP - 1) / HP;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* Bs = reinterpret_cast<bf16*>(smem_raw);   // [64][LDC]  B rows of this source tile
-  bf16* Cs = Bs + SM::kC;                         // [64][LDC]  C rows of the current target tile
-  bf16* Yb = Cs + SM::kC;                         // [2 slots][2 planes][64][kLY]
-  float* dcs = reinterpret_cast<float*>(Yb + 2 * 2 * kPlane);  // [2][64] dc (log2) of a stage
-  float* rW = dcs + 2 * 64;                                     // [2][4 waves][64]
+  bf16* Cs = reinterpret_cast<bf16*>(smem_raw);      // [2][64][LDC]   C rows of a target tile
+  bf16* Ys = Cs + 2 * SM::kC;                        // [2][2 slots][hi, lo][64][kLY] stage tiles
+  float* dcs = reinterpret_cast<float*>(Ys + 2 * SM::kY);   // [2][2 slots][64] dc of the tile rows
+  float4* xb = reinterpret_cast<float4*>(dcs + 2 * 2 * 64);  // [2 slots][4 strips][4 kt][64] dCB
+  float* rW = reinterpret_cast<float*>(xb + 2 * 4 * 4 * 64); // [2][2 slots][4 strips][64]
+  float* sdc = rW + 2 * 2 * 4 * 64;   // [HPG][64] dc (log2) of the source positions
+  float* sdt = sdc + HPG * 64;        // [HPG][64] dt of the source positions (0 past the length)
+  float* sdl = sdt + HPG * 64;        // [HPG]     dc (log2) at the chunk end
 
   const int stiles = d.Lc / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -208,11 +206,14 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_col_kernel(
   const int lim = max(0, chunk_limit(len, c, d.Lc));
   const long tok0 = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc;
   const int u_rs = d.H * 64, act_rs = d.G * N;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lg = lane >> 4, li = lane & 15;
-  const int sig = s0 + 16 * w + li;   // this lane's source position
+  const int tid = threadIdx.x, lane = tid & 63, lg = lane >> 4, li = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (scalar)
+  const int strip = w & 3, hs = w >> 2;   // column strip, head slot
+  const int sl = 16 * strip + li;         // this lane's source row within the tile
+  const int sig = s0 + sl;                // this lane's source position
   const int h0 = g * HPG;
   const long bhc0 = (static_cast<long>(b) * d.H + h0) * d.nc + c;  // bhc of head k: bhc0 + k nc
-  // block-uniform bases; per-lane offsets below are 32-bit
+  // block-uniform bases; per-lane offsets are 32-bit
   const bf16* uc = u + tok0 * u_rs + h0 * 64;                       // [Lc][H*64] from head h0
   const bf16* Bc = Bm + tok0 * act_rs + static_cast<long>(g) * N;   // [Lc][G*N]
   const bf16* Cc = Cm + tok0 * act_rs + static_cast<long>(g) * N;
@@ -223,6 +224,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_col_kernel(
   const int hstride = d.nc * d.Lc;       // dc / dt / partial rows between heads
   bf16* duc = du + tok0 * u_rs + h0 * 64;
   bf16* dBc = dB + tok0 * act_rs + static_cast<long>(g) * N;
+  // dCB: one plane per pass (the row kernel sums them)
+  const long dcb_plane = static_cast<long>(d.b) * d.nc * d.G * d.Lc * d.Lc;
   float* dcbc = dCB + ((static_cast<long>(b) * d.nc + c) * d.G + g) * d.Lc * d.Lc;
   float* ddtc = ddt_part + bhc0 * d.Lc;
   float* xBc = xB_part + bhc0 * d.Lc;
@@ -231,193 +234,194 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_col_kernel(
   const int rstride = d.nc * stiles * d.Lc;
 
   if (s0 >= lim) {  // nothing of this source tile is inside the length: zero outputs / partials
-    for (int e = tid; e < 64 * HPG * 8; e += 256) {
+    for (int e = tid; e < 64 * HPG * 8; e += 512) {
       const int row = e / (HPG * 8), col8 = e % (HPG * 8);
       if (s0 + row < qlim)
         *reinterpret_cast<uint4*>(duc + static_cast<unsigned>((s0 + row) * u_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
     }
-    for (int e = tid; e < 64 * (N / 8); e += 256) {
+    for (int e = tid; e < 64 * (N / 8); e += 512) {
       const int row = e / (N / 8), col8 = e % (N / 8);
       if (s0 + row < qlim)
         *reinterpret_cast<uint4*>(dBc + static_cast<unsigned>((s0 + row) * act_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
     }
     for (int k = 0; k < HPG; ++k) {
-      for (int e = tid; e < 64; e += 256) {
+      for (int e = tid; e < 64; e += 512) {
         ddtc[k * hstride + s0 + e] = 0.f;
         xBc[k * hstride + s0 + e] = 0.f;
         qc[k * hstride + s0 + e] = 0.f;
       }
-      for (int t = s0 + tid; t < d.Lc; t += 256) rc[k * rstride + t] = 0.f;
+      for (int t = s0 + tid; t < d.Lc; t += 512) rc[k * rstride + t] = 0.f;
     }
     return;
   }
 
   const bool sv = sig < lim;
-  const int scl = min(sig, lim - 1);                    // clamped source row (valid address)
-  const bf16* Bl = Bs + (16 * w + li) * LDC + 8 * lg;   // this lane's B row (operand fragments)
-  const int tend = (lim + 63) / 64;   // target tiles inside the length
+  const int scl = min(sig, lim - 1);            // clamped source row (valid address)
+  const int ntile = (lim + 63) / 64 - S;        // target tiles T = S .. S + ntile - 1
+  for (int e = tid; e < HPG * 64; e += 512) {
+    const int k = e / 64, r = e % 64;
+    const int sc = min(s0 + r, lim - 1);
+    sdc[e] = dcc[k * hstride + sc] * kLog2e;
+    sdt[e] = s0 + r < lim ? dtc[k * hstride + sc] : 0.f;
+  }
+  if (tid < HPG) sdl[tid] = dcc[tid * hstride + d.Lc - 1] * kLog2e;
 
-  v4f dBT[NT];      // dB^T (rows n = 16 nt + 4 lg + r, column sig), all heads
+  // B fragments of this lane's source row (operand of C.B^T and dS.B^T)
+  v8bf Bf[NK];
+  {
+    const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 8 * lg);
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) dBT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+  }
 
-  // ---- stage prefetch registers ----
+  // ---- stages.  A stage holds, for both head slots of the current pass, one
+  // fp32 64 x 64 tile (dS n-half or dy target tile) as hi / lo bf16 planes;
+  // target-tile stages also bring the C tile and the rows' dc.  Thread tid
+  // stages head slot tid / 256. ----
+  const int ts = tid >> 8, ti = tid & 255;
   float4 pf[4];
-  uint4 pc[NK];
-  uint4 pu[2];
+  BfTile<NK, 512> pc;
   float pdc = 0.f;
-  v8bf uf[2];
-  const unsigned uoff = static_cast<unsigned>(scl * u_rs + 8 * lg);
-  auto load_u = [&](int k) {
-    const bf16* urow = uc + k * 64;
-    pu[0] = *reinterpret_cast<const uint4*>(urow + uoff);
-    pu[1] = *reinterpret_cast<const uint4*>(urow + uoff + 32);
-    if (!sv) pu[0] = pu[1] = uint4{0u, 0u, 0u, 0u};
+  auto load_state = [&](int kb, int hp, int half) {
+    const int k = kb + min(ts, hp - 1);
+    f32_tile_load(pf, dSc + k * (64 * N) + 64 * half, N, 64, ti);
   };
-  auto load_state = [&](int k, int half) {
-    load_u(k);
-    f32_tile_load(pf, dSc + k * (64 * N) + 64 * half, N, 64, tid);
+  auto load_intra = [&](int kb, int hp, int T) {
+    const int k = kb + min(ts, hp - 1);
+    const int t0 = 64 * T, rv = min(64, lim - t0);
+    f32_tile_load(pf, dyc + t0 * u_rs + k * 64, u_rs, rv, ti);
+    pc.load(Cc + t0 * act_rs, act_rs, rv, tid);
+    pdc = dcc[(kb + min((tid >> 6) & 1, hp - 1)) * hstride + t0 + (tid & 63)] * kLog2e;
   };
-  auto load_intra = [&](int T, int k, bool with_c) {
-    load_u(k);
-    const int t0 = 64 * T;
-    const int rv = min(64, lim - t0);
-    f32_tile_load(pf, dyc + t0 * u_rs + k * 64, u_rs, rv, tid);
-    if (with_c) bf_tile_load<NK>(pc, Cc + t0 * act_rs, act_rs, rv, tid);
-    pdc = dcc[k * hstride + t0 + (tid & 63)] * kLog2e;
-  };
-  auto commit = [&](int slot, bool intra, bool with_c) {
-    f32_tile_commit(Yb + slot * 2 * kPlane, pf, tid);
+  auto commit = [&](int slot, bool intra, int T) {
+    f32_tile_commit(Ys + slot * SM::kY + ts * 2 * kPlane, pf, ti);
     if (intra) {
-      if (with_c) bf_tile_commit<NK>(Cs, LDC, pc, tid);
-      if (tid < 64) dcs[slot * 64 + tid] = pdc;
+      pc.commit(Cs + (T & 1) * SM::kC, LDC, tid);
+      if (tid < 128) dcs[slot * 128 + tid] = pdc;
     }
   };
-  auto take_u = [&]() {
-    uf[0] = __builtin_bit_cast(v8bf, pu[0]);
-    uf[1] = __builtin_bit_cast(v8bf, pu[1]);
-  };
-  // row partials of an intra stage are summed over the 4 waves one stage later
-  int pend_slot = -1, pend_k = 0, pend_T = 0;
-  auto flush_r = [&]() {
-    if (pend_slot >= 0 && tid < 64) {
-      const float* r = rW + pend_slot * 256;
-      rc[pend_k * rstride + 64 * pend_T + tid] = r[tid] + r[64 + tid] + r[128 + tid] + r[192 + tid];
+  auto flush_r = [&](int stage, int kb, int hp, int T) {   // sum the 4 strips' row partials
+    if (tid < 64 * hp) {
+      const int h2 = tid >> 6, r = tid & 63;
+      const float* rr = rW + ((stage & 1) * 2 + h2) * 256;
+      rc[(kb + h2) * rstride + 64 * T + r] = rr[r] + rr[64 + r] + rr[128 + r] + rr[192 + r];
     }
-    pend_slot = -1;
   };
 
-  // B rows of the source tile (kept for the whole block) and the first stage
-  bf_tile_load<NK>(pc, Bc + s0 * act_rs, act_rs, min(64, lim - s0), tid);
-  bf_tile_commit<NK>(Bs, LDC, pc, tid);
-  load_state(0, 0);
-  commit(0, false, false);
-  take_u();
+  v4f dBT[NTW];   // dB^T rows n = 16 (NTW hs + nt) + 4 lg + r, column sig; all heads
+#pragma unroll
+  for (int nt = 0; nt < NTW; ++nt) dBT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+  int j = 0;      // running stage index (LDS slot parity)
+  load_state(0, HP, 0);
+  commit(0, false, 0);
   __syncthreads();
-  int idx = 0;   // running stage index (LDS slot parity)
 
 #pragma unroll
   for (int pass = 0; pass < NPASS; ++pass) {
-    const int kb = pass * HP;                       // first head of the pass
-    constexpr int HPmax = HP;
-    const int hp = (HPG - kb) < HP ? (HPG - kb) : HP;   // heads in this pass (compile-time)
-    v4f duT[HPmax][4];  // du^T (rows p = 16 pt + 4 lg + r, column sig), before the dt factor
-    float qacc[HPmax];
+    const int kb = pass * HP;
+    const int hp = (HPG - kb) < HP ? (HPG - kb) : HP;   // heads in this pass
+    const bool last_pass = pass == NPASS - 1;
+    const bool active = hs < hp;                        // this wave has a head in this pass
+    const int k = kb + min(hs, hp - 1);                 // this wave's head
+    const float dck = sdc[k * 64 + sl], dtk = sdt[k * 64 + sl];
+    const float ek = sv ? fast_exp2(fminf(sdl[k] - dck, 0.f)) : 0.f;   // e^{dc_last - dc_sig}
+    // u fragments of this lane's source row for the pass's heads: [head slot][k-step]
+    v8bf uf[HP][2];
 #pragma unroll
-    for (int kk = 0; kk < HPmax; ++kk) {
-      qacc[kk] = 0.f;
+    for (int h2 = 0; h2 < HP; ++h2) {
+      const bf16* urow = uc + (kb + min(h2, hp - 1)) * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
 #pragma unroll
-      for (int pt = 0; pt < 4; ++pt) duT[kk][pt] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int ks = 0; ks < 2; ++ks) uf[h2][ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
     }
+    v8bf ufo[2];  // this wave's own head
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) ufo[ks] = (HP > 1 && hs == 1) ? uf[HP - 1][ks] : uf[0][ks];
+    v4f duT[4];   // du^T of this wave's head (rows p = 16 pt + 4 lg + r, column sig)
+    float qacc = 0.f;
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) duT[pt] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    // ---- state stages of the pass: (head, n half): du^T += dS B^T ; dB^T += w dS^T u^T ----
+    // ---- state stages (n half): du^T += dS B^T ; dB^T += w dS^T u^T ----
 #pragma unroll
-    for (int j = 0; j < NH * HPmax; ++j) {
-      if (j >= NH * hp) break;
-      const int kk = j / NH, half = j % NH, k = kb + kk;
-      if (j + 1 < NH * hp) load_state(k + (j + 1) / NH - kk, (j + 1) % NH);
-      else load_intra(S, kb, true);
-      flush_r();
-      const bf16* Yh = Yb + (idx & 1) * 2 * kPlane;
-      const bf16* Yl = Yh + kPlane;
+    for (int half = 0; half < NH; ++half, ++j) {
+      if (half + 1 < NH) load_state(kb, hp, half + 1);
+      else load_intra(kb, hp, S);
+      const bf16* Y = Ys + (j & 1) * SM::kY;
+      if (active) {
+        const bf16* Yh = Y + hs * 2 * kPlane;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const v8bf bb = load_v8bf(Bl + 64 * half + 32 * ks);
+        for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt) {
-          const int off = (16 * pt + li) * kLY + 32 * ks + 8 * lg;
-          duT[kk][pt] = mfma_bf16(load_v8bf(Yh + off), bb, duT[kk][pt]);
-          duT[kk][pt] = mfma_bf16(load_v8bf(Yl + off), bb, duT[kk][pt]);
+          for (int pt = 0; pt < 4; ++pt) {
+            const int off = (16 * pt + li) * kLY + 32 * ks + 8 * lg;
+            duT[pt] = mfma_bf16(load_v8bf(Yh + off), Bf[2 * half + ks], duT[pt]);
+            duT[pt] = mfma_bf16(load_v8bf(Yh + kPlane + off), Bf[2 * half + ks], duT[pt]);
+          }
+      }
+      // dB^T over this head slot's n tiles that fall in this half, all heads of the pass
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) {
+        const int n16 = NTW * hs + nt;   // 16-row n tile index
+        if (n16 / 4 != half) continue;
+#pragma unroll
+        for (int h2 = 0; h2 < HP; ++h2) {
+          if (h2 >= hp) break;
+          const bf16* Yh = Y + h2 * 2 * kPlane;
+          const int kk = kb + h2;
+          const float wk = sv ? fast_exp2(fminf(sdl[kk] - sdc[kk * 64 + sl], 0.f)) * sdt[kk * 64 + sl] : 0.f;
+          v4f tmp = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const int off = (32 * ks + 8 * lg) * kLY + 16 * (n16 % 4);
+            tmp = mfma_bf16(lds_tr8(Yh + off, kLY, lane), uf[h2][ks], tmp);
+            tmp = mfma_bf16(lds_tr8(Yh + kPlane + off, kLY, lane), uf[h2][ks], tmp);
+          }
+          dBT[nt] += tmp * wk;
         }
       }
-      const float dcl = dcc[k * hstride + d.Lc - 1] * kLog2e;
-      const float dck = dcc[k * hstride + scl] * kLog2e;
-      const float dtk = dtc[k * hstride + scl];
-      const float e = sv ? fast_exp2(fminf(dcl - dck, 0.f)) : 0.f;
-      const float wk = e * dtk;
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        v4f tmp = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const int off = (32 * ks + 8 * lg) * kLY + 16 * nt;
-          tmp = mfma_bf16(lds_tr8(Yh + off, kLY, lane), uf[ks], tmp);
-          tmp = mfma_bf16(lds_tr8(Yl + off, kLY, lane), uf[ks], tmp);
-        }
-        dBT[4 * half + nt] += tmp * wk;
-      }
-      if (half == NH - 1) {
-        // head k's state part is complete: scale by e^{dc_last - dc_sig}; x_B
+      if (half == NH - 1 && active) {
+        // this head's state part is complete: scale by e^{dc_last - dc_sig}; x_B
         const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
         float s = 0.f;
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) {
-          duT[kk][pt] *= e;
-          s += dot4_bf16(duT[kk][pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
+          duT[pt] *= ek;
+          s += dot4_bf16(duT[pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
         }
         s = group_sum(sv ? s : 0.f) * dtk;
         if (lg == 0) xBc[k * hstride + sig] = s;
       }
-      commit((idx + 1) & 1, j + 1 >= NH * hp, j + 1 >= NH * hp);
-      ++idx;
+      commit((j + 1) & 1, half + 1 >= NH, S);
       __syncthreads();
-      take_u();
     }
 
-    // ---- intra stages of the pass: (target tile T, head) ----
-    for (int T = S; T < tend; ++T) {
+    // ---- target-tile stages ----
+    for (int Ti = 0; Ti < ntile; ++Ti, ++j) {
+      const int T = S + Ti;
       const int t0 = 64 * T;
-      const bool diag = T == S || t0 + 64 > lim;   // tile needs the causal / length masks
-      v4f CB[4], dCBa[4];
+      const bool has_next = Ti + 1 < ntile || !last_pass;
+      if (Ti + 1 < ntile) load_intra(kb, hp, T + 1);
+      else if (!last_pass) load_state(kb + HP, (HPG - kb - HP) < HP ? (HPG - kb - HP) : HP, 0);
+      if (Ti > 0) flush_r(j - 1, kb, hp, T - 1);
+      const int slot = j & 1;
+      const bf16* Yh = Ys + slot * SM::kY + min(hs, hp - 1) * 2 * kPlane;
+      const bf16* Yl = Yh + kPlane;
+      const float* dcT = dcs + slot * 128 + 64 * min(hs, hp - 1);
+      const bf16* Cb = Cs + (T & 1) * SM::kC;
+      const bool diag = Ti == 0 || t0 + 64 > lim;   // tile needs the causal / length masks
+      // C.B^T of this strip
+      v4f CB[4];
 #pragma unroll
-      for (int kk = 0; kk < HPmax; ++kk) {
-        if (kk >= hp) break;
-        const int k = kb + kk;
-        const bool last_pass = pass == NPASS - 1;
-        const bool last_stage = last_pass && kk == hp - 1 && T + 1 == tend;
-        // prefetch the next stage: next head, next tile, or the next pass's first state stage
-        if (kk + 1 < hp) load_intra(T, k + 1, false);
-        else if (T + 1 < tend) load_intra(T + 1, kb, true);
-        else if (!last_pass) load_state(kb + HP, 0);
-        flush_r();
-        const int slot = idx & 1;
-        const bf16* Yh = Yb + slot * 2 * kPlane;
-        const bf16* Yl = Yh + kPlane;
-        const float* dcT = dcs + slot * 64;
-        if (kk == 0) {
+      for (int kt = 0; kt < 4; ++kt) {
+        CB[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+        const bf16* crow = Cb + key_of_row(kt, li) * LDC + 8 * lg;
 #pragma unroll
-          for (int kt = 0; kt < 4; ++kt) {
-            CB[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-            dCBa[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-          }
+        for (int ks = 0; ks < NK; ++ks) CB[kt] = mfma_bf16(load_v8bf(crow + 32 * ks), Bf[ks], CB[kt]);
+      }
+      v4f dCBa[4];
 #pragma unroll
-          for (int ks = 0; ks < NK; ++ks) {
-            const v8bf bb = load_v8bf(Bl + 32 * ks);
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-              CB[kt] = mfma_bf16(load_v8bf(Cs + key_of_row(kt, li) * LDC + 8 * lg + 32 * ks), bb, CB[kt]);
-          }
-        }
+      for (int kt = 0; kt < 4; ++kt) dCBa[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+      if (active) {
         // W[t, sig] = dy[t] . u[sig]
         v4f W[4];
 #pragma unroll
@@ -426,13 +430,11 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_col_kernel(
           const int off = key_of_row(kt, li) * kLY + 8 * lg;
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
-            W[kt] = mfma_bf16(load_v8bf(Yh + off + 32 * ks), uf[ks], W[kt]);
-            W[kt] = mfma_bf16(load_v8bf(Yl + off + 32 * ks), uf[ks], W[kt]);
+            W[kt] = mfma_bf16(load_v8bf(Yh + off + 32 * ks), ufo[ks], W[kt]);
+            W[kt] = mfma_bf16(load_v8bf(Yl + off + 32 * ks), ufo[ks], W[kt]);
           }
         }
-        // decay and masks; dCB += W', M = W' o CB (q: column sums, r: row sums); W <- L
-        const float dck = dcc[k * hstride + scl] * kLog2e;
-        const float dtk = sv ? dtc[k * hstride + scl] : 0.f;
+        // decay and masks; dCB = W', M = W' o CB (q: column sums, r: row sums); W <- L
         float m[16];
         float qs = 0.f;
 #pragma unroll
@@ -448,7 +450,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_col_kernel(
               dec = (t >= sig && t < lim) ? dec : 0.f;
             }
             const float wv = W[kt][r] * dtk * dec;
-            dCBa[kt][r] += wv;
+            dCBa[kt][r] = wv;
             float mv = wv * CB[kt][r];
             if (diag) mv = (t0 + tb + r > sig) ? mv : 0.f;
             m[4 * kt + r] = mv;
@@ -456,11 +458,9 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_col_kernel(
             W[kt][r] = CB[kt][r] * dec;
           }
         }
-        qacc[kk] += qs;
-        rW[slot * 256 + w * 64 + key_of_row(li >> 2, 4 * lg + (li & 3))] = transpose_reduce16(m, li);
-        pend_slot = slot;
-        pend_k = k;
-        pend_T = T;
+        qacc += qs;
+        rW[((j & 1) * 2 + hs) * 256 + strip * 64 + key_of_row(li >> 2, 4 * lg + (li & 3))] =
+            transpose_reduce16(m, li);
         // du^T[p, sig] += sum_t dy[t, p] L[t, sig]
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -471,88 +471,81 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_col_kernel(
             const int off = (32 * ks + 8 * lg) * kLY + 16 * pt;
             const v8bf ah = lds_tr8(Yh + off, kLY, lane);
             const v8bf al = lds_tr8(Yl + off, kLY, lane);
-            duT[kk][pt] = mfma_bf16(ah, lh, duT[kk][pt]);
-            duT[kk][pt] = mfma_bf16(al, lh, duT[kk][pt]);
-            duT[kk][pt] = mfma_bf16(ah, ll, duT[kk][pt]);
+            duT[pt] = mfma_bf16(ah, lh, duT[pt]);
+            duT[pt] = mfma_bf16(al, lh, duT[pt]);
+            duT[pt] = mfma_bf16(ah, ll, duT[pt]);
           }
         }
-        const bool next_c = kk == hp - 1 && !last_stage;   // the next stage replaces Cs
-        float* dcbt = dcbc + t0 * d.Lc;                      // rows of tile T
-        if (kk == hp - 1) {
-          // this pass's heads are done with tile T: dCB partial; on the last pass the
-          // full dCB feeds dB^T[n, sig] += sum_t C[t, n] dCB[t, sig]
-          if (!last_pass) {
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                dcbt[static_cast<unsigned>(key_of_row(kt, 4 * lg + r) * d.Lc + sig)] = dCBa[kt][r];
-          } else {
-            if (NPASS > 1) {
-#pragma unroll
-              for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                  dCBa[kt][r] += dcbt[static_cast<unsigned>(key_of_row(kt, 4 * lg + r) * d.Lc + sig)];
-            }
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-              v8bf dh, dl;
-              split_p(dCBa[2 * ks], dCBa[2 * ks + 1], dh, dl);
-#pragma unroll
-              for (int nt = 0; nt < NT; ++nt) {
-                const v8bf a = lds_tr8(Cs + (32 * ks + 8 * lg) * LDC + 16 * nt, LDC, lane);
-                dBT[nt] = mfma_bf16(a, dh, dBT[nt]);
-                dBT[nt] = mfma_bf16(a, dl, dBT[nt]);
-              }
-            }
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                dcbt[static_cast<unsigned>(key_of_row(kt, 4 * lg + r) * d.Lc + sig)] = dCBa[kt][r];
-          }
-          if (next_c) __syncthreads();   // every wave is done with Cs before the next tile lands
-        }
-        if (!last_stage) {
-          const bool next_intra = kk + 1 < hp || T + 1 < tend;
-          commit((idx + 1) & 1, next_intra, next_c && next_intra);
-        }
-        ++idx;
-        __syncthreads();
-        if (!last_stage) take_u();
       }
-    }
-
-    // ---- pass epilogue: du, ddt_direct, q of the pass's heads ----
+      // dCB of the pass's heads: add the other head slot's contribution of the
+      // strip (zeros from a slot without a head in this pass)
+      {
+        float4* xo = xb + (hs * 4 + strip) * 4 * 64;
 #pragma unroll
-    for (int kk = 0; kk < HPmax; ++kk) {
-      if (kk >= hp) break;
-      const int k = kb + kk;
+        for (int kt = 0; kt < 4; ++kt) xo[kt * 64 + lane] = make_float4(dCBa[kt][0], dCBa[kt][1], dCBa[kt][2], dCBa[kt][3]);
+        __syncthreads();
+        const float4* xi = xb + ((1 - hs) * 4 + strip) * 4 * 64;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          const float4 o = xi[kt * 64 + lane];
+          dCBa[kt] += v4f{o.x, o.y, o.z, o.w};
+        }
+      }
+      // head slot hs stores rows kt in {2 hs, 2 hs + 1} of this pass's dCB tile
+      {
+        float* dcbt = dcbc + pass * dcb_plane + t0 * d.Lc;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+          if ((kt >> 1) == hs) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              dcbt[static_cast<unsigned>(key_of_row(kt, 4 * lg + r) * d.Lc + sig)] = dCBa[kt][r];
+          }
+      }
+      // dB^T[n, sig] += sum_t C[t, n] dCB[t, sig] for this slot's n tiles
+      {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          v8bf dh, dl;
+          split_p(dCBa[2 * ks], dCBa[2 * ks + 1], dh, dl);
+#pragma unroll
+          for (int nt = 0; nt < NTW; ++nt) {
+            const v8bf a = lds_tr8(Cb + (32 * ks + 8 * lg) * LDC + 16 * (NTW * hs + nt), LDC, lane);
+            dBT[nt] = mfma_bf16(a, dh, dBT[nt]);
+            dBT[nt] = mfma_bf16(a, dl, dBT[nt]);
+          }
+        }
+      }
+      if (has_next) commit((j + 1) & 1, Ti + 1 < ntile, T + 1);
+      __syncthreads();
+    }
+    flush_r(j - 1, kb, hp, S + ntile - 1);
+
+    // ---- pass epilogue: du, ddt_direct, q of this wave's head ----
+    if (active) {
       const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
-      const float dtk = sv ? dtc[k * hstride + scl] : 0.f;
       float s = 0.f;
 #pragma unroll
-      for (int pt = 0; pt < 4; ++pt) s += dot4_bf16(duT[kk][pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
+      for (int pt = 0; pt < 4; ++pt) s += dot4_bf16(duT[pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
       s = group_sum(sv ? s : 0.f);
-      const float q = group_sum(qacc[kk]);
+      const float q = group_sum(qacc);
       if (sig < qlim) {
         bf16* durow = duc + k * 64 + static_cast<unsigned>(sig * u_rs + 4 * lg);
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt) *reinterpret_cast<uint2*>(durow + 16 * pt) = pack4_bf16(duT[kk][pt] * dtk);
+        for (int pt = 0; pt < 4; ++pt) *reinterpret_cast<uint2*>(durow + 16 * pt) = pack4_bf16(duT[pt] * dtk);
       }
       if (lg == 0) {
         ddtc[k * hstride + sig] = s;
         qc[k * hstride + sig] = q;
       }
-      for (int t = 64 * tend + tid; t < d.Lc; t += 256) rc[k * rstride + t] = 0.f;
     }
+    for (int kk = 0; kk < hp; ++kk)
+      for (int t = 64 * (S + ntile) + tid; t < d.Lc; t += 512) rc[(kb + kk) * rstride + t] = 0.f;
   }
-  flush_r();
   if (sig < qlim) {
-    bf16* dbrow = dBc + static_cast<unsigned>(sig * act_rs + 4 * lg);
+    bf16* dbrow = dBc + static_cast<unsigned>(sig * act_rs + 16 * NTW * hs + 4 * lg);
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<uint2*>(dbrow + 16 * nt) = pack4_bf16(dBT[nt]);
+    for (int nt = 0; nt < NTW; ++nt) *reinterpret_cast<uint2*>(dbrow + 16 * nt) = pack4_bf16(dBT[nt]);
   }
 }
 
@@ -593,17 +586,20 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_row_kernel(
   const int lim = max(0, chunk_limit(len, c, d.Lc));
   const long tok0 = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc;
   const int u_rs = d.H * 64, act_rs = d.G * N;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lg = lane >> 4, li = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, lg = lane >> 4, li = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (scalar)
   const int tau = t0 + 16 * w + li;
   const int h0 = g * HPG;
   const long bhc0 = (static_cast<long>(b) * d.H + h0) * d.nc + c;
   const int hstride = d.nc * d.Lc;
-  // block-uniform bases; per-lane offsets below are 32-bit
+  // block-uniform bases; per-lane offsets are 32-bit
   const bf16* Bc = Bm + tok0 * act_rs + static_cast<long>(g) * N;
   const bf16* Cc = Cm + tok0 * act_rs + static_cast<long>(g) * N;
   const float* dyc = dy + tok0 * u_rs + h0 * 64;
   const float* Hc = states + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (64L * N);
   const float* dcc = dc + bhc0 * d.Lc;
+  constexpr int NPASS = (HPG + 1) / 2;   // dCB planes written by the column kernel
+  const long dcb_plane = static_cast<long>(d.b) * d.nc * d.G * d.Lc * d.Lc;
   const float* dcbc = dCB + ((static_cast<long>(b) * d.nc + c) * d.G + g) * d.Lc * d.Lc;
   bf16* dCc = dC + tok0 * act_rs + static_cast<long>(g) * N;
   float* xCc = xC_part + bhc0 * d.Lc;
@@ -631,20 +627,43 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_row_kernel(
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) dCT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  float4 pf[4];   // state stage: H_in tile
-  uint4 pc[NK];   // intra stage: B tile
-  float4 pg[4];   // dy[tau] of a head (state) / dCB[tau] row piece (intra)
+  float4 pf[4];          // state stage: H_in tile
+  BfTile<NK, 256> pc;    // intra stage: B tile
+  float4 pg[4];          // dy[tau] of a head (state) / dCB[tau] row piece (intra)
   float4 cur[4];
   const unsigned dcb_off = static_cast<unsigned>(tcl * d.Lc + 8 * lg);
   const unsigned dy_off = static_cast<unsigned>(tcl * u_rs + 8 * lg);
+  auto frag_load = [&](const float* p) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      pg[2 * ks] = *reinterpret_cast<const float4*>(p + 32 * ks);
+      pg[2 * ks + 1] = *reinterpret_cast<const float4*>(p + 32 * ks + 4);
+    }
+    if (!tv) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
   auto load_state = [&](int k, int half) {
     f32_tile_load(pf, Hc + k * (64 * N) + 64 * half, N, 64, tid);
-    if (half == 0) f32_frag_load(pg, dyc + k * 64 + dy_off, tv);
+    if (half == 0) frag_load(dyc + k * 64 + dy_off);
   };
   auto load_intra = [&](int S) {
     const int s0 = 64 * S;
-    bf_tile_load<NK>(pc, Bc + s0 * act_rs, act_rs, min(64, lim - s0), tid);
-    f32_frag_load(pg, dcbc + s0 + dcb_off, tv);
+    pc.load(Bc + s0 * act_rs, act_rs, min(64, lim - s0), tid);
+    frag_load(dcbc + s0 + dcb_off);
+#pragma unroll
+    for (int p = 1; p < NPASS; ++p) {
+      const float* q = dcbc + p * dcb_plane + s0 + dcb_off;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const float4 a = *reinterpret_cast<const float4*>(q + 32 * ks);
+        const float4 e = *reinterpret_cast<const float4*>(q + 32 * ks + 4);
+        pg[2 * ks] = make_float4(pg[2 * ks].x + a.x, pg[2 * ks].y + a.y, pg[2 * ks].z + a.z, pg[2 * ks].w + a.w);
+        pg[2 * ks + 1] = make_float4(pg[2 * ks + 1].x + e.x, pg[2 * ks + 1].y + e.y,
+                                     pg[2 * ks + 1].z + e.z, pg[2 * ks + 1].w + e.w);
+      }
+    }
   };
 
   load_state(0, 0);
@@ -691,7 +710,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_row_kernel(
       if (lg == 0) xCc[k * hstride + tau] = s;
     }
     if (j + 1 < nS) f32_tile_commit(slots + ((j + 1) & 1) * SM::slot_elems, pf, tid);
-    else bf_tile_commit<NK>(slots + ((j + 1) & 1) * SM::slot_elems, LDC, pc, tid);
+    else pc.commit(slots + ((j + 1) & 1) * SM::slot_elems, LDC, tid);
     if (j + 1 >= nS || (j + 1) % NH == 0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) cur[i] = pg[i];
@@ -717,7 +736,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_row_kernel(
         dCT[nt] = mfma_bf16(a, fl[ks], dCT[nt]);
       }
     if (has_next) {
-      bf_tile_commit<NK>(slots + ((idx + 1) & 1) * SM::slot_elems, LDC, pc, tid);
+      pc.commit(slots + ((idx + 1) & 1) * SM::slot_elems, LDC, tid);
 #pragma unroll
       for (int i = 0; i < 4; ++i) cur[i] = pg[i];
     }
@@ -751,7 +770,7 @@ int launch_fused(const bf16* u, const bf16* Bm, const bf16* Cm, const float* dy,
     const size_t smem = ColSmem<NK, HPG>::bytes;
     if (int rc = allow_smem(ssd_bwd_col_kernel<NK, HPG>, smem, "ssd_bwd_col")) return rc;
     ProfScope prof_("ssd_bwd_col", s);
-    hipLaunchKernelGGL((ssd_bwd_col_kernel<NK, HPG>), dim3(blocks), dim3(256), smem, s, u, Bm, Cm,
+    hipLaunchKernelGGL((ssd_bwd_col_kernel<NK, HPG>), dim3(blocks), dim3(512), smem, s, u, Bm, Cm,
                        dy, dt, dc, dS, length, du, dB, dCB, ddt_part, xB_part, qpart, rpart, d);
     SA_CHECK_LAUNCH("ssd_bwd_col");
   }
@@ -789,11 +808,15 @@ int launch_fused_nk(int hpg, const bf16* u, const bf16* Bm, const bf16* Cm, cons
 
 }  // namespace
 
+bool ssd_bwd_fused_shape_ok(const SsdDims& d) {
+  const int hpg = d.H / d.G;
+  return d.P == 64 && (d.N == 64 || d.N == 128) && d.Lc % 64 == 0 && hpg >= 1 && hpg <= 4;
+}
+
 bool ssd_bwd_fused_ok(const SsdDims& d, const void* u, const void* B, const void* C,
                       const void* dy) {
-  const int hpg = d.H / d.G;
-  return d.P == 64 && (d.N == 64 || d.N == 128) && d.Lc % 64 == 0 && hpg >= 1 && hpg <= 4 &&
-         aligned16(u) && aligned16(B) && aligned16(C) && aligned16(dy);
+  return ssd_bwd_fused_shape_ok(d) && aligned16(u) && aligned16(B) && aligned16(C) &&
+         aligned16(dy);
 }
 
 int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const float* dy,

@@ -47,6 +47,7 @@ int launch_chunk_outer(const void* a, const void* b, const float* dt, const floa
 
 // fused bf16 backward (headdim 64): column kernel (du, dB, decay sums, dCB)
 // and row kernel (dC, x_C); defined in ssd_bwd_fused.hip
+bool ssd_bwd_fused_shape_ok(const SsdDims& d);
 bool ssd_bwd_fused_ok(const SsdDims& d, const void* u, const void* B, const void* C,
                       const void* dy);
 int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const float* dy,
