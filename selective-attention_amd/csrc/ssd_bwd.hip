@@ -873,7 +873,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
   if (fused) {
     // 3-5 fused: du, dB, dC, decay sums
     if ((rc = launch_ssd_bwd_fused(u, Bm, Cm, dy, dt, dc, states, dS, length, du_, dB_, dC_, dCB,
-                                   ddt_part, xB_part, xC_part, qpart, rsum, d, s)))
+                                   ddt_part, xB_part, xC_part, qpart, rsum, d, lo >= 0.f, s)))
       return rc;
     ptiles = ntiles = qtiles = 1;
     rtiles = d.Lc / 64;

@@ -164,8 +164,8 @@ struct ColSmem {
   static constexpr int HP = HPG < 2 ? HPG : 2;
   static constexpr size_t kC = 64 * LDC;            // bf16 per C tile
   static constexpr size_t kY = 2 * 2 * kPlane;      // bf16 per stage (2 head slots, hi + lo)
-  static constexpr size_t bytes = 2 * kC * 2 + 2 * kY * 2 + 2 * 2 * 64 * 4 + 2 * 4 * 4 * 64 * 16 +
-                                  2 * 2 * 4 * 64 * 4 + (2 * HPG * 64 + 4) * 4;
+  static constexpr size_t bytes = 2 * kC * 2 + 2 * kY * 2 + 2 * 2 * 2 * 64 * 4 +
+                                  2 * 4 * 4 * 64 * 16 + 2 * 2 * 4 * 64 * 4 + (2 * HPG * 64 + 4) * 4;
 };
 
 template <int NK, int HPG>
@@ -174,7 +174,8 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
     const float* __restrict__ dy, const float* __restrict__ dt, const float* __restrict__ dc,
     const float* __restrict__ dS, const int64_t* __restrict__ length, bf16* __restrict__ du,
     bf16* __restrict__ dB, float* __restrict__ dCB, float* __restrict__ ddt_part,
-    float* __restrict__ xB_part, float* __restrict__ qpart, float* __restrict__ rpart, SsdDims d) {
+    float* __restrict__ xB_part, float* __restrict__ qpart, float* __restrict__ rpart, SsdDims d,
+    int mono) {
   using SM = ColSmem<NK, HPG>;
   constexpr int N = SM::N, LDC = SM::LDC;
   constexpr int NH = N / 64;                 // 64-wide n halves of a dS tile
@@ -186,7 +187,8 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
   bf16* Cs = reinterpret_cast<bf16*>(smem_raw);      // [2][64][LDC]   C rows of a target tile
   bf16* Ys = Cs + 2 * SM::kC;                        // [2][2 slots][hi, lo][64][kLY] stage tiles
   float* dcs = reinterpret_cast<float*>(Ys + 2 * SM::kY);   // [2][2 slots][64] dc of the tile rows
-  float4* xb = reinterpret_cast<float4*>(dcs + 2 * 2 * 64);  // [2 slots][4 strips][4 kt][64] dCB
+  float* ats = dcs + 2 * 2 * 64;   // [2][2 slots][64] e^{dc_t - dc_t0} of the tile rows
+  float4* xb = reinterpret_cast<float4*>(ats + 2 * 2 * 64);  // [2 slots][4 strips][4 kt][64] dCB
   float* rW = reinterpret_cast<float*>(xb + 2 * 4 * 4 * 64); // [2][2 slots][4 strips][64]
   float* sdc = rW + 2 * 2 * 4 * 64;   // [HPG][64] dc (log2) of the source positions
   float* sdt = sdc + HPG * 64;        // [HPG][64] dt of the source positions (0 past the length)
@@ -281,7 +283,7 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
   const int ts = tid >> 8, ti = tid & 255;
   float4 pf[4];
   BfTile<NK, 512> pc;
-  float pdc = 0.f;
+  float pdc = 0.f, pdc0 = 0.f;
   auto load_state = [&](int kb, int hp, int half) {
     const int k = kb + min(ts, hp - 1);
     f32_tile_load(pf, dSc + k * (64 * N) + 64 * half, N, 64, ti);
@@ -291,13 +293,18 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
     const int t0 = 64 * T, rv = min(64, lim - t0);
     f32_tile_load(pf, dyc + t0 * u_rs + k * 64, u_rs, rv, ti);
     pc.load(Cc + t0 * act_rs, act_rs, rv, tid);
-    pdc = dcc[(kb + min((tid >> 6) & 1, hp - 1)) * hstride + t0 + (tid & 63)] * kLog2e;
+    const float* dch = dcc + (kb + min((tid >> 6) & 1, hp - 1)) * hstride + t0;
+    pdc = dch[tid & 63] * kLog2e;
+    pdc0 = dch[0] * kLog2e;
   };
   auto commit = [&](int slot, bool intra, int T) {
     f32_tile_commit(Ys + slot * SM::kY + ts * 2 * kPlane, pf, ti);
     if (intra) {
       pc.commit(Cs + (T & 1) * SM::kC, LDC, tid);
-      if (tid < 128) dcs[slot * 128 + tid] = pdc;
+      if (tid < 128) {
+        dcs[slot * 128 + tid] = pdc;
+        ats[slot * 128 + tid] = fast_exp2(fminf(pdc - pdc0, 0.f));
+      }
     }
   };
   auto flush_r = [&](int stage, int kb, int hp, int T) {   // sum the 4 strips' row partials
@@ -407,8 +414,13 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
       const bf16* Yh = Ys + slot * SM::kY + min(hs, hp - 1) * 2 * kPlane;
       const bf16* Yl = Yh + kPlane;
       const float* dcT = dcs + slot * 128 + 64 * min(hs, hp - 1);
+      const float* atT = ats + slot * 128 + 64 * min(hs, hp - 1);
       const bf16* Cb = Cs + (T & 1) * SM::kC;
       const bool diag = Ti == 0 || t0 + 64 > lim;   // tile needs the causal / length masks
+      // off the diagonal with a monotone dc (dt >= 0), e^{min(dc_t - dc_sig, 0)} =
+      // e^{min(dc_t - dc_t0, 0)} e^{min(dc_t0 - dc_sig, 0)}: a row table times a
+      // per-lane factor
+      const bool fact = !diag && mono;
       // C.B^T of this strip
       v4f CB[4];
 #pragma unroll
@@ -437,43 +449,56 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
         // decay and masks; dCB = W', M = W' o CB (q: column sums, r: row sums); W <- L
         float m[16];
         float qs = 0.f;
+        if (fact) {
+          const float bk = fast_exp2(fminf(dcT[0] - dck, 0.f));
+          const float bdt = bk * dtk;
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);   // first of 4 consecutive rows
-          const float4 dq = *reinterpret_cast<const float4*>(dcT + tb);
-          const float dv[4] = {dq.x, dq.y, dq.z, dq.w};
+          for (int kt = 0; kt < 4; ++kt) {
+            const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);
+            const float4 aq = *reinterpret_cast<const float4*>(atT + tb);
+            const float av[4] = {aq.x, aq.y, aq.z, aq.w};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float dec = fast_exp2(fminf(dv[r] - dck, 0.f));
-            if (diag) {
-              const int t = t0 + tb + r;
-              dec = (t >= sig && t < lim) ? dec : 0.f;
+            for (int r = 0; r < 4; ++r) {
+              const float wv = W[kt][r] * (av[r] * bdt);
+              dCBa[kt][r] = wv;
+              const float mv = wv * CB[kt][r];
+              m[4 * kt + r] = mv;
+              qs += mv;
+              W[kt][r] = CB[kt][r] * (av[r] * bk);
             }
-            const float wv = W[kt][r] * dtk * dec;
-            dCBa[kt][r] = wv;
-            float mv = wv * CB[kt][r];
-            if (diag) mv = (t0 + tb + r > sig) ? mv : 0.f;
-            m[4 * kt + r] = mv;
-            qs += mv;
-            W[kt][r] = CB[kt][r] * dec;
+          }
+        } else {
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) {
+            const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);   // first of 4 consecutive rows
+            const float4 dq = *reinterpret_cast<const float4*>(dcT + tb);
+            const float dv[4] = {dq.x, dq.y, dq.z, dq.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int t = t0 + tb + r;
+              float dec = fast_exp2(fminf(dv[r] - dck, 0.f));
+              dec = (t >= sig && t < lim) ? dec : 0.f;
+              const float wv = W[kt][r] * dtk * dec;
+              dCBa[kt][r] = wv;
+              const float mv = t > sig ? wv * CB[kt][r] : 0.f;
+              m[4 * kt + r] = mv;
+              qs += mv;
+              W[kt][r] = CB[kt][r] * dec;
+            }
           }
         }
         qacc += qs;
         rW[((j & 1) * 2 + hs) * 256 + strip * 64 + key_of_row(li >> 2, 4 * lg + (li & 3))] =
             transpose_reduce16(m, li);
-        // du^T[p, sig] += sum_t dy[t, p] L[t, sig]
+        // du^T[p, sig] += sum_t dy[t, p] L[t, sig]  (L as one bf16 plane, dy as hi + lo)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          v8bf lh, ll;
-          split_p(W[2 * ks], W[2 * ks + 1], lh, ll);
+          const v8bf lh = pack_p(W[2 * ks], W[2 * ks + 1]);
 #pragma unroll
           for (int pt = 0; pt < 4; ++pt) {
             const int off = (32 * ks + 8 * lg) * kLY + 16 * pt;
-            const v8bf ah = lds_tr8(Yh + off, kLY, lane);
-            const v8bf al = lds_tr8(Yl + off, kLY, lane);
-            duT[pt] = mfma_bf16(ah, lh, duT[pt]);
-            duT[pt] = mfma_bf16(al, lh, duT[pt]);
-            duT[pt] = mfma_bf16(ah, ll, duT[pt]);
+            duT[pt] = mfma_bf16(lds_tr8(Yh + off, kLY, lane), lh, duT[pt]);
+            duT[pt] = mfma_bf16(lds_tr8(Yl + off, kLY, lane), lh, duT[pt]);
           }
         }
       }
@@ -764,14 +789,16 @@ template <int NK, int HPG>
 int launch_fused(const bf16* u, const bf16* Bm, const bf16* Cm, const float* dy, const float* dt,
                  const float* dc, const float* states, const float* dS, const int64_t* length,
                  bf16* du, bf16* dB, bf16* dC, float* dCB, float* ddt_part, float* xB_part,
-                 float* xC_part, float* qpart, float* rpart, const SsdDims& d, hipStream_t s) {
+                 float* xC_part, float* qpart, float* rpart, const SsdDims& d, int mono,
+                 hipStream_t s) {
   const long blocks = static_cast<long>(d.b) * d.nc * d.G * (d.Lc / 64);
   {
     const size_t smem = ColSmem<NK, HPG>::bytes;
     if (int rc = allow_smem(ssd_bwd_col_kernel<NK, HPG>, smem, "ssd_bwd_col")) return rc;
     ProfScope prof_("ssd_bwd_col", s);
     hipLaunchKernelGGL((ssd_bwd_col_kernel<NK, HPG>), dim3(blocks), dim3(512), smem, s, u, Bm, Cm,
-                       dy, dt, dc, dS, length, du, dB, dCB, ddt_part, xB_part, qpart, rpart, d);
+                       dy, dt, dc, dS, length, du, dB, dCB, ddt_part, xB_part, qpart, rpart, d,
+                       mono);
     SA_CHECK_LAUNCH("ssd_bwd_col");
   }
   {
@@ -790,11 +817,11 @@ int launch_fused_nk(int hpg, const bf16* u, const bf16* Bm, const bf16* Cm, cons
                     const float* dt, const float* dc, const float* states, const float* dS,
                     const int64_t* length, bf16* du, bf16* dB, bf16* dC, float* dCB,
                     float* ddt_part, float* xB_part, float* xC_part, float* qpart, float* rpart,
-                    const SsdDims& d, hipStream_t s) {
+                    const SsdDims& d, int mono, hipStream_t s) {
 #define SA_FUSED_CASE(H)                                                                       \
   case H:                                                                                      \
     return launch_fused<NK, H>(u, Bm, Cm, dy, dt, dc, states, dS, length, du, dB, dC, dCB,     \
-                               ddt_part, xB_part, xC_part, qpart, rpart, d, s);
+                               ddt_part, xB_part, xC_part, qpart, rpart, d, mono, s);
   switch (hpg) {
     SA_FUSED_CASE(1)
     SA_FUSED_CASE(2)
@@ -823,18 +850,19 @@ int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const floa
                          const float* dt, const float* dc, const float* states, const float* dS,
                          const int64_t* length, void* du, void* dB, void* dC, float* dCB,
                          float* ddt_part, float* xB_part, float* xC_part, float* qpart,
-                         float* rpart, const SsdDims& d, hipStream_t s) {
+                         float* rpart, const SsdDims& d, bool dt_nonneg, hipStream_t s) {
   const int hpg = d.H / d.G;
+  const int mono = dt_nonneg ? 1 : 0;
   const bf16* u_ = static_cast<const bf16*>(u);
   const bf16* B_ = static_cast<const bf16*>(B);
   const bf16* C_ = static_cast<const bf16*>(C);
   if (d.N == 64)
     return launch_fused_nk<2>(hpg, u_, B_, C_, dy, dt, dc, states, dS, length,
                               static_cast<bf16*>(du), static_cast<bf16*>(dB), static_cast<bf16*>(dC),
-                              dCB, ddt_part, xB_part, xC_part, qpart, rpart, d, s);
+                              dCB, ddt_part, xB_part, xC_part, qpart, rpart, d, mono, s);
   return launch_fused_nk<4>(hpg, u_, B_, C_, dy, dt, dc, states, dS, length,
                             static_cast<bf16*>(du), static_cast<bf16*>(dB), static_cast<bf16*>(dC),
-                            dCB, ddt_part, xB_part, xC_part, qpart, rpart, d, s);
+                            dCB, ddt_part, xB_part, xC_part, qpart, rpart, d, mono, s);
 }
 
 }  // namespace sa

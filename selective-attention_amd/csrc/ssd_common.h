@@ -46,7 +46,8 @@ int launch_chunk_outer(const void* a, const void* b, const float* dt, const floa
                        const int64_t* length, float* out, const SsdDims& d, hipStream_t s);
 
 // fused bf16 backward (headdim 64): column kernel (du, dB, decay sums, dCB)
-// and row kernel (dC, x_C); defined in ssd_bwd_fused.hip
+// and row kernel (dC, x_C); defined in ssd_bwd_fused.hip.  dt_nonneg: every dt
+// is >= 0 (delta_min >= 0), so each head's dc is monotone within a chunk
 bool ssd_bwd_fused_shape_ok(const SsdDims& d);
 bool ssd_bwd_fused_ok(const SsdDims& d, const void* u, const void* B, const void* C,
                       const void* dy);
@@ -54,6 +55,6 @@ int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const floa
                          const float* dt, const float* dc, const float* states, const float* dS,
                          const int64_t* length, void* du, void* dB, void* dC, float* dCB,
                          float* ddt_part, float* xB_part, float* xC_part, float* qpart,
-                         float* rpart, const SsdDims& d, hipStream_t s);
+                         float* rpart, const SsdDims& d, bool dt_nonneg, hipStream_t s);
 
 }  // namespace sa
