@@ -329,23 +329,30 @@ __global__ __launch_bounds__(256) void chunk_scan_fwd_kernel(
 // tile, 64-wide p tile, chunk of HC heads); wave w owns tau columns
 // 16w..16w+15.  The raw C.B^T tile of each 64-row sigma tile is computed once
 // (transposed, rows = sigma in key_of_row order, columns = tau) and shared by
-// the HC heads: per head it is decayed/masked in registers and fed as the
-// B operand of Y^T[p][tau] += U^T[p][sigma] S^T[sigma][tau].  C rows stay in
-// registers for the whole block; B rows and U^T tiles go through LDS.
+// the HC heads: per head it is decayed in registers and fed as the B operand
+// of Y^T[p][tau] += U^T[p][sigma] S^T[sigma][tau] (U read through LDS
+// transpose reads).  C rows stay in registers for the whole block.
 //   Y^T = U^T . S^T + exp(dc_tau) * H_in . C^T
+// With dt >= 0 (mono) the decay of a sigma tile below the diagonal factors as
+//   e^{dc_tau - dc_sig} = e^{dc_tau - dc_t0} * e^{dc_t0 - dc_sig}  (both <= 1):
+// the sigma factor (times dt) is a per-tile table, the tau factor scales the
+// accumulator once before the diagonal tile, which is decayed exactly.
+// Tiles are prefetched into registers during the previous tile's MFMAs.
 // ---------------------------------------------------------------------------
 template <int NK, int HC>
-__global__ __launch_bounds__(256) void chunk_scan_fwd_bf16_kernel(
+__global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
     const bf16* __restrict__ u, const bf16* __restrict__ Bm, const bf16* __restrict__ Cm,
     const float* __restrict__ dt, const float* __restrict__ dc, const float* __restrict__ states,
-    float* __restrict__ y, SsdDims d) {
+    float* __restrict__ y, SsdDims d, int mono) {
   constexpr int N = 32 * NK;
   constexpr int LDN = N + 8, LDU = 64 + 8;
+  constexpr int HQ = N / 16;   // float4 of an H tile per thread (64 x N fp32 / 256 threads)
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* Bs = reinterpret_cast<bf16*>(smem_raw);  // [64][LDN]   B rows of the sigma tile
-  bf16* UT = Bs + 64 * LDN;                      // [HC][64][LDU] U^T per head
-  float* dcJ = reinterpret_cast<float*>(UT + HC * 64 * LDU);  // [HC][64] (log2 domain)
-  float* dtJ = dcJ + HC * 64;                                  // [HC][64]
+  bf16* Bs = reinterpret_cast<bf16*>(smem_raw);  // [64][LDN]     B rows of the sigma tile
+  bf16* Us = Bs + 64 * LDN;                      // [HC][64][LDU] U rows per head; later H_in tile
+  float* tab = reinterpret_cast<float*>(Us + HC * 64 * LDU);  // [HC][64] e^{dc_t0 - dc_sig} dt_sig
+  float* dcd = tab + HC * 64;                                 // [HC][64] dc_sig (log2)
+  float* dtd = dcd + HC * 64;                                 // [HC][64] dt_sig (0 past qlim)
 
   const int hpg = d.H / d.G;
   const int nhc = (hpg + HC - 1) / HC;
@@ -368,24 +375,28 @@ __global__ __launch_bounds__(256) void chunk_scan_fwd_bf16_kernel(
   const int h0 = g * hpg + hc * HC;
   const int nh = min(HC, hpg - hc * HC);
 
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int cl = lane & 15, lg = lane >> 4;
-  const int tau = t0 + 16 * wid + cl;  // this lane's output column
+  const int tid = threadIdx.x, lane = tid & 63, cl = lane & 15, lg = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tau = t0 + 16 * w + cl;  // this lane's output column
   const long tok0 = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc;
-  const long act_rs = static_cast<long>(d.G) * d.N;
-  const long u_rs = static_cast<long>(d.H) * d.P;
+  const int act_rs = d.G * N, u_rs = d.H * d.P;
+  const bf16* Bc = Bm + tok0 * act_rs + static_cast<long>(g) * N;
+  const bf16* uc = u + tok0 * u_rs + h0 * d.P;
+  const long crow0 = ((static_cast<long>(b) * d.H + h0) * d.nc + c) * d.Lc;   // dc / dt rows
+  const long hrow = static_cast<long>(d.nc) * d.Lc;                          // per head
 
   v8bf Cw[NK];
   {
-    const bf16* crow = Cm + (tok0 + min(tau, qlim - 1)) * act_rs + static_cast<long>(g) * d.N;
+    const bf16* crow = Cm + (tok0 + min(tau, qlim - 1)) * act_rs + static_cast<long>(g) * N + 8 * lg;
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks) Cw[ks] = tau < qlim ? load_v8bf(crow + 32 * ks + 8 * lg) : zero_v8bf();
+    for (int ks = 0; ks < NK; ++ks) Cw[ks] = tau < qlim ? load_v8bf(crow + 32 * ks) : zero_v8bf();
   }
-  float dct[HC];
+  float dct[HC], lf[HC];
 #pragma unroll
   for (int k = 0; k < HC; ++k) {
-    const long crow = ((static_cast<long>(b) * d.H + h0 + min(k, nh - 1)) * d.nc + c) * d.Lc;
-    dct[k] = tau < d.Lc ? dc[crow + tau] * kLog2e : 0.f;
+    const float* dch = dc + crow0 + min(k, nh - 1) * hrow;
+    dct[k] = dch[min(tau, d.Lc - 1)] * kLog2e;
+    lf[k] = fast_exp2(fminf(dct[k] - dch[t0] * kLog2e, 0.f));
   }
   v4f acc[HC][4];
 #pragma unroll
@@ -393,67 +404,74 @@ __global__ __launch_bounds__(256) void chunk_scan_fwd_bf16_kernel(
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[k][t] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  const int s_end = min(t0 + 64, qlim);
-  const int tid = threadIdx.x;
-  for (int s0 = 0; s0 < s_end; s0 += 64) {
-    const int sv = min(64, qlim - s0);
-    // issue every global load of the sigma tile, then commit to LDS
-    uint4 rb[NK];
+  // ---- sigma-tile staging (registers -> LDS) ----
+  uint4 pb[NK];
+  uint4 pu[HC][2];
+  float pdc = 0.f, pdt = 0.f, pdc0 = 0.f;
+  auto load_tile = [&](int s) {
+    const int s0 = 64 * s, sv = min(64, qlim - s0);
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
-      const int v = tid + 256 * i;
-      const int r = v / (N / 8), k0 = (v % (N / 8)) * 8;
-      rb[i] = ld16(Bm + (tok0 + s0 + r) * act_rs + static_cast<long>(g) * d.N + k0, r < sv);
+      const int e = tid + 256 * i;
+      const int row = e / (4 * NK), c8 = e % (4 * NK);
+      pb[i] = *reinterpret_cast<const uint4*>(Bc + static_cast<unsigned>((s0 + min(row, sv - 1)) * act_rs + 8 * c8));
+      if (row >= sv) pb[i] = uint4{0u, 0u, 0u, 0u};
     }
-    uint4 ub[(HC * 128 + 255) / 256][4];
 #pragma unroll
-    for (int j = 0; j < (HC * 128 + 255) / 256; ++j) {
-      const int it = tid + 256 * j;
-      const int k = it / 128, a = it % 16, cg = (it / 16) % 8;
-      const int pcol = p0 + 8 * cg;
-      const bool okc = k < nh && pcol < d.P;
+    for (int k = 0; k < HC; ++k)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        ub[j][i] = ld16(u + (tok0 + s0 + 4 * a + i) * u_rs + static_cast<long>(h0 + min(k, nh - 1)) * d.P + pcol,
-                        okc && 4 * a + i < sv);
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid + 256 * i;
+        const int row = e >> 3, col = p0 + 8 * (e & 7);
+        const bf16* src = uc + min(k, nh - 1) * d.P +
+                          static_cast<unsigned>((s0 + min(row, sv - 1)) * u_rs + min(col, d.P - 8));
+        pu[k][i] = *reinterpret_cast<const uint4*>(src);
+        if (row >= sv || col >= d.P || k >= nh) pu[k][i] = uint4{0u, 0u, 0u, 0u};
+      }
+    {
+      const int k = tid >> 6, sig = s0 + (tid & 63);
+      const float* dch = dc + crow0 + min(k, nh - 1) * hrow;
+      pdc = dch[min(sig, d.Lc - 1)] * kLog2e;
+      pdc0 = dch[t0] * kLog2e;
+      pdt = dt[crow0 + min(k, nh - 1) * hrow + min(sig, d.Lc - 1)];
+      if (sig >= qlim || k >= nh) pdt = 0.f;
     }
-    float dcv[(HC * 64 + 255) / 256], dtv[(HC * 64 + 255) / 256];
-#pragma unroll
-    for (int j = 0; j < (HC * 64 + 255) / 256; ++j) {
-      const int e = tid + 256 * j;
-      const int k = e / 64, sl = e % 64;
-      const long crow = ((static_cast<long>(b) * d.H + h0 + min(k, nh - 1)) * d.nc + c) * d.Lc;
-      const bool ok = k < nh && s0 + sl < d.Lc;
-      dcv[j] = ok ? dc[crow + s0 + sl] * kLog2e : 0.f;
-      dtv[j] = ok ? dt[crow + s0 + sl] : 0.f;
-    }
-    __syncthreads();  // the previous tile's LDS reads are done
+  };
+  auto commit_tile = [&]() {
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
-      const int v = tid + 256 * i;
-      const int r = v / (N / 8), k0 = (v % (N / 8)) * 8;
-      *reinterpret_cast<uint4*>(Bs + r * LDN + k0) = rb[i];
+      const int e = tid + 256 * i;
+      const int row = e / (4 * NK), c8 = e % (4 * NK);
+      *reinterpret_cast<uint4*>(Bs + row * LDN + 8 * c8) = pb[i];
     }
 #pragma unroll
-    for (int j = 0; j < (HC * 128 + 255) / 256; ++j) {
-      const int it = tid + 256 * j;
-      const int k = it / 128, a = it % 16, cg = (it / 16) % 8;
-      if (k < HC) {
-        bf16* dst = UT + k * 64 * LDU + (8 * cg) * LDU + 4 * a;
+    for (int k = 0; k < HC; ++k)
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj)
-          *reinterpret_cast<uint2*>(dst + jj * LDU) = col4_bf16(ub[j][0], ub[j][1], ub[j][2], ub[j][3], jj);
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid + 256 * i;
+        *reinterpret_cast<uint4*>(Us + k * 64 * LDU + (e >> 3) * LDU + 8 * (e & 7)) = pu[k][i];
       }
+    if (tid < HC * 64) {
+      dcd[tid] = pdc;
+      dtd[tid] = pdt;
+      tab[tid] = pdt * fast_exp2(fminf(pdc0 - pdc, 0.f));
     }
+  };
+
+  load_tile(0);
+  commit_tile();
+  __syncthreads();
+  for (int s = 0; s <= ti; ++s) {
+    const bool diag = s == ti;
+    if (!diag) load_tile(s + 1);
+    const int s0 = 64 * s;
+    const bool fact = mono && !diag;
+    if (mono && diag) {
 #pragma unroll
-    for (int j = 0; j < (HC * 64 + 255) / 256; ++j) {
-      const int e = tid + 256 * j;
-      if (e < HC * 64) {
-        dcJ[e] = dcv[j];
-        dtJ[e] = dtv[j];
-      }
+      for (int k = 0; k < HC; ++k)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[k][t] *= lf[k];
     }
-    __syncthreads();
     v4f cbt[4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
@@ -467,56 +485,88 @@ __global__ __launch_bounds__(256) void chunk_scan_fwd_bf16_kernel(
       if (k >= nh) break;
       v4f sk[4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 4; ++kt) {
+        const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);   // 4 consecutive sigma rows
+        if (fact) {
+          const float4 tq = *reinterpret_cast<const float4*>(tab + k * 64 + tb);
+          sk[kt] = cbt[kt] * v4f{tq.x, tq.y, tq.z, tq.w};
+        } else {
+          const float4 dq = *reinterpret_cast<const float4*>(dcd + k * 64 + tb);
+          const float4 tq = *reinterpret_cast<const float4*>(dtd + k * 64 + tb);
+          const float dv[4] = {dq.x, dq.y, dq.z, dq.w}, tv[4] = {tq.x, tq.y, tq.z, tq.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int sl = key_of_row(kt, 4 * lg + i);
-          const int sg = s0 + sl;
-          float v = 0.f;
-          if (sg <= tau && sg < qlim)
-            v = cbt[kt][i] * fast_exp2(fminf(dct[k] - dcJ[k * 64 + sl], 0.f)) * dtJ[k * 64 + sl];
-          sk[kt][i] = v;
+          for (int i = 0; i < 4; ++i) {
+            const float e = fast_exp2(fminf(dct[k] - dv[i], 0.f)) * tv[i];
+            sk[kt][i] = s0 + tb + i <= tau ? cbt[kt][i] * e : 0.f;
+          }
         }
-      const bf16* ut = UT + k * 64 * LDU + cl * LDU + 8 * lg;
+      }
+      const bf16* ut = Us + k * 64 * LDU;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const v8bf pb = pack_p(sk[2 * ks], sk[2 * ks + 1]);
+        const v8bf pbk = pack_p(sk[2 * ks], sk[2 * ks + 1]);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-          acc[k][t] = mfma_bf16(load_v8bf(ut + 16 * t * LDU + 32 * ks), pb, acc[k][t]);
+          acc[k][t] = mfma_bf16(lds_tr8(ut + (32 * ks + 8 * lg) * LDU + 16 * t, LDU, lane), pbk, acc[k][t]);
       }
+    }
+    __syncthreads();  // every wave is done with this tile
+    if (!diag) {
+      commit_tile();
+      __syncthreads();
     }
   }
 
-  // state contribution exp(dc_tau) * H_in . C^T, then the store
+  // ---- state contribution exp(dc_tau) * H_in . C^T, one head per stage, then the store ----
+  bf16* Hs = Us;   // [64][LDN] bf16 (fits in the U tiles' space)
+  float4 ph[HQ];
+  auto load_h = [&](int k) {
+    const float* Hb = states + (((static_cast<long>(b) * d.nc + c) * d.H + h0 + k) * d.P + p0) * N;
+#pragma unroll
+    for (int i = 0; i < HQ; ++i) {
+      const int e = tid + 256 * i;
+      const int row = e / (N / 4), c4 = e % (N / 4);
+      ph[i] = *reinterpret_cast<const float4*>(Hb + static_cast<unsigned>(min(row, d.P - p0 - 1) * N + 4 * c4));
+      if (p0 + row >= d.P) ph[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto commit_h = [&]() {
+#pragma unroll
+    for (int i = 0; i < HQ; ++i) {
+      const int e = tid + 256 * i;
+      const int row = e / (N / 4), c4 = e % (N / 4);
+      *reinterpret_cast<uint2*>(Hs + row * LDN + 4 * c4) =
+          uint2{pack_bf16x2(ph[i].x, ph[i].y), pack_bf16x2(ph[i].z, ph[i].w)};
+    }
+  };
+  load_h(0);
+  commit_h();
+  __syncthreads();
 #pragma unroll
   for (int k = 0; k < HC; ++k) {
     if (k >= nh) break;
-    const int h = h0 + k;
-    const float* Hb = states + (((static_cast<long>(b) * d.nc + c) * d.H + h) * d.P) * d.N;
+    const bool more = k + 1 < nh;
+    if (more) load_h(k + 1);
     const float e = fast_exp2(dct[k]);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int p = p0 + 16 * t + cl;
       v4f st = v4f{0.f, 0.f, 0.f, 0.f};
-      if (p < d.P) {
-        const float* hrow = Hb + static_cast<long>(p) * d.N + 8 * lg;
+      const bf16* hrow2 = Hs + (16 * t + cl) * LDN + 8 * lg;
 #pragma unroll
-        for (int ks = 0; ks < NK; ++ks) {
-          const float4 a = *reinterpret_cast<const float4*>(hrow + 32 * ks);
-          const float4 bq = *reinterpret_cast<const float4*>(hrow + 32 * ks + 4);
-          const uint4 r = {pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w), pack_bf16x2(bq.x, bq.y),
-                           pack_bf16x2(bq.z, bq.w)};
-          st = mfma_bf16(__builtin_bit_cast(v8bf, r), Cw[ks], st);
-        }
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < NK; ++ks) st = mfma_bf16(zero_v8bf(), Cw[ks], st);
-      }
+      for (int ks = 0; ks < NK; ++ks) st = mfma_bf16(load_v8bf(hrow2 + 32 * ks), Cw[ks], st);
       acc[k][t] += st * e;
     }
-    if (tau < qlim) {
-      float* yrow = y + (tok0 + tau) * u_rs + static_cast<long>(h) * d.P;
+    if (more) {
+      __syncthreads();
+      commit_h();
+      __syncthreads();
+    }
+  }
+  if (tau < qlim) {
+#pragma unroll
+    for (int k = 0; k < HC; ++k) {
+      if (k >= nh) break;
+      float* yrow = y + (tok0 + tau) * u_rs + static_cast<long>(h0 + k) * d.P;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int p = p0 + 16 * t + 4 * lg;
@@ -602,13 +652,13 @@ int launch_chunk_scan(const void* u, const void* B, const void* C, const float* 
 template <int NK>
 int launch_chunk_scan_bf16_nk(const void* u, const void* B, const void* C, const float* dt,
                               const float* dc, const float* states, float* y, const SsdDims& d,
-                              hipStream_t s) {
+                              int mono, hipStream_t s) {
   constexpr int HC = 4;
   const int hpg = d.H / d.G;
   const int nhc = (hpg + HC - 1) / HC;
   const long blocks = static_cast<long>((d.Lc + 63) / 64) * ((d.P + 63) / 64) * nhc * d.G *
                       d.nc * d.b;
-  const size_t smem = sizeof(bf16) * (64 * (32 * NK + 8) + HC * 64 * 72) + sizeof(float) * HC * 128;
+  const size_t smem = sizeof(bf16) * (64 * (32 * NK + 8) + HC * 64 * 72) + sizeof(float) * HC * 192;
   if (smem > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(
         reinterpret_cast<const void*>(chunk_scan_fwd_bf16_kernel<NK, HC>),
@@ -618,29 +668,29 @@ int launch_chunk_scan_bf16_nk(const void* u, const void* B, const void* C, const
   ProfScope prof_("chunk_scan_fwd", s);
   hipLaunchKernelGGL((chunk_scan_fwd_bf16_kernel<NK, HC>), dim3(blocks), dim3(256), smem, s,
                      static_cast<const bf16*>(u), static_cast<const bf16*>(B),
-                     static_cast<const bf16*>(C), dt, dc, states, y, d);
+                     static_cast<const bf16*>(C), dt, dc, states, y, d, mono);
   SA_CHECK_LAUNCH("chunk_scan_fwd_bf16");
   return 0;
 }
 
 inline bool chunk_scan_bf16_ok(const SsdDims& d, const void* u, const void* B, const void* C,
                                const float* states) {
-  return d.N % 32 == 0 && d.N <= 256 && d.P % 16 == 0 && aligned16(u) && aligned16(B) &&
+  return d.N % 32 == 0 && d.N <= 256 && d.P % 8 == 0 && aligned16(u) && aligned16(B) &&
          aligned16(C) && aligned16(states);
 }
 
 int launch_chunk_scan_bf16(const void* u, const void* B, const void* C, const float* dt,
                            const float* dc, const float* states, float* y, const SsdDims& d,
-                           hipStream_t s) {
+                           int mono, hipStream_t s) {
   switch (d.N / 32) {
-    case 1: return launch_chunk_scan_bf16_nk<1>(u, B, C, dt, dc, states, y, d, s);
-    case 2: return launch_chunk_scan_bf16_nk<2>(u, B, C, dt, dc, states, y, d, s);
-    case 3: return launch_chunk_scan_bf16_nk<3>(u, B, C, dt, dc, states, y, d, s);
-    case 4: return launch_chunk_scan_bf16_nk<4>(u, B, C, dt, dc, states, y, d, s);
-    case 5: return launch_chunk_scan_bf16_nk<5>(u, B, C, dt, dc, states, y, d, s);
-    case 6: return launch_chunk_scan_bf16_nk<6>(u, B, C, dt, dc, states, y, d, s);
-    case 7: return launch_chunk_scan_bf16_nk<7>(u, B, C, dt, dc, states, y, d, s);
-    default: return launch_chunk_scan_bf16_nk<8>(u, B, C, dt, dc, states, y, d, s);
+    case 1: return launch_chunk_scan_bf16_nk<1>(u, B, C, dt, dc, states, y, d, mono, s);
+    case 2: return launch_chunk_scan_bf16_nk<2>(u, B, C, dt, dc, states, y, d, mono, s);
+    case 3: return launch_chunk_scan_bf16_nk<3>(u, B, C, dt, dc, states, y, d, mono, s);
+    case 4: return launch_chunk_scan_bf16_nk<4>(u, B, C, dt, dc, states, y, d, mono, s);
+    case 5: return launch_chunk_scan_bf16_nk<5>(u, B, C, dt, dc, states, y, d, mono, s);
+    case 6: return launch_chunk_scan_bf16_nk<6>(u, B, C, dt, dc, states, y, d, mono, s);
+    case 7: return launch_chunk_scan_bf16_nk<7>(u, B, C, dt, dc, states, y, d, mono, s);
+    default: return launch_chunk_scan_bf16_nk<8>(u, B, C, dt, dc, states, y, d, mono, s);
   }
 }
 
@@ -654,7 +704,7 @@ int ssd_fwd_impl(const void* u, const float* A, const void* B, const void* C,
   if ((rc = launch_chunk_outer<MT, T, T, 0>(u, B, dt, dc, length, states, d, s))) return rc;
   if ((rc = launch_state_passing_fwd(states, h_init, h_last, dc, d, s))) return rc;
   if (sizeof(T) == 2 && chunk_scan_bf16_ok(d, u, B, C, states))
-    return launch_chunk_scan_bf16(u, B, C, dt, dc, states, y, d, s);
+    return launch_chunk_scan_bf16(u, B, C, dt, dc, states, y, d, lo >= 0.f ? 1 : 0, s);
   return launch_chunk_scan<MT, T>(u, B, C, dt, dc, states, y, d, s);
 }
 
