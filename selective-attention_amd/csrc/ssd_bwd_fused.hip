@@ -78,29 +78,6 @@ __device__ __forceinline__ void f32_tile_commit(bf16* tile, const float4 (&r)[4]
   pl[0] = uint4{lo[0], lo[1], lo[2], lo[3]};
   pl[1] = uint4{lo[4], lo[5], lo[6], lo[7]};
 }
-// 64 x (32 NK) bf16 tile, raw 16-byte copies shared by NTHR threads
-template <int NK, int NTHR>
-struct BfTile {
-  static constexpr int PER = 64 * 4 * NK / NTHR;   // uint4 per thread
-  uint4 v[PER];
-  __device__ __forceinline__ void load(const bf16* src, int rs, int rows_valid, int tid) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int e = tid + NTHR * i;
-      const int row = e / (4 * NK), c8 = e % (4 * NK);
-      v[i] = *reinterpret_cast<const uint4*>(src + static_cast<unsigned>(min(row, rows_valid - 1) * rs + 8 * c8));
-      if (row >= rows_valid) v[i] = uint4{0u, 0u, 0u, 0u};
-    }
-  }
-  __device__ __forceinline__ void commit(bf16* dst, int ld, int tid) const {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int e = tid + NTHR * i;
-      const int row = e / (4 * NK), c8 = e % (4 * NK);
-      *reinterpret_cast<uint4*>(dst + row * ld + 8 * c8) = v[i];
-    }
-  }
-};
 __device__ __forceinline__ uint2 pack4_bf16(const v4f& v) {
   return uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
 }

@@ -159,6 +159,165 @@ __global__ __launch_bounds__(256) void chunk_outer_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// chunk outer products, bf16 fast path (P and N multiples of 64):
+//   MODE 0: states[p][n] = sum_t u[t,p] w_t B[t,n],  w_t = e^{min(dc_last - dc_t, 0)} dt_t
+//   MODE 1: dH[p][n]     = sum_t dy[t,p] e^{dc_t} C[t,n]   (t < length)
+// One block per (b, chunk, head, 64-wide p tile), 4 waves; wave w computes
+// D^T[n][p] for its N/4 columns n and the 64 p.  Both operands come from
+// row-major t tiles in LDS through transpose reads: A = X^T (X = B or C) and
+// the B operand = the scaled U (MODE 0, one bf16 plane) or the scaled dy
+// (MODE 1, hi + lo planes).  Each lane ends with 4 consecutive n of one p
+// (16-byte stores).  t tiles are double-buffered and prefetched into
+// registers during the previous tile's MFMAs.
+// ---------------------------------------------------------------------------
+template <int NK, int MODE>
+__global__ __launch_bounds__(256, 2) void chunk_outer_bf16_kernel(
+    const void* __restrict__ a_src, const bf16* __restrict__ x_src, const float* __restrict__ dt,
+    const float* __restrict__ dc, const int64_t* __restrict__ length, float* __restrict__ out,
+    SsdDims d) {
+  constexpr int N = 32 * NK, LDX = N + 8, LDA = 64 + 8;
+  constexpr int NPL = MODE == 1 ? 2 : 1;   // planes of the scaled operand
+  constexpr int NTW = N / 64;              // 16-wide n tiles per wave
+  constexpr int STAGE = NPL * 64 * LDA + 64 * LDX;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  bf16* sm = reinterpret_cast<bf16*>(smem_raw);   // [2][STAGE]: As [NPL][64][LDA], Xs [64][LDX]
+
+  const int ptiles = d.P / 64;
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int pti = bid % ptiles;
+  int rest = bid / ptiles;
+  const int h = rest % d.H;
+  rest /= d.H;
+  const int c = rest % d.nc;
+  const int b = rest / d.nc;
+  const int p0 = 64 * pti;
+  const int g = h / (d.H / d.G);
+  const long crow = ((static_cast<long>(b) * d.H + h) * d.nc + c) * d.Lc;
+  const int qlim = min(d.Lc, d.L - c * d.Lc);
+  const int klim = MODE == 0 ? qlim : max(0, chunk_limit(seq_limit(length, b, d.L), c, d.Lc));
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  float* o = out + (((static_cast<long>(b) * d.nc + c) * d.H + h) * d.P + p0) * N;
+  v4f acc[NTW][4];
+#pragma unroll
+  for (int i = 0; i < NTW; ++i)
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) acc[i][pt] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  if (klim > 0) {
+    const long tok0 = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc;
+    const int a_rs = d.H * d.P, x_rs = d.G * N;
+    const bf16* xc = x_src + tok0 * x_rs + static_cast<long>(g) * N;
+    const float dcl = dc[crow + d.Lc - 1] * kLog2e;
+    auto row_scale = [&](int t) __attribute__((always_inline)) {   // scale of row t (0 past klim)
+      const int tc = min(t, klim - 1);
+      float sc;
+      if constexpr (MODE == 0) sc = fast_exp2(fminf(dcl - dc[crow + tc] * kLog2e, 0.f)) * dt[crow + tc];
+      else sc = fast_exp2(dc[crow + tc] * kLog2e);
+      return t < klim ? sc : 0.f;
+    };
+    // prefetch registers
+    uint4 pa0[MODE == 0 ? 2 : 1];
+    float4 pa1[MODE == 1 ? 4 : 1];
+    float psc[2];
+    BfTile<NK, 256> px;
+    auto load_tile = [&](int tt) __attribute__((always_inline)) {
+      const int t0 = 64 * tt, kv = min(64, klim - t0);
+      if constexpr (MODE == 0) {
+        const bf16* ac = static_cast<const bf16*>(a_src) + tok0 * a_rs + h * d.P + p0;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int e = tid + 256 * i, row = e >> 3;
+          pa0[i] = *reinterpret_cast<const uint4*>(ac + static_cast<unsigned>((t0 + min(row, kv - 1)) * a_rs + 8 * (e & 7)));
+          psc[i] = row_scale(t0 + row);
+        }
+      } else {
+        const float* ac = static_cast<const float*>(a_src) + tok0 * a_rs + h * d.P + p0;
+        const int row = tid >> 2;
+        const float* pp = ac + static_cast<unsigned>((t0 + min(row, kv - 1)) * a_rs + 16 * (tid & 3));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pa1[i] = *reinterpret_cast<const float4*>(pp + 4 * i);
+        psc[0] = row_scale(t0 + row);
+      }
+      px.load(xc + static_cast<long>(t0) * x_rs, x_rs, kv, tid);
+    };
+    auto commit_tile = [&](int slot) __attribute__((always_inline)) {
+      bf16* As = sm + slot * STAGE;
+      bf16* Xs = As + NPL * 64 * LDA;
+      if constexpr (MODE == 0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int e = tid + 256 * i, row = e >> 3;
+          const uint32_t q[4] = {pa0[i].x, pa0[i].y, pa0[i].z, pa0[i].w};
+          uint32_t r[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            r[j] = pack_bf16x2(bf16lo_to_f32(q[j]) * psc[i], bf16hi_to_f32(q[j]) * psc[i]);
+          *reinterpret_cast<uint4*>(As + row * LDA + 8 * (e & 7)) = uint4{r[0], r[1], r[2], r[3]};
+        }
+      } else {
+        const int row = tid >> 2, c0 = 16 * (tid & 3);
+        uint32_t hi[8], lo[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v[4] = {pa1[i].x * psc[0], pa1[i].y * psc[0], pa1[i].z * psc[0], pa1[i].w * psc[0]};
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const uint32_t hh = pack_bf16x2(v[2 * j], v[2 * j + 1]);
+            hi[2 * i + j] = hh;
+            lo[2 * i + j] = pack_bf16x2(v[2 * j] - bf16lo_to_f32(hh), v[2 * j + 1] - bf16hi_to_f32(hh));
+          }
+        }
+        uint4* ph = reinterpret_cast<uint4*>(As + row * LDA + c0);
+        uint4* pl = reinterpret_cast<uint4*>(As + 64 * LDA + row * LDA + c0);
+        ph[0] = uint4{hi[0], hi[1], hi[2], hi[3]};
+        ph[1] = uint4{hi[4], hi[5], hi[6], hi[7]};
+        pl[0] = uint4{lo[0], lo[1], lo[2], lo[3]};
+        pl[1] = uint4{lo[4], lo[5], lo[6], lo[7]};
+      }
+      px.commit(Xs, LDX, tid);
+    };
+
+    const int ntt = (klim + 63) / 64;
+    load_tile(0);
+    commit_tile(0);
+    __syncthreads();
+    for (int tt = 0; tt < ntt; ++tt) {
+      const bool has_next = tt + 1 < ntt;
+      if (has_next) load_tile(tt + 1);
+      const bf16* As = sm + (tt & 1) * STAGE;
+      const bf16* Xs = As + NPL * 64 * LDA;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        v8bf bop[4][NPL];
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+          for (int pl = 0; pl < NPL; ++pl)
+            bop[pt][pl] = lds_tr8(As + pl * 64 * LDA + (32 * ks + 8 * lg) * LDA + 16 * pt, LDA, lane);
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) {
+          const v8bf a = lds_tr8(Xs + (32 * ks + 8 * lg) * LDX + 16 * (NTW * w + i), LDX, lane);
+#pragma unroll
+          for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+            for (int pl = 0; pl < NPL; ++pl) acc[i][pt] = mfma_bf16(a, bop[pt][pl], acc[i][pt]);
+        }
+      }
+      if (has_next) commit_tile((tt + 1) & 1);
+      __syncthreads();
+    }
+  }
+  // D^T[n][p]: lane holds n = 16 nt + 4 lg + r of p = 16 pt + li
+#pragma unroll
+  for (int i = 0; i < NTW; ++i)
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt)
+      *reinterpret_cast<float4*>(o + static_cast<unsigned>((16 * pt + li) * N + 16 * (NTW * w + i) + 4 * lg)) =
+          make_float4(acc[i][pt][0], acc[i][pt][1], acc[i][pt][2], acc[i][pt][3]);
+}
+
+// ---------------------------------------------------------------------------
 // state passing (forward): sequential over chunks, parallel over (b, h, P*N).
 // Loads of a group of chunks are issued together before the dependent math.
 // ---------------------------------------------------------------------------
@@ -599,9 +758,35 @@ int launch_chunk_cumsum(const void* delta_raw, const float* A, const float* bias
   return 0;
 }
 
+template <int NK, int MODE>
+int launch_chunk_outer_bf16_nk(const void* a, const void* x, const float* dt, const float* dc,
+                               const int64_t* length, float* out, const SsdDims& d, hipStream_t s) {
+  const long blocks = static_cast<long>(d.P / 64) * d.H * d.nc * d.b;
+  const size_t smem = 2 * sizeof(bf16) * ((MODE == 1 ? 2 : 1) * 64 * 72 + 64 * (32 * NK + 8));
+  if (smem > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(chunk_outer_bf16_kernel<NK, MODE>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
+    SA_CHECK_ARG(e == hipSuccess, "chunk_outer_bf16: %zu B of LDS refused", smem);
+  }
+  ProfScope prof_(MODE == 0 ? "chunk_state_fwd" : "chunk_dstate_bwd", s);
+  hipLaunchKernelGGL((chunk_outer_bf16_kernel<NK, MODE>), dim3(blocks), dim3(256), smem, s, a,
+                     static_cast<const bf16*>(x), dt, dc, length, out, d);
+  SA_CHECK_LAUNCH("chunk_outer_bf16");
+  return 0;
+}
+
 template <typename MT, typename TA, typename TB, int MODE>
 int launch_chunk_outer(const void* a, const void* bsrc, const float* dt, const float* dc,
                        const int64_t* length, float* out, const SsdDims& d, hipStream_t s) {
+  if (sizeof(MT) == 2 && sizeof(TB) == 2 && d.P % 64 == 0 && d.N % 64 == 0 && aligned16(a) &&
+      aligned16(bsrc)) {
+    switch (d.N / 64) {
+      case 1: return launch_chunk_outer_bf16_nk<2, MODE>(a, bsrc, dt, dc, length, out, d, s);
+      case 2: return launch_chunk_outer_bf16_nk<4, MODE>(a, bsrc, dt, dc, length, out, d, s);
+      case 3: return launch_chunk_outer_bf16_nk<6, MODE>(a, bsrc, dt, dc, length, out, d, s);
+      default: return launch_chunk_outer_bf16_nk<8, MODE>(a, bsrc, dt, dc, length, out, d, s);
+    }
+  }
   const long blocks = static_cast<long>((d.P + 63) / 64) * ((d.N + 63) / 64) * d.b * d.nc * d.H;
   const int vec_a = aligned16(a) && (static_cast<long>(d.H) * d.P) % 8 == 0 && d.P % 8 == 0;
   const int vec_b = aligned16(bsrc) && (static_cast<long>(d.G) * d.N) % 8 == 0 && d.N % 8 == 0;

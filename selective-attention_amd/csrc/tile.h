@@ -185,4 +185,29 @@ __device__ __forceinline__ void stage_transposed(MT* lds, int ld, const TS* src,
 
 __host__ __device__ constexpr int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
+// 64 x (32 NK) bf16 tile in registers, raw 16-byte copies shared by NTHR threads.
+// Rows past rows_valid read row rows_valid - 1 and are zeroed (unconditional loads).
+template <int NK, int NTHR>
+struct BfTile {
+  static constexpr int PER = 64 * 4 * NK / NTHR;   // uint4 per thread
+  uint4 v[PER];
+  __device__ __forceinline__ void load(const bf16* src, int rs, int rows_valid, int tid) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + NTHR * i;
+      const int row = e / (4 * NK), c8 = e % (4 * NK);
+      v[i] = *reinterpret_cast<const uint4*>(src + static_cast<unsigned>(min(row, rows_valid - 1) * rs + 8 * c8));
+      if (row >= rows_valid) v[i] = uint4{0u, 0u, 0u, 0u};
+    }
+  }
+  __device__ __forceinline__ void commit(bf16* dst, int ld, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + NTHR * i;
+      const int row = e / (4 * NK), c8 = e % (4 * NK);
+      *reinterpret_cast<uint4*>(dst + row * ld + 8 * c8) = v[i];
+    }
+  }
+};
+
 }  // namespace sa
