@@ -173,181 +173,339 @@ __global__ __launch_bounds__(256) void sparse_attn_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// paged GQA decode, split over pages.  One wave per (batch row, kv head,
-// split of PPS pages); the query heads of the group sit in the first lanes
-// of each 16-lane column group (columns >= group size are padding).  No LDS:
-// K rows and V^T rows go from HBM straight into MFMA operands; all loads of
-// a 64-key tile are issued before its first MFMA.
+// paged GQA decode, stream-K over 64-key tiles.  The work is the global list
+// of tiles in (batch row, kv head, tile) order; a plan kernel prefix-sums the
+// tiles per row, and the decode kernel runs one resident round of W waves,
+// wave w taking tiles [floor(wT/W), floor((w+1)T/W)).  Every wave streams the
+// same number of tiles whatever the spread of sequence lengths, so no wave
+// slot idles while a long split finishes.  A wave writes one partial
+// (unnormalised O^T, running max and sum) for each (row, kv head) it touches,
+// under segment id  row * Hkv + kv head + w:  ids grow along the tile order,
+// so the segments of one (row, kv head) are consecutive and the merge kernel
+// reads them as one contiguous run.
+//
+// Inside a wave the query heads of the group sit in the first lanes of each
+// 16-lane column group (columns >= group size are padding).  No LDS: K rows
+// and V^T rows go from HBM straight into MFMA operands.  The K and V halves
+// of consecutive tiles are software-pipelined through one register buffer
+// each: K of tile t+1 is in flight while tile t's softmax and V^T.P^T run, V
+// of tile t+1 while tile t+1's K.Q^T runs, so the wave always has HBM reads
+// outstanding.  Page ids are fetched 64 at a time, one per lane, and
+// broadcast with readlane.
 // ---------------------------------------------------------------------------
-template <int D>
-struct DecodeTile {
-  v8bf kf[4][D / 32];
-  v8bf vf[2][D / 16];
-  long kbase;  // key index of the tile's first key in the K pool (per kv head)
-  int nk;      // valid keys (0: skip)
-  int pos0;    // sequence position of the tile's first key
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
 };
 
-template <int D>
-__device__ __forceinline__ void decode_load(DecodeTile<D>& T, const bf16* __restrict__ kp,
-                                            const bf16* __restrict__ vp, int page, int Hkv,
-                                            int kvh, int ps, int num_pages, int k0, int nk_page,
-                                            int pos0, int c, int g) {
-  constexpr int KS = D / 32, DT = D / 16;
-  T.nk = (page < 0 || page >= num_pages) ? 0 : min(64, nk_page - k0);
-  T.pos0 = pos0;
-  const long pbase = (static_cast<long>(max(page, 0)) * Hkv + kvh) * ps;
-  T.kbase = pbase + k0;
-  const bf16* kbase = kp + (pbase + k0) * D;
-  const bf16* vbase = vp + pbase * D + k0;  // V^T page: [D][ps]
-  const int nk = T.nk;
-  // Every address below stays inside the (clamped) page: keys past nk are
-  // read but never used -- their scores are replaced by -inf and their V
-  // entries are zeroed by a bit mask, so stale pool contents cannot leak in.
-#pragma unroll
-  for (int kt = 0; kt < 4; ++kt) {
-    const int key = key_of_row(kt, c);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) T.kf[kt][ks] = load_v8bf(kbase + key * D + 32 * ks + 8 * g);
-  }
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const int kk = 32 * ks + 8 * g;
-    uint32_t mk[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w)
-      mk[w] = (kk + 2 * w < nk ? 0x0000ffffu : 0u) | (kk + 2 * w + 1 < nk ? 0xffff0000u : 0u);
-#pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      uint4 r = *reinterpret_cast<const uint4*>(vbase + static_cast<long>(16 * t + c) * ps + kk);
-      r.x &= mk[0];
-      r.y &= mk[1];
-      r.z &= mk[2];
-      r.w &= mk[3];
-      T.vf[ks][t] = __builtin_bit_cast(v8bf, r);
-    }
-  }
-}
+struct DecodeSlot {
+  long kidx;  // index of the tile's first key in the (page, kv head, key) pool
+  int nk;     // valid keys of the tile (0: invalid page id)
+  int pos0;   // sequence position of the tile's first key
+  int k0;     // offset of the tile inside its page
+};
 
+// K rows of a 64-key tile as A operands of S^T = K.Q^T: lane (c, g) reads key
+// key_of_row(kt, c), dims 32ks + 8g .. +7
 template <int D>
-__device__ __forceinline__ void decode_compute(const DecodeTile<D>& T, const v8bf (&qf)[D / 32],
-                                               v4f (&acc)[D / 16], float& m, float& l,
-                                               const float* __restrict__ key_bias, int n,
-                                               int grp, float scale_log2, int c, int g) {
-  constexpr int KS = D / 32, DT = D / 16;
-  if (T.nk <= 0) return;
-  v4f sc[4];
-#pragma unroll
-  for (int kt = 0; kt < 4; ++kt) {
-    sc[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) sc[kt] = mfma_bf16(T.kf[kt][ks], qf[ks], sc[kt]);
-  }
+__device__ __forceinline__ void decode_load_k(v8bf (&kf)[4][D / 32], const bf16* __restrict__ kt0,
+                                              int c, int g) {
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kl = key_of_row(kt, 4 * g + i);
-      float val = kNegInf;
-      if (kl < T.nk && c < grp) {
-        val = sc[kt][i] * scale_log2;
-        if (key_bias && T.pos0 + kl != n - 1) val += key_bias[T.kbase + kl] * kLog2e;
-      }
-      sc[kt][i] = val;
+    for (int ks = 0; ks < D / 32; ++ks)
+      kf[kt][ks] = load_v8bf(kt0 + static_cast<unsigned>(key_of_row(kt, c) * D + 32 * ks + 8 * g));
+}
+
+// V^T rows of a 64-key tile as A operands of O^T += V^T.P^T: lane (c, g)
+// reads dim 16t + c, keys 32ks + 8g .. +7 (a 16-byte run of the page's V^T row)
+// (voff = 2 (c * ps + 8g) bytes, per lane; the row step 32 * ps bytes is
+// wave-uniform and goes into the scalar offset)
+template <int D>
+__device__ __forceinline__ void decode_load_v(v8bf (&vf)[2][D / 16], const bf16* __restrict__ vt0,
+                                              int ps, unsigned voff) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(vt0);
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t)
+      vf[ks][t] = buf_load_v8bf(r, voff, static_cast<unsigned>(32 * t * ps + 64 * ks));
+}
+
+// tiles of row r: ceil(clamp(seq_lens[r], 0, max_pages * ps) / 64)
+__device__ __forceinline__ int decode_row_len(const int32_t* seq_lens, int r, int max_pages, int ps) {
+  return min(max(seq_lens[r], 0), max_pages * ps);
+}
+
+// cum_row[r] = 64-key tiles of rows < r (per kv head), r = 0..b.  One block.
+__global__ __launch_bounds__(1024) void paged_decode_plan_kernel(
+    const int32_t* __restrict__ seq_lens, int b, int ps, int max_pages,
+    int32_t* __restrict__ cum_row) {
+  __shared__ int wtot[16];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  int carry = 0;
+  if (tid == 0) cum_row[0] = 0;
+  for (int base = 0; base < b; base += 1024) {
+    const int r = base + tid;
+    int v = r < b ? (decode_row_len(seq_lens, r, max_pages, ps) + 63) >> 6 : 0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(v, o, 64);
+      if (lane >= o) v += t;
     }
-  softmax_block<4, DT>(sc, acc, m, l);
+    if (lane == 63) wtot[wid] = v;
+    __syncthreads();
+    int pre = carry, tot = 0;
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const v8bf pb = pack_p(sc[2 * ks], sc[2 * ks + 1]);
-#pragma unroll
-    for (int t = 0; t < DT; ++t) acc[t] = mfma_bf16(T.vf[ks][t], pb, acc[t]);
+    for (int j = 0; j < 16; ++j) {
+      pre += j < wid ? wtot[j] : 0;
+      tot += wtot[j];
+    }
+    if (r < b) cum_row[r + 1] = pre + v;
+    carry += tot;
+    __syncthreads();  // wtot is rewritten by the next chunk
   }
 }
 
-template <int D>
-__global__ __launch_bounds__(64) void paged_decode_kernel(
+// first tile of wave w and the wave that holds tile g (W waves, T tiles)
+__device__ __forceinline__ long decode_wave_begin(int w, long T, int W) {
+  return static_cast<long>(w) * T / W;
+}
+__device__ __forceinline__ int decode_wave_of(long g, long T, int W) {
+  return static_cast<int>(((g + 1) * W + T - 1) / T - 1);
+}
+
+template <int D, bool BIAS>
+__global__ __launch_bounds__(64, 2) void paged_decode_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ kp, const bf16* __restrict__ vp,
     const int32_t* __restrict__ page_table, const int32_t* __restrict__ seq_lens,
-    const float* __restrict__ key_bias, float* __restrict__ part_o, float* __restrict__ part_ml,
-    int Hq, int Hkv, int ps, int max_pages, int num_pages, int pps, int max_splits,
-    float scale_log2) {
+    const float* __restrict__ key_bias, const int32_t* __restrict__ cum_row,
+    float* __restrict__ part_o, float* __restrict__ part_ml, int b, int Hq, int Hkv, int ps,
+    int max_pages, int num_pages, int W, float scale_log2) {
   constexpr int DT = D / 16, KS = D / 32;
-  const int item = blockIdx.x;
-  const int split = item % max_splits;
-  const int rest = item / max_splits;
-  const int kvh = rest % Hkv;
-  const int bi = rest / Hkv;
+  const int w = blockIdx.x;
+  const long T = static_cast<long>(Hkv) * cum_row[b];
+  // with at most T waves every wave gets at least one tile, which keeps the
+  // segment ids of one (row, kv head) consecutive
+  W = static_cast<int>(min(static_cast<long>(W), T));
+  if (w >= W) return;
+  long gt = decode_wave_begin(w, T, W);
+  const long gt_end = decode_wave_begin(w + 1, T, W);
   const int grp = Hq / Hkv;
-  const int n = min(max(seq_lens[bi], 0), max_pages * ps);
-  const int npg = (n + ps - 1) / ps;
-  const int p_begin = split * pps, p_end = min(npg, p_begin + pps);
-  if (p_begin >= p_end) return;
   const int lane = threadIdx.x, c = lane & 15, g = lane >> 4;
+  const int pshift = ps == 128 ? 7 : 6;  // page size 64 or 128
+  const int tshift = pshift - 6;         // log2(64-key tiles per page)
+  const unsigned voff = static_cast<unsigned>(2 * (c * ps + 8 * g));
 
-  const bf16* qrow = q + (static_cast<long>(bi) * Hq + kvh * grp + min(c, grp - 1)) * D;
-  v8bf qf[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) qf[ks] = c < grp ? load_v8bf(qrow + 32 * ks + 8 * g) : zero_v8bf();
-
-  float m = kNegInf, l = 0.0f;
-  v4f acc[DT];
-#pragma unroll
-  for (int t = 0; t < DT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  // 64-key tiles of this split, in order
-  const int tiles_per_page = ps / 64;
-  const int ntiles = (p_end - p_begin) * tiles_per_page;
-  const int32_t* prow = page_table + static_cast<long>(bi) * max_pages;
-  auto load = [&](DecodeTile<D>& T, int t) {
-    const int pg = p_begin + t / tiles_per_page;
-    const int k0 = (t % tiles_per_page) * 64;
-    decode_load<D>(T, kp, vp, prow[pg], Hkv, kvh, ps, num_pages, k0, min(ps, n - pg * ps),
-                   pg * ps + k0, c, g);
-  };
-  DecodeTile<D> A;
-  for (int t = 0; t < ntiles; ++t) {
-    load(A, t);
-    decode_compute<D>(A, qf, acc, m, l, key_bias, n, grp, scale_log2, c, g);
-  }
-  // partial results: O^T[d][q] unnormalised, with m (log2 domain) and l
-  const long slot = (static_cast<long>(bi) * Hkv + kvh) * max_splits + split;
-  if (c < grp) {
-    float* po = part_o + (slot * grp + c) * D;
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-      *reinterpret_cast<float4*>(po + 16 * t + 4 * g) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
-    if (g == 0) {
-      part_ml[(slot * grp + c) * 2] = m;
-      part_ml[(slot * grp + c) * 2 + 1] = l;
+  // row of the first tile: the largest r with Hkv * cum_row[r] <= gt, by a
+  // 64-ary search (cum_row is non-decreasing; invariant: answer in [lo, lo + span))
+  int bi = 0;
+  {
+    int lo = 0, span = b;
+    while (span > 1) {
+      const int step = (span + 63) >> 6;
+      const int r = lo + lane * step;
+      const bool le = r < lo + span && static_cast<long>(Hkv) * cum_row[r] <= gt;
+      const int k = __popcll(__ballot(le));  // >= 1: lane 0 reads cum_row[lo]
+      const int nlo = lo + (k - 1) * step;
+      span = min(step, lo + span - nlo);
+      lo = nlo;
     }
+    bi = lo;
+  }
+
+  while (gt < gt_end) {
+    long rb = static_cast<long>(Hkv) * cum_row[bi];
+    int tb = cum_row[bi + 1] - cum_row[bi];
+    while (gt >= rb + static_cast<long>(Hkv) * tb) {  // rows with no tiles
+      ++bi;
+      rb = static_cast<long>(Hkv) * cum_row[bi];
+      tb = cum_row[bi + 1] - cum_row[bi];
+    }
+    const int off = static_cast<int>(gt - rb);
+    const int kvh = off / tb;
+    const int t_begin = off - kvh * tb;
+    const int t_end = t_begin + static_cast<int>(min(gt_end - gt, static_cast<long>(tb - t_begin)));
+    const int n = decode_row_len(seq_lens, bi, max_pages, ps);
+    const int32_t* prow = page_table + static_cast<long>(bi) * max_pages;
+
+    const bf16* qrow = q + (static_cast<long>(bi) * Hq + kvh * grp + min(c, grp - 1)) * D;
+    v8bf qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = c < grp ? load_v8bf(qrow + 32 * ks + 8 * g) : zero_v8bf();
+    float m = kNegInf, l = 0.0f;
+    v4f acc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    // runs of at most 64 pages: lane j holds the id of the run's page p0 + j
+    for (int r0 = t_begin; r0 < t_end;) {
+      const int p0 = r0 >> tshift;
+      const int r1 = min(t_end, (p0 + 64) << tshift);
+      const int my_page = lane <= ((r1 - 1) >> tshift) - p0 ? prow[p0 + lane] : -1;
+      // Invalid page ids (< 0 or >= num_pages) read page 0, which exists
+      // (num_pages >= 1), and contribute no keys.  Tile t < ceil(n / 64)
+      // holds min(64, n - 64t) >= 1 keys.
+      auto slot_of = [&](int t) {
+        const int page = __builtin_amdgcn_readlane(my_page, (t >> tshift) - p0);
+        const int k0 = (t & tshift) * 64;
+        const bool ok = page >= 0 && page < num_pages;
+        DecodeSlot sl;
+        sl.nk = ok ? min(64, n - 64 * t) : 0;
+        sl.kidx = (static_cast<long>(ok ? page : 0) * Hkv + kvh) * ps + k0;
+        sl.pos0 = 64 * t;
+        sl.k0 = k0;
+        return sl;
+      };
+      auto k_ptr = [&](const DecodeSlot& sl) { return kp + sl.kidx * D; };
+      // V^T page (D, ps) of (page, kv head) starts at key index kidx - k0
+      auto v_ptr = [&](const DecodeSlot& sl) { return vp + (sl.kidx - sl.k0) * D + sl.k0; };
+
+      v8bf kf[4][KS];
+      v8bf vf[2][DT];
+      DecodeSlot cur = slot_of(r0);
+      decode_load_k<D>(kf, k_ptr(cur), c, g);
+      decode_load_v<D>(vf, v_ptr(cur), ps, voff);
+      // Wait for the run's first tile here, so that at the loop head the only
+      // loads in flight are the previous iteration's K then V.  With the last
+      // tile peeled off, the loads inside the loop are unconditional and every
+      // wait in the body stays partial: K.Q^T waits for K only, V^T.P^T for V
+      // of this tile only (the next tile's K still in flight).
+      __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+      auto tile = [&](auto more_c, const DecodeSlot& nxt) __attribute__((always_inline)) {
+        constexpr bool kMore = decltype(more_c)::value;
+        const int g8 = 8 * g;
+        // log-gate bias of the lane's keys 8g..8g+7 and 32+8g..32+8g+7 (a page
+        // holds ps >= 64 keys, so all 64 reads stay inside the page)
+        float4 bv[4];
+        if constexpr (BIAS) {
+          const float* brow = key_bias + cur.kidx + g8;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            bv[j] = *reinterpret_cast<const float4*>(brow + 32 * (j >> 1) + 4 * (j & 1));
+        }
+        // S^T = K.Q^T for the 64 keys of the tile
+        v4f sc[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          sc[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) sc[kt] = mfma_bf16(kf[kt][ks], qf[ks], sc[kt]);
+        }
+        if constexpr (kMore) decode_load_k<D>(kf, k_ptr(nxt), c, g);
+        // scale, bias (not on the newest key), mask keys past the tile / padding
+        // columns.  Entry (kt, i) of lane (c, g) is key 8g + r of the tile with
+        // r = key_of_row(kt, i) (key_of_row(kt, 4g + i) = 8g + key_of_row(kt, i)),
+        // so every bound below is a scalar compared with 8g.
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = key_of_row(kt, i);
+            float val = kNegInf;
+            if (g8 < cur.nk - r && c < grp) {
+              val = sc[kt][i] * scale_log2;
+              if constexpr (BIAS) {
+                const float4 b4 = bv[kt];  // keys 32(kt/2) + 4(kt%2) + 8g + i
+                const float bi4 = i == 0 ? b4.x : i == 1 ? b4.y : i == 2 ? b4.z : b4.w;
+                if (g8 != n - 1 - cur.pos0 - r) val += bi4 * kLog2e;
+              }
+            }
+            sc[kt][i] = val;
+          }
+        softmax_block<4, DT>(sc, acc, m, l);
+        if (cur.nk > 0) {
+          // keys past nk hold stale pool contents (possibly inf/nan): zero their V
+          if (cur.nk < 64) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+              const int kk = 32 * ks + 8 * g;
+              uint32_t mk[4];
+#pragma unroll
+              for (int q2 = 0; q2 < 4; ++q2)
+                mk[q2] = (kk + 2 * q2 < cur.nk ? 0x0000ffffu : 0u) |
+                         (kk + 2 * q2 + 1 < cur.nk ? 0xffff0000u : 0u);
+#pragma unroll
+              for (int tt = 0; tt < DT; ++tt) {
+                uint4 x = __builtin_bit_cast(uint4, vf[ks][tt]);
+                x.x &= mk[0];
+                x.y &= mk[1];
+                x.z &= mk[2];
+                x.w &= mk[3];
+                vf[ks][tt] = __builtin_bit_cast(v8bf, x);
+              }
+            }
+          }
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const v8bf pb = pack_p(sc[2 * ks], sc[2 * ks + 1]);
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt) acc[tt] = mfma_bf16(vf[ks][tt], pb, acc[tt]);
+          }
+        }
+        if constexpr (kMore) decode_load_v<D>(vf, v_ptr(nxt), ps, voff);
+      };
+      for (int t = r0; t + 1 < r1; ++t) {
+        const DecodeSlot nxt = slot_of(t + 1);
+        tile(BoolC<true>{}, nxt);
+        cur = nxt;
+      }
+      tile(BoolC<false>{}, cur);
+      r0 = r1;
+    }
+
+    // partial of this segment: O^T[d][q] unnormalised, with m (log2 domain) and l
+    const long seg = static_cast<long>(bi) * Hkv + kvh + w;
+    if (c < grp) {
+      float* po = part_o + (seg * grp + c) * D;
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+        *reinterpret_cast<float4*>(po + 16 * t + 4 * g) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+      if (g == 0) {
+        part_ml[(seg * grp + c) * 2] = m;
+        part_ml[(seg * grp + c) * 2 + 1] = l;
+      }
+    }
+    gt += t_end - t_begin;
   }
 }
 
-// merge the splits of one (batch row, query head); one wave, the split
-// weights exp2(m_s - M) computed lane-parallel into LDS
+// merge the segments of one (batch row, query head); one wave, the segment
+// weights exp2(m_s - M) computed lane-parallel into LDS.  A row with no keys
+// gets zeros.
+constexpr int kDecodeMaxWaves = 8192;
+
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
-    const int32_t* __restrict__ seq_lens, bf16* __restrict__ o, int Hq, int Hkv, int D, int ps,
-    int max_pages, int pps, int max_splits) {
-  __shared__ float wsh[1024];
+    const int32_t* __restrict__ cum_row, bf16* __restrict__ o, int b, int Hq, int Hkv, int D,
+    int W) {
+  __shared__ float wsh[kDecodeMaxWaves];
   const int qh = blockIdx.x % Hq;
   const int bi = blockIdx.x / Hq;
   const int grp = Hq / Hkv;
   const int kvh = qh / grp, qi = qh % grp;
-  const int n = min(max(seq_lens[bi], 0), max_pages * ps);
-  const int npg = (n + ps - 1) / ps;
-  const int nsplit = min((npg + pps - 1) / pps, 1024);
-  const long slot0 = (static_cast<long>(bi) * Hkv + kvh) * max_splits;
   const int lane = threadIdx.x;
+  bf16* orow = o + (static_cast<long>(bi) * Hq + qh) * D;
+  const int tb = cum_row[bi + 1] - cum_row[bi];
+  if (tb <= 0) {
+    for (int d0 = 2 * lane; d0 < D; d0 += 128) *reinterpret_cast<uint32_t*>(orow + d0) = 0u;
+    return;
+  }
+  const long T = static_cast<long>(Hkv) * cum_row[b];
+  W = static_cast<int>(min(static_cast<long>(W), T));  // as in the decode kernel
+  const long g0 = static_cast<long>(Hkv) * cum_row[bi] + static_cast<long>(kvh) * tb;
+  const int w0 = decode_wave_of(g0, T, W), w1 = decode_wave_of(g0 + tb - 1, T, W);
+  const int nseg = w1 - w0 + 1;  // <= W
+  const long slot0 = static_cast<long>(bi) * Hkv + kvh + w0;
   float M = kNegInf;
-  for (int s = lane; s < nsplit; s += 64) M = fmaxf(M, part_ml[((slot0 + s) * grp + qi) * 2]);
+  for (int s = lane; s < nseg; s += 64) M = fmaxf(M, part_ml[((slot0 + s) * grp + qi) * 2]);
   M = wave_max(M);
   float L = 0.0f;
-  for (int s = lane; s < nsplit; s += 64) {
+  for (int s = lane; s < nseg; s += 64) {
     const float ms = part_ml[((slot0 + s) * grp + qi) * 2];
-    const float w = (ms == kNegInf) ? 0.0f : fast_exp2(ms - M);
-    wsh[s] = w;
-    L += w * part_ml[((slot0 + s) * grp + qi) * 2 + 1];
+    const float wgt = (ms == kNegInf) ? 0.0f : fast_exp2(ms - M);
+    wsh[s] = wgt;
+    L += wgt * part_ml[((slot0 + s) * grp + qi) * 2 + 1];
   }
   L = wave_sum(L);
   __syncthreads();
@@ -355,7 +513,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
   for (int d0 = 2 * lane; d0 < D; d0 += 128) {
     float a0 = 0.f, a1 = 0.f;
     int s = 0;
-    for (; s + 4 <= nsplit; s += 4) {
+    for (; s + 4 <= nseg; s += 4) {
       float2 v[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -366,22 +524,52 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
         a1 += wsh[s + j] * v[j].y;
       }
     }
-    for (; s < nsplit; ++s) {
+    for (; s < nseg; ++s) {
       const float2 v = *reinterpret_cast<const float2*>(part_o + ((slot0 + s) * grp + qi) * D + d0);
       a0 += wsh[s] * v.x;
       a1 += wsh[s] * v.y;
     }
-    *reinterpret_cast<uint32_t*>(o + (static_cast<long>(bi) * Hq + qh) * D + d0) =
-        pack_bf16x2(a0 * inv, a1 * inv);
+    *reinterpret_cast<uint32_t*>(orow + d0) = pack_bf16x2(a0 * inv, a1 * inv);
   }
 }
 
-constexpr int kDecodePPS = 8;  // pages per split
+// workspace: segment partials for b * Hkv + kDecodeMaxWaves segment ids, then
+// cum_row (b + 1 ints)
+struct DecodeWs {
+  float* part_o;
+  float* part_ml;
+  int32_t* cum_row;
+};
+inline size_t decode_ws_layout(int b, int Hq, int Hkv, int D, void* base, DecodeWs* out) {
+  const size_t segs = static_cast<size_t>(b) * Hkv + kDecodeMaxWaves;
+  const size_t grp = static_cast<size_t>(Hq / Hkv);
+  const size_t o_bytes = (segs * grp * D * sizeof(float) + 255) & ~size_t(255);
+  const size_t ml_bytes = (segs * grp * 2 * sizeof(float) + 255) & ~size_t(255);
+  const size_t cum_bytes = ((static_cast<size_t>(b) + 1) * sizeof(int32_t) + 255) & ~size_t(255);
+  if (out) {
+    char* p = static_cast<char*>(base);
+    out->part_o = reinterpret_cast<float*>(p);
+    out->part_ml = reinterpret_cast<float*>(p + o_bytes);
+    out->cum_row = reinterpret_cast<int32_t*>(p + o_bytes + ml_bytes);
+  }
+  return o_bytes + ml_bytes + cum_bytes + 256;
+}
 
-inline size_t decode_ws_bytes(int b, int Hq, int Hkv, int D, int max_pages) {
-  const int max_splits = (max_pages + kDecodePPS - 1) / kDecodePPS;
-  const size_t slots = static_cast<size_t>(b) * Hkv * max_splits * (Hq / Hkv);
-  return slots * (D + 2) * sizeof(float) + 256;
+// waves of one resident round: CUs x resident 64-thread blocks per CU
+template <typename K>
+int decode_waves(K kern, int variant) {
+  static int cache[64][4] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
+  if (cache[dev][variant] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64, 0) != hipSuccess ||
+        cus <= 0 || per_cu <= 0)
+      return 1024;
+    cache[dev][variant] = min(cus * per_cu, kDecodeMaxWaves);
+  }
+  return cache[dev][variant];
 }
 
 }  // namespace sa
@@ -389,7 +577,7 @@ inline size_t decode_ws_bytes(int b, int Hq, int Hkv, int D, int max_pages) {
 extern "C" size_t sa_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                                  int head_dim, int max_pages) {
   if (batch < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads || max_pages < 0) return 0;
-  return sa::decode_ws_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_pages);
+  return sa::decode_ws_layout(batch, num_q_heads, num_kv_heads, head_dim, nullptr, nullptr);
 }
 
 extern "C" int sa_paged_decode_fwd(int dtype, const void* q, const void* k_pages,
@@ -407,41 +595,51 @@ extern "C" int sa_paged_decode_fwd(int dtype, const void* q, const void* k_pages
                head_dim);
   SA_CHECK_ARG(page_size == 64 || page_size == 128,
                "sa_paged_decode_fwd: page_size %d not in {64, 128}", page_size);
+  SA_CHECK_ARG(max_pages >= 0 && static_cast<long>(max_pages) * page_size <= (1L << 30),
+               "sa_paged_decode_fwd: max_pages %d too large", max_pages);
+  SA_CHECK_ARG(static_cast<long>(batch) * num_kv_heads * ((static_cast<long>(max_pages) * page_size + 63) / 64) < (1L << 31),
+               "sa_paged_decode_fwd: more than 2^31 key tiles");
   SA_CHECK_ARG(q && k_pages && v_pages && page_table && seq_lens && o && workspace,
                "sa_paged_decode_fwd: null pointer");
-  const size_t need = sa::decode_ws_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_pages);
+  SA_CHECK_ARG(num_pages >= 1 || batch == 0, "sa_paged_decode_fwd: empty page pool");
+  SA_CHECK_ARG(!key_bias || (reinterpret_cast<uintptr_t>(key_bias) & 15) == 0,
+               "sa_paged_decode_fwd: key_bias must be 16-byte aligned");
+  sa::DecodeWs ws;
+  const size_t need = sa::decode_ws_layout(batch, num_q_heads, num_kv_heads, head_dim, workspace, &ws);
   SA_CHECK_ARG(workspace_bytes >= need, "sa_paged_decode_fwd: workspace %zu B < %zu B",
                workspace_bytes, need);
-  if (batch == 0 || max_pages == 0) return 0;
+  if (batch == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int max_splits = (max_pages + sa::kDecodePPS - 1) / sa::kDecodePPS;
-  const int grp = num_q_heads / num_kv_heads;
-  float* part_o = static_cast<float*>(workspace);
-  float* part_ml = part_o + static_cast<size_t>(batch) * num_kv_heads * max_splits * grp * head_dim;
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf(static_cast<float>(head_dim));
   const float sl2 = scale * sa::kLog2e;
-  const long items = static_cast<long>(batch) * num_kv_heads * max_splits;
+  {
+    sa::ProfScope prof_("paged_decode_plan", s);
+    hipLaunchKernelGGL(sa::paged_decode_plan_kernel, dim3(1), dim3(1024), 0, s, seq_lens, batch,
+                       page_size, max_pages, ws.cum_row);
+    SA_CHECK_LAUNCH("paged_decode_plan");
+  }
+  int W = 0;
   {
     sa::ProfScope prof_("paged_decode", s);
+    auto launch = [&](auto kern, int variant) {
+      W = sa::decode_waves(kern, variant);
+      hipLaunchKernelGGL(kern, dim3(W), dim3(64), 0, s, static_cast<const sa::bf16*>(q),
+                         static_cast<const sa::bf16*>(k_pages),
+                         static_cast<const sa::bf16*>(v_pages), page_table, seq_lens, key_bias,
+                         ws.cum_row, ws.part_o, ws.part_ml, batch, num_q_heads, num_kv_heads,
+                         page_size, max_pages, num_pages, W, sl2);
+    };
     if (head_dim == 128)
-      hipLaunchKernelGGL(sa::paged_decode_kernel<128>, dim3(items), dim3(64), 0, s,
-                         static_cast<const sa::bf16*>(q), static_cast<const sa::bf16*>(k_pages),
-                         static_cast<const sa::bf16*>(v_pages), page_table, seq_lens, key_bias,
-                         part_o, part_ml, num_q_heads, num_kv_heads, page_size, max_pages,
-                         num_pages, sa::kDecodePPS, max_splits, sl2);
+      key_bias ? launch(sa::paged_decode_kernel<128, true>, 0) : launch(sa::paged_decode_kernel<128, false>, 1);
     else
-      hipLaunchKernelGGL(sa::paged_decode_kernel<64>, dim3(items), dim3(64), 0, s,
-                         static_cast<const sa::bf16*>(q), static_cast<const sa::bf16*>(k_pages),
-                         static_cast<const sa::bf16*>(v_pages), page_table, seq_lens, key_bias,
-                         part_o, part_ml, num_q_heads, num_kv_heads, page_size, max_pages,
-                         num_pages, sa::kDecodePPS, max_splits, sl2);
+      key_bias ? launch(sa::paged_decode_kernel<64, true>, 2) : launch(sa::paged_decode_kernel<64, false>, 3);
     SA_CHECK_LAUNCH("paged_decode");
   }
   {
     sa::ProfScope prof_("paged_decode_merge", s);
     hipLaunchKernelGGL(sa::paged_decode_merge_kernel, dim3(batch * num_q_heads), dim3(64), 0, s,
-                       part_o, part_ml, seq_lens, static_cast<sa::bf16*>(o), num_q_heads,
-                       num_kv_heads, head_dim, page_size, max_pages, sa::kDecodePPS, max_splits);
+                       ws.part_o, ws.part_ml, ws.cum_row, static_cast<sa::bf16*>(o), batch,
+                       num_q_heads, num_kv_heads, head_dim, W);
     SA_CHECK_LAUNCH("paged_decode_merge");
   }
   return 0;

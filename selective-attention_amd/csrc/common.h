@@ -161,6 +161,18 @@ __device__ __forceinline__ void wave_mma_split(v4f (&acc)[TM][TN], const MT* A, 
 __device__ __forceinline__ v8bf load_v8bf(const bf16* p) {
   return *reinterpret_cast<const v8bf*>(p);
 }
+// Raw buffer reads (stride 0, gfx9 config dword 0x00020000): the base lives
+// in a wave-uniform resource, the lane offset in one VGPR and the per-load
+// step in an SGPR, so a run of loads from one base needs no per-load VALU
+// address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ v8bf buf_load_v8bf(__amdgpu_buffer_rsrc_t r, unsigned voff_bytes,
+                                              unsigned soff_bytes) {
+  return __builtin_bit_cast(v8bf, __builtin_amdgcn_raw_buffer_load_b128(r, voff_bytes, soff_bytes, 0));
+}
 __device__ __forceinline__ v8bf zero_v8bf() {
   const uint4 z = {0u, 0u, 0u, 0u};
   return __builtin_bit_cast(v8bf, z);

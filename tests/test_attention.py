@@ -239,6 +239,42 @@ def test_paged_decode_parity(b, Hq, Hkv, D, minl, maxl, with_bias):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_paged_decode_page128(with_bias):
+    """128-token pages: two 64-key tiles per page, the second one partial or
+    empty on each row's last page."""
+    print(f"decode page_size=128 bias={with_bias}", flush=True)
+    d = workloads.decode_inputs(batch=6, nheads_q=8, nheads_kv=2, headdim=128, min_len=1,
+                                max_len=700, page_size=128, seed=5)
+    g = torch.Generator().manual_seed(11)
+    bias = torch.randn(d.k_pages.shape[:3], generator=g) if with_bias else None
+    o = _run_decode(d, bias)
+    exp = ref.paged_decode_attn(d.q, d.k_pages, d.v_pages, d.page_table, d.seq_lens,
+                                key_bias=bias)
+    assert_parity(o, exp, torch.bfloat16, "o")
+
+
+@pytest.mark.gpu
+def test_paged_decode_empty_rows_and_single_long_row():
+    """Rows with no cached tokens get zeros; one long row is spread over many
+    waves (more waves than tiles), each contributing a one-tile segment."""
+    print("decode empty rows", flush=True)
+    d = workloads.decode_inputs(batch=9, nheads_q=4, nheads_kv=1, headdim=64, min_len=1,
+                                max_len=300, seed=7)
+    d.seq_lens[[0, 4, 8]] = 0
+    o = _run_decode(d)
+    exp = ref.paged_decode_attn(d.q, d.k_pages, d.v_pages, d.page_table, d.seq_lens)
+    assert_parity(o, exp, torch.bfloat16, "o")
+    assert (o[[0, 4, 8]].float() == 0).all()
+    print("decode single long row", flush=True)
+    d = workloads.decode_inputs(batch=1, nheads_q=16, nheads_kv=2, headdim=128, min_len=5000,
+                                max_len=5000, seed=8)
+    o = _run_decode(d)
+    exp = ref.paged_decode_attn(d.q, d.k_pages, d.v_pages, d.page_table, d.seq_lens)
+    assert_parity(o, exp, torch.bfloat16, "o")
+
+
+@pytest.mark.gpu
 def test_paged_decode_config3_sample():
     """Config 3 (b64, 32q/8kv, D128, len U[1024,32768], 64-token pages) on the
     device; four rows checked against the oracle."""
