@@ -127,7 +127,8 @@ int sa_sparse_attn_fwd(int dtype, const void* q, const void* k, const void* v,
                        int total_tokens, int num_heads, int head_dim, float softmax_scale, void* o,
                        void* stream);
 
-/* Workspace bytes of sa_paged_decode_fwd (split partials). */
+/* Workspace bytes of sa_paged_decode_fwd: segment partials for
+ * batch * num_kv_heads + 8192 segments, plus a per-row tile prefix sum. */
 size_t sa_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                       int max_pages);
 
@@ -140,8 +141,10 @@ size_t sa_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_hea
  *   page_size in {64,128}, D in {64,128}, Hq/Hkv <= 16; page_table:
  *   (batch, max_pages) int32; seq_lens: (batch,) int32; key_bias:
  *   (num_pages, Hkv, page_size) f32 or NULL (not applied to the newest key).
- *   Out-of-range page ids are skipped.  Two launches: split-KV partials, then
- *   a log-sum-exp merge.
+ *   Page ids outside [0, num_pages) contribute no keys; num_pages >= 1;
+ *   key_bias 16-byte aligned.  Three launches: a per-row tile prefix sum,
+ *   the stream-K decode (one resident round of waves, equal tile ranges,
+ *   one partial per (row, kv head) a wave touches), then a log-sum-exp merge.
  */
 int sa_paged_decode_fwd(int dtype, const void* q, const void* k_pages, const void* v_pages,
                         const int32_t* page_table, const int32_t* seq_lens, const float* key_bias,
