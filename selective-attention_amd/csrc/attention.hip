@@ -18,6 +18,8 @@
 // operand is a single 16-byte read: from LDS for prefill (V transposed on
 // staging) and straight from HBM for decode, whose V pages are stored
 // transposed, (num_pages, Hkv, D, page_size).
+#include <type_traits>
+
 #include "common.h"
 #include "prof.h"
 #include "tile.h"
@@ -57,119 +59,343 @@ __device__ __forceinline__ void softmax_block(v4f (&s)[KT], v4f (&o)[DT], float&
   for (int t = 0; t < DT; ++t) o[t] *= alpha;
 }
 
-// O^T[d][q] += sum_key V^T[d][key] P^T[key][q] over 64 keys; Vt points at
-// V^T[0][tile start] with row stride ldv; s: probabilities from softmax_block
-template <int DT>
-__device__ __forceinline__ void pv_block(v4f (&o)[DT], const v4f (&s)[4], const bf16* Vt, int ldv,
-                                         int lane) {
-  const int c = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const v8bf pb = pack_p(s[2 * ks], s[2 * ks + 1]);
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-      o[t] = mfma_bf16(load_v8bf(Vt + (16 * t + c) * ldv + 32 * ks + 8 * g), pb, o[t]);
-  }
-}
-
 // ---------------------------------------------------------------------------
-// block-sparse varlen prefill.  One workgroup per (head, 64-query block);
-// wave w owns query rows 16w..16w+15 of the block.
+// block-sparse varlen prefill.  One workgroup per (head, 64-query block),
+// four waves: wave w owns query rows 32 (w & 1) .. +31 and, of every selected
+// 64-key block, keys 32 (w >> 1) .. +31.  Each K or V^T fragment read from
+// LDS feeds two MFMAs (two 16-query tiles).  The two key halves run
+// independent online softmaxes and are merged through LDS at the end.
+//
+// K and V tiles go from HBM straight into LDS (global_load_lds, 16 bytes per
+// lane) in two stages: the next selected block streams in while the current
+// one is computed, with no staging registers.  The tiles are unpadded
+// ([key][D] bf16) with the 16-byte chunks of row r permuted by kv_swz(r), so
+// the K fragment reads (16 rows, one chunk) and the V^T transpose reads
+// (ds_read_b64_tr_b16: 8 rows, a chunk pair) hit distinct LDS banks.
 // ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(256) void sparse_attn_fwd_kernel(
+struct SparseSmem {
+  static constexpr size_t tile = 64 * D;               // bf16 per K or V tile
+  static constexpr size_t bytes = 2 * 2 * tile * 2;    // [2 stages][K, V]; also holds the merge
+};
+
+// chunk permutation of row r.  D = 128 (16 chunks, a row spans all 64 banks):
+// bijective on (r & 3, (r >> 3) & 3), and (r & 3, (r >> 3) & 1) selects the
+// chunk pair.  D = 64 (8 chunks, two rows per bank period): the same with r & 1
+// taken by the bank half.  Bit 2 of r is never used, so rows r and r + 4 (the
+// two halves of one transpose read) share the permutation.
+template <int D>
+__device__ __forceinline__ int kv_swz(int r) {
+  if constexpr (D == 128) return ((r & 3) << 2) | (((r >> 3) & 1) << 1) | ((r >> 4) & 1);
+  else return (((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 1) | ((r >> 4) & 1);
+}
+
+// s_waitcnt immediate: vmcnt(N), expcnt and lgkmcnt not waited for
+template <int N>
+constexpr int vm_wait() {
+  return (N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14);
+}
+constexpr int kLgkmWait0 = 0xF | (7 << 4) | (3 << 14);   // lgkmcnt(0) only
+
+// Online softmax with a lazy reference: the running max m of a query column
+// is raised (and O, l rescaled) only when a block's max exceeds it by more
+// than 2^8, so probabilities stay <= 256 and most blocks skip the rescale.
+template <int KT, int DT>
+__device__ __forceinline__ void softmax_lazy(v4f (&s)[KT], v4f (&o)[DT], float& m, float& l) {
+  float mx = kNegInf;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][i]);
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const bool raise = mx > m + 8.0f;
+  if (__ballot(raise)) {
+    const float m_new = raise ? mx : m;
+    const float alpha = (m == kNegInf) ? 0.0f : fast_exp2(m - m_new);
+    l *= alpha;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] *= alpha;
+    m = m_new;
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = (s[kt][i] == kNegInf) ? 0.0f : fast_exp2(s[kt][i] - m);
+      s[kt][i] = p;
+      sum += p;
+    }
+  sum += __shfl_xor(sum, 16, 64);
+  sum += __shfl_xor(sum, 32, 64);
+  l += sum;
+}
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const int32_t* __restrict__ cu, int nseq, const int32_t* __restrict__ block_idx, int n_qblk,
     int max_blocks, const float* __restrict__ key_bias, bf16* __restrict__ o, int T, int H,
     float scale_log2) {
   constexpr int BS = 64;
-  constexpr int LDK = D + 8, LDV = BS + 8;
+  using SM = SparseSmem<D>;
   constexpr int DT = D / 16, KS = D / 32;
-  __shared__ __align__(16) bf16 Ks[BS * LDK];
-  __shared__ __align__(16) bf16 Vt[D * LDV];
+  constexpr int IPW = D / 32;   // 1 KB DMA instructions per wave per tile (tile = 128 D bytes)
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  bf16* sm = reinterpret_cast<bf16*>(smem_raw);   // [2 stages][K tile, V tile]
 
   const int lid = xcd_swizzle(blockIdx.x, gridDim.x);
   const int h = lid / n_qblk;
   const int gq = lid - h * n_qblk;
-  // locate the query block's sequence: q blocks are numbered sequence by sequence
-  int s = 0, first = 0, start = 0, n = 0;
-  for (; s < nseq; ++s) {
-    const int a = min(max(cu[s], 0), T), b = min(max(cu[s + 1], a), T);
-    const int nb = (b - a + BS - 1) / BS;
-    if (gq < first + nb) {
-      start = a;
-      n = b - a;
-      break;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // locate the query block's sequence (q blocks are numbered sequence by
+  // sequence): 64 sequences per step, one per lane, a prefix sum of their
+  // block counts and a ballot for the one holding block gq
+  int start = 0, n = 0, jq = -1;
+  for (int s0 = 0, first = 0; s0 < nseq && jq < 0; s0 += 64) {
+    const int si = s0 + lane;
+    int a = 0, nb = 0, len = 0;
+    if (si < nseq) {
+      a = min(max(cu[si], 0), T);
+      len = min(max(cu[si + 1], a), T) - a;
+      nb = (len + BS - 1) / BS;
     }
-    first += nb;
+    int incl = nb;
+#pragma unroll
+    for (int o2 = 1; o2 < 64; o2 <<= 1) {
+      const int t = __shfl_up(incl, o2, 64);
+      if (lane >= o2) incl += t;
+    }
+    const int excl = first + incl - nb;
+    const uint64_t hit = __ballot(si < nseq && gq >= excl && gq < excl + nb);
+    if (hit) {
+      const int L = __builtin_ctzll(hit);
+      start = __builtin_amdgcn_readlane(a, L);
+      n = __builtin_amdgcn_readlane(len, L);
+      jq = gq - __builtin_amdgcn_readlane(excl, L);
+    }
+    first += __builtin_amdgcn_readlane(incl, 63);
   }
-  if (s == nseq) return;  // more query blocks than the packing holds
-  const int jq = gq - first;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (jq < 0) return;  // more query blocks than the packing holds
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qh = w & 1, kh = w >> 1;
   const int c = lane & 15, g = lane >> 4;
-  const int qloc = jq * BS + 16 * wid + c;  // this lane's query (local position)
   const long rs = static_cast<long>(H) * D;
-  const bf16* qrow = q + (start + static_cast<long>(min(qloc, n - 1))) * rs + static_cast<long>(h) * D;
-  v8bf qf[KS];
+  const bf16* kbase = k + static_cast<long>(start) * rs + static_cast<long>(h) * D;
+  const bf16* vbase = v + static_cast<long>(start) * rs + static_cast<long>(h) * D;
+
+  // this lane's two query columns (16-query tiles jt = 0, 1 of the wave's 32 rows)
+  int qloc[2];
+  v8bf qf[2][KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-    qf[ks] = qloc < n ? load_v8bf(qrow + 32 * ks + 8 * g) : zero_v8bf();
+  for (int jt = 0; jt < 2; ++jt) {
+    qloc[jt] = jq * BS + 32 * qh + 16 * jt + c;
+    const bf16* qrow = q + (start + static_cast<long>(min(qloc[jt], n - 1))) * rs + static_cast<long>(h) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[jt][ks] = qloc[jt] < n ? load_v8bf(qrow + 32 * ks + 8 * g) : zero_v8bf();
+  }
   const float* bias = key_bias ? key_bias + static_cast<long>(h) * T + start : nullptr;
+  // the whole query block is inside the sequence: only the diagonal block needs masks
+  const bool qfull = (jq + 1) * BS <= n;
 
-  float m = kNegInf, l = 0.0f;
-  v4f acc[DT];
-#pragma unroll
-  for (int t = 0; t < DT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-
+  // the selected blocks that are inside the sequence and causally visible, in order
   const int32_t* sel = block_idx + (static_cast<long>(h) * n_qblk + gq) * max_blocks;
   const int nkb = (n + BS - 1) / BS;
-  for (int e = 0; e < max_blocks; ++e) {
-    const int kb = sel[e];
-    if (kb < 0 || kb >= nkb || kb > jq) continue;  // unused slot / outside the causal range
+  const bool simple = max_blocks <= 64;
+  int my_kb = -1;
+  uint64_t vmask = 0;
+  if (simple) {
+    my_kb = lane < max_blocks ? sel[lane] : -1;
+    vmask = __ballot(my_kb >= 0 && my_kb < nkb && my_kb <= jq);
+  }
+  auto next_valid = [&](int e) -> int {   // first valid slot >= e, or max_blocks
+    if (simple) {
+      const uint64_t mm = e >= 64 ? 0ull : (vmask >> e);
+      return mm ? e + __builtin_ctzll(mm) : max_blocks;
+    }
+    for (; e < max_blocks; ++e) {
+      const int kb = sel[e];
+      if (kb >= 0 && kb < nkb && kb <= jq) return e;
+    }
+    return max_blocks;
+  };
+  auto block_of = [&](int e) -> int { return simple ? __builtin_amdgcn_readlane(my_kb, e) : sel[e]; };
+
+  // DMA of block kb into a stage: lane l of this wave's instruction i fills
+  // tile bytes 1024 (IPW w + i) + 16 l, i.e. row `row`, stored chunk `ch`,
+  // which holds logical chunk ch ^ kv_swz(row).  Rows past the sequence
+  // repeat its last key (their scores are masked to -inf, so p = 0).
+  auto issue_kv = [&](int kb, int stage) {
+    const int k0 = kb * BS, nk = min(BS, n - k0);
+    bf16* Kt = sm + stage * 2 * SM::tile;
+    bf16* Vt = Kt + SM::tile;
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int pos = ((w * IPW + i) << 10) + (lane << 4);
+      const int row = pos / (2 * D), ch = (pos % (2 * D)) >> 4;
+      const long off = static_cast<long>(k0 + min(row, nk - 1)) * rs + 8 * (ch ^ kv_swz<D>(row));
+      __builtin_amdgcn_global_load_lds(kbase + off, Kt + ((w * IPW + i) << 9), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vbase + off, Vt + ((w * IPW + i) << 9), 16, 0, 0);
+    }
+  };
+
+  float m[2] = {kNegInf, kNegInf}, l[2] = {0.f, 0.f};
+  v4f acc[2][DT];
+#pragma unroll
+  for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[jt][t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // per-lane pieces of the swizzled LDS addresses
+  int krow_off[2], kswz[2];
+#pragma unroll
+  for (int u2 = 0; u2 < 2; ++u2) {
+    const int r = key_of_row(2 * kh + u2, c);
+    krow_off[u2] = r * D;
+    kswz[u2] = kv_swz<D>(r);
+  }
+  const int vr = 32 * kh + 8 * g + ((lane & 15) >> 2);   // V^T read rows vr and vr + 4
+  const int vswz = kv_swz<D>(vr);
+  const int vhalf = 4 * ((lane & 15) & 1);               // element offset inside the chunk
+  const int vchunk = ((lane & 15) & 3) >> 1;              // chunk of the pair
+
+  int e = next_valid(0);
+  int stage = 0;
+  if (e < max_blocks) issue_kv(block_of(e), 0);
+  while (e < max_blocks) {
+    const int kb = block_of(e);
+    const int en = next_valid(e + 1);
     const int k0 = kb * BS;
     const int nk = min(BS, n - k0);
-    __syncthreads();
-    stage_rows<bf16>(Ks, LDK, k + (start + static_cast<long>(k0)) * rs + static_cast<long>(h) * D, rs,
-                     BS, D, nk, D, true, NoScale{});
-    stage_transposed<bf16>(Vt, LDV, v + (start + static_cast<long>(k0)) * rs + static_cast<long>(h) * D,
-                           rs, BS, D, nk, D, true, NoScale{});
-    __syncthreads();
-    v4f sc[4];
+    // bias of the wave's keys 32 kh + 8g + 0..7 (issued before the next DMA, so
+    // the wait below covers it)
+    float bk[8];
+    if (bias) {
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      sc[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        sc[kt] = mfma_bf16(load_v8bf(Ks + key_of_row(kt, c) * LDK + 32 * ks + 8 * g), qf[ks],
-                           sc[kt]);
+      for (int i = 0; i < 8; ++i) bk[i] = bias[min(k0 + 32 * kh + 8 * g + i, n - 1)];
     }
+    if (en < max_blocks) {
+      issue_kv(block_of(en), stage ^ 1);
+      __builtin_amdgcn_s_waitcnt(vm_wait<2 * IPW>());   // this block's tiles have landed
+    } else {
+      __builtin_amdgcn_s_waitcnt(vm_wait<0>());
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const bf16* Ks = sm + stage * 2 * SM::tile;
+    const bf16* Vs = Ks + SM::tile;
+
+    // S^T = K . Q^T for the wave's 32 keys (score tiles kt = 2 kh, 2 kh + 1)
+    v4f sc[2][2];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kl = key_of_row(kt, 4 * g + i);
-        const int key = k0 + kl;
-        float val = kNegInf;
-        if (kl < nk && key <= qloc && qloc < n) {
-          val = sc[kt][i] * scale_log2;
-          if (bias && key != qloc) val += bias[key] * kLog2e;
-        }
-        sc[kt][i] = val;
+      for (int u2 = 0; u2 < 2; ++u2) sc[jt][u2] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u2 = 0; u2 < 2; ++u2) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const v8bf kf = load_v8bf(Ks + krow_off[u2] + 8 * ((4 * ks + g) ^ kswz[u2]));
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt) sc[jt][u2] = mfma_bf16(kf, qf[jt][ks], sc[jt][u2]);
       }
-    softmax_block<4, DT>(sc, acc, m, l);
-    pv_block<DT>(acc, sc, Vt, LDV, lane);
-  }
-  if (qloc < n) {
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    bf16* orow = o + (start + static_cast<long>(qloc)) * rs + static_cast<long>(h) * D;
+    }
+    // scale; bias (not on the diagonal) and causal / length masks where needed
+    const bool interior = kb < jq && qfull;
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      uint2 w;
-      w.x = pack_bf16x2(acc[t][0] * inv, acc[t][1] * inv);
-      w.y = pack_bf16x2(acc[t][2] * inv, acc[t][3] * inv);
-      *reinterpret_cast<uint2*>(orow + 16 * t + 4 * g) = w;
+    for (int jt = 0; jt < 2; ++jt) {
+#pragma unroll
+      for (int u2 = 0; u2 < 2; ++u2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kl = key_of_row(2 * kh + u2, 4 * g + i);   // = 32 kh + 8g + 4 u2 + i
+          float val = sc[jt][u2][i] * scale_log2;
+          if (!interior) {
+            const int key = k0 + kl;
+            if (!(kl < nk && key <= qloc[jt] && qloc[jt] < n)) val = kNegInf;
+            else if (bias && key != qloc[jt]) val += bk[4 * u2 + i] * kLog2e;
+          } else if (bias) {
+            val += bk[4 * u2 + i] * kLog2e;
+          }
+          sc[jt][u2][i] = val;
+        }
+      softmax_lazy<2, DT>(sc[jt], acc[jt], m[jt], l[jt]);
+    }
+    // O^T += V^T . P^T over the wave's 32 keys
+    {
+      const v8bf pb0 = pack_p(sc[0][0], sc[0][1]);
+      const v8bf pb1 = pack_p(sc[1][0], sc[1][1]);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+        const bf16* p = Vs + vr * D + 8 * ((2 * t + vchunk) ^ vswz) + vhalf;
+        const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p));
+        const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + 4 * D));
+        const v8bf vf = __builtin_bit_cast(v8bf, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+        acc[0][t] = mfma_bf16(vf, pb0, acc[0][t]);
+        acc[1][t] = mfma_bf16(vf, pb1, acc[1][t]);
+      }
+    }
+    // every wave is done with this stage before it is refilled
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kLgkmWait0);
+    __builtin_amdgcn_s_barrier();
+    stage ^= 1;
+    e = en;
+  }
+
+  // merge the two key halves: waves kh = 1 hand (m, l, O^T) to waves kh = 0
+  float* xch = reinterpret_cast<float*>(smem_raw);   // [qh][2 jt][DT][64 lanes] float4 + m, l
+  float4* xo = reinterpret_cast<float4*>(xch) + qh * 2 * DT * 64;
+  float* xm = xch + 4 * (2 * 2 * DT * 64) + qh * 2 * 2 * 64;
+  if (kh == 1) {
+#pragma unroll
+    for (int jt = 0; jt < 2; ++jt) {
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+        xo[(jt * DT + t) * 64 + lane] = make_float4(acc[jt][t][0], acc[jt][t][1], acc[jt][t][2], acc[jt][t][3]);
+      xm[(jt * 2) * 64 + lane] = m[jt];
+      xm[(jt * 2 + 1) * 64 + lane] = l[jt];
     }
   }
+  __syncthreads();
+  if (kh == 1) return;
+#pragma unroll
+  for (int jt = 0; jt < 2; ++jt) {
+    const float m1 = xm[(jt * 2) * 64 + lane], l1 = xm[(jt * 2 + 1) * 64 + lane];
+    const float mm = fmaxf(m[jt], m1);
+    const float a0 = m[jt] == kNegInf ? 0.f : fast_exp2(m[jt] - mm);
+    const float a1 = m1 == kNegInf ? 0.f : fast_exp2(m1 - mm);
+    const float lt = l[jt] * a0 + l1 * a1;
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (qloc[jt] < n) {
+      bf16* orow = o + (start + static_cast<long>(qloc[jt])) * rs + static_cast<long>(h) * D;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const float4 o1 = xo[(jt * DT + t) * 64 + lane];
+        const float r0 = (acc[jt][t][0] * a0 + o1.x * a1) * inv, r1 = (acc[jt][t][1] * a0 + o1.y * a1) * inv;
+        const float r2 = (acc[jt][t][2] * a0 + o1.z * a1) * inv, r3 = (acc[jt][t][3] * a0 + o1.w * a1) * inv;
+        *reinterpret_cast<uint2*>(orow + 16 * t + 4 * g) = uint2{pack_bf16x2(r0, r1), pack_bf16x2(r2, r3)};
+      }
+    }
+  }
+}
+
+// raise the kernel's dynamic LDS limit once per process (D = 128 needs 64 KB)
+template <int D>
+int sparse_smem_attr() {
+  static bool done = false;
+  if (!done) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_attn_fwd_kernel<D>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(SparseSmem<D>::bytes));
+    SA_CHECK_ARG(e == hipSuccess, "sa_sparse_attn_fwd: %zu B of LDS refused: %s",
+                 SparseSmem<D>::bytes, hipGetErrorString(e));
+    done = true;
+  }
+  return 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -664,19 +890,20 @@ extern "C" int sa_sparse_attn_fwd(int dtype, const void* q, const void* k, const
   hipStream_t s = static_cast<hipStream_t>(stream);
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf(static_cast<float>(head_dim));
   const long blocks = static_cast<long>(num_heads) * n_qblk;
-  sa::ProfScope prof_("sparse_attn_fwd", s);
-  if (head_dim == 128)
-    hipLaunchKernelGGL(sa::sparse_attn_fwd_kernel<128>, dim3(blocks), dim3(256), 0, s,
-                       static_cast<const sa::bf16*>(q), static_cast<const sa::bf16*>(k),
-                       static_cast<const sa::bf16*>(v), cu_seqlens, num_seqs, block_idx, n_qblk,
-                       max_blocks, key_bias, static_cast<sa::bf16*>(o), total_tokens, num_heads,
-                       scale * sa::kLog2e);
-  else
-    hipLaunchKernelGGL(sa::sparse_attn_fwd_kernel<64>, dim3(blocks), dim3(256), 0, s,
-                       static_cast<const sa::bf16*>(q), static_cast<const sa::bf16*>(k),
-                       static_cast<const sa::bf16*>(v), cu_seqlens, num_seqs, block_idx, n_qblk,
-                       max_blocks, key_bias, static_cast<sa::bf16*>(o), total_tokens, num_heads,
-                       scale * sa::kLog2e);
+  auto launch = [&](auto dc) -> int {
+    constexpr int D = decltype(dc)::value;
+    if (sa::sparse_smem_attr<D>()) return 1;
+    sa::ProfScope prof_("sparse_attn_fwd", s);
+    hipLaunchKernelGGL(sa::sparse_attn_fwd_kernel<D>, dim3(blocks), dim3(256),
+                       sa::SparseSmem<D>::bytes, s, static_cast<const sa::bf16*>(q),
+                       static_cast<const sa::bf16*>(k), static_cast<const sa::bf16*>(v), cu_seqlens,
+                       num_seqs, block_idx, n_qblk, max_blocks, key_bias, static_cast<sa::bf16*>(o),
+                       total_tokens, num_heads, scale * sa::kLog2e);
+    return 0;
+  };
+  const int rc = head_dim == 128 ? launch(std::integral_constant<int, 128>{})
+                                 : launch(std::integral_constant<int, 64>{});
+  if (rc) return rc;
   SA_CHECK_LAUNCH("sparse_attn_fwd");
   return 0;
 }

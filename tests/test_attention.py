@@ -189,6 +189,19 @@ def test_sparse_attn_full_selection_matches_causal():
 
 
 @pytest.mark.gpu
+def test_sparse_attn_more_than_64_slots():
+    """A selection row longer than one wave (71 slots): the valid blocks are
+    found by the scalar scan instead of the wave ballot."""
+    lens, H, D = [4500], 1, 64
+    q, k, v, cu = packed(lens, H, D, seed=4)
+    idx = full_causal_selection(lens, H)
+    assert idx.shape[2] > 64
+    o = _run_sparse(q, k, v, cu, idx)
+    exp = ref.sparse_attn_varlen(q, k, v, cu, idx)
+    assert_parity(o, exp, torch.bfloat16, "o")
+
+
+@pytest.mark.gpu
 def test_sparse_attn_missing_diagonal_gives_zero_rows():
     lens, H, D = [128], 1, 64
     q, k, v, cu = packed(lens, H, D)
