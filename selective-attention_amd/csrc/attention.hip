@@ -18,8 +18,6 @@
 // operand is a single 16-byte read: from LDS for prefill (V transposed on
 // staging) and straight from HBM for decode, whose V pages are stored
 // transposed, (num_pages, Hkv, D, page_size).
-#include <type_traits>
-
 #include "common.h"
 #include "prof.h"
 #include "tile.h"
@@ -97,9 +95,13 @@ constexpr int vm_wait() {
 }
 constexpr int kLgkmWait0 = 0xF | (7 << 4) | (3 << 14);   // lgkmcnt(0) only
 
-// Online softmax with a lazy reference: the running max m of a query column
-// is raised (and O, l rescaled) only when a block's max exceeds it by more
-// than 2^8, so probabilities stay <= 256 and most blocks skip the rescale.
+// Online softmax with a lazy reference.  s[kt][i] holds log2-domain scores of
+// this lane's keys for query column lane & 15 (-inf where masked).  The
+// running reference m of a column (log2 domain, shared by its
+// four lane groups) is raised, and O and the partial sums rescaled, only when
+// some score exceeds it by more than 2^8: the common block needs no cross-lane
+// reduction at all, and probabilities stay <= 256.  l is this lane's partial
+// row sum (its own keys); the four lane groups' parts are added at the end.
 template <int KT, int DT>
 __device__ __forceinline__ void softmax_lazy(v4f (&s)[KT], v4f (&o)[DT], float& m, float& l) {
   float mx = kNegInf;
@@ -107,32 +109,33 @@ __device__ __forceinline__ void softmax_lazy(v4f (&s)[KT], v4f (&o)[DT], float& 
   for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][i]);
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  const bool raise = mx > m + 8.0f;
-  if (__ballot(raise)) {
-    const float m_new = raise ? mx : m;
-    const float alpha = (m == kNegInf) ? 0.0f : fast_exp2(m - m_new);
-    l *= alpha;
+  if (__ballot(mx > m + 8.0f)) {
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (mx > m + 8.0f) {   // the column's new reference
+      const float alpha = (m == kNegInf) ? 0.0f : fast_exp2(m - mx);
+      l *= alpha;
 #pragma unroll
-    for (int t = 0; t < DT; ++t) o[t] *= alpha;
-    m = m_new;
+      for (int t = 0; t < DT; ++t) o[t] *= alpha;
+      m = mx;
+    }
   }
+  // masked scores are -inf; a column without any admissible key yet keeps
+  // m = -inf and only -inf scores, so a zero reference gives p = 0 there
+  const float mref = m == kNegInf ? 0.0f : m;
   float sum = 0.0f;
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float p = (s[kt][i] == kNegInf) ? 0.0f : fast_exp2(s[kt][i] - m);
+      const float p = fast_exp2(s[kt][i] - mref);
       s[kt][i] = p;
       sum += p;
     }
-  sum += __shfl_xor(sum, 16, 64);
-  sum += __shfl_xor(sum, 32, 64);
   l += sum;
 }
 
-template <int D>
+template <int D, bool BIAS>
 __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const int32_t* __restrict__ cu, int nseq, const int32_t* __restrict__ block_idx, int n_qblk,
@@ -196,7 +199,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     for (int ks = 0; ks < KS; ++ks)
       qf[jt][ks] = qloc[jt] < n ? load_v8bf(qrow + 32 * ks + 8 * g) : zero_v8bf();
   }
-  const float* bias = key_bias ? key_bias + static_cast<long>(h) * T + start : nullptr;
+  const float* bias = BIAS ? key_bias + static_cast<long>(h) * T + start : nullptr;
   // the whole query block is inside the sequence: only the diagonal block needs masks
   const bool qfull = (jq + 1) * BS <= n;
 
@@ -231,13 +234,16 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     const int k0 = kb * BS, nk = min(BS, n - k0);
     bf16* Kt = sm + stage * 2 * SM::tile;
     bf16* Vt = Kt + SM::tile;
+    const bf16* kb0 = kbase + static_cast<long>(k0) * rs;
+    const bf16* vb0 = vbase + static_cast<long>(k0) * rs;
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
       const int pos = ((w * IPW + i) << 10) + (lane << 4);
-      const int row = pos / (2 * D), ch = (pos % (2 * D)) >> 4;
-      const long off = static_cast<long>(k0 + min(row, nk - 1)) * rs + 8 * (ch ^ kv_swz<D>(row));
-      __builtin_amdgcn_global_load_lds(kbase + off, Kt + ((w * IPW + i) << 9), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vbase + off, Vt + ((w * IPW + i) << 9), 16, 0, 0);
+      const int row = pos / (2 * D);
+      const int rr = nk == BS ? row : min(row, nk - 1);
+      const long off = static_cast<long>(rr) * rs + 8 * (((pos % (2 * D)) >> 4) ^ kv_swz<D>(row));
+      __builtin_amdgcn_global_load_lds(kb0 + off, Kt + ((w * IPW + i) << 9), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vb0 + off, Vt + ((w * IPW + i) << 9), 16, 0, 0);
     }
   };
 
@@ -272,7 +278,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     // bias of the wave's keys 32 kh + 8g + 0..7 (issued before the next DMA, so
     // the wait below covers it)
     float bk[8];
-    if (bias) {
+    if constexpr (BIAS) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) bk[i] = bias[min(k0 + 32 * kh + 8 * g + i, n - 1)];
     }
@@ -311,14 +317,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int kl = key_of_row(2 * kh + u2, 4 * g + i);   // = 32 kh + 8g + 4 u2 + i
+          const int key = k0 + kl;
           float val = sc[jt][u2][i] * scale_log2;
-          if (!interior) {
-            const int key = k0 + kl;
-            if (!(kl < nk && key <= qloc[jt] && qloc[jt] < n)) val = kNegInf;
-            else if (bias && key != qloc[jt]) val += bk[4 * u2 + i] * kLog2e;
-          } else if (bias) {
-            val += bk[4 * u2 + i] * kLog2e;
-          }
+          if constexpr (BIAS) val += (interior || key != qloc[jt]) ? bk[4 * u2 + i] * kLog2e : 0.f;
+          if (!interior) val = (kl < nk && key <= qloc[jt] && qloc[jt] < n) ? val : kNegInf;
           sc[jt][u2][i] = val;
         }
       softmax_lazy<2, DT>(sc[jt], acc[jt], m[jt], l[jt]);
@@ -346,6 +348,12 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     e = en;
   }
 
+  // the row sums so far are per lane (its own keys): add the four lane groups
+#pragma unroll
+  for (int jt = 0; jt < 2; ++jt) {
+    l[jt] += __shfl_xor(l[jt], 16, 64);
+    l[jt] += __shfl_xor(l[jt], 32, 64);
+  }
   // merge the two key halves: waves kh = 1 hand (m, l, O^T) to waves kh = 0
   float* xch = reinterpret_cast<float*>(smem_raw);   // [qh][2 jt][DT][64 lanes] float4 + m, l
   float4* xo = reinterpret_cast<float4*>(xch) + qh * 2 * DT * 64;
@@ -384,17 +392,30 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
 }
 
 // raise the kernel's dynamic LDS limit once per process (D = 128 needs 64 KB)
-template <int D>
+template <int D, bool BIAS>
 int sparse_smem_attr() {
   static bool done = false;
   if (!done) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_attn_fwd_kernel<D>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_attn_fwd_kernel<D, BIAS>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(SparseSmem<D>::bytes));
     SA_CHECK_ARG(e == hipSuccess, "sa_sparse_attn_fwd: %zu B of LDS refused: %s",
                  SparseSmem<D>::bytes, hipGetErrorString(e));
     done = true;
   }
+  return 0;
+}
+
+template <int D, bool BIAS>
+int launch_sparse(const void* q, const void* k, const void* v, const int32_t* cu, int nseq,
+                  const int32_t* block_idx, int n_qblk, int max_blocks, const float* key_bias,
+                  void* o, int T, int H, float scale_log2, long blocks, hipStream_t s) {
+  if (sparse_smem_attr<D, BIAS>()) return 1;
+  ProfScope prof_("sparse_attn_fwd", s);
+  hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, BIAS>), dim3(blocks), dim3(256), SparseSmem<D>::bytes,
+                     s, static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                     static_cast<const bf16*>(v), cu, nseq, block_idx, n_qblk, max_blocks, key_bias,
+                     static_cast<bf16*>(o), T, H, scale_log2);
   return 0;
 }
 
@@ -890,19 +911,13 @@ extern "C" int sa_sparse_attn_fwd(int dtype, const void* q, const void* k, const
   hipStream_t s = static_cast<hipStream_t>(stream);
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf(static_cast<float>(head_dim));
   const long blocks = static_cast<long>(num_heads) * n_qblk;
-  auto launch = [&](auto dc) -> int {
-    constexpr int D = decltype(dc)::value;
-    if (sa::sparse_smem_attr<D>()) return 1;
-    sa::ProfScope prof_("sparse_attn_fwd", s);
-    hipLaunchKernelGGL(sa::sparse_attn_fwd_kernel<D>, dim3(blocks), dim3(256),
-                       sa::SparseSmem<D>::bytes, s, static_cast<const sa::bf16*>(q),
-                       static_cast<const sa::bf16*>(k), static_cast<const sa::bf16*>(v), cu_seqlens,
-                       num_seqs, block_idx, n_qblk, max_blocks, key_bias, static_cast<sa::bf16*>(o),
-                       total_tokens, num_heads, scale * sa::kLog2e);
-    return 0;
-  };
-  const int rc = head_dim == 128 ? launch(std::integral_constant<int, 128>{})
-                                 : launch(std::integral_constant<int, 64>{});
+  const float sl2 = scale * sa::kLog2e;
+  const int rc =
+      head_dim == 128
+          ? (key_bias ? sa::launch_sparse<128, true>(q, k, v, cu_seqlens, num_seqs, block_idx, n_qblk, max_blocks, key_bias, o, total_tokens, num_heads, sl2, blocks, s)
+                      : sa::launch_sparse<128, false>(q, k, v, cu_seqlens, num_seqs, block_idx, n_qblk, max_blocks, key_bias, o, total_tokens, num_heads, sl2, blocks, s))
+          : (key_bias ? sa::launch_sparse<64, true>(q, k, v, cu_seqlens, num_seqs, block_idx, n_qblk, max_blocks, key_bias, o, total_tokens, num_heads, sl2, blocks, s)
+                      : sa::launch_sparse<64, false>(q, k, v, cu_seqlens, num_seqs, block_idx, n_qblk, max_blocks, key_bias, o, total_tokens, num_heads, sl2, blocks, s));
   if (rc) return rc;
   SA_CHECK_LAUNCH("sparse_attn_fwd");
   return 0;
