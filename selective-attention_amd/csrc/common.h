@@ -161,6 +161,21 @@ __device__ __forceinline__ void wave_mma_split(v4f (&acc)[TM][TN], const MT* A, 
 __device__ __forceinline__ v8bf load_v8bf(const bf16* p) {
   return *reinterpret_cast<const v8bf*>(p);
 }
+// Non-temporal (streaming) accesses for data touched once per step: such
+// lines are kept out of the caches and leave no write-back traffic behind.
+typedef float v4f_nt __attribute__((ext_vector_type(4)));
+typedef unsigned v2u_nt __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float4 ld_nt(const float4* p) {
+  const v4f_nt v = __builtin_nontemporal_load(reinterpret_cast<const v4f_nt*>(p));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void st_nt(float4* p, const float4& v) {
+  __builtin_nontemporal_store(v4f_nt{v.x, v.y, v.z, v.w}, reinterpret_cast<v4f_nt*>(p));
+}
+__device__ __forceinline__ void st_nt(uint2* p, const uint2& v) {
+  __builtin_nontemporal_store(v2u_nt{v.x, v.y}, reinterpret_cast<v2u_nt*>(p));
+}
+
 // Raw buffer reads (stride 0, gfx9 config dword 0x00020000): the base lives
 // in a wave-uniform resource, the lane offset in one VGPR and the per-load
 // step in an SGPR, so a run of loads from one base needs no per-load VALU

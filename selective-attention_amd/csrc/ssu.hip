@@ -17,8 +17,6 @@
 
 namespace sa {
 
-typedef float v4f_nt __attribute__((ext_vector_type(4)));
-
 template <typename T, int ROW_LANES, int ROWS>
 __global__ __launch_bounds__(256) void ssu_fwd_kernel(
     const T* __restrict__ u, const float* __restrict__ A, const T* __restrict__ Bm,
@@ -57,15 +55,14 @@ __global__ __launch_bounds__(256) void ssu_fwd_kernel(
     if (vec4) {
       for (int n = 4 * lane_in_row; n < N; n += 4 * ROW_LANES) {
         if (!valid) break;
-        const v4f_nt hl = __builtin_nontemporal_load(reinterpret_cast<const v4f_nt*>(hrow + n));
-        float4 hv = make_float4(hl[0], hl[1], hl[2], hl[3]);
+        float4 hv = ld_nt(reinterpret_cast<const float4*>(hrow + n));
         float b0 = load_f32(Brow + n), b1 = load_f32(Brow + n + 1), b2 = load_f32(Brow + n + 2), b3 = load_f32(Brow + n + 3);
         float c0 = load_f32(Crow + n), c1 = load_f32(Crow + n + 1), c2 = load_f32(Crow + n + 2), c3 = load_f32(Crow + n + 3);
         hv.x = hv.x * decay + du * b0;
         hv.y = hv.y * decay + du * b1;
         hv.z = hv.z * decay + du * b2;
         hv.w = hv.w * decay + du * b3;
-        __builtin_nontemporal_store(v4f_nt{hv.x, hv.y, hv.z, hv.w}, reinterpret_cast<v4f_nt*>(hrow + n));
+        st_nt(reinterpret_cast<float4*>(hrow + n), hv);
         part += hv.x * c0 + hv.y * c1 + hv.z * c2 + hv.w * c3;
       }
     } else {
