@@ -67,8 +67,8 @@ __device__ __forceinline__ void softmax_block(v4f (&s)[KT], v4f (&o)[DT], float&
 // K and V tiles go from HBM straight into LDS (global_load_lds, 16 bytes per
 // lane) in two stages: the next selected block streams in while the current
 // one is computed, with no staging registers.  The tiles are unpadded
-// ([key][D] bf16) with the 16-byte chunks of row r permuted by kv_swz(r), so
-// the K fragment reads (16 rows, one chunk) and the V^T transpose reads
+// ([key][D] bf16) with the 16-byte chunks of row r permuted (k_swz, v_swz),
+// so the K fragment reads (16 rows, one chunk) and the V^T transpose reads
 // (ds_read_b64_tr_b16: 8 rows, a chunk pair) hit distinct LDS banks.
 // ---------------------------------------------------------------------------
 template <int D>
@@ -77,13 +77,21 @@ struct SparseSmem {
   static constexpr size_t bytes = 2 * 2 * tile * 2;    // [2 stages][K, V]; also holds the merge
 };
 
-// chunk permutation of row r.  D = 128 (16 chunks, a row spans all 64 banks):
-// bijective on (r & 3, (r >> 3) & 3), and (r & 3, (r >> 3) & 1) selects the
-// chunk pair.  D = 64 (8 chunks, two rows per bank period): the same with r & 1
-// taken by the bank half.  Bit 2 of r is never used, so rows r and r + 4 (the
-// two halves of one transpose read) share the permutation.
+// chunk permutations of row r (16-byte chunks; D = 128: 16 per row, D = 64:
+// 8).  The K tile is read as MFMA A fragments (16 rows key_of_row(kt, 0..15),
+// one chunk per 16-lane group), the V tile by ds_read_b64_tr_b16 (rows
+// 8g + 0..3 and + 4, one chunk pair per group), so each gets its own
+// permutation; both were chosen with the LDS bank-conflict counter
+// (SQ_LDS_BANK_CONFLICT = 0 for these read sets on gfx950).  The V
+// permutation never uses bit 2 of r, so rows r and r + 4 (the two halves of
+// one transpose read) share it.
 template <int D>
-__device__ __forceinline__ int kv_swz(int r) {
+__device__ __forceinline__ int k_swz(int r) {
+  if constexpr (D == 128) return (r & 3) | (((r >> 3) & 3) << 2);
+  else return (((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 1) | ((r >> 4) & 1);
+}
+template <int D>
+__device__ __forceinline__ int v_swz(int r) {
   if constexpr (D == 128) return ((r & 3) << 2) | (((r >> 3) & 1) << 1) | ((r >> 4) & 1);
   else return (((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 1) | ((r >> 4) & 1);
 }
@@ -228,7 +236,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
 
   // DMA of block kb into a stage: lane l of this wave's instruction i fills
   // tile bytes 1024 (IPW w + i) + 16 l, i.e. row `row`, stored chunk `ch`,
-  // which holds logical chunk ch ^ kv_swz(row).  Rows past the sequence
+  // which holds logical chunk ch ^ k_swz(row) (K) or ch ^ v_swz(row) (V).  Rows past the sequence
   // repeat its last key (their scores are masked to -inf, so p = 0).
   auto issue_kv = [&](int kb, int stage) {
     const int k0 = kb * BS, nk = min(BS, n - k0);
@@ -241,9 +249,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
       const int pos = ((w * IPW + i) << 10) + (lane << 4);
       const int row = pos / (2 * D);
       const int rr = nk == BS ? row : min(row, nk - 1);
-      const long off = static_cast<long>(rr) * rs + 8 * (((pos % (2 * D)) >> 4) ^ kv_swz<D>(row));
-      __builtin_amdgcn_global_load_lds(kb0 + off, Kt + ((w * IPW + i) << 9), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vb0 + off, Vt + ((w * IPW + i) << 9), 16, 0, 0);
+      const int ch = (pos % (2 * D)) >> 4;
+      const long koff = static_cast<long>(rr) * rs + 8 * (ch ^ k_swz<D>(row));
+      const long voff = static_cast<long>(rr) * rs + 8 * (ch ^ v_swz<D>(row));
+      __builtin_amdgcn_global_load_lds(kb0 + koff, Kt + ((w * IPW + i) << 9), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vb0 + voff, Vt + ((w * IPW + i) << 9), 16, 0, 0);
     }
   };
 
@@ -260,10 +270,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
   for (int u2 = 0; u2 < 2; ++u2) {
     const int r = key_of_row(2 * kh + u2, c);
     krow_off[u2] = r * D;
-    kswz[u2] = kv_swz<D>(r);
+    kswz[u2] = k_swz<D>(r);
   }
   const int vr = 32 * kh + 8 * g + ((lane & 15) >> 2);   // V^T read rows vr and vr + 4
-  const int vswz = kv_swz<D>(vr);
+  const int vswz = v_swz<D>(vr);
   const int vhalf = 4 * ((lane & 15) & 1);               // element offset inside the chunk
   const int vchunk = ((lane & 15) & 3) >> 1;              // chunk of the pair
 
