@@ -467,15 +467,20 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
         qacc += qs;
         rW[((j & 1) * 2 + hs) * 256 + strip * 64 + key_of_row(li >> 2, 4 * lg + (li & 3))] =
             transpose_reduce16(m, li);
-        // du^T[p, sig] += sum_t dy[t, p] L[t, sig]  (L as one bf16 plane, dy as hi + lo)
+        // du^T[p, sig] += sum_t dy[t, p] L[t, sig]  (L and dy as hi + lo: with weak
+        // decay and small dt, ddt = sum_p u du cancels to ~1e-2 of its terms, and
+        // a single-plane L leaves ~0.2 % of the tensor scale of error there)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const v8bf lh = pack_p(W[2 * ks], W[2 * ks + 1]);
+          v8bf lh, ll;
+          split_p(W[2 * ks], W[2 * ks + 1], lh, ll);
 #pragma unroll
           for (int pt = 0; pt < 4; ++pt) {
             const int off = (32 * ks + 8 * lg) * kLY + 16 * pt;
-            duT[pt] = mfma_bf16(lds_tr8(Yh + off, kLY, lane), lh, duT[pt]);
+            const v8bf yh = lds_tr8(Yh + off, kLY, lane);
+            duT[pt] = mfma_bf16(yh, lh, duT[pt]);
             duT[pt] = mfma_bf16(lds_tr8(Yl + off, kLY, lane), lh, duT[pt]);
+            duT[pt] = mfma_bf16(yh, ll, duT[pt]);
           }
         }
       }

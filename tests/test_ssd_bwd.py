@@ -91,6 +91,17 @@ def test_ssd_bwd_fused_parity(name, shape, chunk):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("softplus,limit", [(False, (-0.02, 0.05)), (True, (-1.0, float("inf")))])
+def test_ssd_bwd_fused_signed_limits(softplus, limit):
+    """Fused bf16 backward on its exact-decay branch (negative lower dt limit;
+    with softplus off some dt are negative)."""
+    from tests.test_ssd_fwd import signed_dt_inputs
+    print(f"ssd bwd fused signed softplus={softplus} limit={limit}", flush=True)
+    x = signed_dt_inputs(softplus, b=2, L=256, H=4, P=64, N=128, G=2, lens=[256, 170])
+    check(x, 128, torch.bfloat16, softplus, limit)
+
+
+@pytest.mark.gpu
 def test_ssd_bwd_fused_deterministic():
     x = make_inputs(b=2, L=256, H=8, P=64, N=128, G=2, dtype=torch.bfloat16, lens=[256, 190])
     g = torch.Generator().manual_seed(3)

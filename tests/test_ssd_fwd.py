@@ -186,3 +186,32 @@ def test_ssd_fwd_bf16_fast_path(name, shape, chunk):
     y, h = run_fwd(x, chunk)
     assert_parity(y, y_ref, torch.bfloat16, "y")
     assert_parity(h, h_ref, torch.bfloat16, "h_last")
+
+
+def signed_dt_inputs(softplus, dtype=torch.bfloat16, **shape):
+    """Inputs for the exact-decay branch: with softplus off, dt = clamp(delta_raw)
+    takes both signs (|A| kept small so exp(dc) stays moderate)."""
+    x = make_inputs(dtype=dtype, with_bias=False, **shape)
+    g = torch.Generator().manual_seed(17)
+    x["A"] = -(torch.rand(x["A"].shape, generator=g) * 0.5 + 0.1)
+    if not softplus:
+        x["delta_raw"] = (torch.randn(x["delta_raw"].shape, generator=g) * 0.03 + 0.01).to(dtype)
+    return x
+
+
+SIGNED_LIMITS = [(False, (-0.02, 0.05)), (True, (-1.0, float("inf")))]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("softplus,limit", SIGNED_LIMITS)
+def test_ssd_fwd_bf16_fast_path_signed_limits(softplus, limit):
+    """A negative lower dt limit switches the bf16 chunk scan from the
+    factorised off-diagonal decay to the exact per-element form (dc need not
+    be monotone); with softplus off some dt are negative."""
+    print(f"ssd fwd fast signed softplus={softplus} limit={limit}", flush=True)
+    x = signed_dt_inputs(softplus, b=2, L=256, H=4, P=64, N=128, G=2, lens=[256, 170])
+    y_ref, h_ref = ref.ssd_scan_forward(**x, chunk_size=64, use_delta_softplus=softplus,
+                                        delta_limit=limit)
+    y, h = run_fwd(x, 64, softplus=softplus, limit=limit)
+    assert_parity(y, y_ref, torch.bfloat16, "y")
+    assert_parity(h, h_ref, torch.bfloat16, "h_last")
