@@ -483,6 +483,12 @@ __global__ __launch_bounds__(256) void chunk_scan_fwd_kernel(
       }
 }
 
+// bf16 elements of the chunk-scan region that holds the HC heads' U tiles
+// ([HC][64][72]) and, after the sigma loop, one H_in tile ([64][N + 8])
+constexpr int chunk_scan_ureg(int NK, int HC) {
+  return HC * 64 * 72 > 64 * (32 * NK + 8) ? HC * 64 * 72 : 64 * (32 * NK + 8);
+}
+
 // ---------------------------------------------------------------------------
 // chunk scan, bf16 fast path.  One block per (b, chunk, group, 64-row tau
 // tile, 64-wide p tile, chunk of HC heads); wave w owns tau columns
@@ -506,10 +512,11 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
   constexpr int N = 32 * NK;
   constexpr int LDN = N + 8, LDU = 64 + 8;
   constexpr int HQ = N / 16;   // float4 of an H tile per thread (64 x N fp32 / 256 threads)
+  constexpr int UREG = chunk_scan_ureg(NK, HC);   // bf16 of the U tiles / H_in tile region
   extern __shared__ __align__(16) unsigned char smem_raw[];
   bf16* Bs = reinterpret_cast<bf16*>(smem_raw);  // [64][LDN]     B rows of the sigma tile
   bf16* Us = Bs + 64 * LDN;                      // [HC][64][LDU] U rows per head; later H_in tile
-  float* tab = reinterpret_cast<float*>(Us + HC * 64 * LDU);  // [HC][64] e^{dc_t0 - dc_sig} dt_sig
+  float* tab = reinterpret_cast<float*>(Us + UREG);   // [HC][64] e^{dc_t0 - dc_sig} dt_sig
   float* dcd = tab + HC * 64;                                 // [HC][64] dc_sig (log2)
   float* dtd = dcd + HC * 64;                                 // [HC][64] dt_sig (0 past qlim)
 
@@ -617,12 +624,33 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
     }
   };
 
+  // H_in staging for the state contribution (one head per stage, bf16 in the U tiles' space)
+  bf16* Hs = Us;   // [64][LDN] bf16, in the U tiles' region
+  float4 ph[HQ];
+  auto load_h = [&](int k) {
+    const float* Hb = states + (((static_cast<long>(b) * d.nc + c) * d.H + h0 + k) * d.P + p0) * N;
+#pragma unroll
+    for (int i = 0; i < HQ; ++i) {
+      const int e = tid + 256 * i;
+      const int row = e / (N / 4), c4 = e % (N / 4);
+      ph[i] = *reinterpret_cast<const float4*>(Hb + static_cast<unsigned>(min(row, d.P - p0 - 1) * N + 4 * c4));
+      if (p0 + row >= d.P) ph[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto commit_h = [&]() {
+#pragma unroll
+    for (int i = 0; i < HQ; ++i) {
+      const int e = tid + 256 * i;
+      const int row = e / (N / 4), c4 = e % (N / 4);
+      *reinterpret_cast<uint2*>(Hs + row * LDN + 4 * c4) =
+          uint2{pack_bf16x2(ph[i].x, ph[i].y), pack_bf16x2(ph[i].z, ph[i].w)};
+    }
+  };
   load_tile(0);
   commit_tile();
   __syncthreads();
-  for (int s = 0; s <= ti; ++s) {
-    const bool diag = s == ti;
-    if (!diag) load_tile(s + 1);
+  // one sigma tile: C.B^T, decay, Y^T += U^T S^T for every head
+  auto sigma_tile = [&](int s, bool diag) __attribute__((always_inline)) {
     const int s0 = 64 * s;
     const bool fact = mono && !diag;
     if (mono && diag) {
@@ -669,36 +697,23 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
           acc[k][t] = mfma_bf16(lds_tr8(ut + (32 * ks + 8 * lg) * LDU + 16 * t, LDU, lane), pbk, acc[k][t]);
       }
     }
+  };
+  for (int s = 0; s < ti; ++s) {
+    load_tile(s + 1);
+    sigma_tile(s, false);
     __syncthreads();  // every wave is done with this tile
-    if (!diag) {
-      commit_tile();
-      __syncthreads();
-    }
+    commit_tile();
+    __syncthreads();
   }
+  // the diagonal tile prefetches the first head's H_in instead (when its
+  // registers fit beside the tile's: state_dim <= 192)
+  constexpr bool kEarlyH = NK <= 6;
+  if constexpr (kEarlyH) load_h(0);
+  sigma_tile(ti, true);
+  __syncthreads();
+  if constexpr (!kEarlyH) load_h(0);
 
   // ---- state contribution exp(dc_tau) * H_in . C^T, one head per stage, then the store ----
-  bf16* Hs = Us;   // [64][LDN] bf16 (fits in the U tiles' space)
-  float4 ph[HQ];
-  auto load_h = [&](int k) {
-    const float* Hb = states + (((static_cast<long>(b) * d.nc + c) * d.H + h0 + k) * d.P + p0) * N;
-#pragma unroll
-    for (int i = 0; i < HQ; ++i) {
-      const int e = tid + 256 * i;
-      const int row = e / (N / 4), c4 = e % (N / 4);
-      ph[i] = *reinterpret_cast<const float4*>(Hb + static_cast<unsigned>(min(row, d.P - p0 - 1) * N + 4 * c4));
-      if (p0 + row >= d.P) ph[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  };
-  auto commit_h = [&]() {
-#pragma unroll
-    for (int i = 0; i < HQ; ++i) {
-      const int e = tid + 256 * i;
-      const int row = e / (N / 4), c4 = e % (N / 4);
-      *reinterpret_cast<uint2*>(Hs + row * LDN + 4 * c4) =
-          uint2{pack_bf16x2(ph[i].x, ph[i].y), pack_bf16x2(ph[i].z, ph[i].w)};
-    }
-  };
-  load_h(0);
   commit_h();
   __syncthreads();
 #pragma unroll
@@ -838,12 +853,13 @@ template <int NK>
 int launch_chunk_scan_bf16_nk(const void* u, const void* B, const void* C, const float* dt,
                               const float* dc, const float* states, float* y, const SsdDims& d,
                               int mono, hipStream_t s) {
-  constexpr int HC = 4;
+  constexpr int HC = NK <= 6 ? 4 : 2;   // heads per block (state_dim > 192: registers)
   const int hpg = d.H / d.G;
   const int nhc = (hpg + HC - 1) / HC;
   const long blocks = static_cast<long>((d.Lc + 63) / 64) * ((d.P + 63) / 64) * nhc * d.G *
                       d.nc * d.b;
-  const size_t smem = sizeof(bf16) * (64 * (32 * NK + 8) + HC * 64 * 72) + sizeof(float) * HC * 192;
+  const size_t smem = sizeof(bf16) * (64 * (32 * NK + 8) + chunk_scan_ureg(NK, HC)) +
+                      sizeof(float) * HC * 192;
   if (smem > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(
         reinterpret_cast<const void*>(chunk_scan_fwd_bf16_kernel<NK, HC>),

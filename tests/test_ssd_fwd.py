@@ -174,6 +174,8 @@ FAST_CASES = [
     ("chunk96", dict(b=2, L=300, H=4, P=64, N=128, G=2, lens=[300, 95]), 96),
     ("chunk32", dict(b=1, L=100, H=2, P=16, N=32, G=2, with_h=False), 32),
     ("p128_n192_c256", dict(b=2, L=600, H=2, P=128, N=192, G=1, lens=[600, 517]), 256),
+    # state_dim 256: two heads per block, the second head chunk partial
+    ("n256_hpg3", dict(b=1, L=160, H=3, P=64, N=256, G=1, lens=[150]), 64),
 ]
 
 
