@@ -256,6 +256,76 @@ def run_sparse(args, torch):
                          "algorithmic_flops": flops, "qk_pairs": pairs}}
 
 
+def run_ssm_io(args, torch):
+    """The SSM block's stages around the scan at config 1's model shapes
+    (b8, L4096, x_dim 2048 = 32 heads x 64, B/C 8 groups x 128, conv K=4,
+    bf16 activations, fp32 y): the SiLU + causal-conv prologue (forward and
+    backward) and the D-skip / SiLU-gate epilogue (forward and backward).
+    Each kernel's time comes from HIP events on its launch stream; bytes are
+    the algorithmic ones (each input read once, each output written once)."""
+    from selective_attention.kernels.ssm_io import (ssm_conv_backward, ssm_conv_forward,
+                                                    ssm_gate_backward, ssm_gate_forward)
+    from selective_attention.profiling import kernel_timer
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    b, L, x_dim, bc_dim, K = 8, 4096, 2048, 1024, 4
+    ch = x_dim + 2 * bc_dim
+    bf = torch.bfloat16
+    hbc = torch.randn(b, L, ch, device=dev, generator=g).to(bf)
+    w = torch.randn(ch, K, device=dev, generator=g) * 0.5
+    bias = torch.randn(ch, device=dev, generator=g) * 0.1
+    dxbc = torch.randn(b, L, ch, device=dev, generator=g).to(bf)
+    dx, dB, dC = dxbc[..., :x_dim].contiguous(), dxbc[..., x_dim:x_dim + bc_dim].contiguous(), \
+        dxbc[..., x_dim + bc_dim:].contiguous()
+    y = torch.randn(b, L, x_dim, device=dev, generator=g)
+    x = torch.randn(b, L, x_dim, device=dev, generator=g).to(bf)
+    gate = torch.randn(b, L, x_dim, device=dev, generator=g).to(bf)
+    D = torch.randn(x_dim, device=dev, generator=g)
+    dout = torch.randn(b, L, x_dim, device=dev, generator=g).to(bf)
+
+    def step():
+        ssm_conv_forward(hbc, w, bias, x_dim, bc_dim)
+        ssm_conv_backward(hbc, w, dx, dB, dC, x_dim, bc_dim)
+        ssm_gate_forward(y, x, D, gate)
+        ssm_gate_backward(dout, y, x, D, gate)
+
+    steps = max(args.steps, 10)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    with kernel_timer() as kt:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    act = b * L * ch * 2            # one bf16 pass over hBC-shaped data
+    row = b * L * x_dim             # elements of y / x / gate
+    nbytes = {"ssm_conv_fwd": 2 * act, "ssm_conv_bwd": 3 * act,
+              "ssm_gate_fwd": row * (4 + 2 + 2 + 2), "ssm_gate_bwd": row * (2 + 4 + 2 + 2 + 4 + 2 + 2)}
+    # each backward's fixed-order reduction of its weight / D partials counts with it
+    extra = {"ssm_conv_bwd": "ssm_conv_grad_reduce", "ssm_gate_bwd": "ssm_gate_dD_reduce"}
+    kernels = {}
+    for k, nb in nbytes.items():
+        us = kt.stats[k]["avg_us"]
+        if k in extra and extra[k] in kt.stats:
+            us += kt.stats[extra[k]]["avg_us"]
+        gbs = nb / (us / 1e6) / 1e9
+        kernels[k] = {"avg_us": round(us, 2), "algorithmic_bytes": nb, "achieved_gbs": round(gbs, 1),
+                      "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    tot_b = sum(nbytes.values())
+    tot_us = sum(v["avg_us"] for v in kernels.values())
+    gbs = tot_b / (tot_us / 1e6) / 1e9
+    return {"us": round(tot_us, 1),
+            "config": {"workload": "ssm_io_config1", "batch": b, "seq_len": L, "x_dim": x_dim,
+                       "bc_dim": bc_dim, "conv_kernel": K, "activations": "bf16", "y": "fp32"},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "algorithmic_bytes": tot_b},
+            "kernels": kernels,
+            "aux_kernels_us": {k: round(v["avg_us"], 2) for k, v in kt.stats.items() if k not in nbytes},
+            "note": "ssm_conv_bwd / ssm_gate_bwd include their partial-sum reductions"}
+
+
 def cpu_baseline(torch, budget_s):
     """The fp32 CPU restatement (oracle/ssd.py) of the same fwd+bwd on one
     batch row of config 1; tokens/s of that row."""
@@ -298,7 +368,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--ssd-only", action="store_true", help="skip the decode / sparse lines")
+    ap.add_argument("--ssd-only", action="store_true", help="skip the decode / sparse / ssm_io lines")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the timed work, run 3 plain device copies of this many MiB "
@@ -332,6 +402,7 @@ def main():
     if not args.ssd_only:
         out["decode"] = run_decode(args, torch)
         out["sparse_attn"] = run_sparse(args, torch)
+        out["ssm_io"] = run_ssm_io(args, torch)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, args.cpu_budget_s)
     if args.copy_probe_mib > 0:

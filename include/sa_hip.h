@@ -152,6 +152,72 @@ int sa_paged_decode_fwd(int dtype, const void* q, const void* k_pages, const voi
                         int max_pages, int num_pages, float softmax_scale, void* o,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * SSM prologue: SiLU, then the depthwise causal conv (zero history), then the
+ * split into x / B / C.  Replaces the torch ops of SSM.forward
+ * (reference modules/ssm.py:116-125: F.silu, nn.Conv1d(padding=K-1) sliced
+ * to seq_len, torch.split) and, with conv_ctx set, SSMCache.build_conv_ctx
+ * (inference/ssm_cache.py:8-36).
+ *   hbc (b,L,channels): dtype `dtype`; weight (channels,K) float32 (the
+ *   Conv1d weight (channels,1,K)); bias (channels,) float32 or NULL
+ *   x (b,L,x_dim), B and C (b,L,bc_dim), x_dim + 2*bc_dim = channels:
+ *   dtype `dtype`, each contiguous
+ *   xBC[b,t,c] = bias[c] + sum_{j<K} weight[c,j] * silu(hbc[b,t-K+1+j,c])
+ *   conv_ctx (b,channels,K) or NULL: hbc[b, len_b-K+j, c] for
+ *   0 <= len_b-K+j < len_b, else 0; len_b = lengths[b] (int64) or L.
+ *   x, B and C all NULL: only conv_ctx is written.  1 <= K <= 8.
+ */
+int sa_ssm_conv_fwd(int dtype, const void* hbc, const float* weight, const float* bias, int batch,
+                    int seqlen, int channels, int kernel, int x_dim, int bc_dim, void* x, void* B,
+                    void* C, const int64_t* lengths, void* conv_ctx, void* stream);
+
+size_t sa_ssm_conv_bwd_workspace_size(int batch, int seqlen, int channels, int kernel);
+
+/*
+ * Backward of sa_ssm_conv_fwd (the reference gets it from torch autograd
+ * through F.silu and nn.Conv1d, modules/ssm.py:116-118).
+ *   dx, dB, dC: gradients of x, B, C (dtype `dtype`); dhbc (b,L,channels);
+ *   dweight (channels,K), dbias (channels,) or NULL: float32, overwritten.
+ *   The weight and bias gradients are summed per 256-row block and then in a
+ *   fixed order (bit-reproducible).
+ */
+int sa_ssm_conv_bwd(int dtype, const void* hbc, const float* weight, const void* dx,
+                    const void* dB, const void* dC, int batch, int seqlen, int channels,
+                    int kernel, int x_dim, int bc_dim, void* dhbc, float* dweight, float* dbias,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * SSM decode-step prologue.  Replaces SSMCache.update
+ * (inference/ssm_cache.py:38-43: roll the context left, put the new row
+ * last) and the conv of SSM.step (modules/ssm.py:173-182).
+ *   hbc_t (b,channels), conv_ctx (b,channels,K) updated in place: dtype
+ *   `dtype`; weight, bias as in sa_ssm_conv_fwd; x (b,x_dim), B, C (b,bc_dim).
+ */
+int sa_ssm_conv_step(int dtype, const void* hbc_t, void* conv_ctx, const float* weight,
+                     const float* bias, int batch, int channels, int kernel, int x_dim,
+                     int bc_dim, void* x, void* B, void* C, void* stream);
+
+/*
+ * SSM epilogue: out = (y + D*x) * silu(gate).  Replaces
+ * modules/ssm.py:144-150 (and the step's :200-202).
+ *   y (rows,dim) float32 (the scan output); x, gate, out (rows,dim): dtype
+ *   `dtype`; D (dim,) float32.
+ */
+int sa_ssm_gate_fwd(int dtype, const float* y, const void* x, const float* D, const void* gate,
+                    int64_t rows, int dim, void* out, void* stream);
+
+size_t sa_ssm_gate_bwd_workspace_size(int64_t rows, int dim);
+
+/*
+ * Backward of sa_ssm_gate_fwd (torch autograd in the reference):
+ *   dy = dout*silu(gate) (float32); dx = D*dy; dgate = dout*(y+D*x)*silu'(gate)
+ *   (dtype `dtype`); dD (dim,) float32 = sum over rows of dy*x, summed per
+ *   256-row block and then in a fixed order.
+ */
+int sa_ssm_gate_bwd(int dtype, const void* dout, const float* y, const void* x, const float* D,
+                    const void* gate, int64_t rows, int dim, float* dy, void* dx, void* dgate,
+                    float* dD, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,10 @@ Contents (each function cites the reference file:line it restates):
              attention (brute-force dense masked softmax; no reference kernel
              exists for these, the gated-softmax semantics come from
              modules/selective_attention.py).
+  ssm_io.py - the SSM block's stages around the scan (modules/ssm.py):
+             SiLU + causal depthwise conv prologue, its decode-time context
+             (inference/ssm_cache.py), the D-skip / SiLU-gate epilogue, and
+             their hand-written backward formulas.
 
 How each function is pinned (tests/test_oracle_*.py):
   ssd forward   - chunked == sequential recurrence (fp64), chunk-size
@@ -27,6 +31,10 @@ How each function is pinned (tests/test_oracle_*.py):
   attention     - == F.scaled_dot_product_attention (textbook softmax
                   attention) when the selection covers every causal block /
                   the page table is the identity; brute-force loops.
+  ssm_io        - conv == the reference's F.silu / F.conv1d(padding=K-1) /
+                  slice composition and == a brute-force loop; streaming
+                  decode steps == the batch conv; context == a brute-force
+                  gather; backward formulas == torch.autograd (fp64).
 The reference ships no golden vectors or known-answer tests for this path
 (its one test file is an integration test that is broken as shipped), so
 nothing here is pinned against reference-produced numbers.  Rounding-level

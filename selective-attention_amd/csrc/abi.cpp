@@ -23,7 +23,7 @@ void sa_set_error(const char* fmt, ...) {
 
 const char* sa_last_error(void) { return g_err; }
 
-int sa_version(void) { return 1; }
+int sa_version(void) { return 2; }
 
 }  // extern "C"
 

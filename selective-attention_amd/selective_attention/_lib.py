@@ -39,10 +39,20 @@ SIGNATURES: dict[str, list] = {
     "sa_ssd_bwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                    _i, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i,
                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    "sa_ssm_conv_fwd": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp],
+    "sa_ssm_conv_bwd_workspace_size": [_i, _i, _i, _i],
+    "sa_ssm_conv_bwd": [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp,
+                        _vp, _sz, _vp],
+    "sa_ssm_conv_step": [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp],
+    "sa_ssm_gate_fwd": [_i, _vp, _vp, _vp, _vp, _i64, _i, _vp, _vp],
+    "sa_ssm_gate_bwd_workspace_size": [_i64, _i],
+    "sa_ssm_gate_bwd": [_i, _vp, _vp, _vp, _vp, _vp, _i64, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
 }
 
 RESTYPES = {"sa_last_error": ctypes.c_char_p, "sa_profile_enable": None, "sa_ssd_bwd_workspace_size": ctypes.c_size_t,
-            "sa_paged_decode_workspace_size": ctypes.c_size_t}
+            "sa_paged_decode_workspace_size": ctypes.c_size_t,
+            "sa_ssm_conv_bwd_workspace_size": ctypes.c_size_t,
+            "sa_ssm_gate_bwd_workspace_size": ctypes.c_size_t}
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
