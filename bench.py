@@ -256,6 +256,40 @@ def run_sparse(args, torch):
                          "algorithmic_flops": flops, "qk_pairs": pairs}}
 
 
+def _scan_gate_fusion(args, torch):
+    """SSD forward + SSM epilogue at config 1: the scan then the gate kernel
+    (fp32 y written and re-read) against the epilogue fused into the chunk
+    scan (bf16 out and yd written, no y)."""
+    from selective_attention import workloads
+    from selective_attention.kernels.ssd_scan import ssd_scan_forward, ssd_scan_forward_gated
+    from selective_attention.kernels.ssm_io import ssm_gate_forward
+
+    dev = torch.device("cuda:0")
+    cfg = dict(workloads.SSD_CONFIGS[1])
+    x = workloads.ssd_inputs(**cfg, device=dev)
+    b, L, H, P = x["u"].shape
+    g = torch.Generator(device=dev).manual_seed(1)
+    D = torch.randn(H * P, device=dev, generator=g)
+    gate = torch.randn(b, L, H, P, device=dev, generator=g).to(x["u"].dtype)
+    lim = (0.0, float("inf"))
+
+    def unfused():
+        y, _ = ssd_scan_forward(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], None, None, None,
+                                cfg["chunk"], True, lim)
+        return ssm_gate_forward(y.view(b, L, H * P), x["u"].view(b, L, H * P), D,
+                                gate.view(b, L, H * P))
+
+    def fused():
+        return ssd_scan_forward_gated(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], None, None,
+                                      None, cfg["chunk"], True, lim, D, gate)
+
+    steps = max(args.steps, 10)
+    ms_u = _time_events(torch, unfused, steps, args.warmup)
+    ms_f = _time_events(torch, fused, steps, args.warmup)
+    return {"unfused_us": round(ms_u * 1e3, 1), "fused_us": round(ms_f * 1e3, 1),
+            "config": "ssd_scan_fwd_config1 + (y + D u) silu(gate), bf16 out"}
+
+
 def run_ssm_io(args, torch):
     """The SSM block's stages around the scan at config 1's model shapes
     (b8, L4096, x_dim 2048 = 32 heads x 64, B/C 8 groups x 128, conv K=4,
@@ -315,7 +349,9 @@ def run_ssm_io(args, torch):
     tot_b = sum(nbytes.values())
     tot_us = sum(v["avg_us"] for v in kernels.values())
     gbs = tot_b / (tot_us / 1e6) / 1e9
+    fused = _scan_gate_fusion(args, torch)
     return {"us": round(tot_us, 1),
+            "scan_gate_forward": fused,
             "config": {"workload": "ssm_io_config1", "batch": b, "seq_len": L, "x_dim": x_dim,
                        "bc_dim": bc_dim, "conv_kernel": K, "activations": "bf16", "y": "fp32"},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,

@@ -213,10 +213,34 @@ size_t sa_ssm_gate_bwd_workspace_size(int64_t rows, int dim);
  *   dy = dout*silu(gate) (float32); dx = D*dy; dgate = dout*(y+D*x)*silu'(gate)
  *   (dtype `dtype`); dD (dim,) float32 = sum over rows of dy*x, summed per
  *   256-row block and then in a fixed order.
+ *   y: the float32 scan output, or with y_is_yd the `dtype` tensor yd = y+D*x
+ *   that sa_ssd_fwd_gated saves.
  */
-int sa_ssm_gate_bwd(int dtype, const void* dout, const float* y, const void* x, const float* D,
-                    const void* gate, int64_t rows, int dim, float* dy, void* dx, void* dgate,
-                    float* dD, void* workspace, size_t workspace_bytes, void* stream);
+int sa_ssm_gate_bwd(int dtype, const void* dout, const void* y, int y_is_yd, const void* x,
+                    const float* D, const void* gate, int64_t rows, int dim, float* dy, void* dx,
+                    void* dgate, float* dD, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * 1 when sa_ssd_fwd_gated handles these sizes (bfloat16, head_dim % 8 == 0,
+ * state_dim a multiple of 32 up to 256), else 0.
+ */
+int sa_ssd_fwd_gated_supported(int dtype, int head_dim, int state_dim);
+
+/*
+ * SSD chunked scan forward with the SSM epilogue fused into its output
+ * stage: SSDScanFn (ops/ssd_scan.py:7-80) followed by modules/ssm.py:144-150
+ * ((y + D*u) * silu(gate)) in one pass, so the float32 y is never written.
+ * Arguments as sa_ssd_fwd, plus D (H*P,) float32 and gate (b,L,H,P) bf16;
+ * outputs out = (y + D*u)*silu(gate) and yd = y + D*u, (b,L,H,P) bf16 (yd is
+ * what sa_ssm_gate_bwd needs), with h_last, dt, dc, states as in sa_ssd_fwd.
+ * D, gate, out, yd 16-byte aligned.
+ */
+int sa_ssd_fwd_gated(int dtype, const void* u, const float* A, const void* B, const void* C,
+                     const void* delta_raw, const float* delta_bias, const float* h_init,
+                     const int64_t* length, int batch, int seqlen, int num_heads, int head_dim,
+                     int num_groups, int state_dim, int chunk_size, int use_softplus,
+                     float delta_min, float delta_max, const float* D, const void* gate, void* out,
+                     void* yd, float* h_last, float* dt, float* dc, float* states, void* stream);
 
 #ifdef __cplusplus
 }

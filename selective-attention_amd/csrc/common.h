@@ -39,6 +39,11 @@ __device__ __forceinline__ float bf16hi_to_f32(uint32_t w) { return __uint_as_fl
 // evaluated as exp2(d * log2(e)) on pre-scaled cumulative sums
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 constexpr float kLog2e = 1.4426950408889634f;
+// sigmoid on the transcendental unit (v_exp_f32, v_rcp_f32; ~1 ulp each):
+// the SiLU of the SSM block's conv prologue and gate epilogue
+__device__ __forceinline__ float fast_sigmoid(float z) {
+  return __builtin_amdgcn_rcpf(1.0f + fast_exp2(-z * kLog2e));
+}
 
 template <typename T> struct Conv;
 template <> struct Conv<float> {

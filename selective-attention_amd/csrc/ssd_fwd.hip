@@ -483,6 +483,16 @@ __global__ __launch_bounds__(256) void chunk_scan_fwd_kernel(
       }
 }
 
+// The SSM epilogue fused into the bf16 chunk scan (modules/ssm.py:144-150):
+// out = (y + D u) silu(gate) and yd = y + D u, both bf16 (b, L, H, P), in place
+// of the fp32 y.  D: (H * P,) float32; gate: (b, L, H, P) bf16.
+struct GateOut {
+  const float* D;
+  const bf16* gate;
+  bf16* out;
+  bf16* yd;
+};
+
 // bf16 elements of the chunk-scan region that holds the HC heads' U tiles
 // ([HC][64][72]) and, after the sigma loop, one H_in tile ([64][N + 8])
 constexpr int chunk_scan_ureg(int NK, int HC) {
@@ -504,11 +514,11 @@ constexpr int chunk_scan_ureg(int NK, int HC) {
 // accumulator once before the diagonal tile, which is decayed exactly.
 // Tiles are prefetched into registers during the previous tile's MFMAs.
 // ---------------------------------------------------------------------------
-template <int NK, int HC>
+template <int NK, int HC, bool GATED>
 __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
     const bf16* __restrict__ u, const bf16* __restrict__ Bm, const bf16* __restrict__ Cm,
     const float* __restrict__ dt, const float* __restrict__ dc, const float* __restrict__ states,
-    float* __restrict__ y, SsdDims d, int mono) {
+    float* __restrict__ y, GateOut go, SsdDims d, int mono) {
   constexpr int N = 32 * NK;
   constexpr int LDN = N + 8, LDU = 64 + 8;
   constexpr int HQ = N / 16;   // float4 of an H tile per thread (64 x N fp32 / 256 threads)
@@ -740,12 +750,30 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
 #pragma unroll
     for (int k = 0; k < HC; ++k) {
       if (k >= nh) break;
-      float* yrow = y + (tok0 + tau) * u_rs + static_cast<long>(h0 + k) * d.P;
+      const long row = (tok0 + tau) * u_rs + static_cast<long>(h0 + k) * d.P;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int p = p0 + 16 * t + 4 * lg;
-        if (p < d.P)
-          *reinterpret_cast<float4*>(yrow + p) = make_float4(acc[k][t][0], acc[k][t][1], acc[k][t][2], acc[k][t][3]);
+        if (p >= d.P) continue;
+        if constexpr (GATED) {
+          // SSM epilogue: yd = y + D u, out = yd silu(gate) (bf16; y itself is not stored)
+          const uint2 uq = *reinterpret_cast<const uint2*>(u + row + p);
+          const uint2 gq = *reinterpret_cast<const uint2*>(go.gate + row + p);
+          const float4 dq = *reinterpret_cast<const float4*>(go.D + (h0 + k) * d.P + p);
+          const float uv[4] = {bf16lo_to_f32(uq.x), bf16hi_to_f32(uq.x), bf16lo_to_f32(uq.y), bf16hi_to_f32(uq.y)};
+          const float gv[4] = {bf16lo_to_f32(gq.x), bf16hi_to_f32(gq.x), bf16lo_to_f32(gq.y), bf16hi_to_f32(gq.y)};
+          const float Dv[4] = {dq.x, dq.y, dq.z, dq.w};
+          float yd[4], o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            yd[i] = acc[k][t][i] + Dv[i] * uv[i];
+            o[i] = yd[i] * gv[i] * fast_sigmoid(gv[i]);
+          }
+          *reinterpret_cast<uint2*>(go.out + row + p) = uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+          *reinterpret_cast<uint2*>(go.yd + row + p) = uint2{pack_bf16x2(yd[0], yd[1]), pack_bf16x2(yd[2], yd[3])};
+        } else {
+          *reinterpret_cast<float4*>(y + row + p) = make_float4(acc[k][t][0], acc[k][t][1], acc[k][t][2], acc[k][t][3]);
+        }
       }
     }
   }
@@ -852,7 +880,7 @@ int launch_chunk_scan(const void* u, const void* B, const void* C, const float* 
 template <int NK>
 int launch_chunk_scan_bf16_nk(const void* u, const void* B, const void* C, const float* dt,
                               const float* dc, const float* states, float* y, const SsdDims& d,
-                              int mono, hipStream_t s) {
+                              int mono, const GateOut* go, hipStream_t s) {
   constexpr int HC = NK <= 6 ? 4 : 2;   // heads per block (state_dim > 192: registers)
   const int hpg = d.H / d.G;
   const int nhc = (hpg + HC - 1) / HC;
@@ -860,18 +888,22 @@ int launch_chunk_scan_bf16_nk(const void* u, const void* B, const void* C, const
                       d.nc * d.b;
   const size_t smem = sizeof(bf16) * (64 * (32 * NK + 8) + chunk_scan_ureg(NK, HC)) +
                       sizeof(float) * HC * 192;
-  if (smem > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(chunk_scan_fwd_bf16_kernel<NK, HC>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
-    SA_CHECK_ARG(e == hipSuccess, "chunk_scan_fwd_bf16: %zu B of LDS refused", smem);
-  }
-  ProfScope prof_("chunk_scan_fwd", s);
-  hipLaunchKernelGGL((chunk_scan_fwd_bf16_kernel<NK, HC>), dim3(blocks), dim3(256), smem, s,
-                     static_cast<const bf16*>(u), static_cast<const bf16*>(B),
-                     static_cast<const bf16*>(C), dt, dc, states, y, d, mono);
-  SA_CHECK_LAUNCH("chunk_scan_fwd_bf16");
-  return 0;
+  auto run = [&](auto kernel, const char* name) -> int {
+    if (smem > 64 * 1024) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         static_cast<int>(smem));
+      SA_CHECK_ARG(e == hipSuccess, "chunk_scan_fwd_bf16: %zu B of LDS refused", smem);
+    }
+    ProfScope prof_(name, s);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), smem, s, static_cast<const bf16*>(u),
+                       static_cast<const bf16*>(B), static_cast<const bf16*>(C), dt, dc, states,
+                       y, go ? *go : GateOut{}, d, mono);
+    SA_CHECK_LAUNCH("chunk_scan_fwd_bf16");
+    return 0;
+  };
+  if (go) return run(chunk_scan_fwd_bf16_kernel<NK, HC, true>, "chunk_scan_fwd_gated");
+  return run(chunk_scan_fwd_bf16_kernel<NK, HC, false>, "chunk_scan_fwd");
 }
 
 inline bool chunk_scan_bf16_ok(const SsdDims& d, const void* u, const void* B, const void* C,
@@ -882,16 +914,16 @@ inline bool chunk_scan_bf16_ok(const SsdDims& d, const void* u, const void* B, c
 
 int launch_chunk_scan_bf16(const void* u, const void* B, const void* C, const float* dt,
                            const float* dc, const float* states, float* y, const SsdDims& d,
-                           int mono, hipStream_t s) {
+                           int mono, const GateOut* go, hipStream_t s) {
   switch (d.N / 32) {
-    case 1: return launch_chunk_scan_bf16_nk<1>(u, B, C, dt, dc, states, y, d, mono, s);
-    case 2: return launch_chunk_scan_bf16_nk<2>(u, B, C, dt, dc, states, y, d, mono, s);
-    case 3: return launch_chunk_scan_bf16_nk<3>(u, B, C, dt, dc, states, y, d, mono, s);
-    case 4: return launch_chunk_scan_bf16_nk<4>(u, B, C, dt, dc, states, y, d, mono, s);
-    case 5: return launch_chunk_scan_bf16_nk<5>(u, B, C, dt, dc, states, y, d, mono, s);
-    case 6: return launch_chunk_scan_bf16_nk<6>(u, B, C, dt, dc, states, y, d, mono, s);
-    case 7: return launch_chunk_scan_bf16_nk<7>(u, B, C, dt, dc, states, y, d, mono, s);
-    default: return launch_chunk_scan_bf16_nk<8>(u, B, C, dt, dc, states, y, d, mono, s);
+    case 1: return launch_chunk_scan_bf16_nk<1>(u, B, C, dt, dc, states, y, d, mono, go, s);
+    case 2: return launch_chunk_scan_bf16_nk<2>(u, B, C, dt, dc, states, y, d, mono, go, s);
+    case 3: return launch_chunk_scan_bf16_nk<3>(u, B, C, dt, dc, states, y, d, mono, go, s);
+    case 4: return launch_chunk_scan_bf16_nk<4>(u, B, C, dt, dc, states, y, d, mono, go, s);
+    case 5: return launch_chunk_scan_bf16_nk<5>(u, B, C, dt, dc, states, y, d, mono, go, s);
+    case 6: return launch_chunk_scan_bf16_nk<6>(u, B, C, dt, dc, states, y, d, mono, go, s);
+    case 7: return launch_chunk_scan_bf16_nk<7>(u, B, C, dt, dc, states, y, d, mono, go, s);
+    default: return launch_chunk_scan_bf16_nk<8>(u, B, C, dt, dc, states, y, d, mono, go, s);
   }
 }
 
@@ -899,13 +931,16 @@ template <typename T, typename MT>
 int ssd_fwd_impl(const void* u, const float* A, const void* B, const void* C,
                  const void* delta_raw, const float* bias, const float* h_init,
                  const int64_t* length, const SsdDims& d, int sp, float lo, float hi, float* y,
-                 float* h_last, float* dt, float* dc, float* states, hipStream_t s) {
+                 float* h_last, float* dt, float* dc, float* states, hipStream_t s,
+                 const GateOut* go = nullptr) {
   int rc;
+  const bool fast = sizeof(T) == 2 && chunk_scan_bf16_ok(d, u, B, C, states);
+  SA_CHECK_ARG(!go || fast, "sa_ssd_fwd_gated: the fused epilogue needs the bf16 fast path "
+               "(state_dim a multiple of 32, <= 256; head_dim a multiple of 8; 16-byte aligned)");
   if ((rc = launch_chunk_cumsum<T>(delta_raw, A, bias, length, dt, dc, d, sp, lo, hi, s))) return rc;
   if ((rc = launch_chunk_outer<MT, T, T, 0>(u, B, dt, dc, length, states, d, s))) return rc;
   if ((rc = launch_state_passing_fwd(states, h_init, h_last, dc, d, s))) return rc;
-  if (sizeof(T) == 2 && chunk_scan_bf16_ok(d, u, B, C, states))
-    return launch_chunk_scan_bf16(u, B, C, dt, dc, states, y, d, lo >= 0.f ? 1 : 0, s);
+  if (fast) return launch_chunk_scan_bf16(u, B, C, dt, dc, states, y, d, lo >= 0.f ? 1 : 0, go, s);
   return launch_chunk_scan<MT, T>(u, B, C, dt, dc, states, y, d, s);
 }
 
@@ -947,4 +982,35 @@ extern "C" int sa_ssd_fwd(int dtype, const void* u, const float* A, const void* 
                                                 dt, dc, states, s);
   sa_set_error("sa_ssd_fwd: unsupported dtype %d", dtype);
   return 1;
+}
+
+extern "C" int sa_ssd_fwd_gated_supported(int dtype, int head_dim, int state_dim) {
+  return dtype == sa::kBF16 && head_dim % 8 == 0 && state_dim % 32 == 0 && state_dim <= 256 ? 1 : 0;
+}
+
+extern "C" int sa_ssd_fwd_gated(int dtype, const void* u, const float* A, const void* B,
+                                const void* C, const void* delta_raw, const float* delta_bias,
+                                const float* h_init, const int64_t* length, int batch, int seqlen,
+                                int num_heads, int head_dim, int num_groups, int state_dim,
+                                int chunk_size, int use_softplus, float delta_min, float delta_max,
+                                const float* D, const void* gate, void* out, void* yd,
+                                float* h_last, float* dt, float* dc, float* states, void* stream) {
+  sa::SsdDims d;
+  int rc = sa::make_dims(batch, seqlen, num_heads, head_dim, num_groups, state_dim, chunk_size, &d,
+                         "sa_ssd_fwd_gated");
+  if (rc) return rc;
+  SA_CHECK_ARG(sa_ssd_fwd_gated_supported(dtype, head_dim, state_dim),
+               "sa_ssd_fwd_gated: needs bfloat16 activations, head_dim %% 8 == 0 and state_dim a "
+               "multiple of 32 up to 256 (got dtype %d, P=%d, N=%d)", dtype, head_dim, state_dim);
+  SA_CHECK_ARG(u && A && B && C && delta_raw && length && D && gate && out && yd && h_last && dt &&
+                   dc && states,
+               "sa_ssd_fwd_gated: null tensor pointer");
+  SA_CHECK_ARG(sa::aligned16(D) && sa::aligned16(gate) && sa::aligned16(out) && sa::aligned16(yd),
+               "sa_ssd_fwd_gated: D, gate, out and yd must be 16-byte aligned");
+  if (d.b == 0 || d.L == 0) return 0;
+  const sa::GateOut go{D, static_cast<const sa::bf16*>(gate), static_cast<sa::bf16*>(out),
+                       static_cast<sa::bf16*>(yd)};
+  return sa::ssd_fwd_impl<sa::bf16, sa::bf16>(u, A, B, C, delta_raw, delta_bias, h_init, length, d,
+                                              use_softplus, delta_min, delta_max, nullptr, h_last,
+                                              dt, dc, states, static_cast<hipStream_t>(stream), &go);
 }

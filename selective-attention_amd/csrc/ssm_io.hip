@@ -35,10 +35,7 @@ constexpr int kConvRows = kRuns * kConvRun;   // rows per block
 constexpr int kGateRows = kRuns * kGateRun;
 constexpr int kGbwdRows = kRuns * kGbwdRun;
 
-// sigmoid on the transcendental unit: v_exp_f32 and v_rcp_f32 (~1 ulp each)
-__device__ __forceinline__ float sigmoid_f(float z) {
-  return __builtin_amdgcn_rcpf(1.0f + fast_exp2(-z * kLog2e));
-}
+__device__ __forceinline__ float sigmoid_f(float z) { return fast_sigmoid(z); }
 __device__ __forceinline__ float silu_f(float z) { return z * sigmoid_f(z); }
 // d silu / dz = s (1 + z (1 - s)), s = sigmoid(z)
 __device__ __forceinline__ float dsilu_f(float z) {
@@ -419,9 +416,10 @@ __global__ __launch_bounds__(256) void ssm_gate_fwd_kernel(const float* __restri
   }
 }
 
-template <typename T, int V>
+// YD: y holds yd = y + D x in T (saved by the fused scan epilogue) instead of the fp32 y
+template <typename T, int V, bool YD>
 __global__ __launch_bounds__(256) void ssm_gate_bwd_kernel(
-    const T* __restrict__ dout, const float* __restrict__ y, const T* __restrict__ x,
+    const T* __restrict__ dout, const void* __restrict__ y, const T* __restrict__ x,
     const float* __restrict__ D, const T* __restrict__ g, float* __restrict__ dy,
     T* __restrict__ dx, T* __restrict__ dg, float* __restrict__ part, long rows, int dim) {
   __shared__ float red[kRuns][kCG * V];
@@ -440,7 +438,8 @@ __global__ __launch_bounds__(256) void ssm_gate_bwd_kernel(
       const long off = (r0 + i) * dim + c0;
       float ov[V], yv[V], xv[V], gv[V], a[V], b2[V], c2[V];
       load_v<T, V>(dout + off, ov);
-      load_v<float, V>(y + off, yv);
+      if constexpr (YD) load_v<T, V>(static_cast<const T*>(y) + off, yv);
+      else load_v<float, V>(static_cast<const float*>(y) + off, yv);
       load_v<T, V>(x + off, xv);
       load_v<T, V>(g + off, gv);
 #pragma unroll
@@ -449,7 +448,8 @@ __global__ __launch_bounds__(256) void ssm_gate_bwd_kernel(
         const float d = ov[v] * gv[v] * s;                       // dout silu(g)
         a[v] = d;
         b2[v] = dv[v] * d;
-        c2[v] = ov[v] * (yv[v] + dv[v] * xv[v]) * s * (1.0f + gv[v] * (1.0f - s));
+        const float yd = YD ? yv[v] : yv[v] + dv[v] * xv[v];
+        c2[v] = ov[v] * yd * s * (1.0f + gv[v] * (1.0f - s));
         dd[v] += d * xv[v];
       }
       store_v<float, V>(dy + off, a);
@@ -741,10 +741,10 @@ extern "C" size_t sa_ssm_gate_bwd_workspace_size(int64_t rows, int dim) {
   return rb * dim * sizeof(float);
 }
 
-extern "C" int sa_ssm_gate_bwd(int dtype, const void* dout, const float* y, const void* x,
-                               const float* D, const void* gate, int64_t rows, int dim, float* dy,
-                               void* dx, void* dgate, float* dD, void* workspace,
-                               size_t workspace_bytes, void* stream) {
+extern "C" int sa_ssm_gate_bwd(int dtype, const void* dout, const void* y, int y_is_yd,
+                               const void* x, const float* D, const void* gate, int64_t rows,
+                               int dim, float* dy, void* dx, void* dgate, float* dD,
+                               void* workspace, size_t workspace_bytes, void* stream) {
   SA_CHECK_ARG(rows >= 0 && dim > 0, "sa_ssm_gate_bwd: bad sizes rows=%lld dim=%d",
                static_cast<long long>(rows), dim);
   SA_CHECK_ARG(dtype == sa::kF32 || dtype == sa::kBF16, "sa_ssm_gate_bwd: unsupported dtype %d", dtype);
@@ -768,17 +768,17 @@ extern "C" int sa_ssm_gate_bwd(int dtype, const void* dout, const float* y, cons
   float* part = static_cast<float*>(workspace);
   {
     sa::ProfScope prof_("ssm_gate_bwd", s);
-#define SA_GATE_BWD(TT, VV)                                                                      \
-  hipLaunchKernelGGL((sa::ssm_gate_bwd_kernel<TT, VV>), grid, dim3(256), 0, s,                   \
+#define SA_GATE_BWD(TT, VV, YDD)                                                                 \
+  hipLaunchKernelGGL((sa::ssm_gate_bwd_kernel<TT, VV, YDD>), grid, dim3(256), 0, s,              \
                      static_cast<const TT*>(dout), y, static_cast<const TT*>(x), D,              \
                      static_cast<const TT*>(gate), dy, static_cast<TT*>(dx),                     \
                      static_cast<TT*>(dgate), part, static_cast<long>(rows), dim)
     if (dtype == sa::kF32) {
-      if (vec) SA_GATE_BWD(float, 8);
-      else SA_GATE_BWD(float, 1);
+      if (vec) { if (y_is_yd) SA_GATE_BWD(float, 8, true); else SA_GATE_BWD(float, 8, false); }
+      else { if (y_is_yd) SA_GATE_BWD(float, 1, true); else SA_GATE_BWD(float, 1, false); }
     } else {
-      if (vec) SA_GATE_BWD(bf16, 8);
-      else SA_GATE_BWD(bf16, 1);
+      if (vec) { if (y_is_yd) SA_GATE_BWD(bf16, 8, true); else SA_GATE_BWD(bf16, 8, false); }
+      else { if (y_is_yd) SA_GATE_BWD(bf16, 1, true); else SA_GATE_BWD(bf16, 1, false); }
     }
 #undef SA_GATE_BWD
     SA_CHECK_LAUNCH("ssm_gate_bwd");

@@ -46,7 +46,12 @@ SIGNATURES: dict[str, list] = {
     "sa_ssm_conv_step": [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp],
     "sa_ssm_gate_fwd": [_i, _vp, _vp, _vp, _vp, _i64, _i, _vp, _vp],
     "sa_ssm_gate_bwd_workspace_size": [_i64, _i],
-    "sa_ssm_gate_bwd": [_i, _vp, _vp, _vp, _vp, _vp, _i64, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    "sa_ssm_gate_bwd": [_i, _vp, _vp, _i, _vp, _vp, _vp, _i64, _i, _vp, _vp, _vp, _vp, _vp, _sz,
+                        _vp],
+    "sa_ssd_fwd_gated_supported": [_i, _i, _i],
+    "sa_ssd_fwd_gated": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                         _i, _i, _i, _i, _i, _i, _i, _i, _f, _f,
+                         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
 }
 
 RESTYPES = {"sa_last_error": ctypes.c_char_p, "sa_profile_enable": None, "sa_ssd_bwd_workspace_size": ctypes.c_size_t,

@@ -104,6 +104,49 @@ def ssd_scan_forward(
     return y, h_last
 
 
+def ssd_scan_forward_gated(u, A, B, C, delta_raw, delta_bias, h_init, length, chunk_size,
+                           use_delta_softplus, delta_limit, D, gate):
+    """ssd_scan_forward with the SSM epilogue (modules/ssm.py:144-150) fused into
+    the chunk scan's output stage.  bf16 only (check gated_supported first).
+
+    Args: as ssd_scan_forward, plus D (H*P,) and gate (b, L, H, P).
+    Returns: out = (y + D u) silu(gate) and yd = y + D u, both (b, L, H, P)
+    bf16, h_last, and saved (dt, dc, states).
+    """
+    code, u, A32, B, C, delta_raw, bias32, h0, length = _prep(
+        u, A, B, C, delta_raw, delta_bias, h_init, length)
+    b, L, H, P = u.shape
+    G, N = B.shape[2], B.shape[3]
+    nc = max(1, math.ceil(L / chunk_size))
+    dev = u.device
+    f32 = torch.float32
+    D32 = _f32_aligned(D)
+    gate = as_dtype(gate, u.dtype).contiguous()
+    out = torch.empty((b, L, H, P), dtype=u.dtype, device=dev)
+    yd = torch.empty((b, L, H, P), dtype=u.dtype, device=dev)
+    h_last = torch.empty((b, H, P, N), dtype=f32, device=dev)
+    dt = torch.empty((b, H, nc, chunk_size), dtype=f32, device=dev)
+    dc = torch.empty((b, H, nc, chunk_size), dtype=f32, device=dev)
+    states = torch.empty((b, nc, H, P, N), dtype=f32, device=dev)
+    lo, hi = limits(delta_limit)
+    if L == 0:
+        h_last.copy_(h0 if h0 is not None else torch.zeros_like(h_last))
+    else:
+        _lib.call(
+            "sa_ssd_fwd_gated", code, _lib.ptr(u), _lib.ptr(A32), _lib.ptr(B), _lib.ptr(C),
+            _lib.ptr(delta_raw), _lib.ptr(bias32), _lib.ptr(h0), _lib.ptr(length),
+            b, L, H, P, G, N, int(chunk_size), 1 if use_delta_softplus else 0, lo, hi,
+            _lib.ptr(D32), _lib.ptr(gate), _lib.ptr(out), _lib.ptr(yd),
+            _lib.ptr(h_last), _lib.ptr(dt), _lib.ptr(dc), _lib.ptr(states), _lib.stream_of(u))
+    return out, yd, h_last, (dt, dc, states)
+
+
+def gated_supported(dtype: torch.dtype, head_dim: int, state_dim: int) -> bool:
+    """Whether ssd_scan_forward_gated handles these sizes."""
+    code = act_dtype_code(dtype)
+    return bool(_lib.load().sa_ssd_fwd_gated_supported(code, head_dim, state_dim))
+
+
 def ssd_scan_backward(u, A, B, C, delta_raw, delta_bias, h_init, y_grad, h_last_grad, length,
                       chunk_size, use_delta_softplus=True, delta_limit=(0.0, float("inf")),
                       is_causal=True, saved=None):

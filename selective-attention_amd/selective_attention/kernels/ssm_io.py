@@ -111,12 +111,13 @@ def ssm_gate_forward(y, x, D, gate):
     return out
 
 
-def ssm_gate_backward(dout, y, x, D, gate):
-    """(dy float32, dx, dD float32, dgate) of ssm_gate_forward."""
+def ssm_gate_backward(dout, y, x, D, gate, y_is_yd=False):
+    """(dy float32, dx, dD float32, dgate) of ssm_gate_forward.  With y_is_yd,
+    y is yd = y + D x in the dtype of x (saved by the fused scan epilogue)."""
     dim = x.shape[-1]
     rows = x.numel() // dim if dim else 0
     dout = as_dtype(dout, x.dtype).contiguous()
-    y32 = as_dtype(y, torch.float32).contiguous()
+    y32 = as_dtype(y, x.dtype if y_is_yd else torch.float32).contiguous()
     x = x.contiguous()
     gate = as_dtype(gate, x.dtype).contiguous()
     D32 = as_dtype(D, torch.float32).contiguous()
@@ -126,7 +127,8 @@ def ssm_gate_backward(dout, y, x, D, gate):
     dD = torch.empty(dim, dtype=torch.float32, device=x.device)
     nbytes = _lib.load().sa_ssm_gate_bwd_workspace_size(rows, dim)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
-    _lib.call("sa_ssm_gate_bwd", act_dtype_code(x.dtype), _lib.ptr(dout), _lib.ptr(y32), _lib.ptr(x),
-              _lib.ptr(D32), _lib.ptr(gate), rows, dim, _lib.ptr(dy), _lib.ptr(dx), _lib.ptr(dgate),
-              _lib.ptr(dD), _lib.ptr(ws), nbytes, _lib.stream_of(x))
+    _lib.call("sa_ssm_gate_bwd", act_dtype_code(x.dtype), _lib.ptr(dout), _lib.ptr(y32),
+              1 if y_is_yd else 0, _lib.ptr(x), _lib.ptr(D32), _lib.ptr(gate), rows, dim,
+              _lib.ptr(dy), _lib.ptr(dx), _lib.ptr(dgate), _lib.ptr(dD), _lib.ptr(ws), nbytes,
+              _lib.stream_of(x))
     return dy, dx, dD, dgate

@@ -52,40 +52,8 @@ class SSDScanFn(torch.autograd.Function):
             y: (batch_size, seq_len, num_heads, head_dim)
             h_last: (batch_size, num_heads, head_dim, state_dim)
         """
-        check_ndim(u, 4, name="u")
-        check_ndim(A, 1, name="A")
-        check_ndim(B, 4, name="B")
-        check_ndim(C, 4, name="C")
-        check_ndim(delta_raw, 3, name="delta_raw")
-        check_ndim(delta_bias, 1, name="delta_bias", optional=True)
-        check_ndim(h_init, 4, name="h_init", optional=True)
-        check_ndim(length, 1, name="length", optional=True)
-
-        batch_size, seq_len, num_heads, head_dim = u.shape
-        num_groups, state_dim = B.shape[2], B.shape[3]
-
-        check_shape(A, (num_heads,), name="A")
-        check_shape(B, (batch_size, seq_len, num_groups, state_dim), name="B")
-        check_shape(C, (batch_size, seq_len, num_groups, state_dim), name="C")
-        check_shape(delta_raw, (batch_size, seq_len, num_heads), name="delta_raw")
-        check_shape(delta_bias, (num_heads,), name="delta_bias", optional=True)
-        check_shape(h_init, (batch_size, num_heads, head_dim, state_dim), name="h_init",
-                    optional=True)
-        check_shape(length, (batch_size,), name="length", optional=True)
-        if num_heads % num_groups != 0:
-            raise ValueError(f"num_heads ({num_heads}) must be a multiple of num_groups ({num_groups})")
-
-        u = to_contiguous(u)
-        A = to_contiguous(A)
-        B = to_contiguous(B)
-        C = to_contiguous(C)
-        delta_raw = to_contiguous(delta_raw)
-        delta_bias = to_contiguous(delta_bias)
-        h_init = to_contiguous(h_init)
-        length = to_contiguous(length)
-
-        if length is None:
-            length = torch.full((batch_size,), seq_len, dtype=torch.long, device=u.device)
+        u, A, B, C, delta_raw, delta_bias, h_init, length = check_scan_args(
+            u, A, B, C, delta_raw, delta_bias, h_init, length)
 
         y, h_last, saved = ssd_scan_forward(
             u, A, B, C, delta_raw, delta_bias, h_init, length,
@@ -113,3 +81,44 @@ class SSDScanFn(torch.autograd.Function):
         u_grad, A_grad, B_grad, C_grad, delta_raw_grad, delta_bias_grad, h_init_grad = grads
         return (u_grad, A_grad, B_grad, C_grad, delta_raw_grad, delta_bias_grad, h_init_grad,
                 None, None, None, None, None)
+
+
+def check_scan_args(u, A, B, C, delta_raw, delta_bias, h_init, length):
+    """The reference's validation and contiguity handling (ops/ssd_scan.py:38-68):
+    ValueError on a bad ndim / shape before any launch, contiguous copies,
+    `length` defaulting to the full sequence on the inputs' device."""
+    check_ndim(u, 4, name="u")
+    check_ndim(A, 1, name="A")
+    check_ndim(B, 4, name="B")
+    check_ndim(C, 4, name="C")
+    check_ndim(delta_raw, 3, name="delta_raw")
+    check_ndim(delta_bias, 1, name="delta_bias", optional=True)
+    check_ndim(h_init, 4, name="h_init", optional=True)
+    check_ndim(length, 1, name="length", optional=True)
+
+    batch_size, seq_len, num_heads, head_dim = u.shape
+    num_groups, state_dim = B.shape[2], B.shape[3]
+
+    check_shape(A, (num_heads,), name="A")
+    check_shape(B, (batch_size, seq_len, num_groups, state_dim), name="B")
+    check_shape(C, (batch_size, seq_len, num_groups, state_dim), name="C")
+    check_shape(delta_raw, (batch_size, seq_len, num_heads), name="delta_raw")
+    check_shape(delta_bias, (num_heads,), name="delta_bias", optional=True)
+    check_shape(h_init, (batch_size, num_heads, head_dim, state_dim), name="h_init",
+                optional=True)
+    check_shape(length, (batch_size,), name="length", optional=True)
+    if num_heads % num_groups != 0:
+        raise ValueError(f"num_heads ({num_heads}) must be a multiple of num_groups ({num_groups})")
+
+    u = to_contiguous(u)
+    A = to_contiguous(A)
+    B = to_contiguous(B)
+    C = to_contiguous(C)
+    delta_raw = to_contiguous(delta_raw)
+    delta_bias = to_contiguous(delta_bias)
+    h_init = to_contiguous(h_init)
+    length = to_contiguous(length)
+
+    if length is None:
+        length = torch.full((batch_size,), seq_len, dtype=torch.long, device=u.device)
+    return u, A, B, C, delta_raw, delta_bias, h_init, length

@@ -16,6 +16,10 @@ ops inside SSM.forward / SSM.step); they follow the reference conventions
   (modules/ssm.py:173-182); conv_ctx is updated in place.
 * SSMGateFn.apply(y, x, D, gate) -> (y + D x) silu(gate):
   modules/ssm.py:144-150 (and :200-202), in the dtype of x.
+* SSDScanGatedFn.apply(u, A, B, C, delta_raw, delta_bias, h_init, length,
+  chunk_size, use_delta_softplus, delta_limit, D, gate) -> (out, h_last):
+  the scan and the epilogue in one op (modules/ssm.py:136-150), fused into
+  the chunk scan's output stage for bf16.
 """
 from __future__ import annotations
 
@@ -122,3 +126,72 @@ class SSMGateFn(torch.autograd.Function):
         y, x, D, gate = ctx.saved_tensors
         dy, dx, dD, dgate = ssm_gate_backward(dout, y, x, D, gate)
         return dy.to(y.dtype), dx, dD.to(D.dtype), dgate.to(gate.dtype)
+
+
+class SSDScanGatedFn(torch.autograd.Function):
+    """SSDScanFn followed by the SSM epilogue, as SSM.forward runs them
+    (modules/ssm.py:136-150): out = (y + D u) silu(gate), h_last.
+
+    For bf16 activations (head_dim % 8 == 0, state_dim a multiple of 32 up to
+    256) the epilogue is fused into the chunk scan's output stage: the fp32 y
+    is never written; the scan saves yd = y + D u (bf16) for the gate's
+    backward instead.  Other inputs run the scan and SSMGateFn's kernel in
+    turn.  u is used twice (scan input and D skip); its gradient is the sum.
+    """
+
+    @staticmethod
+    def forward(ctx, u, A, B, C, delta_raw, delta_bias, h_init, length, chunk_size: int,
+                use_delta_softplus: bool, delta_limit, D, gate):
+        """
+        Args: as SSDScanFn (u (batch_size, seq_len, num_heads, head_dim), ...), plus
+            D: (num_heads * head_dim,); gate: (batch_size, seq_len, num_heads, head_dim)
+        Returns:
+            out: (batch_size, seq_len, num_heads, head_dim), dtype of u
+            h_last: (batch_size, num_heads, head_dim, state_dim) float32
+        """
+        from ..kernels.ssd_scan import gated_supported, ssd_scan_forward, ssd_scan_forward_gated
+        from .ssd_scan import check_scan_args
+        u, A, B, C, delta_raw, delta_bias, h_init, length = check_scan_args(
+            u, A, B, C, delta_raw, delta_bias, h_init, length)
+        b, L, H, P = u.shape
+        check_ndim(D, 1, name="D")
+        check_shape(D, (H * P,), name="D")
+        check_shape(gate, (b, L, H, P), name="gate")
+        gate = gate.contiguous()
+        fused = gated_supported(u.dtype, P, B.shape[3])
+        if fused:
+            out, ysave, h_last, saved = ssd_scan_forward_gated(
+                u, A, B, C, delta_raw, delta_bias, h_init, length, chunk_size,
+                use_delta_softplus, delta_limit, D, gate)
+        else:
+            y, h_last, saved = ssd_scan_forward(u, A, B, C, delta_raw, delta_bias, h_init, length,
+                                                chunk_size, use_delta_softplus, delta_limit, True,
+                                                return_saved=True)
+            out = ssm_gate_forward(y.view(b, L, H * P), u.view(b, L, H * P), D,
+                                   gate.view(b, L, H * P)).view(b, L, H, P)
+            ysave = y
+        ctx.save_for_backward(u, A, B, C, delta_raw, delta_bias, h_init, length, D, gate, ysave,
+                              *saved)
+        ctx.fused = fused
+        ctx.cfg = (chunk_size, use_delta_softplus, delta_limit)
+        return out, h_last
+
+    @staticmethod
+    def backward(ctx, dout, h_last_grad):
+        from ..kernels.ssd_scan import ssd_scan_backward
+        u, A, B, C, delta_raw, delta_bias, h_init, length, D, gate, ysave, dt, dc, states = \
+            ctx.saved_tensors
+        chunk_size, sp, limit = ctx.cfg
+        if dout is None:
+            dout = torch.zeros_like(u)
+        P = u.shape[-1]
+        dy, d_skip, dD, dgate = ssm_gate_backward(
+            dout.reshape(*u.shape[:2], -1), ysave.reshape(*u.shape[:2], -1),
+            u.reshape(*u.shape[:2], -1), D, gate.reshape(*u.shape[:2], -1), y_is_yd=ctx.fused)
+        grads = ssd_scan_backward(u, A, B, C, delta_raw, delta_bias, h_init, dy.view(u.shape),
+                                  h_last_grad, length, chunk_size, sp, limit, True,
+                                  saved=(dt, dc, states))
+        du, dA, dB, dC, ddr, dbias, dh0 = grads
+        du = du + d_skip.view(u.shape)
+        return (du, dA, dB, dC, ddr, dbias, dh0, None, None, None, None,
+                dD.to(D.dtype), dgate.view(u.shape).to(gate.dtype))

@@ -309,3 +309,59 @@ def test_ssm_block_core_chain():
     assert_parity(bd.grad, b64.grad, torch.bfloat16, "dbias")
     assert_parity(gd.grad, g64.grad, torch.bfloat16, "dgate")
     assert_parity(Dd.grad, D64.grad, torch.bfloat16, "dD")
+
+
+GATED_CASES = [
+    # bf16, head_dim 64, state_dim 64: the fused scan epilogue (y never written)
+    ("fused_bf16", torch.bfloat16, dict(b=2, L=200, H=4, P=64, N=64, G=2, lens=[200, 131]), 64),
+    # float32: the scan and the gate kernel in turn
+    ("unfused_f32", torch.float32, dict(b=2, L=90, H=2, P=24, N=40, G=1), 32),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,dtype,shape,chunk", GATED_CASES, ids=[c[0] for c in GATED_CASES])
+def test_ssd_scan_gated_parity(name, dtype, shape, chunk):
+    """SSDScanGatedFn (modules/ssm.py:136-150) against the oracle: scan,
+    (y + D u) silu(gate), and every gradient (du includes the D skip)."""
+    from oracle import ssd as ssd_ref
+    from selective_attention.kernels.ssd_scan import gated_supported
+    from selective_attention.ops import SSDScanGatedFn
+    from tests.test_ssd_fwd import make_inputs
+    print(f"ssd scan gated {name}", flush=True)
+    x = make_inputs(dtype=dtype, **shape)
+    b, L, H, P = x["u"].shape
+    N = x["B"].shape[-1]
+    assert gated_supported(dtype, P, N) == (dtype == torch.bfloat16)
+    g = torch.Generator().manual_seed(4)
+    D = torch.randn(H * P, generator=g)
+    gate = (torch.randn(b, L, H, P, generator=g) * 2).to(dtype)
+    dout = torch.randn(b, L, H, P, generator=g).to(dtype)
+    dh = torch.randn(b, H, P, N, generator=g)
+
+    names = ["u", "A", "B", "C", "delta_raw", "delta_bias", "h_init"]
+    leaves = {k: x[k].cuda().requires_grad_(True) for k in names if x[k] is not None}
+    Dd, gd = D.cuda().requires_grad_(True), gate.cuda().requires_grad_(True)
+    length = None if x["length"] is None else x["length"].cuda()
+    out, h = SSDScanGatedFn.apply(leaves["u"], leaves["A"], leaves["B"], leaves["C"],
+                                  leaves["delta_raw"], leaves.get("delta_bias"), leaves.get("h_init"),
+                                  length, chunk, True, (0.0, float("inf")), Dd, gd)
+    torch.autograd.backward([out, h], [dout.cuda(), dh.cuda()])
+    torch.cuda.synchronize()
+    assert out.dtype == dtype and h.dtype == torch.float32
+
+    y_ref, h_ref = ssd_ref.ssd_scan_forward(**x, chunk_size=chunk)
+    flat = lambda t: t.reshape(b, L, H * P)
+    out_ref = ref.gate_forward(flat(y_ref), flat(x["u"]), D, flat(gate)).reshape(b, L, H, P)
+    dy, dskip, dD, dgate = ref.gate_backward(flat(dout), flat(y_ref), flat(x["u"]), D, flat(gate))
+    grads = ssd_ref.ssd_scan_backward(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], x["delta_bias"],
+                                      x["h_init"], dy.reshape(b, L, H, P), dh, x["length"], chunk)
+    exp = dict(zip(names, grads))
+    exp["u"] = exp["u"] + dskip.reshape(b, L, H, P)
+    assert_parity(out, out_ref, dtype, "out")
+    assert_parity(h, h_ref, dtype, "h_last")
+    for k, leaf in leaves.items():
+        tol = dtype if k in ("u", "B", "C", "delta_raw") or dtype == torch.float32 else torch.bfloat16
+        assert_parity(leaf.grad, exp[k], tol, f"d{k}")
+    assert_parity(Dd.grad, dD, dtype, "dD")
+    assert_parity(gd.grad, dgate.reshape(b, L, H, P), dtype, "dgate")
