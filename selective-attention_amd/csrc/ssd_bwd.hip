@@ -657,20 +657,43 @@ __global__ __launch_bounds__(256) void chunk_dbdc_bwd_kernel(
 // ---------------------------------------------------------------------------
 // exclusive block scan of one value per thread (256 threads); returns the
 // exclusive prefix and writes the block total to *total
-__device__ __forceinline__ float block_excl_scan(float v, float* wtot, float* total) {
+// exclusive prefix sums of three values at once (one pair of barriers);
+// wt3 holds 4 waves x 3 floats
+__device__ __forceinline__ void block_excl_scan3(const float (&v)[3], float* wt3, float (&base)[3],
+                                                 float (&tot)[3]) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const float incl = wave_incl_scan(v, lane);
-  if (lane == 63) wtot[wid] = incl;
-  __syncthreads();
-  float base = incl - v;
-  float tot = 0.f;
-  for (int w = 0; w < 4; ++w) {
-    if (w < wid) base += wtot[w];
-    tot += wtot[w];
+  float incl[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    incl[i] = wave_incl_scan(v[i], lane);
+    if (lane == 63) wt3[wid * 3 + i] = incl[i];
   }
   __syncthreads();
-  *total = tot;
-  return base;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    base[i] = incl[i] - v[i];
+    tot[i] = 0.f;
+    for (int w = 0; w < 4; ++w) {
+      if (w < wid) base[i] += wt3[w * 3 + i];
+      tot[i] += wt3[w * 3 + i];
+    }
+  }
+  __syncthreads();
+}
+
+// block sums of two values at once
+__device__ __forceinline__ void block_sum2(float& a, float& b, float* wt3) {
+  a = wave_sum(a);
+  b = wave_sum(b);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) {
+    wt3[wid * 3] = a;
+    wt3[wid * 3 + 1] = b;
+  }
+  __syncthreads();
+  a = wt3[0] + wt3[3] + wt3[6] + wt3[9];
+  b = wt3[1] + wt3[4] + wt3[7] + wt3[10];
+  __syncthreads();
 }
 
 __device__ __forceinline__ float block_sum(float v, float* wtot) {
@@ -693,7 +716,7 @@ __global__ __launch_bounds__(256) void chunk_cumsum_bwd_kernel(
     const float* __restrict__ ddc_part, T* __restrict__ ddelta_raw, float* __restrict__ dA_part,
     float* __restrict__ db_part, SsdDims d, int ptiles, int ntiles, int ttiles, int rtiles,
     int per_bh, int has_init, int softplus, float lo, float hi) {
-  __shared__ float wtot[4];
+  __shared__ float wtot[4 * 3];
   const int h = blockIdx.x % d.H;
   const int c = (blockIdx.x / d.H) % d.nc;
   const int b = blockIdx.x / (d.H * d.nc);
@@ -705,17 +728,14 @@ __global__ __launch_bounds__(256) void chunk_cumsum_bwd_kernel(
   const int per = (d.Lc + 255) / 256;
   const int tb = threadIdx.x * per;
 
-  // ddc_last of this chunk (sum of the state-passing partials)
+  // every global load is issued here, ahead of the block reductions (a
+  // barrier orders memory, so loads placed after one wait for it)
   float ddc = 0.f;
   for (int k = threadIdx.x; k < per_bh; k += 256) ddc += ddc_part[bhc * per_bh + k];
-  ddc = block_sum(ddc, wtot);
-  if (!has_init && c == 0) ddc = 0.f;
-
-  float qr[4], xb[4], xc[4];
-  float sqr = 0.f, sxb = 0.f, sxc = 0.f;
+  float qr[4], xb[4], xc[4], zv[4], dtv[4], ddtd[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    qr[j] = xb[j] = xc[j] = 0.f;
+    qr[j] = xb[j] = xc[j] = zv[j] = dtv[j] = ddtd[j] = 0.f;
     const int t = tb + j;
     if (j < per && t < d.Lc) {
       float q = 0.f, x1 = 0.f, x2 = 0.f;
@@ -729,18 +749,29 @@ __global__ __launch_bounds__(256) void chunk_cumsum_bwd_kernel(
       for (int k = 0; k < rtiles && 64 * k <= t; ++k) r += rsum[(bhc * rtiles + k) * d.Lc + t];
       qr[j] = q - r;
       xb[j] = t < lim - 1 ? x1 : 0.f;
-      xc[j] = (t < lim ? x2 : 0.f) + (t == d.Lc - 1 ? ddc : 0.f);
+      xc[j] = t < lim ? x2 : 0.f;
+      if (t < lim) {
+        const long off = (static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc + t) * d.H + h;
+        zv[j] = load_f32(delta_raw + off);
+        dtv[j] = dt[crow + t];
+        for (int k = 0; k < ptiles; ++k) ddtd[j] += ddt_part[(bhc * ptiles + k) * d.Lc + t];
+      }
     }
+  }
+  // ddc_last of this chunk (sum of the state-passing partials)
+  ddc = block_sum(ddc, wtot);
+  if (!has_init && c == 0) ddc = 0.f;
+  float sqr = 0.f, sxb = 0.f, sxc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j < per && tb + j == d.Lc - 1) xc[j] += ddc;
     sqr += qr[j];
     sxb += xb[j];
     sxc += xc[j];
   }
-  float tq, tb_, tc;
-  const float eq = block_excl_scan(sqr, wtot, &tq);
-  const float eb = block_excl_scan(sxb, wtot, &tb_);
-  const float ec = block_excl_scan(sxc, wtot, &tc);
-  (void)tq;
-  (void)tb_;
+  float ex[3], tt[3];
+  block_excl_scan3({sqr, sxb, sxc}, wtot, ex, tt);
+  const float eq = ex[0], eb = ex[1], ec = ex[2], tc = tt[2];
   const float a = A[h];
   const float bias = delta_bias ? delta_bias[h] : 0.0f;
   float rq = eq, rb = eb, rc = ec;
@@ -758,22 +789,19 @@ __global__ __launch_bounds__(256) void chunk_cumsum_bwd_kernel(
         float g = 0.f;
         if (t < lim) {
           const float da = dA_intra + dA_B + dA_C;
-          float ddtd = 0.f;
-          for (int k = 0; k < ptiles; ++k) ddtd += ddt_part[(bhc * ptiles + k) * d.Lc + t];
-          const float z = load_f32(delta_raw + off) + bias;
+          const float z = zv[j] + bias;
           const float sp = softplus ? softplus20(z) : z;
-          g = da * a + ddtd;
+          g = da * a + ddtd[j];
           if (sp < lo || sp > hi) g = 0.f;
           if (softplus && z <= 20.0f) g *= sigmoidf_acc(z);
-          dA_loc += da * dt[crow + t];
+          dA_loc += da * dtv[j];
           db_loc += g;
         }
         ddelta_raw[off] = from_f32<T>(g);
       }
     }
   }
-  dA_loc = block_sum(dA_loc, wtot);
-  db_loc = block_sum(db_loc, wtot);
+  block_sum2(dA_loc, db_loc, wtot);
   if (threadIdx.x == 0) {
     dA_part[(static_cast<long>(b) * d.nc + c) * d.H + h] = dA_loc;
     db_part[(static_cast<long>(b) * d.nc + c) * d.H + h] = db_loc;
