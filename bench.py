@@ -256,6 +256,86 @@ def run_sparse(args, torch):
                          "algorithmic_flops": flops, "qk_pairs": pairs}}
 
 
+def run_selective_mha(args, torch):
+    """SelectiveMHA's attention at config 4's shapes (16 heads x 64, batch 4,
+    8192-token prefill): the gated causal prefill on the block-sparse kernel
+    (every causal block selected, log-gate as key bias, ~20 % of keys
+    dropped), then one decode step over the prefill's paged cache (append the
+    new token, attend, and take it out again so every step sees the same
+    length).  Kernel times come from HIP events on the launch stream."""
+    from selective_attention.ops.selective_mha import PagedSelectiveAttnCache, selective_mha_prefill
+    from selective_attention.profiling import kernel_timer
+
+    dev = torch.device("cuda:0")
+    b, H, L, D = 4, 16, 8192, 64
+    g = torch.Generator(device=dev).manual_seed(4)
+    rnd = lambda *shape: torch.randn(*shape, device=dev, generator=g)
+    q, k, v = (rnd(b, H, L, D).to(torch.bfloat16) for _ in range(3))
+    gate = torch.sigmoid(rnd(b, H, L) + 1.0)
+    lg = torch.log(torch.where(gate < 0.6, torch.zeros_like(gate), gate))
+
+    def prefill():
+        return selective_mha_prefill(q, k, v, lg)
+
+    steps = max(args.steps // 2, 5)
+    ms_pre = _time_events(torch, prefill, steps, max(args.warmup, 1))
+    with kernel_timer() as kt:
+        for _ in range(steps):
+            prefill()
+        torch.cuda.synchronize()
+    pre_kernels = {n: round(x["avg_us"], 2) for n, x in kt.stats.items()}
+    pairs = b * H * L * (L + 1) // 2
+    flops = 4 * D * pairs
+    sp_us = pre_kernels.get("sparse_attn_fwd", ms_pre * 1e3)
+    tf = flops / (sp_us / 1e6) / 1e12
+
+    cache = PagedSelectiveAttnCache(b, H, D, max_tokens=L + 64, device=dev)
+    cache.build(k, v, lg)
+    qt, kt_, vt = (rnd(b, H, D).to(torch.bfloat16) for _ in range(3))
+    lgt = torch.log(torch.sigmoid(rnd(b, H) + 1.0))
+
+    def step():
+        cache.append(kt_, vt, lgt)
+        o = cache.attend(qt)
+        cache.unappend()
+        return o
+
+    cache.append(kt_, vt, lgt)
+
+    def attend():
+        return cache.attend(qt)
+
+    dsteps = max(args.steps, 20)
+    ms_att = _time_events(torch, attend, dsteps, args.warmup)
+    with kernel_timer() as kt:
+        for _ in range(dsteps):
+            attend()
+        torch.cuda.synchronize()
+    dec_kernels = {n: round(x["avg_us"], 2) for n, x in kt.stats.items()}
+    cache.unappend()
+    ms_step = _time_events(torch, step, dsteps, args.warmup)
+    n = L + 1
+    dec_bytes = b * H * n * (2 * D * 2 + 4) + 2 * b * H * D * 2 + b * ((n + 63) // 64) * 4
+    gbs = dec_bytes / (ms_att / 1e3) / 1e9
+    return {
+        "prefill_us": round(ms_pre * 1e3, 1),
+        "prefill_tokens_per_s": round(b * L / (ms_pre / 1e3), 1),
+        "prefill_kernels_avg_us": pre_kernels,
+        "decode_attend_us": round(ms_att * 1e3, 1),
+        "decode_step_us": round(ms_step * 1e3, 1),
+        "decode_kernels_avg_us": dec_kernels,
+        "config": {"workload": "selective_mha_config4", "batch": b, "heads": H, "headdim": D,
+                   "prefill_len": L, "gate_threshold": 0.6, "page_size": 64},
+        "roofline": {
+            "prefill": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_DENSE_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(tf / BF16_DENSE_TFLOPS, 4),
+                        "algorithmic_flops": flops, "qk_pairs": pairs},
+            "decode_attend": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                              "algorithmic_bytes": dec_bytes}},
+    }
+
+
 def _scan_gate_fusion(args, torch):
     """SSD forward + SSM epilogue at config 1: the scan then the gate kernel
     (fp32 y written and re-read) against the epilogue fused into the chunk
@@ -439,6 +519,7 @@ def main():
         out["decode"] = run_decode(args, torch)
         out["sparse_attn"] = run_sparse(args, torch)
         out["ssm_io"] = run_ssm_io(args, torch)
+        out["selective_mha"] = run_selective_mha(args, torch)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, args.cpu_budget_s)
     if args.copy_probe_mib > 0:

@@ -14,7 +14,9 @@ Contents (each function cites the reference file:line it restates):
   attn.py  - block-sparse varlen causal attention and paged GQA decode
              attention (brute-force dense masked softmax; no reference kernel
              exists for these, the gated-softmax semantics come from
-             modules/selective_attention.py).
+             modules/selective_attention.py); SelectiveMHA's inference
+             attention (prefill in the form of the reference's compressed
+             branch, decode in mode "pos") and its log-gate.
   ssm_io.py - the SSM block's stages around the scan (modules/ssm.py):
              SiLU + causal depthwise conv prologue, its decode-time context
              (inference/ssm_cache.py), the D-skip / SiLU-gate epilogue, and
@@ -35,6 +37,11 @@ How each function is pinned (tests/test_oracle_*.py):
                   slice composition and == a brute-force loop; streaming
                   decode steps == the batch conv; context == a brute-force
                   gather; backward formulas == torch.autograd (fp64).
+  selective_mha - prefill (compressed-branch form) == the reference's other
+                  branch (full causal matrix, gate on every column, diagonal
+                  restored) on the same inputs; all gates 1 == causal SDPA;
+                  every key dropped == v; decode over keys 0..t == prefill
+                  row t.
 The reference ships no golden vectors or known-answer tests for this path
 (its one test file is an integration test that is broken as shipped), so
 nothing here is pinned against reference-produced numbers.  Rounding-level

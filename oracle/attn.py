@@ -98,3 +98,60 @@ def paged_decode_attn(q, k_pages, v_pages, page_table, seq_lens, softmax_scale=N
         p = torch.softmax(sc, dim=-1)
         o[i] = torch.einsum("hn,hnd->hd", p, V)
     return o
+
+
+
+def selective_mha_log_gate(select_gate, score_std, penalty, threshold=None, lengths=None):
+    """log_select_gate of SelectiveMHA.forward in inference
+    (modules/selective_attention.py:198-200, :259-267): gates below the
+    per-head threshold become 0; log(gate) * score_std * penalty; -inf past a
+    length.  select_gate (b, H, L); score_std, threshold (H,)."""
+    g = select_gate.to(torch.float64).clone()
+    if threshold is not None:
+        g[g < threshold.to(torch.float64)[None, :, None]] = 0.0
+    lg = torch.log(g) * score_std.to(torch.float64)[None, :, None] * penalty
+    if lengths is not None:
+        pad = torch.arange(g.shape[-1])[None, :] >= lengths.to(torch.int64)[:, None]
+        lg = lg.masked_fill(pad[:, None, :], float("-inf"))
+    return lg
+
+
+def selective_mha_prefill_ref(q_rot, k_rot, v, log_gate, lengths=None, dtype=torch.float64):
+    """SelectiveMHA.forward's inference attention (modules/selective_attention.py:
+    222-290), restated in the form of its compressed branch (_build_attn_matrix
+    :63-83, _gated_softmax :125-127, the output :279-281): query t attends the
+    keys j < t whose gate is kept (finite log_gate), each with its log_gate,
+    plus its own key without it (the self-score column).
+
+    q_rot, k_rot, v (b, H, L, D); log_gate (b, H, L) from
+    selective_mha_log_gate.  Returns (b, H, L, D); rows past a length are 0.
+    """
+    b, H, L, D = q_rot.shape
+    scale = D ** -0.5
+    q, k, vv = (t.to(dtype) for t in (q_rot, k_rot, v))
+    lg = log_gate.to(dtype)
+    lens = [L] * b if lengths is None else [int(x) for x in lengths.tolist()]
+    out = torch.zeros(b, H, L, D, dtype=dtype)
+    for i in range(b):
+        n = lens[i]
+        for h in range(H):
+            kept = torch.nonzero(torch.isfinite(lg[i, h, :n])).flatten()
+            for t in range(n):
+                js = kept[kept < t]
+                s = torch.cat([(k[i, h, js] @ q[i, h, t]) * scale + lg[i, h, js],
+                               ((q[i, h, t] @ k[i, h, t]) * scale).reshape(1)])
+                w = torch.softmax(s, 0)
+                out[i, h, t] = w[:-1] @ vv[i, h, js] + w[-1] * vv[i, h, t]
+    return out
+
+
+def selective_mha_decode_ref(q_rot, k_cache, v_cache, log_gate_cache, dtype=torch.float64):
+    """SelectiveMHA.step's attention (modules/selective_attention.py:399-405,
+    _gated_softmax mode "pos" :121-123): softmax over the cached keys with
+    the gate on every key but the newest.  q_rot (b, H, D); caches
+    (b, H, n, D) / (b, H, n).  Keys with a -inf gate drop out, as the
+    reference's compaction (_reset_cache :11-25) drops them."""
+    D = q_rot.shape[-1]
+    s = torch.einsum("bhd,bhnd->bhn", q_rot.to(dtype), k_cache.to(dtype)) * D ** -0.5
+    s[..., :-1] = s[..., :-1] + log_gate_cache[..., :-1].to(dtype)
+    return torch.einsum("bhn,bhnd->bhd", torch.softmax(s, -1), v_cache.to(dtype))

@@ -1,0 +1,224 @@
+"""SelectiveMHA's attention (inference) on the gfx950 attention ops.
+
+The reference computes SelectiveMHA's gated attention densely in torch
+(modules/selective_attention.py): _build_attn_matrix (:27-97) and
+_gated_softmax (:99-144) for prefill, SelectiveMHA.step (:392-405) over a
+per-head compacted cache (inference/selective_attn_cache.py,
+_reset_cache :11-25) for decode.  Here the same attention runs on the new
+ops:
+
+* selective_mha_prefill: each batch row is one sequence for
+  sparse_attn_varlen, with every causal block selected.  The gate
+  enters as key_bias = log_gate (the diagonal is exempt, as in mode "seq").
+  A key the reference drops from its compressed cache (gate zeroed or below
+  the threshold, or past the length) carries key_bias = -inf, which removes
+  it from the softmax exactly as compression does, while the query's own key
+  stays in unbiased (the reference's self-score column).
+* PagedSelectiveAttnCache: the decode cache as 64-token bf16 pages shared
+  by every head of a batch row, with the gate of each cached key kept as
+  key_bias pages (-inf for dropped keys; the newest key is exempt, as in
+  mode "pos").  Compaction becomes a page-table rewrite: drop_evicted_pages
+  removes pages whose keys every head has dropped, without moving data.
+
+Training (the per-head score statistics and gradients through the
+attention) is not covered: there is no attention backward kernel here.
+"""
+from __future__ import annotations
+
+import torch
+
+from .attention import paged_decode_attn, sparse_attn_varlen
+
+
+def selective_mha_prefill(q_rot: torch.Tensor, k_rot: torch.Tensor, v: torch.Tensor,
+                          log_gate: torch.Tensor, lengths: torch.Tensor | None = None,
+                          block_size: int = 64) -> torch.Tensor:
+    """
+    Args (the module's tensors after RoPE, modules/selective_attention.py:250-255):
+        q_rot, k_rot, v: (batch_size, num_heads, seq_len, head_dim) bf16; a
+            (batch_size, seq_len, num_heads, head_dim) tensor transposed to
+            this shape is read in place, any other layout is copied once
+        log_gate: (batch_size, num_heads, seq_len), log(select_gate) * score_std *
+            penalty; -inf for keys the reference drops (gate zeroed or below the
+            threshold)
+        lengths: (batch_size,) or None
+    Returns:
+        out: (batch_size, num_heads, seq_len, head_dim) bf16, a transposed view of
+        (batch_size, seq_len, num_heads, head_dim) memory (the layout the
+        module's output projection reads); rows past a length are 0.
+
+    Each batch row is one sequence of seq_len rows for the block-sparse
+    kernel (cu_seqlens = 0, L, 2L, ...).  Padding needs no packing: a query
+    t < length only reaches keys j <= t, and query blocks that lie wholly
+    past the length select no key block, so their rows come out 0.
+    """
+    b, H, L, D = q_rot.shape
+    dev = q_rot.device
+    T = b * L
+    if T == 0:
+        return torch.zeros(b, L, H, D, dtype=torch.bfloat16, device=dev).transpose(1, 2)
+
+    def rows(x):   # (b, H, L, D) -> (b * L, H, D) rows, in place when possible
+        return x.transpose(1, 2).to(torch.bfloat16).contiguous().view(T, H, D)
+
+    qp, kp, vp = rows(q_rot), rows(k_rot), rows(v)
+    bias = log_gate.to(torch.float32).transpose(0, 1).reshape(H, T)
+    nb = (L + block_size - 1) // block_size
+    cu = torch.arange(b + 1, dtype=torch.int32, device=dev) * L
+    # query block jq of row i selects key blocks 0..jq, or nothing when it
+    # starts past the row's length
+    jq = torch.arange(nb, dtype=torch.int32, device=dev)
+    m = torch.arange(nb, dtype=torch.int32, device=dev)
+    sel = torch.where(m[None, :] <= jq[:, None], m[None, :], torch.full_like(m, -1)[None, :])
+    sel = sel[None].expand(b, nb, nb)
+    if lengths is not None:
+        lens = lengths.to(dev, torch.int64).clamp(0, L)
+        live = (jq[None, :].to(torch.int64) * block_size < lens[:, None])        # (b, nb)
+        sel = torch.where(live[:, :, None], sel, torch.full_like(sel, -1))
+    block_idx = sel.reshape(1, b * nb, nb).expand(H, b * nb, nb).contiguous()
+    o = sparse_attn_varlen(qp, kp, vp, cu, block_idx, block_size, None, bias)
+    out = o.view(b, L, H, D)
+    if lengths is not None:
+        # rows past the length inside a row's last live block
+        pad = torch.arange(L, device=dev)[None, :] >= lens[:, None]
+        out.masked_fill_(pad[:, :, None, None], 0.0)
+    return out.transpose(1, 2)
+
+
+class PagedSelectiveAttnCache:
+    """Paged decode cache of SelectiveMHA (one per layer).
+
+    k / v pages: (num_pages, num_heads, page_size, head_dim) and
+    (num_pages, num_heads, head_dim, page_size) bf16; gate pages
+    (num_pages, num_heads, page_size) fp32; page_table (batch, max_pages)
+    int32 and seq_lens (batch,) int32 index them.  Pages are allocated from a
+    fixed pool; a batch row's tokens are in page order, its newest token last.
+    """
+
+    def __init__(self, batch_size: int, num_heads: int, head_dim: int, max_tokens: int,
+                 device, page_size: int = 64):
+        self.b, self.H, self.D, self.ps = batch_size, num_heads, head_dim, page_size
+        self.max_pages = (max_tokens + page_size - 1) // page_size
+        n = batch_size * self.max_pages
+        self.k_pages = torch.zeros(n, num_heads, page_size, head_dim, dtype=torch.bfloat16, device=device)
+        self.v_pages = torch.zeros(n, num_heads, head_dim, page_size, dtype=torch.bfloat16, device=device)
+        self.gate_pages = torch.full((n, num_heads, page_size), float("-inf"), dtype=torch.float32,
+                                     device=device)
+        self.free = list(range(n - 1, -1, -1))
+        self.rows = [[] for _ in range(batch_size)]   # page ids per batch row
+        self.lens = [0] * batch_size
+        self.device = device
+        # device copies of the page table and lengths, refreshed when the host
+        # bookkeeping changed since the last attend
+        self._pt = None
+        self._sl = None
+        self._pt_dirty = self._sl_dirty = True
+
+    # --- bookkeeping -------------------------------------------------------
+    def _alloc(self) -> int:
+        if not self.free:
+            raise RuntimeError("PagedSelectiveAttnCache: page pool exhausted")
+        pid = self.free.pop()
+        self.gate_pages[pid].fill_(float("-inf"))
+        return pid
+
+    def _slot(self, i: int, t: int):
+        while len(self.rows[i]) * self.ps <= t:
+            self.rows[i].append(self._alloc())
+            self._pt_dirty = True
+        return self.rows[i][t // self.ps], t % self.ps
+
+    def page_table(self) -> torch.Tensor:
+        """(batch, max_pages) int32 on the cache's device."""
+        if self._pt_dirty or self._pt is None:
+            pt = torch.zeros(self.b, self.max_pages, dtype=torch.int32)
+            for i, r in enumerate(self.rows):
+                if r:
+                    pt[i, :len(r)] = torch.tensor(r, dtype=torch.int32)
+            self._pt = pt.to(self.device)
+            self._pt_dirty = False
+        return self._pt
+
+    def seq_lens(self) -> torch.Tensor:
+        """(batch,) int32 on the cache's device."""
+        if self._sl_dirty or self._sl is None:
+            self._sl = torch.tensor(self.lens, dtype=torch.int32).to(self.device)
+            self._sl_dirty = False
+        return self._sl
+
+    # --- the reference's cache operations ------------------------------------
+    def build(self, k_rot, v, log_gate, lengths=None):
+        """SelectiveAttnCache.build_kv after prefill (selective_attn_cache.py:9-28):
+        k_rot, v (batch, heads, seq_len, head_dim); log_gate (batch, heads, seq_len)."""
+        L = k_rot.shape[2]
+        lens = [L] * self.b if lengths is None else [min(int(x), L) for x in lengths.tolist()]
+        H, D, ps = self.H, self.D, self.ps
+        for i in range(self.b):
+            for pid in self.rows[i]:
+                self.free.append(pid)
+            n = lens[i]
+            npg = (n + ps - 1) // ps
+            pids = [self._alloc() for _ in range(npg)]
+            self.rows[i] = pids
+            self.lens[i] = n
+            self._pt_dirty = self._sl_dirty = True
+            if npg == 0:
+                continue
+            idx = torch.tensor(pids, device=self.device)
+            kk = torch.zeros(H, npg * ps, D, dtype=torch.bfloat16, device=self.device)
+            vv = torch.zeros_like(kk)
+            gg = torch.full((H, npg * ps), float("-inf"), dtype=torch.float32, device=self.device)
+            kk[:, :n] = k_rot[i, :, :n]
+            vv[:, :n] = v[i, :, :n]
+            gg[:, :n] = log_gate[i, :, :n].float()
+            self.k_pages[idx] = kk.view(H, npg, ps, D).permute(1, 0, 2, 3)
+            self.v_pages[idx] = vv.view(H, npg, ps, D).permute(1, 0, 3, 2)
+            self.gate_pages[idx] = gg.view(H, npg, ps).permute(1, 0, 2)
+
+    def append(self, k_rot, v, log_gate):
+        """SelectiveAttnCache.update_kv (:30-47): one token per batch row;
+        k_rot, v (batch, heads, head_dim); log_gate (batch, heads)."""
+        slots = [self._slot(i, self.lens[i]) for i in range(self.b)]
+        idx = torch.tensor(slots, dtype=torch.int64).to(self.device)
+        pid, s = idx[:, 0], idx[:, 1]
+        self.k_pages[pid, :, s] = k_rot.to(torch.bfloat16)          # (batch, heads, head_dim)
+        self.v_pages[pid, :, :, s] = v.to(torch.bfloat16)
+        self.gate_pages[pid, :, s] = log_gate.to(torch.float32)     # (batch, heads)
+        for i in range(self.b):
+            self.lens[i] += 1
+        self._sl_dirty = True
+
+    def unappend(self, rows=None):
+        """Drop the newest token again (SelectiveMHA.step :414-415 when no head
+        keeps it)."""
+        for i in (range(self.b) if rows is None else rows):
+            self.lens[i] -= 1
+        self._sl_dirty = True
+
+    def attend(self, q_rot) -> torch.Tensor:
+        """softmax(q.k * scale + [not newest] * log_gate) v over the cached keys
+        (modules/selective_attention.py:399-405); q_rot (batch, heads, head_dim)."""
+        return paged_decode_attn(q_rot.to(torch.bfloat16).contiguous(), self.k_pages, self.v_pages,
+                                 self.page_table(), self.seq_lens(), None, self.gate_pages)
+
+    def drop_evicted_pages(self) -> int:
+        """The reference's periodic compaction (_reset_cache :11-25) as a page
+        table rewrite: every full page (not the newest one) whose keys all heads
+        have dropped (-inf gate) leaves the row's page list.  Returns the number
+        of pages freed."""
+        freed = 0
+        for i in range(self.b):
+            keep = []
+            pages = self.rows[i]
+            for p_idx, pid in enumerate(pages):
+                last = p_idx == len(pages) - 1
+                if not last and bool(torch.isinf(self.gate_pages[pid]).all()):
+                    self.free.append(pid)
+                    self.lens[i] -= self.ps
+                    freed += 1
+                else:
+                    keep.append(pid)
+            self.rows[i] = keep
+        if freed:
+            self._pt_dirty = self._sl_dirty = True
+        return freed
