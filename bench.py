@@ -336,6 +336,90 @@ def run_selective_mha(args, torch):
     }
 
 
+def run_causal_lm(args, torch, new_tokens=256):
+    """Config 4: the random-init hybrid causal LM (config4(): d_model 1024, six
+    blocks of SSD (expand 2, d_state 128, headdim 64) then selective attention
+    (16 heads x 64), vocab 32000, bf16), batch 4 prefill of 8192 uniform-random
+    tokens, then `new_tokens` greedy decode steps; attention gate threshold 0.5
+    per head (the reference's warm-up value), score statistics set to 1.
+    Prefill and decode are timed with the host clock around synchronised runs
+    (decode is host-launch bound)."""
+    from selective_attention.inference import CausalBlockCache, GenerationConfig, InferenceState
+    from selective_attention.models import CausalLM, config4
+    from selective_attention.profiling import kernel_timer
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = config4("cuda")
+    m = CausalLM(cfg)
+    with torch.no_grad():
+        for blk in m.layers:
+            blk.mha.score_std_ema.fill_(1.0)
+    m = m.to_bf16().to(dev).eval()
+    b, L = 4, 8192
+    g = torch.Generator(device=dev).manual_seed(1)
+    ids = torch.randint(10, cfg.vocab_size, (b, L), device=dev, generator=g)
+    thr = torch.full((cfg.num_layers, cfg.model_dim // cfg.head_dim), 0.5, device=dev)
+    gen = GenerationConfig(bos_token_id=-1, eos_token_id=-1, pad_token_id=0,
+                           max_new_tokens=new_tokens, attn_gate_thresholds=thr)
+    lengths = torch.full((b,), L, device=dev)
+
+    def prefill():
+        cache = [CausalBlockCache(reserve=new_tokens) for _ in m.layers]
+        h = m._hidden(ids, lengths, thr, cache)
+        return cache, m.lm_head(m.norm(h[:, -1]))
+
+    with torch.no_grad():
+        m.generate(ids[:, :512], GenerationConfig(bos_token_id=-1, eos_token_id=-1, pad_token_id=0,
+                                                  max_new_tokens=4, attn_gate_thresholds=thr))
+        prefill()
+        torch.cuda.synchronize()
+        reps = 3
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            cache, logits = prefill()
+        torch.cuda.synchronize()
+        t_pre = (time.perf_counter() - t0) / reps
+        with kernel_timer() as kt:
+            prefill()
+            torch.cuda.synchronize()
+        pre_kernels = {n: round(x["total_ms"] * 1e3, 1) for n, x in kt.stats.items()}
+        # eager decode steps (one host launch per op), for comparison
+        state = InferenceState(lengths.clone())
+        nxt = logits.argmax(-1)
+        for _ in range(4):
+            logits = m.step(nxt, cache, state, gen)
+            state.update()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(32):
+            nxt = torch.argmax(torch.softmax(logits, -1), -1)
+            logits = m.step(nxt, cache, state, gen)
+            state.update()
+        torch.cuda.synchronize()
+        t_eager = (time.perf_counter() - t0) / 32
+        del cache
+        # generate(): prefill + new_tokens greedy steps, the decode step replayed from a graph
+        t0 = time.perf_counter()
+        seq = m.generate(ids, gen)
+        torch.cuda.synchronize()
+        t_gen = time.perf_counter() - t0
+        t_dec = (t_gen - t_pre) / (new_tokens - 1)
+        assert seq.shape == (b, L + new_tokens)
+    return {"generate_s": round(t_gen, 4),
+            "tokens_per_s": round(b * (L + new_tokens) / t_gen, 1),
+            "prefill_ms": round(t_pre * 1e3, 2),
+            "prefill_tokens_per_s": round(b * L / t_pre, 1),
+            "decode_ms_per_step": round(t_dec * 1e3, 3),
+            "decode_tokens_per_s": round(b / t_dec, 1),
+            "decode_eager_ms_per_step": round(t_eager * 1e3, 3),
+            "prefill_kernel_us_total": pre_kernels,
+            "config": {"workload": "hybrid_lm_config4", "batch": b, "prompt": L,
+                       "new_tokens": new_tokens, "model_dim": cfg.model_dim,
+                       "blocks": cfg.num_layers, "mixers": "SSD, attention alternating",
+                       "vocab": cfg.vocab_size, "dtype": "bf16", "attn_gate_threshold": 0.5}}
+
+
 def _scan_gate_fusion(args, torch):
     """SSD forward + SSM epilogue at config 1: the scan then the gate kernel
     (fp32 y written and re-read) against the epilogue fused into the chunk

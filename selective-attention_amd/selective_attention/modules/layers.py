@@ -1,0 +1,84 @@
+"""Library layers of the causal LM, as the reference defines them (torch ops;
+they are not on the kernel path): RMSNorm (modules/rms_norm.py:4-44), RoPE
+(modules/rope.py:9-64), SwiGLU (modules/feed_forward.py:4-11)."""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+
+class RMSNorm(nn.Module):
+    """x * rsqrt(mean(x^2) + eps) * (1 + weight), computed in fp32 and
+    returned in the dtype of x; the weight starts at 0 (modules/rms_norm.py)."""
+
+    def __init__(self, dim: int, num_groups: int | None = None, eps: float = 1e-6,
+                 elementwise_affine: bool = True):
+        super().__init__()
+        self.eps = eps
+        self.num_groups = num_groups
+        self.elementwise_affine = elementwise_affine
+        if elementwise_affine:
+            shape = (dim,) if num_groups is None else (num_groups, dim)
+            self.weight = nn.Parameter(torch.zeros(shape))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        out = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        if self.elementwise_affine:
+            out = out * (1.0 + self.weight.float())
+        return out.type_as(x)
+
+
+def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+class RoPE(nn.Module):
+    """Rotary embedding with inverse frequencies base^(-i / (dim/2)) and the
+    angle table [theta, theta] over the head dimension (modules/rope.py)."""
+
+    def __init__(self, dim: int, base: float = 10000):
+        super().__init__()
+        assert dim % 2 == 0
+        self.dim, self.base = dim, base
+        half = dim // 2
+        inv_freq = 1.0 / (base ** (torch.arange(0, half, dtype=torch.float32) / half))
+        self.register_buffer("inv_freq", inv_freq, persistent=False)
+
+    def cos_sin(self, positions: torch.Tensor):
+        ang = positions.to(torch.float32).unsqueeze(-1) * self.inv_freq.unsqueeze(0)
+        ang = torch.cat([ang, ang], dim=-1)
+        return torch.cos(ang), torch.sin(ang)
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor, mode: str = "seq"):
+        """mode "seq": q, k (batch, heads, seq_len, head_dim), positions (seq_len,);
+        mode "pos": q, k (batch, heads, head_dim), positions (batch,)."""
+        cos, sin = self.cos_sin(positions)
+        if mode == "seq":
+            cos, sin = cos[None, None], sin[None, None]
+        else:
+            cos, sin = cos[:, None], sin[:, None]
+        return q * cos + _rotate_half(q) * sin, k * cos + _rotate_half(k) * sin
+
+    def rotate_rows(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        """x (batch, seq_len, heads, head_dim) with positions (seq_len,): the
+        "seq" rotation applied in the (batch, seq_len, heads, head_dim) layout
+        the projections produce, in fp32."""
+        cos, sin = self.cos_sin(positions)
+        cos, sin = cos[None, :, None], sin[None, :, None]
+        return x * cos + _rotate_half(x) * sin
+
+
+class SwiGLU(nn.Module):
+    """out(w1(x) * silu(w2(x))) (modules/feed_forward.py)."""
+
+    def __init__(self, dim: int, hidden_dim: int):
+        super().__init__()
+        self.w1 = nn.Linear(dim, hidden_dim)
+        self.w2 = nn.Linear(dim, hidden_dim)
+        self.out = nn.Linear(hidden_dim, dim)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.out(self.w1(x) * F.silu(self.w2(x)))

@@ -1,0 +1,142 @@
+"""SelectiveMHA (modules/selective_attention.py:146-446), inference, on the
+gfx950 attention ops.
+
+Parameters and interfaces follow the reference.  Prefill runs
+selective_mha_prefill (the block-sparse kernel over every causal block with
+the log-gate as key bias) and fills the paged cache; step appends to the
+paged cache and runs the paged decode kernel.  A key whose gate is zeroed
+(below the threshold, or past a length) enters as key bias -inf: the
+reference's compression of the cache (its compressed branch, :63-83) drops
+exactly those keys.  Writing the drop as -inf directly, instead of
+log(0) * score_std * penalty, also keeps a zero score_std_ema (its value
+before any training step) from turning dropped keys into NaN.
+
+The training forward (per-head score statistics and gradients through the
+attention) needs an attention backward kernel, which this package does not
+have: forward() in training mode raises NotImplementedError.  Only the
+causal variant is provided.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from ..ops.selective_mha import selective_mha_prefill
+from .layers import RoPE
+
+
+def _threshold(thr, num_heads: int, device):
+    if thr is None:
+        return None
+    if isinstance(thr, (int, float)):
+        return torch.full((num_heads,), float(thr), device=device)
+    return torch.as_tensor(thr, device=device).reshape(num_heads)
+
+
+class SelectiveMHA(nn.Module):
+    def __init__(self, layer_idx: int, dim: int, head_dim: int, log_gate_penalty: float,
+                 is_causal: bool = True):
+        super().__init__()
+        if not is_causal:
+            raise NotImplementedError("SelectiveMHA: only the causal variant is built")
+        self.layer_idx = layer_idx
+        assert dim % head_dim == 0
+        self.dim = dim
+        self.num_heads = dim // head_dim
+        self.head_dim = head_dim
+        self.is_causal = is_causal
+        self.scale = head_dim ** -0.5
+        self.log_gate_penalty = log_gate_penalty
+
+        self.gate_proj = nn.Linear(dim, self.num_heads + dim)
+        self.rope = RoPE(head_dim)
+        self.q_proj = nn.Linear(dim, dim, bias=False)
+        self.k_proj = nn.Linear(dim, dim, bias=False)
+        self.v_proj = nn.Linear(dim, dim)
+        self.out_proj = nn.Linear(dim, dim)
+        self.register_buffer("score_std_ema", torch.zeros(self.num_heads))
+        nn.init.constant_(self.gate_proj.bias, 2.0)
+
+    def _gates(self, hidden_states):
+        gate = torch.sigmoid(self.gate_proj(hidden_states))
+        return torch.split(gate, [self.num_heads, self.dim], dim=-1)
+
+    def _log_gate(self, select_gate, kept):
+        """log(gate) * score_std_ema * penalty where kept, -inf elsewhere;
+        select_gate (batch, heads[, seq_len]) -> float32."""
+        std = self.score_std_ema.float()
+        std = std[None, :, None] if select_gate.dim() == 3 else std[None, :]
+        lg = torch.log(select_gate.float()) * std * self.log_gate_penalty
+        return torch.where(kept, lg, torch.full_like(lg, float("-inf")))
+
+    def forward(self, hidden_states: torch.Tensor, lengths: torch.Tensor | None = None,
+                attn_gate_threshold: torch.Tensor | None = None, cache=None,
+                analysis_cfg=None, stats=None):
+        """
+        Args:
+            hidden_states: (batch_size, seq_len, dim)
+            lengths: (batch_size,)
+            attn_gate_threshold: (num_heads,) or a float
+            cache: SelectiveAttnCache filled for decoding, or None
+        Returns:
+            hidden_states: (batch_size, seq_len, dim)
+        """
+        if self.training:
+            raise NotImplementedError(
+                "SelectiveMHA: the training forward needs an attention backward kernel, "
+                "which is not built; use eval() for inference")
+        b, L, _ = hidden_states.shape
+        dev = hidden_states.device
+        H, D = self.num_heads, self.head_dim
+        select_gate, out_gate = self._gates(hidden_states)
+        select_gate = select_gate.transpose(1, 2)                     # (b, H, L)
+        thr = _threshold(attn_gate_threshold, H, dev)
+        kept = select_gate > 0.0
+        if thr is not None:
+            kept &= select_gate >= thr[None, :, None]
+        if lengths is not None:
+            lens = lengths.to(dev)
+            kept &= (torch.arange(L, device=dev)[None, :] < lens[:, None])[:, None, :]
+        v = self.v_proj(hidden_states)
+        if not bool(kept.any()):
+            # every key dropped: each query attends only itself (:208-209)
+            return self.out_proj(v * out_gate)
+        pos = torch.arange(L, device=dev)
+        q = self.rope.rotate_rows(self.q_proj(hidden_states).view(b, L, H, D), pos)
+        k = self.rope.rotate_rows(self.k_proj(hidden_states).view(b, L, H, D), pos)
+        q = q.to(torch.bfloat16).transpose(1, 2)                      # (b, H, L, D) views
+        k = k.to(torch.bfloat16).transpose(1, 2)
+        vh = v.view(b, L, H, D).to(torch.bfloat16).transpose(1, 2)
+        log_gate = self._log_gate(select_gate, kept)
+        out = selective_mha_prefill(q, k, vh, log_gate, lengths)
+        if cache is not None:
+            cache.build_kv(k, vh, log_gate, lengths)
+        out = out.transpose(1, 2).reshape(b, L, self.dim).to(hidden_states.dtype)
+        return self.out_proj(out * out_gate)
+
+    def step(self, hidden_states: torch.Tensor, cache, state, gen_cfg, analysis_cfg=None,
+             stats=None):
+        """hidden_states (batch_size, dim) -> (batch_size, dim).  The new key
+        always gets a slot; when no head of any row keeps it, its gate is -inf
+        everywhere and it takes no weight in later steps, which is what the
+        reference's write_idx rollback (:414-415) achieves."""
+        b = hidden_states.shape[0]
+        dev = hidden_states.device
+        H, D = self.num_heads, self.head_dim
+        thr = None
+        if gen_cfg.attn_gate_thresholds is not None:
+            thr = _threshold(gen_cfg.attn_gate_thresholds[self.layer_idx], H, dev)
+        if state.step % gen_cfg.cache_update_interval == 0:
+            cache.compact()
+        select_gate, out_gate = self._gates(hidden_states)             # (b, H), (b, dim)
+        kept = select_gate > 0.0
+        if thr is not None:
+            kept &= select_gate >= thr[None, :]
+        log_gate = self._log_gate(select_gate, kept)
+        q = self.q_proj(hidden_states).view(b, H, D)
+        k = self.k_proj(hidden_states).view(b, H, D)
+        v = self.v_proj(hidden_states).view(b, H, D)
+        q, k = self.rope(q, k, state.lengths.to(dev), mode="pos")
+        cache.update_kv(k.to(torch.bfloat16), v.to(torch.bfloat16), log_gate)
+        out = cache.attend(q.to(torch.bfloat16)).reshape(b, self.dim).to(hidden_states.dtype)
+        return self.out_proj(out * out_gate)

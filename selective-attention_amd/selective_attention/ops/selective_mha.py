@@ -96,9 +96,10 @@ class PagedSelectiveAttnCache:
     """
 
     def __init__(self, batch_size: int, num_heads: int, head_dim: int, max_tokens: int,
-                 device, page_size: int = 64):
+                 device, page_size: int = 64, grow: bool = False):
         self.b, self.H, self.D, self.ps = batch_size, num_heads, head_dim, page_size
-        self.max_pages = (max_tokens + page_size - 1) // page_size
+        self.grow = grow
+        self.max_pages = max(1, (max_tokens + page_size - 1) // page_size)
         n = batch_size * self.max_pages
         self.k_pages = torch.zeros(n, num_heads, page_size, head_dim, dtype=torch.bfloat16, device=device)
         self.v_pages = torch.zeros(n, num_heads, head_dim, page_size, dtype=torch.bfloat16, device=device)
@@ -113,11 +114,32 @@ class PagedSelectiveAttnCache:
         self._pt = None
         self._sl = None
         self._pt_dirty = self._sl_dirty = True
+        # device mode (see enter_device_mode): lengths live on the device
+        self.lens_dev = None
 
     # --- bookkeeping -------------------------------------------------------
+    def _grow(self):
+        """Double the page pool (rows keep their page ids; the page table gets
+        twice the columns)."""
+        n = self.k_pages.shape[0]
+        dev = self.device
+
+        def bigger(t, fill):
+            out = torch.full((2 * n,) + tuple(t.shape[1:]), fill, dtype=t.dtype, device=dev)
+            out[:n] = t
+            return out
+        self.k_pages = bigger(self.k_pages, 0)
+        self.v_pages = bigger(self.v_pages, 0)
+        self.gate_pages = bigger(self.gate_pages, float("-inf"))
+        self.free = list(range(2 * n - 1, n - 1, -1)) + self.free
+        self.max_pages *= 2
+        self._pt_dirty = True
+
     def _alloc(self) -> int:
         if not self.free:
-            raise RuntimeError("PagedSelectiveAttnCache: page pool exhausted")
+            if not self.grow:
+                raise RuntimeError("PagedSelectiveAttnCache: page pool exhausted")
+            self._grow()
         pid = self.free.pop()
         self.gate_pages[pid].fill_(float("-inf"))
         return pid
@@ -129,9 +151,10 @@ class PagedSelectiveAttnCache:
         return self.rows[i][t // self.ps], t % self.ps
 
     def page_table(self) -> torch.Tensor:
-        """(batch, max_pages) int32 on the cache's device."""
+        """(batch, pages) int32 on the cache's device (at least max_pages columns)."""
         if self._pt_dirty or self._pt is None:
-            pt = torch.zeros(self.b, self.max_pages, dtype=torch.int32)
+            width = max([self.max_pages] + [len(r) for r in self.rows])
+            pt = torch.zeros(self.b, width, dtype=torch.int32)
             for i, r in enumerate(self.rows):
                 if r:
                     pt[i, :len(r)] = torch.tensor(r, dtype=torch.int32)
@@ -141,6 +164,8 @@ class PagedSelectiveAttnCache:
 
     def seq_lens(self) -> torch.Tensor:
         """(batch,) int32 on the cache's device."""
+        if self.lens_dev is not None:
+            return self.lens_dev
         if self._sl_dirty or self._sl is None:
             self._sl = torch.tensor(self.lens, dtype=torch.int32).to(self.device)
             self._sl_dirty = False
@@ -175,9 +200,40 @@ class PagedSelectiveAttnCache:
             self.v_pages[idx] = vv.view(H, npg, ps, D).permute(1, 0, 3, 2)
             self.gate_pages[idx] = gg.view(H, npg, ps).permute(1, 0, 2)
 
+    # --- device mode: appends without host work, for graph capture ---------
+    def enter_device_mode(self, extra_tokens: int):
+        """Give every row pages for `extra_tokens` more tokens, fix the page
+        table, and keep the lengths on the device: append / unappend / attend
+        then make no host round trip and no allocation that depends on host
+        state, so a decode step can be captured in a graph and replayed.  At
+        most `extra_tokens` appends may follow (a row that runs past its pages
+        writes into its last page instead of faulting)."""
+        if extra_tokens > 0:
+            for i in range(self.b):
+                self._slot(i, self.lens[i] + extra_tokens - 1)
+        self.page_table()
+        self.lens_dev = torch.tensor(self.lens, dtype=torch.int32).to(self.device)
+        self._rows_dev = torch.arange(self.b, device=self.device)
+
+    def exit_device_mode(self):
+        self.lens = [int(x) for x in self.lens_dev.tolist()]
+        self.lens_dev = None
+        self._sl_dirty = True
+
+    def _append_device(self, k_rot, v, log_gate):
+        col = torch.clamp(self.lens_dev // self.ps, max=self._pt.shape[1] - 1).long()
+        pid = self._pt[self._rows_dev, col].long()
+        s = (self.lens_dev % self.ps).long()
+        self.k_pages[pid, :, s] = k_rot.to(torch.bfloat16)
+        self.v_pages[pid, :, :, s] = v.to(torch.bfloat16)
+        self.gate_pages[pid, :, s] = log_gate.to(torch.float32)
+        self.lens_dev += 1
+
     def append(self, k_rot, v, log_gate):
         """SelectiveAttnCache.update_kv (:30-47): one token per batch row;
         k_rot, v (batch, heads, head_dim); log_gate (batch, heads)."""
+        if self.lens_dev is not None:
+            return self._append_device(k_rot, v, log_gate)
         slots = [self._slot(i, self.lens[i]) for i in range(self.b)]
         idx = torch.tensor(slots, dtype=torch.int64).to(self.device)
         pid, s = idx[:, 0], idx[:, 1]
@@ -191,6 +247,12 @@ class PagedSelectiveAttnCache:
     def unappend(self, rows=None):
         """Drop the newest token again (SelectiveMHA.step :414-415 when no head
         keeps it)."""
+        if self.lens_dev is not None:
+            if rows is None:
+                self.lens_dev -= 1
+            else:
+                self.lens_dev[torch.as_tensor(list(rows), device=self.device)] -= 1
+            return
         for i in (range(self.b) if rows is None else rows):
             self.lens[i] -= 1
         self._sl_dirty = True
@@ -205,7 +267,9 @@ class PagedSelectiveAttnCache:
         """The reference's periodic compaction (_reset_cache :11-25) as a page
         table rewrite: every full page (not the newest one) whose keys all heads
         have dropped (-inf gate) leaves the row's page list.  Returns the number
-        of pages freed."""
+        of pages freed (0 in device mode, where the page table is fixed)."""
+        if self.lens_dev is not None:
+            return 0
         freed = 0
         for i in range(self.b):
             keep = []
