@@ -604,6 +604,7 @@ def main():
         out["sparse_attn"] = run_sparse(args, torch)
         out["ssm_io"] = run_ssm_io(args, torch)
         out["selective_mha"] = run_selective_mha(args, torch)
+        out["causal_lm"] = run_causal_lm(args, torch)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, args.cpu_budget_s)
     if args.copy_probe_mib > 0:
