@@ -127,6 +127,30 @@ int sa_sparse_attn_fwd(int dtype, const void* q, const void* k, const void* v,
                        int total_tokens, int num_heads, int head_dim, float softmax_scale, void* o,
                        void* stream);
 
+/*
+ * Dense varlen attention (prefill), bfloat16, in three modes:
+ *   mode 0  causal self-attention: query i of a sequence sees keys j <= i;
+ *           the key bias is not applied on j = i (SelectiveMHA, is_causal,
+ *           modules/selective_attention.py:27-144, mode "seq")
+ *   mode 1  bidirectional self-attention: every key of the sequence, bias not
+ *           applied on j = i (SelectiveMHA with is_causal=False, the encoder
+ *           blocks of modules/bi_block.py:51-94; self mask :84-86)
+ *   mode 2  cross-attention: query i of sequence s sees every key of the key
+ *           sequence cu_seqlens_k[s]..cu_seqlens_k[s+1]; the bias is not
+ *           applied on its key 0 (CrossSelectiveMHA,
+ *           modules/cross_selective_attention.py:63-157)
+ * No counterpart kernel in the reference (its attention is dense torch).
+ *   q, o: (total_q, num_heads, head_dim); k, v: (total_k, num_heads, head_dim)
+ *   bf16, head_dim in {64,128}; cu_seqlens_q / _k: (num_seqs+1,) int32
+ *   (cu_seqlens_k only read in mode 2; modes 0 and 1 need total_k == total_q);
+ *   key_bias: (num_heads, total_k) f32 or NULL; softmax_scale <= 0 selects
+ *   1/sqrt(head_dim).  A query with no key gets zeros.
+ */
+int sa_attn_varlen_fwd(int dtype, int mode, const void* q, const void* k, const void* v,
+                       const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int num_seqs,
+                       const float* key_bias, int total_q, int total_k, int num_heads, int head_dim,
+                       float softmax_scale, void* o, void* stream);
+
 /* Workspace bytes of sa_paged_decode_fwd: segment partials for
  * batch * num_kv_heads + 8192 segments, plus a per-row tile prefix sum. */
 size_t sa_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,

@@ -155,3 +155,38 @@ def selective_mha_decode_ref(q_rot, k_cache, v_cache, log_gate_cache, dtype=torc
     s = torch.einsum("bhd,bhnd->bhn", q_rot.to(dtype), k_cache.to(dtype)) * D ** -0.5
     s[..., :-1] = s[..., :-1] + log_gate_cache[..., :-1].to(dtype)
     return torch.einsum("bhn,bhnd->bhd", torch.softmax(s, -1), v_cache.to(dtype))
+
+
+def attn_varlen(q, k, v, cu_q, mode="causal", cu_k=None, key_bias=None, softmax_scale=None,
+                dtype=torch.float64):
+    """Dense varlen attention in three modes (the attention of SelectiveMHA
+    is_causal=True / False, modules/selective_attention.py:27-144, and of
+    CrossSelectiveMHA, modules/cross_selective_attention.py:100-157):
+      causal  query i sees keys j <= i of its sequence, bias not on j = i
+      full    every key of its sequence, bias not on j = i
+      cross   every key of cu_k[s]..cu_k[s+1], bias not on that range's key 0
+    q (Tq, H, D); k, v (Tk, H, D); key_bias (H, Tk) or None.  Returns (Tq, H, D);
+    a query with no key gets zeros."""
+    Tq, H, D = q.shape
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
+    cq = [int(x) for x in cu_q.tolist()]
+    ck = cq if mode != "cross" else [int(x) for x in cu_k.tolist()]
+    qf, kf, vf = q.to(dtype), k.to(dtype), v.to(dtype)
+    o = torch.zeros((Tq, H, D), dtype=dtype)
+    for s in range(len(cq) - 1):
+        a, b, ka, kb = cq[s], cq[s + 1], ck[s], ck[s + 1]
+        n, nk = b - a, kb - ka
+        if n <= 0 or nk <= 0:
+            continue
+        qi = torch.arange(n)[:, None]
+        kj = torch.arange(nk)[None, :]
+        allow = (kj <= qi) if mode == "causal" else torch.ones(n, nk, dtype=torch.bool)
+        exempt = (kj == 0).expand(n, nk) if mode == "cross" else (kj == qi)
+        for h in range(H):
+            sc = (qf[a:b, h] @ kf[ka:kb, h].T) * scale
+            if key_bias is not None:
+                bias = key_bias[h, ka:kb].to(dtype)[None, :].expand(n, nk)
+                sc = sc + torch.where(exempt, torch.zeros_like(bias), bias)
+            sc = sc.masked_fill(~allow, float("-inf"))
+            o[a:b, h] = torch.softmax(sc, dim=-1) @ vf[ka:kb, h]
+    return o

@@ -143,11 +143,20 @@ __device__ __forceinline__ void softmax_lazy(v4f (&s)[KT], v4f (&o)[DT], float& 
   l += sum;
 }
 
-template <int D, bool BIAS>
+// MODE (which keys a query sees, and which key is exempt from the bias):
+//   kCausalSelf  keys j <= i of the query's own sequence; j = i exempt
+//   kFullSelf    every key of the query's own sequence;  j = i exempt
+//   kCross       every key of the sequence's key range cu_k[s]..cu_k[s+1]
+//                (k, v, key_bias indexed by key token); key 0 exempt
+// block_idx == nullptr selects every key block the mode admits (dense).
+constexpr int kCausalSelf = 0, kFullSelf = 1, kCross = 2;
+
+template <int D, bool BIAS, int MODE>
 __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const int32_t* __restrict__ cu, int nseq, const int32_t* __restrict__ block_idx, int n_qblk,
-    int max_blocks, const float* __restrict__ key_bias, bf16* __restrict__ o, int T, int H,
+    const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_k, int nseq,
+    const int32_t* __restrict__ block_idx, int n_qblk, int max_blocks,
+    const float* __restrict__ key_bias, bf16* __restrict__ o, int T, int Tk, int H,
     float scale_log2) {
   constexpr int BS = 64;
   using SM = SparseSmem<D>;
@@ -163,7 +172,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
   // locate the query block's sequence (q blocks are numbered sequence by
   // sequence): 64 sequences per step, one per lane, a prefix sum of their
   // block counts and a ballot for the one holding block gq
-  int start = 0, n = 0, jq = -1;
+  int start = 0, n = 0, jq = -1, seq = 0;
   for (int s0 = 0, first = 0; s0 < nseq && jq < 0; s0 += 64) {
     const int si = s0 + lane;
     int a = 0, nb = 0, len = 0;
@@ -185,16 +194,23 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
       start = __builtin_amdgcn_readlane(a, L);
       n = __builtin_amdgcn_readlane(len, L);
       jq = gq - __builtin_amdgcn_readlane(excl, L);
+      seq = s0 + L;
     }
     first += __builtin_amdgcn_readlane(incl, 63);
   }
   if (jq < 0) return;  // more query blocks than the packing holds
+  // the key range: the query's own sequence, or its key sequence for kCross
+  int kstart = start, nks = n;
+  if constexpr (MODE == kCross) {
+    kstart = min(max(cu_k[seq], 0), Tk);
+    nks = min(max(cu_k[seq + 1], kstart), Tk) - kstart;
+  }
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qh = w & 1, kh = w >> 1;
   const int c = lane & 15, g = lane >> 4;
   const long rs = static_cast<long>(H) * D;
-  const bf16* kbase = k + static_cast<long>(start) * rs + static_cast<long>(h) * D;
-  const bf16* vbase = v + static_cast<long>(start) * rs + static_cast<long>(h) * D;
+  const bf16* kbase = k + static_cast<long>(kstart) * rs + static_cast<long>(h) * D;
+  const bf16* vbase = v + static_cast<long>(kstart) * rs + static_cast<long>(h) * D;
 
   // this lane's two query columns (16-query tiles jt = 0, 1 of the wave's 32 rows)
   int qloc[2];
@@ -207,39 +223,45 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     for (int ks = 0; ks < KS; ++ks)
       qf[jt][ks] = qloc[jt] < n ? load_v8bf(qrow + 32 * ks + 8 * g) : zero_v8bf();
   }
-  const float* bias = BIAS ? key_bias + static_cast<long>(h) * T + start : nullptr;
+  const float* bias = BIAS ? key_bias + static_cast<long>(h) * Tk + kstart : nullptr;
   // the whole query block is inside the sequence: only the diagonal block needs masks
   const bool qfull = (jq + 1) * BS <= n;
 
-  // the selected blocks that are inside the sequence and causally visible, in order
-  const int32_t* sel = block_idx + (static_cast<long>(h) * n_qblk + gq) * max_blocks;
-  const int nkb = (n + BS - 1) / BS;
-  const bool simple = max_blocks <= 64;
+  // the selected blocks that are inside the key range (and causally visible
+  // for kCausalSelf), in order; dense: slots are the blocks themselves
+  const bool dense = block_idx == nullptr;
+  const int nkb = (nks + BS - 1) / BS;
+  const int nslot = dense ? (MODE == kCausalSelf ? min(jq + 1, nkb) : nkb) : max_blocks;
+  const int32_t* sel = dense ? nullptr : block_idx + (static_cast<long>(h) * n_qblk + gq) * max_blocks;
+  const bool simple = !dense && max_blocks <= 64;
   int my_kb = -1;
   uint64_t vmask = 0;
   if (simple) {
     my_kb = lane < max_blocks ? sel[lane] : -1;
-    vmask = __ballot(my_kb >= 0 && my_kb < nkb && my_kb <= jq);
+    vmask = __ballot(my_kb >= 0 && my_kb < nkb && (MODE != kCausalSelf || my_kb <= jq));
   }
-  auto next_valid = [&](int e) -> int {   // first valid slot >= e, or max_blocks
+  auto next_valid = [&](int e) -> int {   // first valid slot >= e, or nslot
+    if (dense) return min(e, nslot);
     if (simple) {
       const uint64_t mm = e >= 64 ? 0ull : (vmask >> e);
       return mm ? e + __builtin_ctzll(mm) : max_blocks;
     }
     for (; e < max_blocks; ++e) {
       const int kb = sel[e];
-      if (kb >= 0 && kb < nkb && kb <= jq) return e;
+      if (kb >= 0 && kb < nkb && (MODE != kCausalSelf || kb <= jq)) return e;
     }
     return max_blocks;
   };
-  auto block_of = [&](int e) -> int { return simple ? __builtin_amdgcn_readlane(my_kb, e) : sel[e]; };
+  auto block_of = [&](int e) -> int {
+    return dense ? e : simple ? __builtin_amdgcn_readlane(my_kb, e) : sel[e];
+  };
 
   // DMA of block kb into a stage: lane l of this wave's instruction i fills
   // tile bytes 1024 (IPW w + i) + 16 l, i.e. row `row`, stored chunk `ch`,
   // which holds logical chunk ch ^ k_swz(row) (K) or ch ^ v_swz(row) (V).  Rows past the sequence
   // repeat its last key (their scores are masked to -inf, so p = 0).
   auto issue_kv = [&](int kb, int stage) {
-    const int k0 = kb * BS, nk = min(BS, n - k0);
+    const int k0 = kb * BS, nk = min(BS, nks - k0);
     bf16* Kt = sm + stage * 2 * SM::tile;
     bf16* Vt = Kt + SM::tile;
     const bf16* kb0 = kbase + static_cast<long>(k0) * rs;
@@ -279,20 +301,20 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
 
   int e = next_valid(0);
   int stage = 0;
-  if (e < max_blocks) issue_kv(block_of(e), 0);
-  while (e < max_blocks) {
+  if (e < nslot) issue_kv(block_of(e), 0);
+  while (e < nslot) {
     const int kb = block_of(e);
     const int en = next_valid(e + 1);
     const int k0 = kb * BS;
-    const int nk = min(BS, n - k0);
+    const int nk = min(BS, nks - k0);
     // bias of the wave's keys 32 kh + 8g + 0..7 (issued before the next DMA, so
     // the wait below covers it)
     float bk[8];
     if constexpr (BIAS) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) bk[i] = bias[min(k0 + 32 * kh + 8 * g + i, n - 1)];
+      for (int i = 0; i < 8; ++i) bk[i] = bias[min(k0 + 32 * kh + 8 * g + i, nks - 1)];
     }
-    if (en < max_blocks) {
+    if (en < nslot) {
       issue_kv(block_of(en), stage ^ 1);
       __builtin_amdgcn_s_waitcnt(vm_wait<2 * IPW>());   // this block's tiles have landed
     } else {
@@ -318,8 +340,13 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
         for (int jt = 0; jt < 2; ++jt) sc[jt][u2] = mfma_bf16(kf, qf[jt][ks], sc[jt][u2]);
       }
     }
-    // scale; bias (not on the diagonal) and causal / length masks where needed
-    const bool interior = kb < jq && qfull;
+    // scale; bias (not on the exempt key) and causal / length masks where needed.
+    // Interior blocks (no mask, no exempt key): for kCausalSelf the blocks
+    // before the diagonal; otherwise full key blocks other than the one
+    // holding the exempt key (the diagonal block, or block 0 for kCross)
+    const bool interior = MODE == kCausalSelf
+                              ? (kb < jq && qfull)
+                              : (qfull && k0 + BS <= nks && kb != (MODE == kCross ? 0 : jq));
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) {
 #pragma unroll
@@ -329,8 +356,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
           const int kl = key_of_row(2 * kh + u2, 4 * g + i);   // = 32 kh + 8g + 4 u2 + i
           const int key = k0 + kl;
           float val = sc[jt][u2][i] * scale_log2;
-          if constexpr (BIAS) val += (interior || key != qloc[jt]) ? bk[4 * u2 + i] * kLog2e : 0.f;
-          if (!interior) val = (kl < nk && key <= qloc[jt] && qloc[jt] < n) ? val : kNegInf;
+          const bool exempt = MODE == kCross ? key == 0 : key == qloc[jt];
+          if constexpr (BIAS) val += (interior || !exempt) ? bk[4 * u2 + i] * kLog2e : 0.f;
+          if (!interior)
+            val = (kl < nk && (MODE != kCausalSelf || key <= qloc[jt]) && qloc[jt] < n) ? val : kNegInf;
           sc[jt][u2][i] = val;
         }
       softmax_lazy<2, DT>(sc[jt], acc[jt], m[jt], l[jt]);
@@ -402,11 +431,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
 }
 
 // raise the kernel's dynamic LDS limit once per process (D = 128 needs 64 KB)
-template <int D, bool BIAS>
+template <int D, bool BIAS, int MODE>
 int sparse_smem_attr() {
   static bool done = false;
   if (!done) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_attn_fwd_kernel<D, BIAS>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_attn_fwd_kernel<D, BIAS, MODE>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(SparseSmem<D>::bytes));
     SA_CHECK_ARG(e == hipSuccess, "sa_sparse_attn_fwd: %zu B of LDS refused: %s",
@@ -416,17 +445,45 @@ int sparse_smem_attr() {
   return 0;
 }
 
-template <int D, bool BIAS>
-int launch_sparse(const void* q, const void* k, const void* v, const int32_t* cu, int nseq,
-                  const int32_t* block_idx, int n_qblk, int max_blocks, const float* key_bias,
-                  void* o, int T, int H, float scale_log2, long blocks, hipStream_t s) {
-  if (sparse_smem_attr<D, BIAS>()) return 1;
-  ProfScope prof_("sparse_attn_fwd", s);
-  hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, BIAS>), dim3(blocks), dim3(256), SparseSmem<D>::bytes,
-                     s, static_cast<const bf16*>(q), static_cast<const bf16*>(k),
-                     static_cast<const bf16*>(v), cu, nseq, block_idx, n_qblk, max_blocks, key_bias,
-                     static_cast<bf16*>(o), T, H, scale_log2);
+template <int D, bool BIAS, int MODE>
+int launch_sparse(const void* q, const void* k, const void* v, const int32_t* cu,
+                  const int32_t* cu_k, int nseq, const int32_t* block_idx, int n_qblk,
+                  int max_blocks, const float* key_bias, void* o, int T, int Tk, int H,
+                  float scale_log2, long blocks, hipStream_t s) {
+  if (sparse_smem_attr<D, BIAS, MODE>()) return 1;
+  ProfScope prof_(MODE == kCausalSelf ? "sparse_attn_fwd" : MODE == kFullSelf ? "attn_full_fwd" : "attn_cross_fwd", s);
+  hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, BIAS, MODE>), dim3(blocks), dim3(256),
+                     SparseSmem<D>::bytes, s, static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                     static_cast<const bf16*>(v), cu, cu_k, nseq, block_idx, n_qblk, max_blocks,
+                     key_bias, static_cast<bf16*>(o), T, Tk, H, scale_log2);
   return 0;
+}
+
+template <int D, int MODE>
+int launch_attn_d(const void* q, const void* k, const void* v, const int32_t* cu,
+                  const int32_t* cu_k, int nseq, const int32_t* block_idx, int n_qblk,
+                  int max_blocks, const float* key_bias, void* o, int T, int Tk, int H,
+                  float scale_log2, long blocks, hipStream_t s) {
+  return key_bias ? launch_sparse<D, true, MODE>(q, k, v, cu, cu_k, nseq, block_idx, n_qblk, max_blocks,
+                                                 key_bias, o, T, Tk, H, scale_log2, blocks, s)
+                  : launch_sparse<D, false, MODE>(q, k, v, cu, cu_k, nseq, block_idx, n_qblk,
+                                                  max_blocks, key_bias, o, T, Tk, H, scale_log2, blocks, s);
+}
+
+int launch_attn(int mode, int D, const void* q, const void* k, const void* v, const int32_t* cu,
+                const int32_t* cu_k, int nseq, const int32_t* block_idx, int n_qblk, int max_blocks,
+                const float* key_bias, void* o, int T, int Tk, int H, float scale_log2, long blocks,
+                hipStream_t s) {
+#define SA_ATTN_ARGS q, k, v, cu, cu_k, nseq, block_idx, n_qblk, max_blocks, key_bias, o, T, Tk, H, scale_log2, blocks, s
+  if (D == 128) {
+    if (mode == kCausalSelf) return launch_attn_d<128, kCausalSelf>(SA_ATTN_ARGS);
+    if (mode == kFullSelf) return launch_attn_d<128, kFullSelf>(SA_ATTN_ARGS);
+    return launch_attn_d<128, kCross>(SA_ATTN_ARGS);
+  }
+  if (mode == kCausalSelf) return launch_attn_d<64, kCausalSelf>(SA_ATTN_ARGS);
+  if (mode == kFullSelf) return launch_attn_d<64, kFullSelf>(SA_ATTN_ARGS);
+  return launch_attn_d<64, kCross>(SA_ATTN_ARGS);
+#undef SA_ATTN_ARGS
 }
 
 // ---------------------------------------------------------------------------
@@ -922,13 +979,43 @@ extern "C" int sa_sparse_attn_fwd(int dtype, const void* q, const void* k, const
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf(static_cast<float>(head_dim));
   const long blocks = static_cast<long>(num_heads) * n_qblk;
   const float sl2 = scale * sa::kLog2e;
-  const int rc =
-      head_dim == 128
-          ? (key_bias ? sa::launch_sparse<128, true>(q, k, v, cu_seqlens, num_seqs, block_idx, n_qblk, max_blocks, key_bias, o, total_tokens, num_heads, sl2, blocks, s)
-                      : sa::launch_sparse<128, false>(q, k, v, cu_seqlens, num_seqs, block_idx, n_qblk, max_blocks, key_bias, o, total_tokens, num_heads, sl2, blocks, s))
-          : (key_bias ? sa::launch_sparse<64, true>(q, k, v, cu_seqlens, num_seqs, block_idx, n_qblk, max_blocks, key_bias, o, total_tokens, num_heads, sl2, blocks, s)
-                      : sa::launch_sparse<64, false>(q, k, v, cu_seqlens, num_seqs, block_idx, n_qblk, max_blocks, key_bias, o, total_tokens, num_heads, sl2, blocks, s));
+  const int rc = sa::launch_attn(sa::kCausalSelf, head_dim, q, k, v, cu_seqlens, cu_seqlens, num_seqs,
+                                 block_idx, n_qblk, max_blocks, key_bias, o, total_tokens,
+                                 total_tokens, num_heads, sl2, blocks, s);
   if (rc) return rc;
   SA_CHECK_LAUNCH("sparse_attn_fwd");
+  return 0;
+}
+
+extern "C" int sa_attn_varlen_fwd(int dtype, int mode, const void* q, const void* k, const void* v,
+                                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                  int num_seqs, const float* key_bias, int total_q, int total_k,
+                                  int num_heads, int head_dim, float softmax_scale, void* o,
+                                  void* stream) {
+  SA_CHECK_ARG(dtype == sa::kBF16, "sa_attn_varlen_fwd: only bfloat16 is supported");
+  SA_CHECK_ARG(mode == sa::kCausalSelf || mode == sa::kFullSelf || mode == sa::kCross,
+               "sa_attn_varlen_fwd: mode %d not in {0 causal, 1 full, 2 cross}", mode);
+  SA_CHECK_ARG(head_dim == 64 || head_dim == 128, "sa_attn_varlen_fwd: head_dim %d not in {64,128}",
+               head_dim);
+  SA_CHECK_ARG(num_seqs >= 0 && num_heads > 0 && total_q >= 0 && total_k >= 0,
+               "sa_attn_varlen_fwd: bad sizes");
+  SA_CHECK_ARG(mode == sa::kCross || total_k == total_q,
+               "sa_attn_varlen_fwd: self-attention needs total_k == total_q");
+  SA_CHECK_ARG(q && k && v && cu_seqlens_q && o && (mode != sa::kCross || cu_seqlens_k),
+               "sa_attn_varlen_fwd: null pointer");
+  if (num_seqs == 0 || total_q == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf(static_cast<float>(head_dim));
+  // upper bound on the query blocks (sum over sequences of ceil(len / 64));
+  // blocks past the real count find no sequence and exit
+  const int n_qblk = total_q / 64 + num_seqs;
+  const long blocks = static_cast<long>(num_heads) * n_qblk;
+  const int32_t* cu_k = mode == sa::kCross ? cu_seqlens_k : cu_seqlens_q;
+  const int Tk = mode == sa::kCross ? total_k : total_q;
+  const int rc = sa::launch_attn(mode, head_dim, q, k, v, cu_seqlens_q, cu_k, num_seqs, nullptr,
+                                 n_qblk, 0, key_bias, o, total_q, Tk, num_heads,
+                                 scale * sa::kLog2e, blocks, s);
+  if (rc) return rc;
+  SA_CHECK_LAUNCH("attn_varlen_fwd");
   return 0;
 }

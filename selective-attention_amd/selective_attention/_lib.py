@@ -36,6 +36,7 @@ SIGNATURES: dict[str, list] = {
                             _vp, _vp, _sz, _vp],
     "sa_sparse_attn_fwd": [_i, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _vp, _i, _i, _i, _f,
                            _vp, _vp],
+    "sa_attn_varlen_fwd": [_i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _f, _vp, _vp],
     "sa_ssd_bwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                    _i, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i,
                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],

@@ -56,6 +56,47 @@ def sparse_attn_varlen(q, k, v, cu_seqlens, block_idx, block_size=64, softmax_sc
     return o
 
 
+ATTN_MODES = {"causal": 0, "full": 1, "cross": 2}
+
+
+def attn_varlen(q, k, v, cu_seqlens_q, mode="causal", cu_seqlens_k=None, key_bias=None,
+                softmax_scale=None):
+    """
+    Dense varlen attention over packed sequences (sa_attn_varlen_fwd).
+
+    Args:
+        q: (total_q, num_heads, head_dim) bfloat16; k, v: (total_k, num_heads, head_dim)
+        cu_seqlens_q: (num_seqs + 1,) int32 query offsets
+        mode: "causal" (keys j <= i of the own sequence), "full" (every key
+            of the own sequence) or "cross" (every key of the sequence's range
+            in cu_seqlens_k)
+        key_bias: (num_heads, total_k) float32 or None, added to every score
+            except the query's own key ("causal", "full") or key 0 of the key
+            sequence ("cross")
+
+    Returns:
+        o: (total_q, num_heads, head_dim) bfloat16; a query with no key gets zeros.
+    """
+    require_device(q, k, v, cu_seqlens_q, cu_seqlens_k, key_bias)
+    if mode not in ATTN_MODES:
+        raise ValueError(f"attn_varlen: mode {mode!r} not in {sorted(ATTN_MODES)}")
+    Tq, H, D = q.shape
+    Tk = k.shape[0]
+    for t in (q, k, v):
+        if t.dtype != torch.bfloat16:
+            raise TypeError("attn_varlen: q, k, v must be bfloat16")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    cu_q = _i32(cu_seqlens_q)
+    cu_k = None if cu_seqlens_k is None else _i32(cu_seqlens_k)
+    bias = None if key_bias is None else key_bias.to(torch.float32).contiguous()
+    o = torch.empty_like(q)
+    scale = -1.0 if softmax_scale is None else float(softmax_scale)
+    _lib.call("sa_attn_varlen_fwd", _lib.DTYPE_BF16, ATTN_MODES[mode], _lib.ptr(q), _lib.ptr(k),
+              _lib.ptr(v), _lib.ptr(cu_q), _lib.ptr(cu_k), cu_q.shape[0] - 1, _lib.ptr(bias), Tq, Tk,
+              H, D, scale, _lib.ptr(o), _lib.stream_of(q))
+    return o
+
+
 def paged_decode_attn(q, k_pages, v_pages, page_table, seq_lens, softmax_scale=None,
                       key_bias=None):
     """

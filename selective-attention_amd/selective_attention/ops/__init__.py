@@ -1,4 +1,4 @@
-from .attention import paged_decode_attn, sparse_attn_varlen
+from .attention import attn_varlen, paged_decode_attn, sparse_attn_varlen
 from .selective_mha import PagedSelectiveAttnCache, selective_mha_prefill
 from .ssd_scan import SSDScanFn
 from .ssm_io import SSDScanGatedFn, SSMConvFn, SSMGateFn, build_conv_ctx, ssm_conv_step
@@ -6,4 +6,4 @@ from .ssu import SSUFn
 
 __all__ = ["SSDScanFn", "SSUFn", "sparse_attn_varlen", "paged_decode_attn", "SSMConvFn",
            "SSMGateFn", "SSDScanGatedFn", "build_conv_ctx", "ssm_conv_step",
-           "selective_mha_prefill", "PagedSelectiveAttnCache"]
+           "selective_mha_prefill", "PagedSelectiveAttnCache", "attn_varlen"]

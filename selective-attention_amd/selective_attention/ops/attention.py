@@ -30,6 +30,30 @@ def sparse_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                  key_bias)
 
 
+def attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                mode: str = "causal", cu_seqlens_k: torch.Tensor | None = None,
+                key_bias: torch.Tensor | None = None,
+                softmax_scale: float | None = None) -> torch.Tensor:
+    """Dense varlen attention: causal or bidirectional self-attention of
+    packed sequences, or cross-attention of packed queries over packed key
+    sequences, with the gate's log as a per-key bias (see
+    kernels.attention.attn_varlen)."""
+    check_ndim(q, 3, name="q")
+    Tq, H, D = q.shape
+    check_ndim(k, 3, name="k")
+    Tk = k.shape[0]
+    check_shape(k, (Tk, H, D), name="k")
+    check_shape(v, (Tk, H, D), name="v")
+    check_ndim(cu_seqlens_q, 1, name="cu_seqlens_q")
+    if mode == "cross":
+        check_ndim(cu_seqlens_k, 1, name="cu_seqlens_k")
+        check_shape(cu_seqlens_k, tuple(cu_seqlens_q.shape), name="cu_seqlens_k")
+    elif Tk != Tq:
+        raise ValueError(f"[k] self-attention needs as many keys as queries ({Tk} != {Tq})")
+    check_shape(key_bias, (H, Tk), name="key_bias", optional=True)
+    return _k.attn_varlen(q, k, v, cu_seqlens_q, mode, cu_seqlens_k, key_bias, softmax_scale)
+
+
 def paged_decode_attn(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
                       page_table: torch.Tensor, seq_lens: torch.Tensor,
                       softmax_scale: float | None = None,

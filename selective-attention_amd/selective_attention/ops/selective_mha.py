@@ -7,8 +7,9 @@ per-head compacted cache (inference/selective_attn_cache.py,
 _reset_cache :11-25) for decode.  Here the same attention runs on the new
 ops:
 
-* selective_mha_prefill: each batch row is one sequence for
-  sparse_attn_varlen, with every causal block selected.  The gate
+* selective_mha_prefill: each batch row is one sequence for the dense
+  causal mode of attn_varlen (the block-sparse kernel over every causal
+  block).  The gate
   enters as key_bias = log_gate (the diagonal is exempt, as in mode "seq").
   A key the reference drops from its compressed cache (gate zeroed or below
   the threshold, or past the length) carries key_bias = -inf, which removes
@@ -27,7 +28,7 @@ from __future__ import annotations
 
 import torch
 
-from .attention import paged_decode_attn, sparse_attn_varlen
+from .attention import attn_varlen, paged_decode_attn
 
 
 def selective_mha_prefill(q_rot: torch.Tensor, k_rot: torch.Tensor, v: torch.Tensor,
@@ -47,10 +48,11 @@ def selective_mha_prefill(q_rot: torch.Tensor, k_rot: torch.Tensor, v: torch.Ten
         (batch_size, seq_len, num_heads, head_dim) memory (the layout the
         module's output projection reads); rows past a length are 0.
 
-    Each batch row is one sequence of seq_len rows for the block-sparse
-    kernel (cu_seqlens = 0, L, 2L, ...).  Padding needs no packing: a query
-    t < length only reaches keys j <= t, and query blocks that lie wholly
-    past the length select no key block, so their rows come out 0.
+    Each batch row is one sequence (cu_seqlens = 0, L, 2L, ...; with
+    lengths, its valid rows and its padding rows are two sequences), so
+    nothing is packed or copied: a query t < length only reaches keys j <= t
+    of its row.  block_size is kept for the signature (the kernel's blocks
+    are 64 keys).
     """
     b, H, L, D = q_rot.shape
     dev = q_rot.device
@@ -63,26 +65,21 @@ def selective_mha_prefill(q_rot: torch.Tensor, k_rot: torch.Tensor, v: torch.Ten
 
     qp, kp, vp = rows(q_rot), rows(k_rot), rows(v)
     bias = log_gate.to(torch.float32).transpose(0, 1).reshape(H, T)
-    nb = (L + block_size - 1) // block_size
-    cu = torch.arange(b + 1, dtype=torch.int32, device=dev) * L
-    # query block jq of row i selects key blocks 0..jq, or nothing when it
-    # starts past the row's length
-    jq = torch.arange(nb, dtype=torch.int32, device=dev)
-    m = torch.arange(nb, dtype=torch.int32, device=dev)
-    sel = torch.where(m[None, :] <= jq[:, None], m[None, :], torch.full_like(m, -1)[None, :])
-    sel = sel[None].expand(b, nb, nb)
-    if lengths is not None:
+    starts = torch.arange(b + 1, dtype=torch.int32, device=dev) * L
+    if lengths is None:
+        cu = starts
+    else:
+        # sequences [i L, i L + len_i) and, between them, the padding rows as
+        # sequences of their own (attended among themselves, then zeroed)
         lens = lengths.to(dev, torch.int64).clamp(0, L)
-        live = (jq[None, :].to(torch.int64) * block_size < lens[:, None])        # (b, nb)
-        sel = torch.where(live[:, :, None], sel, torch.full_like(sel, -1))
-    block_idx = sel.reshape(1, b * nb, nb).expand(H, b * nb, nb).contiguous()
-    o = sparse_attn_varlen(qp, kp, vp, cu, block_idx, block_size, None, bias)
-    out = o.view(b, L, H, D)
+        cu = torch.empty(2 * b + 1, dtype=torch.int32, device=dev)
+        cu[0::2] = starts
+        cu[1::2] = starts[:-1] + lens.to(torch.int32)
+    o = attn_varlen(qp, kp, vp, cu, "causal", key_bias=bias).view(b, L, H, D)
     if lengths is not None:
-        # rows past the length inside a row's last live block
         pad = torch.arange(L, device=dev)[None, :] >= lens[:, None]
-        out.masked_fill_(pad[:, :, None, None], 0.0)
-    return out.transpose(1, 2)
+        o.masked_fill_(pad[:, :, None, None], 0.0)
+    return o.transpose(1, 2)
 
 
 class PagedSelectiveAttnCache:

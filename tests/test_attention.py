@@ -299,3 +299,102 @@ def test_paged_decode_config3_sample():
     exp = ref.paged_decode_attn(d.q[rows].cpu(), kp.cpu(), vp.cpu(), d.page_table[rows].cpu(),
                                 d.seq_lens[rows].cpu())
     assert_parity(o[rows], exp, torch.bfloat16, "o")
+
+
+# ------------------------------------------------- dense varlen attention (modes)
+def test_oracle_attn_varlen_causal_is_full_selection():
+    lens, H, D = [70, 130, 5], 2, 16
+    q, k, v, cu = packed(lens, H, D, dtype=F64)
+    g = torch.Generator().manual_seed(2)
+    bias = torch.randn(H, sum(lens), generator=g, dtype=F64)
+    bias[:, ::7] = float("-inf")
+    exp = ref.sparse_attn_varlen(q, k, v, cu, full_causal_selection(lens, H), key_bias=bias)
+    torch.testing.assert_close(ref.attn_varlen(q, k, v, cu, "causal", key_bias=bias), exp,
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_oracle_attn_varlen_full_and_cross_are_sdpa():
+    lens, H, D = [33, 9], 2, 8
+    q, k, v, cu = packed(lens, H, D, seed=4, dtype=F64)
+    o = ref.attn_varlen(q, k, v, cu, "full")
+    for s in range(2):
+        a, b = int(cu[s]), int(cu[s + 1])
+        e = F.scaled_dot_product_attention(q[a:b].transpose(0, 1), k[a:b].transpose(0, 1),
+                                           v[a:b].transpose(0, 1))
+        torch.testing.assert_close(o[a:b], e.transpose(0, 1), rtol=1e-12, atol=1e-12)
+    klens = [17, 40]
+    _, kk, vv, cuk = packed(klens, H, D, seed=5, dtype=F64)
+    o = ref.attn_varlen(q, kk, vv, cu, "cross", cuk)
+    for s in range(2):
+        a, b, c, d = int(cu[s]), int(cu[s + 1]), int(cuk[s]), int(cuk[s + 1])
+        e = F.scaled_dot_product_attention(q[a:b].transpose(0, 1), kk[c:d].transpose(0, 1),
+                                           vv[c:d].transpose(0, 1))
+        torch.testing.assert_close(o[a:b], e.transpose(0, 1), rtol=1e-12, atol=1e-12)
+
+
+def test_oracle_attn_varlen_brute_force_exemptions():
+    """Loop form of the biased softmax: full mode exempts the query's own key,
+    cross mode the first key of the key sequence."""
+    H, D = 1, 4
+    q, k, v, cu = packed([6], H, D, seed=6, dtype=F64)
+    _, kk, vv, cuk = packed([5], H, D, seed=7, dtype=F64)
+    bias = torch.tensor([[0.3, -1.0, 2.0, -0.5, 0.1, 0.7]], dtype=F64)
+    o = ref.attn_varlen(q, k, v, cu, "full", key_bias=bias)
+    oc = ref.attn_varlen(q, kk, vv, cu, "cross", cuk, key_bias=bias[:, :5])
+    for i in range(6):
+        sc = torch.tensor([float(q[i, 0] @ k[j, 0]) / 2.0 + (0.0 if j == i else float(bias[0, j]))
+                           for j in range(6)], dtype=F64)
+        torch.testing.assert_close(o[i, 0], torch.softmax(sc, 0) @ v[:, 0], rtol=1e-12, atol=1e-12)
+        sc = torch.tensor([float(q[i, 0] @ kk[j, 0]) / 2.0 + (0.0 if j == 0 else float(bias[0, j]))
+                           for j in range(5)], dtype=F64)
+        torch.testing.assert_close(oc[i, 0], torch.softmax(sc, 0) @ vv[:, 0], rtol=1e-12, atol=1e-12)
+
+
+VARLEN_CASES = {
+    # name: (mode, q lens, k lens (cross), D, bias)
+    "causal_d128_bias": ("causal", [200, 64, 1, 130], None, 128, True),
+    "full_d64_bias": ("full", [150, 0, 64, 33], None, 64, True),
+    "full_d128": ("full", [257, 19], None, 128, False),
+    "cross_d64_bias": ("cross", [100, 1, 70, 0], [37, 300, 0, 5], 64, True),
+    "cross_d128": ("cross", [65, 128], [129, 1], 128, False),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", list(VARLEN_CASES))
+def test_attn_varlen_parity(case):
+    from selective_attention.ops import attn_varlen
+    mode, lens, klens, D, with_bias = VARLEN_CASES[case]
+    H = 3
+    q, k, v, cu = packed(lens, H, D, seed=11)
+    cuk = None
+    if mode == "cross":
+        _, k, v, cuk = packed(klens, H, D, seed=12)
+    bias = None
+    if with_bias:
+        g = torch.Generator().manual_seed(13)
+        bias = torch.randn(H, k.shape[0], generator=g)
+        bias[:, ::5] = float("-inf")
+    print(f"attn_varlen case={case}", flush=True)
+    o = attn_varlen(q.cuda(), k.cuda(), v.cuda(), cu.cuda(), mode,
+                    None if cuk is None else cuk.cuda(), None if bias is None else bias.cuda())
+    torch.cuda.synchronize()
+    e = ref.attn_varlen(q, k, v, cu, mode, cuk, bias)
+    assert_parity(o, e, torch.bfloat16, name=case)
+
+
+@pytest.mark.gpu
+def test_attn_varlen_causal_dense_equals_full_selection():
+    """The dense causal mode and the block-sparse op with every causal block
+    selected run the same kernel body: identical bits."""
+    from selective_attention.ops import attn_varlen, sparse_attn_varlen
+    lens, H, D = [300, 65, 1], 2, 64
+    q, k, v, cu = packed(lens, H, D, seed=14)
+    g = torch.Generator().manual_seed(15)
+    bias = torch.randn(H, sum(lens), generator=g).cuda()
+    qd, kd, vd, cud = q.cuda(), k.cuda(), v.cuda(), cu.cuda()
+    print("attn_varlen dense vs table", flush=True)
+    a = attn_varlen(qd, kd, vd, cud, "causal", key_bias=bias)
+    b = sparse_attn_varlen(qd, kd, vd, cud, full_causal_selection(lens, H).cuda(), key_bias=bias)
+    torch.cuda.synchronize()
+    assert torch.equal(a.cpu(), b.cpu())
