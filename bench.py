@@ -420,6 +420,76 @@ def run_causal_lm(args, torch, new_tokens=256):
                        "vocab": cfg.vocab_size, "dtype": "bf16", "attn_gate_threshold": 0.5}}
 
 
+def run_seq2seq(args, torch, enc_len=4096, new_tokens=128):
+    """The seq2seq LM (no BASELINE config: a synthetic workload at config 4's
+    dimensions): d_model 1024, six encoder BiBlocks and six decoder
+    CrossBlocks (SSD d_state 128, 16 attention heads x 64), vocab 32000,
+    bf16; batch 4 encoder inputs of `enc_len` random tokens, greedy decoding
+    of `new_tokens` tokens; gate thresholds 0.5, score statistics 1.  Host
+    clock around synchronised runs; decode per step = (generate - prefill) /
+    (new_tokens - 1)."""
+    from selective_attention.inference import CrossBlockCache, GenerationConfig
+    from selective_attention.models import Seq2SeqLM, Seq2SeqLMConfig
+    from selective_attention.profiling import kernel_timer
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = Seq2SeqLMConfig(vocab_size=32000, model_dim=1024, head_dim=64, ssm_state_dim=128,
+                          ssm_num_groups=1, ssm_chunk_size=256, num_layers=6, dropout_rate=0.0,
+                          device="cuda")
+    m = Seq2SeqLM(cfg)
+    with torch.no_grad():
+        for mod in m.modules():
+            if hasattr(mod, "score_std_ema"):
+                mod.score_std_ema.fill_(1.0)
+    m = m.to_bf16().to(dev).eval()
+    b = 4
+    g = torch.Generator(device=dev).manual_seed(1)
+    ids = torch.randint(10, cfg.vocab_size, (b, enc_len), device=dev, generator=g)
+    H = cfg.model_dim // cfg.head_dim
+    thr = torch.full((cfg.num_layers, H), 0.5, device=dev)
+    gen = GenerationConfig(bos_token_id=1, eos_token_id=-1, pad_token_id=0,
+                           max_new_tokens=new_tokens, enc_attn_gate_thresholds=thr,
+                           attn_gate_thresholds=thr, cross_attn_gate_thresholds=thr)
+    lengths = torch.full((b,), enc_len, device=dev)
+    bos = torch.ones(b, 1, dtype=torch.long, device=dev)
+
+    def prefill():
+        cache = [CrossBlockCache(reserve=new_tokens) for _ in m.decoder_layers]
+        return m(ids, lengths, bos, thr, thr, thr, cache)
+
+    with torch.no_grad():
+        m.generate(ids[:, :256], GenerationConfig(bos_token_id=1, eos_token_id=-1, pad_token_id=0,
+                                                  max_new_tokens=4))
+        prefill()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            prefill()
+        torch.cuda.synchronize()
+        t_pre = (time.perf_counter() - t0) / 3
+        with kernel_timer() as kt:
+            prefill()
+            torch.cuda.synchronize()
+        kernels = {n: round(x["total_ms"] * 1e3, 1) for n, x in kt.stats.items()}
+        t0 = time.perf_counter()
+        seq = m.generate(ids, gen)
+        torch.cuda.synchronize()
+        t_gen = time.perf_counter() - t0
+    assert seq.shape == (b, new_tokens)
+    t_dec = (t_gen - t_pre) / (new_tokens - 1)
+    return {"generate_s": round(t_gen, 4),
+            "encode_prefill_ms": round(t_pre * 1e3, 2),
+            "encoder_tokens_per_s": round(b * enc_len / t_pre, 1),
+            "decode_ms_per_step": round(t_dec * 1e3, 3),
+            "decode_tokens_per_s": round(b / t_dec, 1),
+            "prefill_kernel_us_total": kernels,
+            "config": {"workload": "seq2seq_synthetic", "batch": b, "encoder_len": enc_len,
+                       "new_tokens": new_tokens, "model_dim": cfg.model_dim,
+                       "encoder_blocks": cfg.num_layers, "decoder_blocks": cfg.num_layers,
+                       "vocab": cfg.vocab_size, "dtype": "bf16", "attn_gate_threshold": 0.5}}
+
+
 def _scan_gate_fusion(args, torch):
     """SSD forward + SSM epilogue at config 1: the scan then the gate kernel
     (fp32 y written and re-read) against the epilogue fused into the chunk
@@ -605,6 +675,7 @@ def main():
         out["ssm_io"] = run_ssm_io(args, torch)
         out["selective_mha"] = run_selective_mha(args, torch)
         out["causal_lm"] = run_causal_lm(args, torch)
+        out["seq2seq"] = run_seq2seq(args, torch)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, args.cpu_budget_s)
     if args.copy_probe_mib > 0:

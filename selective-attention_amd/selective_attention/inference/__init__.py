@@ -90,6 +90,29 @@ class SelectiveAttnCache:
         return 0 if self.pages is None else max(self.pages.lens)
 
 
+class CrossSelectiveAttnCache:
+    """inference/cross_selective_attn_cache.py: the context's keys and values
+    for the decoder's cross-attention, here as (batch * context_len, heads,
+    head_dim) bf16 rows with the per-key bias (heads, batch * context_len)
+    and the key offsets cu_k (batch + 1,).  Filled at prefill, read-only
+    while decoding."""
+
+    def __init__(self):
+        self.k = None
+        self.v = None
+        self.key_bias = None
+        self.cu_k = None
+
+
+class CrossBlockCache:
+    """inference/cross_block_cache.py: SSM, self-attention and cross-attention caches."""
+
+    def __init__(self, reserve: int = 256):
+        self.ssm_cache = SSMCache()
+        self.attn_cache = SelectiveAttnCache(reserve)
+        self.cross_attn_cache = CrossSelectiveAttnCache()
+
+
 class CausalBlockCache:
     """inference/causal_block_cache.py: one SSM cache and one attention cache per block."""
 
@@ -123,5 +146,5 @@ class GenerationConfig:
     cache_update_interval: int = 100
 
 
-__all__ = ["SSMCache", "SelectiveAttnCache", "CausalBlockCache", "InferenceState",
-           "GenerationConfig"]
+__all__ = ["SSMCache", "SelectiveAttnCache", "CrossSelectiveAttnCache", "CausalBlockCache",
+           "CrossBlockCache", "InferenceState", "GenerationConfig"]

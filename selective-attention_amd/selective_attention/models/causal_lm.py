@@ -20,6 +20,7 @@ import torch.nn as nn
 
 from ..inference import CausalBlockCache, GenerationConfig, InferenceState
 from ..modules import CausalBlock, RMSNorm
+from ._graph import graph_decode
 
 
 @dataclass
@@ -143,42 +144,26 @@ class CausalLM(nn.Module):
     def _generate_graph(self, logits, cache, state, gen_cfg, seq_ids, L, check_every):
         new = gen_cfg.max_new_tokens
         H, D = self.cfg.model_dim // self.cfg.head_dim, self.cfg.head_dim
-        b = logits.shape[0]
-        like = torch.empty(b, H, D, device=logits.device)
+        like = torch.empty(logits.shape[0], H, D, device=logits.device)
         for c in cache:
             c.attn_cache.prepare_decode(new, like)
         try:
             tok = torch.argmax(torch.softmax(logits, dim=-1), dim=-1)
             seq_ids[:, L] = tok
-            state.step = 1
+            state.step = 0
 
             def body():
                 lg = self.step(tok, cache, state, gen_cfg)
                 tok.copy_(torch.argmax(torch.softmax(lg, dim=-1), dim=-1))
                 state.lengths.add_(1)
 
+            def on_token(i):
+                seq_ids[:, L + i] = tok
+                state.step = i
+
             eos = gen_cfg.eos_token_id
-            done = lambda: bool((seq_ids[:, L:L + state.step] == eos).any(dim=1).all())
-            if new == 1 or done():
-                return
-            # the first decode step runs eagerly on the capture stream (it warms the
-            # libraries' per-stream state), the rest are replays of its graph
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                body()
-            torch.cuda.current_stream().wait_stream(side)
-            seq_ids[:, L + 1] = tok
-            state.step = 2
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=side):
-                body()
-            while state.step < new:
-                if state.step % check_every == 0 and done():
-                    break
-                graph.replay()
-                seq_ids[:, L + state.step] = tok
-                state.step += 1
+            done = lambda: bool((seq_ids[:, L:L + state.step + 1] == eos).any(dim=1).all())
+            graph_decode(body, new - 1, on_token, done, check_every)
         finally:
             for c in cache:
                 c.attn_cache.pages.exit_device_mode()

@@ -11,16 +11,20 @@ exactly those keys.  Writing the drop as -inf directly, instead of
 log(0) * score_std * penalty, also keeps a zero score_std_ema (its value
 before any training step) from turning dropped keys into NaN.
 
+With is_causal=False (the encoder's BiBlock) every key of the sequence is
+visible, the query's own key again exempt (the reference's self column /
+self mask, :84-86); that variant has no decode step.
+
 The training forward (per-head score statistics and gradients through the
 attention) needs an attention backward kernel, which this package does not
-have: forward() in training mode raises NotImplementedError.  Only the
-causal variant is provided.
+have: forward() in training mode raises NotImplementedError.
 """
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
 
+from ..ops.attention import attn_varlen
 from ..ops.selective_mha import selective_mha_prefill
 from .layers import RoPE
 
@@ -37,8 +41,6 @@ class SelectiveMHA(nn.Module):
     def __init__(self, layer_idx: int, dim: int, head_dim: int, log_gate_penalty: float,
                  is_causal: bool = True):
         super().__init__()
-        if not is_causal:
-            raise NotImplementedError("SelectiveMHA: only the causal variant is built")
         self.layer_idx = layer_idx
         assert dim % head_dim == 0
         self.dim = dim
@@ -108,11 +110,29 @@ class SelectiveMHA(nn.Module):
         k = k.to(torch.bfloat16).transpose(1, 2)
         vh = v.view(b, L, H, D).to(torch.bfloat16).transpose(1, 2)
         log_gate = self._log_gate(select_gate, kept)
-        out = selective_mha_prefill(q, k, vh, log_gate, lengths)
-        if cache is not None:
-            cache.build_kv(k, vh, log_gate, lengths)
-        out = out.transpose(1, 2).reshape(b, L, self.dim).to(hidden_states.dtype)
-        return self.out_proj(out * out_gate)
+        if self.is_causal:
+            out = selective_mha_prefill(q, k, vh, log_gate, lengths)
+            if cache is not None:
+                cache.build_kv(k, vh, log_gate, lengths)
+            out = out.transpose(1, 2).reshape(b, L, self.dim)
+        else:
+            out = self._bidirectional(q, k, vh, log_gate, lengths)
+        return self.out_proj(out.to(hidden_states.dtype) * out_gate)
+
+    def _bidirectional(self, q, k, v, log_gate, lengths):
+        """Every key of the row (dropped and padded ones at -inf), the query's
+        own key unbiased; q, k, v (b, H, L, D) views of (b, L, H, D) memory.
+        Returns (b, L, dim) with rows past a length set to 0."""
+        b, H, L, D = q.shape
+        dev = q.device
+        rows = lambda x: x.transpose(1, 2).contiguous().view(b * L, H, D)
+        cu = torch.arange(b + 1, dtype=torch.int32, device=dev) * L
+        bias = log_gate.transpose(0, 1).reshape(H, b * L)
+        out = attn_varlen(rows(q), rows(k), rows(v), cu, "full", key_bias=bias).view(b, L, H * D)
+        if lengths is not None:
+            pad = torch.arange(L, device=dev)[None, :] >= lengths.to(dev)[:, None]
+            out = out.masked_fill(pad[:, :, None], 0.0)
+        return out
 
     def step(self, hidden_states: torch.Tensor, cache, state, gen_cfg, analysis_cfg=None,
              stats=None):
@@ -120,6 +140,8 @@ class SelectiveMHA(nn.Module):
         always gets a slot; when no head of any row keeps it, its gate is -inf
         everywhere and it takes no weight in later steps, which is what the
         reference's write_idx rollback (:414-415) achieves."""
+        if not self.is_causal:
+            raise NotImplementedError("SelectiveMHA.step: the bidirectional variant has no decode step")
         b = hidden_states.shape[0]
         dev = hidden_states.device
         H, D = self.num_heads, self.head_dim
