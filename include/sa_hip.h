@@ -151,6 +151,39 @@ int sa_attn_varlen_fwd(int dtype, int mode, const void* q, const void* k, const 
                        const float* key_bias, int total_q, int total_k, int num_heads, int head_dim,
                        float softmax_scale, void* o, void* stream);
 
+/*
+ * RMSNorm of `rows` rows of `dim` elements (modules/rms_norm.py:33-44):
+ * out = x * rsqrt(mean(x^2) + eps) * (1 + weight[row % groups]), fp32
+ * arithmetic, out in x's dtype (f32 or bf16); weight (groups, dim) f32.
+ */
+int sa_rms_norm_fwd(int dtype, const void* x, const float* weight, long rows, int dim, int groups,
+                    float eps, void* out, void* stream);
+
+/*
+ * Rotary embedding of two tensors at once (q and k; modules/rope.py:9-64):
+ * y = x cos(p f) + rotate_half(x) sin(p f) for x0 -> y0 and x1 -> y1, each
+ * (rows, heads, head_dim) in `dtype` (f32 or bf16), y in bf16; f = inv_freq
+ * (head_dim / 2,) f32; position of row r = positions[r % period] (int64), or
+ * r % period when positions is NULL.  head_dim % 8 == 0.
+ */
+int sa_rope_bf16(int dtype, const void* x0, const void* x1, void* y0, void* y1, long rows,
+                 int heads, int head_dim, const float* inv_freq, const int64_t* positions,
+                 int period, void* stream);
+
+/*
+ * One decode token per batch row into a paged KV cache
+ * (SelectiveAttnCache.update_kv, inference/selective_attn_cache.py:30-42):
+ * slot seq_lens[r], page page_table[r][slot / page_size] (column clamped to
+ * max_pages - 1); k, v (batch, heads, head_dim) bf16 into k_pages
+ * (num_pages, heads, page_size, head_dim) and v_pages (num_pages, heads,
+ * head_dim, page_size), log_gate (batch, heads) f32 into gate_pages
+ * (num_pages, heads, page_size); then seq_lens[r] += 1 on the device.
+ */
+int sa_paged_kv_append(const void* k, const void* v, const float* log_gate,
+                       const int32_t* page_table, int32_t* seq_lens, int batch, int heads,
+                       int head_dim, int page_size, int max_pages, void* k_pages, void* v_pages,
+                       float* gate_pages, void* stream);
+
 /* Workspace bytes of sa_paged_decode_fwd: segment partials for
  * batch * num_kv_heads + 8192 segments, plus a per-row tile prefix sum. */
 size_t sa_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,

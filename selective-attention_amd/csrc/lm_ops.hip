@@ -1,0 +1,222 @@
+// Model-side ops of the LMs around the mixers (gfx950): fused RMSNorm, fused
+// rotary embedding of q and k, and the paged KV-cache append of a decode step.
+//
+// Each replaces a chain of small torch kernels (RMSNorm: cast, square, mean,
+// add, rsqrt, two multiplies, cast back; RoPE: slices, concatenation, cos,
+// sin, multiplies, sum, cast; append: index arithmetic and three scatters),
+// which at decode batch sizes are launch-bound.  All three are HBM streams
+// (or tiny): one read and one write per element.
+//
+//   rms_norm   out = x * rsqrt(mean(x^2) + eps) * (1 + w[row % groups])
+//              (modules/rms_norm.py:33-44), fp32 arithmetic, out in x's dtype.
+//              One wave per row; the row is read twice, the second time from
+//              cache.
+//   rope       y = x cos(p f) + rotate_half(x) sin(p f), f the module's
+//              inv_freq buffer (modules/rope.py:9-64), angles and products
+//              in fp32 as the module computes them, y in bf16 (the attention
+//              kernels' input).  Position of row r: positions[r % period],
+//              or r % period when positions is null (prefill: r = b L + t).
+//   paged_append  one token per batch row into its page (SelectiveAttnCache
+//              update_kv, inference/selective_attn_cache.py:30-42): slot =
+//              seq_lens[row], page = page_table[row][slot / page_size]; K
+//              row-major per page, V transposed per page, the log-gate beside
+//              them; then seq_lens[row] += 1.  One block per row.
+#include "common.h"
+#include "prof.h"
+
+namespace sa {
+namespace {
+
+template <typename T>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const T* __restrict__ x,
+                                                       const float* __restrict__ w,
+                                                       T* __restrict__ out, long rows, int dim,
+                                                       int groups, float eps) {
+  const int lane = threadIdx.x & 63;
+  const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * dim;
+  T* orow = out + row * dim;
+  float ss = 0.0f;
+  for (int i = lane; i < dim; i += 64) {
+    const float v = to_f32(xr[i]);
+    ss += v * v;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
+  const float* wr = w + static_cast<long>(row % groups) * dim;
+  for (int i = lane; i < dim; i += 64) orow[i] = from_f32<T>(to_f32(xr[i]) * scale * (1.0f + wr[i]));
+}
+
+// 8-wide bf16 variant for dim % 512 == 0 (16-byte loads, 8 elements a lane a step)
+__global__ __launch_bounds__(256) void rms_norm_bf16x8_kernel(const uint4* __restrict__ x,
+                                                              const float* __restrict__ w,
+                                                              uint4* __restrict__ out, long rows,
+                                                              int dim, int groups, float eps) {
+  const int lane = threadIdx.x & 63;
+  const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nv = dim / 8;
+  const uint4* xr = x + row * nv;
+  uint4* orow = out + row * nv;
+  float ss = 0.0f;
+  for (int i = lane; i < nv; i += 64) {
+    const uint4 q = xr[i];
+    const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = bf16lo_to_f32(u[j]), b = bf16hi_to_f32(u[j]);
+      ss += a * a + b * b;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
+  const float* wr = w + static_cast<long>(row % groups) * dim;
+  for (int i = lane; i < nv; i += 64) {
+    const uint4 q = xr[i];
+    const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+    uint32_t r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float w0 = 1.0f + wr[8 * i + 2 * j], w1 = 1.0f + wr[8 * i + 2 * j + 1];
+      r[j] = pack_bf16x2(bf16lo_to_f32(u[j]) * scale * w0, bf16hi_to_f32(u[j]) * scale * w1);
+    }
+    orow[i] = uint4{r[0], r[1], r[2], r[3]};
+  }
+}
+
+// thread = (row, head, 4 consecutive pairs i .. i+3 of the half dimension)
+template <typename T>
+__global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x0, const T* __restrict__ x1,
+                                                   bf16* __restrict__ y0, bf16* __restrict__ y1,
+                                                   long rows, int heads, int D,
+                                                   const float* __restrict__ inv_freq,
+                                                   const int64_t* __restrict__ positions, int period) {
+  const int half = D / 2, quads = half / 4;
+  const long per_tensor = rows * heads * quads;
+  long id = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (id >= 2 * per_tensor) return;
+  const bool second = id >= per_tensor;
+  if (second) id -= per_tensor;
+  const T* x = second ? x1 : x0;
+  bf16* y = second ? y1 : y0;
+  const int qd = static_cast<int>(id % quads);
+  const long rh = id / quads;                 // row * heads + head
+  const long row = rh / heads;
+  const long pi = row % period;
+  const float pos = positions ? static_cast<float>(positions[pi]) : static_cast<float>(pi);
+  const T* xr = x + rh * D;
+  bf16* yr = y + rh * D;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = 4 * qd + j;
+    const float ang = pos * inv_freq[i];
+    const float c = cosf(ang), s = sinf(ang);
+    const float a = to_f32(xr[i]), b = to_f32(xr[i + half]);
+    // x cos + rotate_half(x) sin with each product and the sum rounded to
+    // fp32 on its own (no contraction to fma), as the module's torch ops do
+    yr[i] = from_f32<bf16>(__fadd_rn(__fmul_rn(a, c), -__fmul_rn(b, s)));
+    yr[i + half] = from_f32<bf16>(__fadd_rn(__fmul_rn(b, c), __fmul_rn(a, s)));
+  }
+}
+
+__global__ __launch_bounds__(256) void paged_append_kernel(
+    const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ log_gate,
+    const int32_t* __restrict__ page_table, int32_t* __restrict__ seq_lens, int heads, int D,
+    int ps, int max_pages, bf16* __restrict__ k_pages, bf16* __restrict__ v_pages,
+    float* __restrict__ gate_pages) {
+  const int row = blockIdx.x;
+  const int t = seq_lens[row];
+  const int col = min(t / ps, max_pages - 1);
+  const long pid = page_table[static_cast<long>(row) * max_pages + col];
+  const int s = t % ps;
+  const int n = heads * D;
+  for (int e = threadIdx.x; e < n; e += blockDim.x) {
+    const int h = e / D, d = e - h * D;
+    const long src = (static_cast<long>(row) * heads + h) * D + d;
+    const long ph = pid * heads + h;
+    k_pages[(ph * ps + s) * D + d] = k[src];
+    v_pages[(ph * D + d) * ps + s] = v[src];
+    if (d == 0) gate_pages[ph * ps + s] = log_gate[static_cast<long>(row) * heads + h];
+  }
+  __syncthreads();   // every thread has read seq_lens[row]
+  if (threadIdx.x == 0) seq_lens[row] = t + 1;
+}
+
+}  // namespace
+}  // namespace sa
+
+extern "C" int sa_rms_norm_fwd(int dtype, const void* x, const float* weight, long rows, int dim,
+                               int groups, float eps, void* out, void* stream) {
+  SA_CHECK_ARG(dtype == sa::kF32 || dtype == sa::kBF16, "sa_rms_norm_fwd: dtype %d", dtype);
+  SA_CHECK_ARG(rows >= 0 && dim > 0 && groups > 0, "sa_rms_norm_fwd: bad sizes");
+  SA_CHECK_ARG(x && weight && out, "sa_rms_norm_fwd: null pointer");
+  if (rows == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const long blocks = (rows + 3) / 4;
+  sa::ProfScope prof_("rms_norm", s);
+  if (dtype == sa::kBF16 && dim % 512 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+    hipLaunchKernelGGL(sa::rms_norm_bf16x8_kernel, dim3(blocks), dim3(256), 0, s,
+                       static_cast<const uint4*>(x), weight, static_cast<uint4*>(out), rows, dim,
+                       groups, eps);
+  } else if (dtype == sa::kBF16) {
+    hipLaunchKernelGGL(sa::rms_norm_kernel<sa::bf16>, dim3(blocks), dim3(256), 0, s,
+                       static_cast<const sa::bf16*>(x), weight, static_cast<sa::bf16*>(out), rows,
+                       dim, groups, eps);
+  } else {
+    hipLaunchKernelGGL(sa::rms_norm_kernel<float>, dim3(blocks), dim3(256), 0, s,
+                       static_cast<const float*>(x), weight, static_cast<float*>(out), rows, dim,
+                       groups, eps);
+  }
+  SA_CHECK_LAUNCH("rms_norm");
+  return 0;
+}
+
+extern "C" int sa_rope_bf16(int dtype, const void* x0, const void* x1, void* y0, void* y1,
+                            long rows, int heads, int head_dim, const float* inv_freq,
+                            const int64_t* positions, int period, void* stream) {
+  SA_CHECK_ARG(dtype == sa::kF32 || dtype == sa::kBF16, "sa_rope_bf16: dtype %d", dtype);
+  SA_CHECK_ARG(rows >= 0 && heads > 0 && head_dim > 0 && head_dim % 8 == 0 && period > 0,
+               "sa_rope_bf16: bad sizes (head_dim must be a multiple of 8)");
+  SA_CHECK_ARG(x0 && x1 && y0 && y1 && inv_freq, "sa_rope_bf16: null pointer");
+  if (rows == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const long threads = 2 * rows * heads * (head_dim / 8);
+  const long blocks = (threads + 255) / 256;
+  sa::ProfScope prof_("rope", s);
+  if (dtype == sa::kBF16) {
+    hipLaunchKernelGGL(sa::rope_kernel<sa::bf16>, dim3(blocks), dim3(256), 0, s,
+                       static_cast<const sa::bf16*>(x0), static_cast<const sa::bf16*>(x1),
+                       static_cast<sa::bf16*>(y0), static_cast<sa::bf16*>(y1), rows, heads, head_dim,
+                       inv_freq, positions, period);
+  } else {
+    hipLaunchKernelGGL(sa::rope_kernel<float>, dim3(blocks), dim3(256), 0, s,
+                       static_cast<const float*>(x0), static_cast<const float*>(x1),
+                       static_cast<sa::bf16*>(y0), static_cast<sa::bf16*>(y1), rows, heads, head_dim,
+                       inv_freq, positions, period);
+  }
+  SA_CHECK_LAUNCH("rope");
+  return 0;
+}
+
+extern "C" int sa_paged_kv_append(const void* k, const void* v, const float* log_gate,
+                                  const int32_t* page_table, int32_t* seq_lens, int batch,
+                                  int heads, int head_dim, int page_size, int max_pages,
+                                  void* k_pages, void* v_pages, float* gate_pages, void* stream) {
+  SA_CHECK_ARG(batch >= 0 && heads > 0 && head_dim > 0 && page_size > 0 && max_pages > 0,
+               "sa_paged_kv_append: bad sizes");
+  SA_CHECK_ARG(k && v && log_gate && page_table && seq_lens && k_pages && v_pages && gate_pages,
+               "sa_paged_kv_append: null pointer");
+  if (batch == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  sa::ProfScope prof_("paged_append", s);
+  hipLaunchKernelGGL(sa::paged_append_kernel, dim3(batch), dim3(256), 0, s,
+                     static_cast<const sa::bf16*>(k), static_cast<const sa::bf16*>(v), log_gate,
+                     page_table, seq_lens, heads, head_dim, page_size, max_pages,
+                     static_cast<sa::bf16*>(k_pages), static_cast<sa::bf16*>(v_pages), gate_pages);
+  SA_CHECK_LAUNCH("paged_append");
+  return 0;
+}

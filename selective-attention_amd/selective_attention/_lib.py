@@ -37,6 +37,9 @@ SIGNATURES: dict[str, list] = {
     "sa_sparse_attn_fwd": [_i, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _vp, _i, _i, _i, _f,
                            _vp, _vp],
     "sa_attn_varlen_fwd": [_i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _f, _vp, _vp],
+    "sa_rms_norm_fwd": [_i, _vp, _vp, _i64, _i, _i, _f, _vp, _vp],
+    "sa_rope_bf16": [_i, _vp, _vp, _vp, _vp, _i64, _i, _i, _vp, _vp, _i, _vp],
+    "sa_paged_kv_append": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp],
     "sa_ssd_bwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                    _i, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i,
                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],

@@ -1,0 +1,59 @@
+"""Host wrappers of the model-side ops (csrc/lm_ops.hip): fused RMSNorm, fused
+rotary embedding of q and k, and the paged KV-cache append of a decode step."""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from .common import act_dtype_code, require_device
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """x (..., dim) contiguous f32 / bf16; weight (dim,) or (groups, dim) with
+    x (..., groups, dim).  Returns x * rsqrt(mean(x^2) + eps) * (1 + weight)
+    in x's dtype."""
+    require_device(x, weight)
+    dim = x.shape[-1]
+    groups = 1 if weight.dim() == 1 else weight.shape[0]
+    w = weight.to(torch.float32).contiguous()
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    _lib.call("sa_rms_norm_fwd", act_dtype_code(x.dtype), _lib.ptr(x), _lib.ptr(w),
+              x.numel() // max(dim, 1), dim, groups, float(eps), _lib.ptr(out), _lib.stream_of(x))
+    return out
+
+
+def rope_qk(q: torch.Tensor, k: torch.Tensor, inv_freq: torch.Tensor,
+            positions: torch.Tensor | None, period: int):
+    """q, k (..., heads, head_dim) with the same shape; row r of the flattened
+    leading dimensions is at positions[r % period] (int64), or at r % period
+    when positions is None.  Returns the rotated q, k in bfloat16."""
+    require_device(q, k, inv_freq, positions)
+    H, D = q.shape[-2], q.shape[-1]
+    q, k = q.contiguous(), k.to(q.dtype).contiguous()
+    rows = q.numel() // (H * D)
+    yq = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    yk = torch.empty_like(yq)
+    pos = None if positions is None else positions.to(torch.int64).contiguous()
+    f = inv_freq.to(torch.float32).contiguous()
+    _lib.call("sa_rope_bf16", act_dtype_code(q.dtype), _lib.ptr(q), _lib.ptr(k), _lib.ptr(yq),
+              _lib.ptr(yk), rows, H, D, _lib.ptr(f), _lib.ptr(pos), int(period), _lib.stream_of(q))
+    return yq, yk
+
+
+def paged_kv_append(k, v, log_gate, page_table, seq_lens, k_pages, v_pages, gate_pages):
+    """k, v (batch, heads, head_dim) bf16; log_gate (batch, heads) f32;
+    page_table (batch, max_pages) int32; seq_lens (batch,) int32, advanced
+    in place; the pages as in PagedSelectiveAttnCache."""
+    require_device(k, v, log_gate, page_table, seq_lens, k_pages, v_pages, gate_pages)
+    b, H, D = k.shape
+    ps = k_pages.shape[2]
+    k = k.to(torch.bfloat16).contiguous()
+    v = v.to(torch.bfloat16).contiguous()
+    lg = log_gate.to(torch.float32).contiguous()
+    for t, name in ((page_table, "page_table"), (seq_lens, "seq_lens")):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"paged_kv_append: {name} must be a contiguous int32 tensor")
+    _lib.call("sa_paged_kv_append", _lib.ptr(k), _lib.ptr(v), _lib.ptr(lg), _lib.ptr(page_table),
+              _lib.ptr(seq_lens), b, H, D, ps, page_table.shape[1], _lib.ptr(k_pages),
+              _lib.ptr(v_pages), _lib.ptr(gate_pages), _lib.stream_of(k))

@@ -1,11 +1,15 @@
-"""Library layers of the causal LM, as the reference defines them (torch ops;
-they are not on the kernel path): RMSNorm (modules/rms_norm.py:4-44), RoPE
-(modules/rope.py:9-64), SwiGLU (modules/feed_forward.py:4-11)."""
+"""Library layers of the LMs, as the reference defines them: RMSNorm
+(modules/rms_norm.py:4-44), RoPE (modules/rope.py:9-64), SwiGLU
+(modules/feed_forward.py:4-11).  In inference RMSNorm and the rotation of q
+and k run as single fused kernels (kernels/lm_ops.py); with autograd (the
+SSM blocks can train) RMSNorm keeps its torch composite."""
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+
+from ..kernels.lm_ops import rms_norm, rope_qk
 
 
 class RMSNorm(nn.Module):
@@ -23,6 +27,10 @@ class RMSNorm(nn.Module):
             self.weight = nn.Parameter(torch.zeros(shape))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if (self.elementwise_affine and x.is_cuda and x.is_contiguous()
+                and x.dtype in (torch.float32, torch.bfloat16)
+                and not (torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad))):
+            return rms_norm(x, self.weight, self.eps)     # one fused kernel (inference)
         xf = x.float()
         out = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
         if self.elementwise_affine:
@@ -62,13 +70,12 @@ class RoPE(nn.Module):
             cos, sin = cos[:, None], sin[:, None]
         return q * cos + _rotate_half(q) * sin, k * cos + _rotate_half(k) * sin
 
-    def rotate_rows(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
-        """x (batch, seq_len, heads, head_dim) with positions (seq_len,): the
-        "seq" rotation applied in the (batch, seq_len, heads, head_dim) layout
-        the projections produce, in fp32."""
-        cos, sin = self.cos_sin(positions)
-        cos, sin = cos[None, :, None], sin[None, :, None]
-        return x * cos + _rotate_half(x) * sin
+    def rotate_qk(self, q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor | None,
+                  period: int):
+        """q, k (..., heads, head_dim) on the GPU, rotated in one fused kernel
+        and returned in bf16; row r of the leading dimensions at
+        positions[r % period], or at r % period when positions is None."""
+        return rope_qk(q, k, self.inv_freq, positions, period)
 
 
 class SwiGLU(nn.Module):

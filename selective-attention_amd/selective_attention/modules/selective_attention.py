@@ -103,11 +103,9 @@ class SelectiveMHA(nn.Module):
         if not bool(kept.any()):
             # every key dropped: each query attends only itself (:208-209)
             return self.out_proj(v * out_gate)
-        pos = torch.arange(L, device=dev)
-        q = self.rope.rotate_rows(self.q_proj(hidden_states).view(b, L, H, D), pos)
-        k = self.rope.rotate_rows(self.k_proj(hidden_states).view(b, L, H, D), pos)
-        q = q.to(torch.bfloat16).transpose(1, 2)                      # (b, H, L, D) views
-        k = k.to(torch.bfloat16).transpose(1, 2)
+        q, k = self.rope.rotate_qk(self.q_proj(hidden_states).view(b, L, H, D),
+                                   self.k_proj(hidden_states).view(b, L, H, D), None, L)
+        q, k = q.transpose(1, 2), k.transpose(1, 2)                   # (b, H, L, D) views
         vh = v.view(b, L, H, D).to(torch.bfloat16).transpose(1, 2)
         log_gate = self._log_gate(select_gate, kept)
         if self.is_causal:
@@ -158,7 +156,7 @@ class SelectiveMHA(nn.Module):
         q = self.q_proj(hidden_states).view(b, H, D)
         k = self.k_proj(hidden_states).view(b, H, D)
         v = self.v_proj(hidden_states).view(b, H, D)
-        q, k = self.rope(q, k, state.lengths.to(dev), mode="pos")
-        cache.update_kv(k.to(torch.bfloat16), v.to(torch.bfloat16), log_gate)
-        out = cache.attend(q.to(torch.bfloat16)).reshape(b, self.dim).to(hidden_states.dtype)
+        q, k = self.rope.rotate_qk(q, k, state.lengths.to(dev), b)
+        cache.update_kv(k, v.to(torch.bfloat16), log_gate)
+        out = cache.attend(q).reshape(b, self.dim).to(hidden_states.dtype)
         return self.out_proj(out * out_gate)

@@ -28,6 +28,7 @@ from __future__ import annotations
 
 import torch
 
+from ..kernels.lm_ops import paged_kv_append
 from .attention import attn_varlen, paged_decode_attn
 
 
@@ -210,7 +211,6 @@ class PagedSelectiveAttnCache:
                 self._slot(i, self.lens[i] + extra_tokens - 1)
         self.page_table()
         self.lens_dev = torch.tensor(self.lens, dtype=torch.int32).to(self.device)
-        self._rows_dev = torch.arange(self.b, device=self.device)
 
     def exit_device_mode(self):
         self.lens = [int(x) for x in self.lens_dev.tolist()]
@@ -218,13 +218,8 @@ class PagedSelectiveAttnCache:
         self._sl_dirty = True
 
     def _append_device(self, k_rot, v, log_gate):
-        col = torch.clamp(self.lens_dev // self.ps, max=self._pt.shape[1] - 1).long()
-        pid = self._pt[self._rows_dev, col].long()
-        s = (self.lens_dev % self.ps).long()
-        self.k_pages[pid, :, s] = k_rot.to(torch.bfloat16)
-        self.v_pages[pid, :, :, s] = v.to(torch.bfloat16)
-        self.gate_pages[pid, :, s] = log_gate.to(torch.float32)
-        self.lens_dev += 1
+        paged_kv_append(k_rot, v, log_gate, self._pt, self.lens_dev, self.k_pages, self.v_pages,
+                        self.gate_pages)
 
     def append(self, k_rot, v, log_gate):
         """SelectiveAttnCache.update_kv (:30-47): one token per batch row;

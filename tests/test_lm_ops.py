@@ -1,0 +1,121 @@
+"""Model-side fused kernels (csrc/lm_ops.hip) against the reference's torch
+formulas: RMSNorm (modules/rms_norm.py:33-44), RoPE (modules/rope.py:9-64),
+and the paged KV append against the cache's host-side append."""
+import pytest
+import torch
+
+from selective_attention.modules.layers import RMSNorm, RoPE
+
+BF16 = torch.bfloat16
+
+
+def rms_ref(x, w, eps=1e-6):
+    """The module's own composite (fp32 arithmetic, result in x's dtype)."""
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * (1.0 + w.float())).type_as(x)
+
+
+def ulp_bf16_close(a, e, ulps=1):
+    """|a - e| <= ulps bf16 ulps of e (elementwise)."""
+    a, e = a.float(), e.float()
+    ulp = torch.ldexp(torch.ones_like(e), torch.frexp(e.abs().clamp_min(1e-30)).exponent - 8)
+    return bool(((a - e).abs() <= ulps * ulp).all())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,groups,dtype", [((7, 1024), None, BF16), ((3, 5, 100), None, BF16),
+                                                ((6, 4, 64), 4, BF16), ((9, 1024), None, torch.float32)])
+def test_rms_norm_kernel(shape, groups, dtype):
+    from selective_attention.kernels.lm_ops import rms_norm
+    g = torch.Generator().manual_seed(0)
+    x = (3 * torch.randn(*shape, generator=g)).to(dtype)
+    w = 0.3 * torch.randn((shape[-1],) if groups is None else (groups, shape[-1]), generator=g)
+    print(f"rms_norm {shape} groups={groups} {dtype}", flush=True)
+    out = rms_norm(x.cuda(), w.cuda(), 1e-6).cpu()
+    exp = rms_ref(x, w)
+    if dtype == torch.float32:
+        torch.testing.assert_close(out, exp, rtol=2e-6, atol=1e-6)
+    else:
+        assert ulp_bf16_close(out, exp, 1)
+
+
+@pytest.mark.gpu
+def test_rms_norm_module_dispatch():
+    """The module runs the kernel under no_grad and the composite with autograd;
+    both agree."""
+    m = RMSNorm(256).cuda()
+    with torch.no_grad():
+        m.weight.copy_(0.2 * torch.randn(256))
+    x = torch.randn(33, 256, device="cuda").to(BF16)
+    with torch.no_grad():
+        a = m(x)
+    xr = x.clone().requires_grad_(True)
+    b = m(xr)
+    b.float().sum().backward()
+    assert xr.grad is not None
+    assert ulp_bf16_close(a.cpu(), b.detach().cpu(), 1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["seq", "pos"])
+def test_rope_kernel(mode):
+    rope = RoPE(64).cuda()
+    g = torch.Generator().manual_seed(1)
+    if mode == "seq":
+        b, L, H, D = 2, 300, 4, 64
+        q = torch.randn(b, L, H, D, generator=g).to(BF16).cuda()
+        k = torch.randn(b, L, H, D, generator=g).to(BF16).cuda()
+        eq, ek = rope(q.transpose(1, 2), k.transpose(1, 2), torch.arange(L, device="cuda"), "seq")
+        eq, ek = eq.transpose(1, 2), ek.transpose(1, 2)
+        yq, yk = rope.rotate_qk(q, k, None, L)
+    else:
+        b, H, D = 5, 4, 64
+        q = torch.randn(b, H, D, generator=g).to(BF16).cuda()
+        k = torch.randn(b, H, D, generator=g).to(BF16).cuda()
+        pos = torch.tensor([0, 7, 4096, 31999, 123456], device="cuda")
+        eq, ek = rope(q, k, pos, "pos")
+        yq, yk = rope.rotate_qk(q, k, pos, b)
+    print(f"rope {mode}", flush=True)
+    torch.cuda.synchronize()
+    assert ulp_bf16_close(yq.cpu(), eq.to(BF16).cpu(), 1)
+    assert ulp_bf16_close(yk.cpu(), ek.to(BF16).cpu(), 1)
+
+
+@pytest.mark.gpu
+def test_paged_kv_append_kernel():
+    """Device-mode appends (one kernel per step) leave the same pages and
+    lengths as the host-side appends."""
+    from selective_attention.ops.selective_mha import PagedSelectiveAttnCache
+    b, H, D, L = 3, 2, 64, 100
+    g = torch.Generator().manual_seed(2)
+    k = torch.randn(b, H, L, D, generator=g).to(BF16).cuda()
+    v = torch.randn(b, H, L, D, generator=g).to(BF16).cuda()
+    lg = torch.randn(b, H, L, generator=g).cuda()
+    lens = torch.tensor([100, 63, 1])
+    caches = []
+    for device_mode in (False, True):
+        c = PagedSelectiveAttnCache(b, H, D, max_tokens=300, device="cuda")
+        c.build(k, v, lg, lens)
+        if device_mode:
+            c.enter_device_mode(80)
+        for t in range(70):
+            gt = torch.Generator().manual_seed(100 + t)
+            c.append(torch.randn(b, H, D, generator=gt).to(BF16).cuda(),
+                     torch.randn(b, H, D, generator=gt).to(BF16).cuda(),
+                     torch.randn(b, H, generator=gt).cuda())
+        if device_mode:
+            c.exit_device_mode()
+        caches.append(c)
+    print("paged append", flush=True)
+    host, dev = caches
+    assert host.lens == dev.lens == [170, 133, 71]
+    for i in range(b):
+        n = host.lens[i]
+        for c2 in (host, dev):
+            assert len(c2.rows[i]) * 64 >= n
+        for t in range(n):
+            ph, s = host.rows[i][t // 64], t % 64
+            pd = dev.rows[i][t // 64]
+            assert torch.equal(host.k_pages[ph, :, s], dev.k_pages[pd, :, s])
+            assert torch.equal(host.v_pages[ph, :, :, s], dev.v_pages[pd, :, :, s])
+            assert torch.equal(host.gate_pages[ph, :, s], dev.gate_pages[pd, :, s])
