@@ -94,14 +94,15 @@ class CrossSelectiveAttnCache:
     """inference/cross_selective_attn_cache.py: the context's keys and values
     for the decoder's cross-attention, here as (batch * context_len, heads,
     head_dim) bf16 rows with the per-key bias (heads, batch * context_len)
-    and the key offsets cu_k (batch + 1,).  Filled at prefill, read-only
-    while decoding."""
+    and the key offsets cu_k (batch + 1,), and the same context as decode
+    pages.  Filled at prefill, read-only while decoding."""
 
     def __init__(self):
         self.k = None
         self.v = None
         self.key_bias = None
         self.cu_k = None
+        self.pages = None   # (k_pages, v_pages, page_table, seq_lens, gate_pages) for decode
 
 
 class CrossBlockCache:

@@ -8,8 +8,9 @@ cache is given) key 0's gate is 1, padding and keys below the threshold are
 dropped (:102-118: the reference compresses them away; here they carry bias
 -inf); without a cache the reference applies no threshold (:119-125), and
 neither does this module.  The context keys, values and biases are kept in
-the cache for the decode steps, which run the same kernel with one query per
-row.  No RoPE, as in the reference.  Training raises NotImplementedError (no
+the cache for the decode steps, as pages for the split-KV paged decode
+kernel (one query per row over the whole context spreads over every CU).
+No RoPE, as in the reference.  Training raises NotImplementedError (no
 attention backward kernel).
 """
 from __future__ import annotations
@@ -17,7 +18,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from ..ops.attention import attn_varlen
+from ..ops.attention import attn_varlen, paged_decode_attn
 from .selective_attention import _threshold
 
 
@@ -86,13 +87,38 @@ class CrossSelectiveMHA(nn.Module):
         out = attn_varlen(q, k, v, cu_q, "cross", cu_k, key_bias=bias)
         if cache is not None:
             cache.k, cache.v, cache.key_bias, cache.cu_k = k, v, bias, cu_k
+            cache.pages = self._pages(k, v, bias, b, context.shape[1])
         return self.out_proj(out.view(b, L, self.dim).to(hidden_states.dtype))
 
+    def _pages(self, k, v, bias, b, Lc, ps=64):
+        """The context as decode pages for the stream-K paged kernel: per row,
+        keys 1 .. Lc-1, then padding (bias -inf), then key 0 in the row's last
+        slot, the slot that kernel leaves unbiased (key 0's bias is 0 here
+        anyway, so its exemption changes nothing)."""
+        H, D = self.num_heads, self.head_dim
+        dev = k.device
+        npg = (Lc + ps - 1) // ps
+        Lp = npg * ps
+        kk = torch.zeros(b, Lp, H, D, dtype=torch.bfloat16, device=dev)
+        vv = torch.zeros_like(kk)
+        bb = torch.full((b, Lp, H), float("-inf"), dtype=torch.float32, device=dev)
+        k3, v3 = k.view(b, Lc, H, D), v.view(b, Lc, H, D)
+        b3 = bias.view(H, b, Lc).permute(1, 2, 0)
+        kk[:, :Lc - 1], vv[:, :Lc - 1], bb[:, :Lc - 1] = k3[:, 1:], v3[:, 1:], b3[:, 1:]
+        kk[:, Lp - 1], vv[:, Lp - 1], bb[:, Lp - 1] = k3[:, 0], v3[:, 0], b3[:, 0]
+        k_pages = kk.view(b, npg, ps, H, D).permute(0, 1, 3, 2, 4).reshape(b * npg, H, ps, D).contiguous()
+        v_pages = vv.view(b, npg, ps, H, D).permute(0, 1, 3, 4, 2).reshape(b * npg, H, D, ps).contiguous()
+        g_pages = bb.view(b, npg, ps, H).permute(0, 1, 3, 2).reshape(b * npg, H, ps).contiguous()
+        table = torch.arange(b * npg, dtype=torch.int32, device=dev).view(b, npg)
+        lens = torch.full((b,), Lp, dtype=torch.int32, device=dev)
+        return k_pages, v_pages, table, lens, g_pages
+
     def step(self, hidden_states: torch.Tensor, cache, gen_cfg, analysis_cfg=None, stats=None):
-        """hidden_states (batch_size, dim) -> (batch_size, dim)."""
+        """hidden_states (batch_size, dim) -> (batch_size, dim): one query per
+        row over the context pages (split-KV paged decode kernel)."""
         b = hidden_states.shape[0]
         H, D = self.num_heads, self.head_dim
         q = self.q_proj(hidden_states).to(torch.bfloat16).reshape(b, H, D)
-        cu_q = torch.arange(b + 1, dtype=torch.int32, device=q.device)
-        out = attn_varlen(q, cache.k, cache.v, cu_q, "cross", cache.cu_k, key_bias=cache.key_bias)
-        return self.out_proj(out.view(b, self.dim).to(hidden_states.dtype))
+        k_pages, v_pages, table, lens, g_pages = cache.pages
+        out = paged_decode_attn(q, k_pages, v_pages, table, lens, None, g_pages)
+        return self.out_proj(out.reshape(b, self.dim).to(hidden_states.dtype))
