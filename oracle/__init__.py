@@ -17,6 +17,10 @@ Contents (each function cites the reference file:line it restates):
              modules/selective_attention.py); SelectiveMHA's inference
              attention (prefill in the form of the reference's compressed
              branch, decode in mode "pos") and its log-gate.
+  lm.py    - the causal LM and the seq2seq LM in inference (LMRef,
+             Seq2SeqRef): fp64 compositions of the functions above with
+             torch linears / norms / RoPE / SwiGLU, optionally rounding to
+             bf16 where the bf16 model stores a tensor.
   ssm_io.py - the SSM block's stages around the scan (modules/ssm.py):
              SiLU + causal depthwise conv prologue, its decode-time context
              (inference/ssm_cache.py), the D-skip / SiLU-gate epilogue, and
@@ -37,6 +41,10 @@ How each function is pinned (tests/test_oracle_*.py):
                   slice composition and == a brute-force loop; streaming
                   decode steps == the batch conv; context == a brute-force
                   gather; backward formulas == torch.autograd (fp64).
+  lm            - prefill of the first tokens + decode steps == the full
+                  forward (the reference's own test_forward_step
+                  invariant), for the causal LM and the seq2seq decoder,
+                  in fp64; a RoPE position slip is shown to fail it.
   selective_mha - prefill (compressed-branch form) == the reference's other
                   branch (full causal matrix, gate on every column, diagonal
                   restored) on the same inputs; all gates 1 == causal SDPA;
