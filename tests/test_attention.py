@@ -398,3 +398,25 @@ def test_attn_varlen_causal_dense_equals_full_selection():
     b = sparse_attn_varlen(qd, kd, vd, cud, full_causal_selection(lens, H).cuda(), key_bias=bias)
     torch.cuda.synchronize()
     assert torch.equal(a.cpu(), b.cpu())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["full", "cross"])
+def test_attn_varlen_many_sequences(mode):
+    """130 sequences (the kernel finds a query block's sequence 64 sequences
+    per step), lengths 0..97, cross keys of other lengths (some empty)."""
+    from selective_attention.ops import attn_varlen
+    g = torch.Generator().manual_seed(21)
+    lens = torch.randint(0, 98, (130,), generator=g).tolist()
+    H, D = 2, 64
+    q, k, v, cu = packed(lens, H, D, seed=22)
+    cuk = None
+    if mode == "cross":
+        klens = torch.randint(0, 70, (130,), generator=g).tolist()
+        _, k, v, cuk = packed(klens, H, D, seed=23)
+    bias = torch.randn(H, k.shape[0], generator=g)
+    print(f"attn_varlen many sequences {mode}", flush=True)
+    o = attn_varlen(q.cuda(), k.cuda(), v.cuda(), cu.cuda(), mode,
+                    None if cuk is None else cuk.cuda(), bias.cuda())
+    torch.cuda.synchronize()
+    assert_parity(o, ref.attn_varlen(q, k, v, cu, mode, cuk, bias), torch.bfloat16, name=mode)
