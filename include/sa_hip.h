@@ -160,6 +160,31 @@ int sa_rms_norm_fwd(int dtype, const void* x, const float* weight, long rows, in
                     float eps, void* out, void* stream);
 
 /*
+ * Residual add fused with the next RMSNorm (the pre-norm blocks,
+ * modules/causal_block.py:84-98): out = bf16(x + y), nrm = RMSNorm(out) with
+ * weight (dim,) f32; bf16 rows of dim elements, dim % 512 == 0, dim <= 4096,
+ * 16-byte aligned.
+ */
+int sa_add_rms_norm_bf16(const void* x, const void* y, const float* weight, long rows, int dim,
+                         float eps, void* out, void* nrm, void* stream);
+
+/*
+ * SelectiveMHA.step's gates (modules/selective_attention.py:378-387): g =
+ * gate_proj output (rows, heads + dim) bf16; s = bf16(sigmoid(g)); for the
+ * first `heads` columns log_gate (rows, heads) f32 = log(s) * score_std[h] *
+ * penalty where s > 0 and s >= thr[h] (thr may be NULL), -inf elsewhere;
+ * the rest -> out_gate (rows, dim) bf16 = s.
+ */
+int sa_mha_gates_bf16(const void* g, const float* thr, const float* score_std, float penalty,
+                      long rows, int heads, int dim, float* log_gate, void* out_gate, void* stream);
+
+/*
+ * SwiGLU's gated product (modules/feed_forward.py:10-11): out = bf16(a *
+ * bf16(silu(c))), n bf16 elements (n % 8 == 0, 16-byte aligned).
+ */
+int sa_silu_mul_bf16(const void* a, const void* c, long n, void* out, void* stream);
+
+/*
  * Rotary embedding of two tensors at once (q and k; modules/rope.py:9-64):
  * y = x cos(p f) + rotate_half(x) sin(p f) for x0 -> y0 and x1 -> y1, each
  * (rows, heads, head_dim) in `dtype` (f32 or bf16), y in bf16; f = inv_freq

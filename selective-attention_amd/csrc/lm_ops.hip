@@ -1,5 +1,7 @@
-// Model-side ops of the LMs around the mixers (gfx950): fused RMSNorm, fused
-// rotary embedding of q and k, and the paged KV-cache append of a decode step.
+// Model-side ops of the LMs around the mixers (gfx950): fused RMSNorm (alone
+// and with the residual add before it), fused rotary embedding of q and k,
+// SelectiveMHA's gate math, SwiGLU's gated product, and the paged KV-cache
+// append of a decode step.
 //
 // Each replaces a chain of small torch kernels (RMSNorm: cast, square, mean,
 // add, rsqrt, two multiplies, cast back; RoPE: slices, concatenation, cos,
@@ -145,8 +147,160 @@ __global__ __launch_bounds__(256) void paged_append_kernel(
   if (threadIdx.x == 0) seq_lens[row] = t + 1;
 }
 
+// out = x + y (rounded to x's dtype), nrm = rms_norm(out): the residual add
+// of a pre-norm block fused with the next norm.  bf16, dim % 512 == 0,
+// dim <= 512 VPL; the row stays in registers between the two passes.
+template <int VPL>
+__global__ __launch_bounds__(256) void add_rms_norm_kernel(const uint4* __restrict__ x,
+                                                           const uint4* __restrict__ y,
+                                                           const float* __restrict__ w,
+                                                           uint4* __restrict__ out,
+                                                           uint4* __restrict__ nrm, long rows,
+                                                           int dim, float eps) {
+  const int lane = threadIdx.x & 63;
+  const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nv = dim / 8;
+  const long base = row * nv;
+  uint32_t sv[VPL][4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int i = lane + 64 * j;
+    if (i < nv) {
+      const uint4 a = x[base + i], c = y[base + i];
+      const uint32_t ua[4] = {a.x, a.y, a.z, a.w}, uc[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        sv[j][q] = pack_bf16x2(bf16lo_to_f32(ua[q]) + bf16lo_to_f32(uc[q]),
+                               bf16hi_to_f32(ua[q]) + bf16hi_to_f32(uc[q]));
+        const float lo = bf16lo_to_f32(sv[j][q]), hi = bf16hi_to_f32(sv[j][q]);
+        ss += lo * lo + hi * hi;
+      }
+      out[base + i] = uint4{sv[j][0], sv[j][1], sv[j][2], sv[j][3]};
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int i = lane + 64 * j;
+    if (i < nv) {
+      uint32_t r[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float w0 = 1.0f + w[8 * i + 2 * q], w1 = 1.0f + w[8 * i + 2 * q + 1];
+        r[q] = pack_bf16x2(bf16lo_to_f32(sv[j][q]) * scale * w0, bf16hi_to_f32(sv[j][q]) * scale * w1);
+      }
+      nrm[base + i] = uint4{r[0], r[1], r[2], r[3]};
+    }
+  }
+}
+
+// SelectiveMHA's gates at a decode step: g = gate_proj output (rows, H + dim)
+// bf16.  Columns < H: select gate s = bf16(sigmoid(g)); kept = s > 0 and
+// s >= thr[h]; lg = kept ? log(s) * std[h] * penalty : -inf (fp32, (rows, H)).
+// Columns >= H: the out gate bf16(sigmoid(g)) ((rows, dim)).
+__global__ __launch_bounds__(256) void mha_gates_kernel(const bf16* __restrict__ g,
+                                                        const float* __restrict__ thr,
+                                                        const float* __restrict__ std_h,
+                                                        float penalty, float* __restrict__ lg,
+                                                        bf16* __restrict__ og, long rows, int H,
+                                                        int dim) {
+  const int W = H + dim;
+  const long id = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (id >= rows * W) return;
+  const long r = id / W;
+  const int col = static_cast<int>(id - r * W);
+  const float z = to_f32(g[id]);
+  const float sg = to_f32(from_f32<bf16>(1.0f / (1.0f + expf(-z))));
+  if (col < H) {
+    const bool kept = sg > 0.0f && (thr == nullptr || sg >= thr[col]);
+    lg[r * H + col] = kept ? __fmul_rn(__fmul_rn(logf(sg), std_h[col]), penalty) : -__builtin_huge_valf();
+  } else {
+    og[r * dim + (col - H)] = from_f32<bf16>(sg);
+  }
+}
+
+// SwiGLU's gated product: out = bf16(a * bf16(silu(c))), all bf16
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint4* __restrict__ a,
+                                                       const uint4* __restrict__ c,
+                                                       uint4* __restrict__ out, long n8) {
+  const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n8) return;
+  const uint4 qa = a[i], qc = c[i];
+  const uint32_t ua[4] = {qa.x, qa.y, qa.z, qa.w}, uc[4] = {qc.x, qc.y, qc.z, qc.w};
+  uint32_t r[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float c0 = bf16lo_to_f32(uc[q]), c1 = bf16hi_to_f32(uc[q]);
+    const uint32_t s = pack_bf16x2(c0 / (1.0f + expf(-c0)), c1 / (1.0f + expf(-c1)));
+    r[q] = pack_bf16x2(bf16lo_to_f32(ua[q]) * bf16lo_to_f32(s), bf16hi_to_f32(ua[q]) * bf16hi_to_f32(s));
+  }
+  out[i] = uint4{r[0], r[1], r[2], r[3]};
+}
+
 }  // namespace
 }  // namespace sa
+
+extern "C" int sa_add_rms_norm_bf16(const void* x, const void* y, const float* weight, long rows,
+                                    int dim, float eps, void* out, void* nrm, void* stream) {
+  SA_CHECK_ARG(rows >= 0 && dim > 0 && dim % 512 == 0 && dim <= 4096,
+               "sa_add_rms_norm_bf16: dim %d must be a multiple of 512, at most 4096", dim);
+  SA_CHECK_ARG(x && y && weight && out && nrm, "sa_add_rms_norm_bf16: null pointer");
+  SA_CHECK_ARG(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
+                 reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(nrm)) & 15) == 0,
+               "sa_add_rms_norm_bf16: tensors must be 16-byte aligned");
+  if (rows == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const long blocks = (rows + 3) / 4;
+  sa::ProfScope prof_("add_rms_norm", s);
+  const int vpl = dim / 512;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, s, static_cast<const uint4*>(x),
+                       static_cast<const uint4*>(y), weight, static_cast<uint4*>(out),
+                       static_cast<uint4*>(nrm), rows, dim, eps);
+  };
+  if (vpl <= 2) go(sa::add_rms_norm_kernel<2>);
+  else if (vpl <= 4) go(sa::add_rms_norm_kernel<4>);
+  else go(sa::add_rms_norm_kernel<8>);
+  SA_CHECK_LAUNCH("add_rms_norm");
+  return 0;
+}
+
+extern "C" int sa_mha_gates_bf16(const void* g, const float* thr, const float* score_std,
+                                 float penalty, long rows, int heads, int dim, float* log_gate,
+                                 void* out_gate, void* stream) {
+  SA_CHECK_ARG(rows >= 0 && heads > 0 && dim > 0, "sa_mha_gates_bf16: bad sizes");
+  SA_CHECK_ARG(g && score_std && log_gate && out_gate, "sa_mha_gates_bf16: null pointer");
+  if (rows == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const long n = rows * (heads + dim);
+  sa::ProfScope prof_("mha_gates", s);
+  hipLaunchKernelGGL(sa::mha_gates_kernel, dim3((n + 255) / 256), dim3(256), 0, s,
+                     static_cast<const sa::bf16*>(g), thr, score_std, penalty, log_gate,
+                     static_cast<sa::bf16*>(out_gate), rows, heads, dim);
+  SA_CHECK_LAUNCH("mha_gates");
+  return 0;
+}
+
+extern "C" int sa_silu_mul_bf16(const void* a, const void* c, long n, void* out, void* stream) {
+  SA_CHECK_ARG(n >= 0 && n % 8 == 0, "sa_silu_mul_bf16: n %ld must be a multiple of 8", n);
+  SA_CHECK_ARG(a && c && out, "sa_silu_mul_bf16: null pointer");
+  SA_CHECK_ARG(((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(c) |
+                 reinterpret_cast<uintptr_t>(out)) & 15) == 0,
+               "sa_silu_mul_bf16: tensors must be 16-byte aligned");
+  if (n == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const long n8 = n / 8;
+  sa::ProfScope prof_("silu_mul", s);
+  hipLaunchKernelGGL(sa::silu_mul_kernel, dim3((n8 + 255) / 256), dim3(256), 0, s,
+                     static_cast<const uint4*>(a), static_cast<const uint4*>(c),
+                     static_cast<uint4*>(out), n8);
+  SA_CHECK_LAUNCH("silu_mul");
+  return 0;
+}
 
 extern "C" int sa_rms_norm_fwd(int dtype, const void* x, const float* weight, long rows, int dim,
                                int groups, float eps, void* out, void* stream) {

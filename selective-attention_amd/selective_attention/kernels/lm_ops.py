@@ -1,5 +1,7 @@
-"""Host wrappers of the model-side ops (csrc/lm_ops.hip): fused RMSNorm, fused
-rotary embedding of q and k, and the paged KV-cache append of a decode step."""
+"""Host wrappers of the model-side ops (csrc/lm_ops.hip): fused RMSNorm (alone
+and with the residual add before it), fused rotary embedding of q and k,
+SelectiveMHA's decode-step gates, SwiGLU's gated product, and the paged
+KV-cache append of a decode step."""
 from __future__ import annotations
 
 import torch
@@ -57,3 +59,48 @@ def paged_kv_append(k, v, log_gate, page_table, seq_lens, k_pages, v_pages, gate
     _lib.call("sa_paged_kv_append", _lib.ptr(k), _lib.ptr(v), _lib.ptr(lg), _lib.ptr(page_table),
               _lib.ptr(seq_lens), b, H, D, ps, page_table.shape[1], _lib.ptr(k_pages),
               _lib.ptr(v_pages), _lib.ptr(gate_pages), _lib.stream_of(k))
+
+
+def add_rms_norm_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    d = x.shape[-1]
+    return (x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and weight.dim() == 1
+            and d % 512 == 0 and d <= 4096)
+
+
+def add_rms_norm(x: torch.Tensor, y: torch.Tensor, weight: torch.Tensor, eps: float):
+    """(x + y, RMSNorm(x + y)) for bf16 rows; see add_rms_norm_supported."""
+    require_device(x, y, weight)
+    y = y.to(x.dtype).contiguous()
+    w = weight.to(torch.float32).contiguous()
+    out = torch.empty_like(x)
+    nrm = torch.empty_like(x)
+    dim = x.shape[-1]
+    _lib.call("sa_add_rms_norm_bf16", _lib.ptr(x), _lib.ptr(y), _lib.ptr(w), x.numel() // dim, dim,
+              float(eps), _lib.ptr(out), _lib.ptr(nrm), _lib.stream_of(x))
+    return out, nrm
+
+
+def mha_gates(g: torch.Tensor, threshold: torch.Tensor | None, score_std: torch.Tensor,
+              penalty: float, heads: int):
+    """g (rows, heads + dim) bf16 -> (log_gate (rows, heads) f32, out_gate (rows, dim) bf16)."""
+    require_device(g, threshold, score_std)
+    g = g.contiguous()
+    rows, W = g.shape
+    dim = W - heads
+    lg = torch.empty(rows, heads, dtype=torch.float32, device=g.device)
+    og = torch.empty(rows, dim, dtype=torch.bfloat16, device=g.device)
+    thr = None if threshold is None else threshold.to(torch.float32).contiguous()
+    std = score_std.to(torch.float32).contiguous()
+    _lib.call("sa_mha_gates_bf16", _lib.ptr(g), _lib.ptr(thr), _lib.ptr(std), float(penalty), rows,
+              heads, dim, _lib.ptr(lg), _lib.ptr(og), _lib.stream_of(g))
+    return lg, og
+
+
+def silu_mul(a: torch.Tensor, c: torch.Tensor) -> torch.Tensor:
+    """bf16(a * bf16(silu(c))) for bf16 tensors of one shape (numel % 8 == 0)."""
+    require_device(a, c)
+    a, c = a.contiguous(), c.contiguous()
+    out = torch.empty_like(a)
+    _lib.call("sa_silu_mul_bf16", _lib.ptr(a), _lib.ptr(c), a.numel(), _lib.ptr(out),
+              _lib.stream_of(a))
+    return out

@@ -1,6 +1,7 @@
 """CausalBlock (modules/causal_block.py:13-139): pre-norm residual block of
 SSM, SelectiveMHA and SwiGLU, with the reference's constructor arguments and
-forward / step interfaces."""
+forward / step interfaces.  Each residual add inside the block runs with the
+next norm (RMSNorm.add_forward: one kernel in inference)."""
 from __future__ import annotations
 
 import torch
@@ -35,19 +36,18 @@ class CausalBlock(nn.Module):
         """(batch, seq_len, model_dim) -> (hidden_states, last_ssm_hiddens)."""
         h, last = self.ssm(self.norm1(hidden_states), lengths=lengths,
                            cache=cache.ssm_cache if cache is not None else None)
-        hidden_states = hidden_states + self.dropout(h)
-        h = self.mha(self.norm2(hidden_states), lengths=lengths,
-                     attn_gate_threshold=attn_gate_threshold,
+        hidden_states, n = self.norm2.add_forward(hidden_states, self.dropout(h))
+        h = self.mha(n, lengths=lengths, attn_gate_threshold=attn_gate_threshold,
                      cache=cache.attn_cache if cache is not None else None)
-        hidden_states = hidden_states + self.dropout(h)
-        hidden_states = hidden_states + self.dropout(self.ffn(self.norm3(hidden_states)))
+        hidden_states, n = self.norm3.add_forward(hidden_states, self.dropout(h))
+        hidden_states = hidden_states + self.dropout(self.ffn(n))
         return hidden_states, last
 
     def step(self, hidden_states: torch.Tensor, cache, state, gen_cfg, analysis_cfg=None,
              stats=None):
         """(batch, model_dim) -> (batch, model_dim)."""
-        hidden_states = hidden_states + self.dropout(self.ssm.step(self.norm1(hidden_states),
-                                                                   cache.ssm_cache))
-        hidden_states = hidden_states + self.dropout(
-            self.mha.step(self.norm2(hidden_states), cache.attn_cache, state, gen_cfg))
-        return hidden_states + self.dropout(self.ffn(self.norm3(hidden_states)))
+        h = self.ssm.step(self.norm1(hidden_states), cache.ssm_cache)
+        hidden_states, n = self.norm2.add_forward(hidden_states, self.dropout(h))
+        h = self.mha.step(n, cache.attn_cache, state, gen_cfg)
+        hidden_states, n = self.norm3.add_forward(hidden_states, self.dropout(h))
+        return hidden_states + self.dropout(self.ffn(n))

@@ -9,7 +9,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ..kernels.lm_ops import rms_norm, rope_qk
+from ..kernels.lm_ops import add_rms_norm, add_rms_norm_supported, rms_norm, rope_qk, silu_mul
 
 
 class RMSNorm(nn.Module):
@@ -36,6 +36,16 @@ class RMSNorm(nn.Module):
         if self.elementwise_affine:
             out = out * (1.0 + self.weight.float())
         return out.type_as(x)
+
+    def add_forward(self, x: torch.Tensor, y: torch.Tensor):
+        """(x + y, self(x + y)): a pre-norm block's residual add and its next
+        norm, in one kernel in inference for bf16 rows of 512k <= 4096 elements."""
+        if (self.elementwise_affine and add_rms_norm_supported(x, self.weight)
+                and not (torch.is_grad_enabled()
+                         and (x.requires_grad or y.requires_grad or self.weight.requires_grad))):
+            return add_rms_norm(x, y, self.weight, self.eps)
+        s = x + y
+        return s, self(s)
 
 
 def _rotate_half(x: torch.Tensor) -> torch.Tensor:
@@ -88,4 +98,9 @@ class SwiGLU(nn.Module):
         self.out = nn.Linear(hidden_dim, dim)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.out(self.w1(x) * F.silu(self.w2(x)))
+        a, c = self.w1(x), self.w2(x)
+        if (a.is_cuda and a.dtype == torch.bfloat16 and c.dtype == torch.bfloat16
+                and a.numel() % 8 == 0
+                and not (torch.is_grad_enabled() and (a.requires_grad or c.requires_grad))):
+            return self.out(silu_mul(a, c))          # one fused kernel (inference)
+        return self.out(a * F.silu(c))

@@ -24,6 +24,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
+from ..kernels.lm_ops import mha_gates
 from ..ops.attention import attn_varlen
 from ..ops.selective_mha import selective_mha_prefill
 from .layers import RoPE
@@ -148,11 +149,16 @@ class SelectiveMHA(nn.Module):
             thr = _threshold(gen_cfg.attn_gate_thresholds[self.layer_idx], H, dev)
         if state.step % gen_cfg.cache_update_interval == 0:
             cache.compact()
-        select_gate, out_gate = self._gates(hidden_states)             # (b, H), (b, dim)
-        kept = select_gate > 0.0
-        if thr is not None:
-            kept &= select_gate >= thr[None, :]
-        log_gate = self._log_gate(select_gate, kept)
+        g = self.gate_proj(hidden_states)
+        if g.is_cuda and g.dtype == torch.bfloat16:
+            # sigmoid, split, threshold and log-gate in one kernel
+            log_gate, out_gate = mha_gates(g, thr, self.score_std_ema, self.log_gate_penalty, H)
+        else:
+            select_gate, out_gate = torch.split(torch.sigmoid(g), [H, self.dim], dim=-1)
+            kept = select_gate > 0.0
+            if thr is not None:
+                kept &= select_gate >= thr[None, :]
+            log_gate = self._log_gate(select_gate, kept)
         q = self.q_proj(hidden_states).view(b, H, D)
         k = self.k_proj(hidden_states).view(b, H, D)
         v = self.v_proj(hidden_states).view(b, H, D)

@@ -39,10 +39,10 @@ class BiBlock(nn.Module):
                 attn_gate_threshold=None, analysis_cfg=None, stats=None):
         """(batch, seq_len, model_dim) -> (hidden_states, last_ssm_hiddens)."""
         h, last = self.ssm(self.norm1(hidden_states), lengths=lengths)
-        hidden_states = hidden_states + self.dropout(h)
-        hidden_states = hidden_states + self.dropout(
-            self.mha(self.norm2(hidden_states), lengths=lengths, attn_gate_threshold=attn_gate_threshold))
-        hidden_states = hidden_states + self.dropout(self.ffn(self.norm3(hidden_states)))
+        hidden_states, n = self.norm2.add_forward(hidden_states, self.dropout(h))
+        h = self.mha(n, lengths=lengths, attn_gate_threshold=attn_gate_threshold)
+        hidden_states, n = self.norm3.add_forward(hidden_states, self.dropout(h))
+        hidden_states = hidden_states + self.dropout(self.ffn(n))
         return hidden_states, last
 
 
@@ -71,24 +71,23 @@ class CrossBlock(nn.Module):
         """(batch, seq_len, model_dim) -> (batch, seq_len, model_dim)."""
         h, _ = self.ssm(self.norm1(hidden_states), ssm_hiddens=ssm_hiddens,
                         cache=cache.ssm_cache if cache is not None else None)
-        hidden_states = hidden_states + self.dropout(h)
-        hidden_states = hidden_states + self.dropout(
-            self.mha(self.norm2(hidden_states), attn_gate_threshold=self_attn_gate_threshold,
-                     cache=cache.attn_cache if cache is not None else None))
-        hidden_states = hidden_states + self.dropout(
-            self.cross_mha(self.norm3(hidden_states), context=context,
-                           context_lengths=context_lengths,
+        hidden_states, n = self.norm2.add_forward(hidden_states, self.dropout(h))
+        h = self.mha(n, attn_gate_threshold=self_attn_gate_threshold,
+                     cache=cache.attn_cache if cache is not None else None)
+        hidden_states, n = self.norm3.add_forward(hidden_states, self.dropout(h))
+        h = self.cross_mha(n, context=context, context_lengths=context_lengths,
                            attn_gate_threshold=cross_attn_gate_threshold,
-                           cache=cache.cross_attn_cache if cache is not None else None))
-        return hidden_states + self.dropout(self.ffn(self.norm4(hidden_states)))
+                           cache=cache.cross_attn_cache if cache is not None else None)
+        hidden_states, n = self.norm4.add_forward(hidden_states, self.dropout(h))
+        return hidden_states + self.dropout(self.ffn(n))
 
     def step(self, hidden_states: torch.Tensor, cache, state, gen_cfg, analysis_cfg=None,
              stats=None):
         """(batch, model_dim) -> (batch, model_dim)."""
-        hidden_states = hidden_states + self.dropout(self.ssm.step(self.norm1(hidden_states),
-                                                                   cache.ssm_cache))
-        hidden_states = hidden_states + self.dropout(
-            self.mha.step(self.norm2(hidden_states), cache.attn_cache, state, gen_cfg))
-        hidden_states = hidden_states + self.dropout(
-            self.cross_mha.step(self.norm3(hidden_states), cache.cross_attn_cache, gen_cfg))
-        return hidden_states + self.dropout(self.ffn(self.norm4(hidden_states)))
+        h = self.ssm.step(self.norm1(hidden_states), cache.ssm_cache)
+        hidden_states, n = self.norm2.add_forward(hidden_states, self.dropout(h))
+        h = self.mha.step(n, cache.attn_cache, state, gen_cfg)
+        hidden_states, n = self.norm3.add_forward(hidden_states, self.dropout(h))
+        h = self.cross_mha.step(n, cache.cross_attn_cache, gen_cfg)
+        hidden_states, n = self.norm4.add_forward(hidden_states, self.dropout(h))
+        return hidden_states + self.dropout(self.ffn(n))

@@ -62,6 +62,17 @@ class SSM(nn.Module):
         self.out_proj = nn.Linear(self.inner_dim, model_dim)
         self.dropout = nn.Dropout(dropout_rate)
 
+    def _A(self) -> torch.Tensor:
+        """A = -exp(A_log) in fp32; in inference computed once per value of
+        A_log (the decode step then launches nothing for it)."""
+        if torch.is_grad_enabled() and self.A_log.requires_grad:
+            return -torch.exp(self.A_log.float())
+        key = (self.A_log.data_ptr(), self.A_log._version, self.A_log.device)
+        if getattr(self, "_A_key", None) != key:
+            self._A_val = -torch.exp(self.A_log.detach().float())
+            self._A_key = key
+        return self._A_val
+
     def _split(self, proj: torch.Tensor):
         return torch.split(proj, [self.inner_dim + 2 * self.bc_dim, self.inner_dim, self.num_heads],
                            dim=-1)
@@ -79,7 +90,7 @@ class SSM(nn.Module):
         """
         b, L, _ = hidden_states.shape
         hBC, gate, delta_raw = self._split(self.in_proj(hidden_states))
-        A = -torch.exp(self.A_log.float())
+        A = self._A()
         if cache is not None and not self.training:
             # prefill: the decode context (raw rows before SiLU) from the conv's own pass
             x, B, C, ctx = ssm_conv_forward(hBC, self.conv.weight, self.conv.bias, self.inner_dim,
@@ -104,7 +115,7 @@ class SSM(nn.Module):
         hBC, gate, delta_raw = self._split(self.in_proj(hidden_states))
         x, B, C = ssm_conv_step(hBC, cache.conv_ctx, self.conv.weight, self.conv.bias,
                                 self.inner_dim, self.bc_dim)
-        A = -torch.exp(self.A_log.float())
+        A = self._A()
         H, P, G, N = self.num_heads, self.head_dim, self.num_groups, self.state_dim
         y, cache.h = SSUFn.forward(x.view(b, H, P), A, B.view(b, G, N), C.view(b, G, N),
                                    delta_raw, self.delta_bias, cache.h)

@@ -119,3 +119,56 @@ def test_paged_kv_append_kernel():
             assert torch.equal(host.k_pages[ph, :, s], dev.k_pages[pd, :, s])
             assert torch.equal(host.v_pages[ph, :, :, s], dev.v_pages[pd, :, :, s])
             assert torch.equal(host.gate_pages[ph, :, s], dev.gate_pages[pd, :, s])
+
+
+@pytest.mark.gpu
+def test_add_rms_norm_kernel():
+    from selective_attention.kernels.lm_ops import add_rms_norm
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(37, 1024, generator=g).to(BF16)
+    y = torch.randn(37, 1024, generator=g).to(BF16)
+    w = 0.3 * torch.randn(1024, generator=g)
+    print("add_rms_norm", flush=True)
+    s, n = add_rms_norm(x.cuda(), y.cuda(), w.cuda(), 1e-6)
+    es = (x + y)                       # torch's bf16 add (fp32 arithmetic, rounded)
+    assert torch.equal(s.cpu(), es)
+    assert ulp_bf16_close(n.cpu(), rms_ref(es, w), 1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("with_thr", [False, True])
+def test_mha_gates_kernel(with_thr):
+    """The step's gate math against the module's torch path (sigmoid, split,
+    threshold, log-gate)."""
+    from selective_attention.kernels.lm_ops import mha_gates
+    g = torch.Generator().manual_seed(4)
+    H, dim = 16, 1024
+    z = (torch.randn(5, H + dim, generator=g) + 2.0).to(BF16)
+    z[0, :4] = -200.0                  # sigmoid rounds to 0 in bf16: dropped
+    thr = torch.full((H,), 0.9) if with_thr else None
+    std = 0.5 + torch.rand(H, generator=g)
+    print(f"mha_gates thr={with_thr}", flush=True)
+    lg, og = mha_gates(z.cuda(), None if thr is None else thr.cuda(), std.cuda(), 2.0, H)
+    sg = torch.sigmoid(z.cuda()).cpu()
+    s, o = sg[:, :H], sg[:, H:]
+    kept = s > 0
+    if thr is not None:
+        kept &= s >= thr[None, :]
+    elg = torch.where(kept, torch.log(s.float()) * std * 2.0, torch.full((5, H), float("-inf")))
+    assert torch.equal(og.cpu(), o)
+    assert torch.equal(torch.isinf(lg.cpu()), torch.isinf(elg))
+    f = torch.isfinite(elg)
+    torch.testing.assert_close(lg.cpu()[f], elg[f], rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.gpu
+def test_silu_mul_kernel():
+    import torch.nn.functional as F
+    from selective_attention.kernels.lm_ops import silu_mul
+    g = torch.Generator().manual_seed(5)
+    a = (3 * torch.randn(9, 4096, generator=g)).to(BF16)
+    c = (3 * torch.randn(9, 4096, generator=g)).to(BF16)
+    print("silu_mul", flush=True)
+    out = silu_mul(a.cuda(), c.cuda()).cpu()
+    exp = (a.cuda() * F.silu(c.cuda())).cpu()
+    assert ulp_bf16_close(out, exp, 1)
