@@ -179,6 +179,15 @@ int sa_mha_gates_bf16(const void* g, const float* thr, const float* score_std, f
                       long rows, int heads, int dim, float* log_gate, void* out_gate, void* stream);
 
 /*
+ * Small-batch linear layer of the decode steps (nn.Linear with x of at most 8
+ * rows): y (M, N) = bf16(x (M, K) . W (N, K)^T + bias (N,)), bf16, fp32
+ * accumulation; M in 1..8, K % 8 == 0, K <= 4096, x and W 16-byte aligned; bias may
+ * be NULL.
+ */
+int sa_gemv_bf16(const void* x, const void* W, const void* bias, int M, int N, int K, void* y,
+                 void* stream);
+
+/*
  * SwiGLU's gated product (modules/feed_forward.py:10-11): out = bf16(a *
  * bf16(silu(c))), n bf16 elements (n % 8 == 0, 16-byte aligned).
  */

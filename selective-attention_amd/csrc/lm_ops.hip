@@ -241,8 +241,111 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint4* __restrict__
   out[i] = uint4{r[0], r[1], r[2], r[3]};
 }
 
+// y[m, n] = bf16(sum_k x[m, k] W[n, k] + bias[n]) for M <= 8 rows (decode).
+// A 256-thread block computes 4 output columns, one per wave; x (M x K bf16)
+// is staged in LDS once per block.  Lane l of a wave streams the 16-byte
+// pieces k = 8 l + 512 j of W's row n (all of them issued before the first
+// FMA, KP <= 8 pieces: K <= 4096), takes the matching x pieces from LDS, and
+// the wave sums the M partials with xor shuffles.  fp32 accumulation.
+template <int M, int KP>
+__global__ __launch_bounds__(256) void gemv_bf16_kernel(const uint4* __restrict__ x,
+                                                        const uint4* __restrict__ W,
+                                                        const bf16* __restrict__ bias,
+                                                        bf16* __restrict__ y, int N, int K) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  uint4* xs = reinterpret_cast<uint4*>(smem_raw);   // [M][K / 8]
+  const int kv = K / 8;
+  for (int e = threadIdx.x; e < M * kv; e += 256) xs[e] = x[e];
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nr = min(n, N - 1);
+  const uint4* wr = W + static_cast<long>(nr) * kv;
+  uint4 wq[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    const int p = lane + 64 * j;
+    wq[j] = p < kv ? wr[p] : uint4{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+  float acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    const int p = lane + 64 * j;
+    if (p >= kv) break;
+    const uint32_t wu[4] = {wq[j].x, wq[j].y, wq[j].z, wq[j].w};
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint4 xq = xs[m * kv + p];
+      const uint32_t xu[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        acc[m] += bf16lo_to_f32(xu[q]) * bf16lo_to_f32(wu[q]) + bf16hi_to_f32(xu[q]) * bf16hi_to_f32(wu[q]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc[m] += __shfl_xor(acc[m], o, 64);
+  }
+  if (lane < M && n < N) {
+    float v = acc[0];
+#pragma unroll
+    for (int m = 1; m < M; ++m) v = lane == m ? acc[m] : v;
+    const float bv = bias ? to_f32(bias[n]) : 0.0f;
+    y[static_cast<long>(lane) * N + n] = from_f32<bf16>(v + bv);
+  }
+}
+
 }  // namespace
 }  // namespace sa
+
+namespace sa {
+namespace {
+template <int M>
+int launch_gemv(const uint4* x, const uint4* W, const bf16* bias, bf16* y, int N, int K,
+                hipStream_t s) {
+  const dim3 grid((N + 3) / 4);
+  const size_t smem = static_cast<size_t>(M) * K * 2;   // <= 64 KB (M <= 8, K <= 4096)
+  const int kp = (K / 8 + 63) / 64;                      // 16-byte pieces per lane
+  if (kp <= 2)
+    hipLaunchKernelGGL((gemv_bf16_kernel<M, 2>), grid, dim3(256), smem, s, x, W, bias, y, N, K);
+  else if (kp <= 4)
+    hipLaunchKernelGGL((gemv_bf16_kernel<M, 4>), grid, dim3(256), smem, s, x, W, bias, y, N, K);
+  else
+    hipLaunchKernelGGL((gemv_bf16_kernel<M, 8>), grid, dim3(256), smem, s, x, W, bias, y, N, K);
+  return 0;
+}
+}  // namespace
+}  // namespace sa
+
+extern "C" int sa_gemv_bf16(const void* x, const void* W, const void* bias, int M, int N, int K,
+                            void* y, void* stream) {
+  SA_CHECK_ARG(M >= 1 && M <= 8 && N > 0 && K > 0 && K % 8 == 0 && K * M <= 8 * 4096 && K <= 4096,
+               "sa_gemv_bf16: M %d must be 1..8 and K %d a multiple of 8, at most 4096", M, K);
+  SA_CHECK_ARG(x && W && y, "sa_gemv_bf16: null pointer");
+  SA_CHECK_ARG(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W)) & 15) == 0,
+               "sa_gemv_bf16: x and W must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  sa::ProfScope prof_("gemv", s);
+  const uint4* xv = static_cast<const uint4*>(x);
+  const uint4* wv = static_cast<const uint4*>(W);
+  const sa::bf16* bv = static_cast<const sa::bf16*>(bias);
+  sa::bf16* yv = static_cast<sa::bf16*>(y);
+  switch (M) {
+    case 1: sa::launch_gemv<1>(xv, wv, bv, yv, N, K, s); break;
+    case 2: sa::launch_gemv<2>(xv, wv, bv, yv, N, K, s); break;
+    case 3: sa::launch_gemv<3>(xv, wv, bv, yv, N, K, s); break;
+    case 4: sa::launch_gemv<4>(xv, wv, bv, yv, N, K, s); break;
+    case 5: sa::launch_gemv<5>(xv, wv, bv, yv, N, K, s); break;
+    case 6: sa::launch_gemv<6>(xv, wv, bv, yv, N, K, s); break;
+    case 7: sa::launch_gemv<7>(xv, wv, bv, yv, N, K, s); break;
+    default: sa::launch_gemv<8>(xv, wv, bv, yv, N, K, s); break;
+  }
+  SA_CHECK_LAUNCH("gemv");
+  return 0;
+}
 
 extern "C" int sa_add_rms_norm_bf16(const void* x, const void* y, const float* weight, long rows,
                                     int dim, float eps, void* out, void* nrm, void* stream) {

@@ -104,3 +104,28 @@ def silu_mul(a: torch.Tensor, c: torch.Tensor) -> torch.Tensor:
     _lib.call("sa_silu_mul_bf16", _lib.ptr(a), _lib.ptr(c), a.numel(), _lib.ptr(out),
               _lib.stream_of(a))
     return out
+
+
+def gemv_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    K = x.shape[-1]
+    return (x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
+            and weight.is_contiguous() and K % 8 == 0 and K <= 4096
+            and 0 < x.numel() // max(K, 1) <= 8
+            and weight.data_ptr() % 16 == 0)
+
+
+def gemv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    """x (..., K) with at most 8 rows, weight (N, K), bias (N,) or None, all
+    bf16 -> (..., N): the decode steps' linear layers."""
+    require_device(x, weight, bias)
+    K = x.shape[-1]
+    N = weight.shape[0]
+    xc = x.contiguous()
+    if xc.data_ptr() % 16:
+        xc = xc.clone()
+    M = xc.numel() // K
+    y = torch.empty(*x.shape[:-1], N, dtype=torch.bfloat16, device=x.device)
+    b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    _lib.call("sa_gemv_bf16", _lib.ptr(xc), _lib.ptr(weight), _lib.ptr(b), M, N, K, _lib.ptr(y),
+              _lib.stream_of(x))
+    return y

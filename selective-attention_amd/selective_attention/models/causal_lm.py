@@ -19,6 +19,7 @@ import torch
 import torch.nn as nn
 
 from ..inference import CausalBlockCache, GenerationConfig, InferenceState
+from ..modules.layers import Linear
 from ..modules import CausalBlock, RMSNorm
 from ._graph import graph_decode
 
@@ -63,7 +64,7 @@ class CausalLM(nn.Module):
                         dropout_rate=cfg.dropout_rate, device=cfg.device)
             for i in range(cfg.num_layers)])
         self.norm = RMSNorm(cfg.model_dim)
-        self.lm_head = nn.Linear(cfg.model_dim, cfg.vocab_size, bias=False)
+        self.lm_head = Linear(cfg.model_dim, cfg.vocab_size, bias=False)
         self.lm_head.weight = self.embedding.weight
 
     def to_bf16(self) -> "CausalLM":

@@ -13,6 +13,7 @@ import torch
 import torch.nn as nn
 
 from ..inference import CrossBlockCache, GenerationConfig, InferenceState
+from ..modules.layers import Linear
 from ..modules import SSM, BiBlock, CrossBlock, RMSNorm
 from ._graph import graph_decode
 
@@ -60,7 +61,7 @@ class Seq2SeqLM(nn.Module):
                        device=cfg.device)
         self.decoder_layers = nn.ModuleList([CrossBlock(layer_idx=i, **blk)
                                              for i in range(cfg.num_layers)])
-        self.lm_head = nn.Linear(cfg.model_dim, cfg.vocab_size, bias=False)
+        self.lm_head = Linear(cfg.model_dim, cfg.vocab_size, bias=False)
         self.lm_head.weight = self.embedding.weight
         self.dropout = nn.Dropout(cfg.dropout_rate)
 

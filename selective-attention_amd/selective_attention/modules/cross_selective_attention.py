@@ -19,6 +19,7 @@ import torch
 import torch.nn as nn
 
 from ..ops.attention import attn_varlen, paged_decode_attn
+from .layers import Linear
 from .selective_attention import _threshold
 
 
@@ -32,11 +33,11 @@ class CrossSelectiveMHA(nn.Module):
         self.head_dim = head_dim
         self.scale = head_dim ** -0.5
         self.log_gate_penalty = log_gate_penalty
-        self.q_proj = nn.Linear(dim, dim, bias=False)
-        self.k_proj = nn.Linear(dim, dim, bias=False)
-        self.v_proj = nn.Linear(dim, dim)
-        self.out_proj = nn.Linear(dim, dim)
-        self.select_gate_proj = nn.Linear(dim, self.num_heads)
+        self.q_proj = Linear(dim, dim, bias=False)
+        self.k_proj = Linear(dim, dim, bias=False)
+        self.v_proj = Linear(dim, dim)
+        self.out_proj = Linear(dim, dim)
+        self.select_gate_proj = Linear(dim, self.num_heads)
         self.register_buffer("score_std_ema", torch.zeros(self.num_heads))
         nn.init.constant_(self.select_gate_proj.bias, 2.0)
 

@@ -9,7 +9,21 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ..kernels.lm_ops import add_rms_norm, add_rms_norm_supported, rms_norm, rope_qk, silu_mul
+from ..kernels.lm_ops import (add_rms_norm, add_rms_norm_supported, gemv, gemv_supported,
+                              rms_norm, rope_qk, silu_mul)
+
+
+class Linear(nn.Linear):
+    """nn.Linear (same parameters and state-dict names) whose inference
+    forward on at most 8 bf16 rows, the decode steps' shape, runs the
+    small-batch GEMV kernel instead of a GEMM."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if (gemv_supported(x, self.weight)
+                and (self.bias is None or self.bias.dtype == torch.bfloat16)
+                and not (torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad))):
+            return gemv(x, self.weight, self.bias)
+        return super().forward(x)
 
 
 class RMSNorm(nn.Module):
@@ -93,9 +107,9 @@ class SwiGLU(nn.Module):
 
     def __init__(self, dim: int, hidden_dim: int):
         super().__init__()
-        self.w1 = nn.Linear(dim, hidden_dim)
-        self.w2 = nn.Linear(dim, hidden_dim)
-        self.out = nn.Linear(hidden_dim, dim)
+        self.w1 = Linear(dim, hidden_dim)
+        self.w2 = Linear(dim, hidden_dim)
+        self.out = Linear(hidden_dim, dim)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         a, c = self.w1(x), self.w2(x)

@@ -27,7 +27,7 @@ import torch.nn as nn
 from ..kernels.lm_ops import mha_gates
 from ..ops.attention import attn_varlen
 from ..ops.selective_mha import selective_mha_prefill
-from .layers import RoPE
+from .layers import Linear, RoPE
 
 
 def _threshold(thr, num_heads: int, device):
@@ -51,12 +51,12 @@ class SelectiveMHA(nn.Module):
         self.scale = head_dim ** -0.5
         self.log_gate_penalty = log_gate_penalty
 
-        self.gate_proj = nn.Linear(dim, self.num_heads + dim)
+        self.gate_proj = Linear(dim, self.num_heads + dim)
         self.rope = RoPE(head_dim)
-        self.q_proj = nn.Linear(dim, dim, bias=False)
-        self.k_proj = nn.Linear(dim, dim, bias=False)
-        self.v_proj = nn.Linear(dim, dim)
-        self.out_proj = nn.Linear(dim, dim)
+        self.q_proj = Linear(dim, dim, bias=False)
+        self.k_proj = Linear(dim, dim, bias=False)
+        self.v_proj = Linear(dim, dim)
+        self.out_proj = Linear(dim, dim)
         self.register_buffer("score_std_ema", torch.zeros(self.num_heads))
         nn.init.constant_(self.gate_proj.bias, 2.0)
 

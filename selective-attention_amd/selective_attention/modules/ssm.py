@@ -16,6 +16,7 @@ import torch
 import torch.nn as nn
 
 from ..kernels.ssm_io import ssm_conv_forward
+from .layers import Linear
 from ..ops import SSDScanGatedFn, SSMConvFn, SSMGateFn, SSUFn, ssm_conv_step
 
 
@@ -42,7 +43,7 @@ class SSM(nn.Module):
         self.delta_limit = delta_limit
         self.bc_dim = num_groups * state_dim
 
-        self.in_proj = nn.Linear(model_dim, 2 * self.inner_dim + 2 * self.bc_dim + self.num_heads)
+        self.in_proj = Linear(model_dim, 2 * self.inner_dim + 2 * self.bc_dim + self.num_heads)
         conv_dim = self.inner_dim + 2 * self.bc_dim
         self.conv = nn.Conv1d(conv_dim, conv_dim, conv_kernel_size, groups=conv_dim,
                               padding=conv_kernel_size - 1)
@@ -59,7 +60,7 @@ class SSM(nn.Module):
         self.D = nn.Parameter(torch.ones(self.inner_dim))
         self.D._no_weight_decay = True
 
-        self.out_proj = nn.Linear(self.inner_dim, model_dim)
+        self.out_proj = Linear(self.inner_dim, model_dim)
         self.dropout = nn.Dropout(dropout_rate)
 
     def _A(self) -> torch.Tensor:

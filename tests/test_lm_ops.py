@@ -172,3 +172,44 @@ def test_silu_mul_kernel():
     out = silu_mul(a.cuda(), c.cuda()).cpu()
     exp = (a.cuda() * F.silu(c.cuda())).cpu()
     assert ulp_bf16_close(out, exp, 1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,bias", [(1, 1040, 1024, True), (4, 4384, 1024, True),
+                                        (5, 1024, 4096, True), (8, 32000, 1024, False),
+                                        (4, 32000, 1024, False),
+                                        (3, 100, 2048, False)])
+def test_gemv_kernel(M, N, K, bias):
+    """The decode linear layers: within one bf16 ulp of the exactly rounded
+    product (fp32 accumulation), for every M the kernel instantiates."""
+    from selective_attention.kernels.lm_ops import gemv
+    g = torch.Generator().manual_seed(M * 7 + N)
+    x = torch.randn(M, K, generator=g).to(BF16)
+    W = (torch.randn(N, K, generator=g) / K ** 0.5).to(BF16)
+    b = torch.randn(N, generator=g).to(BF16) if bias else None
+    print(f"gemv M={M} N={N} K={K}", flush=True)
+    y = gemv(x.cuda(), W.cuda(), None if b is None else b.cuda()).cpu()
+    exact = x.double() @ W.double().T + (0 if b is None else b.double())
+    # one bf16 ulp of the exact value plus the fp32 accumulation bound
+    # K * 2^-24 * sum_k |x_k w_k| (matters where the sum cancels to ~0)
+    mag = x.double().abs() @ W.double().abs().T
+    ulp = torch.ldexp(torch.ones_like(exact), torch.frexp(exact.abs().clamp_min(1e-30)).exponent - 8)
+    err = (y.double() - exact).abs()
+    bound = ulp + K * 2.0 ** -24 * mag
+    worst = (err / bound).max().item()
+    assert worst <= 1.0, f"worst err/bound {worst:.3f} (max err {err.max().item():.3e})"
+
+
+@pytest.mark.gpu
+def test_linear_dispatch():
+    """Linear runs the GEMV for <= 8 bf16 rows in inference and the GEMM
+    otherwise; both agree with F.linear to bf16 rounding."""
+    import torch.nn.functional as F
+    from selective_attention.modules.layers import Linear
+    lin = Linear(512, 768).cuda().to(BF16)
+    for rows in (4, 9):
+        x = torch.randn(rows, 512, device="cuda").to(BF16)
+        with torch.no_grad():
+            y = lin(x)
+            e = F.linear(x.float(), lin.weight.float(), lin.bias.float())
+        assert ulp_bf16_close(y.cpu(), e.to(BF16).cpu(), 1)
