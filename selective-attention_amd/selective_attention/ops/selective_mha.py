@@ -133,13 +133,16 @@ class PagedSelectiveAttnCache:
         self.max_pages *= 2
         self._pt_dirty = True
 
-    def _alloc(self) -> int:
+    def _alloc(self, fill: bool = True) -> int:
+        """A free page; its gates are reset to -inf unless the caller writes
+        every slot itself (or resets a batch of pages at once)."""
         if not self.free:
             if not self.grow:
                 raise RuntimeError("PagedSelectiveAttnCache: page pool exhausted")
             self._grow()
         pid = self.free.pop()
-        self.gate_pages[pid].fill_(float("-inf"))
+        if fill:
+            self.gate_pages[pid].fill_(float("-inf"))
         return pid
 
     def _slot(self, i: int, t: int):
@@ -181,7 +184,7 @@ class PagedSelectiveAttnCache:
                 self.free.append(pid)
             n = lens[i]
             npg = (n + ps - 1) // ps
-            pids = [self._alloc() for _ in range(npg)]
+            pids = [self._alloc(fill=False) for _ in range(npg)]   # every slot written below
             self.rows[i] = pids
             self.lens[i] = n
             self._pt_dirty = self._sl_dirty = True
@@ -207,8 +210,16 @@ class PagedSelectiveAttnCache:
         most `extra_tokens` appends may follow (a row that runs past its pages
         writes into its last page instead of faulting)."""
         if extra_tokens > 0:
+            fresh = []
             for i in range(self.b):
-                self._slot(i, self.lens[i] + extra_tokens - 1)
+                need = (self.lens[i] + extra_tokens + self.ps - 1) // self.ps
+                while len(self.rows[i]) < need:
+                    pid = self._alloc(fill=False)
+                    self.rows[i].append(pid)
+                    fresh.append(pid)
+            if fresh:   # reset the new pages' gates in one launch
+                self.gate_pages[torch.tensor(fresh, device=self.device)] = float("-inf")
+                self._pt_dirty = True
         self.page_table()
         self.lens_dev = torch.tensor(self.lens, dtype=torch.int32).to(self.device)
 
