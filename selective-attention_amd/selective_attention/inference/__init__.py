@@ -87,7 +87,12 @@ class SelectiveAttnCache:
 
     @property
     def write_idx(self) -> int:
-        return 0 if self.pages is None else max(self.pages.lens)
+        """Tokens held by the longest row (the reference's cache length)."""
+        if self.pages is None:
+            return 0
+        if self.pages.lens_dev is not None:
+            return int(self.pages.lens_dev.max())
+        return max(self.pages.lens)
 
 
 class CrossSelectiveAttnCache:

@@ -268,18 +268,26 @@ class PagedSelectiveAttnCache:
 
     def drop_evicted_pages(self) -> int:
         """The reference's periodic compaction (_reset_cache :11-25) as a page
-        table rewrite: every full page (not the newest one) whose keys all heads
-        have dropped (-inf gate) leaves the row's page list.  Returns the number
-        of pages freed (0 in device mode, where the page table is fixed)."""
+        table rewrite: every full page before the one holding the row's newest
+        token whose keys all heads have dropped (-inf gate) leaves the row's
+        page list (pages reserved past the newest token hold no tokens and
+        stay).  Returns the number of pages freed (0 in device mode, where the
+        page table is fixed)."""
         if self.lens_dev is not None:
             return 0
+        # one device check for every candidate page of every row
+        cand = [(i, j, pages[j]) for i, pages in enumerate(self.rows)
+                for j in range(max(0, (self.lens[i] - 1) // self.ps))]
+        if not cand:
+            return 0
+        ids = torch.tensor([pid for _, _, pid in cand], device=self.device)
+        dead = torch.isinf(self.gate_pages[ids]).flatten(1).all(dim=1).tolist()
+        drop = {(i, j) for (i, j, _), d in zip(cand, dead) if d}
         freed = 0
         for i in range(self.b):
             keep = []
-            pages = self.rows[i]
-            for p_idx, pid in enumerate(pages):
-                last = p_idx == len(pages) - 1
-                if not last and bool(torch.isinf(self.gate_pages[pid]).all()):
+            for j, pid in enumerate(self.rows[i]):
+                if (i, j) in drop:
                     self.free.append(pid)
                     self.lens[i] -= self.ps
                     freed += 1

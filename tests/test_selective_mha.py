@@ -235,3 +235,17 @@ def test_selective_mha_prefill_view_input():
     torch.cuda.synchronize()
     assert torch.equal(o1.cpu(), o2.cpu())
     assert (o1[1, :, 99:] == 0).all()
+
+
+def test_drop_evicted_pages_keeps_reserved_pages():
+    """Pages reserved past a row's newest token (enter_device_mode) hold no
+    tokens: compaction must neither free them nor shorten the row."""
+    cache = PagedSelectiveAttnCache(1, 1, 8, max_tokens=64 * 6, device="cpu")
+    z = torch.zeros(1, 1, 130, 8)
+    lg = torch.zeros(1, 1, 130)
+    lg[0, 0, :64] = float("-inf")                     # page 0 fully dropped
+    cache.build(z, z, lg)
+    cache.rows[0] += [cache._alloc(), cache._alloc()]  # reserve two empty pages
+    assert cache.drop_evicted_pages() == 1
+    assert cache.lens == [66] and len(cache.rows[0]) == 4
+    assert cache.drop_evicted_pages() == 0 and cache.lens == [66]
