@@ -4,8 +4,9 @@ final RMSNorm, LM head tied to the embedding; forward, step and greedy
 generate with the reference's interfaces.
 
 Precision: to_bf16() puts the matmul weights and activations in bfloat16
-and keeps the SSM's A_log / delta_bias / D, the RMSNorm weights and the
-attention score statistics in float32 (all are per-channel vectors).
+and keeps the SSM's A_log / delta_bias / D and conv weights, the RMSNorm
+weights and the attention score statistics in float32 (all are per-channel
+vectors); RoPE's frequencies and angles are fp32 whatever the module dtype.
 Not built: training through SelectiveMHA (no attention backward kernel),
 the gate-analysis statistics and compute_attn_gate_threshold (calibration
 runs on analysis histograms, outside the kernel path).
@@ -70,8 +71,8 @@ class CausalLM(nn.Module):
     def to_bf16(self) -> "CausalLM":
         self.to(torch.bfloat16)
         for blk in self.layers:
-            for p in (blk.ssm.A_log, blk.ssm.delta_bias, blk.ssm.D, blk.norm1.weight,
-                      blk.norm2.weight, blk.norm3.weight):
+            for p in (blk.ssm.A_log, blk.ssm.delta_bias, blk.ssm.D, blk.ssm.conv.weight,
+                      blk.ssm.conv.bias, blk.norm1.weight, blk.norm2.weight, blk.norm3.weight):
                 p.data = p.data.float()
             blk.mha.score_std_ema.data = blk.mha.score_std_ema.data.float()
         self.norm.weight.data = self.norm.weight.data.float()

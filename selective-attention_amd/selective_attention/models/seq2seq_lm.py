@@ -67,7 +67,8 @@ class Seq2SeqLM(nn.Module):
 
     def to_bf16(self) -> "Seq2SeqLM":
         fp32 = [p for n, p in self.named_parameters()
-                if n.endswith(("A_log", "delta_bias", ".D")) or "norm" in n]
+                if n.endswith(("A_log", "delta_bias", ".D", "ssm.conv.weight", "ssm.conv.bias"))
+                or "norm" in n]
         keep = {id(p): p.data.clone() for p in fp32}
         self.to(torch.bfloat16)
         for p in fp32:

@@ -78,9 +78,22 @@ class RoPE(nn.Module):
         half = dim // 2
         inv_freq = 1.0 / (base ** (torch.arange(0, half, dtype=torch.float32) / half))
         self.register_buffer("inv_freq", inv_freq, persistent=False)
+        # fp32 copy kept outside Module.to(): casting the model to bf16 casts
+        # the buffer too, and bf16 frequencies put the angle off by radians at
+        # positions in the thousands
+        self._inv_fp32 = {}
+
+    def freqs(self, device) -> torch.Tensor:
+        """The inverse frequencies in fp32 on `device` (computed once per device)."""
+        key = str(device)
+        if key not in self._inv_fp32:
+            half = self.dim // 2
+            f = 1.0 / (self.base ** (torch.arange(0, half, dtype=torch.float32) / half))
+            self._inv_fp32[key] = f.to(device)
+        return self._inv_fp32[key]
 
     def cos_sin(self, positions: torch.Tensor):
-        ang = positions.to(torch.float32).unsqueeze(-1) * self.inv_freq.unsqueeze(0)
+        ang = positions.to(torch.float32).unsqueeze(-1) * self.freqs(positions.device).unsqueeze(0)
         ang = torch.cat([ang, ang], dim=-1)
         return torch.cos(ang), torch.sin(ang)
 
@@ -99,7 +112,7 @@ class RoPE(nn.Module):
         """q, k (..., heads, head_dim) on the GPU, rotated in one fused kernel
         and returned in bf16; row r of the leading dimensions at
         positions[r % period], or at r % period when positions is None."""
-        return rope_qk(q, k, self.inv_freq, positions, period)
+        return rope_qk(q, k, self.freqs(q.device), positions, period)
 
 
 class SwiGLU(nn.Module):

@@ -213,3 +213,17 @@ def test_linear_dispatch():
             y = lin(x)
             e = F.linear(x.float(), lin.weight.float(), lin.bias.float())
         assert ulp_bf16_close(y.cpu(), e.to(BF16).cpu(), 1)
+
+
+@pytest.mark.gpu
+def test_rope_keeps_fp32_frequencies_after_bf16_cast():
+    """Casting the module to bf16 must not round RoPE's frequencies: at
+    position 8192 a bf16 frequency puts the angle off by radians."""
+    rope = RoPE(64).cuda().to(BF16)
+    assert rope.inv_freq.dtype == BF16                  # the registered buffer is cast ...
+    q = torch.randn(1, 2, 64, device="cuda").to(BF16)
+    pos = torch.tensor([8191], device="cuda")
+    yq, _ = rope.rotate_qk(q, q, pos, 1)
+    ref = RoPE(64)                                       # ... the rotation still uses fp32 ones
+    eq, _ = ref(q.float().cpu(), q.float().cpu(), pos.cpu(), "pos")
+    assert ulp_bf16_close(yq.cpu(), eq.to(BF16), 1)
