@@ -16,9 +16,17 @@ Extra fields on the same JSON line:
   cpu_baseline  the CPU restatement (oracle/ssd.py, fp32 torch) of the same
                 fwd+bwd on a bounded sample (one batch row), on this host.
   decode        config 3 decode step (paged GQA attention + state update),
-                us/step, when those ops are built.
+                us/step, against the HBM roofline.
+  sparse_attn   config 2 block-sparse varlen attention, against bf16 MFMA.
+  ssm_io        the SSM block's conv prologue and gate epilogue at config 1's
+                model shapes, and the scan with the epilogue fused.
+  selective_mha SelectiveMHA's prefill and paged decode at config 4's
+                attention shapes.
+  causal_lm     config 4: the hybrid LM's batch-4 prefill of 8192 tokens and
+                256 greedy decode steps (decode step replayed from a graph).
+  seq2seq       the seq2seq LM at config 4's dimensions (synthetic workload).
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--ssd-only]
 """
 from __future__ import annotations
 
