@@ -188,6 +188,24 @@ int sa_gemv_bf16(const void* x, const void* W, const void* bias, int M, int N, i
                  void* stream);
 
 /*
+ * Several small-batch linear layers of the same x in one launch (the decode
+ * step's gate/q/k/v projections of SelectiveMHA.step,
+ * modules/selective_attention.py:370,380-382; SwiGLU's two input
+ * projections, modules/feed_forward.py:11-12; the three row blocks of
+ * SSM.in_proj that SSM.step splits, modules/ssm.py:163-165): for i < nseg
+ * (1..4),
+ * y[i] (M, N[i]) = bf16(xs (M, K) . W[i] (N[i], K)^T + bias[i]), each y[i]
+ * contiguous.  xs = x, or bf16(x * xscale) elementwise when xscale (M, K)
+ * bf16 is not NULL (the out_gate product before out_proj,
+ * modules/selective_attention.py:446).  bias
+ * may be NULL (no biases) or hold NULL entries.  Limits as sa_gemv_bf16;
+ * the pointer arrays are read on the host during the call.
+ */
+int sa_gemv_bf16_multi(const void* x, const void* xscale, int M, int K, int nseg,
+                       const void* const* W, const void* const* bias, const int* N, void* const* y,
+                       void* stream);
+
+/*
  * SwiGLU's gated product (modules/feed_forward.py:10-11): out = bf16(a *
  * bf16(silu(c))), n bf16 elements (n % 8 == 0, 16-byte aligned).
  */

@@ -241,25 +241,55 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint4* __restrict__
   out[i] = uint4{r[0], r[1], r[2], r[3]};
 }
 
-// y[m, n] = bf16(sum_k x[m, k] W[n, k] + bias[n]) for M <= 8 rows (decode).
-// A 256-thread block computes 4 output columns, one per wave; x (M x K bf16)
-// is staged in LDS once per block.  Lane l of a wave streams the 16-byte
-// pieces k = 8 l + 512 j of W's row n (all of them issued before the first
-// FMA, KP <= 8 pieces: K <= 4096), takes the matching x pieces from LDS, and
-// the wave sums the M partials with xor shuffles.  fp32 accumulation.
+// y[m, n] = bf16(sum_k x[m, k] W[n, k] + bias[n]) for M <= 8 rows (decode),
+// for up to kGemvSegs weight matrices of the same x in one launch (segment i:
+// W_i (N_i, K), bias_i, its own contiguous output y_i (M, N_i); blocks
+// blk0[i] .. blk0[i+1]-1 compute its columns).  A 256-thread block computes 4
+// output columns, one per wave; x (M x K bf16) is staged in LDS once per
+// block, optionally times xscale (M x K bf16) and rounded to bf16, i.e. the
+// bf16 product x * xscale.  Lane l of a wave streams the 16-byte pieces
+// k = 8 l + 512 j of W's row n (all of them issued before the first FMA,
+// KP <= 8 pieces: K <= 4096), takes the matching x pieces from LDS, and the
+// wave sums the M partials with xor shuffles.  fp32 accumulation.
+constexpr int kGemvSegs = 4;
+struct GemvSegs {
+  const uint4* W[kGemvSegs];
+  const bf16* bias[kGemvSegs];
+  bf16* y[kGemvSegs];
+  int N[kGemvSegs];
+  int blk0[kGemvSegs + 1];
+  int nseg;
+};
+
+__device__ __forceinline__ uint32_t mul_bf16x2(uint32_t a, uint32_t b) {
+  return pack_bf16x2(bf16lo_to_f32(a) * bf16lo_to_f32(b), bf16hi_to_f32(a) * bf16hi_to_f32(b));
+}
+
 template <int M, int KP>
 __global__ __launch_bounds__(256) void gemv_bf16_kernel(const uint4* __restrict__ x,
-                                                        const uint4* __restrict__ W,
-                                                        const bf16* __restrict__ bias,
-                                                        bf16* __restrict__ y, int N, int K) {
+                                                        const uint4* __restrict__ xscale,
+                                                        const GemvSegs sg, int K) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   uint4* xs = reinterpret_cast<uint4*>(smem_raw);   // [M][K / 8]
   const int kv = K / 8;
-  for (int e = threadIdx.x; e < M * kv; e += 256) xs[e] = x[e];
+  for (int e = threadIdx.x; e < M * kv; e += 256) {
+    uint4 v = x[e];
+    if (xscale) {
+      const uint4 g = xscale[e];
+      v = uint4{mul_bf16x2(v.x, g.x), mul_bf16x2(v.y, g.y), mul_bf16x2(v.z, g.z), mul_bf16x2(v.w, g.w)};
+    }
+    xs[e] = v;
+  }
+  // this block's segment (block-uniform)
+  const int bid = blockIdx.x;
+  int seg = 0;
+#pragma unroll
+  for (int i = 1; i < kGemvSegs; ++i) seg += (i < sg.nseg && bid >= sg.blk0[i]) ? 1 : 0;
+  const int N = sg.N[seg];
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n = (bid - sg.blk0[seg]) * 4 + (threadIdx.x >> 6);
   const int nr = min(n, N - 1);
-  const uint4* wr = W + static_cast<long>(nr) * kv;
+  const uint4* wr = sg.W[seg] + static_cast<long>(nr) * kv;
   uint4 wq[KP];
 #pragma unroll
   for (int j = 0; j < KP; ++j) {
@@ -293,8 +323,9 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(const uint4* __restrict_
     float v = acc[0];
 #pragma unroll
     for (int m = 1; m < M; ++m) v = lane == m ? acc[m] : v;
+    const bf16* bias = sg.bias[seg];
     const float bv = bias ? to_f32(bias[n]) : 0.0f;
-    y[static_cast<long>(lane) * N + n] = from_f32<bf16>(v + bv);
+    sg.y[seg][static_cast<long>(lane) * N + n] = from_f32<bf16>(v + bv);
   }
 }
 
@@ -304,17 +335,59 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(const uint4* __restrict_
 namespace sa {
 namespace {
 template <int M>
-int launch_gemv(const uint4* x, const uint4* W, const bf16* bias, bf16* y, int N, int K,
-                hipStream_t s) {
-  const dim3 grid((N + 3) / 4);
+void launch_gemv(const uint4* x, const uint4* xscale, const GemvSegs& sg, int K, hipStream_t s) {
+  const dim3 grid(sg.blk0[sg.nseg]);
   const size_t smem = static_cast<size_t>(M) * K * 2;   // <= 64 KB (M <= 8, K <= 4096)
   const int kp = (K / 8 + 63) / 64;                      // 16-byte pieces per lane
   if (kp <= 2)
-    hipLaunchKernelGGL((gemv_bf16_kernel<M, 2>), grid, dim3(256), smem, s, x, W, bias, y, N, K);
+    hipLaunchKernelGGL((gemv_bf16_kernel<M, 2>), grid, dim3(256), smem, s, x, xscale, sg, K);
   else if (kp <= 4)
-    hipLaunchKernelGGL((gemv_bf16_kernel<M, 4>), grid, dim3(256), smem, s, x, W, bias, y, N, K);
+    hipLaunchKernelGGL((gemv_bf16_kernel<M, 4>), grid, dim3(256), smem, s, x, xscale, sg, K);
   else
-    hipLaunchKernelGGL((gemv_bf16_kernel<M, 8>), grid, dim3(256), smem, s, x, W, bias, y, N, K);
+    hipLaunchKernelGGL((gemv_bf16_kernel<M, 8>), grid, dim3(256), smem, s, x, xscale, sg, K);
+}
+
+int gemv_run(const char* who, const void* x, const void* xscale, int M, int K, int nseg,
+             const void* const* W, const void* const* bias, const int* N, void* const* y,
+             void* stream) {
+  SA_CHECK_ARG(M >= 1 && M <= 8 && K > 0 && K % 8 == 0 && K <= 4096,
+               "%s: M %d must be 1..8 and K %d a multiple of 8, at most 4096", who, M, K);
+  SA_CHECK_ARG(nseg >= 1 && nseg <= kGemvSegs, "%s: %d weight matrices, 1..%d allowed", who, nseg,
+               kGemvSegs);
+  SA_CHECK_ARG(x && W && N && y, "%s: null pointer", who);
+  SA_CHECK_ARG(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(xscale)) & 15) == 0,
+               "%s: x and xscale must be 16-byte aligned", who);
+  GemvSegs sg{};
+  sg.nseg = nseg;
+  sg.blk0[0] = 0;
+  for (int i = 0; i < nseg; ++i) {
+    SA_CHECK_ARG(W[i] && y[i] && N[i] > 0, "%s: weight matrix %d: null pointer or N %d", who, i,
+                 N[i]);
+    SA_CHECK_ARG((reinterpret_cast<uintptr_t>(W[i]) & 15) == 0, "%s: W %d must be 16-byte aligned",
+                 who, i);
+    SA_CHECK_ARG(sg.blk0[i] + (N[i] + 3) / 4 < (1 << 30), "%s: too many columns", who);
+    sg.W[i] = static_cast<const uint4*>(W[i]);
+    sg.bias[i] = bias ? static_cast<const bf16*>(bias[i]) : nullptr;
+    sg.y[i] = static_cast<bf16*>(y[i]);
+    sg.N[i] = N[i];
+    sg.blk0[i + 1] = sg.blk0[i] + (N[i] + 3) / 4;
+  }
+  for (int i = nseg; i < kGemvSegs; ++i) sg.blk0[i + 1] = sg.blk0[nseg];
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  ProfScope prof_("gemv", s);
+  const uint4* xv = static_cast<const uint4*>(x);
+  const uint4* gv = static_cast<const uint4*>(xscale);
+  switch (M) {
+    case 1: launch_gemv<1>(xv, gv, sg, K, s); break;
+    case 2: launch_gemv<2>(xv, gv, sg, K, s); break;
+    case 3: launch_gemv<3>(xv, gv, sg, K, s); break;
+    case 4: launch_gemv<4>(xv, gv, sg, K, s); break;
+    case 5: launch_gemv<5>(xv, gv, sg, K, s); break;
+    case 6: launch_gemv<6>(xv, gv, sg, K, s); break;
+    case 7: launch_gemv<7>(xv, gv, sg, K, s); break;
+    default: launch_gemv<8>(xv, gv, sg, K, s); break;
+  }
+  SA_CHECK_LAUNCH(who);
   return 0;
 }
 }  // namespace
@@ -322,29 +395,13 @@ int launch_gemv(const uint4* x, const uint4* W, const bf16* bias, bf16* y, int N
 
 extern "C" int sa_gemv_bf16(const void* x, const void* W, const void* bias, int M, int N, int K,
                             void* y, void* stream) {
-  SA_CHECK_ARG(M >= 1 && M <= 8 && N > 0 && K > 0 && K % 8 == 0 && K * M <= 8 * 4096 && K <= 4096,
-               "sa_gemv_bf16: M %d must be 1..8 and K %d a multiple of 8, at most 4096", M, K);
-  SA_CHECK_ARG(x && W && y, "sa_gemv_bf16: null pointer");
-  SA_CHECK_ARG(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W)) & 15) == 0,
-               "sa_gemv_bf16: x and W must be 16-byte aligned");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  sa::ProfScope prof_("gemv", s);
-  const uint4* xv = static_cast<const uint4*>(x);
-  const uint4* wv = static_cast<const uint4*>(W);
-  const sa::bf16* bv = static_cast<const sa::bf16*>(bias);
-  sa::bf16* yv = static_cast<sa::bf16*>(y);
-  switch (M) {
-    case 1: sa::launch_gemv<1>(xv, wv, bv, yv, N, K, s); break;
-    case 2: sa::launch_gemv<2>(xv, wv, bv, yv, N, K, s); break;
-    case 3: sa::launch_gemv<3>(xv, wv, bv, yv, N, K, s); break;
-    case 4: sa::launch_gemv<4>(xv, wv, bv, yv, N, K, s); break;
-    case 5: sa::launch_gemv<5>(xv, wv, bv, yv, N, K, s); break;
-    case 6: sa::launch_gemv<6>(xv, wv, bv, yv, N, K, s); break;
-    case 7: sa::launch_gemv<7>(xv, wv, bv, yv, N, K, s); break;
-    default: sa::launch_gemv<8>(xv, wv, bv, yv, N, K, s); break;
-  }
-  SA_CHECK_LAUNCH("gemv");
-  return 0;
+  return sa::gemv_run("sa_gemv_bf16", x, nullptr, M, K, 1, &W, &bias, &N, &y, stream);
+}
+
+extern "C" int sa_gemv_bf16_multi(const void* x, const void* xscale, int M, int K, int nseg,
+                                  const void* const* W, const void* const* bias, const int* N,
+                                  void* const* y, void* stream) {
+  return sa::gemv_run("sa_gemv_bf16_multi", x, xscale, M, K, nseg, W, bias, N, y, stream);
 }
 
 extern "C" int sa_add_rms_norm_bf16(const void* x, const void* y, const float* weight, long rows,

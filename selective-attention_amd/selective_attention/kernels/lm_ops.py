@@ -129,3 +129,39 @@ def gemv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> to
     _lib.call("sa_gemv_bf16", _lib.ptr(xc), _lib.ptr(weight), _lib.ptr(b), M, N, K, _lib.ptr(y),
               _lib.stream_of(x))
     return y
+
+
+def gemv_multi(x: torch.Tensor, weights, biases, xscale: torch.Tensor | None = None):
+    """x (..., K) with at most 8 rows; weights: 1..4 bf16 (N_i, K) matrices
+    (contiguous, 16-byte aligned: row blocks of one weight qualify); biases:
+    matching (N_i,) bf16 tensors or None -> [(..., N_i)], one launch.  With
+    xscale (same shape as x) the product bf16(x * xscale) is the input."""
+    import ctypes
+    require_device(x, *weights)
+    K = x.shape[-1]
+    n = len(weights)
+    if not 1 <= n <= 4:
+        raise ValueError(f"gemv_multi: 1..4 weight matrices, got {n}")
+    for w in weights:
+        if w.shape[-1] != K or not gemv_supported(x, w):
+            raise ValueError(f"gemv_multi: weight {tuple(w.shape)} does not fit x {tuple(x.shape)}")
+    xc = x.contiguous()
+    if xc.data_ptr() % 16:
+        xc = xc.clone()
+    gc = None
+    if xscale is not None:
+        if xscale.shape != x.shape or xscale.dtype != torch.bfloat16:
+            raise ValueError("gemv_multi: xscale must be bf16 of x's shape")
+        gc = xscale.contiguous()
+        if gc.data_ptr() % 16:
+            gc = gc.clone()
+    M = xc.numel() // K
+    ys = [torch.empty(*x.shape[:-1], w.shape[0], dtype=torch.bfloat16, device=x.device)
+          for w in weights]
+    bs = [None if b is None else b.to(torch.bfloat16).contiguous() for b in biases]
+    arr = ctypes.c_void_p * n
+    _lib.call("sa_gemv_bf16_multi", _lib.ptr(xc), _lib.ptr(gc), M, K, n,
+              arr(*[w.data_ptr() for w in weights]), arr(*[_lib.ptr(b) for b in bs]),
+              (ctypes.c_int * n)(*[w.shape[0] for w in weights]),
+              arr(*[y.data_ptr() for y in ys]), _lib.stream_of(x))
+    return ys

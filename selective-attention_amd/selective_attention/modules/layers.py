@@ -9,8 +9,14 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ..kernels.lm_ops import (add_rms_norm, add_rms_norm_supported, gemv, gemv_supported,
-                              rms_norm, rope_qk, silu_mul)
+from ..kernels.lm_ops import (add_rms_norm, add_rms_norm_supported, gemv, gemv_multi,
+                              gemv_supported, rms_norm, rope_qk, silu_mul)
+
+
+def _gemv_ok(x: torch.Tensor, lin: nn.Linear) -> bool:
+    return (gemv_supported(x, lin.weight)
+            and (lin.bias is None or lin.bias.dtype == torch.bfloat16)
+            and not (torch.is_grad_enabled() and (x.requires_grad or lin.weight.requires_grad)))
 
 
 class Linear(nn.Linear):
@@ -19,11 +25,28 @@ class Linear(nn.Linear):
     small-batch GEMV kernel instead of a GEMM."""
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if (gemv_supported(x, self.weight)
-                and (self.bias is None or self.bias.dtype == torch.bfloat16)
-                and not (torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad))):
+        if _gemv_ok(x, self):
             return gemv(x, self.weight, self.bias)
         return super().forward(x)
+
+    def split_forward(self, x: torch.Tensor, sizes) -> list:
+        """torch.split(self(x), sizes, dim=-1).  On the decode shape the
+        weight's row blocks go to one multi-GEMV launch that writes each
+        piece as its own contiguous tensor (no copies of split views)."""
+        if _gemv_ok(x, self) and len(sizes) <= 4:
+            bs = [None] * len(sizes) if self.bias is None else torch.split(self.bias, sizes)
+            return gemv_multi(x, torch.split(self.weight, sizes), bs)
+        return list(torch.split(self(x), sizes, dim=-1))
+
+
+def project(x: torch.Tensor, linears, xscale: torch.Tensor | None = None) -> list:
+    """[lin(x * xscale if xscale is given else x) for lin in linears]: one
+    multi-GEMV launch on the decode shape (at most 4 layers), where the
+    product x * xscale is taken in bf16 as torch does."""
+    if len(linears) <= 4 and all(_gemv_ok(x, lin) for lin in linears):
+        return gemv_multi(x, [lin.weight for lin in linears], [lin.bias for lin in linears], xscale)
+    xs = x if xscale is None else x * xscale
+    return [lin(xs) for lin in linears]
 
 
 class RMSNorm(nn.Module):
@@ -125,7 +148,7 @@ class SwiGLU(nn.Module):
         self.out = Linear(hidden_dim, dim)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        a, c = self.w1(x), self.w2(x)
+        a, c = project(x, [self.w1, self.w2])
         if (a.is_cuda and a.dtype == torch.bfloat16 and c.dtype == torch.bfloat16
                 and a.numel() % 8 == 0
                 and not (torch.is_grad_enabled() and (a.requires_grad or c.requires_grad))):

@@ -27,7 +27,7 @@ import torch.nn as nn
 from ..kernels.lm_ops import mha_gates
 from ..ops.attention import attn_varlen
 from ..ops.selective_mha import selective_mha_prefill
-from .layers import Linear, RoPE
+from .layers import Linear, RoPE, project
 
 
 def _threshold(thr, num_heads: int, device):
@@ -149,7 +149,7 @@ class SelectiveMHA(nn.Module):
             thr = _threshold(gen_cfg.attn_gate_thresholds[self.layer_idx], H, dev)
         if state.step % gen_cfg.cache_update_interval == 0:
             cache.compact()
-        g = self.gate_proj(hidden_states)
+        g, q, k, v = project(hidden_states, [self.gate_proj, self.q_proj, self.k_proj, self.v_proj])
         if g.is_cuda and g.dtype == torch.bfloat16:
             # sigmoid, split, threshold and log-gate in one kernel
             log_gate, out_gate = mha_gates(g, thr, self.score_std_ema, self.log_gate_penalty, H)
@@ -159,10 +159,8 @@ class SelectiveMHA(nn.Module):
             if thr is not None:
                 kept &= select_gate >= thr[None, :]
             log_gate = self._log_gate(select_gate, kept)
-        q = self.q_proj(hidden_states).view(b, H, D)
-        k = self.k_proj(hidden_states).view(b, H, D)
-        v = self.v_proj(hidden_states).view(b, H, D)
+        q, k, v = q.view(b, H, D), k.view(b, H, D), v.view(b, H, D)
         q, k = self.rope.rotate_qk(q, k, state.lengths.to(dev), b)
         cache.update_kv(k, v.to(torch.bfloat16), log_gate)
         out = cache.attend(q).reshape(b, self.dim).to(hidden_states.dtype)
-        return self.out_proj(out * out_gate)
+        return project(out, [self.out_proj], xscale=out_gate)[0]

@@ -113,7 +113,8 @@ class SSM(nn.Module):
         """hidden_states (batch_size, model_dim) -> (batch_size, model_dim);
         cache.conv_ctx and cache.h are updated in place."""
         b = hidden_states.shape[0]
-        hBC, gate, delta_raw = self._split(self.in_proj(hidden_states))
+        hBC, gate, delta_raw = self.in_proj.split_forward(
+            hidden_states, [self.inner_dim + 2 * self.bc_dim, self.inner_dim, self.num_heads])
         x, B, C = ssm_conv_step(hBC, cache.conv_ctx, self.conv.weight, self.conv.bias,
                                 self.inner_dim, self.bc_dim)
         A = self._A()

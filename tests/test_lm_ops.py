@@ -201,6 +201,45 @@ def test_gemv_kernel(M, N, K, bias):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_gemv_multi_matches_single(M):
+    """One launch over several weight matrices (sizes not multiples of the
+    block's 4 columns, biases present and absent, one matrix a row block of
+    another) equals the single-matrix GEMV bit for bit; with xscale it equals
+    the GEMV of the bf16 product x * xscale (torch's rounding of it)."""
+    from selective_attention.kernels.lm_ops import gemv, gemv_multi
+    K = 1024
+    g = torch.Generator().manual_seed(40 + M)
+    x = torch.randn(M, K, generator=g).to(BF16).cuda()
+    s = torch.randn(M, K, generator=g).to(BF16).cuda()
+    big = (torch.randn(4384, K, generator=g) / K ** 0.5).to(BF16).cuda()
+    Ws = list(torch.split(big, [2304, 2048, 32]))
+    Ws.append((torch.randn(1041, K, generator=g) / K ** 0.5).to(BF16).cuda())
+    bs = [torch.randn(W.shape[0], generator=g).to(BF16).cuda() if i != 1 else None
+          for i, W in enumerate(Ws)]
+    print(f"gemv_multi M={M} K={K} N={[W.shape[0] for W in Ws]}", flush=True)
+    for xscale in (None, s):
+        ys = gemv_multi(x, Ws, bs, xscale)
+        xin = x if xscale is None else x * xscale
+        for W, b, y in zip(Ws, bs, ys):
+            assert y.is_contiguous() and y.shape == (M, W.shape[0])
+            assert torch.equal(y, gemv(xin, W, b))
+
+
+def test_gemv_multi_rejects_bad_counts():
+    """Argument errors come back as errors before anything is launched."""
+    import ctypes
+    from selective_attention import _lib
+    arr = ctypes.c_void_p * 1
+    with pytest.raises(RuntimeError, match="weight matrices"):
+        _lib.call("sa_gemv_bf16_multi", 16, None, 1, 64, 0, arr(16), arr(None),
+                  (ctypes.c_int * 1)(4), arr(16), None)
+    with pytest.raises(RuntimeError, match="weight matrix 0"):
+        _lib.call("sa_gemv_bf16_multi", 16, None, 1, 64, 1, arr(16), arr(None),
+                  (ctypes.c_int * 1)(0), arr(16), None)
+
+
+@pytest.mark.gpu
 def test_linear_dispatch():
     """Linear runs the GEMV for <= 8 bf16 rows in inference and the GEMM
     otherwise; both agree with F.linear to bf16 rounding."""
