@@ -62,6 +62,20 @@ int sa_ssu_fwd(int dtype, const void* u, const float* A, const void* B, const vo
                float delta_min, float delta_max, void* stream);
 
 /*
+ * sa_ssu_fwd with the SSM block's epilogue of the decode step (SSM.step,
+ * reference modules/ssm.py:195-204: y + D x, times silu(gate)) applied in
+ * the same kernel: out (b,H,P) = (bf(y) + D[h*P + p] u) * silu(gate), with y
+ * first rounded to `dtype` as the unfused path stores it; u is the x of that
+ * epilogue.  D (H*P,) float32; gate (b,H,P) dtype; out (b,H,P) dtype.  The
+ * state update is sa_ssu_fwd's.
+ */
+int sa_ssu_fwd_gated(int dtype, const void* u, const float* A, const void* B, const void* C,
+                     const void* delta_raw, const float* delta_bias, float* h, const float* D,
+                     const void* gate, void* out, int batch, int num_heads, int head_dim,
+                     int num_groups, int state_dim, int use_softplus, float delta_min,
+                     float delta_max, void* stream);
+
+/*
  * SSD chunked scan, forward.  Replaces ssd_scan_forward (reference
  * triton_kernels/ssd_scan/forward.py:223-276: chunk_cumsum_forward :14,
  * chunk_state_forward :62, state_passing_forward :102, bmm_chunk_forward

@@ -17,12 +17,13 @@
 
 namespace sa {
 
-template <typename T, int ROW_LANES, int ROWS>
+template <typename T, int ROW_LANES, int ROWS, bool GATED>
 __global__ __launch_bounds__(256) void ssu_fwd_kernel(
     const T* __restrict__ u, const float* __restrict__ A, const T* __restrict__ Bm,
     const T* __restrict__ Cm, const T* __restrict__ delta_raw, const float* __restrict__ delta_bias,
-    float* __restrict__ h, T* __restrict__ y, int batch, int H, int P, int G, int N, int softplus,
-    float dmin, float dmax, int vec4) {
+    float* __restrict__ h, T* __restrict__ y, const float* __restrict__ Dskip,
+    const T* __restrict__ gate, int batch, int H, int P, int G, int N, int softplus, float dmin,
+    float dmax, int vec4) {
   constexpr int kRowsPerBlock = (256 / ROW_LANES) * ROWS;
   const int lane_in_row = threadIdx.x % ROW_LANES;
   const int row_slot = threadIdx.x / ROW_LANES;  // 0 .. 256/ROW_LANES-1
@@ -75,71 +76,112 @@ __global__ __launch_bounds__(256) void ssu_fwd_kernel(
     }
 #pragma unroll
     for (int o = ROW_LANES / 2; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
-    if (valid && lane_in_row == 0) st(y + rr, part);
+    if (valid && lane_in_row == 0) {
+      if constexpr (GATED) {
+        // SSM block epilogue on y rounded to T: (y + D u) silu(gate), as the gate kernel
+        const float yv = to_f32(from_f32<T>(part));
+        const float xv = load_f32(u + rr);
+        const float gv = load_f32(gate + rr);
+        st(y + rr, (yv + Dskip[hh * P + p] * xv) * (gv * fast_sigmoid(gv)));
+      } else {
+        st(y + rr, part);
+      }
+    }
   }
 }
 
 template <typename T, int ROW_LANES>
 static int launch_ssu(const void* u, const float* A, const void* B, const void* C,
-                      const void* delta_raw, const float* delta_bias, float* h, void* y, int batch,
-                      int H, int P, int G, int N, int softplus, float dmin, float dmax,
-                      hipStream_t stream) {
+                      const void* delta_raw, const float* delta_bias, float* h, void* y,
+                      const float* Dskip, const void* gate, int batch, int H, int P, int G, int N,
+                      int softplus, float dmin, float dmax, hipStream_t stream) {
   constexpr int ROWS = 2;
   constexpr int kRowsPerBlock = (256 / ROW_LANES) * ROWS;
   const long total_rows = static_cast<long>(batch) * H * P;
   const long blocks = (total_rows + kRowsPerBlock - 1) / kRowsPerBlock;
   if (blocks == 0) return 0;
-  ProfScope prof_("ssu_fwd", stream);
-  hipLaunchKernelGGL((ssu_fwd_kernel<T, ROW_LANES, ROWS>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(256), 0, stream, static_cast<const T*>(u), A, static_cast<const T*>(B),
-                     static_cast<const T*>(C), static_cast<const T*>(delta_raw), delta_bias, h,
-                     static_cast<T*>(y), batch, H, P, G, N, softplus, dmin, dmax,
-                     (N % 4 == 0 && (reinterpret_cast<uintptr_t>(h) & 15) == 0) ? 1 : 0);
-  SA_CHECK_LAUNCH("ssu_fwd");
+  ProfScope prof_(gate ? "ssu_fwd_gated" : "ssu_fwd", stream);
+  const int vec4 = (N % 4 == 0 && (reinterpret_cast<uintptr_t>(h) & 15) == 0) ? 1 : 0;
+  if (gate)
+    hipLaunchKernelGGL((ssu_fwd_kernel<T, ROW_LANES, ROWS, true>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(256), 0, stream, static_cast<const T*>(u), A, static_cast<const T*>(B),
+                       static_cast<const T*>(C), static_cast<const T*>(delta_raw), delta_bias, h,
+                       static_cast<T*>(y), Dskip, static_cast<const T*>(gate), batch, H, P, G, N,
+                       softplus, dmin, dmax, vec4);
+  else
+    hipLaunchKernelGGL((ssu_fwd_kernel<T, ROW_LANES, ROWS, false>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(256), 0, stream, static_cast<const T*>(u), A, static_cast<const T*>(B),
+                       static_cast<const T*>(C), static_cast<const T*>(delta_raw), delta_bias, h,
+                       static_cast<T*>(y), nullptr, nullptr, batch, H, P, G, N, softplus, dmin,
+                       dmax, vec4);
+  SA_CHECK_LAUNCH(gate ? "ssu_fwd_gated" : "ssu_fwd");
   return 0;
 }
 
 template <typename T>
 static int dispatch_ssu(const void* u, const float* A, const void* B, const void* C,
                         const void* delta_raw, const float* delta_bias, float* h, void* y,
-                        int batch, int H, int P, int G, int N, int softplus, float dmin,
-                        float dmax, hipStream_t stream) {
+                        const float* Dskip, const void* gate, int batch, int H, int P, int G,
+                        int N, int softplus, float dmin, float dmax, hipStream_t stream) {
   // lanes per state row: enough float4 strips to cover N once, at most 64
   const bool vec4 = N % 4 == 0 && (reinterpret_cast<uintptr_t>(h) & 15) == 0;
   const int strips = vec4 ? N / 4 : N;
   if (strips <= 8)
-    return launch_ssu<T, 8>(u, A, B, C, delta_raw, delta_bias, h, y, batch, H, P, G, N, softplus,
-                            dmin, dmax, stream);
+    return launch_ssu<T, 8>(u, A, B, C, delta_raw, delta_bias, h, y, Dskip, gate, batch, H,
+                            P, G, N, softplus, dmin, dmax, stream);
   if (strips <= 16)
-    return launch_ssu<T, 16>(u, A, B, C, delta_raw, delta_bias, h, y, batch, H, P, G, N, softplus,
-                             dmin, dmax, stream);
+    return launch_ssu<T, 16>(u, A, B, C, delta_raw, delta_bias, h, y, Dskip, gate, batch, H,
+                             P, G, N, softplus, dmin, dmax, stream);
   if (strips <= 32)
-    return launch_ssu<T, 32>(u, A, B, C, delta_raw, delta_bias, h, y, batch, H, P, G, N, softplus,
-                             dmin, dmax, stream);
-  return launch_ssu<T, 64>(u, A, B, C, delta_raw, delta_bias, h, y, batch, H, P, G, N, softplus,
-                           dmin, dmax, stream);
+    return launch_ssu<T, 32>(u, A, B, C, delta_raw, delta_bias, h, y, Dskip, gate, batch, H,
+                             P, G, N, softplus, dmin, dmax, stream);
+  return launch_ssu<T, 64>(u, A, B, C, delta_raw, delta_bias, h, y, Dskip, gate, batch, H,
+                           P, G, N, softplus, dmin, dmax, stream);
 }
 
+}  // namespace sa
+
+namespace sa {
+static int ssu_entry(const char* who, int dtype, const void* u, const float* A, const void* B,
+                     const void* C, const void* delta_raw, const float* delta_bias, float* h,
+                     void* y, const float* Dskip, const void* gate, int batch, int num_heads,
+                     int head_dim, int num_groups, int state_dim, int use_softplus,
+                     float delta_min, float delta_max, void* stream) {
+  SA_CHECK_ARG(batch >= 0 && num_heads > 0 && head_dim > 0 && num_groups > 0 && state_dim > 0,
+               "%s: bad sizes b=%d H=%d P=%d G=%d N=%d", who, batch, num_heads, head_dim,
+               num_groups, state_dim);
+  SA_CHECK_ARG(num_heads % num_groups == 0, "%s: num_heads %% num_groups != 0", who);
+  SA_CHECK_ARG(u && A && B && C && delta_raw && h && y, "%s: null tensor pointer", who);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == kF32)
+    return dispatch_ssu<float>(u, A, B, C, delta_raw, delta_bias, h, y, Dskip, gate, batch,
+                               num_heads, head_dim, num_groups, state_dim, use_softplus, delta_min,
+                               delta_max, s);
+  if (dtype == kBF16)
+    return dispatch_ssu<bf16>(u, A, B, C, delta_raw, delta_bias, h, y, Dskip, gate, batch,
+                              num_heads, head_dim, num_groups, state_dim, use_softplus, delta_min,
+                              delta_max, s);
+  sa_set_error("%s: unsupported dtype %d", who, dtype);
+  return 1;
+}
 }  // namespace sa
 
 extern "C" int sa_ssu_fwd(int dtype, const void* u, const float* A, const void* B, const void* C,
                           const void* delta_raw, const float* delta_bias, float* h, void* y,
                           int batch, int num_heads, int head_dim, int num_groups, int state_dim,
                           int use_softplus, float delta_min, float delta_max, void* stream) {
-  SA_CHECK_ARG(batch >= 0 && num_heads > 0 && head_dim > 0 && num_groups > 0 && state_dim > 0,
-               "sa_ssu_fwd: bad sizes b=%d H=%d P=%d G=%d N=%d", batch, num_heads, head_dim,
-               num_groups, state_dim);
-  SA_CHECK_ARG(num_heads % num_groups == 0, "sa_ssu_fwd: num_heads %% num_groups != 0");
-  SA_CHECK_ARG(u && A && B && C && delta_raw && h && y, "sa_ssu_fwd: null tensor pointer");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == sa::kF32)
-    return sa::dispatch_ssu<float>(u, A, B, C, delta_raw, delta_bias, h, y, batch, num_heads,
-                                   head_dim, num_groups, state_dim, use_softplus, delta_min,
-                                   delta_max, s);
-  if (dtype == sa::kBF16)
-    return sa::dispatch_ssu<sa::bf16>(u, A, B, C, delta_raw, delta_bias, h, y, batch, num_heads,
-                                      head_dim, num_groups, state_dim, use_softplus, delta_min,
-                                      delta_max, s);
-  sa_set_error("sa_ssu_fwd: unsupported dtype %d", dtype);
-  return 1;
+  return sa::ssu_entry("sa_ssu_fwd", dtype, u, A, B, C, delta_raw, delta_bias, h, y, nullptr,
+                       nullptr, batch, num_heads, head_dim, num_groups, state_dim, use_softplus,
+                       delta_min, delta_max, stream);
+}
+
+extern "C" int sa_ssu_fwd_gated(int dtype, const void* u, const float* A, const void* B,
+                                const void* C, const void* delta_raw, const float* delta_bias,
+                                float* h, const float* D, const void* gate, void* out, int batch,
+                                int num_heads, int head_dim, int num_groups, int state_dim,
+                                int use_softplus, float delta_min, float delta_max, void* stream) {
+  SA_CHECK_ARG(D && gate, "sa_ssu_fwd_gated: null D or gate");
+  return sa::ssu_entry("sa_ssu_fwd_gated", dtype, u, A, B, C, delta_raw, delta_bias, h, out, D,
+                       gate, batch, num_heads, head_dim, num_groups, state_dim, use_softplus,
+                       delta_min, delta_max, stream);
 }

@@ -27,6 +27,8 @@ SIGNATURES: dict[str, list] = {
     "sa_profile_enable": [_i],
     "sa_profile_collect": [ctypes.c_char_p, _i, ctypes.POINTER(_f), ctypes.POINTER(_i), _i],
     "sa_ssu_fwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _f, _vp],
+    "sa_ssu_fwd_gated": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                         _i, _f, _f, _vp],
     "sa_ssd_fwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                    _i, _i, _i, _i, _i, _i, _i, _i, _f, _f,
                    _vp, _vp, _vp, _vp, _vp, _vp],

@@ -4,8 +4,9 @@ Parameters, their initialisation and the forward / step interfaces follow
 the reference.  The compute between in_proj and out_proj runs in the
 kernels: SSMConvFn (SiLU + causal depthwise conv + split; with the decode
 context in the same pass at prefill), SSDScanGatedFn (the chunked scan with
-the D-skip / SiLU-gate epilogue fused for bf16), and at decode ssm_conv_step,
-SSUFn and SSMGateFn.
+the D-skip / SiLU-gate epilogue fused for bf16), and at decode ssm_conv_step
+and the state update with the same epilogue in one kernel (ssu_gated_forward;
+SSUFn then SSMGateFn when autograd is recording).
 """
 from __future__ import annotations
 
@@ -16,6 +17,7 @@ import torch
 import torch.nn as nn
 
 from ..kernels.ssm_io import ssm_conv_forward
+from ..kernels.ssu import ssu_gated_forward
 from .layers import Linear
 from ..ops import SSDScanGatedFn, SSMConvFn, SSMGateFn, SSUFn, ssm_conv_step
 
@@ -119,6 +121,13 @@ class SSM(nn.Module):
                                 self.inner_dim, self.bc_dim)
         A = self._A()
         H, P, G, N = self.num_heads, self.head_dim, self.num_groups, self.state_dim
+        if (not torch.is_grad_enabled() and cache.h.dtype == torch.float32
+                and cache.h.is_contiguous() and gate.dtype == x.dtype):
+            # state update, y + D x and the SiLU gate in one kernel
+            out = ssu_gated_forward(x.view(b, H, P), A, B.view(b, G, N), C.view(b, G, N),
+                                    delta_raw, self.delta_bias, cache.h, self.D,
+                                    gate.reshape(b, H, P)).view(b, self.inner_dim)
+            return self.out_proj(out)
         y, cache.h = SSUFn.forward(x.view(b, H, P), A, B.view(b, G, N), C.view(b, G, N),
                                    delta_raw, self.delta_bias, cache.h)
         out = SSMGateFn.apply(y.reshape(b, self.inner_dim), x, self.D, gate)

@@ -104,6 +104,32 @@ def test_ssu_parity_small(dtype, shape, bias):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [dict(b=3, H=4, P=8, N=12, G=2), dict(b=4, H=32, P=64, N=128, G=1)])
+def test_ssu_gated_matches_unfused(dtype, shape):
+    """The decode step's fused kernel (state update, y + D u, SiLU gate)
+    against SSUFn then the gate kernel: the same state bit for bit, and the
+    same output (y rounded to the activation dtype in both)."""
+    from selective_attention.kernels.ssm_io import ssm_gate_forward
+    from selective_attention.kernels.ssu import ssu_gated_forward
+    print(f"ssu gated dtype={dtype} shape={shape}", flush=True)
+    x = _small(dtype=dtype, bias=True, **shape)
+    b, H, P = x["u"].shape
+    g = torch.Generator().manual_seed(3)
+    D = torch.randn(H * P, generator=g).cuda()
+    gate = torch.randn(b, H, P, generator=g).to(dtype).cuda()
+    y, h1 = _run_gpu(x, dtype)
+    e = ssm_gate_forward(y.reshape(b, H * P), x["u"].cuda().reshape(b, H * P), D,
+                         gate.reshape(b, H * P)).view(b, H, P)
+    xd = {k: (None if v is None else v.cuda()) for k, v in x.items()}
+    out = ssu_gated_forward(xd["u"], xd["A"], xd["B"], xd["C"], xd["delta_raw"],
+                            xd["delta_bias"], xd["h"], D, gate)
+    torch.cuda.synchronize()
+    assert torch.equal(xd["h"], h1)
+    assert out.dtype == dtype and torch.equal(out, e)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("softplus,limit", [(False, (0.0, 0.3)), (True, (0.02, 0.05))])
 def test_ssu_parity_limits(softplus, limit):
     x = _small()
