@@ -94,11 +94,14 @@ class CausalLM(nn.Module):
 
     def step(self, input_ids: torch.Tensor, cache: list, state: InferenceState,
              gen_cfg: GenerationConfig, analysis_cfg=None, stats=None):
-        """input_ids (batch_size,) -> logits (batch_size, vocab_size)."""
+        """input_ids (batch_size,) -> logits (batch_size, vocab_size).  Each
+        block's last residual add runs with the next block's first norm (and
+        the last one with the final norm): one kernel each."""
         h = self.embedding(input_ids)
+        pend = None
         for i, layer in enumerate(self.layers):
-            h = layer.step(h, cache[i], state, gen_cfg)
-        return self.lm_head(self.norm(h))
+            h, pend = layer.step(h, cache[i], state, gen_cfg, pending=pend, defer_add=True)
+        return self.lm_head(self.norm.add_forward(h, pend)[1])
 
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, gen_cfg: GenerationConfig, analysis_cfg=None,

@@ -111,11 +111,13 @@ class Seq2SeqLM(nn.Module):
 
     def step(self, input_ids: torch.Tensor, cache, state: InferenceState,
              gen_cfg: GenerationConfig, analysis_cfg=None, stats=None):
-        """input_ids (batch,) -> logits (batch, vocab_size)."""
+        """input_ids (batch,) -> logits (batch, vocab_size); residual adds
+        as in CausalLM.step."""
         h = self.embedding(input_ids)
+        pend = None
         for i, layer in enumerate(self.decoder_layers):
-            h = layer.step(h, cache[i], state, gen_cfg)
-        return self.lm_head(self.norm4(h))
+            h, pend = layer.step(h, cache[i], state, gen_cfg, pending=pend, defer_add=True)
+        return self.lm_head(self.norm4.add_forward(h, pend)[1])
 
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, gen_cfg: GenerationConfig, analysis_cfg=None,

@@ -44,10 +44,18 @@ class CausalBlock(nn.Module):
         return hidden_states, last
 
     def step(self, hidden_states: torch.Tensor, cache, state, gen_cfg, analysis_cfg=None,
-             stats=None):
-        """(batch, model_dim) -> (batch, model_dim)."""
-        h = self.ssm.step(self.norm1(hidden_states), cache.ssm_cache)
+             stats=None, pending=None, defer_add: bool = False):
+        """(batch, model_dim) -> (batch, model_dim).  A model stepping its
+        blocks may leave each block's last residual add to the next: `pending`
+        is added to hidden_states first (with norm1, one kernel), and with
+        defer_add the block returns (hidden_states, ffn output) unsummed."""
+        if pending is None:
+            n = self.norm1(hidden_states)
+        else:
+            hidden_states, n = self.norm1.add_forward(hidden_states, pending)
+        h = self.ssm.step(n, cache.ssm_cache)
         hidden_states, n = self.norm2.add_forward(hidden_states, self.dropout(h))
         h = self.mha.step(n, cache.attn_cache, state, gen_cfg)
         hidden_states, n = self.norm3.add_forward(hidden_states, self.dropout(h))
-        return hidden_states + self.dropout(self.ffn(n))
+        f = self.dropout(self.ffn(n))
+        return (hidden_states, f) if defer_add else hidden_states + f

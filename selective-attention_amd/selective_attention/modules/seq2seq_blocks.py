@@ -82,12 +82,18 @@ class CrossBlock(nn.Module):
         return hidden_states + self.dropout(self.ffn(n))
 
     def step(self, hidden_states: torch.Tensor, cache, state, gen_cfg, analysis_cfg=None,
-             stats=None):
-        """(batch, model_dim) -> (batch, model_dim)."""
-        h = self.ssm.step(self.norm1(hidden_states), cache.ssm_cache)
+             stats=None, pending=None, defer_add: bool = False):
+        """(batch, model_dim) -> (batch, model_dim); pending / defer_add as in
+        CausalBlock.step (the last residual add left to the next block)."""
+        if pending is None:
+            n = self.norm1(hidden_states)
+        else:
+            hidden_states, n = self.norm1.add_forward(hidden_states, pending)
+        h = self.ssm.step(n, cache.ssm_cache)
         hidden_states, n = self.norm2.add_forward(hidden_states, self.dropout(h))
         h = self.mha.step(n, cache.attn_cache, state, gen_cfg)
         hidden_states, n = self.norm3.add_forward(hidden_states, self.dropout(h))
         h = self.cross_mha.step(n, cache.cross_attn_cache, gen_cfg)
         hidden_states, n = self.norm4.add_forward(hidden_states, self.dropout(h))
-        return hidden_states + self.dropout(self.ffn(n))
+        f = self.dropout(self.ffn(n))
+        return (hidden_states, f) if defer_add else hidden_states + f
