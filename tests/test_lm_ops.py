@@ -215,6 +215,8 @@ def test_gemv_multi_matches_single(M):
     big = (torch.randn(4384, K, generator=g) / K ** 0.5).to(BF16).cuda()
     Ws = list(torch.split(big, [2304, 2048, 32]))
     Ws.append((torch.randn(1041, K, generator=g) / K ** 0.5).to(BF16).cuda())
+    if M == 1:   # single-column and tiny matrices: blocks with idle waves
+        Ws = [(torch.randn(n, K, generator=g) / K ** 0.5).to(BF16).cuda() for n in (1, 2, 3, 5)]
     bs = [torch.randn(W.shape[0], generator=g).to(BF16).cuda() if i != 1 else None
           for i, W in enumerate(Ws)]
     print(f"gemv_multi M={M} K={K} N={[W.shape[0] for W in Ws]}", flush=True)

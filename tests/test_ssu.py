@@ -105,7 +105,8 @@ def test_ssu_parity_small(dtype, shape, bias):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("shape", [dict(b=3, H=4, P=8, N=12, G=2), dict(b=4, H=32, P=64, N=128, G=1)])
+@pytest.mark.parametrize("shape", [dict(b=3, H=4, P=8, N=12, G=2), dict(b=2, H=6, P=5, N=7, G=3),
+                                   dict(b=4, H=32, P=64, N=128, G=1)])
 def test_ssu_gated_matches_unfused(dtype, shape):
     """The decode step's fused kernel (state update, y + D u, SiLU gate)
     against SSUFn then the gate kernel: the same state bit for bit, and the
