@@ -166,27 +166,30 @@ def test_causal_lm_decode_parity():
 
 
 @pytest.mark.gpu
-def test_causal_lm_steps_reproduce_forward():
+@pytest.mark.parametrize("batch", [4, 10])
+def test_causal_lm_steps_reproduce_forward(batch):
     """The reference's test_forward_step on this model: full forward logits
-    against prefill + decode steps, both on the GPU."""
+    against prefill + decode steps, both on the GPU.  Batch 10 runs the
+    decode step's projections as GEMMs (more than 8 rows) with split views
+    into the gated state update."""
     cfg = tiny_cfg()
     m = tiny_model(cfg, seed=4).to_bf16().cuda()
     thr_l = [0.88] * cfg.num_layers
-    lens = torch.tensor([200, 150, 120, 90])
-    ids = tokens(4, 200, cfg.vocab_size, lens.tolist(), seed=5).cuda()
+    lens = torch.tensor([200, 150, 120, 90, 200, 111, 160, 95, 180, 130][:batch])
+    ids = tokens(batch, 200, cfg.vocab_size, lens.tolist(), seed=5).cuda()
     gen = GenerationConfig(bos_token_id=-1, eos_token_id=-1, pad_token_id=0,
                            attn_gate_thresholds=thr_l)
-    print("causal_lm steps vs forward", flush=True)
+    print(f"causal_lm steps vs forward batch={batch}", flush=True)
     with torch.no_grad():
         full = m(ids, lens.cuda(), thr_l).float()
         cache = [CausalBlockCache() for _ in range(cfg.num_layers)]
-        pre = torch.tensor([32, 64, 70, 48], device="cuda")
+        pre = torch.tensor([32, 64, 70, 48, 40, 33, 90, 50, 66, 45][:batch], device="cuda")
         m(ids, pre, thr_l, cache)
         state = InferenceState(pre.clone())
-        for i in range(40):
-            tok = ids[torch.arange(4, device="cuda"), state.lengths]
+        for i in range(40 if batch <= 8 else 20):
+            tok = ids[torch.arange(batch, device="cuda"), state.lengths]
             out = m.step(tok, cache, state, gen).float()
-            exp = full[torch.arange(4, device="cuda"), state.lengths]
+            exp = full[torch.arange(batch, device="cuda"), state.lengths]
             assert_logits_close(out, exp, f"step {i}")
             assert_argmax_agrees(out.argmax(-1), exp, f"step {i}")
             state.update()
