@@ -237,6 +237,24 @@ int sa_rope_bf16(int dtype, const void* x0, const void* x1, void* y0, void* y1, 
                  int period, void* stream);
 
 /*
+ * Paged cache build after a prefill (PagedSelectiveAttnCache.build; the
+ * reference's SelectiveAttnCache.build_kv, inference/selective_attn_cache.py:9-28):
+ * for row r and page slot j < ceil(seq_lens[r] / page_size), page
+ * page_table[r, j] receives tokens j*page_size .. of row r for every head:
+ * k_pages (n, heads, page_size, head_dim) and v_pages transposed
+ * (n, heads, head_dim, page_size) bf16, gate_pages (n, heads, page_size) f32
+ * = log_gate; zero K / V and -inf gates past seq_lens[r].  k, v bf16 with
+ * element strides sb (batch), st (token), sh (head), head_dim contiguous;
+ * log_gate f32 with strides gb, gh, gt.  page_table (batch, max_pages) int32;
+ * head_dim % 8 == 0, page_size % 8 == 0.
+ */
+int sa_paged_kv_build(const void* k, const void* v, long sb, long st, long sh,
+                      const float* log_gate, long gb, long gh, long gt, const int32_t* page_table,
+                      const int32_t* seq_lens, int batch, int heads, int head_dim, int page_size,
+                      int max_pages, void* k_pages, void* v_pages, float* gate_pages,
+                      void* stream);
+
+/*
  * One decode token per batch row into a paged KV cache
  * (SelectiveAttnCache.update_kv, inference/selective_attn_cache.py:30-42):
  * slot seq_lens[r], page page_table[r][slot / page_size] (column clamped to

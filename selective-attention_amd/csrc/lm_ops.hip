@@ -516,6 +516,87 @@ extern "C" int sa_rope_bf16(int dtype, const void* x0, const void* x1, void* y0,
   return 0;
 }
 
+namespace sa {
+namespace {
+// Paged cache build after prefill.  Block (page slot j of row r, head h)
+// writes the K page [ps][D], the V page transposed [D][ps] (through an LDS
+// tile) and the gate page [ps] of tokens j ps .. j ps + ps - 1 of row r:
+// zero K / V and a -inf gate past the row's length.  k / v element strides
+// (batch, token, head; D contiguous) and log_gate strides (batch, head, token).
+__global__ __launch_bounds__(256) void paged_build_kernel(
+    const bf16* __restrict__ k, const bf16* __restrict__ v, long sb, long st, long sh,
+    const float* __restrict__ lg, long gb, long gh, long gt, const int32_t* __restrict__ page_table,
+    const int32_t* __restrict__ seq_lens, int H, int D, int ps, int max_pages,
+    bf16* __restrict__ k_pages, bf16* __restrict__ v_pages, float* __restrict__ gate_pages) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  bf16* tile = reinterpret_cast<bf16*>(smem_raw);   // [ps][D + 8] V rows of the page
+  const int LDT = D + 8;
+  const int r = blockIdx.x / max_pages, j = blockIdx.x % max_pages, h = blockIdx.y;
+  const int n = seq_lens[r];
+  const int t0 = j * ps;
+  if (t0 >= n) return;   // block-uniform: this page slot holds no token of the row
+  const long pg = (static_cast<long>(page_table[r * max_pages + j]) * H + h) * ps * D;
+  const bf16* kr = k + r * sb + h * sh;
+  const bf16* vr = v + r * sb + h * sh;
+  const int dv = D / 8;
+  for (int e = threadIdx.x; e < ps * dv; e += 256) {
+    const int sl = e / dv, c8 = e % dv, t = t0 + sl;
+    uint4 kq = uint4{0u, 0u, 0u, 0u}, vq = uint4{0u, 0u, 0u, 0u};
+    if (t < n) {
+      kq = *reinterpret_cast<const uint4*>(kr + t * st + 8 * c8);
+      vq = *reinterpret_cast<const uint4*>(vr + t * st + 8 * c8);
+    }
+    *reinterpret_cast<uint4*>(k_pages + pg + static_cast<long>(sl) * D + 8 * c8) = kq;
+    *reinterpret_cast<uint4*>(tile + sl * LDT + 8 * c8) = vq;
+  }
+  const float* gr = lg + r * gb + h * gh;
+  float* gp = gate_pages + (pg / D);
+  for (int sl = threadIdx.x; sl < ps; sl += 256) gp[sl] = t0 + sl < n ? gr[(t0 + sl) * gt] : -__builtin_inff();
+  __syncthreads();
+  // V^T: eight consecutive slots of one d row per thread
+  const int s8n = ps / 8;
+  for (int e = threadIdx.x; e < D * s8n; e += 256) {
+    const int d = e / s8n, s8 = e % s8n;
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = tile[(8 * s8 + 2 * i) * LDT + d].x, hi = tile[(8 * s8 + 2 * i + 1) * LDT + d].x;
+      w[i] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4*>(v_pages + pg + static_cast<long>(d) * ps + 8 * s8) = uint4{w[0], w[1], w[2], w[3]};
+  }
+}
+}  // namespace
+}  // namespace sa
+
+extern "C" int sa_paged_kv_build(const void* k, const void* v, long sb, long st, long sh,
+                                 const float* log_gate, long gb, long gh, long gt,
+                                 const int32_t* page_table, const int32_t* seq_lens, int batch,
+                                 int heads, int head_dim, int page_size, int max_pages,
+                                 void* k_pages, void* v_pages, float* gate_pages, void* stream) {
+  SA_CHECK_ARG(batch >= 0 && heads > 0 && head_dim > 0 && head_dim % 8 == 0 && head_dim <= 256 &&
+                   page_size > 0 && page_size % 8 == 0 && max_pages > 0 &&
+                   static_cast<long>(page_size) * (head_dim + 8) * 2 <= 64 * 1024,
+               "sa_paged_kv_build: bad sizes batch=%d heads=%d head_dim=%d page_size=%d max_pages=%d",
+               batch, heads, head_dim, page_size, max_pages);
+  SA_CHECK_ARG(k && v && log_gate && page_table && seq_lens && k_pages && v_pages && gate_pages,
+               "sa_paged_kv_build: null pointer");
+  SA_CHECK_ARG(((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15) == 0 &&
+                   sb % 8 == 0 && st % 8 == 0 && sh % 8 == 0,
+               "sa_paged_kv_build: k / v and their strides must keep 16-byte alignment");
+  if (batch == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  sa::ProfScope prof_("paged_build", s);
+  const size_t smem = static_cast<size_t>(page_size) * (head_dim + 8) * 2;
+  hipLaunchKernelGGL(sa::paged_build_kernel, dim3(batch * max_pages, heads), dim3(256), smem, s,
+                     static_cast<const sa::bf16*>(k), static_cast<const sa::bf16*>(v), sb, st, sh,
+                     log_gate, gb, gh, gt, page_table, seq_lens, heads, head_dim, page_size,
+                     max_pages, static_cast<sa::bf16*>(k_pages), static_cast<sa::bf16*>(v_pages),
+                     gate_pages);
+  SA_CHECK_LAUNCH("paged_build");
+  return 0;
+}
+
 extern "C" int sa_paged_kv_append(const void* k, const void* v, const float* log_gate,
                                   const int32_t* page_table, int32_t* seq_lens, int batch,
                                   int heads, int head_dim, int page_size, int max_pages,

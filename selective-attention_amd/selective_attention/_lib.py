@@ -41,6 +41,8 @@ SIGNATURES: dict[str, list] = {
     "sa_attn_varlen_fwd": [_i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _f, _vp, _vp],
     "sa_rms_norm_fwd": [_i, _vp, _vp, _i64, _i, _i, _f, _vp, _vp],
     "sa_rope_bf16": [_i, _vp, _vp, _vp, _vp, _i64, _i, _i, _vp, _vp, _i, _vp],
+    "sa_paged_kv_build": [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _i, _i, _i,
+                          _i, _i, _vp, _vp, _vp, _vp],
     "sa_paged_kv_append": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp],
     "sa_add_rms_norm_bf16": [_vp, _vp, _vp, _i64, _i, _f, _vp, _vp, _vp],
     "sa_mha_gates_bf16": [_vp, _vp, _vp, _f, _i64, _i, _i, _vp, _vp, _vp],

@@ -61,6 +61,33 @@ def paged_kv_append(k, v, log_gate, page_table, seq_lens, k_pages, v_pages, gate
               _lib.ptr(v_pages), _lib.ptr(gate_pages), _lib.stream_of(k))
 
 
+def paged_kv_build(k, v, log_gate, page_table, seq_lens, k_pages, v_pages, gate_pages):
+    """k, v (batch, heads, seq_len, head_dim) bf16 (any strides with head_dim
+    contiguous, e.g. transposed views of (batch, seq_len, heads, head_dim));
+    log_gate (batch, heads, seq_len); page_table (batch, max_pages) int32;
+    seq_lens (batch,) int32: tokens t < seq_lens[r] of row r go to its pages
+    (PagedSelectiveAttnCache layouts), the rest of its last page is zeroed
+    with -inf gates.  One launch."""
+    require_device(k, v, log_gate, page_table, seq_lens, k_pages, v_pages, gate_pages)
+    b, H, L, D = k.shape
+    if b == 0 or L == 0:
+        return   # no tokens: no row has a page to write
+    ps = k_pages.shape[2]
+    k = k.to(torch.bfloat16)
+    v = v.to(torch.bfloat16)
+    if k.stride(3) != 1 or v.stride() != k.stride() or any(x % 8 for x in k.stride()[:3]):
+        k, v = k.contiguous(), v.contiguous()
+    lg = log_gate.to(torch.float32)
+    for t, name in ((page_table, "page_table"), (seq_lens, "seq_lens")):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"paged_kv_build: {name} must be a contiguous int32 tensor")
+    sb, sh, st = k.stride(0), k.stride(1), k.stride(2)
+    _lib.call("sa_paged_kv_build", _lib.ptr(k), _lib.ptr(v), sb, st, sh, _lib.ptr(lg),
+              lg.stride(0), lg.stride(1), lg.stride(2), _lib.ptr(page_table), _lib.ptr(seq_lens),
+              b, H, D, ps, page_table.shape[1], _lib.ptr(k_pages), _lib.ptr(v_pages),
+              _lib.ptr(gate_pages), _lib.stream_of(k))
+
+
 def add_rms_norm_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
     d = x.shape[-1]
     return (x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and weight.dim() == 1

@@ -28,7 +28,7 @@ from __future__ import annotations
 
 import torch
 
-from ..kernels.lm_ops import paged_kv_append
+from ..kernels.lm_ops import paged_kv_append, paged_kv_build
 from .attention import attn_varlen, paged_decode_attn
 
 
@@ -179,6 +179,16 @@ class PagedSelectiveAttnCache:
         L = k_rot.shape[2]
         lens = [L] * self.b if lengths is None else [min(int(x), L) for x in lengths.tolist()]
         H, D, ps = self.H, self.D, self.ps
+        if k_rot.is_cuda:
+            # pages of every row and head written by one kernel (every slot, no fills)
+            for i in range(self.b):
+                self.free.extend(self.rows[i])
+                self.rows[i] = [self._alloc(fill=False) for _ in range((lens[i] + ps - 1) // ps)]
+                self.lens[i] = lens[i]
+            self._pt_dirty = self._sl_dirty = True
+            paged_kv_build(k_rot, v, log_gate, self.page_table(), self.seq_lens(), self.k_pages,
+                           self.v_pages, self.gate_pages)
+            return
         for i in range(self.b):
             for pid in self.rows[i]:
                 self.free.append(pid)

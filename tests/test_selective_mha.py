@@ -206,6 +206,38 @@ def test_paged_cache_decode_parity(D):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("D", [64, 128])
+def test_paged_build_kernel_matches_torch_build(D):
+    """The one-launch page build (transposed-view inputs, ragged lengths, a
+    row of length 0, a partial last page) writes the same pages, bit for bit,
+    as the torch build of the same cache on the CPU: K, V transposed, gates,
+    zeros and -inf past each row's length."""
+    from selective_attention.ops import PagedSelectiveAttnCache
+    b, H, L = 4, 3, 200
+    g = torch.Generator().manual_seed(9)
+    k = torch.randn(b, L, H, D, generator=g).to(torch.bfloat16).transpose(1, 2)
+    v = torch.randn(b, L, H, D, generator=g).to(torch.bfloat16).transpose(1, 2)
+    lg = torch.randn(b, H, L, generator=g)
+    lg[lg < -1.0] = float("-inf")
+    lengths = torch.tensor([200, 131, 0, 64])
+    print(f"paged build D={D}", flush=True)
+    caches = []
+    for dev in ("cpu", "cuda"):
+        c = PagedSelectiveAttnCache(b, H, D, max_tokens=L + 64, device=dev)
+        c.build(k.to(dev), v.to(dev), lg.to(dev), lengths)
+        caches.append(c)
+    cpu, gpu = caches
+    assert cpu.rows == gpu.rows and cpu.lens == gpu.lens
+    for i in range(b):
+        ids = torch.tensor(cpu.rows[i], dtype=torch.long)
+        if len(ids) == 0:
+            continue
+        assert torch.equal(gpu.k_pages[ids.cuda()].cpu(), cpu.k_pages[ids])
+        assert torch.equal(gpu.v_pages[ids.cuda()].cpu(), cpu.v_pages[ids])
+        assert torch.equal(gpu.gate_pages[ids.cuda()].cpu(), cpu.gate_pages[ids])
+
+
+@pytest.mark.gpu
 def test_decode_step_matches_prefill_row():
     """The two kernels agree where the reference's prefill and step agree:
     query t over cached keys 0..t (newest exempt) == prefill row t."""
