@@ -33,9 +33,12 @@ class Linear(nn.Linear):
         """torch.split(self(x), sizes, dim=-1).  On the decode shape the
         weight's row blocks go to one multi-GEMV launch that writes each
         piece as its own contiguous tensor (no copies of split views)."""
+        bs = [None] * len(sizes) if self.bias is None else torch.split(self.bias, sizes)
         if _gemv_ok(x, self) and len(sizes) <= 4:
-            bs = [None] * len(sizes) if self.bias is None else torch.split(self.bias, sizes)
             return gemv_multi(x, torch.split(self.weight, sizes), bs)
+        if x.is_cuda and not torch.is_grad_enabled():
+            # one GEMM per row block: contiguous pieces, no copies of split views later
+            return [F.linear(x, w, bb) for w, bb in zip(torch.split(self.weight, sizes), bs)]
         return list(torch.split(self(x), sizes, dim=-1))
 
 

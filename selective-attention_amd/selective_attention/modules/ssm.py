@@ -92,7 +92,8 @@ class SSM(nn.Module):
             last_ssm_hiddens: (batch_size, num_heads, head_dim, state_dim) float32
         """
         b, L, _ = hidden_states.shape
-        hBC, gate, delta_raw = self._split(self.in_proj(hidden_states))
+        hBC, gate, delta_raw = self.in_proj.split_forward(
+            hidden_states, [self.inner_dim + 2 * self.bc_dim, self.inner_dim, self.num_heads])
         A = self._A()
         if cache is not None and not self.training:
             # prefill: the decode context (raw rows before SiLU) from the conv's own pass
