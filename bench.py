@@ -13,8 +13,11 @@ Extra fields on the same JSON line:
                 durations (HIP events on the launch stream) and the dominant
                 kernel; `traffic` comes from the committed rocprofv3 PMC
                 summary when present.
-  cpu_baseline  the CPU restatement (oracle/ssd.py, fp32 torch) of the same
-                fwd+bwd on a bounded sample (one batch row), on this host.
+  cpu_baseline  the fp32 CPU restatement (oracle/) on this host's cores:
+                `value` is the config 1 fwd+bwd on one batch row (tokens/s);
+                `legs` adds the whole config 0 forward and the config 3
+                decode step (8 of 64 attention rows, scaled, + the state
+                update); `host` records the CPU count, threads and model.
   decode        config 3 decode step (paged GQA attention + state update),
                 us/step, against the HBM roofline.
   sparse_attn   config 2 block-sparse varlen attention, against bf16 MFMA.
@@ -26,7 +29,11 @@ Extra fields on the same JSON line:
                 256 greedy decode steps (decode step replayed from a graph).
   seq2seq       the seq2seq LM at config 4's dimensions (synthetic workload).
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--ssd-only]
+Timings are medians over the timed calls (each call between its own pair of
+HIP events on the launch stream); ms_per_step_mean is the bracketed total / K.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+                       [--ssd-only] [--legs decode,sparse,...] [--copy-probe-mib M]
 """
 from __future__ import annotations
 
@@ -88,18 +95,7 @@ def run_ssd(args, torch):
                                Lc, True, (0.0, inf), True)
         return torch.autograd.grad((y,), leaves, (dy,))
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
+    ms, ms_mean = _time_steps(torch, step, args.steps, args.warmup)
 
     # profiled pass: same steps, per-kernel HIP events on the launch stream
     with kernel_timer() as kt:
@@ -137,25 +133,35 @@ def run_ssd(args, torch):
         "kernel_sum_us": round(kernel_sum_us, 1),
         "kernels": kernels,
     }
-    return dict(ms=ms, tokens=b * L, roofline=roofline,
+    return dict(ms=ms, ms_mean=ms_mean, tokens=b * L, roofline=roofline,
                 config={"workload": "ssd_scan_fwd_bwd_config1", "batch": b, "seq_len": L,
                         "nheads": H, "headdim": P, "dstate": N, "ngroups": G, "chunk": Lc,
                         "activations": "bf16", "state": "fp32", "y_dtype": "fp32"})
 
 
-def _time_events(torch, fn, steps, warmup):
+def _time_steps(torch, fn, steps, warmup):
+    """`warmup` untimed calls, then exactly `steps` timed calls bracketed by
+    synchronisations, each between its own pair of events on the launch
+    stream.  Returns (median ms per call, mean ms per call)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(stream)
+    for i in range(steps):
         fn()
-    e1.record(stream)
+        ev[i + 1].record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    mid = len(per) // 2
+    median = per[mid] if len(per) % 2 else 0.5 * (per[mid - 1] + per[mid])
+    return median, ev[0].elapsed_time(ev[steps]) / steps
+
+
+def _time_events(torch, fn, steps, warmup):
+    """Median ms per call (see _time_steps)."""
+    return _time_steps(torch, fn, steps, warmup)[0]
 
 
 def run_decode(args, torch):
@@ -604,40 +610,138 @@ def run_ssm_io(args, torch):
             "note": "ssm_conv_bwd / ssm_gate_bwd include their partial-sum reductions"}
 
 
-def cpu_baseline(torch, budget_s):
-    """The fp32 CPU restatement (oracle/ssd.py) of the same fwd+bwd on one
-    batch row of config 1; tokens/s of that row."""
-    from oracle import ssd as ref
-    from selective_attention import workloads
+def _cpu_host(torch, threads):
+    """Who ran the CPU baseline: logical CPUs the OS reports, the CPUs this
+    process may run on, the torch threads used, and the CPU model."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"cpu_count": os.cpu_count(), "affinity_cpus": affinity,
+            "torch_threads": torch.get_num_threads(), "threads_requested": threads,
+            "cpu_model": model}
 
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
-    cfg = dict(workloads.SSD_CONFIGS[1])
-    cfg["batch"] = 1
-    x = workloads.ssd_inputs(**cfg, with_dy=True)
-    f32 = torch.float32
 
-    def once():
-        ref.ssd_scan_forward(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], None, None, None,
-                             cfg["chunk"], True, (0.0, float("inf")), f32)
-        ref.ssd_scan_backward(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], None, None,
-                              x["dy"], None, None, cfg["chunk"], True, (0.0, float("inf")), f32)
-
+def _median_time(fn, budget_s, max_reps=5):
+    """1 warm-up call, then the median of up to max_reps timed calls that fit
+    in budget_s (at least one)."""
     t0 = time.perf_counter()
-    once()  # warm-up (also sizes the sample)
+    fn()
     first = time.perf_counter() - t0
-    reps = max(1, min(5, int(budget_s / max(first, 1e-3))))
+    reps = max(1, min(max_reps, int(budget_s / max(first, 1e-3))))
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        once()
+        fn()
         times.append(time.perf_counter() - t0)
     times.sort()
-    med = times[len(times) // 2]
-    tok = cfg["seqlen"]
-    return {"value": round(tok / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"1 of 8 batch rows (L={tok}) fwd+bwd, fp32 torch restatement, "
-                      f"median of {reps} after 1 warm-up; {med:.2f} s per row"}
+    return times[len(times) // 2], reps
+
+
+def cpu_baseline(torch, budget_s):
+    """The fp32 CPU restatement of the reference's algorithms (oracle/: the
+    reference has no CPU path of its own) on this host, on bounded samples:
+
+      value   config 1 fwd+bwd (oracle/ssd.py through its manual backward) on
+              one of the 8 batch rows: tokens/s of that row
+      legs    config 0 forward (the BASELINE-named CPU configuration, whole),
+              config 3 decode (page gather + GQA softmax for 8 of the 64 rows,
+              plus the whole state update), us per step scaled to 64 rows
+
+    Threads: OMP_NUM_THREADS when set (the GPU box's CPU share), else every
+    logical CPU.  Each figure is the median of up to 5 runs after 1 warm-up."""
+    from oracle import attn as attn_ref
+    from oracle import ssd as ref
+    from oracle import ssu as ssu_ref
+    from selective_attention import workloads
+
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or (os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    f32 = torch.float32
+    inf = float("inf")
+    share = budget_s / 3.0
+
+    # config 1: one batch row, forward + backward
+    cfg = dict(workloads.SSD_CONFIGS[1])
+    cfg["batch"] = 1
+    x = workloads.ssd_inputs(**cfg, with_dy=True)
+
+    def c1():
+        ref.ssd_scan_forward(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], None, None, None,
+                             cfg["chunk"], True, (0.0, inf), f32)
+        ref.ssd_scan_backward(x["u"], x["A"], x["B"], x["C"], x["delta_raw"], None, None,
+                              x["dy"], None, None, cfg["chunk"], True, (0.0, inf), f32)
+
+    t1, r1 = _median_time(c1, share)
+    tok1 = cfg["seqlen"]
+
+    # config 0: the whole forward
+    cfg0 = workloads.SSD_CONFIGS[0]
+    x0 = workloads.ssd_inputs(**cfg0)
+
+    def c0():
+        y, _ = ref.ssd_scan_forward(x0["u"], x0["A"], x0["B"], x0["C"], x0["delta_raw"], None,
+                                    None, None, cfg0["chunk"], True, (0.0, inf), f32)
+        b, L, H, P = x0["u"].shape
+        return y.reshape(b, L, H * P) + x0["D"] * x0["u"].reshape(b, L, H * P)
+
+    t0, r0 = _median_time(c0, share)
+    tok0 = cfg0["batch"] * cfg0["seqlen"]
+
+    # config 3: 8 of the 64 decode rows (their pages copied to the host) + the state update
+    rows = 8
+    d = workloads.decode_inputs(device="cuda:0")
+    lens = d.seq_lens[:rows].to("cpu", torch.int64)
+    ps = d.k_pages.shape[2]
+    npg = [int((n + ps - 1) // ps) for n in lens.tolist()]
+    pt = d.page_table[:rows].to("cpu", torch.int64)
+    used = torch.cat([pt[i, :npg[i]] for i in range(rows)])
+    kp = d.k_pages[used.to(d.k_pages.device)].cpu()
+    vp = d.v_pages[used.to(d.v_pages.device)].cpu()
+    local = torch.full_like(pt, -1)
+    o = 0
+    for i in range(rows):
+        local[i, :npg[i]] = torch.arange(o, o + npg[i])
+        o += npg[i]
+    q = d.q[:rows].cpu()
+    del d
+    s3 = workloads.ssu_inputs()
+
+    def attn():
+        attn_ref.paged_decode_attn(q, kp, vp, local, lens, dtype=f32)
+
+    def ssu():
+        ssu_ref.ssu_forward(s3["u"], s3["A"], s3["B"], s3["C"], s3["delta_raw"], None, s3["h"],
+                            dtype=f32)
+
+    ta, ra = _median_time(attn, share / 2)
+    ts, rs = _median_time(ssu, share / 2)
+    scale = 64 / rows
+    return {"value": round(tok1 / t1, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"config 1 fwd+bwd on 1 of 8 batch rows (L={tok1}), fp32 torch restatement "
+                      f"(oracle/ssd.py), median of {r1} after 1 warm-up: {t1:.2f} s per row",
+            "host": _cpu_host(torch, threads),
+            "legs": {
+                "config0_fwd": {"tokens_per_s": round(tok0 / t0, 1), "ms": round(t0 * 1e3, 2),
+                                "sample": f"whole config 0 forward (b2 L512 H8 P64 N64, y + D x "
+                                          f"and h_last), median of {r0}"},
+                "config3_decode": {"us_per_step": round((ta * scale + ts) * 1e6, 1),
+                                   "attn_us": round(ta * scale * 1e6, 1),
+                                   "ssu_us": round(ts * 1e6, 1),
+                                   "sample": f"paged GQA attention on rows 0-{rows - 1} "
+                                             f"({int(lens.sum())} cached tokens) scaled by "
+                                             f"{scale:g} to 64 rows, plus the whole state update "
+                                             f"(b64 H32 P64 N128), medians of {ra} / {rs}"},
+            }}
 
 
 def main():
@@ -646,7 +750,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--ssd-only", action="store_true", help="skip the decode / sparse / ssm_io lines")
+    ap.add_argument("--ssd-only", action="store_true", help="skip every leg after the headline")
+    ap.add_argument("--legs", default=None,
+                    help="comma-separated subset of the legs after the headline "
+                         "(decode, sparse, ssm_io, selective_mha, causal_lm, seq2seq)")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the timed work, run 3 plain device copies of this many MiB "
@@ -669,6 +776,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "ms_per_step_mean": round(res["ms_mean"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -677,13 +785,18 @@ def main():
         "config": res["config"],
         "roofline": res["roofline"],
     }
-    if not args.ssd_only:
-        out["decode"] = run_decode(args, torch)
-        out["sparse_attn"] = run_sparse(args, torch)
-        out["ssm_io"] = run_ssm_io(args, torch)
-        out["selective_mha"] = run_selective_mha(args, torch)
-        out["causal_lm"] = run_causal_lm(args, torch)
-        out["seq2seq"] = run_seq2seq(args, torch)
+    legs = [("decode", "decode", run_decode), ("sparse", "sparse_attn", run_sparse),
+            ("ssm_io", "ssm_io", run_ssm_io), ("selective_mha", "selective_mha", run_selective_mha),
+            ("causal_lm", "causal_lm", run_causal_lm), ("seq2seq", "seq2seq", run_seq2seq)]
+    want = set() if args.ssd_only else (
+        {n for n, _, _ in legs} if args.legs is None else set(args.legs.split(",")))
+    unknown = want - {n for n, _, _ in legs}
+    if unknown:
+        print(f"bench.py: unknown legs {sorted(unknown)}", file=sys.stderr)
+        sys.exit(2)
+    for name, key, fn in legs:
+        if name in want:
+            out[key] = fn(args, torch)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, args.cpu_budget_s)
     if args.copy_probe_mib > 0:

@@ -29,7 +29,11 @@ def sparse_attn_varlen(q, k, v, cu_seqlens, block_idx, block_size=64, softmax_sc
                        key_bias=None, dtype=torch.float64):
     """q, k, v (T, H, D); cu_seqlens (nseq+1,) int; block_idx (H, n_qblk, M) int,
     local key-block indices (-1 = unused); key_bias (H, T) or None.
-    Returns o (T, H, D) in `dtype`."""
+    Returns o (T, H, D) in `dtype`.
+
+    A row of block_idx is a set of key blocks: a repeated id counts once, and
+    ids outside the sequence's blocks are ignored.  Query blocks past the
+    last row of block_idx select nothing (zero outputs)."""
     T, H, D = q.shape
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
     cu = [int(x) for x in cu_seqlens.tolist()]
@@ -46,10 +50,10 @@ def sparse_attn_varlen(q, k, v, cu_seqlens, block_idx, block_size=64, softmax_sc
         causal = pos[:, None] >= pos[None, :]
         blk_of_key = pos // block_size
         for h in range(H):
-            sel = block_idx[h, qblk:qblk + nb].to(torch.int64)           # (nb, M)
+            sel = block_idx[h, qblk:qblk + nb].to(torch.int64)           # (<= nb, M)
             allowed_blocks = torch.zeros((nb, nb), dtype=torch.bool)
-            for j in range(nb):
-                ids = sel[j][sel[j] >= 0]
+            for j in range(sel.shape[0]):
+                ids = sel[j][(sel[j] >= 0) & (sel[j] < nb)]
                 allowed_blocks[j, ids] = True
             allow = allowed_blocks[blk_of_key[:, None], blk_of_key[None, :]] & causal
             sc = (qf[a:b, h] @ kf[a:b, h].T) * scale

@@ -21,6 +21,7 @@
 #include "common.h"
 #include "prof.h"
 #include "tile.h"
+#include "decode.h"
 
 namespace sa {
 
@@ -148,14 +149,14 @@ __device__ __forceinline__ void softmax_lazy(v4f (&s)[KT], v4f (&o)[DT], float& 
 //   kFullSelf    every key of the query's own sequence;  j = i exempt
 //   kCross       every key of the sequence's key range cu_k[s]..cu_k[s+1]
 //                (k, v, key_bias indexed by key token); key 0 exempt
-// block_idx == nullptr selects every key block the mode admits (dense).
+// dense_all != 0 selects every key block the mode admits (no table).
 constexpr int kCausalSelf = 0, kFullSelf = 1, kCross = 2;
 
 template <int D, bool BIAS, int MODE>
 __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_k, int nseq,
-    const int32_t* __restrict__ block_idx, int n_qblk, int max_blocks,
+    const int32_t* __restrict__ block_idx, int n_qblk, int max_blocks, int grid_qblk, int dense_all,
     const float* __restrict__ key_bias, bf16* __restrict__ o, int T, int Tk, int H,
     float scale_log2) {
   constexpr int BS = 64;
@@ -166,8 +167,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
   bf16* sm = reinterpret_cast<bf16*>(smem_raw);   // [2 stages][K tile, V tile]
 
   const int lid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int h = lid / n_qblk;
-  const int gq = lid - h * n_qblk;
+  // grid_qblk >= the query blocks of the packing: surplus ids find no sequence
+  // and exit; a query block past the rows of block_idx has no selection
+  const int h = lid / grid_qblk;
+  const int gq = lid - h * grid_qblk;
   const int tid = threadIdx.x, lane = tid & 63;
   // locate the query block's sequence (q blocks are numbered sequence by
   // sequence): 64 sequences per step, one per lane, a prefix sum of their
@@ -229,28 +232,40 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
 
   // the selected blocks that are inside the key range (and causally visible
   // for kCausalSelf), in order; dense: slots are the blocks themselves
-  const bool dense = block_idx == nullptr;
+  // A block id repeated within a row is attended once, at its first slot:
+  // the selection is a set of key blocks.
+  const bool dense = dense_all != 0;
+  const bool has_row = dense || (gq < n_qblk && max_blocks > 0);
   const int nkb = (nks + BS - 1) / BS;
-  const int nslot = dense ? (MODE == kCausalSelf ? min(jq + 1, nkb) : nkb) : max_blocks;
-  const int32_t* sel = dense ? nullptr : block_idx + (static_cast<long>(h) * n_qblk + gq) * max_blocks;
+  const int nslot = dense ? (MODE == kCausalSelf ? min(jq + 1, nkb) : nkb) : (has_row ? max_blocks : 0);
+  const int32_t* sel = has_row && !dense ? block_idx + (static_cast<long>(h) * n_qblk + gq) * max_blocks : nullptr;
   const bool simple = !dense && max_blocks <= 64;
   int my_kb = -1;
   uint64_t vmask = 0;
-  if (simple) {
+  if (simple && has_row) {
     my_kb = lane < max_blocks ? sel[lane] : -1;
-    vmask = __ballot(my_kb >= 0 && my_kb < nkb && (MODE != kCausalSelf || my_kb <= jq));
+    bool ok = my_kb >= 0 && my_kb < nkb && (MODE != kCausalSelf || my_kb <= jq);
+    for (int j = 0; j + 1 < max_blocks; ++j) {
+      const int kj = __shfl(my_kb, j, 64);
+      ok = ok && !(lane > j && my_kb == kj);
+    }
+    vmask = __ballot(ok);
   }
   auto next_valid = [&](int e) -> int {   // first valid slot >= e, or nslot
     if (dense) return min(e, nslot);
     if (simple) {
       const uint64_t mm = e >= 64 ? 0ull : (vmask >> e);
-      return mm ? e + __builtin_ctzll(mm) : max_blocks;
+      return mm ? e + __builtin_ctzll(mm) : nslot;
     }
-    for (; e < max_blocks; ++e) {
+    for (; e < nslot; ++e) {
       const int kb = sel[e];
-      if (kb >= 0 && kb < nkb && (MODE != kCausalSelf || kb <= jq)) return e;
+      if (kb >= 0 && kb < nkb && (MODE != kCausalSelf || kb <= jq)) {
+        bool dup = false;
+        for (int j = 0; j < e && !dup; ++j) dup = sel[j] == kb;
+        if (!dup) return e;
+      }
     }
-    return max_blocks;
+    return nslot;
   };
   auto block_of = [&](int e) -> int {
     return dense ? e : simple ? __builtin_amdgcn_readlane(my_kb, e) : sel[e];
@@ -448,33 +463,39 @@ int sparse_smem_attr() {
 template <int D, bool BIAS, int MODE>
 int launch_sparse(const void* q, const void* k, const void* v, const int32_t* cu,
                   const int32_t* cu_k, int nseq, const int32_t* block_idx, int n_qblk,
-                  int max_blocks, const float* key_bias, void* o, int T, int Tk, int H,
-                  float scale_log2, long blocks, hipStream_t s) {
+                  int max_blocks, int grid_qblk, int dense_all, const float* key_bias, void* o, int T,
+                  int Tk, int H, float scale_log2, hipStream_t s) {
+  const long blocks = static_cast<long>(H) * grid_qblk;
   if (sparse_smem_attr<D, BIAS, MODE>()) return 1;
   ProfScope prof_(MODE == kCausalSelf ? "sparse_attn_fwd" : MODE == kFullSelf ? "attn_full_fwd" : "attn_cross_fwd", s);
   hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, BIAS, MODE>), dim3(blocks), dim3(256),
                      SparseSmem<D>::bytes, s, static_cast<const bf16*>(q), static_cast<const bf16*>(k),
                      static_cast<const bf16*>(v), cu, cu_k, nseq, block_idx, n_qblk, max_blocks,
-                     key_bias, static_cast<bf16*>(o), T, Tk, H, scale_log2);
+                     grid_qblk, dense_all, key_bias, static_cast<bf16*>(o), T, Tk,
+                     H, scale_log2);
   return 0;
 }
 
 template <int D, int MODE>
 int launch_attn_d(const void* q, const void* k, const void* v, const int32_t* cu,
                   const int32_t* cu_k, int nseq, const int32_t* block_idx, int n_qblk,
-                  int max_blocks, const float* key_bias, void* o, int T, int Tk, int H,
-                  float scale_log2, long blocks, hipStream_t s) {
+                  int max_blocks, int grid_qblk, int dense_all, const float* key_bias, void* o,
+                  int T, int Tk, int H, float scale_log2, hipStream_t s) {
   return key_bias ? launch_sparse<D, true, MODE>(q, k, v, cu, cu_k, nseq, block_idx, n_qblk, max_blocks,
-                                                 key_bias, o, T, Tk, H, scale_log2, blocks, s)
+                                                 grid_qblk, dense_all, key_bias, o, T, Tk, H, scale_log2, s)
                   : launch_sparse<D, false, MODE>(q, k, v, cu, cu_k, nseq, block_idx, n_qblk,
-                                                  max_blocks, key_bias, o, T, Tk, H, scale_log2, blocks, s);
+                                                  max_blocks, grid_qblk, dense_all, key_bias, o, T, Tk,
+                                                  H, scale_log2, s);
 }
 
+// grid_qblk: query blocks per head in the grid, at least the packing's
+// sum over sequences of ceil(len / 64) (total_q / 64 + nseq bounds it);
+// dense_all: every admissible key block, no table
 int launch_attn(int mode, int D, const void* q, const void* k, const void* v, const int32_t* cu,
                 const int32_t* cu_k, int nseq, const int32_t* block_idx, int n_qblk, int max_blocks,
-                const float* key_bias, void* o, int T, int Tk, int H, float scale_log2, long blocks,
-                hipStream_t s) {
-#define SA_ATTN_ARGS q, k, v, cu, cu_k, nseq, block_idx, n_qblk, max_blocks, key_bias, o, T, Tk, H, scale_log2, blocks, s
+                int grid_qblk, int dense_all, const float* key_bias, void* o, int T, int Tk, int H,
+                float scale_log2, hipStream_t s) {
+#define SA_ATTN_ARGS q, k, v, cu, cu_k, nseq, block_idx, n_qblk, max_blocks, grid_qblk, dense_all, key_bias, o, T, Tk, H, scale_log2, s
   if (D == 128) {
     if (mode == kCausalSelf) return launch_attn_d<128, kCausalSelf>(SA_ATTN_ARGS);
     if (mode == kFullSelf) return launch_attn_d<128, kFullSelf>(SA_ATTN_ARGS);
@@ -787,7 +808,6 @@ __global__ __launch_bounds__(64, 2) void paged_decode_kernel(
 // merge the segments of one (batch row, query head); one wave, the segment
 // weights exp2(m_s - M) computed lane-parallel into LDS.  A row with no keys
 // gets zeros.
-constexpr int kDecodeMaxWaves = 8192;
 
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
@@ -847,28 +867,6 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
   }
 }
 
-// workspace: segment partials for b * Hkv + kDecodeMaxWaves segment ids, then
-// cum_row (b + 1 ints)
-struct DecodeWs {
-  float* part_o;
-  float* part_ml;
-  int32_t* cum_row;
-};
-inline size_t decode_ws_layout(int b, int Hq, int Hkv, int D, void* base, DecodeWs* out) {
-  const size_t segs = static_cast<size_t>(b) * Hkv + kDecodeMaxWaves;
-  const size_t grp = static_cast<size_t>(Hq / Hkv);
-  const size_t o_bytes = (segs * grp * D * sizeof(float) + 255) & ~size_t(255);
-  const size_t ml_bytes = (segs * grp * 2 * sizeof(float) + 255) & ~size_t(255);
-  const size_t cum_bytes = ((static_cast<size_t>(b) + 1) * sizeof(int32_t) + 255) & ~size_t(255);
-  if (out) {
-    char* p = static_cast<char*>(base);
-    out->part_o = reinterpret_cast<float*>(p);
-    out->part_ml = reinterpret_cast<float*>(p + o_bytes);
-    out->cum_row = reinterpret_cast<int32_t*>(p + o_bytes + ml_bytes);
-  }
-  return o_bytes + ml_bytes + cum_bytes + 256;
-}
-
 // waves of one resident round: CUs x resident 64-thread blocks per CU
 template <typename K>
 int decode_waves(K kern, int variant) {
@@ -891,39 +889,52 @@ int decode_waves(K kern, int variant) {
 extern "C" size_t sa_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                                  int head_dim, int max_pages) {
   if (batch < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads || max_pages < 0) return 0;
-  return sa::decode_ws_layout(batch, num_q_heads, num_kv_heads, head_dim, nullptr, nullptr);
+  return sa::decode_ws_layout(batch, num_q_heads, num_kv_heads, head_dim, sa::kDecodeMaxWaves,
+                              nullptr, nullptr);
 }
 
-extern "C" int sa_paged_decode_fwd(int dtype, const void* q, const void* k_pages,
-                                   const void* v_pages, const int32_t* page_table,
-                                   const int32_t* seq_lens, const float* key_bias, int batch,
-                                   int num_q_heads, int num_kv_heads, int head_dim, int page_size,
-                                   int max_pages, int num_pages, float softmax_scale, void* o,
-                                   void* workspace, size_t workspace_bytes, void* stream) {
-  SA_CHECK_ARG(dtype == sa::kBF16, "sa_paged_decode_fwd: only bfloat16 is supported");
+namespace sa {
+
+// Argument checks shared by the decode entry points (0 = ok).
+int decode_check(int dtype, const void* q, const void* k_pages, const void* v_pages,
+                 const int32_t* page_table, const int32_t* seq_lens, const float* key_bias,
+                 int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                 int max_pages, int num_pages, const void* o, const char* who) {
+  SA_CHECK_ARG(dtype == sa::kBF16, "%s: only bfloat16 is supported", who);
   SA_CHECK_ARG(batch >= 0 && num_kv_heads > 0 && num_q_heads > 0 &&
                    num_q_heads % num_kv_heads == 0 && num_q_heads / num_kv_heads <= 16,
-               "sa_paged_decode_fwd: need Hq %% Hkv == 0 and Hq/Hkv <= 16 (Hq=%d Hkv=%d)",
-               num_q_heads, num_kv_heads);
-  SA_CHECK_ARG(head_dim == 64 || head_dim == 128, "sa_paged_decode_fwd: head_dim %d not in {64,128}",
+               "%s: need Hq %% Hkv == 0 and Hq/Hkv <= 16 (Hq=%d Hkv=%d)", who, num_q_heads,
+               num_kv_heads);
+  SA_CHECK_ARG(head_dim == 64 || head_dim == 128, "%s: head_dim %d not in {64,128}", who,
                head_dim);
-  SA_CHECK_ARG(page_size == 64 || page_size == 128,
-               "sa_paged_decode_fwd: page_size %d not in {64, 128}", page_size);
+  SA_CHECK_ARG(page_size == 64 || page_size == 128, "%s: page_size %d not in {64, 128}", who,
+               page_size);
   SA_CHECK_ARG(max_pages >= 0 && static_cast<long>(max_pages) * page_size <= (1L << 30),
-               "sa_paged_decode_fwd: max_pages %d too large", max_pages);
+               "%s: max_pages %d too large", who, max_pages);
   SA_CHECK_ARG(static_cast<long>(batch) * num_kv_heads * ((static_cast<long>(max_pages) * page_size + 63) / 64) < (1L << 31),
-               "sa_paged_decode_fwd: more than 2^31 key tiles");
-  SA_CHECK_ARG(q && k_pages && v_pages && page_table && seq_lens && o && workspace,
-               "sa_paged_decode_fwd: null pointer");
-  SA_CHECK_ARG(num_pages >= 1 || batch == 0, "sa_paged_decode_fwd: empty page pool");
+               "%s: more than 2^31 key tiles", who);
+  SA_CHECK_ARG(q && k_pages && v_pages && page_table && seq_lens && o, "%s: null pointer", who);
+  SA_CHECK_ARG(num_pages >= 1 || batch == 0, "%s: empty page pool", who);
   SA_CHECK_ARG(!key_bias || (reinterpret_cast<uintptr_t>(key_bias) & 15) == 0,
-               "sa_paged_decode_fwd: key_bias must be 16-byte aligned");
-  sa::DecodeWs ws;
-  const size_t need = sa::decode_ws_layout(batch, num_q_heads, num_kv_heads, head_dim, workspace, &ws);
-  SA_CHECK_ARG(workspace_bytes >= need, "sa_paged_decode_fwd: workspace %zu B < %zu B",
-               workspace_bytes, need);
-  if (batch == 0) return 0;
-  hipStream_t s = static_cast<hipStream_t>(stream);
+               "%s: key_bias must be 16-byte aligned", who);
+  return 0;
+}
+
+// waves of the stream-K launch for this head_dim / bias variant
+int decode_wave_count(int head_dim, bool bias) {
+  if (head_dim == 128)
+    return bias ? decode_waves(paged_decode_kernel<128, true>, 0)
+                : decode_waves(paged_decode_kernel<128, false>, 1);
+  return bias ? decode_waves(paged_decode_kernel<64, true>, 2)
+              : decode_waves(paged_decode_kernel<64, false>, 3);
+}
+
+// plan, stream-K decode and merge on workspace `ws` with W waves
+int decode_launch(const void* q, const void* k_pages, const void* v_pages,
+                  const int32_t* page_table, const int32_t* seq_lens, const float* key_bias,
+                  int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                  int max_pages, int num_pages, float softmax_scale, void* o, const DecodeWs& ws,
+                  int W, hipStream_t s) {
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf(static_cast<float>(head_dim));
   const float sl2 = scale * sa::kLog2e;
   {
@@ -932,11 +943,9 @@ extern "C" int sa_paged_decode_fwd(int dtype, const void* q, const void* k_pages
                        page_size, max_pages, ws.cum_row);
     SA_CHECK_LAUNCH("paged_decode_plan");
   }
-  int W = 0;
   {
     sa::ProfScope prof_("paged_decode", s);
-    auto launch = [&](auto kern, int variant) {
-      W = sa::decode_waves(kern, variant);
+    auto launch = [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(W), dim3(64), 0, s, static_cast<const sa::bf16*>(q),
                          static_cast<const sa::bf16*>(k_pages),
                          static_cast<const sa::bf16*>(v_pages), page_table, seq_lens, key_bias,
@@ -944,9 +953,9 @@ extern "C" int sa_paged_decode_fwd(int dtype, const void* q, const void* k_pages
                          page_size, max_pages, num_pages, W, sl2);
     };
     if (head_dim == 128)
-      key_bias ? launch(sa::paged_decode_kernel<128, true>, 0) : launch(sa::paged_decode_kernel<128, false>, 1);
+      key_bias ? launch(sa::paged_decode_kernel<128, true>) : launch(sa::paged_decode_kernel<128, false>);
     else
-      key_bias ? launch(sa::paged_decode_kernel<64, true>, 2) : launch(sa::paged_decode_kernel<64, false>, 3);
+      key_bias ? launch(sa::paged_decode_kernel<64, true>) : launch(sa::paged_decode_kernel<64, false>);
     SA_CHECK_LAUNCH("paged_decode");
   }
   {
@@ -957,6 +966,31 @@ extern "C" int sa_paged_decode_fwd(int dtype, const void* q, const void* k_pages
     SA_CHECK_LAUNCH("paged_decode_merge");
   }
   return 0;
+}
+
+}  // namespace sa
+
+extern "C" int sa_paged_decode_fwd(int dtype, const void* q, const void* k_pages,
+                                   const void* v_pages, const int32_t* page_table,
+                                   const int32_t* seq_lens, const float* key_bias, int batch,
+                                   int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                                   int max_pages, int num_pages, float softmax_scale, void* o,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  if (const int rc = sa::decode_check(dtype, q, k_pages, v_pages, page_table, seq_lens, key_bias,
+                                      batch, num_q_heads, num_kv_heads, head_dim, page_size,
+                                      max_pages, num_pages, o, "sa_paged_decode_fwd"))
+    return rc;
+  SA_CHECK_ARG(workspace, "sa_paged_decode_fwd: null workspace");
+  sa::DecodeWs ws;
+  const size_t need = sa::decode_ws_layout(batch, num_q_heads, num_kv_heads, head_dim,
+                                           sa::kDecodeMaxWaves, workspace, &ws);
+  SA_CHECK_ARG(workspace_bytes >= need, "sa_paged_decode_fwd: workspace %zu B < %zu B",
+               workspace_bytes, need);
+  if (batch == 0) return 0;
+  const int W = sa::decode_wave_count(head_dim, key_bias != nullptr);
+  return sa::decode_launch(q, k_pages, v_pages, page_table, seq_lens, key_bias, batch,
+                           num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_pages,
+                           softmax_scale, o, ws, W, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int sa_sparse_attn_fwd(int dtype, const void* q, const void* k, const void* v,
@@ -974,14 +1008,17 @@ extern "C" int sa_sparse_attn_fwd(int dtype, const void* q, const void* k, const
                "sa_sparse_attn_fwd: bad sizes");
   SA_CHECK_ARG(q && k && v && cu_seqlens && o && (block_idx || n_qblk == 0),
                "sa_sparse_attn_fwd: null pointer");
-  if (n_qblk == 0 || num_seqs == 0 || total_tokens == 0) return 0;
+  if (num_seqs == 0 || total_tokens == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf(static_cast<float>(head_dim));
-  const long blocks = static_cast<long>(num_heads) * n_qblk;
+  // every query block of the packing gets a workgroup, whatever n_qblk says:
+  // rows block_idx lacks select nothing (their outputs are zeros), rows past
+  // the packing are never read
+  const int grid_qblk = n_qblk > total_tokens / 64 + num_seqs ? n_qblk : total_tokens / 64 + num_seqs;
   const float sl2 = scale * sa::kLog2e;
   const int rc = sa::launch_attn(sa::kCausalSelf, head_dim, q, k, v, cu_seqlens, cu_seqlens, num_seqs,
-                                 block_idx, n_qblk, max_blocks, key_bias, o, total_tokens,
-                                 total_tokens, num_heads, sl2, blocks, s);
+                                 block_idx, n_qblk, max_blocks, grid_qblk, 0, key_bias, o, total_tokens,
+                                 total_tokens, num_heads, sl2, s);
   if (rc) return rc;
   SA_CHECK_LAUNCH("sparse_attn_fwd");
   return 0;
@@ -1009,12 +1046,11 @@ extern "C" int sa_attn_varlen_fwd(int dtype, int mode, const void* q, const void
   // upper bound on the query blocks (sum over sequences of ceil(len / 64));
   // blocks past the real count find no sequence and exit
   const int n_qblk = total_q / 64 + num_seqs;
-  const long blocks = static_cast<long>(num_heads) * n_qblk;
   const int32_t* cu_k = mode == sa::kCross ? cu_seqlens_k : cu_seqlens_q;
   const int Tk = mode == sa::kCross ? total_k : total_q;
   const int rc = sa::launch_attn(mode, head_dim, q, k, v, cu_seqlens_q, cu_k, num_seqs, nullptr,
-                                 n_qblk, 0, key_bias, o, total_q, Tk, num_heads,
-                                 scale * sa::kLog2e, blocks, s);
+                                 n_qblk, 0, n_qblk, 1, key_bias, o, total_q, Tk, num_heads,
+                                 scale * sa::kLog2e, s);
   if (rc) return rc;
   SA_CHECK_LAUNCH("attn_varlen_fwd");
   return 0;

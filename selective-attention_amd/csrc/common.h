@@ -332,6 +332,16 @@ extern "C" void sa_set_error(const char* fmt, ...);
     }                                  \
   } while (0)
 
+// a HIP runtime call that must succeed (its code becomes return value 2)
+#define SA_CHECK_LAUNCH_RC(call, what)                                               \
+  do {                                                                               \
+    hipError_t e_ = (call);                                                          \
+    if (e_ != hipSuccess) {                                                          \
+      sa_set_error("%s failed: %s", what, hipGetErrorString(e_));                    \
+      return 2;                                                                      \
+    }                                                                                \
+  } while (0)
+
 #define SA_CHECK_LAUNCH(what)                                                        \
   do {                                                                               \
     hipError_t e_ = hipGetLastError();                                               \

@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256, 2) void chunk_outer_bf16_kernel(
     const float* __restrict__ dc, const int64_t* __restrict__ length, float* __restrict__ out,
     SsdDims d) {
   constexpr int N = 32 * NK, LDX = N + 8, LDA = 64 + 8;
-  constexpr int NPL = MODE == 1 ? 2 : 1;   // planes of the scaled operand
+  constexpr int NPL = 2;                   // hi + lo planes of the scaled operand
   constexpr int NTW = N / 64;              // 16-wide n tiles per wave
   constexpr int STAGE = NPL * 64 * LDA + 64 * LDX;
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -245,15 +245,23 @@ __global__ __launch_bounds__(256, 2) void chunk_outer_bf16_kernel(
       bf16* As = sm + slot * STAGE;
       bf16* Xs = As + NPL * 64 * LDA;
       if constexpr (MODE == 0) {
+        // w * u is fp32 (dt up to z > 20 makes it large): hi + lo planes keep
+        // the chunk states near fp32, which the backward's dC, dA and
+        // d(delta_raw) inherit
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int e = tid + 256 * i, row = e >> 3;
           const uint32_t q[4] = {pa0[i].x, pa0[i].y, pa0[i].z, pa0[i].w};
-          uint32_t r[4];
+          uint32_t r[4], rl[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            r[j] = pack_bf16x2(bf16lo_to_f32(q[j]) * psc[i], bf16hi_to_f32(q[j]) * psc[i]);
+          for (int j = 0; j < 4; ++j) {
+            const float v0 = bf16lo_to_f32(q[j]) * psc[i], v1 = bf16hi_to_f32(q[j]) * psc[i];
+            r[j] = pack_bf16x2(v0, v1);
+            rl[j] = pack_bf16x2(v0 - bf16lo_to_f32(r[j]), v1 - bf16hi_to_f32(r[j]));
+          }
           *reinterpret_cast<uint4*>(As + row * LDA + 8 * (e & 7)) = uint4{r[0], r[1], r[2], r[3]};
+          *reinterpret_cast<uint4*>(As + 64 * LDA + row * LDA + 8 * (e & 7)) =
+              uint4{rl[0], rl[1], rl[2], rl[3]};
         }
       } else {
         const int row = tid >> 2, c0 = 16 * (tid & 3);
@@ -805,7 +813,7 @@ template <int NK, int MODE>
 int launch_chunk_outer_bf16_nk(const void* a, const void* x, const float* dt, const float* dc,
                                const int64_t* length, float* out, const SsdDims& d, hipStream_t s) {
   const long blocks = static_cast<long>(d.P / 64) * d.H * d.nc * d.b;
-  const size_t smem = 2 * sizeof(bf16) * ((MODE == 1 ? 2 : 1) * 64 * 72 + 64 * (32 * NK + 8));
+  const size_t smem = 2 * sizeof(bf16) * (2 * 64 * 72 + 64 * (32 * NK + 8));
   if (smem > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(chunk_outer_bf16_kernel<NK, MODE>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));

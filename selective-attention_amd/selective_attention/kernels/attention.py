@@ -31,7 +31,10 @@ def sparse_attn_varlen(q, k, v, cu_seqlens, block_idx, block_size=64, softmax_sc
             64-token blocks of each sequence, numbered sequence by sequence;
             entries are key-block indices local to the query's sequence
             (block j = positions [64j, 64j+64)), -1 for unused slots.
-            Blocks after the query block and out-of-range entries are ignored.
+            Blocks after the query block and out-of-range entries are ignored;
+            a row is a set (an id repeated in it is attended once).  Query
+            blocks past the last row select nothing (zero outputs); rows past
+            the packing's query blocks are never read.
         key_bias: (num_heads, total_tokens) float32 or None: added to the score
             of key j for every query except j itself.
 

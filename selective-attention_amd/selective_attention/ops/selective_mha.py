@@ -152,13 +152,18 @@ class PagedSelectiveAttnCache:
         return self.rows[i][t // self.ps], t % self.ps
 
     def page_table(self) -> torch.Tensor:
-        """(batch, pages) int32 on the cache's device (at least max_pages columns)."""
+        """(batch, pages) int32 on the cache's device (at least max_pages columns).
+        Columns past a row's pages repeat the row's last page id (0 for a row
+        without pages): the device-side append clamps its column to the
+        table's width, so an append past a row's pages lands in that row's own
+        last page, never in another row's."""
         if self._pt_dirty or self._pt is None:
             width = max([self.max_pages] + [len(r) for r in self.rows])
             pt = torch.zeros(self.b, width, dtype=torch.int32)
             for i, r in enumerate(self.rows):
                 if r:
                     pt[i, :len(r)] = torch.tensor(r, dtype=torch.int32)
+                    pt[i, len(r):] = r[-1]
             self._pt = pt.to(self.device)
             self._pt_dirty = False
         return self._pt
@@ -217,8 +222,9 @@ class PagedSelectiveAttnCache:
         table, and keep the lengths on the device: append / unappend / attend
         then make no host round trip and no allocation that depends on host
         state, so a decode step can be captured in a graph and replayed.  At
-        most `extra_tokens` appends may follow (a row that runs past its pages
-        writes into its last page instead of faulting)."""
+        most `extra_tokens` appends may follow: the table's columns past a row's
+        pages repeat its last page, so a row that runs past them overwrites
+        slots of its own last page (wrong keys for that row alone, no fault)."""
         if extra_tokens > 0:
             fresh = []
             for i in range(self.b):

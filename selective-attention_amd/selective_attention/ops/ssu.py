@@ -31,47 +31,41 @@ class SSUFn(nn.Module):
         use_delta_softplus: bool = True,
         delta_limit: Tuple = (0.0, float("inf")),
     ):
+        """One recurrence step of every (batch row, head) state.
+
+        Shapes (b = batch, H = heads, P = head_dim, G = groups, N = state_dim):
+        u (b, H, P); A (H,); B and C (b, G, N); delta_raw (b, H);
+        delta_bias (H,) or None; h (b, H, P, N), fp32 state.
+
+        Returns (y, h): y (b, H, P) in the dtype of u, and the state after the
+        step -- the caller's tensor itself, updated in place, when it is a
+        contiguous fp32 tensor.
         """
-        Args:
-            u: (batch_size, num_heads, head_dim)
-            A: (num_heads,)
-            B, C: (batch_size, num_groups, state_dim)
-            delta_raw: (batch_size, num_heads)
-            delta_bias: (num_heads,)
-            h: (batch_size, num_heads, head_dim, state_dim)
+        u, A, B, C, delta_raw, delta_bias, h = check_step_args(u, A, B, C, delta_raw,
+                                                               delta_bias, h)
+        return ssu_forward(u, A, B, C, delta_raw, delta_bias, h, use_delta_softplus, delta_limit)
 
-        Returns:
-            y: (batch_size, num_heads, head_dim)
-            h: (batch_size, num_heads, head_dim, state_dim)
-        """
-        check_ndim(u, 3, name="u")
-        check_ndim(A, 1, name="A")
-        check_ndim(B, 3, name="B")
-        check_ndim(C, 3, name="C")
-        check_ndim(delta_raw, 2, name="delta_raw")
-        check_ndim(delta_bias, 1, name="delta_bias", optional=True)
-        check_ndim(h, 4, name="h")
 
-        batch_size, num_heads, head_dim = u.shape
-        num_groups, state_dim = B.shape[1], B.shape[2]
+def check_step_args(u, A, B, C, delta_raw, delta_bias, h):
+    """The reference's validation of a state-update call (ops/ssu.py:38-61):
+    ValueError on a wrong ndim, then on a shape that disagrees with u and B,
+    before any launch; every tensor made contiguous."""
+    expected_ndim = dict(u=3, A=1, B=3, C=3, delta_raw=2, h=4)
+    args = dict(u=u, A=A, B=B, C=C, delta_raw=delta_raw, h=h)
+    for name, t in args.items():
+        check_ndim(t, expected_ndim[name], name=name)
+        if name == "delta_raw":
+            check_ndim(delta_bias, 1, name="delta_bias", optional=True)
 
-        check_shape(A, (num_heads,), name="A")
-        check_shape(B, (batch_size, num_groups, state_dim), name="B")
-        check_shape(C, (batch_size, num_groups, state_dim), name="C")
-        check_shape(delta_raw, (batch_size, num_heads), name="delta_raw")
-        check_shape(delta_bias, (num_heads,), name="delta_bias", optional=True)
-        check_shape(h, (batch_size, num_heads, head_dim, state_dim), name="h")
-        if num_heads % num_groups != 0:
-            raise ValueError(f"num_heads ({num_heads}) must be a multiple of num_groups ({num_groups})")
+    b, nh, p = u.shape
+    ng, n = B.shape[1], B.shape[2]
+    expected_shape = dict(A=(nh,), B=(b, ng, n), C=(b, ng, n), delta_raw=(b, nh),
+                          h=(b, nh, p, n))
+    for name, shape in expected_shape.items():
+        check_shape(args[name], shape, name=name)
+        if name == "delta_raw":
+            check_shape(delta_bias, (nh,), name="delta_bias", optional=True)
+    if nh % ng != 0:
+        raise ValueError(f"num_heads ({nh}) must be a multiple of num_groups ({ng})")
 
-        u = to_contiguous(u)
-        A = to_contiguous(A)
-        B = to_contiguous(B)
-        C = to_contiguous(C)
-        delta_raw = to_contiguous(delta_raw)
-        delta_bias = to_contiguous(delta_bias)
-        h = to_contiguous(h)
-
-        y, h = ssu_forward(u, A, B, C, delta_raw, delta_bias, h, use_delta_softplus, delta_limit)
-
-        return y, h
+    return tuple(to_contiguous(t) for t in (u, A, B, C, delta_raw, delta_bias, h))

@@ -39,3 +39,16 @@ def assert_parity(actual, expected, dtype, name="", fp32_atol_rel=1e-5):
         mx = err.max().item() if e.numel() else 0.0
         assert mx <= BF16_RTOL * max(scale, 1e-30), (
             f"{name}: max err {mx:.3e} > 2e-2 * scale {scale:.3e}")
+
+
+def assert_scaled(actual, expected, name="", frac=BF16_RTOL):
+    """Finite, and max|a-e| <= frac * max|e| (the scale-aware half of the bf16
+    bound) -- for inputs whose dynamic range puts single bf16 roundings of
+    the largest terms above the elementwise atol."""
+    a = actual.detach().to("cpu", torch.float64)
+    e = expected.detach().to("cpu", torch.float64)
+    assert a.shape == e.shape, f"{name}: shape {tuple(a.shape)} vs {tuple(e.shape)}"
+    assert torch.isfinite(a).all(), f"{name}: non-finite values"
+    scale = e.abs().max().item() if e.numel() else 0.0
+    mx = (a - e).abs().max().item() if e.numel() else 0.0
+    assert mx <= frac * max(scale, 1e-30), f"{name}: max err {mx:.3e} > {frac} * scale {scale:.3e}"

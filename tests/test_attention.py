@@ -210,6 +210,100 @@ def test_sparse_attn_missing_diagonal_gives_zero_rows():
     assert torch.count_nonzero(o) == 0
 
 
+def _with_duplicates(idx, g):
+    """Copy each row's valid ids into its -1 slots (after the valid ones, so
+    the first occurrences keep their order)."""
+    out = idx.clone()
+    H, nq, M = idx.shape
+    for h in range(H):
+        for j in range(nq):
+            row = out[h, j]
+            valid = row[row >= 0]
+            free = (row < 0).nonzero().flatten()
+            if len(valid) and len(free):
+                pick = valid[torch.randint(len(valid), (len(free),), generator=g)]
+                row[free] = pick
+    return out
+
+
+def test_oracle_sparse_selection_is_a_set():
+    """Repeated ids count once; rows past the end of block_idx select nothing
+    (the same as a row of -1)."""
+    lens, H, D = [200, 90], 2, 16
+    q, k, v, cu = packed(lens, H, D, seed=8, dtype=F64)
+    g = torch.Generator().manual_seed(9)
+    idx, _, _ = workloads.block_selection(lens, H, 64, 3, g)
+    base = ref.sparse_attn_varlen(q, k, v, cu, idx)
+    dup = _with_duplicates(idx, g)
+    assert not torch.equal(dup, idx)
+    torch.testing.assert_close(ref.sparse_attn_varlen(q, k, v, cu, dup), base, rtol=0, atol=0)
+    short = idx[:, :-2]
+    padded = idx.clone()
+    padded[:, -2:] = -1
+    torch.testing.assert_close(ref.sparse_attn_varlen(q, k, v, cu, short),
+                               ref.sparse_attn_varlen(q, k, v, cu, padded), rtol=0, atol=0)
+    # and the missing rows really are zero (the last two query blocks: seq 1)
+    assert torch.count_nonzero(ref.sparse_attn_varlen(q, k, v, cu, short)[200:]) == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lens,M", [([300, 130, 64], 6), ([4500], 71)])
+def test_sparse_attn_duplicate_ids_attend_once(lens, M):
+    """A block id repeated in a row is attended once, at its first slot: the
+    output equals, bit for bit, the run on the table that keeps only each
+    id's first occurrence (same walk order), and the oracle's set semantics.
+    M = 71 takes the scalar slot scan instead of the wave ballot."""
+    print(f"sparse duplicate ids lens={lens} M={M}", flush=True)
+    H, D = 2, 64
+    g = torch.Generator().manual_seed(12)
+    q, k, v, cu = packed(lens, H, D, seed=6)
+    if M > 64:
+        idx = full_causal_selection(lens, H, M=M)
+        idx[:, :, 1::3] = -1   # thin the rows out so there are free slots to fill
+    else:
+        idx, _, _ = workloads.block_selection(lens, H, 64, M - 2, g)
+        idx = torch.cat([idx, torch.full((H, idx.shape[1], 2), -1, dtype=torch.int32)], dim=2)
+    dup = _with_duplicates(idx, g)
+    assert not torch.equal(dup, idx)
+    first = torch.full_like(dup, -1)
+    for h in range(dup.shape[0]):
+        for j in range(dup.shape[1]):
+            seen = []
+            for kb in dup[h, j].tolist():
+                if kb >= 0 and kb not in seen:
+                    seen.append(kb)
+            first[h, j, :len(seen)] = torch.tensor(seen, dtype=torch.int32)
+    o = _run_sparse(q, k, v, cu, first)
+    o_dup = _run_sparse(q, k, v, cu, dup)
+    assert torch.equal(o_dup, o)
+    assert_parity(o_dup, ref.sparse_attn_varlen(q, k, v, cu, dup), torch.bfloat16, "o")
+
+
+@pytest.mark.gpu
+def test_sparse_attn_short_block_idx_writes_every_row():
+    """block_idx with fewer rows than the packing's query blocks: the rows it
+    lacks select nothing and their outputs are written as zeros (the output
+    buffer starts as NaN and is passed through the C ABI directly)."""
+    from selective_attention import _lib
+    lens, H, D = [200, 150], 2, 128
+    g = torch.Generator().manual_seed(13)
+    q, k, v, cu = packed(lens, H, D, seed=7)
+    idx, _, _ = workloads.block_selection(lens, H, 64, 4, g)
+    nq = idx.shape[1]
+    short = idx[:, : nq - 3].contiguous()
+    qd, kd, vd, cud, sd = q.cuda(), k.cuda(), v.cuda(), cu.cuda(), short.cuda()
+    o = torch.full_like(qd, float("nan"))
+    _lib.call("sa_sparse_attn_fwd", _lib.DTYPE_BF16, _lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd),
+              _lib.ptr(cud), len(lens), _lib.ptr(sd), sd.shape[1], sd.shape[2], 64, None,
+              q.shape[0], H, D, -1.0, _lib.ptr(o), _lib.stream_of(qd))
+    torch.cuda.synchronize()
+    assert torch.isfinite(o.float()).all()
+    exp = ref.sparse_attn_varlen(q, k, v, cu, short)
+    assert_parity(o, exp, torch.bfloat16, "o")
+    # the last three query blocks are the tail of sequence 1 (150 tokens = 3 blocks)
+    assert torch.count_nonzero(o[200:]) == 0
+
+
 @pytest.mark.gpu
 def test_sparse_attn_config2_sample():
     """Config 2 (T=65536, H16, D128) on the device; two heads of the first

@@ -244,16 +244,20 @@ def test_gemv_multi_rejects_bad_counts():
 @pytest.mark.gpu
 def test_linear_dispatch():
     """Linear runs the GEMV for <= 8 bf16 rows in inference and the GEMM
-    otherwise; both agree with F.linear to bf16 rounding."""
+    otherwise; both agree with F.linear in fp32 to bf16 rounding: 1 ulp for
+    the GEMV (one rounding of the fp32 sum plus bias), 2 for the GEMM
+    library (which may round the product before adding the bias)."""
     import torch.nn.functional as F
     from selective_attention.modules.layers import Linear
+    torch.manual_seed(0)
     lin = Linear(512, 768).cuda().to(BF16)
-    for rows in (4, 9):
-        x = torch.randn(rows, 512, device="cuda").to(BF16)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    for rows, ulps in ((4, 1), (9, 2)):
+        x = torch.randn(rows, 512, device="cuda", generator=g).to(BF16)
         with torch.no_grad():
             y = lin(x)
             e = F.linear(x.float(), lin.weight.float(), lin.bias.float())
-        assert ulp_bf16_close(y.cpu(), e.to(BF16).cpu(), 1)
+        assert ulp_bf16_close(y.cpu(), e.to(BF16).cpu(), ulps), f"rows {rows}"
 
 
 @pytest.mark.gpu

@@ -183,6 +183,61 @@ def test_gradcheck_manual_backward():
     assert torch.autograd.gradcheck(fn, args, eps=1e-6, atol=1e-7, rtol=1e-5)
 
 
+def _large_z(x, frac=0.2, lo=20.5, hi=150.0, seed=23):
+    """Put delta_raw above the softplus threshold (20) on a fraction of the tokens."""
+    g = torch.Generator().manual_seed(seed)
+    dr = x["delta_raw"]
+    m = torch.rand(dr.shape, generator=g) < frac
+    x = dict(x)
+    x["delta_raw"] = torch.where(m, lo + (hi - lo) * torch.rand(dr.shape, generator=g, dtype=dr.dtype),
+                                 dr)
+    return x
+
+
+def test_softplus_threshold_branch():
+    """softplus20 is torch's softplus (beta 1, threshold 20): log(exp(z)+1)
+    up to 20, the identity above.  In fp32 the unthresholded formula
+    overflows (exp(100) = inf) where softplus20 stays finite."""
+    z = torch.linspace(-30.0, 200.0, 2301, dtype=F64)
+    torch.testing.assert_close(ref.softplus20(z), torch.nn.functional.softplus(z), rtol=1e-15,
+                               atol=1e-15)
+    assert torch.equal(ref.softplus20(z)[z > 20], z[z > 20])
+    z32 = torch.tensor([19.5, 20.0, 20.5, 100.0], dtype=torch.float32)
+    assert torch.isinf(torch.log(torch.exp(z32) + 1.0)[-1])
+    assert torch.isfinite(ref.softplus20(z32)).all() and ref.softplus20(z32)[-1] == 100.0
+
+
+@pytest.mark.parametrize("chunk", [4, 5])
+def test_chunked_equals_sequential_large_z(chunk):
+    """Tokens with z > 20 (dt = z, the state all but reset) in both forms."""
+    x = _large_z(_inputs(L=13, lens=[13, 9]))
+    y, h = ref.ssd_scan_forward(**x, chunk_size=chunk)
+    ys, hs = ref.ssd_sequential(**x)
+    torch.testing.assert_close(y, ys, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(h, hs, rtol=1e-10, atol=1e-12)
+
+
+def test_manual_backward_equals_autograd_large_z():
+    """The manual backward scales d(delta_raw) by sigmoid(z) only for z <= 20
+    (backward_kernel.py:1024-1025); autograd through softplus20's branches is
+    the independent check, here with ~20 % of the tokens above the threshold."""
+    x = _large_z(_inputs(lens=[12, 8]), lo=20.5, hi=24.0)
+    g = torch.Generator().manual_seed(8)
+    b, L, H, P = x["u"].shape
+    N = x["B"].shape[-1]
+    dy = torch.randn(b, L, H, P, generator=g, dtype=F64)
+    dh = torch.randn(b, H, P, N, generator=g, dtype=F64)
+    z = x["delta_raw"] + x["delta_bias"]
+    assert (z > 20).sum() > 10
+    man = dict(zip(GRAD_NAMES, ref.ssd_scan_backward(
+        x["u"], x["A"], x["B"], x["C"], x["delta_raw"], x["delta_bias"], x["h_init"], dy, dh,
+        x["length"], 4, True, (0.0, math.inf))))
+    auto = _masked_loss_grads(ref.ssd_sequential, x, dy, dh, use_delta_softplus=True,
+                              delta_limit=(0.0, math.inf))
+    for k, v in auto.items():
+        torch.testing.assert_close(man[k], v, rtol=1e-9, atol=1e-11, msg=f"seq {k}")
+
+
 # ---------------------------------------------------------------------------
 # sensitivity: plausible slips in the oracle are caught by the pins above
 # ---------------------------------------------------------------------------

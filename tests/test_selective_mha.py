@@ -169,6 +169,24 @@ def test_paged_cache_rebuild_returns_pages():
     assert sorted(cache.free + cache.rows[0] + cache.rows[1]) == list(range(2 * 3))
 
 
+def test_paged_cache_table_padding_stays_in_row():
+    """Columns of the page table past a row's pages repeat that row's last
+    page: the device-side append clamps an overflowing token to the last
+    column, which then names the row's own page, not another row's."""
+    cache = PagedSelectiveAttnCache(3, 1, 8, max_tokens=200, device="cpu")
+    lens = torch.tensor([130, 10, 64])
+    z = torch.zeros(3, 1, 130, 8)
+    cache.build(z, z, torch.zeros(3, 1, 130), lengths=lens)
+    pt = cache.page_table()
+    for i, r in enumerate(cache.rows):
+        assert len(r) >= 1
+        assert pt[i, :len(r)].tolist() == r
+        assert (pt[i, len(r):] == r[-1]).all(), f"row {i}: {pt[i].tolist()} vs pages {r}"
+    # the append kernel's column for a token past the row's pages
+    col = min(10 ** 6 // cache.ps, pt.shape[1] - 1)
+    assert [int(pt[i, col]) for i in range(3)] == [r[-1] for r in cache.rows]
+
+
 # ------------------------------------------------------------- GPU parity
 PREFILL_CASES = {
     # name: (b, H, L, D, lengths, thr, dead_heads)

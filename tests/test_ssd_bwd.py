@@ -7,7 +7,7 @@ import torch
 from oracle import ssd as ref
 from selective_attention import workloads
 from tests.helpers import assert_parity
-from tests.test_ssd_fwd import make_inputs, to_dev
+from tests.test_ssd_fwd import large_z, make_inputs, to_dev
 
 NAMES = ["u", "A", "B", "C", "delta_raw", "delta_bias", "h_init"]
 
@@ -102,6 +102,36 @@ def test_ssd_bwd_fused_signed_limits(softplus, limit):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype,shape,chunk", [
+    (torch.float32, dict(b=2, L=150, H=4, P=24, N=40, G=2, lens=[150, 97]), 32),
+    (torch.bfloat16, dict(b=2, L=320, H=8, P=64, N=128, G=2, lens=[320, 130]), 128),
+])
+def test_ssd_bwd_softplus_threshold(dtype, shape, chunk):
+    """delta_raw + bias in (20.5, 22) on 3 % of the tokens: d(delta_raw) is
+    not scaled by sigmoid(z) there (backward_kernel.py:1024-1025).  Generic
+    (fp32) and fused bf16 backward, at the stated tolerances."""
+    print(f"ssd bwd large z dtype={dtype} chunk={chunk}", flush=True)
+    check(large_z(make_inputs(dtype=dtype, **shape), frac=0.03, hi=22.0), chunk, dtype)
+
+
+@pytest.mark.gpu
+def test_ssd_bwd_softplus_far_above_threshold():
+    """z up to 150 (bf16 fused backward): every gradient finite and within
+    2e-2 of its scale (single bf16 roundings of terms that large exceed the
+    elementwise atol)."""
+    from tests.helpers import assert_scaled
+    x = large_z(make_inputs(dtype=torch.bfloat16, b=2, L=320, H=8, P=64, N=128, G=2,
+                            lens=[320, 130]))
+    g = torch.Generator().manual_seed(5)
+    dy = torch.randn(2, 320, 8, 64, generator=g)
+    dh = torch.randn(2, 8, 64, 128, generator=g)
+    got = gpu_grads(x, dy, dh, 128)
+    exp = ref_grads(x, dy, dh, 128)
+    for k, v in got.items():
+        assert_scaled(v, exp[k], f"d{k}")
+
+
+@pytest.mark.gpu
 def test_ssd_bwd_fused_deterministic():
     x = make_inputs(b=2, L=256, H=8, P=64, N=128, G=2, dtype=torch.bfloat16, lens=[256, 190])
     g = torch.Generator().manual_seed(3)
@@ -137,14 +167,54 @@ def test_ssd_bwd_config0_shape():
 
 
 @pytest.mark.gpu
-def test_ssd_bwd_config1_heads():
-    """Config 1 head/state/chunk shapes (bf16) on one row of 2048 tokens."""
+def test_ssd_bwd_config1_full_row():
+    """Config 1 (bf16, H32 P64 N128 G8, chunk 256) on one full row of 4096
+    tokens (16 chunks), with a gradient on h_last, against the fp64 oracle."""
+    print("ssd bwd config1 full row", flush=True)
     cfg = dict(workloads.SSD_CONFIGS[1])
-    cfg.update(batch=1, seqlen=2048)
+    cfg.update(batch=1)
     w = workloads.ssd_inputs(**cfg)
     x = dict(u=w["u"], A=w["A"], B=w["B"], C=w["C"], delta_raw=w["delta_raw"], delta_bias=None,
              h_init=None, length=None)
-    check(x, cfg["chunk"], torch.bfloat16, with_dh=False)
+    check(x, cfg["chunk"], torch.bfloat16, with_dh=True)
+
+
+@pytest.mark.gpu
+def test_ssd_config1_full_batch_rows_equal_single_rows():
+    """The benchmark's full config-1 step (b = 8, its own inputs and dy): the
+    rows are independent and every kernel is deterministic, so rows 0 and 7
+    of y, h_last and every per-row gradient equal, bit for bit, a b = 1 run on
+    that row alone.  dA is a sum over rows: its b = 8 value equals the sum of
+    the eight b = 1 values to fp32 rounding."""
+    print("ssd config1 full batch vs single rows", flush=True)
+    from selective_attention.ops import SSDScanFn
+    cfg = workloads.SSD_CONFIGS[1]
+    w = workloads.ssd_inputs(**cfg, device="cuda", with_dy=True)
+    names = ["u", "A", "B", "C", "delta_raw"]
+
+    def run(sl):
+        leaves = {k: (w[k][sl] if k != "A" else w[k]).detach().clone().requires_grad_(True)
+                  for k in names}
+        y, h = SSDScanFn.apply(leaves["u"], leaves["A"], leaves["B"], leaves["C"],
+                               leaves["delta_raw"], None, None, None, cfg["chunk"], True,
+                               (0.0, float("inf")), True)
+        grads = torch.autograd.grad((y,), [leaves[k] for k in names], (w["dy"][sl],))
+        torch.cuda.synchronize()
+        return y.detach(), h.detach(), dict(zip(names, grads))
+
+    y, h, g = run(slice(None))
+    assert torch.isfinite(y).all() and all(torch.isfinite(v.float()).all() for v in g.values())
+    dA_rows = torch.zeros_like(g["A"])
+    for r in range(cfg["batch"]):
+        y1, h1, g1 = run(slice(r, r + 1))
+        dA_rows += g1["A"]
+        if r not in (0, cfg["batch"] - 1):
+            continue
+        assert torch.equal(y[r:r + 1], y1), f"y row {r}"
+        assert torch.equal(h[r:r + 1], h1), f"h_last row {r}"
+        for k in ("u", "B", "C", "delta_raw"):
+            assert torch.equal(g[k][r:r + 1], g1[k]), f"d{k} row {r}"
+    torch.testing.assert_close(g["A"], dA_rows, rtol=1e-5, atol=1e-5 * dA_rows.abs().max().item())
 
 
 @pytest.mark.gpu

@@ -6,7 +6,7 @@ import torch
 
 from oracle import ssd as ref
 from selective_attention import workloads
-from tests.helpers import assert_parity
+from tests.helpers import assert_parity, assert_scaled
 
 F64 = torch.float64
 
@@ -23,6 +23,19 @@ def make_inputs(b=2, L=100, H=4, P=24, N=40, G=2, dtype=torch.float32, seed=0, w
     h0 = torch.randn(b, H, P, N, generator=g) * 0.3 if with_h else None
     length = None if lens is None else torch.tensor(lens, dtype=torch.int64)
     return dict(u=u, A=A, B=B, C=C, delta_raw=dr, delta_bias=bias, h_init=h0, length=length)
+
+
+def large_z(x, frac=0.05, lo=20.5, hi=150.0, seed=21):
+    """Put delta_raw (+ bias) above the softplus threshold 20 on a fraction of
+    the tokens: dt = z there (triton_kernels/softplus.py:5-12), up to 150, so
+    an unthresholded fp32 log(exp(z) + 1) would overflow."""
+    g = torch.Generator().manual_seed(seed)
+    dr = x["delta_raw"].float()
+    m = torch.rand(dr.shape, generator=g) < frac
+    vals = lo + (hi - lo) * torch.rand(dr.shape, generator=g)
+    x = dict(x)
+    x["delta_raw"] = torch.where(m, vals, dr).to(x["delta_raw"].dtype)
+    return x
 
 
 def to_dev(x):
@@ -73,6 +86,40 @@ def test_ssd_fwd_limits(softplus, limit):
     y, h = run_fwd(x, 32, softplus=softplus, limit=limit)
     assert_parity(y, y_ref, torch.float32, "y")
     assert_parity(h, h_ref, torch.float32, "h_last")
+
+
+THRESHOLD_CASES = [
+    (torch.float32, dict(b=2, L=200, H=4, P=24, N=40, G=2, lens=[200, 133]), 64),
+    (torch.bfloat16, dict(b=2, L=320, H=8, P=64, N=128, G=2, lens=[320, 201]), 128),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,shape,chunk", THRESHOLD_CASES)
+def test_ssd_fwd_softplus_threshold(dtype, shape, chunk):
+    """delta_raw + bias in (20.5, 22) on 3 % of the tokens: dt = z there (the
+    identity branch of the softplus), generic (fp32) and bf16 chunk-scan
+    paths, at the stated tolerances."""
+    print(f"ssd fwd large z dtype={dtype} chunk={chunk}", flush=True)
+    x = large_z(make_inputs(dtype=dtype, **shape), frac=0.03, hi=22.0)
+    y_ref, h_ref = ref.ssd_scan_forward(**x, chunk_size=chunk)
+    y, h = run_fwd(x, chunk)
+    assert_parity(y, y_ref, dtype, "y")
+    assert_parity(h, h_ref, dtype, "h_last")
+
+
+@pytest.mark.gpu
+def test_ssd_fwd_softplus_far_above_threshold():
+    """z up to 150 (bf16): an unthresholded fp32 log(exp(z) + 1) overflows
+    past 88.  Outputs stay finite and within 2e-2 of their scale; single
+    bf16 roundings of terms ~dt * u ~ 100 exceed the elementwise atol, so
+    only the scale-aware bound is asserted here."""
+    x = large_z(make_inputs(dtype=torch.bfloat16, b=2, L=320, H=8, P=64, N=128, G=2,
+                            lens=[320, 201]))
+    y_ref, h_ref = ref.ssd_scan_forward(**x, chunk_size=128)
+    y, h = run_fwd(x, 128)
+    assert_scaled(y, y_ref, "y")
+    assert_scaled(h, h_ref, "h_last")
 
 
 @pytest.mark.gpu

@@ -105,6 +105,24 @@ def test_ssu_parity_small(dtype, shape, bias):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ssu_softplus_threshold(dtype):
+    """Rows with delta_raw above the softplus threshold 20 (dt = z, up to 150):
+    the identity branch, no overflow; the state is all but reset there."""
+    print(f"ssu large z dtype={dtype}", flush=True)
+    x = _small(dtype=dtype, bias=True, b=8, H=32, P=64, N=128, G=8)
+    g = torch.Generator().manual_seed(31)
+    dr = x["delta_raw"].float()
+    m = torch.rand(dr.shape, generator=g) < 0.25
+    x["delta_raw"] = torch.where(m, 20.5 + 129.5 * torch.rand(dr.shape, generator=g),
+                                 dr).to(x["delta_raw"].dtype)
+    y_ref, h_ref = ssu_ref.ssu_forward(**x)
+    y, h = _run_gpu(x, dtype)
+    assert_parity(h, h_ref, torch.float32, "h")
+    assert_parity(y, y_ref, dtype, "y")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape", [dict(b=3, H=4, P=8, N=12, G=2), dict(b=2, H=6, P=5, N=7, G=3),
                                    dict(b=4, H=32, P=64, N=128, G=1)])
 def test_ssu_gated_matches_unfused(dtype, shape):
