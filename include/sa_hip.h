@@ -294,6 +294,28 @@ int sa_paged_decode_fwd(int dtype, const void* q, const void* k_pages, const voi
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Allocation-free paged GQA decode attention.  No counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops or harnesses that forbid hipMalloc).  Same
+ * arguments, semantics, kernels and result bits as sa_paged_decode_fwd,
+ * without the workspace: the segment partials live in a file-scope device
+ * array of sa_paged_decode_noalloc_limit() bytes (32 MiB), one per GPU, held
+ * until the process ends.  A call that would need more scratch than that
+ * (batch * Hkv + the launch's waves segments of (Hq/Hkv) * D + 2 floats,
+ * plus the row prefix sum) fails with return value 1 before any launch.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (other streams, other threads) race and must be serialised by the
+ * caller.  Nothing in the array needs clearing between calls.
+ */
+size_t sa_paged_decode_noalloc_limit(void);
+int sa_paged_decode_fwd_noalloc(int dtype, const void* q, const void* k_pages,
+                                const void* v_pages, const int32_t* page_table,
+                                const int32_t* seq_lens, const float* key_bias, int batch,
+                                int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                                int max_pages, int num_pages, float softmax_scale, void* o,
+                                void* stream);
+
+/*
  * SSM prologue: SiLU, then the depthwise causal conv (zero history), then the
  * split into x / B / C.  Replaces the torch ops of SSM.forward
  * (reference modules/ssm.py:116-125: F.silu, nn.Conv1d(padding=K-1) sliced

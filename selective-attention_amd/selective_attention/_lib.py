@@ -36,6 +36,9 @@ SIGNATURES: dict[str, list] = {
     "sa_paged_decode_workspace_size": [_i, _i, _i, _i, _i],
     "sa_paged_decode_fwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f,
                             _vp, _vp, _sz, _vp],
+    "sa_paged_decode_noalloc_limit": [],
+    "sa_paged_decode_fwd_noalloc": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i,
+                                    _f, _vp, _vp],
     "sa_sparse_attn_fwd": [_i, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _vp, _i, _i, _i, _f,
                            _vp, _vp],
     "sa_attn_varlen_fwd": [_i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _f, _vp, _vp],
@@ -70,6 +73,7 @@ SIGNATURES: dict[str, list] = {
 
 RESTYPES = {"sa_last_error": ctypes.c_char_p, "sa_profile_enable": None, "sa_ssd_bwd_workspace_size": ctypes.c_size_t,
             "sa_paged_decode_workspace_size": ctypes.c_size_t,
+            "sa_paged_decode_noalloc_limit": ctypes.c_size_t,
             "sa_ssm_conv_bwd_workspace_size": ctypes.c_size_t,
             "sa_ssm_gate_bwd_workspace_size": ctypes.c_size_t}
 
