@@ -60,8 +60,10 @@ __device__ __forceinline__ void frag_col_sums(const float (&v)[2][2][4], float (
 // workspace layout of the backward (shared by the size query and the launch)
 // ---------------------------------------------------------------------------
 struct BwdWs {
-  size_t dS, dCB, ddt_part, xB_part, xC_part, rsum, qpart, ddc_part, dA_part, db_part, total;
+  size_t dS, dCB, ddt_part, xB_part, xC_part, rsum, qpart, ddc_part, dA_part, db_part;
+  size_t dyp, dSp, dcbp, total;   // bf16 planes of the fused path
   int ptiles, ntiles, ttiles, per_bh;
+  bool fused;
 };
 
 inline size_t al256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -75,10 +77,14 @@ inline BwdWs bwd_layout(const SsdDims& d, size_t mt_bytes) {
   w.per_bh = static_cast<int>((PN + 1023) / 1024);
   const size_t bhc = static_cast<size_t>(d.b) * d.H * d.nc;
   size_t o = 0;
+  w.fused = mt_bytes == 2 && ssd_bwd_fused_shape_ok(d);
   w.dS = o;        o = al256(o + bhc * PN * 4);
-  // the fused bf16 path writes one dCB plane per pair of heads of a group
-  const size_t dcb_planes = mt_bytes == 2 && ssd_bwd_fused_shape_ok(d) ? (d.H / d.G + 1) / 2 : 1;
-  w.dCB = o;       o = al256(o + dcb_planes * d.b * d.nc * d.G * d.Lc * d.Lc * 4);
+  // the generic path's fp32 dCB; the fused path keeps dCB^T as bf16 planes
+  w.dCB = o;       o = al256(o + (w.fused ? 0 : static_cast<size_t>(d.b) * d.nc * d.G * d.Lc * d.Lc * 4));
+  const size_t bncg = static_cast<size_t>(d.b) * d.nc * d.G;
+  w.dyp = o;       o = al256(o + (w.fused ? bhc * d.Lc * 64 * 2 * 2 : 0));
+  w.dSp = o;       o = al256(o + (w.fused ? bhc * PN * 2 * 2 : 0));
+  w.dcbp = o;      o = al256(o + (w.fused ? bncg * w.ttiles * w.ttiles * 2 * 64 * 64 * 2 : 0));
   w.ddt_part = o;  o = al256(o + bhc * w.ptiles * d.Lc * 4);
   w.xB_part = o;   o = al256(o + bhc * w.ntiles * d.Lc * 4);
   w.xC_part = o;   o = al256(o + bhc * w.ntiles * d.Lc * 4);
@@ -97,10 +103,12 @@ inline BwdWs bwd_layout(const SsdDims& d, size_t mt_bytes) {
 //   G <- exp(dc_last[c]) G + dH_intra[c];        dh_init = G
 // dS enters holding dH_intra and leaves holding dS (in place).
 // ---------------------------------------------------------------------------
+// With dSp set, dS is written as bf16 hi + lo planes ([b][nc][H][2][P*N], the
+// fused backward's operand) instead of in place.
 __global__ __launch_bounds__(256) void state_passing_bwd_kernel(
     const float* __restrict__ states, float* __restrict__ dS, const float* __restrict__ dh_last,
     float* __restrict__ dh_init, const float* __restrict__ dc, float* __restrict__ ddc_part,
-    SsdDims d) {
+    bf16* __restrict__ dSp, SsdDims d) {
   constexpr int GRP = 4;
   __shared__ float red[GRP][4];
   const long PN = static_cast<long>(d.P) * d.N;
@@ -155,7 +163,21 @@ __global__ __launch_bounds__(256) void state_passing_bwd_kernel(
 #pragma unroll
         for (int q = 0; q < 4; ++q) s += hin[j][q] * G[q];
         part[j] = s * sc;
-        if (valid) store4(dS + ((static_cast<long>(b) * d.nc + c) * d.H + h) * PN + e0, G);
+        if (valid) {
+          const long bhc = (static_cast<long>(b) * d.nc + c) * d.H + h;
+          if (dSp) {   // full float4 groups only (PN % 4 == 0 on this path)
+            uint32_t hi[2], lo[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              hi[q] = pack_bf16x2(G[2 * q], G[2 * q + 1]);
+              lo[q] = pack_bf16x2(G[2 * q] - bf16lo_to_f32(hi[q]), G[2 * q + 1] - bf16hi_to_f32(hi[q]));
+            }
+            *reinterpret_cast<uint2*>(dSp + bhc * 2 * PN + e0) = uint2{hi[0], hi[1]};
+            *reinterpret_cast<uint2*>(dSp + bhc * 2 * PN + PN + e0) = uint2{lo[0], lo[1]};
+          } else {
+            store4(dS + bhc * PN + e0, G);
+          }
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) G[q] = sc * G[q] + dh[j][q];
       }
@@ -886,22 +908,29 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
   const long bnc = static_cast<long>(d.b) * d.nc;
   int rc;
 
-  const bool fused = sizeof(T) == 2 && ssd_bwd_fused_ok(d, u, Bm, Cm, dy);
-  // 1. dH_intra -> dS buffer
-  if ((rc = launch_chunk_outer<MT, float, T, 1>(dy, C_, dt, dc, length, dS, d, s))) return rc;
-  // 2. reverse state passing
+  const bool fused = sizeof(T) == 2 && w.fused && ssd_bwd_fused_ok(d, u, Bm, Cm, dy);
+  bf16* dyp = reinterpret_cast<bf16*>(ws + w.dyp);
+  bf16* dSp = reinterpret_cast<bf16*>(ws + w.dSp);
+  bf16* dcbp = reinterpret_cast<bf16*>(ws + w.dcbp);
+  // 1. dH_intra -> dS buffer (the fused path also writes dy as hi + lo planes)
+  if (fused) {
+    if ((rc = launch_dstate_planes(dy, C_, dt, dc, length, dS, dyp, d, s))) return rc;
+  } else {
+    if ((rc = launch_chunk_outer<MT, float, T, 1>(dy, C_, dt, dc, length, dS, d, s))) return rc;
+  }
+  // 2. reverse state passing (the fused path writes dS as hi + lo planes)
   {
     const long blocks = static_cast<long>(d.b) * d.H * w.per_bh;
     ProfScope prof_("state_passing_bwd", s);
     hipLaunchKernelGGL(state_passing_bwd_kernel, dim3(blocks), dim3(256), 0, s, states, dS,
-                       dh_last, dh_init, dc, ddc_part, d);
+                       dh_last, dh_init, dc, ddc_part, fused ? dSp : nullptr, d);
     SA_CHECK_LAUNCH("state_passing_bwd");
   }
   int ptiles = w.ptiles, ntiles = w.ntiles, qtiles = w.ttiles, rtiles = 1;
   if (fused) {
     // 3-5 fused: du, dB, dC, decay sums
-    if ((rc = launch_ssd_bwd_fused(u, Bm, Cm, dy, dt, dc, states, dS, length, du_, dB_, dC_, dCB,
-                                   ddt_part, xB_part, xC_part, qpart, rsum, d, lo >= 0.f, s)))
+    if ((rc = launch_ssd_bwd_fused(u, Bm, Cm, dyp, dt, dc, states, dSp, length, du_, dB_, dC_,
+                                   dcbp, ddt_part, xB_part, xC_part, qpart, rsum, d, lo >= 0.f, s)))
       return rc;
     ptiles = ntiles = qtiles = 1;
     rtiles = d.Lc / 64;

@@ -1,89 +1,174 @@
-// SSD chunked scan backward: fused bf16 path for headdim 64 (gfx950).
+// SSD chunked scan backward: the intra-chunk kernels of the bf16 path for
+// headdim 64, state_dim 128, chunk_size a multiple of 64, at most 4 heads per
+// group (gfx950).
 //
-// Replaces, for bf16 activations with headdim 64, state_dim 64 or 128,
-// chunk_size a multiple of 64 and at most 4 heads per group, the reference's
-// intra-chunk backward kernels (triton_kernels/ssd_scan/backward_kernel.py:
-// _chunk_scan_bwd_dx :187-317, _chunk_scan_bwd_dcb :569-668, the dC/dB
-// kernels :337-551 and the decay-gradient sums :689-765, :783-911) with two
-// kernels:
+// Replaces the reference's intra-chunk backward kernels
+// (triton_kernels/ssd_scan/backward_kernel.py: _chunk_scan_bwd_dx :187-317,
+// _chunk_scan_bwd_dcb :569-668, the dC / dB kernels :337-551 and the
+// decay-gradient sums :689-765, :783-911) with two kernels over one chunk of
+// one group (its HPG heads), each tile a 64-token strip:
 //
-//   ssd_bwd_col (one 512-thread block per (b, c, group, 64-wide source tile)):
-//     du, ddt_direct, dB (intra + state), x_B, the column sums q of
-//     M = W o CB, per-tile partial row sums r, and the dCB tiles (fp32, read
-//     by ssd_bwd_row).  Wave w owns the 16 source columns 16 (w & 3) + lane%16
-//     for head slot w >> 2: the two waves of a column strip work on two heads
-//     of the group at once (heads are taken two per pass) and exchange their
-//     dCB contributions through LDS once per target tile.
-//   ssd_bwd_row (one 256-thread block per (b, c, group, 64-wide target tile)):
-//     dC (state + intra through dCB) and x_C; wave w owns 16 target rows.
+//   ssd_bwd_src (one block per (b, c, group, source strip S), 8 waves in two
+//     head slots; wave w owns the 16 source columns
+//     sigma = 64 S + 16 (w % 4) + lane % 16 of its slot's heads):
+//       du     = dt * (e^{dc_last - dc} B.dS^T  +  L^T dy),  L = C.B^T o decay
+//       dB     = sum_h w_h u_h.dS_h  +  dCB^T C,            dCB = sum_h (dy_h u_h^T) dt decay
+//       x_B, ddt_direct, the column sums q and (per source strip) row sums r
+//       of M = W o CB for the decay gradient, and dCB of every target strip
+//       T >= S (bf16 hi + lo planes, [sigma][tau], read by ssd_bwd_tgt)
+//   ssd_bwd_tgt (one block per (b, c, group, target strip T), 4 waves; wave w
+//     owns the 16 target rows tau = 64 T + 16 w + lane % 16):
+//       dC     = sum_h e^{dc} dy_h.H_in_h  +  sum_{S <= T} dCB B,  and x_C
 //
-// All tile products use the 16x16x32 bf16 MFMA.  A product's result fragment
-// (rows in registers, column on the lane) is fed straight back as the B
-// operand of the next product that contracts over those rows; rows are
-// visited through key_of_row so that each lane's 8 rows are consecutive.
-// Operands that must be read along their rows *and* along their columns
-// (dy, C, dS, H_in, B) are staged once, row-major, in LDS: row reads give one
-// orientation, ds_read_b64_tr_b16 (lds_tr8) the other.
+// Operands reach LDS by DMA (global_load_lds, 16 bytes per lane) from bf16
+// planes written by the kernels before them: dy as hi + lo planes (by the
+// dH_intra kernel), dS as hi + lo planes (by the state-passing backward), B,
+// C and u as given.  fp32-origin operands (dy, dS, H_in, the decayed C.B^T
+// and dCB) are carried as hi + lo bf16 planes, their products as
+// hi*hi + lo*hi + hi*lo (or hi*x + lo*x against an exact bf16 operand), so
+// every product is close to an fp32 one.
 //
-// fp32-origin operands (dy, dS, H_in, the decayed C.B^T and dCB) are carried
-// as hi + lo bf16 planes, products as hi*hi + lo*hi + hi*lo (or hi*x + lo*x
-// against an exact bf16 operand), as in the generic kernels.
-//
-// Staging is a list of stages (fp32 tiles converted to hi/lo bf16, plus a
-// bf16 C or B tile on some stages).  The global loads of stage i+1 are issued
-// into registers before the MFMAs of stage i and written to the other LDS
-// slot after them, so one barrier per stage orders the pipeline.
+// A product's result fragment (rows in registers, column on the lane) feeds
+// the next product that contracts over those rows straight from registers:
+// the rows are visited through key_of_row, so each lane holds 8 consecutive
+// rows per 32-row k step.  LDS tiles are unpadded (DMA writes 1 KB runs) and
+// their 16-byte chunks are XOR-swizzled per row so that the row reads (row
+// sets of key_of_row or 16 consecutive rows) and the ds_read_b64_tr_b16
+// transposed reads hit distinct banks.
 #include "ssd_common.h"
 #include "prof.h"
 
 namespace sa {
-namespace {
-
-constexpr int kLY = 72;             // row length of a 64 x 64 bf16 staging plane
-constexpr int kPlane = 64 * kLY;    // elements per plane; a tile holds hi then lo
 
 // ---------------------------------------------------------------------------
-// staging helpers.  Rows past `rows_valid` read a clamped (valid) row and are
-// zeroed afterwards, so the loads are unconditional.
+// LDS layouts.  Chunk c (16 bytes) of row r is stored at chunk c ^ f(r).
 // ---------------------------------------------------------------------------
-// 64 x 64 fp32 tile; thread share (i in [0, 256)): row i/4, 16 columns from 16*(i%4)
-__device__ __forceinline__ void f32_tile_load(float4 (&r)[4], const float* src, int rs,
-                                              int rows_valid, int i) {
-  const int row = i >> 2, c0 = 16 * (i & 3);
-  const float* p = src + static_cast<unsigned>(min(row, rows_valid - 1) * rs + c0);
+// 128-byte rows (64 bf16) read through key_of_row row sets and transposed
+__host__ __device__ __forceinline__ int swz_k128(int r) {
+  return ((r >> 4) & 1) | (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
+}
+// 128-byte rows read as 16 consecutive rows and transposed
+__host__ __device__ __forceinline__ int swz_s128(int r) {
+  return (((r >> 1) & 1) << 1) | ((r >> 2) & 1) | (((r >> 3) & 1) << 2);
+}
+// 256-byte rows (128 bf16) read through key_of_row row sets and transposed
+__host__ __device__ __forceinline__ int swz_k256(int r) {
+  return ((r & 3) << 1) | (((r >> 3) & 1) << 3) | ((r >> 4) & 1);
+}
+
+// element offset of (row, col) in a swizzled tile with RC 16-byte chunks per row
+template <int RC, int (*F)(int)>
+__device__ __forceinline__ int toff(int row, int col) {
+  return row * (RC * 8) + 8 * ((col >> 3) ^ (F(row) & (RC - 1))) + (col & 7);
+}
+
+// 64 rows x RC chunks of bf16 from global (row stride grs elements; rows past
+// rows_valid repeat row rows_valid - 1) into a swizzled LDS tile; the 4 waves
+// of the block share the copy, one 1 KB DMA instruction per 64 chunks
+template <int RC, int (*F)(int)>
+__device__ __forceinline__ void dma_tile(bf16* lds, const bf16* g, long grs, int rows_valid,
+                                         int w, int lane) {
+  constexpr int NI = RC;          // 64 * RC chunks / 64 per instruction
+  constexpr int PW = NI / 4;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) r[q] = *reinterpret_cast<const float4*>(p + 4 * q);
-  if (row >= rows_valid) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) r[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int i = 0; i < PW; ++i) {
+    const int inst = w * PW + i;
+    const int pos = inst * 64 + lane;
+    const int row = pos / RC, pc = pos % RC;
+    const int gr = row < rows_valid ? row : rows_valid - 1;
+    __builtin_amdgcn_global_load_lds(g + gr * grs + 8 * (pc ^ (F(row) & (RC - 1))),
+                                     lds + inst * 512, 16, 0, 0);
   }
 }
-__device__ __forceinline__ void f32_tile_commit(bf16* tile, const float4 (&r)[4], int i) {
-  const int row = i >> 2, c0 = 16 * (i & 3);
-  uint32_t hi[8], lo[8];
+
+// lane offset (elements, row stride grs) of DMA instruction i of wave w for a
+// 64-row swizzled tile with RC chunks per row
+template <int RC, int (*F)(int)>
+__device__ __forceinline__ int dma_off(int i, int w, int lane, int grs) {
+  const int inst = w * (RC / 4) + i;
+  const int pos = inst * 64 + lane;
+  const int row = pos / RC, pc = pos % RC;
+  return row * grs + 8 * (pc ^ (F(row) & (RC - 1)));
+}
+// the tile copy of dma_tile with precomputed lane offsets (full tiles)
+template <int RC>
+__device__ __forceinline__ void dma_pre(bf16* lds, const bf16* g, const int (&off)[RC / 4], int w) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const float v[4] = {r[q].x, r[q].y, r[q].z, r[q].w};
+  for (int i = 0; i < RC / 4; ++i)
+    __builtin_amdgcn_global_load_lds(g + off[i], lds + (w * (RC / 4) + i) * 512, 16, 0, 0);
+}
+
+// the same for a tile copied by 8 waves (RC / 8 instructions each)
+template <int RC>
+__device__ __forceinline__ void dma_pre_w8(bf16* lds, const bf16* g, const int (&off)[RC / 8], int w) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t h = pack_bf16x2(v[2 * j], v[2 * j + 1]);
-      hi[2 * q + j] = h;
-      lo[2 * q + j] = pack_bf16x2(v[2 * j] - bf16lo_to_f32(h), v[2 * j + 1] - bf16hi_to_f32(h));
-    }
+  for (int i = 0; i < RC / 8; ++i)
+    __builtin_amdgcn_global_load_lds(g + off[i], lds + (w * (RC / 8) + i) * 512, 16, 0, 0);
+}
+// 8-wave copy of a partial tile: rows past rows_valid repeat row rows_valid - 1
+template <int RC, int (*F)(int)>
+__device__ __forceinline__ void dma_part_w8(bf16* lds, const bf16* g, long grs, int rows_valid,
+                                            int w, int lane) {
+#pragma unroll
+  for (int i = 0; i < RC / 8; ++i) {
+    const int inst = w * (RC / 8) + i, pos = inst * 64 + lane;
+    const int row = pos / RC, pc = pos % RC;
+    const int gr = row < rows_valid ? row : rows_valid - 1;
+    __builtin_amdgcn_global_load_lds(g + gr * grs + 8 * (pc ^ (F(row) & (RC - 1))),
+                                     lds + inst * 512, 16, 0, 0);
   }
-  uint4* ph = reinterpret_cast<uint4*>(tile + row * kLY + c0);
-  uint4* pl = reinterpret_cast<uint4*>(tile + kPlane + row * kLY + c0);
-  ph[0] = uint4{hi[0], hi[1], hi[2], hi[3]};
-  ph[1] = uint4{hi[4], hi[5], hi[6], hi[7]};
-  pl[0] = uint4{lo[0], lo[1], lo[2], lo[3]};
-  pl[1] = uint4{lo[4], lo[5], lo[6], lo[7]};
 }
-__device__ __forceinline__ uint2 pack4_bf16(const v4f& v) {
-  return uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+// lane offset of 8-wave DMA instruction i of wave w (RC chunks per row)
+template <int RC, int (*F)(int)>
+__device__ __forceinline__ int dma_off_w8(int i, int w, int lane, int grs) {
+  const int inst = w * (RC / 8) + i, pos = inst * 64 + lane;
+  const int row = pos / RC, pc = pos % RC;
+  return row * grs + 8 * (pc ^ (F(row) & (RC - 1)));
 }
+
+// fragment of 8 consecutive bf16 of one swizzled row
+template <int RC, int (*F)(int)>
+__device__ __forceinline__ v8bf row_frag(const bf16* t, int row, int col) {
+  return load_v8bf(t + toff<RC, F>(row, col));
+}
+
+// transposed read: every lane of a 16-lane group receives rows k0..k0+7 of
+// column c0 + (lane & 15) (k0 a multiple of 8, c0 a multiple of 16)
+template <int RC, int (*F)(int)>
+__device__ __forceinline__ v8bf tr_frag(const bf16* t, int k0, int c0, int lane) {
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const int i = lane & 15;
+  const int r0 = k0 + (i >> 2), col = c0 + 4 * (i & 3);
+  const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(t + toff<RC, F>(r0, col)));
+  const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(t + toff<RC, F>(r0 + 4, col)));
+  return __builtin_bit_cast(v8bf, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// transposed read at a precomputed lane offset: `off` addresses rows
+// k0 + i/4 (i = lane & 15), the second half rows k0 + 4 + i/4 at `off2`
+__device__ __forceinline__ v8bf tr_at(const bf16* t, int off, int off2) {
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(t + off));
+  const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(t + off2));
+  return __builtin_bit_cast(v8bf, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+// tile row offset of key_of_row(kt, .) relative to key_of_row(0, .)
+__host__ __device__ constexpr int kro(int kt) { return 32 * (kt >> 1) + 4 * (kt & 1); }
+
+// lane offset of the first transposed read of rows k0.. (k0 = 8 (lane >> 4) +
+// k_extra), columns c0 + 4 (i & 3)
+template <int RC, int (*F)(int)>
+__device__ __forceinline__ int tr_first(int k0, int c0, int lane) {
+  const int i = lane & 15;
+  return toff<RC, F>(k0 + (i >> 2), c0 + 4 * (i & 3));
+}
+
 __device__ __forceinline__ float dot4_bf16(const v4f& a, const uint2& q) {
   return a[0] * bf16lo_to_f32(q.x) + a[1] * bf16hi_to_f32(q.x) + a[2] * bf16lo_to_f32(q.y) +
          a[3] * bf16hi_to_f32(q.y);
+}
+__device__ __forceinline__ uint2 pack4_bf16(const v4f& v) {
+  return uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
 }
 // sum over the 4 lane groups (lanes l, l^16, l^32, l^48)
 __device__ __forceinline__ float group_sum(float v) {
@@ -91,17 +176,15 @@ __device__ __forceinline__ float group_sum(float v) {
   v += __shfl_xor(v, 32, 64);
   return v;
 }
-// DPP lane exchange inside rows of 16 lanes (VALU only, no LDS traffic)
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 // Row sums across the 16 lanes of each lane group: lane li of the group
-// returns sum over the group's lanes of v[li].  Each step pairs lanes that
+// returns the sum over the group's lanes of v[li].  Each step pairs lanes that
 // differ in one bit of li (row_mirror: bit 3, row_half_mirror: bit 2,
-// quad_perm 3210: bit 1, quad_perm 1032: bit 0; the partner also holds the
-// same absolute indices because it agrees on the bits already consumed) and
-// keeps the half of the values selected by that bit.
+// quad_perm 3210: bit 1, quad_perm 1032: bit 0) and keeps the half of the
+// values selected by that bit.
 __device__ __forceinline__ float transpose_reduce16(float (&m)[16], int li) {
   {
     const bool up = li & 8;
@@ -132,44 +215,65 @@ __device__ __forceinline__ float transpose_reduce16(float (&m)[16], int li) {
   return up ? b : a;
 }
 
+constexpr int kPlaneT = 64 * 64;   // bf16 elements of one 64 x 64 plane tile
+
+// index of this thread's wave in the block, as a wave-uniform (scalar) value
+__device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// every outstanding memory operation of the wave has completed (DMA included)
+__device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
+
+// an opaque copy of v: values derived from it are recomputed where they are
+// used instead of being hoisted out of loops into long-lived registers
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // ---------------------------------------------------------------------------
-// column kernel
+// source-strip kernel.  One 512-thread block per (b, c, group, source strip S)
+// and one block per CU.  Wave w = 4 s + q: head slot s (heads s HS .. s HS +
+// HS - 1, HS = ceil(HPG / 2)), source columns sigma = 64 S + 16 q + lane % 16.
+// The two waves of a column strip share the C.B^T tile (each computes it),
+// exchange their heads' dCB through LDS once per target strip, and split dB:
+// slot s owns the dB^T rows n in [N/2 s, N/2 s + N/2).
 // ---------------------------------------------------------------------------
 template <int NK, int HPG>
-struct ColSmem {
-  static constexpr int N = 32 * NK, LDC = N + 8;
-  static constexpr int HP = HPG < 2 ? HPG : 2;
-  static constexpr size_t kC = 64 * LDC;            // bf16 per C tile
-  static constexpr size_t kY = 2 * 2 * kPlane;      // bf16 per stage (2 head slots, hi + lo)
-  static constexpr size_t bytes = 2 * kC * 2 + 2 * kY * 2 + 2 * 2 * 2 * 64 * 4 +
-                                  2 * 4 * 4 * 64 * 16 + 2 * 2 * 4 * 64 * 4 + (2 * HPG * 64 + 4) * 4;
+struct SrcSmem {
+  static constexpr int N = 32 * NK;
+  static constexpr int HS = (HPG + 1) / 2;
+  static constexpr int kStage = 2 * 2 * kPlaneT;   // bf16: two heads' dy tiles (hi, lo) or dS n-halves
+  static constexpr int kC = 64 * N;                // bf16: one C tile
+  static constexpr size_t stage_off = 0;
+  static constexpr size_t c_off = stage_off + 2 * kStage * 2;
+  static constexpr size_t dc_off = c_off + 2 * kC * 2;         // float [2][HPG][64] dc (log2)
+  static constexpr size_t at_off = dc_off + 2 * HPG * 64 * 4;  // float [2][HPG][64] e^{dc - dc_T0}
+  static constexpr size_t r_off = at_off + 2 * HPG * 64 * 4;   // float [2 parity][2 slots][4 q][64]
+  static constexpr size_t x_off = r_off + 2 * 2 * 4 * 64 * 4;  // float4 [8 waves][4 kt][64] dCB exchange
+  static constexpr size_t bytes = x_off + 8 * 4 * 64 * 16;
 };
 
 template <int NK, int HPG>
-__global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
+__global__ __launch_bounds__(512, 1) void ssd_bwd_src_kernel(
     const bf16* __restrict__ u, const bf16* __restrict__ Bm, const bf16* __restrict__ Cm,
-    const float* __restrict__ dy, const float* __restrict__ dt, const float* __restrict__ dc,
-    const float* __restrict__ dS, const int64_t* __restrict__ length, bf16* __restrict__ du,
-    bf16* __restrict__ dB, float* __restrict__ dCB, float* __restrict__ ddt_part,
+    const bf16* __restrict__ dyp, const float* __restrict__ dt, const float* __restrict__ dc,
+    const bf16* __restrict__ dSp, const int64_t* __restrict__ length, bf16* __restrict__ du,
+    bf16* __restrict__ dB, bf16* __restrict__ dcbp, float* __restrict__ ddt_part,
     float* __restrict__ xB_part, float* __restrict__ qpart, float* __restrict__ rpart, SsdDims d,
     int mono) {
-  using SM = ColSmem<NK, HPG>;
-  constexpr int N = SM::N, LDC = SM::LDC;
-  constexpr int NH = N / 64;                 // 64-wide n halves of a dS tile
-  constexpr int NT = N / 16;                 // 16-row n tiles of dB^T
-  constexpr int NTW = NT / 2;                // n tiles owned by one head slot
-  constexpr int HP = SM::HP;                 // heads per pass (one per head slot)
-  constexpr int NPASS = (HPG + HP - 1) / HP;
+  using SM = SrcSmem<NK, HPG>;
+  constexpr int N = SM::N;
+  constexpr int HS = SM::HS;
+  constexpr int NH = N / 64;     // 64-wide n halves of a dS tile
+  constexpr int NTS = N / 32;    // 16-row n tiles of dB^T per slot
+  static_assert(NH == 2, "ssd_bwd_src: state_dim 128");
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* Cs = reinterpret_cast<bf16*>(smem_raw);      // [2][64][LDC]   C rows of a target tile
-  bf16* Ys = Cs + 2 * SM::kC;                        // [2][2 slots][hi, lo][64][kLY] stage tiles
-  float* dcs = reinterpret_cast<float*>(Ys + 2 * SM::kY);   // [2][2 slots][64] dc of the tile rows
-  float* ats = dcs + 2 * 2 * 64;   // [2][2 slots][64] e^{dc_t - dc_t0} of the tile rows
-  float4* xb = reinterpret_cast<float4*>(ats + 2 * 2 * 64);  // [2 slots][4 strips][4 kt][64] dCB
-  float* rW = reinterpret_cast<float*>(xb + 2 * 4 * 4 * 64); // [2][2 slots][4 strips][64]
-  float* sdc = rW + 2 * 2 * 4 * 64;   // [HPG][64] dc (log2) of the source positions
-  float* sdt = sdc + HPG * 64;        // [HPG][64] dt of the source positions (0 past the length)
-  float* sdl = sdt + HPG * 64;        // [HPG]     dc (log2) at the chunk end
+  bf16* stg = reinterpret_cast<bf16*>(smem_raw + SM::stage_off);   // [2][2 slots][hi, lo][64][64]
+  bf16* Cs = reinterpret_cast<bf16*>(smem_raw + SM::c_off);        // [2][64][N]
+  float* dcs = reinterpret_cast<float*>(smem_raw + SM::dc_off);
+  float* ats = reinterpret_cast<float*>(smem_raw + SM::at_off);
+  float* rx = reinterpret_cast<float*>(smem_raw + SM::r_off);
+  float4* xch = reinterpret_cast<float4*>(smem_raw + SM::x_off);
 
   const int stiles = d.Lc / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -186,33 +290,28 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
   const long tok0 = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc;
   const int u_rs = d.H * 64, act_rs = d.G * N;
   const int tid = threadIdx.x, lane = tid & 63, lg = lane >> 4, li = lane & 15;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (scalar)
-  const int strip = w & 3, hs = w >> 2;   // column strip, head slot
-  const int sl = 16 * strip + li;         // this lane's source row within the tile
-  const int sig = s0 + sl;                // this lane's source position
+  const int w = wave_index();
+  const int slot = w >> 2, q = w & 3;
+  const int sl = 16 * q + li;        // this lane's source column within the strip
+  const int sig = s0 + sl;           // its chunk position
   const int h0 = g * HPG;
-  const long bhc0 = (static_cast<long>(b) * d.H + h0) * d.nc + c;  // bhc of head k: bhc0 + k nc
-  // block-uniform bases; per-lane offsets are 32-bit
-  const bf16* uc = u + tok0 * u_rs + h0 * 64;                       // [Lc][H*64] from head h0
-  const bf16* Bc = Bm + tok0 * act_rs + static_cast<long>(g) * N;   // [Lc][G*N]
+  const long bhc0 = (static_cast<long>(b) * d.H + h0) * d.nc + c;   // head k: + k nc
+  const int hstride = d.nc * d.Lc;
+  const long bcg = (static_cast<long>(b) * d.nc + c) * d.G + g;
+  const bf16* uc = u + tok0 * u_rs + h0 * 64;
+  const bf16* Bc = Bm + tok0 * act_rs + static_cast<long>(g) * N;
   const bf16* Cc = Cm + tok0 * act_rs + static_cast<long>(g) * N;
-  const float* dyc = dy + tok0 * u_rs + h0 * 64;
-  const float* dSc = dS + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (64L * N);  // [HPG][64][N]
-  const float* dcc = dc + bhc0 * d.Lc;   // head k: + k nc Lc
+  const float* dcc = dc + bhc0 * d.Lc;
   const float* dtc = dt + bhc0 * d.Lc;
-  const int hstride = d.nc * d.Lc;       // dc / dt / partial rows between heads
   bf16* duc = du + tok0 * u_rs + h0 * 64;
   bf16* dBc = dB + tok0 * act_rs + static_cast<long>(g) * N;
-  // dCB: one plane per pass (the row kernel sums them)
-  const long dcb_plane = static_cast<long>(d.b) * d.nc * d.G * d.Lc * d.Lc;
-  float* dcbc = dCB + ((static_cast<long>(b) * d.nc + c) * d.G + g) * d.Lc * d.Lc;
   float* ddtc = ddt_part + bhc0 * d.Lc;
   float* xBc = xB_part + bhc0 * d.Lc;
   float* qc = qpart + bhc0 * d.Lc;
   float* rc = rpart + (bhc0 * stiles + S) * d.Lc;   // head k: + k nc stiles Lc
   const int rstride = d.nc * stiles * d.Lc;
 
-  if (s0 >= lim) {  // nothing of this source tile is inside the length: zero outputs / partials
+  if (s0 >= lim) {   // the strip is past the length: zero outputs and partials
     for (int e = tid; e < 64 * HPG * 8; e += 512) {
       const int row = e / (HPG * 8), col8 = e % (HPG * 8);
       if (s0 + row < qlim)
@@ -224,10 +323,10 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
         *reinterpret_cast<uint4*>(dBc + static_cast<unsigned>((s0 + row) * act_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
     }
     for (int k = 0; k < HPG; ++k) {
-      for (int e = tid; e < 64; e += 512) {
-        ddtc[k * hstride + s0 + e] = 0.f;
-        xBc[k * hstride + s0 + e] = 0.f;
-        qc[k * hstride + s0 + e] = 0.f;
+      if (tid < 64) {
+        ddtc[k * hstride + s0 + tid] = 0.f;
+        xBc[k * hstride + s0 + tid] = 0.f;
+        qc[k * hstride + s0 + tid] = 0.f;
       }
       for (int t = s0 + tid; t < d.Lc; t += 512) rc[k * rstride + t] = 0.f;
     }
@@ -235,200 +334,314 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
   }
 
   const bool sv = sig < lim;
-  const int scl = min(sig, lim - 1);            // clamped source row (valid address)
-  const int ntile = (lim + 63) / 64 - S;        // target tiles T = S .. S + ntile - 1
-  for (int e = tid; e < HPG * 64; e += 512) {
-    const int k = e / 64, r = e % 64;
-    const int sc = min(s0 + r, lim - 1);
-    sdc[e] = dcc[k * hstride + sc] * kLog2e;
-    sdt[e] = s0 + r < lim ? dtc[k * hstride + sc] : 0.f;
-  }
-  if (tid < HPG) sdl[tid] = dcc[tid * hstride + d.Lc - 1] * kLog2e;
+  const int scl = min(sig, lim - 1);       // clamped source row (a valid address)
+  const int ntile = (lim + 63) / 64 - S;   // target strips T = S .. S + ntile - 1
+  const int nstate = HS * NH;
+  const int nstage = nstate + HS * ntile;
 
-  // B fragments of this lane's source row (operand of C.B^T and dS.B^T)
-  v8bf Bf[NK];
-  {
-    const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 8 * lg);
+  // per head of the group at this lane's column: dc (log2), dt (0 past the
+  // length), the state weight w = e^{min(dc_last - dc, 0)} dt
+  float dck[HPG], dtk[HPG], wsk[HPG];
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+  for (int k = 0; k < HPG; ++k) {
+    dck[k] = dcc[k * hstride + scl] * kLog2e;
+    dtk[k] = sv ? dtc[k * hstride + scl] : 0.f;
+    wsk[k] = fast_exp2(fminf(dcc[k * hstride + d.Lc - 1] * kLog2e - dck[k], 0.f)) * dtk[k];
   }
 
-  // ---- stages.  A stage holds, for both head slots of the current pass, one
-  // fp32 64 x 64 tile (dS n-half or dy target tile) as hi / lo bf16 planes;
-  // target-tile stages also bring the C tile and the rows' dc.  Thread tid
-  // stages head slot tid / 256. ----
-  const int ts = tid >> 8, ti = tid & 255;
-  float4 pf[4];
-  BfTile<NK, 512> pc;
-  float pdc = 0.f, pdc0 = 0.f;
-  auto load_state = [&](int kb, int hp, int half) {
-    const int k = kb + min(ts, hp - 1);
-    f32_tile_load(pf, dSc + k * (64 * N) + 64 * half, N, 64, ti);
-  };
-  auto load_intra = [&](int kb, int hp, int T) {
-    const int k = kb + min(ts, hp - 1);
-    const int t0 = 64 * T, rv = min(64, lim - t0);
-    f32_tile_load(pf, dyc + t0 * u_rs + k * 64, u_rs, rv, ti);
-    pc.load(Cc + t0 * act_rs, act_rs, rv, tid);
-    const float* dch = dcc + (kb + min((tid >> 6) & 1, hp - 1)) * hstride + t0;
-    pdc = dch[tid & 63] * kLog2e;
-    pdc0 = dch[0] * kLog2e;
-  };
-  auto commit = [&](int slot, bool intra, int T) {
-    f32_tile_commit(Ys + slot * SM::kY + ts * 2 * kPlane, pf, ti);
-    if (intra) {
-      pc.commit(Cs + (T & 1) * SM::kC, LDC, tid);
-      if (tid < 128) {
-        dcs[slot * 128 + tid] = pdc;
-        ats[slot * 128 + tid] = fast_exp2(fminf(pdc - pdc0, 0.f));
+  // stage j: j < nstate: dS n half (j % NH) of heads {h, HS + h}, h = j / NH;
+  // then per target strip T = S + Ti the dy tiles of heads {h, HS + h},
+  // h = 0..HS-1 (C_T and the dc tables come with h == 0)
+  const bf16* dyg = dyp + (bcg * stiles) * (HPG * 2L * kPlaneT);   // + (T HPG + k) 2 kPlaneT
+  const bf16* dSg = dSp + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (2L * 64 * N);
+  // DMA lane offsets: instruction i of wave w covers tile chunk rows of one
+  // of the stage's two head tiles (waves 0-3: head slot 0, waves 4-7: slot 1)
+  int o_gs[2], o_gy[2], o_gc[NK / 2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    o_gs[i] = dma_off<8, swz_s128>(i, q, lane, N);
+    o_gy[i] = dma_off<8, swz_k128>(i, q, lane, 64);
+  }
+#pragma unroll
+  for (int i = 0; i < NK / 2; ++i) o_gc[i] = dma_off_w8<NK * 4, swz_k256>(i, w, lane, act_rs);
+  float pdc = 0.f, pdc0 = 0.f;   // dc prefetch of the next target strip (head tid / 64, row tid % 64)
+  auto issue = [&](int jj) {
+    bf16* dst = stg + (jj & 1) * SM::kStage + slot * (2 * kPlaneT);
+    if (jj < nstate) {
+      const int h = jj / NH, half = jj % NH, k = slot * HS + h;
+      if (k < HPG) {
+        const bf16* src = dSg + k * (2L * 64 * N) + 64 * half;
+        dma_pre<8>(dst, src, o_gs, q);
+        dma_pre<8>(dst + kPlaneT, src + 64L * N, o_gs, q);
+      }
+    } else {
+      const int qq = jj - nstate, Ti = qq / HS, h = qq % HS, T = S + Ti, k = slot * HS + h;
+      if (k < HPG) {
+        const bf16* src = dyg + (static_cast<long>(T) * HPG + k) * (2L * kPlaneT);
+        dma_pre<8>(dst, src, o_gy, q);
+        dma_pre<8>(dst + kPlaneT, src + kPlaneT, o_gy, q);
+      }
+      if (h == 0) {
+        const int t0 = 64 * T;
+        bf16* cdst = Cs + (T & 1) * SM::kC;
+        const bf16* csrc = Cc + static_cast<long>(t0) * act_rs;
+        // 8 waves x NK / 2 instructions cover the 64 x N tile
+        if (qlim - t0 >= 64) dma_pre_w8<NK * 4>(cdst, csrc, o_gc, w);
+        else dma_part_w8<NK * 4, swz_k256>(cdst, csrc, act_rs, qlim - t0, w, lane);
+        if (tid < HPG * 64) {
+          const float* dch = dcc + (tid >> 6) * hstride + t0;
+          pdc = dch[tid & 63] * kLog2e;
+          pdc0 = dch[0] * kLog2e;
+        }
       }
     }
   };
-  auto flush_r = [&](int stage, int kb, int hp, int T) {   // sum the 4 strips' row partials
-    if (tid < 64 * hp) {
-      const int h2 = tid >> 6, r = tid & 63;
-      const float* rr = rW + ((stage & 1) * 2 + h2) * 256;
-      rc[(kb + h2) * rstride + 64 * T + r] = rr[r] + rr[64 + r] + rr[128 + r] + rr[192 + r];
+  auto commit_dc = [&](int jj) {   // after the compute of stage jj - 1
+    if (jj < nstage && jj >= nstate && (jj - nstate) % HS == 0 && tid < HPG * 64) {
+      const int T = S + (jj - nstate) / HS;
+      dcs[(T & 1) * HPG * 64 + tid] = pdc;
+      ats[(T & 1) * HPG * 64 + tid] = fast_exp2(fminf(pdc - pdc0, 0.f));
+    }
+  };
+  auto flush_r = [&](int jj) {   // the row sums stage jj left in LDS -> rpart
+    const int qq = jj - nstate, Ti = qq / HS, h = qq % HS;
+    if (tid < 128) {
+      const int sl2 = tid >> 6, t = tid & 63, k = sl2 * HS + h;
+      if (k < HPG) {
+        const float* rr = rx + ((jj & 1) * 2 + sl2) * 256;
+        rc[k * rstride + 64 * (S + Ti) + t] = rr[t] + rr[64 + t] + rr[128 + t] + rr[192 + t];
+      }
     }
   };
 
-  v4f dBT[NTW];   // dB^T rows n = 16 (NTW hs + nt) + 4 lg + r, column sig; all heads
+  // per-lane element offsets of the fragment reads inside a tile (the
+  // swizzle of every row this lane reads depends on lane bits only, so each
+  // read is a precomputed offset plus a compile-time constant)
+  const int rl = 8 * (li >> 2) + (li & 3);   // key_of_row(kt, li) = rl + kro(kt)
+  int o_w[2], o_tr[4], o_c[NK], o_ct[NTS];
 #pragma unroll
-  for (int nt = 0; nt < NTW; ++nt) dBT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
-  int j = 0;      // running stage index (LDS slot parity)
-  load_state(0, HP, 0);
-  commit(0, false, 0);
+  for (int ks = 0; ks < 2; ++ks) o_w[ks] = toff<8, swz_k128>(rl, 32 * ks + 8 * lg);
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) o_tr[pt] = tr_first<8, swz_k128>(8 * lg, 16 * pt, lane);
+#pragma unroll
+  for (int ks = 0; ks < NK; ++ks) o_c[ks] = toff<NK * 4, swz_k256>(rl, 32 * ks + 8 * lg);
+#pragma unroll
+  for (int nt = 0; nt < NTS; ++nt)
+    o_ct[nt] = tr_first<NK * 4, swz_k256>(8 * lg, 16 * (NTS * slot + nt), lane);
+
+  v4f duT[HS][4];   // du^T of this slot's heads: rows p = 16 pt + 4 lg + r, column sig
+  v4f dBT[NTS];     // dB^T rows n = 16 (NTS slot + nt) + 4 lg + r, column sig
+  float qacc[HS];
+#pragma unroll
+  for (int h = 0; h < HS; ++h) {
+    qacc[h] = 0.f;
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) duT[h][pt] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int nt = 0; nt < NTS; ++nt) dBT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  issue(0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  auto end_stage = [&](int jj) {
+    commit_dc(jj);
+    wait_all_mem();
+    __syncthreads();
+  };
 
+  // ---- state stages: du^T += dS.B^T (n half), dB^T += w dS^T.u^T ----
+  {
+    int o_sd[2], o_st[4][2];
 #pragma unroll
-  for (int pass = 0; pass < NPASS; ++pass) {
-    const int kb = pass * HP;
-    const int hp = (HPG - kb) < HP ? (HPG - kb) : HP;   // heads in this pass
-    const bool last_pass = pass == NPASS - 1;
-    const bool active = hs < hp;                        // this wave has a head in this pass
-    const int k = kb + min(hs, hp - 1);                 // this wave's head
-    const float dck = sdc[k * 64 + sl], dtk = sdt[k * 64 + sl];
-    const float ek = sv ? fast_exp2(fminf(sdl[k] - dck, 0.f)) : 0.f;   // e^{dc_last - dc_sig}
-    // u fragments of this lane's source row for the pass's heads: [head slot][k-step]
-    v8bf uf[HP][2];
+    for (int ks = 0; ks < 2; ++ks) o_sd[ks] = toff<8, swz_s128>(li, 32 * ks + 8 * lg);
 #pragma unroll
-    for (int h2 = 0; h2 < HP; ++h2) {
-      const bf16* urow = uc + (kb + min(h2, hp - 1)) * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) uf[h2][ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+    for (int nt4 = 0; nt4 < 4; ++nt4) {
+      o_st[nt4][0] = tr_first<8, swz_s128>(8 * lg, 16 * nt4, lane);
+      o_st[nt4][1] = tr_first<8, swz_s128>(8 * lg + 4, 16 * nt4, lane);
     }
-    v8bf ufo[2];  // this wave's own head
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) ufo[ks] = (HP > 1 && hs == 1) ? uf[HP - 1][ks] : uf[0][ks];
-    v4f duT[4];   // du^T of this wave's head (rows p = 16 pt + 4 lg + r, column sig)
-    float qacc = 0.f;
+    for (int h = 0; h < HS; ++h) {
+      const int k = slot * HS + h;   // this wave's head (valid when k < HPG)
+      const bool kv = k < HPG;
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt) duT[pt] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    // ---- state stages (n half): du^T += dS B^T ; dB^T += w dS^T u^T ----
+      for (int half = 0; half < NH; ++half) {
+        const int j = h * NH + half;
+        if (j + 1 < nstage) issue(j + 1);
+        const bf16* Y = stg + (j & 1) * SM::kStage;
+        if (kv) {
+          const bf16* Yh = Y + slot * (2 * kPlaneT);
+          const bf16* Yl = Yh + kPlaneT;
+          v8bf Bf[2];
+          const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 64 * half + 8 * lg);
 #pragma unroll
-    for (int half = 0; half < NH; ++half, ++j) {
-      if (half + 1 < NH) load_state(kb, hp, half + 1);
-      else load_intra(kb, hp, S);
-      const bf16* Y = Ys + (j & 1) * SM::kY;
-      if (active) {
-        const bf16* Yh = Y + hs * 2 * kPlane;
+          for (int ks = 0; ks < 2; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+          for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt) {
+              const int off = o_sd[ks] + 16 * pt * 64;
+              duT[h][pt] = mfma_bf16(load_v8bf(Yh + off), Bf[ks], duT[h][pt]);
+              duT[h][pt] = mfma_bf16(load_v8bf(Yl + off), Bf[ks], duT[h][pt]);
+            }
+        }
+        if (half == slot) {
+          // this slot's n half of dB^T, from both heads of the stage
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            const int k2 = s2 * HS + h;
+            if (k2 >= HPG) continue;
+            const bf16* Yh = Y + s2 * (2 * kPlaneT);
+            const bf16* Yl = Yh + kPlaneT;
+            v8bf uf[2];
+            const bf16* urow = uc + k2 * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+            float wk = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < HPG; ++kk)
+              if (kk == k2) wk = wsk[kk];
+#pragma unroll
+            for (int nt = 0; nt < NTS; ++nt) {
+              v4f tmp = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int ks = 0; ks < 2; ++ks) {
+                const int a0 = o_st[nt][0] + 32 * ks * 64, a1 = o_st[nt][1] + 32 * ks * 64;
+                tmp = mfma_bf16(tr_at(Yh, a0, a1), uf[ks], tmp);
+                tmp = mfma_bf16(tr_at(Yl, a0, a1), uf[ks], tmp);
+              }
+              dBT[nt] += tmp * wk;
+            }
+          }
+        }
+        if (half == NH - 1 && kv) {
+          // head k's state part is complete: scale by e^{dc_last - dc_sig}; x_B
+          float dk = 0.f, dtv = 0.f;
+#pragma unroll
+          for (int kk = 0; kk < HPG; ++kk)
+            if (kk == k) {
+              dk = dck[kk];
+              dtv = dtk[kk];
+            }
+          const float ek = fast_exp2(fminf(dcc[k * hstride + d.Lc - 1] * kLog2e - dk, 0.f));
+          const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
+          float sx = 0.f;
 #pragma unroll
           for (int pt = 0; pt < 4; ++pt) {
-            const int off = (16 * pt + li) * kLY + 32 * ks + 8 * lg;
-            duT[pt] = mfma_bf16(load_v8bf(Yh + off), Bf[2 * half + ks], duT[pt]);
-            duT[pt] = mfma_bf16(load_v8bf(Yh + kPlane + off), Bf[2 * half + ks], duT[pt]);
+            duT[h][pt] *= ek;
+            sx += dot4_bf16(duT[h][pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
           }
-      }
-      // dB^T over this head slot's n tiles that fall in this half, all heads of the pass
-#pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) {
-        const int n16 = NTW * hs + nt;   // 16-row n tile index
-        if (n16 / 4 != half) continue;
-#pragma unroll
-        for (int h2 = 0; h2 < HP; ++h2) {
-          if (h2 >= hp) break;
-          const bf16* Yh = Y + h2 * 2 * kPlane;
-          const int kk = kb + h2;
-          const float wk = sv ? fast_exp2(fminf(sdl[kk] - sdc[kk * 64 + sl], 0.f)) * sdt[kk * 64 + sl] : 0.f;
-          v4f tmp = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            const int off = (32 * ks + 8 * lg) * kLY + 16 * (n16 % 4);
-            tmp = mfma_bf16(lds_tr8(Yh + off, kLY, lane), uf[h2][ks], tmp);
-            tmp = mfma_bf16(lds_tr8(Yh + kPlane + off, kLY, lane), uf[h2][ks], tmp);
-          }
-          dBT[nt] += tmp * wk;
+          sx = group_sum(sv ? sx : 0.f) * dtv;
+          if (lg == 0) xBc[k * hstride + sig] = sx;
         }
+        end_stage(j + 1);
       }
-      if (half == NH - 1 && active) {
-        // this head's state part is complete: scale by e^{dc_last - dc_sig}; x_B
-        const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
-        float s = 0.f;
-#pragma unroll
-        for (int pt = 0; pt < 4; ++pt) {
-          duT[pt] *= ek;
-          s += dot4_bf16(duT[pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
-        }
-        s = group_sum(sv ? s : 0.f) * dtk;
-        if (lg == 0) xBc[k * hstride + sig] = s;
-      }
-      commit((j + 1) & 1, half + 1 >= NH, S);
-      __syncthreads();
     }
+  }
 
-    // ---- target-tile stages ----
-    for (int Ti = 0; Ti < ntile; ++Ti, ++j) {
-      const int T = S + Ti;
-      const int t0 = 64 * T;
-      const bool has_next = Ti + 1 < ntile || !last_pass;
-      if (Ti + 1 < ntile) load_intra(kb, hp, T + 1);
-      else if (!last_pass) load_state(kb + HP, (HPG - kb - HP) < HP ? (HPG - kb - HP) : HP, 0);
-      if (Ti > 0) flush_r(j - 1, kb, hp, T - 1);
-      const int slot = j & 1;
-      const bf16* Yh = Ys + slot * SM::kY + min(hs, hp - 1) * 2 * kPlane;
-      const bf16* Yl = Yh + kPlane;
-      const float* dcT = dcs + slot * 128 + 64 * min(hs, hp - 1);
-      const float* atT = ats + slot * 128 + 64 * min(hs, hp - 1);
-      const bf16* Cb = Cs + (T & 1) * SM::kC;
-      const bool diag = Ti == 0 || t0 + 64 > lim;   // tile needs the causal / length masks
-      // off the diagonal with a monotone dc (dt >= 0), e^{min(dc_t - dc_sig, 0)} =
-      // e^{min(dc_t - dc_t0, 0)} e^{min(dc_t0 - dc_sig, 0)}: a row table times a
-      // per-lane factor
-      const bool fact = !diag && mono;
-      // C.B^T of this strip
-      v4f CB[4];
+  // dB^T[n, sig] += sum_t C[t, n] dCB[t, sig] of target strip Tp, after the
+  // exchange that completes dCB; this slot also stores half of dCB's planes
+  auto finish_pair = [&](int Tp, v4f (&dCBa)[4]) {
+    const float4* xi = xch + ((1 - slot) * 4 + q) * 4 * 64;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        CB[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-        const bf16* crow = Cb + key_of_row(kt, li) * LDC + 8 * lg;
+    for (int kt = 0; kt < 4; ++kt) {
+      const float4 o = xi[kt * 64 + lane];
+      dCBa[kt] += v4f{o.x, o.y, o.z, o.w};
+    }
+    const bf16* Cb = Cs + (Tp & 1) * SM::kC;
+    bf16* dst = dcbp + ((bcg * stiles + S) * stiles + Tp) * (2L * kPlaneT) + sl * 64 + 8 * lg;
 #pragma unroll
-        for (int ks = 0; ks < NK; ++ks) CB[kt] = mfma_bf16(load_v8bf(crow + 32 * ks), Bf[ks], CB[kt]);
+    for (int ks = 0; ks < 2; ++ks) {
+      v8bf dh, dl;
+      split_p(dCBa[2 * ks], dCBa[2 * ks + 1], dh, dl);
+      if (ks == slot) {
+        *reinterpret_cast<v8bf*>(dst + 32 * ks) = dh;
+        *reinterpret_cast<v8bf*>(dst + kPlaneT + 32 * ks) = dl;
       }
-      v4f dCBa[4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) dCBa[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-      if (active) {
+      for (int nt = 0; nt < NTS; ++nt) {
+        const int a0 = o_ct[nt] + 32 * ks * N;
+        const v8bf a = tr_at(Cb, a0, a0 + 4 * N);
+        dBT[nt] = mfma_bf16(a, dh, dBT[nt]);
+        dBT[nt] = mfma_bf16(a, dl, dBT[nt]);
+      }
+    }
+  };
+
+  // ---- pair stages: target strip T = S + Ti, head k = slot HS + h ----
+  v4f dCBa[4];
+  for (int Ti = 0; Ti < ntile; ++Ti) {
+    const int T = S + Ti, t0 = 64 * T;
+    const bf16* Cb = Cs + (T & 1) * SM::kC;
+    const bool diag = Ti == 0;
+    const bool fact = !diag && mono;
+    v4f CB[4];
+#pragma unroll
+    for (int h = 0; h < HS; ++h) {
+      const int j = nstate + Ti * HS + h;
+      const int k = slot * HS + h;
+      const bool kv = k < HPG;
+      // with one head per slot, stage j + 1 brings the C tile of strip T + 1
+      // into the buffer finish_pair(T - 1) reads, and this stage rewrites the
+      // exchange finish_pair reads: every wave finishes it first
+      if (HS == 1 && Ti > 0) {
+        finish_pair(T - 1, dCBa);
+        __syncthreads();
+      }
+      if (j + 1 < nstage) issue(j + 1);
+      if (j > nstate) flush_r(j - 1);
+      if (HS > 1 && h == 0 && Ti > 0) finish_pair(T - 1, dCBa);
+      const bf16* Yh = stg + (j & 1) * SM::kStage + slot * (2 * kPlaneT);
+      const bf16* Yl = Yh + kPlaneT;
+      if (h == 0) {
+        v8bf Bf[NK];
+        const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 8 * lg);
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          CB[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+          dCBa[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < NK; ++ks)
+            CB[kt] = mfma_bf16(load_v8bf(Cb + o_c[ks] + kro(kt) * N), Bf[ks], CB[kt]);
+        }
+      }
+      if (kv) {
+        const float* dcT = dcs + (T & 1) * HPG * 64 + 64 * k;
+        const float* atT = ats + (T & 1) * HPG * 64 + 64 * k;
+        v8bf uf[2];
+        {
+          const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+        }
+        float dk = 0.f, dtv = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < HPG; ++kk)
+          if (kk == k) {
+            dk = dck[kk];
+            dtv = dtk[kk];
+          }
         // W[t, sig] = dy[t] . u[sig]
         v4f W[4];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
           W[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-          const int off = key_of_row(kt, li) * kLY + 8 * lg;
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
-            W[kt] = mfma_bf16(load_v8bf(Yh + off + 32 * ks), ufo[ks], W[kt]);
-            W[kt] = mfma_bf16(load_v8bf(Yl + off + 32 * ks), ufo[ks], W[kt]);
+            W[kt] = mfma_bf16(load_v8bf(Yh + o_w[ks] + kro(kt) * 64), uf[ks], W[kt]);
+            W[kt] = mfma_bf16(load_v8bf(Yl + o_w[ks] + kro(kt) * 64), uf[ks], W[kt]);
           }
         }
-        // decay and masks; dCB = W', M = W' o CB (q: column sums, r: row sums); W <- L
+        // decay and masks: dCB += W', M = W' o CB (q: column sums, r: row sums); W <- L
         float m[16];
         float qs = 0.f;
         if (fact) {
-          const float bk = fast_exp2(fminf(dcT[0] - dck, 0.f));
-          const float bdt = bk * dtk;
+          // off the diagonal with a monotone dc, e^{min(dc_t - dc_sig, 0)} =
+          // e^{min(dc_t - dc_t0, 0)} e^{min(dc_t0 - dc_sig, 0)}
+          const float bk = fast_exp2(fminf(dcT[0] - dk, 0.f));
+          const float bdt = bk * dtv;
 #pragma unroll
           for (int kt = 0; kt < 4; ++kt) {
             const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);
@@ -437,7 +650,7 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const float wv = W[kt][r] * (av[r] * bdt);
-              dCBa[kt][r] = wv;
+              dCBa[kt][r] += wv;
               const float mv = wv * CB[kt][r];
               m[4 * kt + r] = mv;
               qs += mv;
@@ -447,16 +660,16 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
         } else {
 #pragma unroll
           for (int kt = 0; kt < 4; ++kt) {
-            const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);   // first of 4 consecutive rows
+            const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);
             const float4 dq = *reinterpret_cast<const float4*>(dcT + tb);
             const float dv[4] = {dq.x, dq.y, dq.z, dq.w};
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int t = t0 + tb + r;
-              float dec = fast_exp2(fminf(dv[r] - dck, 0.f));
+              float dec = fast_exp2(fminf(dv[r] - dk, 0.f));
               dec = (t >= sig && t < lim) ? dec : 0.f;
-              const float wv = W[kt][r] * dtk * dec;
-              dCBa[kt][r] = wv;
+              const float wv = W[kt][r] * dtv * dec;
+              dCBa[kt][r] += wv;
               const float mv = t > sig ? wv * CB[kt][r] : 0.f;
               m[4 * kt + r] = mv;
               qs += mv;
@@ -464,120 +677,95 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_col_kernel(
             }
           }
         }
-        qacc += qs;
-        rW[((j & 1) * 2 + hs) * 256 + strip * 64 + key_of_row(li >> 2, 4 * lg + (li & 3))] =
+        qacc[h] += qs;
+        rx[((j & 1) * 2 + slot) * 256 + q * 64 + key_of_row(li >> 2, 4 * lg + (li & 3))] =
             transpose_reduce16(m, li);
-        // du^T[p, sig] += sum_t dy[t, p] L[t, sig]  (L and dy as hi + lo: with weak
-        // decay and small dt, ddt = sum_p u du cancels to ~1e-2 of its terms, and
-        // a single-plane L leaves ~0.2 % of the tensor scale of error there)
+        // du^T[p, sig] += sum_t dy[t, p] L[t, sig]  (L and dy as hi + lo)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           v8bf lh, ll;
           split_p(W[2 * ks], W[2 * ks + 1], lh, ll);
 #pragma unroll
           for (int pt = 0; pt < 4; ++pt) {
-            const int off = (32 * ks + 8 * lg) * kLY + 16 * pt;
-            const v8bf yh = lds_tr8(Yh + off, kLY, lane);
-            duT[pt] = mfma_bf16(yh, lh, duT[pt]);
-            duT[pt] = mfma_bf16(lds_tr8(Yl + off, kLY, lane), lh, duT[pt]);
-            duT[pt] = mfma_bf16(yh, ll, duT[pt]);
+            const int a0 = o_tr[pt] + 32 * ks * 64;
+            const v8bf yh = tr_at(Yh, a0, a0 + 4 * 64);
+            const v8bf yl = tr_at(Yl, a0, a0 + 4 * 64);
+            duT[h][pt] = mfma_bf16(yh, lh, duT[h][pt]);
+            duT[h][pt] = mfma_bf16(yl, lh, duT[h][pt]);
+            duT[h][pt] = mfma_bf16(yh, ll, duT[h][pt]);
           }
         }
       }
-      // dCB of the pass's heads: add the other head slot's contribution of the
-      // strip (zeros from a slot without a head in this pass)
-      {
-        float4* xo = xb + (hs * 4 + strip) * 4 * 64;
+      if (h == HS - 1) {
+        // this slot's part of dCB for the exchange
+        float4* xo = xch + (slot * 4 + q) * 4 * 64;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) xo[kt * 64 + lane] = make_float4(dCBa[kt][0], dCBa[kt][1], dCBa[kt][2], dCBa[kt][3]);
-        __syncthreads();
-        const float4* xi = xb + ((1 - hs) * 4 + strip) * 4 * 64;
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          const float4 o = xi[kt * 64 + lane];
-          dCBa[kt] += v4f{o.x, o.y, o.z, o.w};
-        }
       }
-      // head slot hs stores rows kt in {2 hs, 2 hs + 1} of this pass's dCB tile
-      {
-        float* dcbt = dcbc + pass * dcb_plane + t0 * d.Lc;
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-          if ((kt >> 1) == hs) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              dcbt[static_cast<unsigned>(key_of_row(kt, 4 * lg + r) * d.Lc + sig)] = dCBa[kt][r];
-          }
-      }
-      // dB^T[n, sig] += sum_t C[t, n] dCB[t, sig] for this slot's n tiles
-      {
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          v8bf dh, dl;
-          split_p(dCBa[2 * ks], dCBa[2 * ks + 1], dh, dl);
-#pragma unroll
-          for (int nt = 0; nt < NTW; ++nt) {
-            const v8bf a = lds_tr8(Cb + (32 * ks + 8 * lg) * LDC + 16 * (NTW * hs + nt), LDC, lane);
-            dBT[nt] = mfma_bf16(a, dh, dBT[nt]);
-            dBT[nt] = mfma_bf16(a, dl, dBT[nt]);
-          }
-        }
-      }
-      if (has_next) commit((j + 1) & 1, Ti + 1 < ntile, T + 1);
-      __syncthreads();
+      end_stage(j + 1);
     }
-    flush_r(j - 1, kb, hp, S + ntile - 1);
+  }
+  flush_r(nstage - 1);
+  finish_pair(S + ntile - 1, dCBa);
+  // row-sum partials of target strips past the length are zero
+  for (int k = 0; k < HPG; ++k)
+    for (int t = 64 * (S + ntile) + tid; t < d.Lc; t += 512) rc[k * rstride + t] = 0.f;
 
-    // ---- pass epilogue: du, ddt_direct, q of this wave's head ----
-    if (active) {
-      const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
-      float s = 0.f;
+  // ---- epilogue: du, ddt_direct, q of this slot's heads; this slot's dB half ----
 #pragma unroll
-      for (int pt = 0; pt < 4; ++pt) s += dot4_bf16(duT[pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
-      s = group_sum(sv ? s : 0.f);
-      const float q = group_sum(qacc);
-      if (sig < qlim) {
-        bf16* durow = duc + k * 64 + static_cast<unsigned>(sig * u_rs + 4 * lg);
+  for (int h = 0; h < HS; ++h) {
+    const int k = slot * HS + h;
+    if (k >= HPG) continue;
+    float dtv = 0.f;
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt) *reinterpret_cast<uint2*>(durow + 16 * pt) = pack4_bf16(duT[pt] * dtk);
-      }
-      if (lg == 0) {
-        ddtc[k * hstride + sig] = s;
-        qc[k * hstride + sig] = q;
-      }
+    for (int kk = 0; kk < HPG; ++kk)
+      if (kk == k) dtv = dtk[kk];
+    const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
+    float sx = 0.f;
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) sx += dot4_bf16(duT[h][pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
+    sx = group_sum(sv ? sx : 0.f);
+    const float qv = group_sum(qacc[h]);
+    if (sig < qlim) {
+      bf16* durow = duc + k * 64 + static_cast<unsigned>(sig * u_rs + 4 * lg);
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) *reinterpret_cast<uint2*>(durow + 16 * pt) = pack4_bf16(duT[h][pt] * dtv);
     }
-    for (int kk = 0; kk < hp; ++kk)
-      for (int t = 64 * (S + ntile) + tid; t < d.Lc; t += 512) rc[(kb + kk) * rstride + t] = 0.f;
+    if (lg == 0) {
+      ddtc[k * hstride + sig] = sx;
+      qc[k * hstride + sig] = qv;
+    }
   }
   if (sig < qlim) {
-    bf16* dbrow = dBc + static_cast<unsigned>(sig * act_rs + 16 * NTW * hs + 4 * lg);
+    bf16* dbrow = dBc + static_cast<unsigned>(sig * act_rs + 16 * NTS * slot + 4 * lg);
 #pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) *reinterpret_cast<uint2*>(dbrow + 16 * nt) = pack4_bf16(dBT[nt]);
+    for (int nt = 0; nt < NTS; ++nt) *reinterpret_cast<uint2*>(dbrow + 16 * nt) = pack4_bf16(dBT[nt]);
   }
 }
 
 // ---------------------------------------------------------------------------
-// row kernel: dC and x_C
+// target-strip kernel: dC and x_C
 // ---------------------------------------------------------------------------
 template <int NK>
-struct RowSmem {
-  static constexpr int N = 32 * NK, LDC = N + 8;
-  static constexpr size_t slot_elems = (2 * kPlane > 64 * LDC) ? 2 * kPlane : 64 * LDC;
-  static constexpr size_t bytes = 2 * slot_elems * 2;
+struct TgtSmem {
+  static constexpr int N = 32 * NK;
+  // a stage: H_in of one head (hi, lo: 2 x 64 x N) or B_S (64 x N) + dCB^T (hi, lo: 2 x 64 x 64)
+  static constexpr int kStage = 2 * 64 * N > 64 * N + 2 * kPlaneT ? 2 * 64 * N : 64 * N + 2 * kPlaneT;
+  static constexpr size_t bytes = 2 * kStage * 2;
 };
 
 template <int NK, int HPG>
-__global__ __launch_bounds__(256, 2) void ssd_bwd_row_kernel(
-    const bf16* __restrict__ Bm, const bf16* __restrict__ Cm, const float* __restrict__ dy,
-    const float* __restrict__ dc, const float* __restrict__ states, const float* __restrict__ dCB,
-    const int64_t* __restrict__ length, bf16* __restrict__ dC, float* __restrict__ xC_part,
-    SsdDims d) {
-  using SM = RowSmem<NK>;
-  constexpr int N = SM::N, LDC = SM::LDC;
-  constexpr int NH = N / 64, NT = N / 16;
-  constexpr int nS = NH * HPG;
+__global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
+    const bf16* __restrict__ Bm, const bf16* __restrict__ Cm, const bf16* __restrict__ dyp,
+    const float* __restrict__ dc, const float* __restrict__ states,
+    const bf16* __restrict__ dcbp, const int64_t* __restrict__ length, bf16* __restrict__ dC,
+    float* __restrict__ xC_part, SsdDims d) {
+  using SM = TgtSmem<NK>;
+  constexpr int N = SM::N;
+  constexpr int NT = N / 16;
+  constexpr int RC = N / 8;   // 16-byte chunks per row of an N-wide tile
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* slots = reinterpret_cast<bf16*>(smem_raw);  // [2][slot_elems]
+  bf16* stg = reinterpret_cast<bf16*>(smem_raw);   // [2][kStage]
 
   const int ttiles = d.Lc / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -592,22 +780,19 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_row_kernel(
   const int len = seq_limit(length, b, d.L);
   const int lim = max(0, chunk_limit(len, c, d.Lc));
   const long tok0 = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc;
-  const int u_rs = d.H * 64, act_rs = d.G * N;
+  const int act_rs = d.G * N;
   const int tid = threadIdx.x, lane = tid & 63, lg = lane >> 4, li = lane & 15;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (scalar)
-  const int tau = t0 + 16 * w + li;
+  const int w = wave_index();
+  const int tl = 16 * w + li;   // this lane's target row within the strip
+  const int tau = t0 + tl;
   const int h0 = g * HPG;
   const long bhc0 = (static_cast<long>(b) * d.H + h0) * d.nc + c;
   const int hstride = d.nc * d.Lc;
-  // block-uniform bases; per-lane offsets are 32-bit
+  const long bcg = (static_cast<long>(b) * d.nc + c) * d.G + g;
   const bf16* Bc = Bm + tok0 * act_rs + static_cast<long>(g) * N;
   const bf16* Cc = Cm + tok0 * act_rs + static_cast<long>(g) * N;
-  const float* dyc = dy + tok0 * u_rs + h0 * 64;
   const float* Hc = states + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (64L * N);
   const float* dcc = dc + bhc0 * d.Lc;
-  constexpr int NPASS = (HPG + 1) / 2;   // dCB planes written by the column kernel
-  const long dcb_plane = static_cast<long>(d.b) * d.nc * d.G * d.Lc * d.Lc;
-  const float* dcbc = dCB + ((static_cast<long>(b) * d.nc + c) * d.G + g) * d.Lc * d.Lc;
   bf16* dCc = dC + tok0 * act_rs + static_cast<long>(g) * N;
   float* xCc = xC_part + bhc0 * d.Lc;
 
@@ -618,208 +803,201 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_row_kernel(
         *reinterpret_cast<uint4*>(dCc + static_cast<unsigned>((t0 + row) * act_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
     }
     for (int k = 0; k < HPG; ++k)
-      for (int e = tid; e < 64; e += 256) xCc[k * hstride + t0 + e] = 0.f;
+      if (tid < 64) xCc[k * hstride + t0 + tid] = 0.f;
     return;
   }
-  const bool tv = tau < lim;
-  const int tcl = min(tau, lim - 1);
-  // C[tau, 16 nt + 4 lg + r] for x_C
-  uint2 Cq[NT];
+
+  const int tcl = min(tau, qlim - 1);   // clamped target row (a valid address)
+  // C of this lane's row at the dC^T fragment positions n = 16 nt + 4 lg + r
+  uint2 cv[NT];
   {
     const bf16* crow = Cc + static_cast<unsigned>(tcl * act_rs + 4 * lg);
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) Cq[nt] = *reinterpret_cast<const uint2*>(crow + 16 * nt);
+    for (int nt = 0; nt < NT; ++nt) cv[nt] = *reinterpret_cast<const uint2*>(crow + 16 * nt);
   }
-  v4f dCT[NT], tmp[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) dCT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  float4 pf[4];          // state stage: H_in tile
-  BfTile<NK, 256> pc;    // intra stage: B tile
-  float4 pg[4];          // dy[tau] of a head (state) / dCB[tau] row piece (intra)
-  float4 cur[4];
-  const unsigned dcb_off = static_cast<unsigned>(tcl * d.Lc + 8 * lg);
-  const unsigned dy_off = static_cast<unsigned>(tcl * u_rs + 8 * lg);
-  auto frag_load = [&](const float* p) {
+  // dy planes of this lane's row: [head][k step][hi, lo]
+  const bf16* dyg = dyp + ((bcg * ttiles + T) * HPG) * (2L * kPlaneT) + tl * 64 + 8 * lg;
+  auto load_dy = [&](int k, v8bf (&f)[2][2]) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      pg[2 * ks] = *reinterpret_cast<const float4*>(p + 32 * ks);
-      pg[2 * ks + 1] = *reinterpret_cast<const float4*>(p + 32 * ks + 4);
-    }
-    if (!tv) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  };
-  auto load_state = [&](int k, int half) {
-    f32_tile_load(pf, Hc + k * (64 * N) + 64 * half, N, 64, tid);
-    if (half == 0) frag_load(dyc + k * 64 + dy_off);
-  };
-  auto load_intra = [&](int S) {
-    const int s0 = 64 * S;
-    pc.load(Bc + s0 * act_rs, act_rs, min(64, lim - s0), tid);
-    frag_load(dcbc + s0 + dcb_off);
-#pragma unroll
-    for (int p = 1; p < NPASS; ++p) {
-      const float* q = dcbc + p * dcb_plane + s0 + dcb_off;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const float4 a = *reinterpret_cast<const float4*>(q + 32 * ks);
-        const float4 e = *reinterpret_cast<const float4*>(q + 32 * ks + 4);
-        pg[2 * ks] = make_float4(pg[2 * ks].x + a.x, pg[2 * ks].y + a.y, pg[2 * ks].z + a.z, pg[2 * ks].w + a.w);
-        pg[2 * ks + 1] = make_float4(pg[2 * ks + 1].x + e.x, pg[2 * ks + 1].y + e.y,
-                                     pg[2 * ks + 1].z + e.z, pg[2 * ks + 1].w + e.w);
-      }
+      f[ks][0] = load_v8bf(dyg + k * (2L * kPlaneT) + 32 * ks);
+      f[ks][1] = load_v8bf(dyg + k * (2L * kPlaneT) + kPlaneT + 32 * ks);
     }
   };
 
-  load_state(0, 0);
-  f32_tile_commit(slots, pf, tid);
+  // stage j: j < HPG: H_in of head j (fp32 -> hi, lo through registers);
+  // then S = j - HPG = 0..T: B_S and dCB^T of (S, T) by DMA
+  const int nstage = HPG + T + 1;
+  float4 ph[8];   // H prefetch: row tid / 4, columns 32 (tid % 4) .. +31 (N = 128)
+  static_assert(NK == 4, "ssd_bwd_tgt: state_dim 128");
+  auto load_h = [&](int k) {
+    const float* src = Hc + k * (64L * N) + (tid >> 2) * N + 32 * (tid & 3);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) cur[i] = pg[i];
+    for (int i = 0; i < 8; ++i) ph[i] = *reinterpret_cast<const float4*>(src + 4 * i);
+  };
+  auto commit_h = [&](int jj) {
+    bf16* dst = stg + (jj & 1) * SM::kStage;
+    const int row = tid >> 2;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {   // 16-byte chunks 4 (tid % 4) + cc
+      const float v[8] = {ph[2 * cc].x, ph[2 * cc].y, ph[2 * cc].z, ph[2 * cc].w,
+                          ph[2 * cc + 1].x, ph[2 * cc + 1].y, ph[2 * cc + 1].z, ph[2 * cc + 1].w};
+      uint32_t hi[4], lo[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        hi[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+        lo[e] = pack_bf16x2(v[2 * e] - bf16lo_to_f32(hi[e]), v[2 * e + 1] - bf16hi_to_f32(hi[e]));
+      }
+      const int off = toff<RC, swz_k256>(row, 8 * (4 * (tid & 3) + cc));
+      *reinterpret_cast<uint4*>(dst + off) = uint4{hi[0], hi[1], hi[2], hi[3]};
+      *reinterpret_cast<uint4*>(dst + 64 * N + off) = uint4{lo[0], lo[1], lo[2], lo[3]};
+    }
+  };
+  auto issue_intra = [&](int jj) {
+    const int S = jj - HPG;
+    bf16* dst = stg + (jj & 1) * SM::kStage;
+    dma_tile<RC, swz_k256>(dst, Bc + static_cast<long>(64 * S) * act_rs, act_rs,
+                           min(64, qlim - 64 * S), w, lane);
+    const bf16* src = dcbp + ((bcg * ttiles + S) * ttiles + T) * (2L * kPlaneT);
+    dma_tile<8, swz_k128>(dst + 64 * N, src, 64, 64, w, lane);
+    dma_tile<8, swz_k128>(dst + 64 * N + kPlaneT, src + kPlaneT, 64, 64, w, lane);
+  };
+
+  v4f dCT[NT];   // dC^T rows n = 16 nt + 4 lg + r, column tau
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) dCT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+  v8bf dyf[2][2], dyn[2][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) dyn[ks][0] = dyn[ks][1] = zero_v8bf();
+  load_h(0);
+  load_dy(0, dyf);
+  commit_h(0);
   __syncthreads();
 
-  // ---- state stages: tmp^T[n, tau] = sum_p H[p, n] dy[tau, p] ; dC^T += e tmp^T ; x_C ----
-#pragma unroll
-  for (int j = 0; j < nS; ++j) {
-    const int k = j / NH, half = j % NH;
-    if (j + 1 < nS) load_state((j + 1) / NH, (j + 1) % NH);
-    else load_intra(0);
-    const bf16* Yh = slots + (j & 1) * SM::slot_elems;
-    const bf16* Yl = Yh + kPlane;
-    v8bf fh[2], fl[2];
-    split8(cur[0], cur[1], fh[0], fl[0]);
-    split8(cur[2], cur[3], fh[1], fl[1]);
-    if (half == 0) {
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) tmp[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < nstage; ++j) {
+    if (j + 1 < HPG) {
+      load_h(j + 1);
+      load_dy(j + 1, dyn);
+    } else if (j + 1 < nstage) {
+      issue_intra(j + 1);
     }
+    const bf16* Sg = stg + (j & 1) * SM::kStage;
+    if (j < HPG) {
+      // X^T[n, tau] = sum_p H[p, n] dy[tau, p]; dC^T += e^{dc_tau} X^T; x_C
+      const int k = j;
+      v4f X[NT];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+      for (int nt = 0; nt < NT; ++nt) X[nt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int off = (32 * ks + 8 * lg) * kLY + 16 * nt;
-        const v8bf ah = lds_tr8(Yh + off, kLY, lane);
-        const v8bf al = lds_tr8(Yl + off, kLY, lane);
-        tmp[4 * half + nt] = mfma_bf16(ah, fh[ks], tmp[4 * half + nt]);
-        tmp[4 * half + nt] = mfma_bf16(al, fh[ks], tmp[4 * half + nt]);
-        tmp[4 * half + nt] = mfma_bf16(ah, fl[ks], tmp[4 * half + nt]);
-      }
-    if (half == NH - 1) {
-      const float e = tv ? fast_exp2(dcc[k * hstride + tcl] * kLog2e) : 0.f;
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const v8bf hh = tr_frag<RC, swz_k256>(Sg, 32 * ks + 8 * lg, 16 * nt, lane);
+          const v8bf hl = tr_frag<RC, swz_k256>(Sg + 64 * N, 32 * ks + 8 * lg, 16 * nt, lane);
+          X[nt] = mfma_bf16(hh, dyf[ks][0], X[nt]);
+          X[nt] = mfma_bf16(hl, dyf[ks][0], X[nt]);
+          X[nt] = mfma_bf16(hh, dyf[ks][1], X[nt]);
+        }
+      const float e = fast_exp2(dcc[k * hstride + tcl] * kLog2e);
       float s = 0.f;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        s += dot4_bf16(tmp[nt], Cq[nt]);
-        dCT[nt] += tmp[nt] * e;
+        X[nt] *= e;
+        s += dot4_bf16(X[nt], cv[nt]);
+        dCT[nt] += X[nt];
       }
-      s = group_sum(s) * e;
-      if (lg == 0) xCc[k * hstride + tau] = s;
-    }
-    if (j + 1 < nS) f32_tile_commit(slots + ((j + 1) & 1) * SM::slot_elems, pf, tid);
-    else pc.commit(slots + ((j + 1) & 1) * SM::slot_elems, LDC, tid);
-    if (j + 1 >= nS || (j + 1) % NH == 0) {
+      s = group_sum(s);
+      if (lg == 0) xCc[k * hstride + tau] = tau < lim ? s : 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) cur[i] = pg[i];
-    }
-    __syncthreads();
-  }
-
-  // ---- intra stages: dC^T[n, tau] += sum_sig B[sig, n] dCB[tau, sig], sig tiles S <= T ----
-  for (int S = 0; S <= T; ++S) {
-    const int idx = nS + S;
-    const bool has_next = S < T;
-    if (has_next) load_intra(S + 1);
-    const bf16* sl = slots + (idx & 1) * SM::slot_elems;
-    v8bf fh[2], fl[2];
-    split8(cur[0], cur[1], fh[0], fl[0]);
-    split8(cur[2], cur[3], fh[1], fl[1]);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const v8bf a = lds_tr8(sl + (32 * ks + 8 * lg) * LDC + 16 * nt, LDC, lane);
-        dCT[nt] = mfma_bf16(a, fh[ks], dCT[nt]);
-        dCT[nt] = mfma_bf16(a, fl[ks], dCT[nt]);
+      for (int ks = 0; ks < 2; ++ks) {
+        dyf[ks][0] = dyn[ks][0];
+        dyf[ks][1] = dyn[ks][1];
       }
-    if (has_next) {
-      pc.commit(slots + ((idx + 1) & 1) * SM::slot_elems, LDC, tid);
+    } else {
+      // dC^T[n, tau] += sum_sig B[sig, n] dCB[tau, sig]
+      const bf16* Bt = Sg;
+      const bf16* Dh = Sg + 64 * N;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) cur[i] = pg[i];
+      for (int ks = 0; ks < 2; ++ks) {
+        const v8bf bh = tr_frag<8, swz_k128>(Dh, 32 * ks + 8 * lg, 16 * w, lane);
+        const v8bf bl = tr_frag<8, swz_k128>(Dh + kPlaneT, 32 * ks + 8 * lg, 16 * w, lane);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const v8bf a = tr_frag<RC, swz_k256>(Bt, 32 * ks + 8 * lg, 16 * nt, lane);
+          dCT[nt] = mfma_bf16(a, bh, dCT[nt]);
+          dCT[nt] = mfma_bf16(a, bl, dCT[nt]);
+        }
+      }
     }
+    if (j + 1 < HPG) commit_h(j + 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
   if (tau < qlim) {
-    bf16* dcrow = dCc + static_cast<unsigned>(tau * act_rs + 4 * lg);
+    bf16* row = dCc + static_cast<unsigned>(tau * act_rs + 4 * lg);
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      *reinterpret_cast<uint2*>(dcrow + 16 * nt) = pack4_bf16(tv ? dCT[nt] : v4f{0.f, 0.f, 0.f, 0.f});
+    for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<uint2*>(row + 16 * nt) = pack4_bf16(dCT[nt]);
   }
 }
 
+// The host pass leaves the stubs of ssd_bwd_src_kernel undefined when it only
+// meets them through a launch (its device lambdas are not substituted there);
+// explicit instantiation makes it emit them.
+#define SA_SRC_INST(HPG)                                                                         \
+  template __global__ void ssd_bwd_src_kernel<4, HPG>(                                           \
+      const bf16*, const bf16*, const bf16*, const bf16*, const float*, const float*,            \
+      const bf16*, const int64_t*, bf16*, bf16*, bf16*, float*, float*, float*, float*, SsdDims, \
+      int);
+SA_SRC_INST(1)
+SA_SRC_INST(2)
+SA_SRC_INST(3)
+SA_SRC_INST(4)
+#undef SA_SRC_INST
+
 template <typename K>
-int allow_smem(K kernel, size_t bytes, const char* who) {
+int raise_smem(K kernel, size_t bytes, const char* who) {
   if (bytes <= 64 * 1024) return 0;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     static_cast<int>(bytes));
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           static_cast<int>(bytes));
   SA_CHECK_ARG(e == hipSuccess, "%s: %zu B of LDS refused: %s", who, bytes, hipGetErrorString(e));
   return 0;
 }
 
-template <int NK, int HPG>
-int launch_fused(const bf16* u, const bf16* Bm, const bf16* Cm, const float* dy, const float* dt,
-                 const float* dc, const float* states, const float* dS, const int64_t* length,
-                 bf16* du, bf16* dB, bf16* dC, float* dCB, float* ddt_part, float* xB_part,
-                 float* xC_part, float* qpart, float* rpart, const SsdDims& d, int mono,
-                 hipStream_t s) {
+template <int HPG>
+int launch_fused_hpg(const void* u, const void* B, const void* C, const bf16* dyp,
+                     const float* dt, const float* dc, const float* states, const bf16* dSp,
+                     const int64_t* length, void* du, void* dB, void* dC, bf16* dcbp,
+                     float* ddt_part, float* xB_part, float* xC_part, float* qpart, float* rpart,
+                     const SsdDims& d, bool dt_nonneg, hipStream_t s) {
+  constexpr int NK = 4;
   const long blocks = static_cast<long>(d.b) * d.nc * d.G * (d.Lc / 64);
   {
-    const size_t smem = ColSmem<NK, HPG>::bytes;
-    if (int rc = allow_smem(ssd_bwd_col_kernel<NK, HPG>, smem, "ssd_bwd_col")) return rc;
-    ProfScope prof_("ssd_bwd_col", s);
-    hipLaunchKernelGGL((ssd_bwd_col_kernel<NK, HPG>), dim3(blocks), dim3(512), smem, s, u, Bm, Cm,
-                       dy, dt, dc, dS, length, du, dB, dCB, ddt_part, xB_part, qpart, rpart, d,
-                       mono);
-    SA_CHECK_LAUNCH("ssd_bwd_col");
+    const size_t smem = SrcSmem<NK, HPG>::bytes;
+    if (const int rc = raise_smem(ssd_bwd_src_kernel<NK, HPG>, smem, "ssd_bwd_src")) return rc;
+    ProfScope prof_("ssd_bwd_src", s);
+    hipLaunchKernelGGL((ssd_bwd_src_kernel<NK, HPG>), dim3(blocks), dim3(512), smem, s,
+                       static_cast<const bf16*>(u), static_cast<const bf16*>(B),
+                       static_cast<const bf16*>(C), dyp, dt, dc, dSp, length,
+                       static_cast<bf16*>(du), static_cast<bf16*>(dB), dcbp, ddt_part, xB_part,
+                       qpart, rpart, d, dt_nonneg ? 1 : 0);
+    SA_CHECK_LAUNCH("ssd_bwd_src");
   }
   {
-    const size_t smem = RowSmem<NK>::bytes;
-    if (int rc = allow_smem(ssd_bwd_row_kernel<NK, HPG>, smem, "ssd_bwd_row")) return rc;
-    ProfScope prof_("ssd_bwd_row", s);
-    hipLaunchKernelGGL((ssd_bwd_row_kernel<NK, HPG>), dim3(blocks), dim3(256), smem, s, Bm, Cm,
-                       dy, dc, states, dCB, length, dC, xC_part, d);
-    SA_CHECK_LAUNCH("ssd_bwd_row");
+    const size_t smem = TgtSmem<NK>::bytes;
+    if (const int rc = raise_smem(ssd_bwd_tgt_kernel<NK, HPG>, smem, "ssd_bwd_tgt")) return rc;
+    ProfScope prof_("ssd_bwd_tgt", s);
+    hipLaunchKernelGGL((ssd_bwd_tgt_kernel<NK, HPG>), dim3(blocks), dim3(256), smem, s,
+                       static_cast<const bf16*>(B), static_cast<const bf16*>(C), dyp, dc, states,
+                       dcbp, length, static_cast<bf16*>(dC), xC_part, d);
+    SA_CHECK_LAUNCH("ssd_bwd_tgt");
   }
   return 0;
 }
 
-template <int NK>
-int launch_fused_nk(int hpg, const bf16* u, const bf16* Bm, const bf16* Cm, const float* dy,
-                    const float* dt, const float* dc, const float* states, const float* dS,
-                    const int64_t* length, bf16* du, bf16* dB, bf16* dC, float* dCB,
-                    float* ddt_part, float* xB_part, float* xC_part, float* qpart, float* rpart,
-                    const SsdDims& d, int mono, hipStream_t s) {
-#define SA_FUSED_CASE(H)                                                                       \
-  case H:                                                                                      \
-    return launch_fused<NK, H>(u, Bm, Cm, dy, dt, dc, states, dS, length, du, dB, dC, dCB,     \
-                               ddt_part, xB_part, xC_part, qpart, rpart, d, mono, s);
-  switch (hpg) {
-    SA_FUSED_CASE(1)
-    SA_FUSED_CASE(2)
-    SA_FUSED_CASE(3)
-    SA_FUSED_CASE(4)
-  }
-#undef SA_FUSED_CASE
-  SA_CHECK_ARG(false, "ssd_bwd fused path: %d heads per group unsupported", hpg);
-  return 1;
-}
-
-}  // namespace
-
 bool ssd_bwd_fused_shape_ok(const SsdDims& d) {
   const int hpg = d.H / d.G;
-  return d.P == 64 && (d.N == 64 || d.N == 128) && d.Lc % 64 == 0 && hpg >= 1 && hpg <= 4;
+  return d.P == 64 && d.N == 128 && d.Lc % 64 == 0 && hpg >= 1 && hpg <= 4;
 }
 
 bool ssd_bwd_fused_ok(const SsdDims& d, const void* u, const void* B, const void* C,
@@ -828,23 +1006,17 @@ bool ssd_bwd_fused_ok(const SsdDims& d, const void* u, const void* B, const void
          aligned16(dy);
 }
 
-int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const float* dy,
-                         const float* dt, const float* dc, const float* states, const float* dS,
-                         const int64_t* length, void* du, void* dB, void* dC, float* dCB,
+int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const bf16* dyp,
+                         const float* dt, const float* dc, const float* states, const bf16* dSp,
+                         const int64_t* length, void* du, void* dB, void* dC, bf16* dcbp,
                          float* ddt_part, float* xB_part, float* xC_part, float* qpart,
                          float* rpart, const SsdDims& d, bool dt_nonneg, hipStream_t s) {
-  const int hpg = d.H / d.G;
-  const int mono = dt_nonneg ? 1 : 0;
-  const bf16* u_ = static_cast<const bf16*>(u);
-  const bf16* B_ = static_cast<const bf16*>(B);
-  const bf16* C_ = static_cast<const bf16*>(C);
-  if (d.N == 64)
-    return launch_fused_nk<2>(hpg, u_, B_, C_, dy, dt, dc, states, dS, length,
-                              static_cast<bf16*>(du), static_cast<bf16*>(dB), static_cast<bf16*>(dC),
-                              dCB, ddt_part, xB_part, xC_part, qpart, rpart, d, mono, s);
-  return launch_fused_nk<4>(hpg, u_, B_, C_, dy, dt, dc, states, dS, length,
-                            static_cast<bf16*>(du), static_cast<bf16*>(dB), static_cast<bf16*>(dC),
-                            dCB, ddt_part, xB_part, xC_part, qpart, rpart, d, mono, s);
+  switch (d.H / d.G) {
+    case 1: return launch_fused_hpg<1>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, d, dt_nonneg, s);
+    case 2: return launch_fused_hpg<2>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, d, dt_nonneg, s);
+    case 3: return launch_fused_hpg<3>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, d, dt_nonneg, s);
+    default: return launch_fused_hpg<4>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, d, dt_nonneg, s);
+  }
 }
 
 }  // namespace sa

@@ -45,16 +45,25 @@ template <typename MT, typename TA, typename TB, int MODE>
 int launch_chunk_outer(const void* a, const void* b, const float* dt, const float* dc,
                        const int64_t* length, float* out, const SsdDims& d, hipStream_t s);
 
-// fused bf16 backward (headdim 64): column kernel (du, dB, decay sums, dCB)
-// and row kernel (dC, x_C); defined in ssd_bwd_fused.hip.  dt_nonneg: every dt
-// is >= 0 (delta_min >= 0), so each head's dc is monotone within a chunk
+// fused bf16 backward (headdim 64, state_dim 128): source-strip kernel (du,
+// dB, decay sums, dCB planes) and target-strip kernel (dC, x_C); defined in
+// ssd_bwd_fused.hip.  dyp: dy as bf16 hi + lo planes [b][nc][G][Lc/64][H/G]
+// [2][64][64]; dSp: dS as hi + lo planes [b][nc][H][2][64][N]; dcbp: dCB^T
+// planes [b][nc][G][Lc/64][Lc/64][2][64][64].  dt_nonneg: every dt is >= 0
+// (delta_min >= 0), so each head's dc is monotone within a chunk
 bool ssd_bwd_fused_shape_ok(const SsdDims& d);
 bool ssd_bwd_fused_ok(const SsdDims& d, const void* u, const void* B, const void* C,
                       const void* dy);
-int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const float* dy,
-                         const float* dt, const float* dc, const float* states, const float* dS,
-                         const int64_t* length, void* du, void* dB, void* dC, float* dCB,
+int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const bf16* dyp,
+                         const float* dt, const float* dc, const float* states, const bf16* dSp,
+                         const int64_t* length, void* du, void* dB, void* dC, bf16* dcbp,
                          float* ddt_part, float* xB_part, float* xC_part, float* qpart,
                          float* rpart, const SsdDims& d, bool dt_nonneg, hipStream_t s);
+
+// dH_intra (chunk_outer MODE 1, bf16 dy) that also writes dy as the hi + lo
+// planes of the fused backward
+int launch_dstate_planes(const float* dy, const void* C, const float* dt, const float* dc,
+                         const int64_t* length, float* out, bf16* dyp, const SsdDims& d,
+                         hipStream_t s);
 
 }  // namespace sa

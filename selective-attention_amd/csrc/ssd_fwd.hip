@@ -161,7 +161,10 @@ __global__ __launch_bounds__(256) void chunk_outer_kernel(
 // ---------------------------------------------------------------------------
 // chunk outer products, bf16 fast path (P and N multiples of 64):
 //   MODE 0: states[p][n] = sum_t u[t,p] w_t B[t,n],  w_t = e^{min(dc_last - dc_t, 0)} dt_t
-//   MODE 1: dH[p][n]     = sum_t dy[t,p] e^{dc_t} C[t,n]   (t < length)
+//   MODE 1: dH[p][n]     = sum_t dy[t,p] e^{dc_t} C[t,n]   (t < length); with
+//           dyp set (P = 64) it also writes dy (zero at t >= length) as the
+//           hi + lo bf16 planes the fused backward reads, [b][nc][G][Lc/64]
+//           [H/G][2][64][64]
 // One block per (b, chunk, head, 64-wide p tile), 4 waves; wave w computes
 // D^T[n][p] for its N/4 columns n and the 64 p.  Both operands come from
 // row-major t tiles in LDS through transpose reads: A = X^T (X = B or C) and
@@ -174,7 +177,7 @@ template <int NK, int MODE>
 __global__ __launch_bounds__(256, 2) void chunk_outer_bf16_kernel(
     const void* __restrict__ a_src, const bf16* __restrict__ x_src, const float* __restrict__ dt,
     const float* __restrict__ dc, const int64_t* __restrict__ length, float* __restrict__ out,
-    SsdDims d) {
+    bf16* __restrict__ dyp, SsdDims d) {
   constexpr int N = 32 * NK, LDX = N + 8, LDA = 64 + 8;
   constexpr int NPL = 2;                   // hi + lo planes of the scaled operand
   constexpr int NTW = N / 64;              // 16-wide n tiles per wave
@@ -217,12 +220,14 @@ __global__ __launch_bounds__(256, 2) void chunk_outer_bf16_kernel(
       return t < klim ? sc : 0.f;
     };
     // prefetch registers
+    int slot_tile = 0;   // tile index held by the prefetch registers (dy planes)
     uint4 pa0[MODE == 0 ? 2 : 1];
     float4 pa1[MODE == 1 ? 4 : 1];
     float psc[2];
     BfTile<NK, 256> px;
     auto load_tile = [&](int tt) __attribute__((always_inline)) {
       const int t0 = 64 * tt, kv = min(64, klim - t0);
+      slot_tile = tt;
       if constexpr (MODE == 0) {
         const bf16* ac = static_cast<const bf16*>(a_src) + tok0 * a_rs + h * d.P + p0;
 #pragma unroll
@@ -265,6 +270,32 @@ __global__ __launch_bounds__(256, 2) void chunk_outer_bf16_kernel(
         }
       } else {
         const int row = tid >> 2, c0 = 16 * (tid & 3);
+        if (dyp) {
+          // the unscaled tile rows as planes (zero rows past the length)
+          const int tt = slot_tile;
+          const bool in = 64 * tt + row < klim;
+          uint32_t uh[8], ul[8];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float v[4] = {in ? pa1[i].x : 0.f, in ? pa1[i].y : 0.f, in ? pa1[i].z : 0.f,
+                                in ? pa1[i].w : 0.f};
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+              const uint32_t hh = pack_bf16x2(v[2 * jj], v[2 * jj + 1]);
+              uh[2 * i + jj] = hh;
+              ul[2 * i + jj] = pack_bf16x2(v[2 * jj] - bf16lo_to_f32(hh), v[2 * jj + 1] - bf16hi_to_f32(hh));
+            }
+          }
+          const int hpg = d.H / d.G;
+          const long tileo = ((((static_cast<long>(b) * d.nc + c) * d.G + g) * (d.Lc / 64) + tt) * hpg +
+                              (h - g * hpg)) * (2L * 64 * 64);
+          uint4* ph = reinterpret_cast<uint4*>(dyp + tileo + row * 64 + c0);
+          uint4* pl = reinterpret_cast<uint4*>(dyp + tileo + 64 * 64 + row * 64 + c0);
+          ph[0] = uint4{uh[0], uh[1], uh[2], uh[3]};
+          ph[1] = uint4{uh[4], uh[5], uh[6], uh[7]};
+          pl[0] = uint4{ul[0], ul[1], ul[2], ul[3]};
+          pl[1] = uint4{ul[4], ul[5], ul[6], ul[7]};
+        }
         uint32_t hi[8], lo[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -811,7 +842,8 @@ int launch_chunk_cumsum(const void* delta_raw, const float* A, const float* bias
 
 template <int NK, int MODE>
 int launch_chunk_outer_bf16_nk(const void* a, const void* x, const float* dt, const float* dc,
-                               const int64_t* length, float* out, const SsdDims& d, hipStream_t s) {
+                               const int64_t* length, float* out, const SsdDims& d, hipStream_t s,
+                               bf16* dyp = nullptr) {
   const long blocks = static_cast<long>(d.P / 64) * d.H * d.nc * d.b;
   const size_t smem = 2 * sizeof(bf16) * (2 * 64 * 72 + 64 * (32 * NK + 8));
   if (smem > 64 * 1024) {
@@ -821,7 +853,7 @@ int launch_chunk_outer_bf16_nk(const void* a, const void* x, const float* dt, co
   }
   ProfScope prof_(MODE == 0 ? "chunk_state_fwd" : "chunk_dstate_bwd", s);
   hipLaunchKernelGGL((chunk_outer_bf16_kernel<NK, MODE>), dim3(blocks), dim3(256), smem, s, a,
-                     static_cast<const bf16*>(x), dt, dc, length, out, d);
+                     static_cast<const bf16*>(x), dt, dc, length, out, dyp, d);
   SA_CHECK_LAUNCH("chunk_outer_bf16");
   return 0;
 }
@@ -847,6 +879,14 @@ int launch_chunk_outer(const void* a, const void* bsrc, const float* dt, const f
                      d, vec_a, vec_b);
   SA_CHECK_LAUNCH("chunk_outer");
   return 0;
+}
+
+int launch_dstate_planes(const float* dy, const void* C, const float* dt, const float* dc,
+                         const int64_t* length, float* out, bf16* dyp, const SsdDims& d,
+                         hipStream_t s) {
+  SA_CHECK_ARG(d.P == 64 && d.N == 128 && d.Lc % 64 == 0 && aligned16(dy) && aligned16(C),
+               "launch_dstate_planes: P 64, N 128, chunk %% 64 and aligned operands required");
+  return launch_chunk_outer_bf16_nk<4, 1>(dy, C, dt, dc, length, out, d, s, dyp);
 }
 
 int launch_state_passing_fwd(float* states, const float* h_init, float* h_last, const float* dc,
