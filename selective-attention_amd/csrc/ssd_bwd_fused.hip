@@ -95,7 +95,7 @@ template <int RC>
 __device__ __forceinline__ void dma_pre(bf16* lds, const bf16* g, const int (&off)[RC / 4], int w) {
 #pragma unroll
   for (int i = 0; i < RC / 4; ++i)
-    __builtin_amdgcn_global_load_lds(g + off[i], lds + (w * (RC / 4) + i) * 512, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(g + static_cast<unsigned>(off[i]), lds + (w * (RC / 4) + i) * 512, 16, 0, 0);
 }
 
 // the same for a tile copied by 8 waves (RC / 8 instructions each)
@@ -103,7 +103,7 @@ template <int RC>
 __device__ __forceinline__ void dma_pre_w8(bf16* lds, const bf16* g, const int (&off)[RC / 8], int w) {
 #pragma unroll
   for (int i = 0; i < RC / 8; ++i)
-    __builtin_amdgcn_global_load_lds(g + off[i], lds + (w * (RC / 8) + i) * 512, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(g + static_cast<unsigned>(off[i]), lds + (w * (RC / 8) + i) * 512, 16, 0, 0);
 }
 // 8-wave copy of a partial tile: rows past rows_valid repeat row rows_valid - 1
 template <int RC, int (*F)(int)>
@@ -231,30 +231,31 @@ __device__ __forceinline__ int opaque(int v) {
 }
 
 // ---------------------------------------------------------------------------
-// source-strip kernel.  One 512-thread block per (b, c, group, source strip S)
-// and one block per CU.  Wave w = 4 s + q: head slot s (heads s HS .. s HS +
-// HS - 1, HS = ceil(HPG / 2)), source columns sigma = 64 S + 16 q + lane % 16.
-// The two waves of a column strip share the C.B^T tile (each computes it),
-// exchange their heads' dCB through LDS once per target strip, and split dB:
-// slot s owns the dB^T rows n in [N/2 s, N/2 s + N/2).
+// source-strip kernel.  One 256-thread block per (b, c, group, source strip S),
+// two blocks per CU.  Wave w owns the source columns sigma = 64 S + 16 w +
+// lane % 16.  The group's heads run in passes (one launch each, in order) of
+// HS = min(HPG, 2) heads: du, x_B, ddt, q, r of those heads.  dB and the dCB
+// planes need every head of the group: a pass that is not the last parks its
+// fp32 share of dCB in the 64 bytes per lane that the last pass overwrites
+// with the hi / lo planes; the last pass adds the parked shares back and
+// computes all of dB (the state part of the earlier heads from their dS
+// tiles again).
 // ---------------------------------------------------------------------------
 template <int NK, int HPG>
 struct SrcSmem {
   static constexpr int N = 32 * NK;
-  static constexpr int HS = (HPG + 1) / 2;
-  static constexpr int kStage = 2 * 2 * kPlaneT;   // bf16: two heads' dy tiles (hi, lo) or dS n-halves
+  static constexpr int kStage = 2 * kPlaneT;       // bf16: one head's dy tile or dS n half (hi, lo)
   static constexpr int kC = 64 * N;                // bf16: one C tile
   static constexpr size_t stage_off = 0;
   static constexpr size_t c_off = stage_off + 2 * kStage * 2;
   static constexpr size_t dc_off = c_off + 2 * kC * 2;         // float [2][HPG][64] dc (log2)
   static constexpr size_t at_off = dc_off + 2 * HPG * 64 * 4;  // float [2][HPG][64] e^{dc - dc_T0}
-  static constexpr size_t r_off = at_off + 2 * HPG * 64 * 4;   // float [2 parity][2 slots][4 q][64]
-  static constexpr size_t x_off = r_off + 2 * 2 * 4 * 64 * 4;  // float4 [8 waves][4 kt][64] dCB exchange
-  static constexpr size_t bytes = x_off + 8 * 4 * 64 * 16;
+  static constexpr size_t r_off = at_off + 2 * HPG * 64 * 4;   // float [2 parity][4 waves][64]
+  static constexpr size_t bytes = r_off + 2 * 4 * 64 * 4;
 };
 
-template <int NK, int HPG>
-__global__ __launch_bounds__(512, 1) void ssd_bwd_src_kernel(
+template <int NK, int HPG, int PASS>
+__global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     const bf16* __restrict__ u, const bf16* __restrict__ Bm, const bf16* __restrict__ Cm,
     const bf16* __restrict__ dyp, const float* __restrict__ dt, const float* __restrict__ dc,
     const bf16* __restrict__ dSp, const int64_t* __restrict__ length, bf16* __restrict__ du,
@@ -263,17 +264,22 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_src_kernel(
     int mono) {
   using SM = SrcSmem<NK, HPG>;
   constexpr int N = SM::N;
-  constexpr int HS = SM::HS;
+  constexpr int HS = HPG < 2 ? HPG : 2;          // heads per pass
+  constexpr int NPASS = (HPG + HS - 1) / HS;
+  constexpr int pass = PASS;
+  constexpr bool last = PASS == NPASS - 1;
+  constexpr int KB = PASS * HS;                  // first head of this pass
+  constexpr int KE = KB + HS < HPG ? KB + HS : HPG;   // one past its last
+  static_assert(PASS < NPASS, "ssd_bwd_src: pass");
   constexpr int NH = N / 64;     // 64-wide n halves of a dS tile
-  constexpr int NTS = N / 32;    // 16-row n tiles of dB^T per slot
+  constexpr int NT = N / 16;     // 16-row n tiles of dB^T
   static_assert(NH == 2, "ssd_bwd_src: state_dim 128");
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* stg = reinterpret_cast<bf16*>(smem_raw + SM::stage_off);   // [2][2 slots][hi, lo][64][64]
+  bf16* stg = reinterpret_cast<bf16*>(smem_raw + SM::stage_off);   // [2][hi, lo][64][64]
   bf16* Cs = reinterpret_cast<bf16*>(smem_raw + SM::c_off);        // [2][64][N]
   float* dcs = reinterpret_cast<float*>(smem_raw + SM::dc_off);
   float* ats = reinterpret_cast<float*>(smem_raw + SM::at_off);
   float* rx = reinterpret_cast<float*>(smem_raw + SM::r_off);
-  float4* xch = reinterpret_cast<float4*>(smem_raw + SM::x_off);
 
   const int stiles = d.Lc / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -291,8 +297,7 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_src_kernel(
   const int u_rs = d.H * 64, act_rs = d.G * N;
   const int tid = threadIdx.x, lane = tid & 63, lg = lane >> 4, li = lane & 15;
   const int w = wave_index();
-  const int slot = w >> 2, q = w & 3;
-  const int sl = 16 * q + li;        // this lane's source column within the strip
+  const int sl = 16 * w + li;        // this lane's source column within the strip
   const int sig = s0 + sl;           // its chunk position
   const int h0 = g * HPG;
   const long bhc0 = (static_cast<long>(b) * d.H + h0) * d.nc + c;   // head k: + k nc
@@ -312,23 +317,25 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_src_kernel(
   const int rstride = d.nc * stiles * d.Lc;
 
   if (s0 >= lim) {   // the strip is past the length: zero outputs and partials
-    for (int e = tid; e < 64 * HPG * 8; e += 512) {
-      const int row = e / (HPG * 8), col8 = e % (HPG * 8);
+    for (int e = tid; e < 64 * (KE - KB) * 8; e += 256) {
+      const int row = e / ((KE - KB) * 8), col8 = e % ((KE - KB) * 8);
       if (s0 + row < qlim)
-        *reinterpret_cast<uint4*>(duc + static_cast<unsigned>((s0 + row) * u_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<uint4*>(duc + static_cast<unsigned>((s0 + row) * u_rs + KB * 64 + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
     }
-    for (int e = tid; e < 64 * (N / 8); e += 512) {
-      const int row = e / (N / 8), col8 = e % (N / 8);
-      if (s0 + row < qlim)
-        *reinterpret_cast<uint4*>(dBc + static_cast<unsigned>((s0 + row) * act_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
+    if (last) {
+      for (int e = tid; e < 64 * (N / 8); e += 256) {
+        const int row = e / (N / 8), col8 = e % (N / 8);
+        if (s0 + row < qlim)
+          *reinterpret_cast<uint4*>(dBc + static_cast<unsigned>((s0 + row) * act_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
+      }
     }
-    for (int k = 0; k < HPG; ++k) {
+    for (int k = KB; k < KE; ++k) {
       if (tid < 64) {
         ddtc[k * hstride + s0 + tid] = 0.f;
         xBc[k * hstride + s0 + tid] = 0.f;
         qc[k * hstride + s0 + tid] = 0.f;
       }
-      for (int t = s0 + tid; t < d.Lc; t += 512) rc[k * rstride + t] = 0.f;
+      for (int t = s0 + tid; t < d.Lc; t += 256) rc[k * rstride + t] = 0.f;
     }
     return;
   }
@@ -336,58 +343,49 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_src_kernel(
   const bool sv = sig < lim;
   const int scl = min(sig, lim - 1);       // clamped source row (a valid address)
   const int ntile = (lim + 63) / 64 - S;   // target strips T = S .. S + ntile - 1
-  const int nstate = HS * NH;
-  const int nstage = nstate + HS * ntile;
 
-  // per head of the group at this lane's column: dc (log2), dt (0 past the
-  // length), the state weight w = e^{min(dc_last - dc, 0)} dt
-  float dck[HPG], dtk[HPG], wsk[HPG];
-#pragma unroll
-  for (int k = 0; k < HPG; ++k) {
-    dck[k] = dcc[k * hstride + scl] * kLog2e;
-    dtk[k] = sv ? dtc[k * hstride + scl] : 0.f;
-    wsk[k] = fast_exp2(fminf(dcc[k * hstride + d.Lc - 1] * kLog2e - dck[k], 0.f)) * dtk[k];
-  }
-
-  // stage j: j < nstate: dS n half (j % NH) of heads {h, HS + h}, h = j / NH;
-  // then per target strip T = S + Ti the dy tiles of heads {h, HS + h},
-  // h = 0..HS-1 (C_T and the dc tables come with h == 0)
+  // Stages of pass p: first the state stages, dS n half (j % NH) of head
+  // kb + j / NH, kb = 0 in the last pass (every head up to this pass' own)
+  // and p HS before; then per target strip T = S + Ti the dy tile of head
+  // p HS + h, h = 0..HS-1 (C_T and the dc tables come with h == 0).  jj
+  // counts the stages of all passes and selects the LDS buffer.
+  auto n_state = [&](int p) { return (p == NPASS - 1 ? (p + 1) * HS : HS) * NH; };
+  auto n_stage = [&](int p) { return n_state(p) + HS * ntile; };
   const bf16* dyg = dyp + (bcg * stiles) * (HPG * 2L * kPlaneT);   // + (T HPG + k) 2 kPlaneT
   const bf16* dSg = dSp + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (2L * 64 * N);
-  // DMA lane offsets: instruction i of wave w covers tile chunk rows of one
-  // of the stage's two head tiles (waves 0-3: head slot 0, waves 4-7: slot 1)
-  int o_gs[2], o_gy[2], o_gc[NK / 2];
+  int o_gs[2], o_gy[2], o_gc[NK];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    o_gs[i] = dma_off<8, swz_s128>(i, q, lane, N);
-    o_gy[i] = dma_off<8, swz_k128>(i, q, lane, 64);
+    o_gs[i] = dma_off<8, swz_s128>(i, w, lane, N);
+    o_gy[i] = dma_off<8, swz_k128>(i, w, lane, 64);
   }
 #pragma unroll
-  for (int i = 0; i < NK / 2; ++i) o_gc[i] = dma_off_w8<NK * 4, swz_k256>(i, w, lane, act_rs);
+  for (int i = 0; i < NK; ++i) o_gc[i] = dma_off<NK * 4, swz_k256>(i, w, lane, act_rs);
   float pdc = 0.f, pdc0 = 0.f;   // dc prefetch of the next target strip (head tid / 64, row tid % 64)
-  auto issue = [&](int jj) {
-    bf16* dst = stg + (jj & 1) * SM::kStage + slot * (2 * kPlaneT);
-    if (jj < nstate) {
-      const int h = jj / NH, half = jj % NH, k = slot * HS + h;
+  auto issue = [&](int p, int j, int jj) {
+    if (p >= NPASS) return;
+    bf16* dst = stg + (jj & 1) * SM::kStage;
+    const int nst = n_state(p);
+    if (j < nst) {
+      const int k = (p == NPASS - 1 ? 0 : p * HS) + j / NH, half = j % NH;
       if (k < HPG) {
         const bf16* src = dSg + k * (2L * 64 * N) + 64 * half;
-        dma_pre<8>(dst, src, o_gs, q);
-        dma_pre<8>(dst + kPlaneT, src + 64L * N, o_gs, q);
+        dma_pre<8>(dst, src, o_gs, w);
+        dma_pre<8>(dst + kPlaneT, src + 64L * N, o_gs, w);
       }
     } else {
-      const int qq = jj - nstate, Ti = qq / HS, h = qq % HS, T = S + Ti, k = slot * HS + h;
+      const int qq = j - nst, Ti = qq / HS, h = qq % HS, T = S + Ti, k = p * HS + h;
       if (k < HPG) {
         const bf16* src = dyg + (static_cast<long>(T) * HPG + k) * (2L * kPlaneT);
-        dma_pre<8>(dst, src, o_gy, q);
-        dma_pre<8>(dst + kPlaneT, src + kPlaneT, o_gy, q);
+        dma_pre<8>(dst, src, o_gy, w);
+        dma_pre<8>(dst + kPlaneT, src + kPlaneT, o_gy, w);
       }
       if (h == 0) {
         const int t0 = 64 * T;
         bf16* cdst = Cs + (T & 1) * SM::kC;
         const bf16* csrc = Cc + static_cast<long>(t0) * act_rs;
-        // 8 waves x NK / 2 instructions cover the 64 x N tile
-        if (qlim - t0 >= 64) dma_pre_w8<NK * 4>(cdst, csrc, o_gc, w);
-        else dma_part_w8<NK * 4, swz_k256>(cdst, csrc, act_rs, qlim - t0, w, lane);
+        if (qlim - t0 >= 64) dma_pre<NK * 4>(cdst, csrc, o_gc, w);
+        else dma_tile<NK * 4, swz_k256>(cdst, csrc, act_rs, qlim - t0, w, lane);
         if (tid < HPG * 64) {
           const float* dch = dcc + (tid >> 6) * hstride + t0;
           pdc = dch[tid & 63] * kLog2e;
@@ -396,21 +394,27 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_src_kernel(
       }
     }
   };
-  auto commit_dc = [&](int jj) {   // after the compute of stage jj - 1
-    if (jj < nstage && jj >= nstate && (jj - nstate) % HS == 0 && tid < HPG * 64) {
-      const int T = S + (jj - nstate) / HS;
+  // the next stage after stage j of pass p
+  auto issue_next = [&](int p, int j, int jj) {
+    if (j + 1 < n_stage(p)) issue(p, j + 1, jj + 1);
+  };
+  // end of the stage before stage j of pass p: the dc tables of a new target
+  // strip, then every DMA of the next stage complete and visible
+  auto end_stage = [&](int p, int j) {
+    const int nst = n_state(p);
+    if (j < n_stage(p) && j >= nst && (j - nst) % HS == 0 && tid < HPG * 64) {
+      const int T = S + (j - nst) / HS;
       dcs[(T & 1) * HPG * 64 + tid] = pdc;
       ats[(T & 1) * HPG * 64 + tid] = fast_exp2(fminf(pdc - pdc0, 0.f));
     }
+    wait_all_mem();
+    __syncthreads();
   };
-  auto flush_r = [&](int jj) {   // the row sums stage jj left in LDS -> rpart
-    const int qq = jj - nstate, Ti = qq / HS, h = qq % HS;
-    if (tid < 128) {
-      const int sl2 = tid >> 6, t = tid & 63, k = sl2 * HS + h;
-      if (k < HPG) {
-        const float* rr = rx + ((jj & 1) * 2 + sl2) * 256;
-        rc[k * rstride + 64 * (S + Ti) + t] = rr[t] + rr[64 + t] + rr[128 + t] + rr[192 + t];
-      }
+  auto flush_r = [&](int p, int j, int jj) {   // the row sums pair stage j left in LDS -> rpart
+    const int qq = j - n_state(p), Ti = qq / HS, k = p * HS + qq % HS;
+    if (tid < 64 && k < HPG) {
+      const float* rr = rx + (jj & 1) * 256;
+      rc[k * rstride + 64 * (S + Ti) + tid] = rr[tid] + rr[64 + tid] + rr[128 + tid] + rr[192 + tid];
     }
   };
 
@@ -418,328 +422,325 @@ __global__ __launch_bounds__(512, 1) void ssd_bwd_src_kernel(
   // swizzle of every row this lane reads depends on lane bits only, so each
   // read is a precomputed offset plus a compile-time constant)
   const int rl = 8 * (li >> 2) + (li & 3);   // key_of_row(kt, li) = rl + kro(kt)
-  int o_w[2], o_tr[4], o_c[NK], o_ct[NTS];
+  int o_w[2], o_tr[4], o_c[NK];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) o_w[ks] = toff<8, swz_k128>(rl, 32 * ks + 8 * lg);
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt) o_tr[pt] = tr_first<8, swz_k128>(8 * lg, 16 * pt, lane);
 #pragma unroll
   for (int ks = 0; ks < NK; ++ks) o_c[ks] = toff<NK * 4, swz_k256>(rl, 32 * ks + 8 * lg);
-#pragma unroll
-  for (int nt = 0; nt < NTS; ++nt)
-    o_ct[nt] = tr_first<NK * 4, swz_k256>(8 * lg, 16 * (NTS * slot + nt), lane);
 
-  v4f duT[HS][4];   // du^T of this slot's heads: rows p = 16 pt + 4 lg + r, column sig
-  v4f dBT[NTS];     // dB^T rows n = 16 (NTS slot + nt) + 4 lg + r, column sig
-  float qacc[HS];
-#pragma unroll
-  for (int h = 0; h < HS; ++h) {
-    qacc[h] = 0.f;
-#pragma unroll
-    for (int pt = 0; pt < 4; ++pt) duT[h][pt] = v4f{0.f, 0.f, 0.f, 0.f};
-  }
-#pragma unroll
-  for (int nt = 0; nt < NTS; ++nt) dBT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+  // this lane's 64 bytes of the dCB planes of target strip Tp: 16 bytes at
+  // (hi, lo) x (rows 32 ks + 8 lg .. + 7) of column sl
+  auto dcb_at = [&](int Tp, int kt) -> bf16* {
+    return dcbp + ((bcg * stiles + S) * stiles + Tp) * (2L * kPlaneT) + sl * 64 + 8 * lg +
+           (kt & 1) * kPlaneT + 32 * (kt >> 1);
+  };
 
-  issue(0);
-  __builtin_amdgcn_s_waitcnt(0);
+  issue(pass, 0, 0);
+  wait_all_mem();
   __syncthreads();
-  auto end_stage = [&](int jj) {
-    commit_dc(jj);
-    wait_all_mem();
-    __syncthreads();
-  };
 
-  // ---- state stages: du^T += dS.B^T (n half), dB^T += w dS^T.u^T ----
+  int jj = 0;   // stage counter
+  v4f dBT[NT];  // dB^T rows n = 16 nt + 4 lg + r, column sig (last pass)
   {
-    int o_sd[2], o_st[4][2];
+    const int nst = n_state(pass);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) o_sd[ks] = toff<8, swz_s128>(li, 32 * ks + 8 * lg);
-#pragma unroll
-    for (int nt4 = 0; nt4 < 4; ++nt4) {
-      o_st[nt4][0] = tr_first<8, swz_s128>(8 * lg, 16 * nt4, lane);
-      o_st[nt4][1] = tr_first<8, swz_s128>(8 * lg + 4, 16 * nt4, lane);
-    }
+    for (int nt = 0; nt < NT; ++nt) dBT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+    v4f duT[HS][4];   // du^T of this pass' heads: rows p = 16 pt + 4 lg + r, column sig
+    float qacc[HS], dtk[HS], dck[HS];
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
-      const int k = slot * HS + h;   // this wave's head (valid when k < HPG)
-      const bool kv = k < HPG;
+      const int k = min(pass * HS + h, HPG - 1);
+      dck[h] = dcc[k * hstride + scl] * kLog2e;
+      dtk[h] = sv ? dtc[k * hstride + scl] : 0.f;
+      qacc[h] = 0.f;
 #pragma unroll
-      for (int half = 0; half < NH; ++half) {
-        const int j = h * NH + half;
-        if (j + 1 < nstage) issue(j + 1);
-        const bf16* Y = stg + (j & 1) * SM::kStage;
-        if (kv) {
-          const bf16* Yh = Y + slot * (2 * kPlaneT);
-          const bf16* Yl = Yh + kPlaneT;
-          v8bf Bf[2];
-          const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 64 * half + 8 * lg);
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int pt = 0; pt < 4; ++pt) {
-              const int off = o_sd[ks] + 16 * pt * 64;
-              duT[h][pt] = mfma_bf16(load_v8bf(Yh + off), Bf[ks], duT[h][pt]);
-              duT[h][pt] = mfma_bf16(load_v8bf(Yl + off), Bf[ks], duT[h][pt]);
-            }
-        }
-        if (half == slot) {
-          // this slot's n half of dB^T, from both heads of the stage
-#pragma unroll
-          for (int s2 = 0; s2 < 2; ++s2) {
-            const int k2 = s2 * HS + h;
-            if (k2 >= HPG) continue;
-            const bf16* Yh = Y + s2 * (2 * kPlaneT);
-            const bf16* Yl = Yh + kPlaneT;
-            v8bf uf[2];
-            const bf16* urow = uc + k2 * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
-            float wk = 0.f;
-#pragma unroll
-            for (int kk = 0; kk < HPG; ++kk)
-              if (kk == k2) wk = wsk[kk];
-#pragma unroll
-            for (int nt = 0; nt < NTS; ++nt) {
-              v4f tmp = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int ks = 0; ks < 2; ++ks) {
-                const int a0 = o_st[nt][0] + 32 * ks * 64, a1 = o_st[nt][1] + 32 * ks * 64;
-                tmp = mfma_bf16(tr_at(Yh, a0, a1), uf[ks], tmp);
-                tmp = mfma_bf16(tr_at(Yl, a0, a1), uf[ks], tmp);
-              }
-              dBT[nt] += tmp * wk;
-            }
-          }
-        }
-        if (half == NH - 1 && kv) {
-          // head k's state part is complete: scale by e^{dc_last - dc_sig}; x_B
-          float dk = 0.f, dtv = 0.f;
-#pragma unroll
-          for (int kk = 0; kk < HPG; ++kk)
-            if (kk == k) {
-              dk = dck[kk];
-              dtv = dtk[kk];
-            }
-          const float ek = fast_exp2(fminf(dcc[k * hstride + d.Lc - 1] * kLog2e - dk, 0.f));
-          const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
-          float sx = 0.f;
-#pragma unroll
-          for (int pt = 0; pt < 4; ++pt) {
-            duT[h][pt] *= ek;
-            sx += dot4_bf16(duT[h][pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
-          }
-          sx = group_sum(sv ? sx : 0.f) * dtv;
-          if (lg == 0) xBc[k * hstride + sig] = sx;
-        }
-        end_stage(j + 1);
-      }
+      for (int pt = 0; pt < 4; ++pt) duT[h][pt] = v4f{0.f, 0.f, 0.f, 0.f};
     }
-  }
 
-  // dB^T[n, sig] += sum_t C[t, n] dCB[t, sig] of target strip Tp, after the
-  // exchange that completes dCB; this slot also stores half of dCB's planes
-  auto finish_pair = [&](int Tp, v4f (&dCBa)[4]) {
-    const float4* xi = xch + ((1 - slot) * 4 + q) * 4 * 64;
+    // ---- state stages: dB^T += w dS^T.u^T (last pass), du^T += dS.B^T ----
+    {
+      int o_sd[2], o_st[4][2];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const float4 o = xi[kt * 64 + lane];
-      dCBa[kt] += v4f{o.x, o.y, o.z, o.w};
-    }
-    const bf16* Cb = Cs + (Tp & 1) * SM::kC;
-    bf16* dst = dcbp + ((bcg * stiles + S) * stiles + Tp) * (2L * kPlaneT) + sl * 64 + 8 * lg;
+      for (int ks = 0; ks < 2; ++ks) o_sd[ks] = toff<8, swz_s128>(li, 32 * ks + 8 * lg);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      v8bf dh, dl;
-      split_p(dCBa[2 * ks], dCBa[2 * ks + 1], dh, dl);
-      if (ks == slot) {
-        *reinterpret_cast<v8bf*>(dst + 32 * ks) = dh;
-        *reinterpret_cast<v8bf*>(dst + kPlaneT + 32 * ks) = dl;
+      for (int nt4 = 0; nt4 < 4; ++nt4) {
+        o_st[nt4][0] = tr_first<8, swz_s128>(8 * lg, 16 * nt4, lane);
+        o_st[nt4][1] = tr_first<8, swz_s128>(8 * lg + 4, 16 * nt4, lane);
       }
-#pragma unroll
-      for (int nt = 0; nt < NTS; ++nt) {
-        const int a0 = o_ct[nt] + 32 * ks * N;
-        const v8bf a = tr_at(Cb, a0, a0 + 4 * N);
-        dBT[nt] = mfma_bf16(a, dh, dBT[nt]);
-        dBT[nt] = mfma_bf16(a, dl, dBT[nt]);
-      }
-    }
-  };
-
-  // ---- pair stages: target strip T = S + Ti, head k = slot HS + h ----
-  v4f dCBa[4];
-  for (int Ti = 0; Ti < ntile; ++Ti) {
-    const int T = S + Ti, t0 = 64 * T;
-    const bf16* Cb = Cs + (T & 1) * SM::kC;
-    const bool diag = Ti == 0;
-    const bool fact = !diag && mono;
-    v4f CB[4];
-#pragma unroll
-    for (int h = 0; h < HS; ++h) {
-      const int j = nstate + Ti * HS + h;
-      const int k = slot * HS + h;
-      const bool kv = k < HPG;
-      // with one head per slot, stage j + 1 brings the C tile of strip T + 1
-      // into the buffer finish_pair(T - 1) reads, and this stage rewrites the
-      // exchange finish_pair reads: every wave finishes it first
-      if (HS == 1 && Ti > 0) {
-        finish_pair(T - 1, dCBa);
-        __syncthreads();
-      }
-      if (j + 1 < nstage) issue(j + 1);
-      if (j > nstate) flush_r(j - 1);
-      if (HS > 1 && h == 0 && Ti > 0) finish_pair(T - 1, dCBa);
-      const bf16* Yh = stg + (j & 1) * SM::kStage + slot * (2 * kPlaneT);
-      const bf16* Yl = Yh + kPlaneT;
-      if (h == 0) {
-        v8bf Bf[NK];
-        const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 8 * lg);
-#pragma unroll
-        for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          CB[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-          dCBa[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks < NK; ++ks)
-            CB[kt] = mfma_bf16(load_v8bf(Cb + o_c[ks] + kro(kt) * N), Bf[ks], CB[kt]);
-        }
-      }
-      if (kv) {
-        const float* dcT = dcs + (T & 1) * HPG * 64 + 64 * k;
-        const float* atT = ats + (T & 1) * HPG * 64 + 64 * k;
+      // dB^T rows of the n half in stage buffer Y from head k's dS
+      auto state_dB = [&](const bf16* Yh, int k, int half) {
+        const int kc = k * hstride + scl;
+        const float dtv = sv ? dtc[kc] : 0.f;
+        const float wk = fast_exp2(fminf((dcc[k * hstride + d.Lc - 1] - dcc[kc]) * kLog2e, 0.f)) * dtv;
+        const bf16* Yl = Yh + kPlaneT;
         v8bf uf[2];
-        {
-          const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
+        const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks) uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
-        }
-        float dk = 0.f, dtv = 0.f;
+        for (int ks = 0; ks < 2; ++ks) uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
 #pragma unroll
-        for (int kk = 0; kk < HPG; ++kk)
-          if (kk == k) {
-            dk = dck[kk];
-            dtv = dtk[kk];
-          }
-        // W[t, sig] = dy[t] . u[sig]
-        v4f W[4];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          W[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int nt4 = 0; nt4 < 4; ++nt4) {
+          v4f tmp = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
-            W[kt] = mfma_bf16(load_v8bf(Yh + o_w[ks] + kro(kt) * 64), uf[ks], W[kt]);
-            W[kt] = mfma_bf16(load_v8bf(Yl + o_w[ks] + kro(kt) * 64), uf[ks], W[kt]);
+            const int a0 = o_st[nt4][0] + 32 * ks * 64, a1 = o_st[nt4][1] + 32 * ks * 64;
+            tmp = mfma_bf16(tr_at(Yh, a0, a1), uf[ks], tmp);
+            tmp = mfma_bf16(tr_at(Yl, a0, a1), uf[ks], tmp);
           }
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)   // constant register index of dBT
+            if (h2 == half) dBT[4 * h2 + nt4] += tmp * wk;
         }
-        // decay and masks: dCB += W', M = W' o CB (q: column sums, r: row sums); W <- L
-        float m[16];
-        float qs = 0.f;
-        if (fact) {
-          // off the diagonal with a monotone dc, e^{min(dc_t - dc_sig, 0)} =
-          // e^{min(dc_t - dc_t0, 0)} e^{min(dc_t0 - dc_sig, 0)}
-          const float bk = fast_exp2(fminf(dcT[0] - dk, 0.f));
-          const float bdt = bk * dtv;
-#pragma unroll
-          for (int kt = 0; kt < 4; ++kt) {
-            const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);
-            const float4 aq = *reinterpret_cast<const float4*>(atT + tb);
-            const float av[4] = {aq.x, aq.y, aq.z, aq.w};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float wv = W[kt][r] * (av[r] * bdt);
-              dCBa[kt][r] += wv;
-              const float mv = wv * CB[kt][r];
-              m[4 * kt + r] = mv;
-              qs += mv;
-              W[kt][r] = CB[kt][r] * (av[r] * bk);
-            }
-          }
-        } else {
-#pragma unroll
-          for (int kt = 0; kt < 4; ++kt) {
-            const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);
-            const float4 dq = *reinterpret_cast<const float4*>(dcT + tb);
-            const float dv[4] = {dq.x, dq.y, dq.z, dq.w};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int t = t0 + tb + r;
-              float dec = fast_exp2(fminf(dv[r] - dk, 0.f));
-              dec = (t >= sig && t < lim) ? dec : 0.f;
-              const float wv = W[kt][r] * dtv * dec;
-              dCBa[kt][r] += wv;
-              const float mv = t > sig ? wv * CB[kt][r] : 0.f;
-              m[4 * kt + r] = mv;
-              qs += mv;
-              W[kt][r] = CB[kt][r] * dec;
-            }
-          }
-        }
-        qacc[h] += qs;
-        rx[((j & 1) * 2 + slot) * 256 + q * 64 + key_of_row(li >> 2, 4 * lg + (li & 3))] =
-            transpose_reduce16(m, li);
-        // du^T[p, sig] += sum_t dy[t, p] L[t, sig]  (L and dy as hi + lo)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          v8bf lh, ll;
-          split_p(W[2 * ks], W[2 * ks + 1], lh, ll);
-#pragma unroll
-          for (int pt = 0; pt < 4; ++pt) {
-            const int a0 = o_tr[pt] + 32 * ks * 64;
-            const v8bf yh = tr_at(Yh, a0, a0 + 4 * 64);
-            const v8bf yl = tr_at(Yl, a0, a0 + 4 * 64);
-            duT[h][pt] = mfma_bf16(yh, lh, duT[h][pt]);
-            duT[h][pt] = mfma_bf16(yl, lh, duT[h][pt]);
-            duT[h][pt] = mfma_bf16(yh, ll, duT[h][pt]);
-          }
+      };
+      // last pass: the dB state part of the heads of the earlier passes
+      if (last) {
+        for (int j = 0; j < pass * HS * NH; ++j, ++jj) {
+          issue_next(pass, j, jj);
+          state_dB(stg + (jj & 1) * SM::kStage, j / NH, j % NH);
+          end_stage(pass, j + 1);
         }
       }
-      if (h == HS - 1) {
-        // this slot's part of dCB for the exchange
-        float4* xo = xch + (slot * 4 + q) * 4 * 64;
+      const int jo = last ? pass * HS * NH : 0;   // first stage of this pass' own heads
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) xo[kt * 64 + lane] = make_float4(dCBa[kt][0], dCBa[kt][1], dCBa[kt][2], dCBa[kt][3]);
+      for (int h = 0; h < HS; ++h) {
+        const int k = pass * HS + h;
+        const bool kv = k < HPG;
+#pragma unroll
+        for (int half = 0; half < NH; ++half, ++jj) {
+          const int j = jo + h * NH + half;
+          issue_next(pass, j, jj);
+          const bf16* Yh = stg + (jj & 1) * SM::kStage;
+          const bf16* Yl = Yh + kPlaneT;
+          if (kv) {
+            v8bf Bf[2];
+            const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 64 * half + 8 * lg);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+              for (int pt = 0; pt < 4; ++pt) {
+                const int off = o_sd[ks] + 16 * pt * 64;
+                duT[h][pt] = mfma_bf16(load_v8bf(Yh + off), Bf[ks], duT[h][pt]);
+                duT[h][pt] = mfma_bf16(load_v8bf(Yl + off), Bf[ks], duT[h][pt]);
+              }
+            if (last) state_dB(Yh, k, half);
+            if (half == NH - 1) {
+              // head k's state part is complete: scale by e^{dc_last - dc_sig}; x_B
+              const float ek = fast_exp2(fminf(dcc[k * hstride + d.Lc - 1] * kLog2e - dck[h], 0.f));
+              const bf16* urow4 = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
+              float sx = 0.f;
+#pragma unroll
+              for (int pt = 0; pt < 4; ++pt) {
+                duT[h][pt] *= ek;
+                sx += dot4_bf16(duT[h][pt], *reinterpret_cast<const uint2*>(urow4 + 16 * pt));
+              }
+              sx = group_sum(sv ? sx : 0.f) * dtk[h];
+              if (lg == 0) xBc[k * hstride + sig] = sx;
+            }
+          }
+          end_stage(pass, j + 1);
+        }
       }
-      end_stage(j + 1);
     }
-  }
-  flush_r(nstage - 1);
-  finish_pair(S + ntile - 1, dCBa);
-  // row-sum partials of target strips past the length are zero
-  for (int k = 0; k < HPG; ++k)
-    for (int t = 64 * (S + ntile) + tid; t < d.Lc; t += 512) rc[k * rstride + t] = 0.f;
 
-  // ---- epilogue: du, ddt_direct, q of this slot's heads; this slot's dB half ----
+    // the dCB of target strip Tp: park this pass' share, or (last pass) add
+    // the parked shares, dB^T[n, sig] += sum_t C[t, n] dCB[t, sig] and store
+    // the hi / lo planes
+    auto finish_pair = [&](int Tp, v4f (&dCBa)[4]) {
+      if (!last) {
 #pragma unroll
-  for (int h = 0; h < HS; ++h) {
-    const int k = slot * HS + h;
-    if (k >= HPG) continue;
-    float dtv = 0.f;
+        for (int kt = 0; kt < 4; ++kt)
+          *reinterpret_cast<float4*>(dcb_at(Tp, kt)) = make_float4(dCBa[kt][0], dCBa[kt][1], dCBa[kt][2], dCBa[kt][3]);
+        return;
+      }
+      if (NPASS > 1) {
 #pragma unroll
-    for (int kk = 0; kk < HPG; ++kk)
-      if (kk == k) dtv = dtk[kk];
-    const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
-    float sx = 0.f;
+        for (int kt = 0; kt < 4; ++kt) {
+          const float4 o = *reinterpret_cast<const float4*>(dcb_at(Tp, kt));
+          dCBa[kt] += v4f{o.x, o.y, o.z, o.w};
+        }
+      }
+      const bf16* Cb = Cs + (Tp & 1) * SM::kC;
+      const int ctb = tr_first<NK * 4, swz_k256>(8 * lg, 0, lane);   // column tile 0
+      const int cfx = 16 * (swz_k256(8 * lg + ((lane & 15) >> 2)) >> 1);
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt) sx += dot4_bf16(duT[h][pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
-    sx = group_sum(sv ? sx : 0.f);
-    const float qv = group_sum(qacc[h]);
-    if (sig < qlim) {
-      bf16* durow = duc + k * 64 + static_cast<unsigned>(sig * u_rs + 4 * lg);
+      for (int ks = 0; ks < 2; ++ks) {
+        v8bf dh, dl;
+        split_p(dCBa[2 * ks], dCBa[2 * ks + 1], dh, dl);
+        *reinterpret_cast<v8bf*>(dcb_at(Tp, 2 * ks)) = dh;
+        *reinterpret_cast<v8bf*>(dcb_at(Tp, 2 * ks + 1)) = dl;
 #pragma unroll
-      for (int pt = 0; pt < 4; ++pt) *reinterpret_cast<uint2*>(durow + 16 * pt) = pack4_bf16(duT[h][pt] * dtv);
+        for (int nt = 0; nt < NT; ++nt) {
+          // column tile nt: chunk pair nt of the row, XOR-swizzled
+          const int a0 = ctb - (cfx & 0x70) + (((16 * nt) ^ cfx) & 0x70) + 32 * ks * N;
+          const v8bf a = tr_at(Cb, a0, a0 + 4 * N);
+          dBT[nt] = mfma_bf16(a, dh, dBT[nt]);
+          dBT[nt] = mfma_bf16(a, dl, dBT[nt]);
+          if (nt & 1) __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    };
+
+    // ---- pair stages: target strip T = S + Ti, head k = pass HS + h ----
+    v4f dCBa[4];
+    for (int Ti = 0; Ti < ntile; ++Ti) {
+      const int T = S + Ti, t0 = 64 * T;
+      const bf16* Cb = Cs + (T & 1) * SM::kC;
+      const bool diag = Ti == 0;
+      const bool fact = !diag && mono;
+      v4f CB[4];
+#pragma unroll
+      for (int h = 0; h < HS; ++h, ++jj) {
+        const int j = nst + Ti * HS + h;
+        const int k = pass * HS + h;
+        const bool kv = k < HPG;
+        // with one head per pass, the next stage brings the C tile of strip
+        // T + 1 into the buffer finish_pair(T - 1) reads: finish it first
+        if (HS == 1 && Ti > 0) {
+          finish_pair(T - 1, dCBa);
+          __syncthreads();
+        }
+        issue_next(pass, j, jj);
+        if (j > nst) flush_r(pass, j - 1, jj - 1);
+        if (HS > 1 && h == 0 && Ti > 0) finish_pair(T - 1, dCBa);
+        const bf16* Yh = stg + (jj & 1) * SM::kStage;
+        const bf16* Yl = Yh + kPlaneT;
+        if (h == 0) {
+          v8bf Bf[NK];
+          const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 8 * lg);
+#pragma unroll
+          for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) {
+            CB[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+            dCBa[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < NK; ++ks)
+              CB[kt] = mfma_bf16(load_v8bf(Cb + o_c[ks] + kro(kt) * N), Bf[ks], CB[kt]);
+          }
+        }
+        if (kv) {
+          const float* dcT = dcs + (T & 1) * HPG * 64 + 64 * k;
+          const float* atT = ats + (T & 1) * HPG * 64 + 64 * k;
+          const float dk = dck[h], dtv = dtk[h];
+          v8bf uf[2];
+          {
+            const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+          }
+          // W[t, sig] = dy[t] . u[sig]
+          v4f W[4];
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) {
+            W[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+              W[kt] = mfma_bf16(load_v8bf(Yh + o_w[ks] + kro(kt) * 64), uf[ks], W[kt]);
+              W[kt] = mfma_bf16(load_v8bf(Yl + o_w[ks] + kro(kt) * 64), uf[ks], W[kt]);
+            }
+            __builtin_amdgcn_sched_barrier(0);   // bound the operand reads in flight
+          }
+          // decay and masks: dCB += W', M = W' o CB (q: column sums, r: row sums); W <- L
+          float m[16];
+          float qs = 0.f;
+          if (fact) {
+            // off the diagonal with a monotone dc, e^{min(dc_t - dc_sig, 0)} =
+            // e^{min(dc_t - dc_t0, 0)} e^{min(dc_t0 - dc_sig, 0)}
+            const float bk = fast_exp2(fminf(dcT[0] - dk, 0.f));
+            const float bdt = bk * dtv;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+              const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);
+              const float4 aq = *reinterpret_cast<const float4*>(atT + tb);
+              const float av[4] = {aq.x, aq.y, aq.z, aq.w};
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const float wv = W[kt][r] * (av[r] * bdt);
+                dCBa[kt][r] += wv;
+                const float mv = wv * CB[kt][r];
+                m[4 * kt + r] = mv;
+                qs += mv;
+                W[kt][r] = CB[kt][r] * (av[r] * bk);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+              const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);
+              const float4 dq = *reinterpret_cast<const float4*>(dcT + tb);
+              const float dv[4] = {dq.x, dq.y, dq.z, dq.w};
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int t = t0 + tb + r;
+                float dec = fast_exp2(fminf(dv[r] - dk, 0.f));
+                dec = (t >= sig && t < lim) ? dec : 0.f;
+                const float wv = W[kt][r] * dtv * dec;
+                dCBa[kt][r] += wv;
+                const float mv = t > sig ? wv * CB[kt][r] : 0.f;
+                m[4 * kt + r] = mv;
+                qs += mv;
+                W[kt][r] = CB[kt][r] * dec;
+              }
+            }
+          }
+          qacc[h] += qs;
+          rx[(jj & 1) * 256 + w * 64 + key_of_row(li >> 2, 4 * lg + (li & 3))] =
+              transpose_reduce16(m, li);
+          // du^T[p, sig] += sum_t dy[t, p] L[t, sig]  (L and dy as hi + lo)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            v8bf lh, ll;
+            split_p(W[2 * ks], W[2 * ks + 1], lh, ll);
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt) {
+              const int a0 = o_tr[pt] + 32 * ks * 64;
+              const v8bf yh = tr_at(Yh, a0, a0 + 4 * 64);
+              const v8bf yl = tr_at(Yl, a0, a0 + 4 * 64);
+              duT[h][pt] = mfma_bf16(yh, lh, duT[h][pt]);
+              duT[h][pt] = mfma_bf16(yl, lh, duT[h][pt]);
+              duT[h][pt] = mfma_bf16(yh, ll, duT[h][pt]);
+              if (pt & 1) __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+        }
+        end_stage(pass, j + 1);
+      }
     }
-    if (lg == 0) {
-      ddtc[k * hstride + sig] = sx;
-      qc[k * hstride + sig] = qv;
+    flush_r(pass, n_stage(pass) - 1, jj - 1);
+    finish_pair(S + ntile - 1, dCBa);
+
+    // ---- du, ddt_direct, q of this pass' heads ----
+#pragma unroll
+    for (int h = 0; h < HS; ++h) {
+      const int k = pass * HS + h;
+      if (k >= HPG) continue;
+      const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
+      float sx = 0.f;
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) sx += dot4_bf16(duT[h][pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
+      sx = group_sum(sv ? sx : 0.f);
+      const float qv = group_sum(qacc[h]);
+      if (sig < qlim) {
+        bf16* durow = duc + k * 64 + static_cast<unsigned>(sig * u_rs + 4 * lg);
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) *reinterpret_cast<uint2*>(durow + 16 * pt) = pack4_bf16(duT[h][pt] * dtk[h]);
+      }
+      if (lg == 0) {
+        ddtc[k * hstride + sig] = sx;
+        qc[k * hstride + sig] = qv;
+      }
     }
   }
-  if (sig < qlim) {
-    bf16* dbrow = dBc + static_cast<unsigned>(sig * act_rs + 16 * NTS * slot + 4 * lg);
+  // row-sum partials of target strips past the length are zero
+  for (int k = KB; k < KE; ++k)
+    for (int t = 64 * (S + ntile) + tid; t < d.Lc; t += 256) rc[k * rstride + t] = 0.f;
+  if (last && sig < qlim) {
+    bf16* dbrow = dBc + static_cast<unsigned>(sig * act_rs + 4 * lg);
 #pragma unroll
-    for (int nt = 0; nt < NTS; ++nt) *reinterpret_cast<uint2*>(dbrow + 16 * nt) = pack4_bf16(dBT[nt]);
+    for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<uint2*>(dbrow + 16 * nt) = pack4_bf16(dBT[nt]);
   }
 }
 
@@ -943,15 +944,17 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
 // The host pass leaves the stubs of ssd_bwd_src_kernel undefined when it only
 // meets them through a launch (its device lambdas are not substituted there);
 // explicit instantiation makes it emit them.
-#define SA_SRC_INST(HPG)                                                                         \
-  template __global__ void ssd_bwd_src_kernel<4, HPG>(                                           \
+#define SA_SRC_INST(HPG, PASS)                                                                   \
+  template __global__ void ssd_bwd_src_kernel<4, HPG, PASS>(                                     \
       const bf16*, const bf16*, const bf16*, const bf16*, const float*, const float*,            \
       const bf16*, const int64_t*, bf16*, bf16*, bf16*, float*, float*, float*, float*, SsdDims, \
       int);
-SA_SRC_INST(1)
-SA_SRC_INST(2)
-SA_SRC_INST(3)
-SA_SRC_INST(4)
+SA_SRC_INST(1, 0)
+SA_SRC_INST(2, 0)
+SA_SRC_INST(3, 0)
+SA_SRC_INST(3, 1)
+SA_SRC_INST(4, 0)
+SA_SRC_INST(4, 1)
 #undef SA_SRC_INST
 
 template <typename K>
@@ -972,16 +975,22 @@ int launch_fused_hpg(const void* u, const void* B, const void* C, const bf16* dy
                      const SsdDims& d, bool dt_nonneg, hipStream_t s) {
   constexpr int NK = 4;
   const long blocks = static_cast<long>(d.b) * d.nc * d.G * (d.Lc / 64);
-  {
+  auto src_pass = [&](auto kernel) -> int {
     const size_t smem = SrcSmem<NK, HPG>::bytes;
-    if (const int rc = raise_smem(ssd_bwd_src_kernel<NK, HPG>, smem, "ssd_bwd_src")) return rc;
+    if (const int rc = raise_smem(kernel, smem, "ssd_bwd_src")) return rc;
     ProfScope prof_("ssd_bwd_src", s);
-    hipLaunchKernelGGL((ssd_bwd_src_kernel<NK, HPG>), dim3(blocks), dim3(512), smem, s,
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), smem, s,
                        static_cast<const bf16*>(u), static_cast<const bf16*>(B),
                        static_cast<const bf16*>(C), dyp, dt, dc, dSp, length,
                        static_cast<bf16*>(du), static_cast<bf16*>(dB), dcbp, ddt_part, xB_part,
                        qpart, rpart, d, dt_nonneg ? 1 : 0);
     SA_CHECK_LAUNCH("ssd_bwd_src");
+    return 0;
+  };
+  // heads in passes of two, one launch each (the last one completes dB and dCB)
+  if (const int rc = src_pass(ssd_bwd_src_kernel<NK, HPG, 0>)) return rc;
+  if constexpr (HPG > 2) {
+    if (const int rc = src_pass(ssd_bwd_src_kernel<NK, HPG, 1>)) return rc;
   }
   {
     const size_t smem = TgtSmem<NK>::bytes;
