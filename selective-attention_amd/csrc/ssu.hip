@@ -7,13 +7,17 @@
 // Replaces ssu_forward / ssu_forward_kernel
 // (triton_kernels/ssu/forward.py:7-63, ssu/forward_kernel.py:6-79).
 //
-// Pure HBM stream: the state (b, H, P, N) fp32 is read and written once.  A
-// row (b, h, p) of N states is owned by ROW_LANES lanes, each holding float4
-// strips; ROWS rows per thread are issued back to back for memory-level
-// parallelism.  y is a segmented lane reduction (xor shuffles inside the row
+// Pure HBM stream: the state (b, H, P, N) fp32 is read and written once.
+// Shapes with P and N multiples of 32 run ssu_head_kernel (one block per
+// batch row, head and range of state rows, sharing dt, the decay and B / C);
+// others run ssu_fwd_kernel, where a row (b, h, p) of N states is owned by
+// ROW_LANES lanes holding float4 strips and ROWS rows per thread are issued
+// back to back.  y is a segmented lane reduction (xor shuffles inside the row
 // group).
 #include "common.h"
 #include "prof.h"
+
+constexpr int kSsuStrips = 8;   // float4 of state per thread in the per-head kernel
 
 namespace sa {
 
@@ -90,6 +94,126 @@ __global__ __launch_bounds__(256) void ssu_fwd_kernel(
   }
 }
 
+// Four values of B or C at n (n a multiple of 4, the row 8-byte aligned for
+// bf16 and 16-byte aligned for fp32), kept in their storage type until used.
+template <typename T> struct Quad;
+template <> struct Quad<bf16> {
+  uint2 q;
+  __device__ __forceinline__ void load(const bf16* p) { q = *reinterpret_cast<const uint2*>(p); }
+  __device__ __forceinline__ float operator[](int i) const {
+    const uint32_t w = i < 2 ? q.x : q.y;
+    return (i & 1) ? bf16hi_to_f32(w) : bf16lo_to_f32(w);
+  }
+};
+template <> struct Quad<float> {
+  float4 q;
+  __device__ __forceinline__ void load(const float* p) { q = *reinterpret_cast<const float4*>(p); }
+  __device__ __forceinline__ float operator[](int i) const {
+    return i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
+  }
+};
+
+// One block per (batch row, head, range of 32 PASSES state rows): the rows
+// share dt, the decay and the B / C rows, loaded once per thread.  A row of N
+// states is owned by 8 lanes, each holding VPL float4 strips (n = 4 lane +
+// 32 i), and a thread owns PASSES rows (p = p0 + 32 pass + thread / 8): all of
+// its state loads are issued before any arithmetic.  Plain (cached) loads and
+// stores: on this in-place read-modify-write they measured faster than the
+// non-temporal forms.
+template <typename T, int VPL, int PASSES, bool GATED>
+__global__ __launch_bounds__(256) void ssu_head_kernel(
+    const T* __restrict__ u, const float* __restrict__ A, const T* __restrict__ Bm,
+    const T* __restrict__ Cm, const T* __restrict__ delta_raw, const float* __restrict__ delta_bias,
+    float* __restrict__ h, T* __restrict__ y, const float* __restrict__ Dskip,
+    const T* __restrict__ gate, int H, int P, int G, int softplus, float dmin, float dmax) {
+  constexpr int N = 32 * VPL;
+  const int nrb = P / (32 * PASSES);              // row ranges per (batch row, head)
+  const int bh = blockIdx.x / nrb, p0 = (blockIdx.x % nrb) * (32 * PASSES);
+  const int hh = bh % H, bb = bh / H, g = hh / (H / G);
+  const int li = threadIdx.x & 7, slot = threadIdx.x >> 3;
+  float* hb = h + (static_cast<long>(bh) * P + p0) * N + 4 * li;
+
+  float4 hv[PASSES][VPL];
+#pragma unroll
+  for (int r = 0; r < PASSES; ++r)
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      hv[r][i] = *reinterpret_cast<const float4*>(hb + (32 * r + slot) * N + 32 * i);
+
+  float z = load_f32(delta_raw + bh);
+  if (delta_bias) z += delta_bias[hh];
+  const float dt = make_dt(z, softplus != 0, dmin, dmax);
+  const float decay = expf(A[hh] * dt);
+  const T* Brow = Bm + (static_cast<long>(bb) * G + g) * N + 4 * li;
+  const T* Crow = Cm + (static_cast<long>(bb) * G + g) * N + 4 * li;
+  Quad<T> bv[VPL], cv[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    bv[i].load(Brow + 32 * i);
+    cv[i].load(Crow + 32 * i);
+  }
+  float part[PASSES];
+#pragma unroll
+  for (int r = 0; r < PASSES; ++r) {
+    const int p = 32 * r + slot;   // relative to p0
+    const float du = dt * load_f32(u + static_cast<long>(bh) * P + p0 + p);
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float4 v = hv[r][i];
+      v.x = v.x * decay + du * bv[i][0];
+      v.y = v.y * decay + du * bv[i][1];
+      v.z = v.z * decay + du * bv[i][2];
+      v.w = v.w * decay + du * bv[i][3];
+      *reinterpret_cast<float4*>(hb + p * N + 32 * i) = v;
+      acc += v.x * cv[i][0] + v.y * cv[i][1] + v.z * cv[i][2] + v.w * cv[i][3];
+    }
+    part[r] = acc;
+  }
+#pragma unroll
+  for (int r = 0; r < PASSES; ++r) {
+    float v = part[r];
+    v += __shfl_xor(v, 4, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 1, 64);
+    if (li == 0) {
+      const long row = static_cast<long>(bh) * P + p0 + 32 * r + slot;
+      if constexpr (GATED) {
+        // SSM block epilogue on y rounded to T: (y + D u) silu(gate), as the gate kernel
+        const float yv = to_f32(from_f32<T>(v));
+        const float xv = load_f32(u + row);
+        const float gv = load_f32(gate + row);
+        st(y + row, (yv + Dskip[hh * P + p0 + 32 * r + slot] * xv) * (gv * fast_sigmoid(gv)));
+      } else {
+        st(y + row, v);
+      }
+    }
+  }
+}
+
+template <typename T, int VPL, int PASSES>
+static int launch_ssu_head(const void* u, const float* A, const void* B, const void* C,
+                           const void* delta_raw, const float* delta_bias, float* h, void* y,
+                           const float* Dskip, const void* gate, int batch, int H, int P, int G,
+                           int softplus, float dmin, float dmax, hipStream_t stream) {
+  const long blocks = static_cast<long>(batch) * H * (P / (32 * PASSES));
+  if (blocks == 0) return 0;
+  ProfScope prof_(gate ? "ssu_fwd_gated" : "ssu_fwd", stream);
+  if (gate)
+    hipLaunchKernelGGL((ssu_head_kernel<T, VPL, PASSES, true>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(256), 0, stream, static_cast<const T*>(u), A, static_cast<const T*>(B),
+                       static_cast<const T*>(C), static_cast<const T*>(delta_raw), delta_bias, h,
+                       static_cast<T*>(y), Dskip, static_cast<const T*>(gate), H, P, G, softplus,
+                       dmin, dmax);
+  else
+    hipLaunchKernelGGL((ssu_head_kernel<T, VPL, PASSES, false>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(256), 0, stream, static_cast<const T*>(u), A, static_cast<const T*>(B),
+                       static_cast<const T*>(C), static_cast<const T*>(delta_raw), delta_bias, h,
+                       static_cast<T*>(y), nullptr, nullptr, H, P, G, softplus, dmin, dmax);
+  SA_CHECK_LAUNCH(gate ? "ssu_fwd_gated" : "ssu_fwd");
+  return 0;
+}
+
 template <typename T, int ROW_LANES>
 static int launch_ssu(const void* u, const float* A, const void* B, const void* C,
                       const void* delta_raw, const float* delta_bias, float* h, void* y,
@@ -123,6 +247,24 @@ static int dispatch_ssu(const void* u, const float* A, const void* B, const void
                         const void* delta_raw, const float* delta_bias, float* h, void* y,
                         const float* Dskip, const void* gate, int batch, int H, int P, int G,
                         int N, int softplus, float dmin, float dmax, hipStream_t stream) {
+  // per-head blocks: N = 32 VPL (VPL 1, 2, 4), P a multiple of 32, aligned rows;
+  // PASSES rows per thread so that a thread holds kSsuStrips float4 of state
+  const uintptr_t ba = reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C);
+  const bool head_ok = (reinterpret_cast<uintptr_t>(h) & 15) == 0 &&
+                       (ba & (sizeof(T) == 2 ? 7 : 15)) == 0 && P % 32 == 0 && N % 32 == 0;
+  if (head_ok) {
+    const int vpl = N / 32;
+    int passes = 1;
+    while (passes * 2 * vpl <= kSsuStrips && P % (64 * passes) == 0) passes *= 2;
+#define SA_SSU_HEAD(V, R)                                                                   \
+  if (vpl == V && passes == R)                                                              \
+    return launch_ssu_head<T, V, R>(u, A, B, C, delta_raw, delta_bias, h, y, Dskip, gate, \
+                                    batch, H, P, G, softplus, dmin, dmax, stream);
+    SA_SSU_HEAD(1, 1) SA_SSU_HEAD(1, 2) SA_SSU_HEAD(1, 4) SA_SSU_HEAD(1, 8)
+    SA_SSU_HEAD(2, 1) SA_SSU_HEAD(2, 2) SA_SSU_HEAD(2, 4)
+    SA_SSU_HEAD(4, 1) SA_SSU_HEAD(4, 2)
+#undef SA_SSU_HEAD
+  }
   // lanes per state row: enough float4 strips to cover N once, at most 64
   const bool vec4 = N % 4 == 0 && (reinterpret_cast<uintptr_t>(h) & 15) == 0;
   const int strips = vec4 ? N / 4 : N;

@@ -149,6 +149,47 @@ def test_ssu_gated_matches_unfused(dtype, shape):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [dict(b=2, H=4, P=32, N=64, G=2), dict(b=3, H=2, P=128, N=32, G=1),
+                                   dict(b=1, H=6, P=96, N=128, G=3), dict(b=2, H=2, P=64, N=96, G=2)])
+def test_ssu_parity_head_blocks(dtype, shape):
+    """Shapes of the per-(batch row, head) kernel (P and N multiples of 32:
+    1, 2 or 4 float4 strips per lane and 1, 2 or 4 rows per thread) and two
+    that fall back to the row kernel (P = 96, N = 96)."""
+    print(f"ssu head blocks dtype={dtype} shape={shape}", flush=True)
+    x = _small(dtype=dtype, bias=True, **shape)
+    y_ref, h_ref = ssu_ref.ssu_forward(**x)
+    y, h = _run_gpu(x, dtype)
+    assert_parity(h, h_ref, torch.float32, "h")
+    assert_parity(y, y_ref, dtype, "y")
+
+
+@pytest.mark.gpu
+def test_ssu_gated_strided_views():
+    """Gate and x as column slices of one wider projection (the layout of an
+    in_proj output): the wrapper makes them contiguous, and the result equals
+    the call on contiguous copies bit for bit."""
+    from selective_attention.kernels.ssu import ssu_gated_forward
+    dtype = torch.bfloat16
+    x = _small(dtype=dtype, bias=True, b=4, H=8, P=64, N=128, G=2)
+    b, H, P = x["u"].shape
+    g = torch.Generator().manual_seed(5)
+    proj = torch.randn(b, 3 * H * P, generator=g).to(dtype).cuda()
+    gate_v = proj[:, :H * P].view(b, H, P)
+    u_v = proj[:, 2 * H * P:].view(b, H, P)
+    assert not gate_v.is_contiguous() and not u_v.is_contiguous()
+    D = torch.randn(H * P, generator=g).cuda()
+    xd = {k: (None if v is None else v.cuda()) for k, v in x.items()}
+    h1, h2 = xd["h"].clone(), xd["h"].clone()
+    out_v = ssu_gated_forward(u_v, xd["A"], xd["B"], xd["C"], xd["delta_raw"], xd["delta_bias"],
+                              h1, D, gate_v)
+    out_c = ssu_gated_forward(u_v.contiguous(), xd["A"], xd["B"], xd["C"], xd["delta_raw"],
+                              xd["delta_bias"], h2, D, gate_v.contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(out_v, out_c) and torch.equal(h1, h2)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("softplus,limit", [(False, (0.0, 0.3)), (True, (0.02, 0.05))])
 def test_ssu_parity_limits(softplus, limit):
     x = _small()
