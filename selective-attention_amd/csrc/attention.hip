@@ -65,17 +65,18 @@ __device__ __forceinline__ void softmax_block(v4f (&s)[KT], v4f (&o)[DT], float&
 // LDS feeds two MFMAs (two 16-query tiles).  The two key halves run
 // independent online softmaxes and are merged through LDS at the end.
 //
-// K and V tiles go from HBM straight into LDS (global_load_lds, 16 bytes per
-// lane) in two stages: the next selected block streams in while the current
-// one is computed, with no staging registers.  The tiles are unpadded
+// K and V tiles (and the block's key biases) go from HBM straight into LDS
+// (global_load_lds, 16 bytes per lane) in two stages: the next selected block
+// streams in while the current one is computed, with no staging registers
+// and one barrier per block.  The tiles are unpadded
 // ([key][D] bf16) with the 16-byte chunks of row r permuted (k_swz, v_swz),
 // so the K fragment reads (16 rows, one chunk) and the V^T transpose reads
 // (ds_read_b64_tr_b16: 8 rows, a chunk pair) hit distinct LDS banks.
 // ---------------------------------------------------------------------------
 template <int D>
 struct SparseSmem {
-  static constexpr size_t tile = 64 * D;               // bf16 per K or V tile
-  static constexpr size_t bytes = 2 * 2 * tile * 2;    // [2 stages][K, V]; also holds the merge
+  static constexpr int tile = 64 * D;               // bf16 per K or V tile
+  static constexpr int stage = 2 * tile + 128;      // bf16: K, V, the 64 fp32 key biases
 };
 
 // chunk permutations of row r (16-byte chunks; D = 128: 16 per row, D = 64:
@@ -97,6 +98,36 @@ __device__ __forceinline__ int v_swz(int r) {
   else return (((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 1) | ((r >> 4) & 1);
 }
 
+// LDS DMA written as instructions the compiler does not interpret: it then
+// inserts no waits of its own for them (it cannot tell which LDS bytes a DMA
+// writes, and would otherwise hold every LDS read until all DMA in flight had
+// landed); the kernel waits with explicit vmcnt and barriers.  Each lane's
+// data goes to LDS byte address lds + 16 lane (4 lane for the dword form),
+// from base + off (off in bytes).  m0 carries the LDS address; nothing else
+// in the kernels that use these relies on m0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p)));
+}
+__device__ __forceinline__ void dma_lds16(const void* base, uint32_t off, const void* lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
+               "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_lds4(const void* base, uint32_t off, const void* lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base),
+               "s"(lds_addr(lds)) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// p[i] for a wave-uniform i through the constant address space: a scalar
+// load, counted by lgkmcnt rather than the vector memory counter
+__device__ __forceinline__ int32_t load_uniform(const int32_t* p, int i) {
+  typedef const __attribute__((address_space(4))) int32_t cint;
+  return ((cint*)p)[__builtin_amdgcn_readfirstlane(i)];
+}
+
 // s_waitcnt immediate: vmcnt(N), expcnt and lgkmcnt not waited for
 template <int N>
 constexpr int vm_wait() {
@@ -111,13 +142,17 @@ constexpr int kLgkmWait0 = 0xF | (7 << 4) | (3 << 14);   // lgkmcnt(0) only
 // some score exceeds it by more than 2^8: the common block needs no cross-lane
 // reduction at all, and probabilities stay <= 256.  l is this lane's partial
 // row sum (its own keys); the four lane groups' parts are added at the end.
+// The scores may come unscaled: the log2-domain score is s * sc (sc > 0), and
+// the scale is folded into the exponent's argument.
 template <int KT, int DT>
-__device__ __forceinline__ void softmax_lazy(v4f (&s)[KT], v4f (&o)[DT], float& m, float& l) {
+__device__ __forceinline__ void softmax_lazy(v4f (&s)[KT], v4f (&o)[DT], float& m, float& l,
+                                             float sc = 1.0f) {
   float mx = kNegInf;
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][i]);
+  mx *= sc;
   if (__ballot(mx > m + 8.0f)) {
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -137,7 +172,7 @@ __device__ __forceinline__ void softmax_lazy(v4f (&s)[KT], v4f (&o)[DT], float& 
   for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float p = fast_exp2(s[kt][i] - mref);
+      const float p = fast_exp2(fmaf(s[kt][i], sc, -mref));
       s[kt][i] = p;
       sum += p;
     }
@@ -163,8 +198,9 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
   using SM = SparseSmem<D>;
   constexpr int DT = D / 16, KS = D / 32;
   constexpr int IPW = D / 32;   // 1 KB DMA instructions per wave per tile (tile = 128 D bytes)
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* sm = reinterpret_cast<bf16*>(smem_raw);   // [2 stages][K tile, V tile]
+  // two stages as separate LDS objects; they also hold the final merge
+  __shared__ __align__(16) bf16 stage0[SM::stage];
+  __shared__ __align__(16) bf16 stage1[SM::stage];
 
   const int lid = xcd_swizzle(blockIdx.x, gridDim.x);
   // grid_qblk >= the query blocks of the packing: surplus ids find no sequence
@@ -251,46 +287,70 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     }
     vmask = __ballot(ok);
   }
+  // (wave-uniform slot indices: the general path's table reads are scalar
+  // loads, which do not count against the vector memory counter the DMA
+  // pipeline waits on)
   auto next_valid = [&](int e) -> int {   // first valid slot >= e, or nslot
     if (dense) return min(e, nslot);
     if (simple) {
       const uint64_t mm = e >= 64 ? 0ull : (vmask >> e);
       return mm ? e + __builtin_ctzll(mm) : nslot;
     }
-    for (; e < nslot; ++e) {
-      const int kb = sel[e];
+    for (e = __builtin_amdgcn_readfirstlane(e); e < nslot; ++e) {
+      const int kb = load_uniform(sel, e);
       if (kb >= 0 && kb < nkb && (MODE != kCausalSelf || kb <= jq)) {
         bool dup = false;
-        for (int j = 0; j < e && !dup; ++j) dup = sel[j] == kb;
+        for (int j = 0; j < e && !dup; ++j) dup = load_uniform(sel, j) == kb;
         if (!dup) return e;
       }
     }
     return nslot;
   };
   auto block_of = [&](int e) -> int {
-    return dense ? e : simple ? __builtin_amdgcn_readlane(my_kb, e) : sel[e];
+    return dense ? e : simple ? __builtin_amdgcn_readlane(my_kb, e) : load_uniform(sel, e);
   };
 
   // DMA of block kb into a stage: lane l of this wave's instruction i fills
   // tile bytes 1024 (IPW w + i) + 16 l, i.e. row `row`, stored chunk `ch`,
   // which holds logical chunk ch ^ k_swz(row) (K) or ch ^ v_swz(row) (V).  Rows past the sequence
   // repeat its last key (their scores are masked to -inf, so p = 0).
-  auto issue_kv = [&](int kb, int stage) {
+  // full blocks use per-lane element offsets computed once (32-bit, added to
+  // the block's wave-uniform base); the last, partial block of a sequence
+  // clamps its rows
+  int dma_k[IPW], dma_v[IPW];
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    const int pos = ((w * IPW + i) << 10) + (lane << 4);
+    const int row = pos / (2 * D), ch = (pos % (2 * D)) >> 4;
+    dma_k[i] = row * static_cast<int>(rs) + 8 * (ch ^ k_swz<D>(row));
+    dma_v[i] = row * static_cast<int>(rs) + 8 * (ch ^ v_swz<D>(row));
+  }
+  auto issue_kv = [&](int kb, bf16* Kt) __attribute__((always_inline)) {
     const int k0 = kb * BS, nk = min(BS, nks - k0);
-    bf16* Kt = sm + stage * 2 * SM::tile;
     bf16* Vt = Kt + SM::tile;
     const bf16* kb0 = kbase + static_cast<long>(k0) * rs;
     const bf16* vb0 = vbase + static_cast<long>(k0) * rs;
+    if constexpr (BIAS) {   // the block's key biases (rows past the sequence repeat the last)
+      if (w == 0) dma_lds4(bias, 4u * min(k0 + lane, nks - 1), Vt + SM::tile);
+    }
+    if (nk == BS) {
+#pragma unroll
+      for (int i = 0; i < IPW; ++i) {
+        dma_lds16(kb0, 2u * dma_k[i], Kt + ((w * IPW + i) << 9));
+        dma_lds16(vb0, 2u * dma_v[i], Vt + ((w * IPW + i) << 9));
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
       const int pos = ((w * IPW + i) << 10) + (lane << 4);
       const int row = pos / (2 * D);
-      const int rr = nk == BS ? row : min(row, nk - 1);
+      const int rr = min(row, nk - 1);
       const int ch = (pos % (2 * D)) >> 4;
-      const long koff = static_cast<long>(rr) * rs + 8 * (ch ^ k_swz<D>(row));
-      const long voff = static_cast<long>(rr) * rs + 8 * (ch ^ v_swz<D>(row));
-      __builtin_amdgcn_global_load_lds(kb0 + koff, Kt + ((w * IPW + i) << 9), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vb0 + voff, Vt + ((w * IPW + i) << 9), 16, 0, 0);
+      const int koff = rr * static_cast<int>(rs) + 8 * (ch ^ k_swz<D>(row));
+      const int voff = rr * static_cast<int>(rs) + 8 * (ch ^ v_swz<D>(row));
+      dma_lds16(kb0, 2u * koff, Kt + ((w * IPW + i) << 9));
+      dma_lds16(vb0, 2u * voff, Vt + ((w * IPW + i) << 9));
     }
   };
 
@@ -314,31 +374,35 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
   const int vhalf = 4 * ((lane & 15) & 1);               // element offset inside the chunk
   const int vchunk = ((lane & 15) & 3) >> 1;              // chunk of the pair
 
-  int e = next_valid(0);
-  int stage = 0;
-  if (e < nslot) issue_kv(block_of(e), 0);
-  while (e < nslot) {
+  // Pipeline: the tiles of block e + 1 land in one stage while block e is
+  // computed from the other.  The loop is unrolled by two so that each stage
+  // is a fixed LDS object.
+  int e = 0, en = 0;
+  // one key block: computed from stage cur while the next block's tiles land in nxt
+  auto step = [&](bf16* cur, bf16* nxt) __attribute__((always_inline)) {
     const int kb = block_of(e);
-    const int en = next_valid(e + 1);
+    const int enn = en < nslot ? next_valid(en + 1) : nslot;   // the block after next
     const int k0 = kb * BS;
     const int nk = min(BS, nks - k0);
-    // bias of the wave's keys 32 kh + 8g + 0..7 (issued before the next DMA, so
-    // the wait below covers it)
-    float bk[8];
-    if constexpr (BIAS) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) bk[i] = bias[min(k0 + 32 * kh + 8 * g + i, nks - 1)];
-    }
-    if (en < nslot) {
-      issue_kv(block_of(en), stage ^ 1);
-      __builtin_amdgcn_s_waitcnt(vm_wait<2 * IPW>());   // this block's tiles have landed
-    } else {
-      __builtin_amdgcn_s_waitcnt(vm_wait<0>());
-    }
+    // one barrier per block: this block's tiles have landed and are visible,
+    // and every wave is done with the previous block, whose stage the next
+    // block's DMA refills
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(vm_wait<0>());
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    const bf16* Ks = sm + stage * 2 * SM::tile;
+    if (en < nslot) issue_kv(block_of(en), nxt);
+    const bf16* Ks = cur;
     const bf16* Vs = Ks + SM::tile;
+    // bias of the wave's keys 32 kh + 8g + 0..7
+    float bk[8];
+    if constexpr (BIAS) {
+      const float* bs = reinterpret_cast<const float*>(Vs + SM::tile) + 32 * kh + 8 * g;
+      const float4 b0 = *reinterpret_cast<const float4*>(bs);
+      const float4 b1 = *reinterpret_cast<const float4*>(bs + 4);
+      bk[0] = b0.x; bk[1] = b0.y; bk[2] = b0.z; bk[3] = b0.w;
+      bk[4] = b1.x; bk[5] = b1.y; bk[6] = b1.z; bk[7] = b1.w;
+    }
 
     // S^T = K . Q^T for the wave's 32 keys (score tiles kt = 2 kh, 2 kh + 1)
     v4f sc[2][2];
@@ -362,23 +426,29 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     const bool interior = MODE == kCausalSelf
                               ? (kb < jq && qfull)
                               : (qfull && k0 + BS <= nks && kb != (MODE == kCross ? 0 : jq));
+    // interior blocks without a bias keep raw scores (the scale goes into the
+    // exponent); otherwise scale, bias and masks are applied in place
+    float scl = scale_log2;
+    if (!interior || BIAS) {
+      scl = 1.0f;
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt) {
+      for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-      for (int u2 = 0; u2 < 2; ++u2)
+        for (int u2 = 0; u2 < 2; ++u2)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kl = key_of_row(2 * kh + u2, 4 * g + i);   // = 32 kh + 8g + 4 u2 + i
-          const int key = k0 + kl;
-          float val = sc[jt][u2][i] * scale_log2;
-          const bool exempt = MODE == kCross ? key == 0 : key == qloc[jt];
-          if constexpr (BIAS) val += (interior || !exempt) ? bk[4 * u2 + i] * kLog2e : 0.f;
-          if (!interior)
-            val = (kl < nk && (MODE != kCausalSelf || key <= qloc[jt]) && qloc[jt] < n) ? val : kNegInf;
-          sc[jt][u2][i] = val;
-        }
-      softmax_lazy<2, DT>(sc[jt], acc[jt], m[jt], l[jt]);
+          for (int i = 0; i < 4; ++i) {
+            const int kl = key_of_row(2 * kh + u2, 4 * g + i);   // = 32 kh + 8g + 4 u2 + i
+            const int key = k0 + kl;
+            float val = sc[jt][u2][i] * scale_log2;
+            const bool exempt = MODE == kCross ? key == 0 : key == qloc[jt];
+            if constexpr (BIAS) val += (interior || !exempt) ? bk[4 * u2 + i] * kLog2e : 0.f;
+            if (!interior)
+              val = (kl < nk && (MODE != kCausalSelf || key <= qloc[jt]) && qloc[jt] < n) ? val : kNegInf;
+            sc[jt][u2][i] = val;
+          }
     }
+#pragma unroll
+    for (int jt = 0; jt < 2; ++jt) softmax_lazy<2, DT>(sc[jt], acc[jt], m[jt], l[jt], scl);
     // O^T += V^T . P^T over the wave's 32 keys
     {
       const v8bf pb0 = pack_p(sc[0][0], sc[0][1]);
@@ -394,13 +464,25 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
         acc[1][t] = mfma_bf16(vf, pb1, acc[1][t]);
       }
     }
-    // every wave is done with this stage before it is refilled
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(kLgkmWait0);
-    __builtin_amdgcn_s_barrier();
-    stage ^= 1;
     e = en;
+    en = enn;
+  };
+  e = next_valid(0);
+  en = e < nslot ? next_valid(e + 1) : nslot;
+  // the query fragments (and the selection row) have arrived before the loop:
+  // nothing the compiler tracks is in flight inside it
+  __builtin_amdgcn_s_waitcnt(vm_wait<0>());
+  if (e < nslot) issue_kv(block_of(e), stage0);
+  while (e < nslot) {
+    step(stage0, stage1);
+    if (e >= nslot) break;
+    step(stage1, stage0);
   }
+  // every wave is done with the tiles before the merge reuses the LDS
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 
   // the row sums so far are per lane (its own keys): add the four lane groups
 #pragma unroll
@@ -409,9 +491,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     l[jt] += __shfl_xor(l[jt], 32, 64);
   }
   // merge the two key halves: waves kh = 1 hand (m, l, O^T) to waves kh = 0
-  float* xch = reinterpret_cast<float*>(smem_raw);   // [qh][2 jt][DT][64 lanes] float4 + m, l
-  float4* xo = reinterpret_cast<float4*>(xch) + qh * 2 * DT * 64;
-  float* xm = xch + 4 * (2 * 2 * DT * 64) + qh * 2 * 2 * 64;
+  // [qh][2 jt][DT][64 lanes] float4 in stage 0, [qh][2 jt][m, l][64 lanes] in stage 1
+  float4* xo = reinterpret_cast<float4*>(stage0) + qh * 2 * DT * 64;
+  float* xm = reinterpret_cast<float*>(stage1) + qh * 2 * 2 * 64;
+  static_assert(2 * 2 * DT * 64 * 16 <= SM::stage * 2, "merge fits stage 0");
   if (kh == 1) {
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) {
@@ -445,31 +528,15 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
   }
 }
 
-// raise the kernel's dynamic LDS limit once per process (D = 128 needs 64 KB)
-template <int D, bool BIAS, int MODE>
-int sparse_smem_attr() {
-  static bool done = false;
-  if (!done) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_attn_fwd_kernel<D, BIAS, MODE>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             static_cast<int>(SparseSmem<D>::bytes));
-    SA_CHECK_ARG(e == hipSuccess, "sa_sparse_attn_fwd: %zu B of LDS refused: %s",
-                 SparseSmem<D>::bytes, hipGetErrorString(e));
-    done = true;
-  }
-  return 0;
-}
-
 template <int D, bool BIAS, int MODE>
 int launch_sparse(const void* q, const void* k, const void* v, const int32_t* cu,
                   const int32_t* cu_k, int nseq, const int32_t* block_idx, int n_qblk,
                   int max_blocks, int grid_qblk, int dense_all, const float* key_bias, void* o, int T,
                   int Tk, int H, float scale_log2, hipStream_t s) {
   const long blocks = static_cast<long>(H) * grid_qblk;
-  if (sparse_smem_attr<D, BIAS, MODE>()) return 1;
   ProfScope prof_(MODE == kCausalSelf ? "sparse_attn_fwd" : MODE == kFullSelf ? "attn_full_fwd" : "attn_cross_fwd", s);
   hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, BIAS, MODE>), dim3(blocks), dim3(256),
-                     SparseSmem<D>::bytes, s, static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                     0, s, static_cast<const bf16*>(q), static_cast<const bf16*>(k),
                      static_cast<const bf16*>(v), cu, cu_k, nseq, block_idx, n_qblk, max_blocks,
                      grid_qblk, dense_all, key_bias, static_cast<bf16*>(o), T, Tk,
                      H, scale_log2);
