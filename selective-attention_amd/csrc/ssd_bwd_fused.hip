@@ -246,12 +246,6 @@ struct SrcSmem {
   static constexpr int N = 32 * NK;
   static constexpr int kStage = 2 * kPlaneT;       // bf16: one head's dy tile or dS n half (hi, lo)
   static constexpr int kC = 64 * N;                // bf16: one C tile
-  static constexpr size_t stage_off = 0;
-  static constexpr size_t c_off = stage_off + 2 * kStage * 2;
-  static constexpr size_t dc_off = c_off + 2 * kC * 2;         // float [2][HPG][64] dc (log2)
-  static constexpr size_t at_off = dc_off + 2 * HPG * 64 * 4;  // float [2][HPG][64] e^{dc - dc_T0}
-  static constexpr size_t r_off = at_off + 2 * HPG * 64 * 4;   // float [2 parity][4 waves][64]
-  static constexpr size_t bytes = r_off + 2 * 4 * 64 * 4;
 };
 
 template <int NK, int HPG, int PASS>
@@ -274,12 +268,18 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   constexpr int NH = N / 64;     // 64-wide n halves of a dS tile
   constexpr int NT = N / 16;     // 16-row n tiles of dB^T
   static_assert(NH == 2, "ssd_bwd_src: state_dim 128");
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* stg = reinterpret_cast<bf16*>(smem_raw + SM::stage_off);   // [2][hi, lo][64][64]
-  bf16* Cs = reinterpret_cast<bf16*>(smem_raw + SM::c_off);        // [2][64][N]
-  float* dcs = reinterpret_cast<float*>(smem_raw + SM::dc_off);
-  float* ats = reinterpret_cast<float*>(smem_raw + SM::at_off);
-  float* rx = reinterpret_cast<float*>(smem_raw + SM::r_off);
+  // Separate LDS objects per stage buffer: with the stage parity a
+  // compile-time constant, the compiler sees that the reads of one buffer do
+  // not depend on the DMA into the other and inserts no waits for it.
+  __shared__ __align__(16) bf16 stg0[SM::kStage];   // [hi, lo][64][64]
+  __shared__ __align__(16) bf16 stg1[SM::kStage];
+  __shared__ __align__(16) bf16 Cs0[SM::kC];        // [64][N]
+  __shared__ __align__(16) bf16 Cs1[SM::kC];
+  __shared__ __align__(16) float dcs[2 * HPG * 64];  // [T parity][head][64] dc (log2)
+  __shared__ __align__(16) float ats[2 * HPG * 64];  // [T parity][head][64] e^{dc - dc_T0}
+  __shared__ __align__(16) float rx[2 * 4 * 64];     // [stage parity][4 waves][64] row sums
+  auto stg = [&](int par) -> bf16* { return par ? stg1 : stg0; };
+  auto Cs = [&](int par) -> bf16* { return par ? Cs1 : Cs0; };
 
   const int stiles = d.Lc / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -347,8 +347,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   // Stages of pass p: first the state stages, dS n half (j % NH) of head
   // kb + j / NH, kb = 0 in the last pass (every head up to this pass' own)
   // and p HS before; then per target strip T = S + Ti the dy tile of head
-  // p HS + h, h = 0..HS-1 (C_T and the dc tables come with h == 0).  jj
-  // counts the stages of all passes and selects the LDS buffer.
+  // p HS + h, h = 0..HS-1 (C_T and the dc tables come with h == 0).
   auto n_state = [&](int p) { return (p == NPASS - 1 ? (p + 1) * HS : HS) * NH; };
   auto n_stage = [&](int p) { return n_state(p) + HS * ntile; };
   const bf16* dyg = dyp + (bcg * stiles) * (HPG * 2L * kPlaneT);   // + (T HPG + k) 2 kPlaneT
@@ -362,9 +361,9 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 #pragma unroll
   for (int i = 0; i < NK; ++i) o_gc[i] = dma_off<NK * 4, swz_k256>(i, w, lane, act_rs);
   float pdc = 0.f, pdc0 = 0.f;   // dc prefetch of the next target strip (head tid / 64, row tid % 64)
-  auto issue = [&](int p, int j, int jj) {
+  auto issue = [&](int p, int j, int par) {   // par: the stage's buffer
     if (p >= NPASS) return;
-    bf16* dst = stg + (jj & 1) * SM::kStage;
+    bf16* dst = stg(par);
     const int nst = n_state(p);
     if (j < nst) {
       const int k = (p == NPASS - 1 ? 0 : p * HS) + j / NH, half = j % NH;
@@ -382,21 +381,21 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
       }
       if (h == 0) {
         const int t0 = 64 * T;
-        bf16* cdst = Cs + (T & 1) * SM::kC;
+        bf16* cdst = Cs(T & 1);
         const bf16* csrc = Cc + static_cast<long>(t0) * act_rs;
         if (qlim - t0 >= 64) dma_pre<NK * 4>(cdst, csrc, o_gc, w);
         else dma_tile<NK * 4, swz_k256>(cdst, csrc, act_rs, qlim - t0, w, lane);
-        if (tid < HPG * 64) {
+        if (tid < HPG * 64) {   // raw: nothing waits for these before the stage's end
           const float* dch = dcc + (tid >> 6) * hstride + t0;
-          pdc = dch[tid & 63] * kLog2e;
-          pdc0 = dch[0] * kLog2e;
+          pdc = dch[tid & 63];
+          pdc0 = dch[0];
         }
       }
     }
   };
-  // the next stage after stage j of pass p
-  auto issue_next = [&](int p, int j, int jj) {
-    if (j + 1 < n_stage(p)) issue(p, j + 1, jj + 1);
+  // the next stage after stage j (buffer par) of pass p
+  auto issue_next = [&](int p, int j, int par) {
+    if (j + 1 < n_stage(p)) issue(p, j + 1, par ^ 1);
   };
   // end of the stage before stage j of pass p: the dc tables of a new target
   // strip, then every DMA of the next stage complete and visible
@@ -404,16 +403,16 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     const int nst = n_state(p);
     if (j < n_stage(p) && j >= nst && (j - nst) % HS == 0 && tid < HPG * 64) {
       const int T = S + (j - nst) / HS;
-      dcs[(T & 1) * HPG * 64 + tid] = pdc;
-      ats[(T & 1) * HPG * 64 + tid] = fast_exp2(fminf(pdc - pdc0, 0.f));
+      dcs[(T & 1) * HPG * 64 + tid] = pdc * kLog2e;
+      ats[(T & 1) * HPG * 64 + tid] = fast_exp2(fminf(pdc * kLog2e - pdc0 * kLog2e, 0.f));
     }
     wait_all_mem();
     __syncthreads();
   };
-  auto flush_r = [&](int p, int j, int jj) {   // the row sums pair stage j left in LDS -> rpart
+  auto flush_r = [&](int p, int j, int par) {   // the row sums pair stage j left in LDS -> rpart
     const int qq = j - n_state(p), Ti = qq / HS, k = p * HS + qq % HS;
     if (tid < 64 && k < HPG) {
-      const float* rr = rx + (jj & 1) * 256;
+      const float* rr = rx + par * 256;
       rc[k * rstride + 64 * (S + Ti) + tid] = rr[tid] + rr[64 + tid] + rr[128 + tid] + rr[192 + tid];
     }
   };
@@ -441,7 +440,11 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   wait_all_mem();
   __syncthreads();
 
-  int jj = 0;   // stage counter
+  // Stage buffers alternate; the state stages number NH = 2 per head and the
+  // pair stages HS per target strip, so a state stage's buffer is its n half
+  // and a pair stage's its head (with one head per pass, its strip's parity).
+  // Each stage issues its own register loads before the next stage's DMA, so
+  // that waiting for them does not wait for the DMA.
   v4f dBT[NT];  // dB^T rows n = 16 nt + 4 lg + r, column sig (last pass)
   {
     const int nst = n_state(pass);
@@ -469,16 +472,27 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         o_st[nt4][0] = tr_first<8, swz_s128>(8 * lg, 16 * nt4, lane);
         o_st[nt4][1] = tr_first<8, swz_s128>(8 * lg + 4, 16 * nt4, lane);
       }
-      // dB^T rows of the n half in stage buffer Y from head k's dS
-      auto state_dB = [&](const bf16* Yh, int k, int half) {
-        const int kc = k * hstride + scl;
-        const float dtv = sv ? dtc[kc] : 0.f;
-        const float wk = fast_exp2(fminf((dcc[k * hstride + d.Lc - 1] - dcc[kc]) * kLog2e, 0.f)) * dtv;
-        const bf16* Yl = Yh + kPlaneT;
+      // head k's u row and state weight w = e^{min(dc_last - dc, 0)} dt at this lane's column
+      struct UW {
         v8bf uf[2];
+        float dtv, dc, dcl;
+      };
+      auto load_uw = [&](int k) -> UW {
+        UW r;
+        const int kc = k * hstride + scl;
+        r.dtv = sv ? dtc[kc] : 0.f;
+        r.dc = dcc[kc];
+        r.dcl = dcc[k * hstride + d.Lc - 1];
         const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+        for (int ks = 0; ks < 2; ++ks) r.uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+        return r;
+      };
+      // dB^T rows of the n half in stage buffer Y from head k's dS
+      auto state_dB = [&](const bf16* Yh, const UW& x, int half) {
+        const float wk = fast_exp2(fminf((x.dcl - x.dc) * kLog2e, 0.f)) * x.dtv;
+        const bf16* Yl = Yh + kPlaneT;
+        const v8bf* uf = x.uf;
 #pragma unroll
         for (int nt4 = 0; nt4 < 4; ++nt4) {
           v4f tmp = v4f{0.f, 0.f, 0.f, 0.f};
@@ -495,10 +509,16 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
       };
       // last pass: the dB state part of the heads of the earlier passes
       if (last) {
-        for (int j = 0; j < pass * HS * NH; ++j, ++jj) {
-          issue_next(pass, j, jj);
-          state_dB(stg + (jj & 1) * SM::kStage, j / NH, j % NH);
-          end_stage(pass, j + 1);
+        for (int kk = 0; kk < pass * HS; ++kk) {
+#pragma unroll
+          for (int half = 0; half < NH; ++half) {
+            const int j = kk * NH + half;
+            const UW x = load_uw(kk);
+            __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the DMA
+            issue_next(pass, j, half);
+            state_dB(stg(half), x, half);
+            end_stage(pass, j + 1);
+          }
         }
       }
       const int jo = last ? pass * HS * NH : 0;   // first stage of this pass' own heads
@@ -507,16 +527,29 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         const int k = pass * HS + h;
         const bool kv = k < HPG;
 #pragma unroll
-        for (int half = 0; half < NH; ++half, ++jj) {
+        for (int half = 0; half < NH; ++half) {
           const int j = jo + h * NH + half;
-          issue_next(pass, j, jj);
-          const bf16* Yh = stg + (jj & 1) * SM::kStage;
-          const bf16* Yl = Yh + kPlaneT;
+          v8bf Bf[2];
+          UW x;
+          uint2 ux[4];    // u of head k at this lane's column, for x_B
+          float dcl = 0.f;
           if (kv) {
-            v8bf Bf[2];
             const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 64 * half + 8 * lg);
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+            if (last) x = load_uw(k);
+            if (half == NH - 1) {
+              const bf16* urow4 = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
+#pragma unroll
+              for (int pt = 0; pt < 4; ++pt) ux[pt] = *reinterpret_cast<const uint2*>(urow4 + 16 * pt);
+              dcl = dcc[k * hstride + d.Lc - 1];
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the DMA
+          issue_next(pass, j, half);
+          const bf16* Yh = stg(half);
+          const bf16* Yl = Yh + kPlaneT;
+          if (kv) {
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -525,16 +558,15 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
                 duT[h][pt] = mfma_bf16(load_v8bf(Yh + off), Bf[ks], duT[h][pt]);
                 duT[h][pt] = mfma_bf16(load_v8bf(Yl + off), Bf[ks], duT[h][pt]);
               }
-            if (last) state_dB(Yh, k, half);
+            if (last) state_dB(Yh, x, half);
             if (half == NH - 1) {
               // head k's state part is complete: scale by e^{dc_last - dc_sig}; x_B
-              const float ek = fast_exp2(fminf(dcc[k * hstride + d.Lc - 1] * kLog2e - dck[h], 0.f));
-              const bf16* urow4 = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
+              const float ek = fast_exp2(fminf(dcl * kLog2e - dck[h], 0.f));
               float sx = 0.f;
 #pragma unroll
               for (int pt = 0; pt < 4; ++pt) {
                 duT[h][pt] *= ek;
-                sx += dot4_bf16(duT[h][pt], *reinterpret_cast<const uint2*>(urow4 + 16 * pt));
+                sx += dot4_bf16(duT[h][pt], ux[pt]);
               }
               sx = group_sum(sv ? sx : 0.f) * dtk[h];
               if (lg == 0) xBc[k * hstride + sig] = sx;
@@ -548,7 +580,14 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     // the dCB of target strip Tp: park this pass' share, or (last pass) add
     // the parked shares, dB^T[n, sig] += sum_t C[t, n] dCB[t, sig] and store
     // the hi / lo planes
-    auto finish_pair = [&](int Tp, v4f (&dCBa)[4]) {
+    // (prev: the parked shares, loaded at the end of the stage before)
+    auto load_prev = [&](int Tp, float4 (&prev)[4]) {
+      if (last && NPASS > 1) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) prev[kt] = *reinterpret_cast<const float4*>(dcb_at(Tp, kt));
+      }
+    };
+    auto finish_pair = [&](int Tp, v4f (&dCBa)[4], const float4 (&prev)[4]) {
       if (!last) {
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
@@ -557,12 +596,9 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
       }
       if (NPASS > 1) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          const float4 o = *reinterpret_cast<const float4*>(dcb_at(Tp, kt));
-          dCBa[kt] += v4f{o.x, o.y, o.z, o.w};
-        }
+        for (int kt = 0; kt < 4; ++kt) dCBa[kt] += v4f{prev[kt].x, prev[kt].y, prev[kt].z, prev[kt].w};
       }
-      const bf16* Cb = Cs + (Tp & 1) * SM::kC;
+      const bf16* Cb = Cs(Tp & 1);
       const int ctb = tr_first<NK * 4, swz_k256>(8 * lg, 0, lane);   // column tile 0
       const int cfx = 16 * (swz_k256(8 * lg + ((lane & 15) >> 2)) >> 1);
 #pragma unroll
@@ -585,33 +621,44 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 
     // ---- pair stages: target strip T = S + Ti, head k = pass HS + h ----
     v4f dCBa[4];
+    float4 prev[4];
     for (int Ti = 0; Ti < ntile; ++Ti) {
       const int T = S + Ti, t0 = 64 * T;
-      const bf16* Cb = Cs + (T & 1) * SM::kC;
+      const bf16* Cb = Cs(T & 1);
       const bool diag = Ti == 0;
       const bool fact = !diag && mono;
       v4f CB[4];
 #pragma unroll
-      for (int h = 0; h < HS; ++h, ++jj) {
+      for (int h = 0; h < HS; ++h) {
         const int j = nst + Ti * HS + h;
         const int k = pass * HS + h;
         const bool kv = k < HPG;
-        // with one head per pass, the next stage brings the C tile of strip
-        // T + 1 into the buffer finish_pair(T - 1) reads: finish it first
-        if (HS == 1 && Ti > 0) {
-          finish_pair(T - 1, dCBa);
-          __syncthreads();
-        }
-        issue_next(pass, j, jj);
-        if (j > nst) flush_r(pass, j - 1, jj - 1);
-        if (HS > 1 && h == 0 && Ti > 0) finish_pair(T - 1, dCBa);
-        const bf16* Yh = stg + (jj & 1) * SM::kStage;
-        const bf16* Yl = Yh + kPlaneT;
+        const int par = HS == 1 ? (Ti & 1) : h;
+        // register loads of this stage, before the next stage's DMA
+        v8bf Bf[NK], uf[2];
         if (h == 0) {
-          v8bf Bf[NK];
           const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 8 * lg);
 #pragma unroll
           for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+        }
+        if (kv) {
+          const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+        }
+        __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the DMA
+        // with one head per pass, the next stage brings the C tile of strip
+        // T + 1 into the buffer finish_pair(T - 1) reads: finish it first
+        if (HS == 1 && Ti > 0) {
+          finish_pair(T - 1, dCBa, prev);
+          __syncthreads();
+        }
+        issue_next(pass, j, par);
+        if (j > nst) flush_r(pass, j - 1, par ^ 1);
+        if (HS > 1 && h == 0 && Ti > 0) finish_pair(T - 1, dCBa, prev);
+        const bf16* Yh = stg(par);
+        const bf16* Yl = Yh + kPlaneT;
+        if (h == 0) {
 #pragma unroll
           for (int kt = 0; kt < 4; ++kt) {
             CB[kt] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -625,12 +672,6 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
           const float* dcT = dcs + (T & 1) * HPG * 64 + 64 * k;
           const float* atT = ats + (T & 1) * HPG * 64 + 64 * k;
           const float dk = dck[h], dtv = dtk[h];
-          v8bf uf[2];
-          {
-            const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
-          }
           // W[t, sig] = dy[t] . u[sig]
           v4f W[4];
 #pragma unroll
@@ -687,7 +728,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
             }
           }
           qacc[h] += qs;
-          rx[(jj & 1) * 256 + w * 64 + key_of_row(li >> 2, 4 * lg + (li & 3))] =
+          rx[par * 256 + w * 64 + key_of_row(li >> 2, 4 * lg + (li & 3))] =
               transpose_reduce16(m, li);
           // du^T[p, sig] += sum_t dy[t, p] L[t, sig]  (L and dy as hi + lo)
 #pragma unroll
@@ -706,11 +747,13 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
             }
           }
         }
+        // the parked dCB shares of this strip, for finish_pair in the next stage
+        if (h == HS - 1) load_prev(T, prev);
         end_stage(pass, j + 1);
       }
     }
-    flush_r(pass, n_stage(pass) - 1, jj - 1);
-    finish_pair(S + ntile - 1, dCBa);
+    flush_r(pass, n_stage(pass) - 1, HS == 1 ? ((ntile - 1) & 1) : HS - 1);
+    finish_pair(S + ntile - 1, dCBa, prev);
 
     // ---- du, ddt_direct, q of this pass' heads ----
 #pragma unroll
@@ -976,10 +1019,8 @@ int launch_fused_hpg(const void* u, const void* B, const void* C, const bf16* dy
   constexpr int NK = 4;
   const long blocks = static_cast<long>(d.b) * d.nc * d.G * (d.Lc / 64);
   auto src_pass = [&](auto kernel) -> int {
-    const size_t smem = SrcSmem<NK, HPG>::bytes;
-    if (const int rc = raise_smem(kernel, smem, "ssd_bwd_src")) return rc;
     ProfScope prof_("ssd_bwd_src", s);
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), smem, s,
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), 0, s,
                        static_cast<const bf16*>(u), static_cast<const bf16*>(B),
                        static_cast<const bf16*>(C), dyp, dt, dc, dSp, length,
                        static_cast<bf16*>(du), static_cast<bf16*>(dB), dcbp, ddt_part, xB_part,
