@@ -34,6 +34,10 @@ HIP events on the launch stream); ms_per_step_mean is the bracketed total / K.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
                        [--ssd-only] [--legs decode,sparse,...] [--copy-probe-mib M]
+       python bench.py --pmc-summary run_counter_collection.csv [more.csv ...]
+                       [--pmc-kernels name,name]
+The second form reads rocprofv3 --pmc CSV files (no GPU) and prints, per
+kernel, each counter's mean per dispatch as a markdown table.
 """
 from __future__ import annotations
 
@@ -744,7 +748,67 @@ def cpu_baseline(torch, budget_s):
             }}
 
 
+# shader engines of an MI355X (8 XCDs x 4): SQ_BUSY_CYCLES sums over them, and
+# each has 32 SIMDs, so SIMD-cycles of a dispatch = 32 x SQ_BUSY_CYCLES
+MI355X_SIMDS_PER_SE = 32
+
+
+def pmc_summary(paths, kernels=None):
+    """Markdown table of rocprofv3 --pmc counters: per kernel (template
+    arguments kept, namespace dropped), the mean of each counter over its
+    dispatches; with the SQ counters present also per-wave instruction counts,
+    the share of wave-cycles spent waiting and the MFMA pipe's busy share of
+    all SIMD-cycles."""
+    import collections
+    import csv
+    import re
+    agg = collections.defaultdict(lambda: collections.defaultdict(list))
+    order = []
+    for path in paths:
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                name = r["Kernel_Name"]
+                m = re.search(r"(\w+_kernel)(<[^(]*>)?", name)
+                k = (m.group(1) + (m.group(2) or "")) if m else name[:60]
+                k = k.replace("sa::", "")
+                if "copyBuffer" in k or "elementwise" in k:   # one row per launch shape
+                    k += f" [grid {r.get('Grid_Size', '?')}]"
+                if kernels and not any(x in k for x in kernels):
+                    continue
+                if k not in agg:
+                    order.append(k)
+                agg[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    counters = sorted({c for k in order for c in agg[k]})
+    lines = ["| kernel | dispatches | " + " | ".join(counters) + " | derived |",
+             "|---|---:|" + "---:|" * len(counters) + "---|"]
+    for k in order:
+        mean = {c: sum(v) / len(v) for c, v in agg[k].items()}
+        n = max(len(v) for v in agg[k].values())
+        der = []
+        waves = mean.get("SQ_WAVES")
+        if waves:
+            for c, lab in (("SQ_INSTS_MFMA", "mfma/wave"), ("SQ_INSTS_VALU", "valu/wave"),
+                           ("SQ_INSTS_LDS", "lds/wave")):
+                if c in mean:
+                    der.append(f"{lab} {mean[c] / waves:.0f}")
+        if mean.get("SQ_WAVE_CYCLES") and "SQ_WAIT_ANY" in mean:
+            der.append(f"wait {mean['SQ_WAIT_ANY'] / mean['SQ_WAVE_CYCLES']:.0%} of wave-cycles")
+        if mean.get("SQ_BUSY_CYCLES") and "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
+            der.append(f"MFMA busy {mean['SQ_VALU_MFMA_BUSY_CYCLES'] / (MI355X_SIMDS_PER_SE * mean['SQ_BUSY_CYCLES']):.1%} of SIMD-cycles")
+        vals = " | ".join(f"{mean[c]:,.0f}" if c in mean else "" for c in counters)
+        lines.append(f"| `{k}` | {n} | {vals} | {'; '.join(der)} |")
+    return "\n".join(lines)
+
+
 def main():
+    if "--pmc-summary" in sys.argv:
+        ap = argparse.ArgumentParser()
+        ap.add_argument("--pmc-summary", nargs="+", required=True)
+        ap.add_argument("--pmc-kernels", default=None,
+                        help="comma-separated substrings; only kernels whose name holds one")
+        a = ap.parse_args()
+        print(pmc_summary(a.pmc_summary, a.pmc_kernels.split(",") if a.pmc_kernels else None))
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
