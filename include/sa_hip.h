@@ -193,6 +193,23 @@ int sa_mha_gates_bf16(const void* g, const float* thr, const float* score_std, f
                       long rows, int heads, int dim, float* log_gate, void* out_gate, void* stream);
 
 /*
+ * Per-head statistics of the valid attention scores s_ij = scale * q_i . k_j,
+ * for SelectiveMHA's training forward: out[h] = (count, sum, sum of squares)
+ * in fp64 over every batch row's valid pairs (query and key inside
+ * length[b], and key <= query when causal != 0), the score matrix never
+ * written.  Replaces the dense reduction of the reference's
+ * modules/selective_attention.py:234-246 (its std and running average stay
+ * with the caller).  q, k (batch, heads, seq_len, head_dim) contiguous, bf16
+ * (dtype 1) or fp32 (dtype 0), 16-byte aligned; head_dim 32, 64, 96 or 128;
+ * length (batch,) int64 or NULL (every row full); workspace of
+ * sa_score_stats_workspace_size(batch, heads, seq_len) bytes.  Deterministic.
+ */
+size_t sa_score_stats_workspace_size(int batch, int heads, int seq_len);
+int sa_score_stats(int dtype, const void* q, const void* k, const int64_t* length, int batch,
+                   int heads, int seq_len, int head_dim, int causal, float scale, void* workspace,
+                   size_t workspace_bytes, double* out, void* stream);
+
+/*
  * Small-batch linear layer of the decode steps (nn.Linear with x of at most 8
  * rows): y (M, N) = bf16(x (M, K) . W (N, K)^T + bias (N,)), bf16, fp32
  * accumulation; M in 1..8, K % 8 == 0, K <= 4096, x and W 16-byte aligned; bias may

@@ -194,3 +194,69 @@ def attn_varlen(q, k, v, cu_q, mode="causal", cu_k=None, key_bias=None, softmax_
             sc = sc.masked_fill(~allow, float("-inf"))
             o[a:b, h] = torch.softmax(sc, dim=-1) @ vf[ka:kb, h]
     return o
+
+
+def score_stats(q_rot, k_rot, scale, lengths=None, causal=True, dtype=torch.float64):
+    """Per-head (count, sum, sum of squares) of the valid attention scores,
+    SelectiveMHA's training statistics (modules/selective_attention.py:234-246):
+    s_ij = scale * q_i . k_j over pairs with i, j < length (when given) and
+    j <= i (causal).  q_rot, k_rot (batch, heads, seq_len, head_dim).
+    Returns (heads, 3) in `dtype`."""
+    q, k = q_rot.to(dtype), k_rot.to(dtype)
+    b, H, L, _ = q.shape
+    s = torch.matmul(q, k.transpose(-2, -1)) * scale
+    valid = torch.ones(b, 1, L, L, dtype=torch.bool)
+    if causal:
+        valid &= torch.tril(torch.ones(L, L, dtype=torch.bool))
+    if lengths is not None:
+        ok = torch.arange(L)[None, :] < lengths.to(torch.int64).cpu()[:, None]   # (b, L)
+        valid &= ok[:, None, :, None] & ok[:, None, None, :]
+    valid = valid.expand(b, H, L, L)
+    sv = torch.where(valid, s, torch.zeros_like(s))
+    return torch.stack([valid.sum(dim=(0, 2, 3)).to(dtype), sv.sum(dim=(0, 2, 3)),
+                        (sv * sv).sum(dim=(0, 2, 3))], dim=1)
+
+
+def score_std(stats):
+    """The reference's per-head std from (count, sum, sum of squares)
+    (:239-247): mean = sum / max(count, 1), var = sumsq / max(count, 1) -
+    mean^2, std = sqrt(max(var, 0))."""
+    cnt = stats[:, 0].clamp(min=1)
+    mean = stats[:, 1] / cnt
+    return (stats[:, 2] / cnt - mean * mean).clamp(min=0).sqrt()
+
+
+def selective_mha_train_attn(q_rot, k_rot, v, select_gate, penalty, lengths=None, causal=True,
+                             dtype=torch.float64):
+    """The attention of SelectiveMHA's training forward (:197-277), as the
+    reference composes it, in `dtype` and differentiable: scores scale * q.k
+    (-inf above the diagonal when causal), the per-head std of the valid
+    scores (through which gradients flow), log-gate = log(select_gate) * std
+    * penalty (-inf at padded keys), added to every score but the diagonal,
+    softmax over keys, times v.  q_rot, k_rot, v (batch, heads, seq_len,
+    head_dim); select_gate (batch, heads, seq_len).  Returns (out (batch,
+    heads, seq_len, head_dim), std (heads,))."""
+    q, k, vv, sg = (x.to(dtype) for x in (q_rot, k_rot, v, select_gate))
+    b, H, L, D = q.shape
+    scale = D ** -0.5
+    s = torch.matmul(q, k.transpose(-2, -1)) * scale
+    ninf = torch.tensor(float("-inf"), dtype=dtype)
+    if causal:
+        s = torch.where(torch.tril(torch.ones(L, L, dtype=torch.bool)), s, ninf)
+    valid = torch.isfinite(s)
+    pad = None
+    if lengths is not None:
+        ok = torch.arange(L)[None, :] < lengths.to(torch.int64).cpu()[:, None]
+        pad = ~ok
+        valid = valid & ok[:, None, :, None] & ok[:, None, None, :]
+    cnt = valid.sum(dim=(0, 2, 3)).to(dtype)
+    sv = torch.where(valid, s, torch.zeros((), dtype=dtype))
+    mean = sv.sum(dim=(0, 2, 3)) / cnt.clamp(min=1)
+    var = (sv * sv).sum(dim=(0, 2, 3)) / cnt.clamp(min=1) - mean * mean
+    std = var.clamp(min=0).sqrt()
+    lg = torch.log(sg) * std[None, :, None] * penalty
+    if pad is not None:
+        lg = lg.masked_fill(pad[:, None, :], float("-inf"))
+    diag = torch.eye(L, dtype=torch.bool)
+    s = torch.where(diag, s, s + lg[:, :, None, :])
+    return torch.softmax(s, dim=-1) @ vv, std

@@ -316,3 +316,40 @@ class Seq2SeqRef(LMRef):
             h = self.rnd(h + self.cross_step(self.norm(h, p + "norm3"), st["ckv"], p))
             h = self.rnd(h + self.ffn(self.norm(h, p + "norm4"), p))
         return self.lin(self.norm(h, "norm4"), "embedding", bias=False)
+
+
+def rope_rotate(x, pos, base=10000.0):
+    """The rotation of modules/rope.py on x (..., seq_len, D) at positions
+    pos (seq_len,), angles in fp32 as the module computes them, in the
+    dtype of x (differentiable in x)."""
+    D = x.shape[-1]
+    half = D // 2
+    inv = 1.0 / (base ** (torch.arange(0, half, dtype=torch.float32) / half))
+    ang = pos.to(torch.float32).unsqueeze(-1) * inv
+    ang = torch.cat([ang, ang], -1).to(x.dtype)
+    rot = torch.cat([-x[..., half:], x[..., :half]], -1)
+    return x * torch.cos(ang) + rot * torch.sin(ang)
+
+
+def selective_mha_train_forward(params, x, lengths, head_dim, penalty, causal=True):
+    """SelectiveMHA's training forward (modules/selective_attention.py:197-277)
+    in the dtype of x, differentiable in x and in params: gates =
+    sigmoid(gate_proj(x)) split into (heads, dim); q, k, v projections; RoPE
+    on q and k; the attention of attn.selective_mha_train_attn (the current
+    batch's score std in the log-gate); out_proj(out * out_gate).
+    params: gate_proj.weight/.bias, q_proj.weight, k_proj.weight,
+    v_proj.weight/.bias, out_proj.weight/.bias.  Returns (hidden (batch,
+    seq_len, dim), std (heads,))."""
+    b, L, dim = x.shape
+    H = dim // head_dim
+    g = torch.sigmoid(F.linear(x, params["gate_proj.weight"], params["gate_proj.bias"]))
+    sg, og = g[..., :H].transpose(1, 2), g[..., H:]
+    heads = lambda t: t.view(b, L, H, head_dim).transpose(1, 2)
+    q = heads(F.linear(x, params["q_proj.weight"]))
+    k = heads(F.linear(x, params["k_proj.weight"]))
+    v = heads(F.linear(x, params["v_proj.weight"], params["v_proj.bias"]))
+    pos = torch.arange(L)
+    out, std = attn.selective_mha_train_attn(rope_rotate(q, pos), rope_rotate(k, pos), v, sg,
+                                             penalty, lengths, causal, dtype=x.dtype)
+    out = out.transpose(1, 2).reshape(b, L, dim)
+    return F.linear(out * og, params["out_proj.weight"], params["out_proj.bias"]), std

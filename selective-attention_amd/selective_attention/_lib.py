@@ -50,6 +50,8 @@ SIGNATURES: dict[str, list] = {
     "sa_add_rms_norm_bf16": [_vp, _vp, _vp, _i64, _i, _f, _vp, _vp, _vp],
     "sa_mha_gates_bf16": [_vp, _vp, _vp, _f, _i64, _i, _i, _vp, _vp, _vp],
     "sa_silu_mul_bf16": [_vp, _vp, _i64, _vp, _vp],
+    "sa_score_stats_workspace_size": [_i, _i, _i],
+    "sa_score_stats": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp, _vp],
     "sa_gemv_bf16": [_vp, _vp, _vp, _i, _i, _i, _vp, _vp],
     "sa_gemv_bf16_multi": [_vp, _vp, _i, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                            ctypes.POINTER(_i), ctypes.POINTER(_vp), _vp],
@@ -75,7 +77,8 @@ RESTYPES = {"sa_last_error": ctypes.c_char_p, "sa_profile_enable": None, "sa_ssd
             "sa_paged_decode_workspace_size": ctypes.c_size_t,
             "sa_paged_decode_noalloc_limit": ctypes.c_size_t,
             "sa_ssm_conv_bwd_workspace_size": ctypes.c_size_t,
-            "sa_ssm_gate_bwd_workspace_size": ctypes.c_size_t}
+            "sa_ssm_gate_bwd_workspace_size": ctypes.c_size_t,
+            "sa_score_stats_workspace_size": ctypes.c_size_t}
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1

@@ -143,3 +143,39 @@ def paged_decode_attn(q, k_pages, v_pages, page_table, seq_lens, softmax_scale=N
               max_pages, num_pages, scale, _lib.ptr(o), _lib.ptr(ws), ws.numel(),
               _lib.stream_of(q))
     return o
+
+
+def score_stats(q_rot, k_rot, lengths=None, causal=True, softmax_scale=None):
+    """Per-head (count, sum, sum of squares) of the valid attention scores
+    scale * q.k, the statistics of SelectiveMHA's training forward
+    (modules/selective_attention.py:234-246), reduced in-kernel without
+    forming the score matrix.
+
+    Args:
+        q_rot, k_rot: (batch, heads, seq_len, head_dim) bfloat16 or float32;
+            head_dim 32, 64, 96 or 128
+        lengths: (batch,) or None; pairs with either position at or past a
+            row's length are left out
+        causal: leave out keys after the query
+    Returns:
+        (heads, 3) float64 on the device: count, sum, sum of squares
+    """
+    from .common import act_dtype_code
+    require_device(q_rot, k_rot, lengths)
+    if q_rot.dim() != 4 or q_rot.shape != k_rot.shape:
+        raise ValueError(f"score_stats: q {tuple(q_rot.shape)} and k {tuple(k_rot.shape)} must "
+                         "share a (batch, heads, seq_len, head_dim) shape")
+    if q_rot.dtype != k_rot.dtype:
+        raise ValueError("score_stats: q and k must share a dtype")
+    b, H, L, D = q_rot.shape
+    scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    code = act_dtype_code(q_rot.dtype)
+    q, k = q_rot.contiguous(), k_rot.contiguous()
+    lens = None if lengths is None else lengths.to(torch.int64).contiguous()
+    out = torch.empty((H, 3), dtype=torch.float64, device=q.device)
+    lib = _lib.load()
+    nbytes = lib.sa_score_stats_workspace_size(b, H, L)
+    ws = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=q.device)
+    _lib.call("sa_score_stats", code, _lib.ptr(q), _lib.ptr(k), _lib.ptr(lens), b, H, L, D,
+              1 if causal else 0, scale, _lib.ptr(ws), nbytes, _lib.ptr(out), _lib.stream_of(q))
+    return out

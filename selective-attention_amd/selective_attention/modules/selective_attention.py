@@ -1,5 +1,5 @@
-"""SelectiveMHA (modules/selective_attention.py:146-446), inference, on the
-gfx950 attention ops.
+"""SelectiveMHA (modules/selective_attention.py:146-446) on the gfx950
+attention ops.
 
 Parameters and interfaces follow the reference.  Prefill runs
 selective_mha_prefill (the block-sparse kernel over every causal block with
@@ -15,9 +15,12 @@ With is_causal=False (the encoder's BiBlock) every key of the sequence is
 visible, the query's own key again exempt (the reference's self column /
 self mask, :84-86); that variant has no decode step.
 
-The training forward (per-head score statistics and gradients through the
-attention) needs an attention backward kernel, which this package does not
-have: forward() in training mode raises NotImplementedError.
+Training (:197-277): the per-head std of the valid scores comes from the
+in-kernel statistics (ScoreStdFn: count, sum and sum of squares reduced
+without a score matrix, differentiable), score_std_ema takes the running
+average, the log-gate is log(gate) * std * penalty, and the gated softmax
+runs densely in torch under autograd (this package has no attention
+backward kernel).
 """
 from __future__ import annotations
 
@@ -26,7 +29,7 @@ import torch.nn as nn
 
 from ..kernels.lm_ops import mha_gates
 from ..ops.attention import attn_varlen
-from ..ops.selective_mha import selective_mha_prefill
+from ..ops.selective_mha import ScoreStdFn, gated_attention_train, selective_mha_prefill
 from .layers import Linear, RoPE, project
 
 
@@ -85,9 +88,7 @@ class SelectiveMHA(nn.Module):
             hidden_states: (batch_size, seq_len, dim)
         """
         if self.training:
-            raise NotImplementedError(
-                "SelectiveMHA: the training forward needs an attention backward kernel, "
-                "which is not built; use eval() for inference")
+            return self._train_forward(hidden_states, lengths)
         b, L, _ = hidden_states.shape
         dev = hidden_states.device
         H, D = self.num_heads, self.head_dim
@@ -117,6 +118,32 @@ class SelectiveMHA(nn.Module):
         else:
             out = self._bidirectional(q, k, vh, log_gate, lengths)
         return self.out_proj(out.to(hidden_states.dtype) * out_gate)
+
+    def _train_forward(self, hidden_states, lengths):
+        """The reference's training forward (:197-277): no threshold, the
+        current batch's score std in the log-gate (its gradient included),
+        padded keys at -inf, the diagonal exempt."""
+        b, L, _ = hidden_states.shape
+        dev = hidden_states.device
+        H, D = self.num_heads, self.head_dim
+        select_gate, out_gate = self._gates(hidden_states)
+        select_gate = select_gate.transpose(1, 2)                     # (b, H, L)
+        v = self.v_proj(hidden_states)
+        q = self.q_proj(hidden_states).view(b, L, H, D).transpose(1, 2)
+        k = self.k_proj(hidden_states).view(b, L, H, D).transpose(1, 2)
+        vh = v.view(b, L, H, D).transpose(1, 2)
+        q_rot, k_rot = self.rope(q, k, torch.arange(L, device=dev), mode="seq")
+        lens = None if lengths is None else lengths.to(dev)
+        std = ScoreStdFn.apply(q_rot.contiguous(), k_rot.contiguous(), lens, self.is_causal)
+        with torch.no_grad():
+            self.score_std_ema.mul_(0.9).add_(std.detach().to(self.score_std_ema.dtype), alpha=0.1)
+        log_gate = torch.log(select_gate.float()) * std[None, :, None] * self.log_gate_penalty
+        if lens is not None:
+            pad = torch.arange(L, device=dev)[None, :] >= lens[:, None]
+            log_gate = log_gate.masked_fill(pad[:, None, :], float("-inf"))
+        out = gated_attention_train(q_rot, k_rot, vh, log_gate, self.is_causal)
+        out = out.transpose(1, 2).reshape(b, L, self.dim).to(hidden_states.dtype)
+        return self.out_proj(out * out_gate)
 
     def _bidirectional(self, q, k, v, log_gate, lengths):
         """Every key of the row (dropped and padded ones at -inf), the query's

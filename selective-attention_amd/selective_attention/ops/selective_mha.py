@@ -21,15 +21,94 @@ ops:
   mode "pos").  Compaction becomes a page-table rewrite: drop_evicted_pages
   removes pages whose keys every head has dropped, without moving data.
 
-Training (the per-head score statistics and gradients through the
-attention) is not covered: there is no attention backward kernel here.
+* ScoreStdFn: the per-head std of the valid scores that SelectiveMHA's
+  training forward scales the log-gate by (:234-247).  Its forward is the
+  in-kernel reduction score_stats (count, sum, sum of squares, no score
+  matrix); its backward carries d std_h / d s_ij = (s_ij - mean_h) /
+  (count_h std_h) to q and k by query chunks.
+* gated_attention_train: the training attention itself, the reference's
+  dense gated softmax under autograd (there is no attention backward kernel
+  here), in fp32.
 """
 from __future__ import annotations
 
 import torch
 
+from ..kernels.attention import score_stats
 from ..kernels.lm_ops import paged_kv_append, paged_kv_build
 from .attention import attn_varlen, paged_decode_attn
+
+
+def _valid_pairs(L: int, lengths, causal: bool, i0: int, i1: int, device):
+    """(batch or 1, 1, i1 - i0, L) mask of the valid (query, key) pairs for
+    queries i0..i1-1: key <= query when causal, both inside the row length."""
+    qi = torch.arange(i0, i1, device=device)[:, None]
+    kj = torch.arange(L, device=device)[None, :]
+    m = (kj <= qi) if causal else torch.ones(i1 - i0, L, dtype=torch.bool, device=device)
+    m = m[None, None]
+    if lengths is not None:
+        lens = lengths.to(device=device, dtype=torch.int64)[:, None, None, None]
+        m = m & (qi[None, None] < lens) & (kj[None, None] < lens)
+    return m
+
+
+class ScoreStdFn(torch.autograd.Function):
+    """std_h of the valid scores s_ij = scale q_i . k_j of head h over every
+    batch row (modules/selective_attention.py:234-247: mean = sum / count,
+    var = sumsq / count - mean^2 clamped at 0, std = sqrt(var)), differentiable
+    in q and k.
+
+    forward(q_rot, k_rot, lengths, causal, chunk): q_rot, k_rot (batch,
+    heads, seq_len, head_dim); returns (heads,) float32.  A head whose std
+    is 0 passes no gradient back (the reference's sqrt would give inf * 0).
+    """
+
+    @staticmethod
+    def forward(ctx, q_rot, k_rot, lengths=None, causal=True, chunk=256):
+        st = score_stats(q_rot, k_rot, lengths, causal)
+        cnt = st[:, 0].clamp(min=1)
+        mean = st[:, 1] / cnt
+        std = (st[:, 2] / cnt - mean * mean).clamp(min=0).sqrt()
+        ctx.save_for_backward(q_rot, k_rot, mean, std, cnt)
+        ctx.lengths, ctx.causal, ctx.chunk = lengths, causal, chunk
+        return std.to(torch.float32)
+
+    @staticmethod
+    def backward(ctx, g):
+        q, k, mean, std, cnt = ctx.saved_tensors
+        b, H, L, D = q.shape
+        scale = D ** -0.5
+        coef = torch.where(std > 0, g.double() / (cnt * std.clamp(min=1e-300)),
+                           torch.zeros_like(std)).float()[None, :, None, None]
+        mu = mean.float()[None, :, None, None]
+        kf = k.float()
+        dq = torch.zeros(q.shape, dtype=torch.float32, device=q.device)
+        dk = torch.zeros(k.shape, dtype=torch.float32, device=k.device)
+        for i0 in range(0, L, ctx.chunk):
+            i1 = min(L, i0 + ctx.chunk)
+            qc = q[:, :, i0:i1].float()
+            s = torch.matmul(qc, kf.transpose(-2, -1).contiguous()) * scale
+            gs = torch.where(_valid_pairs(L, ctx.lengths, ctx.causal, i0, i1, q.device),
+                             (s - mu) * coef, torch.zeros((), device=q.device))
+            dq[:, :, i0:i1] = torch.matmul(gs, kf) * scale
+            dk += torch.matmul(gs.transpose(-2, -1).contiguous(), qc) * scale
+        return dq.to(q.dtype), dk.to(k.dtype), None, None, None
+
+
+def gated_attention_train(q_rot, k_rot, v, log_gate, causal=True):
+    """SelectiveMHA's training attention (modules/selective_attention.py:86-95,
+    125-144): softmax_j(scale q_i . k_j + [j != i] log_gate_j) v_j with keys
+    after the query at -inf when causal; dense, in fp32, under autograd.
+    q_rot, k_rot, v (batch, heads, seq_len, head_dim); log_gate (batch,
+    heads, seq_len).  Returns (batch, heads, seq_len, head_dim) float32."""
+    L, D = q_rot.shape[-2], q_rot.shape[-1]
+    s = torch.matmul(q_rot.float(), k_rot.float().transpose(-2, -1).contiguous()) * D ** -0.5
+    diag = torch.eye(L, dtype=torch.bool, device=s.device)
+    s = torch.where(diag, s, s + log_gate.float()[:, :, None, :])
+    if causal:
+        s = s.masked_fill(~torch.tril(torch.ones(L, L, dtype=torch.bool, device=s.device)),
+                          float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), v.float())
 
 
 def selective_mha_prefill(q_rot: torch.Tensor, k_rot: torch.Tensor, v: torch.Tensor,
