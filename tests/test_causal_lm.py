@@ -109,7 +109,8 @@ def test_causal_lm_interfaces_cpu():
     m = CausalLM(cfg)
     assert m.lm_head.weight is m.embedding.weight
     assert len(m.layers) == cfg.num_layers
-    with pytest.raises(NotImplementedError):
+    # training runs the score statistics kernel: no CPU path, a loud error
+    with pytest.raises(ValueError, match="device tensors"):
         m.layers[0].mha.train()(torch.zeros(1, 4, cfg.model_dim))
     from selective_attention.models import config4
     c4 = config4(device="cpu")
