@@ -194,20 +194,25 @@ int sa_mha_gates_bf16(const void* g, const float* thr, const float* score_std, f
 
 /*
  * Per-head statistics of the valid attention scores s_ij = scale * q_i . k_j,
- * for SelectiveMHA's training forward: out[h] = (count, sum, sum of squares)
- * in fp64 over every batch row's valid pairs (query and key inside
- * length[b], and key <= query when causal != 0), the score matrix never
- * written.  Replaces the dense reduction of the reference's
- * modules/selective_attention.py:234-246 (its std and running average stay
- * with the caller).  q, k (batch, heads, seq_len, head_dim) contiguous, bf16
- * (dtype 1) or fp32 (dtype 0), 16-byte aligned; head_dim 32, 64, 96 or 128;
- * length (batch,) int64 or NULL (every row full); workspace of
- * sa_score_stats_workspace_size(batch, heads, seq_len) bytes.  Deterministic.
+ * for the training forwards of SelectiveMHA and CrossSelectiveMHA:
+ * out[h] = (count, sum, sum of squares) in fp64 over every batch row's valid
+ * pairs (query i < q_length[b], key j < k_length[b], and j <= i when
+ * causal != 0), the score matrix never written.  Replaces the dense
+ * reductions of the reference's modules/selective_attention.py:234-246
+ * (q_length = k_length = the row lengths) and
+ * modules/cross_selective_attention.py:129-146 (q_length NULL, k_length the
+ * context lengths); the std and running average stay with the caller.
+ * q (batch, heads, q_len, head_dim), k (batch, heads, k_len, head_dim)
+ * contiguous, bf16 (dtype 1) or fp32 (dtype 0), 16-byte aligned; head_dim
+ * 32, 64, 96 or 128; a NULL length means every position; causal needs
+ * q_len == k_len; workspace of sa_score_stats_workspace_size(batch, heads,
+ * q_len) bytes.  Deterministic.
  */
-size_t sa_score_stats_workspace_size(int batch, int heads, int seq_len);
-int sa_score_stats(int dtype, const void* q, const void* k, const int64_t* length, int batch,
-                   int heads, int seq_len, int head_dim, int causal, float scale, void* workspace,
-                   size_t workspace_bytes, double* out, void* stream);
+size_t sa_score_stats_workspace_size(int batch, int heads, int q_len);
+int sa_score_stats(int dtype, const void* q, const void* k, const int64_t* q_length,
+                   const int64_t* k_length, int batch, int heads, int q_len, int k_len,
+                   int head_dim, int causal, float scale, void* workspace, size_t workspace_bytes,
+                   double* out, void* stream);
 
 /*
  * Small-batch linear layer of the decode steps (nn.Linear with x of at most 8

@@ -196,22 +196,25 @@ def attn_varlen(q, k, v, cu_q, mode="causal", cu_k=None, key_bias=None, softmax_
     return o
 
 
-def score_stats(q_rot, k_rot, scale, lengths=None, causal=True, dtype=torch.float64):
+def score_stats(q, k, scale, q_lengths=None, k_lengths=None, causal=True, dtype=torch.float64):
     """Per-head (count, sum, sum of squares) of the valid attention scores,
-    SelectiveMHA's training statistics (modules/selective_attention.py:234-246):
-    s_ij = scale * q_i . k_j over pairs with i, j < length (when given) and
-    j <= i (causal).  q_rot, k_rot (batch, heads, seq_len, head_dim).
-    Returns (heads, 3) in `dtype`."""
-    q, k = q_rot.to(dtype), k_rot.to(dtype)
-    b, H, L, _ = q.shape
+    the training statistics of SelectiveMHA (modules/selective_attention.py:234-246)
+    and CrossSelectiveMHA (cross_selective_attention.py:129-146):
+    s_ij = scale * q_i . k_j over pairs with i < q_length, j < k_length (when
+    given) and j <= i (causal).  q (batch, heads, q_len, head_dim), k (batch,
+    heads, k_len, head_dim).  Returns (heads, 3) in `dtype`."""
+    q, k = q.to(dtype), k.to(dtype)
+    b, H, Lq, _ = q.shape
+    Lk = k.shape[2]
     s = torch.matmul(q, k.transpose(-2, -1)) * scale
-    valid = torch.ones(b, 1, L, L, dtype=torch.bool)
+    valid = torch.ones(b, 1, Lq, Lk, dtype=torch.bool)
     if causal:
-        valid &= torch.tril(torch.ones(L, L, dtype=torch.bool))
-    if lengths is not None:
-        ok = torch.arange(L)[None, :] < lengths.to(torch.int64).cpu()[:, None]   # (b, L)
-        valid &= ok[:, None, :, None] & ok[:, None, None, :]
-    valid = valid.expand(b, H, L, L)
+        valid &= torch.tril(torch.ones(Lq, Lk, dtype=torch.bool))
+    if q_lengths is not None:
+        valid &= (torch.arange(Lq)[None, :] < q_lengths.to(torch.int64).cpu()[:, None])[:, None, :, None]
+    if k_lengths is not None:
+        valid &= (torch.arange(Lk)[None, :] < k_lengths.to(torch.int64).cpu()[:, None])[:, None, None, :]
+    valid = valid.expand(b, H, Lq, Lk)
     sv = torch.where(valid, s, torch.zeros_like(s))
     return torch.stack([valid.sum(dim=(0, 2, 3)).to(dtype), sv.sum(dim=(0, 2, 3)),
                         (sv * sv).sum(dim=(0, 2, 3))], dim=1)

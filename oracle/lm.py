@@ -353,3 +353,36 @@ def selective_mha_train_forward(params, x, lengths, head_dim, penalty, causal=Tr
                                              penalty, lengths, causal, dtype=x.dtype)
     out = out.transpose(1, 2).reshape(b, L, dim)
     return F.linear(out * og, params["out_proj.weight"], params["out_proj.bias"]), std
+
+
+def cross_mha_train_forward(params, x, ctx, ctx_lengths, head_dim, penalty):
+    """CrossSelectiveMHA's training forward (modules/cross_selective_attention.py:88-161)
+    in the dtype of x, differentiable in x, ctx and params: gate =
+    sigmoid(select_gate_proj(ctx)); scores scale * q.k with keys past the
+    context length at -inf; the per-head std of the finite scores; log-gate =
+    log(gate) * std * penalty added to every key but key 0; softmax; times v;
+    out_proj.  params: q_proj.weight, k_proj.weight, v_proj.weight/.bias,
+    out_proj.weight/.bias, select_gate_proj.weight/.bias.  Returns (hidden
+    (batch, q_len, dim), std (heads,))."""
+    b, L, dim = x.shape
+    Lc = ctx.shape[1]
+    H = dim // head_dim
+    heads = lambda t, n: t.view(b, n, H, head_dim).transpose(1, 2)
+    sg = torch.sigmoid(F.linear(ctx, params["select_gate_proj.weight"],
+                                params["select_gate_proj.bias"])).transpose(1, 2)
+    q = heads(F.linear(x, params["q_proj.weight"]), L)
+    k = heads(F.linear(ctx, params["k_proj.weight"]), Lc)
+    v = heads(F.linear(ctx, params["v_proj.weight"], params["v_proj.bias"]), Lc)
+    s = torch.matmul(q, k.transpose(-2, -1)) * head_dim ** -0.5
+    if ctx_lengths is not None:
+        pad = torch.arange(Lc)[None, :] >= ctx_lengths.to(torch.int64).cpu()[:, None]
+        s = s.masked_fill(pad[:, None, None, :], float("-inf"))
+    valid = torch.isfinite(s)
+    cnt = valid.sum(dim=(0, 2, 3)).to(x.dtype).clamp(min=1)
+    sv = torch.where(valid, s, torch.zeros((), dtype=x.dtype))
+    mean = sv.sum(dim=(0, 2, 3)) / cnt
+    std = ((sv * sv).sum(dim=(0, 2, 3)) / cnt - mean * mean).clamp(min=0).sqrt()
+    lg = torch.log(sg) * std[None, :, None] * penalty
+    s = torch.cat([s[..., :1], s[..., 1:] + lg[:, :, None, 1:]], dim=-1)
+    out = (torch.softmax(s, dim=-1) @ v).transpose(1, 2).reshape(b, L, dim)
+    return F.linear(out, params["out_proj.weight"], params["out_proj.bias"]), std

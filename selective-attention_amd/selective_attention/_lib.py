@@ -51,7 +51,7 @@ SIGNATURES: dict[str, list] = {
     "sa_mha_gates_bf16": [_vp, _vp, _vp, _f, _i64, _i, _i, _vp, _vp, _vp],
     "sa_silu_mul_bf16": [_vp, _vp, _i64, _vp, _vp],
     "sa_score_stats_workspace_size": [_i, _i, _i],
-    "sa_score_stats": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp, _vp],
+    "sa_score_stats": [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp, _vp],
     "sa_gemv_bf16": [_vp, _vp, _vp, _i, _i, _i, _vp, _vp],
     "sa_gemv_bf16_multi": [_vp, _vp, _i, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                            ctypes.POINTER(_i), ctypes.POINTER(_vp), _vp],

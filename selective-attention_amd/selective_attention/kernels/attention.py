@@ -145,37 +145,43 @@ def paged_decode_attn(q, k_pages, v_pages, page_table, seq_lens, softmax_scale=N
     return o
 
 
-def score_stats(q_rot, k_rot, lengths=None, causal=True, softmax_scale=None):
+def score_stats(q, k, q_lengths=None, k_lengths=None, causal=True, softmax_scale=None):
     """Per-head (count, sum, sum of squares) of the valid attention scores
-    scale * q.k, the statistics of SelectiveMHA's training forward
-    (modules/selective_attention.py:234-246), reduced in-kernel without
+    scale * q.k, the statistics of the training forwards of SelectiveMHA
+    (modules/selective_attention.py:234-246) and CrossSelectiveMHA
+    (modules/cross_selective_attention.py:129-146), reduced in-kernel without
     forming the score matrix.
 
     Args:
-        q_rot, k_rot: (batch, heads, seq_len, head_dim) bfloat16 or float32;
-            head_dim 32, 64, 96 or 128
-        lengths: (batch,) or None; pairs with either position at or past a
-            row's length are left out
-        causal: leave out keys after the query
+        q: (batch, heads, q_len, head_dim), k: (batch, heads, k_len, head_dim),
+            bfloat16 or float32; head_dim 32, 64, 96 or 128
+        q_lengths, k_lengths: (batch,) or None; queries / keys at or past a
+            row's length are left out (None: every position)
+        causal: leave out keys after the query (q_len == k_len)
     Returns:
         (heads, 3) float64 on the device: count, sum, sum of squares
     """
     from .common import act_dtype_code
-    require_device(q_rot, k_rot, lengths)
-    if q_rot.dim() != 4 or q_rot.shape != k_rot.shape:
-        raise ValueError(f"score_stats: q {tuple(q_rot.shape)} and k {tuple(k_rot.shape)} must "
-                         "share a (batch, heads, seq_len, head_dim) shape")
-    if q_rot.dtype != k_rot.dtype:
+    require_device(q, k, q_lengths, k_lengths)
+    if q.dim() != 4 or k.dim() != 4 or q.shape[:2] != k.shape[:2] or q.shape[3] != k.shape[3]:
+        raise ValueError(f"score_stats: q {tuple(q.shape)} and k {tuple(k.shape)} must be "
+                         "(batch, heads, len, head_dim) with matching batch, heads, head_dim")
+    if q.dtype != k.dtype:
         raise ValueError("score_stats: q and k must share a dtype")
-    b, H, L, D = q_rot.shape
+    b, H, Lq, D = q.shape
+    Lk = k.shape[2]
+    if causal and Lq != Lk:
+        raise ValueError("score_stats: causal attention needs as many queries as keys")
     scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
-    code = act_dtype_code(q_rot.dtype)
-    q, k = q_rot.contiguous(), k_rot.contiguous()
-    lens = None if lengths is None else lengths.to(torch.int64).contiguous()
+    code = act_dtype_code(q.dtype)
+    q, k = q.contiguous(), k.contiguous()
+    ql = None if q_lengths is None else q_lengths.to(torch.int64).contiguous()
+    kl = None if k_lengths is None else k_lengths.to(torch.int64).contiguous()
     out = torch.empty((H, 3), dtype=torch.float64, device=q.device)
     lib = _lib.load()
-    nbytes = lib.sa_score_stats_workspace_size(b, H, L)
+    nbytes = lib.sa_score_stats_workspace_size(b, H, Lq)
     ws = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=q.device)
-    _lib.call("sa_score_stats", code, _lib.ptr(q), _lib.ptr(k), _lib.ptr(lens), b, H, L, D,
-              1 if causal else 0, scale, _lib.ptr(ws), nbytes, _lib.ptr(out), _lib.stream_of(q))
+    _lib.call("sa_score_stats", code, _lib.ptr(q), _lib.ptr(k), _lib.ptr(ql), _lib.ptr(kl), b, H,
+              Lq, Lk, D, 1 if causal else 0, scale, _lib.ptr(ws), nbytes, _lib.ptr(out),
+              _lib.stream_of(q))
     return out

@@ -1,5 +1,5 @@
-"""CrossSelectiveMHA (modules/cross_selective_attention.py:35-258), inference,
-on the cross mode of the attention kernel.
+"""CrossSelectiveMHA (modules/cross_selective_attention.py:35-258) on the
+cross mode of the attention kernel.
 
 Decoder queries attend every key of their row's context, each key with
 log(gate) * score_std_ema * penalty as its bias, except the context's key 0,
@@ -10,8 +10,11 @@ dropped (:102-118: the reference compresses them away; here they carry bias
 neither does this module.  The context keys, values and biases are kept in
 the cache for the decode steps, as pages for the split-KV paged decode
 kernel (one query per row over the whole context spreads over every CU).
-No RoPE, as in the reference.  Training raises NotImplementedError (no
-attention backward kernel).
+No RoPE, as in the reference.  Training (:88-161): the per-head std of the
+valid scores (every query, keys inside the context length) comes from the
+in-kernel statistics (ScoreStdFn), score_std_ema takes the running average,
+and the gated softmax (key 0 unbiased, padded keys at -inf) runs densely in
+torch under autograd (no attention backward kernel here).
 """
 from __future__ import annotations
 
@@ -19,6 +22,7 @@ import torch
 import torch.nn as nn
 
 from ..ops.attention import attn_varlen, paged_decode_attn
+from ..ops.selective_mha import ScoreStdFn, cross_attention_train
 from .layers import Linear
 from .selective_attention import _threshold
 
@@ -76,9 +80,7 @@ class CrossSelectiveMHA(nn.Module):
             hidden_states: (batch_size, seq_len, dim)
         """
         if self.training:
-            raise NotImplementedError(
-                "CrossSelectiveMHA: the training forward needs an attention backward kernel, "
-                "which is not built; use eval() for inference")
+            return self._train_forward(hidden_states, context, context_lengths)
         b, L, _ = hidden_states.shape
         H, D = self.num_heads, self.head_dim
         k, v, bias, cu_k = self._context(context, context_lengths, attn_gate_threshold,
@@ -90,6 +92,25 @@ class CrossSelectiveMHA(nn.Module):
             cache.k, cache.v, cache.key_bias, cache.cu_k = k, v, bias, cu_k
             cache.pages = self._pages(k, v, bias, b, context.shape[1])
         return self.out_proj(out.view(b, L, self.dim).to(hidden_states.dtype))
+
+    def _train_forward(self, hidden_states, context, context_lengths):
+        """The reference's training forward (:88-161): the current batch's
+        score std in the log-gate (its gradient included), no threshold."""
+        b, L, _ = hidden_states.shape
+        Lc = context.shape[1]
+        dev = hidden_states.device
+        H, D = self.num_heads, self.head_dim
+        gate = torch.sigmoid(self.select_gate_proj(context)).transpose(1, 2)   # (b, H, Lc)
+        q = self.q_proj(hidden_states).view(b, L, H, D).transpose(1, 2)
+        k = self.k_proj(context).view(b, Lc, H, D).transpose(1, 2)
+        v = self.v_proj(context).view(b, Lc, H, D).transpose(1, 2)
+        lens = None if context_lengths is None else context_lengths.to(dev)
+        std = ScoreStdFn.apply(q.contiguous(), k.contiguous(), None, lens, False)
+        with torch.no_grad():
+            self.score_std_ema.mul_(0.9).add_(std.detach().to(self.score_std_ema.dtype), alpha=0.1)
+        log_gate = torch.log(gate.float()) * std[None, :, None] * self.log_gate_penalty
+        out = cross_attention_train(q, k, v, log_gate, lens)
+        return self.out_proj(out.transpose(1, 2).reshape(b, L, self.dim).to(hidden_states.dtype))
 
     def _pages(self, k, v, bias, b, Lc, ps=64):
         """The context as decode pages for the stream-K paged kernel: per row,

@@ -134,7 +134,7 @@ class SelectiveMHA(nn.Module):
         vh = v.view(b, L, H, D).transpose(1, 2)
         q_rot, k_rot = self.rope(q, k, torch.arange(L, device=dev), mode="seq")
         lens = None if lengths is None else lengths.to(dev)
-        std = ScoreStdFn.apply(q_rot.contiguous(), k_rot.contiguous(), lens, self.is_causal)
+        std = ScoreStdFn.apply(q_rot.contiguous(), k_rot.contiguous(), lens, lens, self.is_causal)
         with torch.no_grad():
             self.score_std_ema.mul_(0.9).add_(std.detach().to(self.score_std_ema.dtype), alpha=0.1)
         log_gate = torch.log(select_gate.float()) * std[None, :, None] * self.log_gate_penalty

@@ -26,9 +26,9 @@ ops:
   in-kernel reduction score_stats (count, sum, sum of squares, no score
   matrix); its backward carries d std_h / d s_ij = (s_ij - mean_h) /
   (count_h std_h) to q and k by query chunks.
-* gated_attention_train: the training attention itself, the reference's
-  dense gated softmax under autograd (there is no attention backward kernel
-  here), in fp32.
+* gated_attention_train, cross_attention_train: the training attention
+  itself, the reference's dense gated softmax under autograd (there is no
+  attention backward kernel here), in fp32.
 """
 from __future__ import annotations
 
@@ -39,44 +39,48 @@ from ..kernels.lm_ops import paged_kv_append, paged_kv_build
 from .attention import attn_varlen, paged_decode_attn
 
 
-def _valid_pairs(L: int, lengths, causal: bool, i0: int, i1: int, device):
-    """(batch or 1, 1, i1 - i0, L) mask of the valid (query, key) pairs for
-    queries i0..i1-1: key <= query when causal, both inside the row length."""
+def _valid_pairs(Lk: int, q_lengths, k_lengths, causal: bool, i0: int, i1: int, device):
+    """(batch or 1, 1, i1 - i0, Lk) mask of the valid (query, key) pairs for
+    queries i0..i1-1: key <= query when causal, query and key inside their
+    row lengths (None: every position)."""
     qi = torch.arange(i0, i1, device=device)[:, None]
-    kj = torch.arange(L, device=device)[None, :]
-    m = (kj <= qi) if causal else torch.ones(i1 - i0, L, dtype=torch.bool, device=device)
+    kj = torch.arange(Lk, device=device)[None, :]
+    m = (kj <= qi) if causal else torch.ones(i1 - i0, Lk, dtype=torch.bool, device=device)
     m = m[None, None]
-    if lengths is not None:
-        lens = lengths.to(device=device, dtype=torch.int64)[:, None, None, None]
-        m = m & (qi[None, None] < lens) & (kj[None, None] < lens)
+    if q_lengths is not None:
+        m = m & (qi[None, None] < q_lengths.to(device=device, dtype=torch.int64)[:, None, None, None])
+    if k_lengths is not None:
+        m = m & (kj[None, None] < k_lengths.to(device=device, dtype=torch.int64)[:, None, None, None])
     return m
 
 
 class ScoreStdFn(torch.autograd.Function):
     """std_h of the valid scores s_ij = scale q_i . k_j of head h over every
-    batch row (modules/selective_attention.py:234-247: mean = sum / count,
-    var = sumsq / count - mean^2 clamped at 0, std = sqrt(var)), differentiable
-    in q and k.
+    batch row (modules/selective_attention.py:234-247,
+    cross_selective_attention.py:129-146: mean = sum / count, var = sumsq /
+    count - mean^2 clamped at 0, std = sqrt(var)), differentiable in q and k.
 
-    forward(q_rot, k_rot, lengths, causal, chunk): q_rot, k_rot (batch,
-    heads, seq_len, head_dim); returns (heads,) float32.  A head whose std
-    is 0 passes no gradient back (the reference's sqrt would give inf * 0).
+    forward(q, k, q_lengths, k_lengths, causal, chunk): q (batch, heads,
+    q_len, head_dim), k (batch, heads, k_len, head_dim); returns (heads,)
+    float32.  A head whose std is 0 passes no gradient back (the reference's
+    sqrt would give inf * 0).
     """
 
     @staticmethod
-    def forward(ctx, q_rot, k_rot, lengths=None, causal=True, chunk=256):
-        st = score_stats(q_rot, k_rot, lengths, causal)
+    def forward(ctx, q, k, q_lengths=None, k_lengths=None, causal=True, chunk=256):
+        st = score_stats(q, k, q_lengths, k_lengths, causal)
         cnt = st[:, 0].clamp(min=1)
         mean = st[:, 1] / cnt
         std = (st[:, 2] / cnt - mean * mean).clamp(min=0).sqrt()
-        ctx.save_for_backward(q_rot, k_rot, mean, std, cnt)
-        ctx.lengths, ctx.causal, ctx.chunk = lengths, causal, chunk
+        ctx.save_for_backward(q, k, mean, std, cnt)
+        ctx.q_lengths, ctx.k_lengths, ctx.causal, ctx.chunk = q_lengths, k_lengths, causal, chunk
         return std.to(torch.float32)
 
     @staticmethod
     def backward(ctx, g):
         q, k, mean, std, cnt = ctx.saved_tensors
-        b, H, L, D = q.shape
+        Lq, D = q.shape[2], q.shape[3]
+        Lk = k.shape[2]
         scale = D ** -0.5
         coef = torch.where(std > 0, g.double() / (cnt * std.clamp(min=1e-300)),
                            torch.zeros_like(std)).float()[None, :, None, None]
@@ -84,15 +88,15 @@ class ScoreStdFn(torch.autograd.Function):
         kf = k.float()
         dq = torch.zeros(q.shape, dtype=torch.float32, device=q.device)
         dk = torch.zeros(k.shape, dtype=torch.float32, device=k.device)
-        for i0 in range(0, L, ctx.chunk):
-            i1 = min(L, i0 + ctx.chunk)
+        for i0 in range(0, Lq, ctx.chunk):
+            i1 = min(Lq, i0 + ctx.chunk)
             qc = q[:, :, i0:i1].float()
             s = torch.matmul(qc, kf.transpose(-2, -1).contiguous()) * scale
-            gs = torch.where(_valid_pairs(L, ctx.lengths, ctx.causal, i0, i1, q.device),
-                             (s - mu) * coef, torch.zeros((), device=q.device))
+            valid = _valid_pairs(Lk, ctx.q_lengths, ctx.k_lengths, ctx.causal, i0, i1, q.device)
+            gs = torch.where(valid, (s - mu) * coef, torch.zeros((), device=q.device))
             dq[:, :, i0:i1] = torch.matmul(gs, kf) * scale
             dk += torch.matmul(gs.transpose(-2, -1).contiguous(), qc) * scale
-        return dq.to(q.dtype), dk.to(k.dtype), None, None, None
+        return dq.to(q.dtype), dk.to(k.dtype), None, None, None, None
 
 
 def gated_attention_train(q_rot, k_rot, v, log_gate, causal=True):
@@ -392,3 +396,21 @@ class PagedSelectiveAttnCache:
         if freed:
             self._pt_dirty = self._sl_dirty = True
         return freed
+
+
+def cross_attention_train(q, k, v, log_gate, k_lengths=None):
+    """CrossSelectiveMHA's training attention (modules/cross_selective_attention.py:129-159):
+    softmax_j(scale q_i . k_j + [j > 0] log_gate_j) v_j over the context keys,
+    keys at or past a row's context length at -inf; dense, in fp32, under
+    autograd.  q (batch, heads, q_len, head_dim); k, v (batch, heads,
+    k_len, head_dim); log_gate (batch, heads, k_len).  Returns (batch, heads,
+    q_len, head_dim) float32."""
+    Lk, D = k.shape[2], k.shape[3]
+    s = torch.matmul(q.float(), k.float().transpose(-2, -1).contiguous()) * D ** -0.5
+    if k_lengths is not None:
+        pad = torch.arange(Lk, device=s.device)[None, :] >= k_lengths.to(s.device)[:, None]
+        s = s.masked_fill(pad[:, None, None, :], float("-inf"))
+    bias = log_gate.float().clone()
+    bias[..., 0] = 0.0
+    s = s + bias[:, :, None, :]
+    return torch.matmul(torch.softmax(s, dim=-1), v.float())

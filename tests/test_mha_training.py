@@ -36,7 +36,7 @@ def test_oracle_score_stats_brute_force():
     q, k = qk(2, 3, 11, 8, dtype=F64)
     lens = torch.tensor([11, 6])
     for causal in (True, False):
-        st = ref.score_stats(q, k, 0.35, lens, causal)
+        st = ref.score_stats(q, k, 0.35, lens, lens, causal)
         for h in range(3):
             c = s1 = s2 = 0.0
             for b in range(2):
@@ -51,7 +51,7 @@ def test_oracle_score_stats_brute_force():
 def test_oracle_score_std_is_population_std():
     q, k = qk(2, 2, 13, 16, seed=1, dtype=F64)
     lens = torch.tensor([13, 9])
-    std = ref.score_std(ref.score_stats(q, k, 0.25, lens, True))
+    std = ref.score_std(ref.score_stats(q, k, 0.25, lens, lens, True))
     for h in range(2):
         vals = torch.cat([(0.25 * q[b, h, :n] @ k[b, h, :n].T)[torch.tril(torch.ones(n, n, dtype=torch.bool))]
                           for b, n in ((0, 13), (1, 9))])
@@ -103,9 +103,10 @@ def test_score_stats_kernel_parity(dtype, b, H, L, D, causal, lens):
     q, k = qk(b, H, L, D, seed=L + D, dtype=dtype)
     lt = None if lens is None else torch.tensor(lens)
     scale = D ** -0.5
-    exp = ref.score_stats(q, k, scale, lt, causal)
-    got = score_stats(q.cuda(), k.cuda(), None if lt is None else lt.cuda(), causal).cpu()
-    again = score_stats(q.cuda(), k.cuda(), None if lt is None else lt.cuda(), causal).cpu()
+    exp = ref.score_stats(q, k, scale, lt, lt, causal)
+    ld = None if lt is None else lt.cuda()
+    got = score_stats(q.cuda(), k.cuda(), ld, ld, causal).cpu()
+    again = score_stats(q.cuda(), k.cuda(), ld, ld, causal).cpu()
     assert torch.equal(got, again), "score_stats must be deterministic"
     assert torch.equal(got[:, 0], exp[:, 0]), "count"
     # fp32 products inside the kernel: relative 1e-5 of the sum of squares
@@ -127,10 +128,11 @@ def test_score_std_gradient_matches_autograd(causal, lens):
     lt = None if lens is None else torch.tensor(lens)
     g = torch.randn(H, generator=torch.Generator().manual_seed(8))
     qd, kd = q.cuda().requires_grad_(True), k.cuda().requires_grad_(True)
-    std = ScoreStdFn.apply(qd, kd, None if lt is None else lt.cuda(), causal, 32)
+    ld = None if lt is None else lt.cuda()
+    std = ScoreStdFn.apply(qd, kd, ld, ld, causal, 32)
     std.backward(g.cuda())
     q64, k64 = q.to(F64).requires_grad_(True), k.to(F64).requires_grad_(True)
-    std64 = ref.score_std(ref.score_stats(q64, k64, D ** -0.5, lt, causal))
+    std64 = ref.score_std(ref.score_stats(q64, k64, D ** -0.5, lt, lt, causal))
     std64.backward(g.to(F64))
     assert_parity(std.detach().cpu(), std64.detach(), torch.float32, "std")
     assert_parity(qd.grad.cpu(), q64.grad, torch.float32, "dq")
@@ -179,3 +181,59 @@ def test_selective_mha_training_forward_backward(case):
         assert_parity(p.grad.cpu(), params[n].grad, torch.float32, f"d{n}")
     ema = 0.9 * 0.7 + 0.1 * std64.detach()
     assert_parity(m.score_std_ema.cpu(), ema, torch.float32, "score_std_ema")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float32, 128)])
+def test_score_stats_cross_lengths(dtype, D):
+    """Cross attention's statistics: every query, keys inside the context
+    length (q_len != k_len)."""
+    from selective_attention.kernels.attention import score_stats
+    print(f"score stats cross {dtype} D{D}", flush=True)
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(2, 3, 50, D, generator=g).to(dtype)
+    k = torch.randn(2, 3, 130, D, generator=g).to(dtype)
+    kl = torch.tensor([130, 77])
+    exp = ref.score_stats(q, k, D ** -0.5, None, kl, False)
+    got = score_stats(q.cuda(), k.cuda(), None, kl.cuda(), False).cpu()
+    assert torch.equal(got[:, 0], exp[:, 0]), "count"
+    assert ((got[:, 2] - exp[:, 2]).abs() <= 1e-5 * exp[:, 2].abs() + 1e-9).all(), (got, exp)
+    assert ((got[:, 1] - exp[:, 1]).abs() <= 1e-5 * torch.sqrt(exp[:, 0] * exp[:, 2]) + 1e-9).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lens", [[90, 37], None])
+def test_cross_mha_training_forward_backward(lens):
+    """CrossSelectiveMHA in training mode (fp32 parameters): outputs, the
+    gradients of the decoder input, the context and every parameter, and
+    the running-average update, against the fp64 oracle module."""
+    from selective_attention.modules.cross_selective_attention import CrossSelectiveMHA
+    print(f"CrossSelectiveMHA training lens={lens}", flush=True)
+    torch.manual_seed(31)
+    b, L, Lc, dim, hd = 2, 33, 90, 96, 32
+    m = CrossSelectiveMHA(0, dim, hd, log_gate_penalty=1.2)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn_like(p) * 0.2)
+        m.select_gate_proj.bias.add_(1.0)
+        m.score_std_ema.fill_(0.5)
+    m = m.cuda().train()
+    gen = torch.Generator().manual_seed(32)
+    x, ctx = torch.randn(b, L, dim, generator=gen), torch.randn(b, Lc, dim, generator=gen)
+    w = torch.randn(b, L, dim, generator=gen)
+    lt = None if lens is None else torch.tensor(lens)
+    xd, cd = x.cuda().requires_grad_(True), ctx.cuda().requires_grad_(True)
+    out = m(xd, cd, None if lt is None else lt.cuda())
+    (out * w.cuda()).sum().backward()
+
+    params = {n: p.detach().cpu().to(F64).requires_grad_(True) for n, p in m.named_parameters()}
+    x64, c64 = x.to(F64).requires_grad_(True), ctx.to(F64).requires_grad_(True)
+    out64, std64 = lm_ref.cross_mha_train_forward(params, x64, c64, lt, hd, 1.2)
+    (out64 * w.to(F64)).sum().backward()
+
+    assert_parity(out.detach().cpu(), out64.detach(), torch.float32, "out")
+    assert_parity(xd.grad.cpu(), x64.grad, torch.float32, "dx")
+    assert_parity(cd.grad.cpu(), c64.grad, torch.float32, "dcontext")
+    for n, p in m.named_parameters():
+        assert_parity(p.grad.cpu(), params[n].grad, torch.float32, f"d{n}")
+    assert_parity(m.score_std_ema.cpu(), 0.9 * 0.5 + 0.1 * std64.detach(), torch.float32, "ema")
