@@ -8,9 +8,10 @@
 // decay-gradient sums :689-765, :783-911) with two kernels over one chunk of
 // one group (its HPG heads), each tile a 64-token strip:
 //
-//   ssd_bwd_src (one block per (b, c, group, source strip S), 8 waves in two
-//     head slots; wave w owns the 16 source columns
-//     sigma = 64 S + 16 (w % 4) + lane % 16 of its slot's heads):
+//   ssd_bwd_src (one block per (b, c, group, source strip S), 4 waves; wave
+//     w owns the 16 source columns sigma = 64 S + 16 w + lane % 16; the
+//     group's heads run two at a time, one launch per pair, the last launch
+//     adding the earlier pairs' dCB shares and writing dB and the planes):
 //       du     = dt * (e^{dc_last - dc} B.dS^T  +  L^T dy),  L = C.B^T o decay
 //       dB     = sum_h w_h u_h.dS_h  +  dCB^T C,            dCB = sum_h (dy_h u_h^T) dt decay
 //       x_B, ddt_direct, the column sums q and (per source strip) row sums r
