@@ -105,19 +105,25 @@ __device__ __forceinline__ int v_swz(int r) {
 // data goes to LDS byte address lds + 16 lane (4 lane for the dword form),
 // from base + off (off in bytes).  m0 carries the LDS address; nothing else
 // in the kernels that use these relies on m0.
+//
+// lds_addr: the LDS byte address of a generic pointer into LDS, as a
+// wave-uniform value (the DMA helpers take it through readfirstlane, which
+// costs nothing where it already sits in a scalar register).  A generic LDS address is the shared aperture in the
+// high half and the LDS offset in the low half, so the low 32 bits are the
+// address (no address-space cast, whose null check costs a 64-bit compare
+// and select per use).  Kernels take it once per stage, outside their loops.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p)));
+  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
 }
-__device__ __forceinline__ void dma_lds16(const void* base, uint32_t off, const void* lds) {
+__device__ __forceinline__ void dma_lds16(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
-               "s"(lds_addr(lds)) : "memory", "m0");
+               "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
-__device__ __forceinline__ void dma_lds4(const void* base, uint32_t off, const void* lds) {
+__device__ __forceinline__ void dma_lds4(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base),
-               "s"(lds_addr(lds)) : "memory", "m0");
+               "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
@@ -325,19 +331,23 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     dma_k[i] = row * static_cast<int>(rs) + 8 * (ch ^ k_swz<D>(row));
     dma_v[i] = row * static_cast<int>(rs) + 8 * (ch ^ v_swz<D>(row));
   }
-  auto issue_kv = [&](int kb, bf16* Kt) __attribute__((always_inline)) {
+  // LDS byte addresses of this wave's DMA destinations in stage 0 (stage 1
+  // is SM::stage * 2 bytes further on): K and V chunks 1 KB apart, the biases
+  const uint32_t lds_st0 = lds_addr(stage0), lds_st1 = lds_addr(stage1);
+  const uint32_t lds_wave = static_cast<uint32_t>(w * IPW) << 10;
+  auto issue_kv = [&](int kb, uint32_t st) __attribute__((always_inline)) {
     const int k0 = kb * BS, nk = min(BS, nks - k0);
-    bf16* Vt = Kt + SM::tile;
+    const uint32_t kt = st + lds_wave, vt = kt + 2 * SM::tile;
     const bf16* kb0 = kbase + static_cast<long>(k0) * rs;
     const bf16* vb0 = vbase + static_cast<long>(k0) * rs;
     if constexpr (BIAS) {   // the block's key biases (rows past the sequence repeat the last)
-      if (w == 0) dma_lds4(bias, 4u * min(k0 + lane, nks - 1), Vt + SM::tile);
+      if (w == 0) dma_lds4(bias, 4u * min(k0 + lane, nks - 1), st + 4 * SM::tile);
     }
     if (nk == BS) {
 #pragma unroll
       for (int i = 0; i < IPW; ++i) {
-        dma_lds16(kb0, 2u * dma_k[i], Kt + ((w * IPW + i) << 9));
-        dma_lds16(vb0, 2u * dma_v[i], Vt + ((w * IPW + i) << 9));
+        dma_lds16(kb0, 2u * dma_k[i], kt + (i << 10));
+        dma_lds16(vb0, 2u * dma_v[i], vt + (i << 10));
       }
       return;
     }
@@ -349,8 +359,8 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
       const int ch = (pos % (2 * D)) >> 4;
       const int koff = rr * static_cast<int>(rs) + 8 * (ch ^ k_swz<D>(row));
       const int voff = rr * static_cast<int>(rs) + 8 * (ch ^ v_swz<D>(row));
-      dma_lds16(kb0, 2u * koff, Kt + ((w * IPW + i) << 9));
-      dma_lds16(vb0, 2u * voff, Vt + ((w * IPW + i) << 9));
+      dma_lds16(kb0, 2u * koff, kt + (i << 10));
+      dma_lds16(vb0, 2u * voff, vt + (i << 10));
     }
   };
 
@@ -379,7 +389,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
   // is a fixed LDS object.
   int e = 0, en = 0;
   // one key block: computed from stage cur while the next block's tiles land in nxt
-  auto step = [&](bf16* cur, bf16* nxt) __attribute__((always_inline)) {
+  auto step = [&](bf16* cur, uint32_t nxt_lds) __attribute__((always_inline)) {
     const int kb = block_of(e);
     const int enn = en < nslot ? next_valid(en + 1) : nslot;   // the block after next
     const int k0 = kb * BS;
@@ -391,7 +401,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     __builtin_amdgcn_s_waitcnt(vm_wait<0>());
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (en < nslot) issue_kv(block_of(en), nxt);
+    if (en < nslot) issue_kv(block_of(en), nxt_lds);
     const bf16* Ks = cur;
     const bf16* Vs = Ks + SM::tile;
     // bias of the wave's keys 32 kh + 8g + 0..7
@@ -474,11 +484,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
   // the query fragments (and the selection row) have arrived before the loop:
   // nothing the compiler tracks is in flight inside it
   __builtin_amdgcn_s_waitcnt(vm_wait<0>());
-  if (e < nslot) issue_kv(block_of(e), stage0);
+  if (e < nslot) issue_kv(block_of(e), lds_st0);
   while (e < nslot) {
-    step(stage0, stage1);
+    step(stage0, lds_st1);
     if (e >= nslot) break;
-    step(stage1, stage0);
+    step(stage1, lds_st0);
   }
   // every wave is done with the tiles before the merge reuses the LDS
   __builtin_amdgcn_s_barrier();
