@@ -437,9 +437,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
                               ? (kb < jq && qfull)
                               : (qfull && k0 + BS <= nks && kb != (MODE == kCross ? 0 : jq));
     // interior blocks without a bias keep raw scores (the scale goes into the
-    // exponent); otherwise scale, bias and masks are applied in place
+    // exponent); otherwise scale, bias and masks are applied in place.  The
+    // block-uniform test is made once: tested per element inside the unrolled
+    // loops it became a branch per score.
     float scl = scale_log2;
-    if (!interior || BIAS) {
+    if (!interior) {
       scl = 1.0f;
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt)
@@ -451,11 +453,21 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
             const int key = k0 + kl;
             float val = sc[jt][u2][i] * scale_log2;
             const bool exempt = MODE == kCross ? key == 0 : key == qloc[jt];
-            if constexpr (BIAS) val += (interior || !exempt) ? bk[4 * u2 + i] * kLog2e : 0.f;
-            if (!interior)
-              val = (kl < nk && (MODE != kCausalSelf || key <= qloc[jt]) && qloc[jt] < n) ? val : kNegInf;
+            if constexpr (BIAS) val += exempt ? 0.f : bk[4 * u2 + i] * kLog2e;
+            val = (kl < nk && (MODE != kCausalSelf || key <= qloc[jt]) && qloc[jt] < n) ? val : kNegInf;
             sc[jt][u2][i] = val;
           }
+    } else if constexpr (BIAS) {   // no mask and no exempt key: scale and bias only
+      scl = 1.0f;
+      float bl[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bl[j] = bk[j] * kLog2e;
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+        for (int u2 = 0; u2 < 2; ++u2)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sc[jt][u2][i] = fmaf(sc[jt][u2][i], scale_log2, bl[4 * u2 + i]);
     }
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) softmax_lazy<2, DT>(sc[jt], acc[jt], m[jt], l[jt], scl);
