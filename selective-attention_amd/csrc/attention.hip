@@ -190,14 +190,18 @@ __device__ __forceinline__ void softmax_lazy(v4f (&s)[KT], v4f (&o)[DT], float& 
 //   kFullSelf    every key of the query's own sequence;  j = i exempt
 //   kCross       every key of the sequence's key range cu_k[s]..cu_k[s+1]
 //                (k, v, key_bias indexed by key token); key 0 exempt
-// dense_all != 0 selects every key block the mode admits (no table).
+// SEL (how the key blocks are chosen, fixed per launch):
+//   kSelDense    every key block the mode admits (no table)
+//   kSelShort    a block_idx row of at most 64 slots, held one slot per lane
+//   kSelLong     a longer row, read slot by slot with scalar loads
 constexpr int kCausalSelf = 0, kFullSelf = 1, kCross = 2;
+constexpr int kSelDense = 0, kSelShort = 1, kSelLong = 2;
 
-template <int D, bool BIAS, int MODE>
+template <int D, bool BIAS, int MODE, int SEL>
 __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_k, int nseq,
-    const int32_t* __restrict__ block_idx, int n_qblk, int max_blocks, int grid_qblk, int dense_all,
+    const int32_t* __restrict__ block_idx, int n_qblk, int max_blocks, int grid_qblk,
     const float* __restrict__ key_bias, bf16* __restrict__ o, int T, int Tk, int H,
     float scale_log2) {
   constexpr int BS = 64;
@@ -276,12 +280,12 @@ __global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
   // for kCausalSelf), in order; dense: slots are the blocks themselves
   // A block id repeated within a row is attended once, at its first slot:
   // the selection is a set of key blocks.
-  const bool dense = dense_all != 0;
+  constexpr bool dense = SEL == kSelDense;
   const bool has_row = dense || (gq < n_qblk && max_blocks > 0);
   const int nkb = (nks + BS - 1) / BS;
   const int nslot = dense ? (MODE == kCausalSelf ? min(jq + 1, nkb) : nkb) : (has_row ? max_blocks : 0);
   const int32_t* sel = has_row && !dense ? block_idx + (static_cast<long>(h) * n_qblk + gq) * max_blocks : nullptr;
-  const bool simple = !dense && max_blocks <= 64;
+  constexpr bool simple = SEL == kSelShort;
   int my_kb = -1;
   uint64_t vmask = 0;
   if (simple && has_row) {
@@ -557,11 +561,15 @@ int launch_sparse(const void* q, const void* k, const void* v, const int32_t* cu
                   int Tk, int H, float scale_log2, hipStream_t s) {
   const long blocks = static_cast<long>(H) * grid_qblk;
   ProfScope prof_(MODE == kCausalSelf ? "sparse_attn_fwd" : MODE == kFullSelf ? "attn_full_fwd" : "attn_cross_fwd", s);
-  hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, BIAS, MODE>), dim3(blocks), dim3(256),
-                     0, s, static_cast<const bf16*>(q), static_cast<const bf16*>(k),
-                     static_cast<const bf16*>(v), cu, cu_k, nseq, block_idx, n_qblk, max_blocks,
-                     grid_qblk, dense_all, key_bias, static_cast<bf16*>(o), T, Tk,
-                     H, scale_log2);
+#define SA_SPARSE_LAUNCH(SEL)                                                                     \
+  hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, BIAS, MODE, SEL>), dim3(blocks), dim3(256), 0, s, \
+                     static_cast<const bf16*>(q), static_cast<const bf16*>(k),                    \
+                     static_cast<const bf16*>(v), cu, cu_k, nseq, block_idx, n_qblk, max_blocks,  \
+                     grid_qblk, key_bias, static_cast<bf16*>(o), T, Tk, H, scale_log2)
+  if (dense_all) SA_SPARSE_LAUNCH(kSelDense);
+  else if (max_blocks <= 64) SA_SPARSE_LAUNCH(kSelShort);
+  else SA_SPARSE_LAUNCH(kSelLong);
+#undef SA_SPARSE_LAUNCH
   return 0;
 }
 
