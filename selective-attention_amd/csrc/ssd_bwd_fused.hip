@@ -437,6 +437,24 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
            (kt & 1) * kPlaneT + 32 * (kt >> 1);
   };
 
+  // B of this lane's source row (all N) and u of this pass' heads there are
+  // the same in every stage: a pass other than the last loads them once,
+  // with the first stage, instead of at the start of each stage that uses
+  // them (where each load's latency was exposed).  The last pass has no
+  // registers to spare and loads them per stage.
+  constexpr bool kHold = !last;
+  const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 8 * lg);
+  v8bf Bh[NK], Uh[HS][2];
+#pragma unroll
+  for (int ks = 0; ks < NK; ++ks) Bh[ks] = kHold && sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+#pragma unroll
+  for (int h = 0; h < HS; ++h) {
+    const int k = pass * HS + h;
+    const bf16* urow = uc + min(k, HPG - 1) * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      Uh[h][ks] = kHold && sv && k < HPG ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+  }
   issue(pass, 0, 0);
   wait_all_mem();
   __syncthreads();
@@ -530,14 +548,15 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 #pragma unroll
         for (int half = 0; half < NH; ++half) {
           const int j = jo + h * NH + half;
-          v8bf Bf[2];
+          v8bf Bf[2] = {Bh[2 * half], Bh[2 * half + 1]};
           UW x;
           uint2 ux[4];    // u of head k at this lane's column, for x_B
           float dcl = 0.f;
           if (kv) {
-            const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 64 * half + 8 * lg);
+            if (!kHold) {
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+              for (int ks = 0; ks < 2; ++ks) Bf[ks] = sv ? load_v8bf(brow + 64 * half + 32 * ks) : zero_v8bf();
+            }
             if (last) x = load_uw(k);
             if (half == NH - 1) {
               const bf16* urow4 = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
@@ -636,13 +655,14 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         const bool kv = k < HPG;
         const int par = HS == 1 ? (Ti & 1) : h;
         // register loads of this stage, before the next stage's DMA
-        v8bf Bf[NK], uf[2];
-        if (h == 0) {
-          const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 8 * lg);
+        v8bf Bf[NK], uf[2] = {Uh[h][0], Uh[h][1]};
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) Bf[ks] = Bh[ks];
+        if (!kHold && h == 0) {
 #pragma unroll
           for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
         }
-        if (kv) {
+        if (!kHold && kv) {
           const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
