@@ -197,8 +197,17 @@ __device__ __forceinline__ void softmax_lazy(v4f (&s)[KT], v4f (&o)[DT], float& 
 constexpr int kCausalSelf = 0, kFullSelf = 1, kCross = 2;
 constexpr int kSelDense = 0, kSelShort = 1, kSelLong = 2;
 
+// Workgroups per CU the register budget is set for: at D = 64 a workgroup
+// holds 33 KB of LDS, so four fit (dense self-attention fits 128 VGPRs; the
+// table walks and the cross mode would spill there and take three); at
+// D = 128 (66 KB) two.
+template <int D, int MODE, int SEL>
+constexpr int attn_blocks_per_cu() {
+  return D == 64 ? (SEL == kSelDense && MODE != kCross ? 4 : 3) : 2;
+}
+
 template <int D, bool BIAS, int MODE, int SEL>
-__global__ __launch_bounds__(256, 2) void sparse_attn_fwd_kernel(
+__global__ __launch_bounds__(256, (attn_blocks_per_cu<D, MODE, SEL>())) void sparse_attn_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_k, int nseq,
     const int32_t* __restrict__ block_idx, int n_qblk, int max_blocks, int grid_qblk,
