@@ -238,9 +238,11 @@ __device__ __forceinline__ int opaque(int v) {
 // HS = min(HPG, 2) heads: du, x_B, ddt, q, r of those heads.  dB and the dCB
 // planes need every head of the group: a pass that is not the last parks its
 // fp32 share of dCB in the 64 bytes per lane that the last pass overwrites
-// with the hi / lo planes; the last pass adds the parked shares back and
-// computes all of dB (the state part of the earlier heads from their dS
-// tiles again).
+// with the hi / lo planes, and the state part of dB from its own heads in a
+// workspace slot of the block; the last pass starts dB from that slot, adds
+// the parked dCB shares back, writes the planes and adds dB's intra part.
+// Passes other than the last hold the source row's B and their heads' u rows
+// in registers for the whole pass.
 // ---------------------------------------------------------------------------
 template <int NK, int HPG>
 struct SrcSmem {
@@ -255,8 +257,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     const bf16* __restrict__ dyp, const float* __restrict__ dt, const float* __restrict__ dc,
     const bf16* __restrict__ dSp, const int64_t* __restrict__ length, bf16* __restrict__ du,
     bf16* __restrict__ dB, bf16* __restrict__ dcbp, float* __restrict__ ddt_part,
-    float* __restrict__ xB_part, float* __restrict__ qpart, float* __restrict__ rpart, SsdDims d,
-    int mono) {
+    float* __restrict__ xB_part, float* __restrict__ qpart, float* __restrict__ rpart,
+    float* __restrict__ dbpark, SsdDims d, int mono) {
   using SM = SrcSmem<NK, HPG>;
   constexpr int N = SM::N;
   constexpr int HS = HPG < 2 ? HPG : 2;          // heads per pass
@@ -346,10 +348,9 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   const int ntile = (lim + 63) / 64 - S;   // target strips T = S .. S + ntile - 1
 
   // Stages of pass p: first the state stages, dS n half (j % NH) of head
-  // kb + j / NH, kb = 0 in the last pass (every head up to this pass' own)
-  // and p HS before; then per target strip T = S + Ti the dy tile of head
+  // p HS + j / NH; then per target strip T = S + Ti the dy tile of head
   // p HS + h, h = 0..HS-1 (C_T and the dc tables come with h == 0).
-  auto n_state = [&](int p) { return (p == NPASS - 1 ? (p + 1) * HS : HS) * NH; };
+  auto n_state = [&](int) { return HS * NH; };
   auto n_stage = [&](int p) { return n_state(p) + HS * ntile; };
   const bf16* dyg = dyp + (bcg * stiles) * (HPG * 2L * kPlaneT);   // + (T HPG + k) 2 kPlaneT
   const bf16* dSg = dSp + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (2L * 64 * N);
@@ -367,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     bf16* dst = stg(par);
     const int nst = n_state(p);
     if (j < nst) {
-      const int k = (p == NPASS - 1 ? 0 : p * HS) + j / NH, half = j % NH;
+      const int k = p * HS + j / NH, half = j % NH;
       if (k < HPG) {
         const bf16* src = dSg + k * (2L * 64 * N) + 64 * half;
         dma_pre<8>(dst, src, o_gs, w);
@@ -455,6 +456,22 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     for (int ks = 0; ks < 2; ++ks)
       Uh[h][ks] = kHold && sv && k < HPG ? load_v8bf(urow + 32 * ks) : zero_v8bf();
   }
+  // dB^T rows n = 16 nt + 4 lg + r, column sig.  Every pass forms the state
+  // part of its own heads; a pass other than the last parks it (this
+  // thread's 128 bytes of the block's slot) and the last pass starts from
+  // the parked part, so no pass reads another pass' dS tiles.
+  v4f dBT[NT];
+  float4* const park = reinterpret_cast<float4*>(dbpark) + static_cast<long>(bid) * (NT * 256) + tid;
+  if constexpr (last && NPASS > 1) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const float4 v = park[nt * 256];
+      dBT[nt] = v4f{v.x, v.y, v.z, v.w};
+    }
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) dBT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
   issue(pass, 0, 0);
   wait_all_mem();
   __syncthreads();
@@ -464,24 +481,23 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   // and a pair stage's its head (with one head per pass, its strip's parity).
   // Each stage issues its own register loads before the next stage's DMA, so
   // that waiting for them does not wait for the DMA.
-  v4f dBT[NT];  // dB^T rows n = 16 nt + 4 lg + r, column sig (last pass)
   {
     const int nst = n_state(pass);
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) dBT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
     v4f duT[HS][4];   // du^T of this pass' heads: rows p = 16 pt + 4 lg + r, column sig
-    float qacc[HS], dtk[HS], dck[HS];
+    float qacc[HS], dtk[HS], dck[HS], ekh[HS];
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
       const int k = min(pass * HS + h, HPG - 1);
       dck[h] = dcc[k * hstride + scl] * kLog2e;
       dtk[h] = sv ? dtc[k * hstride + scl] : 0.f;
+      // e^{min(dc_last - dc_sig, 0)}: the state weight is ekh dt
+      ekh[h] = fast_exp2(fminf(dcc[k * hstride + d.Lc - 1] * kLog2e - dck[h], 0.f));
       qacc[h] = 0.f;
 #pragma unroll
       for (int pt = 0; pt < 4; ++pt) duT[h][pt] = v4f{0.f, 0.f, 0.f, 0.f};
     }
 
-    // ---- state stages: dB^T += w dS^T.u^T (last pass), du^T += dS.B^T ----
+    // ---- state stages: dB^T += w dS^T.u^T, du^T += dS.B^T ----
     {
       int o_sd[2], o_st[4][2];
 #pragma unroll
@@ -491,27 +507,10 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         o_st[nt4][0] = tr_first<8, swz_s128>(8 * lg, 16 * nt4, lane);
         o_st[nt4][1] = tr_first<8, swz_s128>(8 * lg + 4, 16 * nt4, lane);
       }
-      // head k's u row and state weight w = e^{min(dc_last - dc, 0)} dt at this lane's column
-      struct UW {
-        v8bf uf[2];
-        float dtv, dc, dcl;
-      };
-      auto load_uw = [&](int k) -> UW {
-        UW r;
-        const int kc = k * hstride + scl;
-        r.dtv = sv ? dtc[kc] : 0.f;
-        r.dc = dcc[kc];
-        r.dcl = dcc[k * hstride + d.Lc - 1];
-        const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) r.uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
-        return r;
-      };
-      // dB^T rows of the n half in stage buffer Y from head k's dS
-      auto state_dB = [&](const bf16* Yh, const UW& x, int half) {
-        const float wk = fast_exp2(fminf((x.dcl - x.dc) * kLog2e, 0.f)) * x.dtv;
+      // dB^T rows of the n half in stage buffer Y from a head's dS, its u row
+      // uf at this lane's column and its state weight wk
+      auto state_dB = [&](const bf16* Yh, const v8bf (&uf)[2], float wk, int half) {
         const bf16* Yl = Yh + kPlaneT;
-        const v8bf* uf = x.uf;
 #pragma unroll
         for (int nt4 = 0; nt4 < 4; ++nt4) {
           v4f tmp = v4f{0.f, 0.f, 0.f, 0.f};
@@ -526,43 +525,29 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
             if (h2 == half) dBT[4 * h2 + nt4] += tmp * wk;
         }
       };
-      // last pass: the dB state part of the heads of the earlier passes
-      if (last) {
-        for (int kk = 0; kk < pass * HS; ++kk) {
-#pragma unroll
-          for (int half = 0; half < NH; ++half) {
-            const int j = kk * NH + half;
-            const UW x = load_uw(kk);
-            __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the DMA
-            issue_next(pass, j, half);
-            state_dB(stg(half), x, half);
-            end_stage(pass, j + 1);
-          }
-        }
-      }
-      const int jo = last ? pass * HS * NH : 0;   // first stage of this pass' own heads
 #pragma unroll
       for (int h = 0; h < HS; ++h) {
         const int k = pass * HS + h;
         const bool kv = k < HPG;
 #pragma unroll
         for (int half = 0; half < NH; ++half) {
-          const int j = jo + h * NH + half;
+          const int j = h * NH + half;
           v8bf Bf[2] = {Bh[2 * half], Bh[2 * half + 1]};
-          UW x;
+          v8bf ul[2] = {Uh[h][0], Uh[h][1]};
           uint2 ux[4];    // u of head k at this lane's column, for x_B
-          float dcl = 0.f;
           if (kv) {
             if (!kHold) {
+              const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
 #pragma unroll
-              for (int ks = 0; ks < 2; ++ks) Bf[ks] = sv ? load_v8bf(brow + 64 * half + 32 * ks) : zero_v8bf();
+              for (int ks = 0; ks < 2; ++ks) {
+                Bf[ks] = sv ? load_v8bf(brow + 64 * half + 32 * ks) : zero_v8bf();
+                ul[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+              }
             }
-            if (last) x = load_uw(k);
             if (half == NH - 1) {
               const bf16* urow4 = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
 #pragma unroll
               for (int pt = 0; pt < 4; ++pt) ux[pt] = *reinterpret_cast<const uint2*>(urow4 + 16 * pt);
-              dcl = dcc[k * hstride + d.Lc - 1];
             }
           }
           __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the DMA
@@ -578,10 +563,10 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
                 duT[h][pt] = mfma_bf16(load_v8bf(Yh + off), Bf[ks], duT[h][pt]);
                 duT[h][pt] = mfma_bf16(load_v8bf(Yl + off), Bf[ks], duT[h][pt]);
               }
-            if (last) state_dB(Yh, x, half);
+            state_dB(Yh, ul, ekh[h] * dtk[h], half);
             if (half == NH - 1) {
               // head k's state part is complete: scale by e^{dc_last - dc_sig}; x_B
-              const float ek = fast_exp2(fminf(dcl * kLog2e - dck[h], 0.f));
+              const float ek = ekh[h];
               float sx = 0.f;
 #pragma unroll
               for (int pt = 0; pt < 4; ++pt) {
@@ -595,6 +580,10 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
           end_stage(pass, j + 1);
         }
       }
+    }
+    if constexpr (!last) {   // the state part of dB for the last pass
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) park[nt * 256] = make_float4(dBT[nt][0], dBT[nt][1], dBT[nt][2], dBT[nt][3]);
     }
 
     // the dCB of target strip Tp: park this pass' share, or (last pass) add
@@ -1011,8 +1000,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
 #define SA_SRC_INST(HPG, PASS)                                                                   \
   template __global__ void ssd_bwd_src_kernel<4, HPG, PASS>(                                     \
       const bf16*, const bf16*, const bf16*, const bf16*, const float*, const float*,            \
-      const bf16*, const int64_t*, bf16*, bf16*, bf16*, float*, float*, float*, float*, SsdDims, \
-      int);
+      const bf16*, const int64_t*, bf16*, bf16*, bf16*, float*, float*, float*, float*, float*,  \
+      SsdDims, int);
 SA_SRC_INST(1, 0)
 SA_SRC_INST(2, 0)
 SA_SRC_INST(3, 0)
@@ -1036,7 +1025,7 @@ int launch_fused_hpg(const void* u, const void* B, const void* C, const bf16* dy
                      const float* dt, const float* dc, const float* states, const bf16* dSp,
                      const int64_t* length, void* du, void* dB, void* dC, bf16* dcbp,
                      float* ddt_part, float* xB_part, float* xC_part, float* qpart, float* rpart,
-                     const SsdDims& d, bool dt_nonneg, hipStream_t s) {
+                     float* dbpark, const SsdDims& d, bool dt_nonneg, hipStream_t s) {
   constexpr int NK = 4;
   const long blocks = static_cast<long>(d.b) * d.nc * d.G * (d.Lc / 64);
   auto src_pass = [&](auto kernel) -> int {
@@ -1045,7 +1034,7 @@ int launch_fused_hpg(const void* u, const void* B, const void* C, const bf16* dy
                        static_cast<const bf16*>(u), static_cast<const bf16*>(B),
                        static_cast<const bf16*>(C), dyp, dt, dc, dSp, length,
                        static_cast<bf16*>(du), static_cast<bf16*>(dB), dcbp, ddt_part, xB_part,
-                       qpart, rpart, d, dt_nonneg ? 1 : 0);
+                       qpart, rpart, dbpark, d, dt_nonneg ? 1 : 0);
     SA_CHECK_LAUNCH("ssd_bwd_src");
     return 0;
   };
@@ -1081,12 +1070,13 @@ int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const bf16
                          const float* dt, const float* dc, const float* states, const bf16* dSp,
                          const int64_t* length, void* du, void* dB, void* dC, bf16* dcbp,
                          float* ddt_part, float* xB_part, float* xC_part, float* qpart,
-                         float* rpart, const SsdDims& d, bool dt_nonneg, hipStream_t s) {
+                         float* rpart, float* dbpark, const SsdDims& d, bool dt_nonneg,
+                         hipStream_t s) {
   switch (d.H / d.G) {
-    case 1: return launch_fused_hpg<1>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, d, dt_nonneg, s);
-    case 2: return launch_fused_hpg<2>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, d, dt_nonneg, s);
-    case 3: return launch_fused_hpg<3>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, d, dt_nonneg, s);
-    default: return launch_fused_hpg<4>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, d, dt_nonneg, s);
+    case 1: return launch_fused_hpg<1>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, dbpark, d, dt_nonneg, s);
+    case 2: return launch_fused_hpg<2>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, dbpark, d, dt_nonneg, s);
+    case 3: return launch_fused_hpg<3>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, dbpark, d, dt_nonneg, s);
+    default: return launch_fused_hpg<4>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, dbpark, d, dt_nonneg, s);
   }
 }
 
