@@ -77,6 +77,8 @@ FUSED_CASES = [
     ("hpg1_lens", dict(b=2, L=192, H=2, P=64, N=128, G=2, lens=[192, 77]), 64),
     ("hpg3_ragged", dict(b=1, L=200, H=3, P=64, N=64, G=1, lens=[171]), 128),
     ("hpg4_partial", dict(b=2, L=320, H=8, P=64, N=128, G=2, lens=[320, 130]), 128),
+    # three heads per group: two source launches, the second with one head (dB parked between them)
+    ("hpg3_n128", dict(b=2, L=256, H=6, P=64, N=128, G=2, lens=[256, 171]), 128),
     ("zero_len", dict(b=2, L=128, H=4, P=64, N=64, G=1, lens=[0, 65], with_h=False), 64),
     # two P tiles, three N slices: bf16 chunk-state / dH_intra kernels, generic column / row kernels
     ("p128_n192", dict(b=2, L=600, H=2, P=128, N=192, G=1, lens=[600, 389]), 256),
