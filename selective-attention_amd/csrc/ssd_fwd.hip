@@ -170,20 +170,21 @@ __global__ __launch_bounds__(256) void chunk_outer_kernel(
 // row-major t tiles in LDS through transpose reads: A = X^T (X = B or C) and
 // the B operand = the scaled U (MODE 0, one bf16 plane) or the scaled dy
 // (MODE 1, hi + lo planes).  Each lane ends with 4 consecutive n of one p
-// (16-byte stores).  t tiles are double-buffered and prefetched into
-// registers during the previous tile's MFMAs.
+// (16-byte stores).  t tiles are prefetched into registers during the
+// previous tile's MFMAs and committed to a single LDS stage (35 KB at
+// N = 128), so three or four blocks share a CU: more resident blocks hide
+// the loads better than a second stage did (chunk states 88 -> 72-78 us).
 // ---------------------------------------------------------------------------
 template <int NK, int MODE>
-__global__ __launch_bounds__(256, 2) void chunk_outer_bf16_kernel(
+__global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
     const void* __restrict__ a_src, const bf16* __restrict__ x_src, const float* __restrict__ dt,
     const float* __restrict__ dc, const int64_t* __restrict__ length, float* __restrict__ out,
     bf16* __restrict__ dyp, SsdDims d) {
   constexpr int N = 32 * NK, LDX = N + 8, LDA = 64 + 8;
   constexpr int NPL = 2;                   // hi + lo planes of the scaled operand
   constexpr int NTW = N / 64;              // 16-wide n tiles per wave
-  constexpr int STAGE = NPL * 64 * LDA + 64 * LDX;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* sm = reinterpret_cast<bf16*>(smem_raw);   // [2][STAGE]: As [NPL][64][LDA], Xs [64][LDX]
+  bf16* sm = reinterpret_cast<bf16*>(smem_raw);   // As [NPL][64][LDA], Xs [64][LDX]
 
   const int ptiles = d.P / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -246,8 +247,8 @@ __global__ __launch_bounds__(256, 2) void chunk_outer_bf16_kernel(
       }
       px.load(xc + static_cast<long>(t0) * x_rs, x_rs, kv, tid);
     };
-    auto commit_tile = [&](int slot) __attribute__((always_inline)) {
-      bf16* As = sm + slot * STAGE;
+    auto commit_tile = [&]() __attribute__((always_inline)) {
+      bf16* As = sm;
       bf16* Xs = As + NPL * 64 * LDA;
       if constexpr (MODE == 0) {
         // w * u is fp32 (dt up to z > 20 makes it large): hi + lo planes keep
@@ -319,12 +320,12 @@ __global__ __launch_bounds__(256, 2) void chunk_outer_bf16_kernel(
 
     const int ntt = (klim + 63) / 64;
     load_tile(0);
-    commit_tile(0);
+    commit_tile();
     __syncthreads();
     for (int tt = 0; tt < ntt; ++tt) {
       const bool has_next = tt + 1 < ntt;
       if (has_next) load_tile(tt + 1);
-      const bf16* As = sm + (tt & 1) * STAGE;
+      const bf16* As = sm;
       const bf16* Xs = As + NPL * 64 * LDA;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
@@ -343,7 +344,8 @@ __global__ __launch_bounds__(256, 2) void chunk_outer_bf16_kernel(
             for (int pl = 0; pl < NPL; ++pl) acc[i][pt] = mfma_bf16(a, bop[pt][pl], acc[i][pt]);
         }
       }
-      if (has_next) commit_tile((tt + 1) & 1);
+      __syncthreads();   // every wave is done with the stage
+      if (has_next) commit_tile();
       __syncthreads();
     }
   }
@@ -845,7 +847,7 @@ int launch_chunk_outer_bf16_nk(const void* a, const void* x, const float* dt, co
                                const int64_t* length, float* out, const SsdDims& d, hipStream_t s,
                                bf16* dyp = nullptr) {
   const long blocks = static_cast<long>(d.P / 64) * d.H * d.nc * d.b;
-  const size_t smem = 2 * sizeof(bf16) * (2 * 64 * 72 + 64 * (32 * NK + 8));
+  const size_t smem = sizeof(bf16) * (2 * 64 * 72 + 64 * (32 * NK + 8));
   if (smem > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(chunk_outer_bf16_kernel<NK, MODE>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
