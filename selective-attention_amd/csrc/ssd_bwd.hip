@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void state_passing_bwd_kernel(
     const float* __restrict__ states, float* __restrict__ dS, const float* __restrict__ dh_last,
     float* __restrict__ dh_init, const float* __restrict__ dc, float* __restrict__ ddc_part,
     bf16* __restrict__ dSp, SsdDims d) {
-  constexpr int GRP = 4;
+  constexpr int GRP = 8;   // chunks whose two loads are in flight together
   __shared__ float red[GRP][4];
   const long PN = static_cast<long>(d.P) * d.N;
   const int per_bh = static_cast<int>((PN + 1023) / 1024);

@@ -391,7 +391,7 @@ __global__ __launch_bounds__(256) void state_passing_fwd_kernel(
   float hv[4] = {0.f, 0.f, 0.f, 0.f};
   if (h_init) load4(h_init + static_cast<long>(bh) * PN + e0, hv);
   const float* dcl = dc + static_cast<long>(bh) * d.nc * d.Lc + (d.Lc - 1);
-  constexpr int GRP = 8;
+  constexpr int GRP = 16;   // chunks whose loads are in flight together (16: all of config 1's)
   for (int c0 = 0; c0 < d.nc; c0 += GRP) {
     float s[GRP][4];
     const int cn = min(GRP, d.nc - c0);
