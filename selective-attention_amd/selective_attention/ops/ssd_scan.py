@@ -62,6 +62,9 @@ class SSDScanFn(torch.autograd.Function):
 
         dt, dc, states = saved
         ctx.save_for_backward(u, A, B, C, delta_raw, delta_bias, h_init, length, dt, dc, states)
+        # an output that takes no gradient arrives as None rather than as a
+        # materialised zero tensor (the backward reads None as zero)
+        ctx.set_materialize_grads(False)
         ctx.chunk_size = chunk_size
         ctx.use_delta_softplus = use_delta_softplus
         ctx.delta_limit = delta_limit

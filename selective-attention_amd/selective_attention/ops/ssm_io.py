@@ -174,6 +174,7 @@ class SSDScanGatedFn(torch.autograd.Function):
                               *saved)
         ctx.fused = fused
         ctx.cfg = (chunk_size, use_delta_softplus, delta_limit)
+        ctx.set_materialize_grads(False)   # an unused h_last arrives as None (read as zero)
         return out, h_last
 
     @staticmethod
