@@ -482,6 +482,18 @@ __global__ __launch_bounds__(256, (attn_blocks_per_cu<D, MODE, SEL>())) void spa
 #pragma unroll
           for (int i = 0; i < 4; ++i) sc[jt][u2][i] = fmaf(sc[jt][u2][i], scale_log2, bl[4 * u2 + i]);
     }
+    // the V^T fragments of the wave's 32 keys, read before the softmax so
+    // that their LDS latency passes under its VALU work
+    v8bf vfr[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+      const bf16* p = Vs + vr * D + 8 * ((2 * t + vchunk) ^ vswz) + vhalf;
+      const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p));
+      const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + 4 * D));
+      vfr[t] = __builtin_bit_cast(v8bf, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) softmax_lazy<2, DT>(sc[jt], acc[jt], m[jt], l[jt], scl);
     // O^T += V^T . P^T over the wave's 32 keys
@@ -490,13 +502,8 @@ __global__ __launch_bounds__(256, (attn_blocks_per_cu<D, MODE, SEL>())) void spa
       const v8bf pb1 = pack_p(sc[1][0], sc[1][1]);
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
-        typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-        const bf16* p = Vs + vr * D + 8 * ((2 * t + vchunk) ^ vswz) + vhalf;
-        const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p));
-        const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + 4 * D));
-        const v8bf vf = __builtin_bit_cast(v8bf, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
-        acc[0][t] = mfma_bf16(vf, pb0, acc[0][t]);
-        acc[1][t] = mfma_bf16(vf, pb1, acc[1][t]);
+        acc[0][t] = mfma_bf16(vfr[t], pb0, acc[0][t]);
+        acc[1][t] = mfma_bf16(vfr[t], pb1, acc[1][t]);
       }
     }
     asm volatile("" ::: "memory");
