@@ -433,15 +433,18 @@ __global__ __launch_bounds__(256, (attn_blocks_per_cu<D, MODE, SEL>())) void spa
     for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
       for (int u2 = 0; u2 < 2; ++u2) sc[jt][u2] = v4f{0.f, 0.f, 0.f, 0.f};
+    v8bf kfr[2][KS];   // every K fragment read before the first MFMA
 #pragma unroll
-    for (int u2 = 0; u2 < 2; ++u2) {
+    for (int u2 = 0; u2 < 2; ++u2)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const v8bf kf = load_v8bf(Ks + krow_off[u2] + 8 * ((4 * ks + g) ^ kswz[u2]));
+      for (int ks = 0; ks < KS; ++ks) kfr[u2][ks] = load_v8bf(Ks + krow_off[u2] + 8 * ((4 * ks + g) ^ kswz[u2]));
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int jt = 0; jt < 2; ++jt) sc[jt][u2] = mfma_bf16(kf, qf[jt][ks], sc[jt][u2]);
-      }
-    }
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int u2 = 0; u2 < 2; ++u2)
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt) sc[jt][u2] = mfma_bf16(kfr[u2][ks], qf[jt][ks], sc[jt][u2]);
     // scale; bias (not on the exempt key) and causal / length masks where needed.
     // Interior blocks (no mask, no exempt key): for kCausalSelf the blocks
     // before the diagonal; otherwise full key blocks other than the one
