@@ -942,16 +942,24 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
       v4f X[NT];
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) X[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+      // the H fragments of column tile nt + 1 are read while tile nt's MFMAs run
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < 2; ++ks) {
+        v8bf hh_n = tr_frag<RC, swz_k256>(Sg, 32 * ks + 8 * lg, 0, lane);
+        v8bf hl_n = tr_frag<RC, swz_k256>(Sg + 64 * N, 32 * ks + 8 * lg, 0, lane);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-          const v8bf hh = tr_frag<RC, swz_k256>(Sg, 32 * ks + 8 * lg, 16 * nt, lane);
-          const v8bf hl = tr_frag<RC, swz_k256>(Sg + 64 * N, 32 * ks + 8 * lg, 16 * nt, lane);
+          const v8bf hh = hh_n, hl = hl_n;
+          if (nt + 1 < NT) {
+            hh_n = tr_frag<RC, swz_k256>(Sg, 32 * ks + 8 * lg, 16 * (nt + 1), lane);
+            hl_n = tr_frag<RC, swz_k256>(Sg + 64 * N, 32 * ks + 8 * lg, 16 * (nt + 1), lane);
+          }
+          __builtin_amdgcn_sched_barrier(0);
           X[nt] = mfma_bf16(hh, dyf[ks][0], X[nt]);
           X[nt] = mfma_bf16(hl, dyf[ks][0], X[nt]);
           X[nt] = mfma_bf16(hh, dyf[ks][1], X[nt]);
         }
+      }
       const float e = fast_exp2(dcc[k * hstride + tcl] * kLog2e);
       float s = 0.f;
 #pragma unroll
@@ -975,9 +983,12 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
       for (int ks = 0; ks < 2; ++ks) {
         const v8bf bh = tr_frag<8, swz_k128>(Dh, 32 * ks + 8 * lg, 16 * w, lane);
         const v8bf bl = tr_frag<8, swz_k128>(Dh + kPlaneT, 32 * ks + 8 * lg, 16 * w, lane);
+        v8bf a_n = tr_frag<RC, swz_k256>(Bt, 32 * ks + 8 * lg, 0, lane);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-          const v8bf a = tr_frag<RC, swz_k256>(Bt, 32 * ks + 8 * lg, 16 * nt, lane);
+          const v8bf a = a_n;
+          if (nt + 1 < NT) a_n = tr_frag<RC, swz_k256>(Bt, 32 * ks + 8 * lg, 16 * (nt + 1), lane);
+          __builtin_amdgcn_sched_barrier(0);
           dCT[nt] = mfma_bf16(a, bh, dCT[nt]);
           dCT[nt] = mfma_bf16(a, bl, dCT[nt]);
         }
