@@ -139,8 +139,11 @@ __device__ __forceinline__ void stage_rows(MT* lds, int ld, const TS* src, long 
         x[j] = (r < rvalid && k0 + j < kvalid) ? load_f32(src + r * rs + k0 + j) : 0.0f;
     }
     if constexpr (!SameT<Scale, NoScale>::value) {
+      // only in-range elements are scaled: past the valid rows or columns the
+      // scale may read a table entry nobody wrote, and 0 * NaN is NaN
 #pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] *= scale(r, k0 + j);
+      for (int j = 0; j < 8; ++j)
+        if (r < rvalid && k0 + j < kvalid) x[j] *= scale(r, k0 + j);
     }
     Store8<MT>::store(lds + r * ld + k0, x, plane);
   }
@@ -173,8 +176,10 @@ __device__ __forceinline__ void stage_transposed(MT* lds, int ld, const TS* src,
           x[i][j] = (r < rvalid && c0 + j < cvalid) ? load_f32(src + r * rs + c0 + j) : 0.0f;
       }
       if constexpr (!SameT<Scale, NoScale>::value) {
+        // only in-range elements are scaled (see stage_rows)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[i][j] *= scale(r, c0 + j);
+        for (int j = 0; j < 8; ++j)
+          if (r < rvalid && c0 + j < cvalid) x[i][j] *= scale(r, c0 + j);
       }
     }
 #pragma unroll

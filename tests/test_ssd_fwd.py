@@ -264,3 +264,39 @@ def test_ssd_fwd_bf16_fast_path_signed_limits(softplus, limit):
     y, h = run_fwd(x, 64, softplus=softplus, limit=limit)
     assert_parity(y, y_ref, torch.bfloat16, "y")
     assert_parity(h, h_ref, torch.bfloat16, "h_last")
+
+
+def _nan_into_lds():
+    """A GEMM of all-NaN matrices: its operand tiles fill tens of KB of LDS on
+    every CU with NaN, which the next kernels there find uninitialised."""
+    junk = torch.full((2048, 2048), float("nan"), device="cuda")
+    (junk @ junk).sum().item()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("chunk", [16, 48, 1])
+def test_ssd_short_chunk_ignores_stale_lds(chunk):
+    """Regression: with chunk_size not a multiple of 32 the fp32 kernels
+    stage positions past the chunk, whose scale entries were never written;
+    0 * (stale NaN) turned them into NaN outputs.  Fills LDS with NaN first,
+    then checks that every output and gradient is finite and matches the
+    oracle."""
+    print(f"ssd short chunk {chunk} after NaN in LDS", flush=True)
+    from selective_attention.ops import SSDScanFn
+    x = make_inputs(b=1, L=70, H=6, P=32, N=24, G=3, dtype=torch.float32, with_h=False,
+                    with_bias=False)
+    y_ref, h_ref = ref.ssd_scan_forward(**x, chunk_size=chunk)
+    for _ in range(3):
+        _nan_into_lds()
+        xd = {k: (v.cuda().requires_grad_(k in ("u", "B", "C", "delta_raw"))
+                  if isinstance(v, torch.Tensor) else v) for k, v in x.items()}
+        y, h = SSDScanFn.apply(xd["u"], xd["A"], xd["B"], xd["C"], xd["delta_raw"], None, None,
+                               None, chunk, True, (0.0, float("inf")), True)
+        _nan_into_lds()
+        grads = torch.autograd.grad((y,), [xd[k] for k in ("u", "B", "C", "delta_raw")],
+                                    (torch.ones_like(y),))
+        torch.cuda.synchronize()
+        assert_parity(y, y_ref, torch.float32, "y")
+        assert_parity(h, h_ref, torch.float32, "h_last")
+        for gname, gv in zip(("du", "dB", "dC", "ddelta_raw"), grads):
+            assert torch.isfinite(gv).all(), f"{gname}: non-finite values"
