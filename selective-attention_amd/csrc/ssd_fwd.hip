@@ -711,12 +711,19 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
         for (int t = 0; t < 4; ++t) acc[k][t] *= lf[k];
     }
     v4f cbt[4];
+    // step i = (ks, kt): the B fragment of step i + 1 is read while step i's
+    // MFMA runs, and consecutive MFMAs go to different accumulators
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      cbt[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-      const bf16* brow = Bs + key_of_row(kt, cl) * LDN + 8 * lg;
+    for (int kt = 0; kt < 4; ++kt) cbt[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+    v8bf bnx = load_v8bf(Bs + key_of_row(0, cl) * LDN + 8 * lg);
 #pragma unroll
-      for (int ks = 0; ks < NK; ++ks) cbt[kt] = mfma_bf16(load_v8bf(brow + 32 * ks), Cw[ks], cbt[kt]);
+    for (int i = 0; i < 4 * NK; ++i) {
+      const int ks = i / 4, kt = i % 4;
+      const v8bf bf = bnx;
+      if (i + 1 < 4 * NK)
+        bnx = load_v8bf(Bs + key_of_row((i + 1) % 4, cl) * LDN + 8 * lg + 32 * ((i + 1) / 4));
+      __builtin_amdgcn_sched_barrier(0);
+      cbt[kt] = mfma_bf16(bf, Cw[ks], cbt[kt]);
     }
 #pragma unroll
     for (int k = 0; k < HC; ++k) {
@@ -773,13 +780,22 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
     const bool more = k + 1 < nh;
     if (more) load_h(k + 1);
     const float e = fast_exp2(dct[k]);
+    {
+      v4f st[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      v4f st = v4f{0.f, 0.f, 0.f, 0.f};
-      const bf16* hrow2 = Hs + (16 * t + cl) * LDN + 8 * lg;
+      for (int t = 0; t < 4; ++t) st[t] = v4f{0.f, 0.f, 0.f, 0.f};
+      v8bf hnx = load_v8bf(Hs + cl * LDN + 8 * lg);
 #pragma unroll
-      for (int ks = 0; ks < NK; ++ks) st = mfma_bf16(load_v8bf(hrow2 + 32 * ks), Cw[ks], st);
-      acc[k][t] += st * e;
+      for (int i = 0; i < 4 * NK; ++i) {
+        const int ks = i / 4, t = i % 4;
+        const v8bf hf = hnx;
+        if (i + 1 < 4 * NK)
+          hnx = load_v8bf(Hs + (16 * ((i + 1) % 4) + cl) * LDN + 8 * lg + 32 * ((i + 1) / 4));
+        __builtin_amdgcn_sched_barrier(0);
+        st[t] = mfma_bf16(hf, Cw[ks], st[t]);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[k][t] += st[t] * e;
     }
     if (more) {
       __syncthreads();
