@@ -127,6 +127,19 @@ __device__ __forceinline__ int dma_off_w8(int i, int w, int lane, int grs) {
   return row * grs + 8 * (pc ^ (F(row) & (RC - 1)));
 }
 
+// Lane offset (elements) for DMA instruction i of wave w into a swz_k128
+// [sigma][tau] plane of a dCB tile.  The source kernel stores a tile in lane
+// order: dCB[tau = 8 c .. 8 c + 7][sigma] of plane p (hi, lo), c = 4 ks + lg,
+// is chunk q = 2 ks + p of lane (lg, li = sigma % 16) of wave sigma / 16, at
+// element 2048 q + 8 (64 wave + 4 li + lg).  This returns the hi plane's
+// chunk for the LDS position; the lo plane's is 2048 elements further on.
+__device__ __forceinline__ int dcb_lane_off(int i, int w, int lane) {
+  const int pos = (w * 2 + i) * 64 + lane;   // LDS chunk, 8 per 128-byte row
+  const int sigma = pos >> 3;
+  const int c = (pos & 7) ^ (swz_k128(sigma) & 7);
+  return 2 * (c >> 2) * 2048 + ((sigma >> 4) * 64 + (sigma & 15) * 4 + (c & 3)) * 8;
+}
+
 // fragment of 8 consecutive bf16 of one swizzled row
 template <int RC, int (*F)(int)>
 __device__ __forceinline__ v8bf row_frag(const bf16* t, int row, int col) {
@@ -431,11 +444,16 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 #pragma unroll
   for (int ks = 0; ks < NK; ++ks) o_c[ks] = toff<NK * 4, swz_k256>(rl, 32 * ks + 8 * lg);
 
-  // this lane's 64 bytes of the dCB planes of target strip Tp: 16 bytes at
-  // (hi, lo) x (rows 32 ks + 8 lg .. + 7) of column sl
-  auto dcb_at = [&](int Tp, int kt) -> bf16* {
-    return dcbp + ((bcg * stiles + S) * stiles + Tp) * (2L * kPlaneT) + sl * 64 + 8 * lg +
-           (kt & 1) * kPlaneT + 32 * (kt >> 1);
+  // this lane's 64 bytes of the dCB tile (S, Tp): chunk q = 2 ks + (hi, lo)
+  // holds dCB[tau = 64 Tp + 32 ks + 8 lg .. + 7][sigma = sig] of that plane.
+  // The tile is stored in lane order, chunk q of lane (lg, li) of wave w at
+  // byte 4096 q + 16 (64 w + 4 li + lg): each store instruction of a wave
+  // writes 1 KB of whole cache lines, and the four chunks of one sigma row
+  // (lg = 0..3) are 64 contiguous bytes for the target kernel's DMA, which
+  // puts the chunks back into [sigma][tau] order (dcb_lane_off).
+  auto dcb_at = [&](int Tp, int q) -> bf16* {
+    return dcbp + ((bcg * stiles + S) * stiles + Tp) * (2L * kPlaneT) + q * 2048 +
+           (w * 64 + li * 4 + lg) * 8;
   };
 
   // B of this lane's source row (all N) and u of this pass' heads there are
@@ -907,14 +925,17 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
       *reinterpret_cast<uint4*>(dst + 64 * N + off) = uint4{lo[0], lo[1], lo[2], lo[3]};
     }
   };
+  int o_dcb[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) o_dcb[i] = dcb_lane_off(i, w, lane);
   auto issue_intra = [&](int jj) {
     const int S = jj - HPG;
     bf16* dst = stg + (jj & 1) * SM::kStage;
     dma_tile<RC, swz_k256>(dst, Bc + static_cast<long>(64 * S) * act_rs, act_rs,
                            min(64, qlim - 64 * S), w, lane);
     const bf16* src = dcbp + ((bcg * ttiles + S) * ttiles + T) * (2L * kPlaneT);
-    dma_tile<8, swz_k128>(dst + 64 * N, src, 64, 64, w, lane);
-    dma_tile<8, swz_k128>(dst + 64 * N + kPlaneT, src + kPlaneT, 64, 64, w, lane);
+    dma_pre<8>(dst + 64 * N, src, o_dcb, w);
+    dma_pre<8>(dst + 64 * N + kPlaneT, src + 2048, o_dcb, w);
   };
 
   v4f dCT[NT];   // dC^T rows n = 16 nt + 4 lg + r, column tau
