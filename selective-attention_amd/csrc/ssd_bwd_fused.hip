@@ -140,6 +140,28 @@ __device__ __forceinline__ int dcb_lane_off(int i, int w, int lane) {
   return 2 * (c >> 2) * 2048 + ((sigma >> 4) * 64 + (sigma & 15) * 4 + (c & 3)) * 8;
 }
 
+// Output tiles leave through LDS.  A lane's 8-byte pieces of a row-major
+// [64 rows][RC 16-byte chunks] bf16 tile go in at chunk c ^ (row % RC), and
+// the tile goes out as whole rows, 16 bytes per lane: each store instruction
+// of a wave then writes whole cache lines (stored from the MFMA fragments,
+// one instruction wrote 32 bytes of each of 16 rows).
+template <int RC>
+__device__ __forceinline__ void stage_out8(bf16* t, int row, int col, uint2 v) {
+  const int c = col >> 3;
+  *reinterpret_cast<uint2*>(t + row * (RC * 8) + 8 * (c ^ (row & (RC - 1))) + (col & 7)) = v;
+}
+// rows r < rows_valid of a staged tile to g + r grs
+template <int RC>
+__device__ __forceinline__ void write_rows(const bf16* t, bf16* g, int grs, int rows_valid, int tid) {
+#pragma unroll
+  for (int i = 0; i < RC / 4; ++i) {
+    const int e = tid + 256 * i, r = e / RC, c = e % RC;
+    if (r < rows_valid)
+      *reinterpret_cast<uint4*>(g + static_cast<unsigned>(r * grs + 8 * c)) =
+          *reinterpret_cast<const uint4*>(t + r * (RC * 8) + 8 * (c ^ (r & (RC - 1))));
+  }
+}
+
 // fragment of 8 consecutive bf16 of one swizzled row
 template <int RC, int (*F)(int)>
 __device__ __forceinline__ v8bf row_frag(const bf16* t, int row, int col) {
@@ -782,6 +804,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     }
     flush_r(pass, n_stage(pass) - 1, HS == 1 ? ((ntile - 1) & 1) : HS - 1);
     finish_pair(S + ntile - 1, dCBa, prev);
+    // every wave is done with the stage buffers: they stage du (stg0) and dB (stg1)
+    __syncthreads();
 
     // ---- du, ddt_direct, q of this pass' heads ----
 #pragma unroll
@@ -794,11 +818,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
       for (int pt = 0; pt < 4; ++pt) sx += dot4_bf16(duT[h][pt], *reinterpret_cast<const uint2*>(urow + 16 * pt));
       sx = group_sum(sv ? sx : 0.f);
       const float qv = group_sum(qacc[h]);
-      if (sig < qlim) {
-        bf16* durow = duc + k * 64 + static_cast<unsigned>(sig * u_rs + 4 * lg);
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt) *reinterpret_cast<uint2*>(durow + 16 * pt) = pack4_bf16(duT[h][pt] * dtk[h]);
-      }
+      for (int pt = 0; pt < 4; ++pt) stage_out8<8>(stg0 + h * 4096, sl, 16 * pt + 4 * lg, pack4_bf16(duT[h][pt] * dtk[h]));
       if (lg == 0) {
         ddtc[k * hstride + sig] = sx;
         qc[k * hstride + sig] = qv;
@@ -808,11 +829,15 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   // row-sum partials of target strips past the length are zero
   for (int k = KB; k < KE; ++k)
     for (int t = 64 * (S + ntile) + tid; t < d.Lc; t += 256) rc[k * rstride + t] = 0.f;
-  if (last && sig < qlim) {
-    bf16* dbrow = dBc + static_cast<unsigned>(sig * act_rs + 4 * lg);
+  if (last) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<uint2*>(dbrow + 16 * nt) = pack4_bf16(dBT[nt]);
+    for (int nt = 0; nt < NT; ++nt) stage_out8<16>(stg1, sl, 16 * nt + 4 * lg, pack4_bf16(dBT[nt]));
   }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < HS; ++h)
+    if (KB + h < HPG) write_rows<8>(stg0 + h * 4096, duc + (KB + h) * 64 + s0 * u_rs, u_rs, qlim - s0, tid);
+  if (last) write_rows<16>(stg1, dBc + s0 * act_rs, act_rs, qlim - s0, tid);
 }
 
 // ---------------------------------------------------------------------------
@@ -1019,11 +1044,11 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  if (tau < qlim) {
-    bf16* row = dCc + static_cast<unsigned>(tau * act_rs + 4 * lg);
+  // (the loop ended with a barrier: the stage buffers are free)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<uint2*>(row + 16 * nt) = pack4_bf16(dCT[nt]);
-  }
+  for (int nt = 0; nt < NT; ++nt) stage_out8<16>(stg, tl, 16 * nt + 4 * lg, pack4_bf16(dCT[nt]));
+  __syncthreads();
+  write_rows<16>(stg, dCc + t0 * act_rs, act_rs, qlim - t0, tid);
 }
 
 // The host pass leaves the stubs of ssd_bwd_src_kernel undefined when it only
