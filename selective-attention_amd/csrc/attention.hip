@@ -163,10 +163,12 @@ __device__ __forceinline__ void softmax_lazy(v4f (&s)[KT], v4f (&o)[DT], float& 
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     if (mx > m + 8.0f) {   // the column's new reference
-      const float alpha = (m == kNegInf) ? 0.0f : fast_exp2(m - mx);
-      l *= alpha;
+      if (m != kNegInf) {   // (while m = -inf, every p so far was 0: l and o are 0)
+        const float alpha = fast_exp2(m - mx);
+        l *= alpha;
 #pragma unroll
-      for (int t = 0; t < DT; ++t) o[t] *= alpha;
+        for (int t = 0; t < DT; ++t) o[t] *= alpha;
+      }
       m = mx;
     }
   }
@@ -301,7 +303,7 @@ __global__ __launch_bounds__(256, (attn_blocks_per_cu<D, MODE, SEL>())) void spa
     my_kb = lane < max_blocks ? sel[lane] : -1;
     bool ok = my_kb >= 0 && my_kb < nkb && (MODE != kCausalSelf || my_kb <= jq);
     for (int j = 0; j + 1 < max_blocks; ++j) {
-      const int kj = __shfl(my_kb, j, 64);
+      const int kj = __builtin_amdgcn_readlane(my_kb, j);
       ok = ok && !(lane > j && my_kb == kj);
     }
     vmask = __ballot(ok);
@@ -552,6 +554,12 @@ __global__ __launch_bounds__(256, (attn_blocks_per_cu<D, MODE, SEL>())) void spa
   }
   __syncthreads();
   if (kh == 1) return;
+  // the wave's 32 merged rows, normalised, go out through LDS as whole rows
+  // (16 bytes per lane): [32 rows][D] bf16 in stage 1 past the m / l
+  // exchange, 16-byte chunk c of row r at c ^ (r % RCH)
+  constexpr int RCH = D / 8;
+  static_assert(1024 + 2 * 32 * D <= SM::stage, "output rows fit stage 1");
+  bf16* ot = stage1 + 1024 + qh * 32 * D;
 #pragma unroll
   for (int jt = 0; jt < 2; ++jt) {
     const float m1 = xm[(jt * 2) * 64 + lane], l1 = xm[(jt * 2 + 1) * 64 + lane];
@@ -560,16 +568,26 @@ __global__ __launch_bounds__(256, (attn_blocks_per_cu<D, MODE, SEL>())) void spa
     const float a1 = m1 == kNegInf ? 0.f : fast_exp2(m1 - mm);
     const float lt = l[jt] * a0 + l1 * a1;
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    if (qloc[jt] < n) {
-      bf16* orow = o + (start + static_cast<long>(qloc[jt])) * rs + static_cast<long>(h) * D;
+    const float b0 = a0 * inv, b1 = a1 * inv;
+    const int r = 16 * jt + c;
 #pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        const float4 o1 = xo[(jt * DT + t) * 64 + lane];
-        const float r0 = (acc[jt][t][0] * a0 + o1.x * a1) * inv, r1 = (acc[jt][t][1] * a0 + o1.y * a1) * inv;
-        const float r2 = (acc[jt][t][2] * a0 + o1.z * a1) * inv, r3 = (acc[jt][t][3] * a0 + o1.w * a1) * inv;
-        *reinterpret_cast<uint2*>(orow + 16 * t + 4 * g) = uint2{pack_bf16x2(r0, r1), pack_bf16x2(r2, r3)};
-      }
+    for (int t = 0; t < DT; ++t) {
+      const float4 o1 = xo[(jt * DT + t) * 64 + lane];
+      const float r0 = fmaf(acc[jt][t][0], b0, o1.x * b1), r1 = fmaf(acc[jt][t][1], b0, o1.y * b1);
+      const float r2 = fmaf(acc[jt][t][2], b0, o1.z * b1), r3 = fmaf(acc[jt][t][3], b0, o1.w * b1);
+      const int ch = 2 * t + (g >> 1);
+      *reinterpret_cast<uint2*>(ot + r * D + 8 * (ch ^ (r & (RCH - 1))) + 4 * (g & 1)) =
+          uint2{pack_bf16x2(r0, r1), pack_bf16x2(r2, r3)};
     }
+  }
+  const int q0 = jq * BS + 32 * qh;
+  bf16* obase = o + (start + static_cast<long>(q0)) * rs + static_cast<long>(h) * D;
+#pragma unroll
+  for (int i = 0; i < RCH / 2; ++i) {
+    const int e = lane + 64 * i, r = e / RCH, ch = e % RCH;
+    if (q0 + r < n)
+      *reinterpret_cast<uint4*>(obase + r * rs + 8 * ch) =
+          *reinterpret_cast<const uint4*>(ot + r * D + 8 * (ch ^ (r & (RCH - 1))));
   }
 }
 
