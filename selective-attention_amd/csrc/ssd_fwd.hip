@@ -803,7 +803,36 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
       __syncthreads();
     }
   }
-  if (tau < qlim) {
+  if constexpr (!GATED) {
+    // y leaves through LDS, two heads per round: lane pieces in at 16-byte
+    // chunk c ^ (row % 16) of [2][64 rows][64 p] fp32, then whole 256-byte
+    // rows out, 16 bytes per lane (stored from the fragments, one
+    // instruction wrote 64 bytes of each of 16 rows)
+    float* ys = reinterpret_cast<float*>(smem_raw);
+    const int rl = 16 * w + cl;
+#pragma unroll
+    for (int r2 = 0; r2 < (HC + 1) / 2; ++r2) {
+      __syncthreads();   // every wave is done with the LDS (last stage, previous round)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int k = 2 * r2 + s2;
+        if (k >= HC) break;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          *reinterpret_cast<float4*>(ys + s2 * 4096 + rl * 64 + 4 * ((4 * t + lg) ^ (rl & 15))) =
+              make_float4(acc[k][t][0], acc[k][t][1], acc[k][t][2], acc[k][t][3]);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int e = tid + 256 * i, s2 = e >> 10, r = (e >> 4) & 63, ch = e & 15;
+        const int k = 2 * r2 + s2;
+        if (k < nh && t0 + r < qlim && p0 + 4 * ch < d.P)
+          *reinterpret_cast<float4*>(y + (tok0 + t0 + r) * u_rs + static_cast<long>(h0 + k) * d.P + p0 + 4 * ch) =
+              *reinterpret_cast<const float4*>(ys + s2 * 4096 + r * 64 + 4 * (ch ^ (r & 15)));
+      }
+    }
+  } else if (tau < qlim) {
 #pragma unroll
     for (int k = 0; k < HC; ++k) {
       if (k >= nh) break;
@@ -828,8 +857,6 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
           }
           *reinterpret_cast<uint2*>(go.out + row + p) = uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
           *reinterpret_cast<uint2*>(go.yd + row + p) = uint2{pack_bf16x2(yd[0], yd[1]), pack_bf16x2(yd[2], yd[3])};
-        } else {
-          *reinterpret_cast<float4*>(y + row + p) = make_float4(acc[k][t][0], acc[k][t][1], acc[k][t][2], acc[k][t][3]);
         }
       }
     }
