@@ -253,26 +253,6 @@ __device__ __forceinline__ float transpose_reduce16(float (&m)[16], int li) {
 
 constexpr int kPlaneT = 64 * 64;   // bf16 elements of one 64 x 64 plane tile
 
-// Launch order of the strip kernels.  bid (after xcd_swizzle) runs on XCD
-// bid / per in slot order bid % per.  Each XCD takes a contiguous range of the
-// (b, c, g) tiles with all of their strips, and runs the strips in the order
-// of their rank j: every tile's rank-0 strip first, then rank 1, ...  The
-// kernels give rank 0 to their longest strips, so the short ones fill the
-// end of the launch instead of leaving CUs idle behind a long one.  Grids
-// that do not split evenly use the plain order (strip fastest).  The source
-// kernel uses it; its strips share little through L2.
-__device__ __forceinline__ void strip_order(int bid, int nblocks, int strips, int& j, int& rest) {
-  const int per = nblocks / 8;
-  if (nblocks % 8 == 0 && per % strips == 0) {
-    const int q = per / strips, xcd = bid / per, slot = bid - xcd * per;
-    j = slot / q;
-    rest = xcd * q + (slot - j * q);
-  } else {
-    j = bid % strips;
-    rest = bid / strips;
-  }
-}
-
 // index of this thread's wave in the block, as a wave-uniform (scalar) value
 __device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
@@ -341,9 +321,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 
   const int stiles = d.Lc / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  // source strip S has 4 - S target strips: S = 0 first
-  int S, rest;
-  strip_order(bid, gridDim.x, stiles, S, rest);
+  const int S = bid % stiles;
+  int rest = bid / stiles;
   const int g = rest % d.G;
   rest /= d.G;
   const int c = rest % d.nc;
@@ -887,8 +866,6 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
 
   const int ttiles = d.Lc / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  // (strip fastest: the four target strips of a tile read its B tiles and
-  // states together, from L2; run longest first they were slower)
   const int T = bid % ttiles;
   int rest = bid / ttiles;
   const int g = rest % d.G;
