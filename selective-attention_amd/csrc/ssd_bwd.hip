@@ -739,8 +739,8 @@ __global__ __launch_bounds__(256) void chunk_cumsum_bwd_kernel(
     const float* __restrict__ xB_part, const float* __restrict__ xC_part,
     const float* __restrict__ rsum, const float* __restrict__ qpart,
     const float* __restrict__ ddc_part, T* __restrict__ ddelta_raw, float* __restrict__ dA_part,
-    float* __restrict__ db_part, SsdDims d, int ptiles, int ntiles, int ttiles, int rtiles,
-    int per_bh, int has_init, int softplus, float lo, float hi) {
+    float* __restrict__ db_part, SsdDims d, int ptiles, int ntiles, int xctiles, int ttiles,
+    int rtiles, int per_bh, int has_init, int softplus, float lo, float hi) {
   __shared__ float wtot[4 * 3];
   const int h = blockIdx.x % d.H;
   const int c = (blockIdx.x / d.H) % d.nc;
@@ -765,10 +765,8 @@ __global__ __launch_bounds__(256) void chunk_cumsum_bwd_kernel(
     if (j < per && t < d.Lc) {
       float q = 0.f, x1 = 0.f, x2 = 0.f;
       for (int k = 0; k < ttiles; ++k) q += qpart[(bhc * ttiles + k) * d.Lc + t];
-      for (int k = 0; k < ntiles; ++k) {
-        x1 += xB_part[(bhc * ntiles + k) * d.Lc + t];
-        x2 += xC_part[(bhc * ntiles + k) * d.Lc + t];
-      }
+      for (int k = 0; k < ntiles; ++k) x1 += xB_part[(bhc * ntiles + k) * d.Lc + t];
+      for (int k = 0; k < xctiles; ++k) x2 += xC_part[(bhc * xctiles + k) * d.Lc + t];
       // row sums: partials of the source tiles k <= t / 64 (rtiles == 1: complete)
       float r = 0.f;
       for (int k = 0; k < rtiles && 64 * k <= t; ++k) r += rsum[(bhc * rtiles + k) * d.Lc + t];
@@ -930,7 +928,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
                        dh_last, dh_init, dc, ddc_part, fused ? dSp : nullptr, d);
     SA_CHECK_LAUNCH("state_passing_bwd");
   }
-  int ptiles = w.ptiles, ntiles = w.ntiles, qtiles = w.ttiles, rtiles = 1;
+  int ptiles = w.ptiles, ntiles = w.ntiles, xctiles = w.ntiles, qtiles = w.ttiles, rtiles = 1;
   if (fused) {
     // 3-5 fused: du, dB, dC, decay sums
     if ((rc = launch_ssd_bwd_fused(u, Bm, Cm, dyp, dt, dc, states, dSp, length, du_, dB_, dC_,
@@ -938,6 +936,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
                                    lo >= 0.f, s)))
       return rc;
     ptiles = ntiles = qtiles = 1;
+    xctiles = 2;   // x_C: one partial per half of N (ssd_bwd_tgt)
     rtiles = d.Lc / 64;
   } else {
   // 3. du, ddt_direct
@@ -978,7 +977,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
     hipLaunchKernelGGL(chunk_cumsum_bwd_kernel<T>, dim3(blocks), dim3(256), 0, s,
                        static_cast<const T*>(delta_raw_), A, bias, length, dt, ddt_part, xB_part,
                        xC_part, rsum, qpart, ddc_part, static_cast<T*>(ddelta_), dA_part, db_part,
-                       d, ptiles, ntiles, qtiles, rtiles, w.per_bh, has_init, sp, lo, hi);
+                       d, ptiles, ntiles, xctiles, qtiles, rtiles, w.per_bh, has_init, sp, lo, hi);
     SA_CHECK_LAUNCH("chunk_cumsum_bwd");
   }
   // 7. dA, dbias

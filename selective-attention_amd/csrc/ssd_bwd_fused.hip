@@ -841,38 +841,47 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// target-strip kernel: dC and x_C
+// target-strip kernel: dC and x_C.  One block per (b, c, group, target strip
+// T, half of N): the two halves of a strip split every product over n (no
+// MFMA is done twice), run side by side (half is the fastest block index)
+// and share dy and the dCB tiles through L2.  A stage is 24 KB of LDS and a
+// block holds two, so three blocks share a CU.  x_C is a sum over n: each
+// half writes its own partial (slot 2 bhc + half).
 // ---------------------------------------------------------------------------
 template <int NK>
 struct TgtSmem {
-  static constexpr int N = 32 * NK;
-  // a stage: H_in of one head (hi, lo: 2 x 64 x N) or B_S (64 x N) + dCB^T (hi, lo: 2 x 64 x 64)
-  static constexpr int kStage = 2 * 64 * N > 64 * N + 2 * kPlaneT ? 2 * 64 * N : 64 * N + 2 * kPlaneT;
+  static constexpr int NH = 16 * NK;   // n of one half
+  // a stage: this half of H_in of one head (hi, lo: 2 x 64 x NH) or this
+  // half of B_S (64 x NH) + dCB^T (hi, lo: 2 x 64 x 64)
+  static constexpr int kStage = 2 * 64 * NH > 64 * NH + 2 * kPlaneT ? 2 * 64 * NH : 64 * NH + 2 * kPlaneT;
   static constexpr size_t bytes = 2 * kStage * 2;
 };
 
 template <int NK, int HPG>
-__global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
+__global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
     const bf16* __restrict__ Bm, const bf16* __restrict__ Cm, const bf16* __restrict__ dyp,
     const float* __restrict__ dc, const float* __restrict__ states,
     const bf16* __restrict__ dcbp, const int64_t* __restrict__ length, bf16* __restrict__ dC,
     float* __restrict__ xC_part, SsdDims d) {
   using SM = TgtSmem<NK>;
-  constexpr int N = SM::N;
-  constexpr int NT = N / 16;
-  constexpr int RC = N / 8;   // 16-byte chunks per row of an N-wide tile
+  constexpr int N = 32 * NK;
+  constexpr int NH = SM::NH;
+  static_assert(NH == 64, "ssd_bwd_tgt: state_dim 128");
+  constexpr int NTH = NH / 16;   // n tiles of this half
   extern __shared__ __align__(16) unsigned char smem_raw[];
   bf16* stg = reinterpret_cast<bf16*>(smem_raw);   // [2][kStage]
 
   const int ttiles = d.Lc / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int T = bid % ttiles;
-  int rest = bid / ttiles;
+  const int half = bid & 1;
+  int rest = bid >> 1;
+  const int T = rest % ttiles;
+  rest /= ttiles;
   const int g = rest % d.G;
   rest /= d.G;
   const int c = rest % d.nc;
   const int b = rest / d.nc;
-  const int t0 = 64 * T;
+  const int t0 = 64 * T, n0 = NH * half;
   const int qlim = min(d.Lc, d.L - c * d.Lc);
   const int len = seq_limit(length, b, d.L);
   const int lim = max(0, chunk_limit(len, c, d.Lc));
@@ -886,31 +895,31 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
   const long bhc0 = (static_cast<long>(b) * d.H + h0) * d.nc + c;
   const int hstride = d.nc * d.Lc;
   const long bcg = (static_cast<long>(b) * d.nc + c) * d.G + g;
-  const bf16* Bc = Bm + tok0 * act_rs + static_cast<long>(g) * N;
-  const bf16* Cc = Cm + tok0 * act_rs + static_cast<long>(g) * N;
-  const float* Hc = states + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (64L * N);
+  const bf16* Bc = Bm + tok0 * act_rs + static_cast<long>(g) * N + n0;
+  const bf16* Cc = Cm + tok0 * act_rs + static_cast<long>(g) * N + n0;
+  const float* Hc = states + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (64L * N) + n0;
   const float* dcc = dc + bhc0 * d.Lc;
-  bf16* dCc = dC + tok0 * act_rs + static_cast<long>(g) * N;
-  float* xCc = xC_part + bhc0 * d.Lc;
+  bf16* dCc = dC + tok0 * act_rs + static_cast<long>(g) * N + n0;
+  float* xCc = xC_part + (bhc0 * 2 + half) * d.Lc;   // head k: + 2 k hstride
 
   if (t0 >= lim) {
-    for (int e = tid; e < 64 * (N / 8); e += 256) {
-      const int row = e / (N / 8), col8 = e % (N / 8);
+    for (int e = tid; e < 64 * (NH / 8); e += 256) {
+      const int row = e / (NH / 8), col8 = e % (NH / 8);
       if (t0 + row < qlim)
         *reinterpret_cast<uint4*>(dCc + static_cast<unsigned>((t0 + row) * act_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
     }
     for (int k = 0; k < HPG; ++k)
-      if (tid < 64) xCc[k * hstride + t0 + tid] = 0.f;
+      if (tid < 64) xCc[2 * k * hstride + t0 + tid] = 0.f;
     return;
   }
 
   const int tcl = min(tau, qlim - 1);   // clamped target row (a valid address)
-  // C of this lane's row at the dC^T fragment positions n = 16 nt + 4 lg + r
-  uint2 cv[NT];
+  // C of this lane's row at the dC^T fragment positions n = n0 + 16 nt + 4 lg + r
+  uint2 cv[NTH];
   {
     const bf16* crow = Cc + static_cast<unsigned>(tcl * act_rs + 4 * lg);
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) cv[nt] = *reinterpret_cast<const uint2*>(crow + 16 * nt);
+    for (int nt = 0; nt < NTH; ++nt) cv[nt] = *reinterpret_cast<const uint2*>(crow + 16 * nt);
   }
   // dy planes of this lane's row: [head][k step][hi, lo]
   const bf16* dyg = dyp + ((bcg * ttiles + T) * HPG) * (2L * kPlaneT) + tl * 64 + 8 * lg;
@@ -922,21 +931,20 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
     }
   };
 
-  // stage j: j < HPG: H_in of head j (fp32 -> hi, lo through registers);
-  // then S = j - HPG = 0..T: B_S and dCB^T of (S, T) by DMA
+  // stage j: j < HPG: this half of H_in of head j (fp32 -> hi, lo through
+  // registers); then S = j - HPG = 0..T: this half of B_S and dCB^T of (S, T) by DMA
   const int nstage = HPG + T + 1;
-  float4 ph[8];   // H prefetch: row tid / 4, columns 32 (tid % 4) .. +31 (N = 128)
-  static_assert(NK == 4, "ssd_bwd_tgt: state_dim 128");
+  float4 ph[4];   // H prefetch: row tid / 4, columns n0 + 16 (tid % 4) .. +15
   auto load_h = [&](int k) {
-    const float* src = Hc + k * (64L * N) + (tid >> 2) * N + 32 * (tid & 3);
+    const float* src = Hc + k * (64L * N) + (tid >> 2) * N + 16 * (tid & 3);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ph[i] = *reinterpret_cast<const float4*>(src + 4 * i);
+    for (int i = 0; i < 4; ++i) ph[i] = *reinterpret_cast<const float4*>(src + 4 * i);
   };
   auto commit_h = [&](int jj) {
     bf16* dst = stg + (jj & 1) * SM::kStage;
     const int row = tid >> 2;
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {   // 16-byte chunks 4 (tid % 4) + cc
+    for (int cc = 0; cc < 2; ++cc) {   // 16-byte chunks 2 (tid % 4) + cc
       const float v[8] = {ph[2 * cc].x, ph[2 * cc].y, ph[2 * cc].z, ph[2 * cc].w,
                           ph[2 * cc + 1].x, ph[2 * cc + 1].y, ph[2 * cc + 1].z, ph[2 * cc + 1].w};
       uint32_t hi[4], lo[4];
@@ -945,9 +953,9 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
         hi[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
         lo[e] = pack_bf16x2(v[2 * e] - bf16lo_to_f32(hi[e]), v[2 * e + 1] - bf16hi_to_f32(hi[e]));
       }
-      const int off = toff<RC, swz_k256>(row, 8 * (4 * (tid & 3) + cc));
+      const int off = toff<8, swz_k128>(row, 8 * (2 * (tid & 3) + cc));
       *reinterpret_cast<uint4*>(dst + off) = uint4{hi[0], hi[1], hi[2], hi[3]};
-      *reinterpret_cast<uint4*>(dst + 64 * N + off) = uint4{lo[0], lo[1], lo[2], lo[3]};
+      *reinterpret_cast<uint4*>(dst + 64 * NH + off) = uint4{lo[0], lo[1], lo[2], lo[3]};
     }
   };
   int o_dcb[2];
@@ -956,16 +964,16 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
   auto issue_intra = [&](int jj) {
     const int S = jj - HPG;
     bf16* dst = stg + (jj & 1) * SM::kStage;
-    dma_tile<RC, swz_k256>(dst, Bc + static_cast<long>(64 * S) * act_rs, act_rs,
-                           min(64, qlim - 64 * S), w, lane);
+    dma_tile<8, swz_k128>(dst, Bc + static_cast<long>(64 * S) * act_rs, act_rs,
+                          min(64, qlim - 64 * S), w, lane);
     const bf16* src = dcbp + ((bcg * ttiles + S) * ttiles + T) * (2L * kPlaneT);
-    dma_pre<8>(dst + 64 * N, src, o_dcb, w);
-    dma_pre<8>(dst + 64 * N + kPlaneT, src + 2048, o_dcb, w);
+    dma_pre<8>(dst + 64 * NH, src, o_dcb, w);
+    dma_pre<8>(dst + 64 * NH + kPlaneT, src + 2048, o_dcb, w);
   };
 
-  v4f dCT[NT];   // dC^T rows n = 16 nt + 4 lg + r, column tau
+  v4f dCT[NTH];   // dC^T rows n = n0 + 16 nt + 4 lg + r, column tau
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) dCT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int nt = 0; nt < NTH; ++nt) dCT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
   v8bf dyf[2][2], dyn[2][2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) dyn[ks][0] = dyn[ks][1] = zero_v8bf();
@@ -985,20 +993,20 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
     if (j < HPG) {
       // X^T[n, tau] = sum_p H[p, n] dy[tau, p]; dC^T += e^{dc_tau} X^T; x_C
       const int k = j;
-      v4f X[NT];
+      v4f X[NTH];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) X[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int nt = 0; nt < NTH; ++nt) X[nt] = v4f{0.f, 0.f, 0.f, 0.f};
       // the H fragments of column tile nt + 1 are read while tile nt's MFMAs run
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        v8bf hh_n = tr_frag<RC, swz_k256>(Sg, 32 * ks + 8 * lg, 0, lane);
-        v8bf hl_n = tr_frag<RC, swz_k256>(Sg + 64 * N, 32 * ks + 8 * lg, 0, lane);
+        v8bf hh_n = tr_frag<8, swz_k128>(Sg, 32 * ks + 8 * lg, 0, lane);
+        v8bf hl_n = tr_frag<8, swz_k128>(Sg + 64 * NH, 32 * ks + 8 * lg, 0, lane);
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
+        for (int nt = 0; nt < NTH; ++nt) {
           const v8bf hh = hh_n, hl = hl_n;
-          if (nt + 1 < NT) {
-            hh_n = tr_frag<RC, swz_k256>(Sg, 32 * ks + 8 * lg, 16 * (nt + 1), lane);
-            hl_n = tr_frag<RC, swz_k256>(Sg + 64 * N, 32 * ks + 8 * lg, 16 * (nt + 1), lane);
+          if (nt + 1 < NTH) {
+            hh_n = tr_frag<8, swz_k128>(Sg, 32 * ks + 8 * lg, 16 * (nt + 1), lane);
+            hl_n = tr_frag<8, swz_k128>(Sg + 64 * NH, 32 * ks + 8 * lg, 16 * (nt + 1), lane);
           }
           __builtin_amdgcn_sched_barrier(0);
           X[nt] = mfma_bf16(hh, dyf[ks][0], X[nt]);
@@ -1009,13 +1017,13 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
       const float e = fast_exp2(dcc[k * hstride + tcl] * kLog2e);
       float s = 0.f;
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
+      for (int nt = 0; nt < NTH; ++nt) {
         X[nt] *= e;
         s += dot4_bf16(X[nt], cv[nt]);
         dCT[nt] += X[nt];
       }
       s = group_sum(s);
-      if (lg == 0) xCc[k * hstride + tau] = tau < lim ? s : 0.f;
+      if (lg == 0) xCc[2 * k * hstride + tau] = tau < lim ? s : 0.f;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         dyf[ks][0] = dyn[ks][0];
@@ -1024,16 +1032,16 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
     } else {
       // dC^T[n, tau] += sum_sig B[sig, n] dCB[tau, sig]
       const bf16* Bt = Sg;
-      const bf16* Dh = Sg + 64 * N;
+      const bf16* Dh = Sg + 64 * NH;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const v8bf bh = tr_frag<8, swz_k128>(Dh, 32 * ks + 8 * lg, 16 * w, lane);
         const v8bf bl = tr_frag<8, swz_k128>(Dh + kPlaneT, 32 * ks + 8 * lg, 16 * w, lane);
-        v8bf a_n = tr_frag<RC, swz_k256>(Bt, 32 * ks + 8 * lg, 0, lane);
+        v8bf a_n = tr_frag<8, swz_k128>(Bt, 32 * ks + 8 * lg, 0, lane);
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
+        for (int nt = 0; nt < NTH; ++nt) {
           const v8bf a = a_n;
-          if (nt + 1 < NT) a_n = tr_frag<RC, swz_k256>(Bt, 32 * ks + 8 * lg, 16 * (nt + 1), lane);
+          if (nt + 1 < NTH) a_n = tr_frag<8, swz_k128>(Bt, 32 * ks + 8 * lg, 16 * (nt + 1), lane);
           __builtin_amdgcn_sched_barrier(0);
           dCT[nt] = mfma_bf16(a, bh, dCT[nt]);
           dCT[nt] = mfma_bf16(a, bl, dCT[nt]);
@@ -1046,9 +1054,9 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_tgt_kernel(
   }
   // (the loop ended with a barrier: the stage buffers are free)
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) stage_out8<16>(stg, tl, 16 * nt + 4 * lg, pack4_bf16(dCT[nt]));
+  for (int nt = 0; nt < NTH; ++nt) stage_out8<8>(stg, tl, 16 * nt + 4 * lg, pack4_bf16(dCT[nt]));
   __syncthreads();
-  write_rows<16>(stg, dCc + t0 * act_rs, act_rs, qlim - t0, tid);
+  write_rows<8>(stg, dCc + t0 * act_rs, act_rs, qlim - t0, tid);
 }
 
 // The host pass leaves the stubs of ssd_bwd_src_kernel undefined when it only
@@ -1104,7 +1112,7 @@ int launch_fused_hpg(const void* u, const void* B, const void* C, const bf16* dy
     const size_t smem = TgtSmem<NK>::bytes;
     if (const int rc = raise_smem(ssd_bwd_tgt_kernel<NK, HPG>, smem, "ssd_bwd_tgt")) return rc;
     ProfScope prof_("ssd_bwd_tgt", s);
-    hipLaunchKernelGGL((ssd_bwd_tgt_kernel<NK, HPG>), dim3(blocks), dim3(256), smem, s,
+    hipLaunchKernelGGL((ssd_bwd_tgt_kernel<NK, HPG>), dim3(2 * blocks), dim3(256), smem, s,
                        static_cast<const bf16*>(B), static_cast<const bf16*>(C), dyp, dc, states,
                        dcbp, length, static_cast<bf16*>(dC), xC_part, d);
     SA_CHECK_LAUNCH("ssd_bwd_tgt");
