@@ -17,9 +17,10 @@
 //       x_B, ddt_direct, the column sums q and (per source strip) row sums r
 //       of M = W o CB for the decay gradient, and dCB of every target strip
 //       T >= S (bf16 hi + lo planes, [sigma][tau], read by ssd_bwd_tgt)
-//   ssd_bwd_tgt (one block per (b, c, group, target strip T), 4 waves; wave w
-//     owns the 16 target rows tau = 64 T + 16 w + lane % 16):
+//   ssd_bwd_tgt (one block per (b, c, group, target strip T, half of N), 4
+//     waves; wave w owns the 16 target rows tau = 64 T + 16 w + lane % 16):
 //       dC     = sum_h e^{dc} dy_h.H_in_h  +  sum_{S <= T} dCB B,  and x_C
+//     (x_C as one partial per half)
 //
 // Operands reach LDS by DMA (global_load_lds, 16 bytes per lane) from bf16
 // planes written by the kernels before them: dy as hi + lo planes (by the
