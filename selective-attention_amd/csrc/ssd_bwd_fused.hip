@@ -724,15 +724,20 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
           const float* atT = ats + (T & 1) * HPG * 64 + 64 * k;
           const float dk = dck[h], dtv = dtk[h];
           // W[t, sig] = dy[t] . u[sig]
+          // the four row tiles' accumulators in turn, one (k step, plane)
+          // slice at a time: no MFMA waits on the one before it
           v4f W[4];
 #pragma unroll
-          for (int kt = 0; kt < 4; ++kt) {
-            W[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+          for (int kt = 0; kt < 4; ++kt) W[kt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-              W[kt] = mfma_bf16(load_v8bf(Yh + o_w[ks] + kro(kt) * 64), uf[ks], W[kt]);
-              W[kt] = mfma_bf16(load_v8bf(Yl + o_w[ks] + kro(kt) * 64), uf[ks], W[kt]);
-            }
+          for (int q2 = 0; q2 < 4; ++q2) {
+            const int ks = q2 >> 1;
+            const bf16* Yp = (q2 & 1) ? Yl : Yh;
+            v8bf f[4];
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) f[kt] = load_v8bf(Yp + o_w[ks] + kro(kt) * 64);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) W[kt] = mfma_bf16(f[kt], uf[ks], W[kt]);
             __builtin_amdgcn_sched_barrier(0);   // bound the operand reads in flight
           }
           // decay and masks: dCB += W', M = W' o CB (q: column sums, r: row sums); W <- L
