@@ -80,6 +80,12 @@ FUSED_CASES = [
     # three heads per group: two source launches, the second with one head (dB parked between them)
     ("hpg3_n128", dict(b=2, L=256, H=6, P=64, N=128, G=2, lens=[256, 171]), 128),
     ("zero_len", dict(b=2, L=128, H=4, P=64, N=64, G=1, lens=[0, 65], with_h=False), 64),
+    # fused path: a zero-length row next to full and partial ones (every strip
+    # of that row takes the kernels' early exits), two heads per group
+    ("hpg2_zero_len", dict(b=3, L=192, H=4, P=64, N=128, G=2, lens=[192, 0, 100]), 64),
+    # fused path, four heads per group, the last chunk 72 rows long (a strip
+    # of 8 rows) and the length ending inside its first strip
+    ("hpg4_tail", dict(b=1, L=200, H=8, P=64, N=128, G=2, lens=[190]), 128),
     # two P tiles, three N slices: bf16 chunk-state / dH_intra kernels, generic column / row kernels
     ("p128_n192", dict(b=2, L=600, H=2, P=128, N=192, G=1, lens=[600, 389]), 256),
 ]
