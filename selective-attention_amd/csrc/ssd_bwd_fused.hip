@@ -383,10 +383,16 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   const int scl = min(sig, lim - 1);       // clamped source row (a valid address)
   const int ntile = (lim + 63) / 64 - S;   // target strips T = S .. S + ntile - 1
 
-  // Stages of pass p: first the state stages, dS n half (j % NH) of head
-  // p HS + j / NH; then per target strip T = S + Ti the dy tile of head
-  // p HS + h, h = 0..HS-1 (C_T and the dc tables come with h == 0).
-  auto n_state = [&](int) { return HS * NH; };
+  // Stages of pass p: first one state stage per head p HS + j, its dS n
+  // half 0 in the stage buffer and n half 1 in a C buffer (no C tile is in
+  // use before the pair stages); then per target strip T = S + Ti the dy
+  // tile of head p HS + h, h = 0..HS-1 (C_T and the dc tables come with
+  // h == 0).
+  auto n_state = [&](int) { return HS; };
+  // C buffers: strip T's tile goes into buffer (T - S) & 1, and state stage j
+  // takes buffer (HS - j) & 1, a compile-time choice (the last state stage
+  // takes buffer 1, which the first pair stage's tile does not go into)
+  auto state_cpar = [&](int j) { return (HS - j) & 1; };
   auto n_stage = [&](int p) { return n_state(p) + HS * ntile; };
   const bf16* dyg = dyp + (bcg * stiles) * (HPG * 2L * kPlaneT);   // + (T HPG + k) 2 kPlaneT
   const bf16* dSg = dSp + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (2L * 64 * N);
@@ -404,11 +410,14 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     bf16* dst = stg(par);
     const int nst = n_state(p);
     if (j < nst) {
-      const int k = p * HS + j / NH, half = j % NH;
+      const int k = p * HS + j;
       if (k < HPG) {
-        const bf16* src = dSg + k * (2L * 64 * N) + 64 * half;
+        const bf16* src = dSg + k * (2L * 64 * N);
+        bf16* cdst = Cs(state_cpar(j));
         dma_pre<8>(dst, src, o_gs, w);
         dma_pre<8>(dst + kPlaneT, src + 64L * N, o_gs, w);
+        dma_pre<8>(cdst, src + 64, o_gs, w);
+        dma_pre<8>(cdst + kPlaneT, src + 64 + 64L * N, o_gs, w);
       }
     } else {
       const int qq = j - nst, Ti = qq / HS, h = qq % HS, T = S + Ti, k = p * HS + h;
@@ -419,7 +428,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
       }
       if (h == 0) {
         const int t0 = 64 * T;
-        bf16* cdst = Cs(T & 1);
+        bf16* cdst = Cs((T - S) & 1);
         const bf16* csrc = Cc + static_cast<long>(t0) * act_rs;
         if (qlim - t0 >= 64) dma_pre<NK * 4>(cdst, csrc, o_gc, w);
         else dma_tile<NK * 4, swz_k256>(cdst, csrc, act_rs, qlim - t0, w, lane);
@@ -513,13 +522,13 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) dBT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
   }
-  issue(pass, 0, 0);
+  issue(pass, 0, n_state(pass) & 1);   // stage j has buffer parity (j + n_state) & 1
   wait_all_mem();
   __syncthreads();
 
-  // Stage buffers alternate; the state stages number NH = 2 per head and the
-  // pair stages HS per target strip, so a state stage's buffer is its n half
-  // and a pair stage's its head (with one head per pass, its strip's parity).
+  // Stage buffers alternate: stage j has buffer parity (j + HS) & 1, so a
+  // pair stage's buffer is its head (with one head per pass, its strip's
+  // parity).
   // Each stage issues its own register loads before the next stage's DMA, so
   // that waiting for them does not wait for the DMA.
   {
@@ -570,56 +579,52 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
       for (int h = 0; h < HS; ++h) {
         const int k = pass * HS + h;
         const bool kv = k < HPG;
+        const int j = h, par = (h + HS) & 1;
+        v8bf Bf[NK], ul[2] = {Uh[h][0], Uh[h][1]};
 #pragma unroll
-        for (int half = 0; half < NH; ++half) {
-          const int j = h * NH + half;
-          v8bf Bf[2] = {Bh[2 * half], Bh[2 * half + 1]};
-          v8bf ul[2] = {Uh[h][0], Uh[h][1]};
-          uint2 ux[4];    // u of head k at this lane's column, for x_B
-          if (kv) {
-            if (!kHold) {
-              const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
+        for (int ks = 0; ks < NK; ++ks) Bf[ks] = Bh[ks];
+        uint2 ux[4];    // u of head k at this lane's column, for x_B
+        if (kv && !kHold) {
+          const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
 #pragma unroll
-              for (int ks = 0; ks < 2; ++ks) {
-                Bf[ks] = sv ? load_v8bf(brow + 64 * half + 32 * ks) : zero_v8bf();
-                ul[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
-              }
-            }
-            if (half == NH - 1) {
+          for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) ul[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+        }
+        __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the DMA
+        issue_next(pass, j, par);
+        if (kv) {
+#pragma unroll
+          for (int half = 0; half < NH; ++half) {
+            if (half == NH - 1) {   // read under the last half's MFMAs
               const bf16* urow4 = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
 #pragma unroll
               for (int pt = 0; pt < 4; ++pt) ux[pt] = *reinterpret_cast<const uint2*>(urow4 + 16 * pt);
             }
-          }
-          __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the DMA
-          issue_next(pass, j, half);
-          const bf16* Yh = stg(half);
-          const bf16* Yl = Yh + kPlaneT;
-          if (kv) {
+            const bf16* Yh = half ? Cs(state_cpar(j)) : stg(par);
+            const bf16* Yl = Yh + kPlaneT;
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
               for (int pt = 0; pt < 4; ++pt) {
                 const int off = o_sd[ks] + 16 * pt * 64;
-                duT[h][pt] = mfma_bf16(load_v8bf(Yh + off), Bf[ks], duT[h][pt]);
-                duT[h][pt] = mfma_bf16(load_v8bf(Yl + off), Bf[ks], duT[h][pt]);
+                duT[h][pt] = mfma_bf16(load_v8bf(Yh + off), Bf[2 * half + ks], duT[h][pt]);
+                duT[h][pt] = mfma_bf16(load_v8bf(Yl + off), Bf[2 * half + ks], duT[h][pt]);
               }
             state_dB(Yh, ul, ekh[h] * dtk[h], half);
-            if (half == NH - 1) {
-              // head k's state part is complete: scale by e^{dc_last - dc_sig}; x_B
-              const float ek = ekh[h];
-              float sx = 0.f;
-#pragma unroll
-              for (int pt = 0; pt < 4; ++pt) {
-                duT[h][pt] *= ek;
-                sx += dot4_bf16(duT[h][pt], ux[pt]);
-              }
-              sx = group_sum(sv ? sx : 0.f) * dtk[h];
-              if (lg == 0) xBc[k * hstride + sig] = sx;
-            }
           }
-          end_stage(pass, j + 1);
+          // head k's state part is complete: scale by e^{dc_last - dc_sig}; x_B
+          const float ek = ekh[h];
+          float sx = 0.f;
+#pragma unroll
+          for (int pt = 0; pt < 4; ++pt) {
+            duT[h][pt] *= ek;
+            sx += dot4_bf16(duT[h][pt], ux[pt]);
+          }
+          sx = group_sum(sv ? sx : 0.f) * dtk[h];
+          if (lg == 0) xBc[k * hstride + sig] = sx;
         }
+        end_stage(pass, j + 1);
       }
     }
     if constexpr (!last) {   // the state part of dB for the last pass
@@ -648,7 +653,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) dCBa[kt] += v4f{prev[kt].x, prev[kt].y, prev[kt].z, prev[kt].w};
       }
-      const bf16* Cb = Cs(Tp & 1);
+      const bf16* Cb = Cs((Tp - S) & 1);
       const int ctb = tr_first<NK * 4, swz_k256>(8 * lg, 0, lane);   // column tile 0
       const int cfx = 16 * (swz_k256(8 * lg + ((lane & 15) >> 2)) >> 1);
 #pragma unroll
@@ -674,7 +679,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     float4 prev[4];
     for (int Ti = 0; Ti < ntile; ++Ti) {
       const int T = S + Ti, t0 = 64 * T;
-      const bf16* Cb = Cs(T & 1);
+      const bf16* Cb = Cs((T - S) & 1);
       const bool diag = Ti == 0;
       const bool fact = !diag && mono;
       v4f CB[4];
