@@ -494,10 +494,11 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   // them (where each load's latency was exposed).  The last pass has no
   // registers to spare and loads them per stage.
   constexpr bool kHold = !last;
+  constexpr bool kHoldB = true;   // B of the source row: every pass
   const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 8 * lg);
   v8bf Bh[NK], Uh[HS][2];
 #pragma unroll
-  for (int ks = 0; ks < NK; ++ks) Bh[ks] = kHold && sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+  for (int ks = 0; ks < NK; ++ks) Bh[ks] = kHoldB && sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
 #pragma unroll
   for (int h = 0; h < HS; ++h) {
     const int k = pass * HS + h;
@@ -586,8 +587,10 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         uint2 ux[4];    // u of head k at this lane's column, for x_B
         if (kv && !kHold) {
           const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
+          if (!kHoldB) {
 #pragma unroll
-          for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+            for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+          }
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) ul[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
         }
@@ -693,7 +696,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         v8bf Bf[NK], uf[2] = {Uh[h][0], Uh[h][1]};
 #pragma unroll
         for (int ks = 0; ks < NK; ++ks) Bf[ks] = Bh[ks];
-        if (!kHold && h == 0) {
+        if (!kHoldB && h == 0) {
 #pragma unroll
           for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
         }
