@@ -86,6 +86,9 @@ FUSED_CASES = [
     # fused path, four heads per group, the last chunk 72 rows long (a strip
     # of 8 rows) and the length ending inside its first strip
     ("hpg4_tail", dict(b=1, L=200, H=8, P=64, N=128, G=2, lens=[190]), 128),
+    # one head per group at chunk 256: single-head source launches over
+    # every start strip S (odd ones included) and up to four target strips
+    ("hpg1_c256", dict(b=2, L=512, H=2, P=64, N=128, G=2, lens=[512, 333]), 256),
     # two P tiles, three N slices: bf16 chunk-state / dH_intra kernels, generic column / row kernels
     ("p128_n192", dict(b=2, L=600, H=2, P=128, N=192, G=1, lens=[600, 389]), 256),
 ]
