@@ -83,7 +83,9 @@ int sa_ssu_fwd_gated(int dtype, const void* u, const float* A, const void* B, co
  * (ops/ssd_scan.py:70-73).
  *   u (b,L,H,P), B,C (b,L,G,N), delta_raw (b,L,H): dtype `dtype`
  *   A (H,), delta_bias (H,) or NULL, h_init (b,H,P,N) or NULL: float32
- *   length (b,) int64 (clamped to [0, L]); chunk_size in [1, 1024]; N <= 256
+ *   length (b,) int64 (clamped to [0, L]), or NULL for full rows (what the
+ *   reference builds with torch.full when the caller passes none);
+ *   chunk_size in [1, 1024]; N <= 256
  * Outputs (float32): y (b,L,H,P), h_last (b,H,P,N), and the intermediates the
  * backward consumes: dt, dc (b,H,nc,Lc) and states (b,nc,H,P,N), which holds
  * the state entering each chunk on return (nc = ceil(L/Lc)).

@@ -1017,7 +1017,7 @@ extern "C" int sa_ssd_bwd(int dtype, const void* u, const float* A, const void* 
   SA_CHECK_ARG(dtype == sa::kF32 || dtype == sa::kBF16, "sa_ssd_bwd: unsupported dtype %d", dtype);
   SA_CHECK_ARG(dtype == sa::kBF16 || state_dim <= 128,
                "sa_ssd_bwd: float32 path supports state_dim <= 128 (got %d)", state_dim);
-  SA_CHECK_ARG(u && A && B && C && delta_raw && length && dy && dt && dc && states && du && dA &&
+  SA_CHECK_ARG(u && A && B && C && delta_raw && dy && dt && dc && states && du && dA &&
                    dB && dC && ddelta_raw && workspace,
                "sa_ssd_bwd: null tensor pointer");
   const size_t need = sa::bwd_layout(d, dtype == sa::kBF16 ? 2 : 4).total;

@@ -10,8 +10,10 @@ struct SsdDims {
   int b, L, H, P, G, N, Lc, nc;
 };
 
-// effective sequence length of batch row b: clamp(length[b], 0, L)
+// effective sequence length of batch row b: clamp(length[b], 0, L), or L
+// when no lengths are given
 __device__ __forceinline__ int seq_limit(const int64_t* length, int b, int L) {
+  if (!length) return L;   // no lengths: every row is full
   long v = length[b];
   return static_cast<int>(v < 0 ? 0 : (v > L ? L : v));
 }

@@ -1059,7 +1059,7 @@ extern "C" int sa_ssd_fwd(int dtype, const void* u, const float* A, const void* 
   int rc = sa::make_dims(batch, seqlen, num_heads, head_dim, num_groups, state_dim, chunk_size, &d,
                          "sa_ssd_fwd");
   if (rc) return rc;
-  SA_CHECK_ARG(u && A && B && C && delta_raw && length && y && h_last && dt && dc && states,
+  SA_CHECK_ARG(u && A && B && C && delta_raw && y && h_last && dt && dc && states,
                "sa_ssd_fwd: null tensor pointer");
   SA_CHECK_ARG(dtype != sa::kF32 || state_dim <= 128,
                "sa_ssd_fwd: float32 path supports state_dim <= 128 (got %d)", state_dim);
@@ -1095,7 +1095,7 @@ extern "C" int sa_ssd_fwd_gated(int dtype, const void* u, const float* A, const 
   SA_CHECK_ARG(sa_ssd_fwd_gated_supported(dtype, head_dim, state_dim),
                "sa_ssd_fwd_gated: needs bfloat16 activations, head_dim %% 8 == 0 and state_dim a "
                "multiple of 32 up to 256 (got dtype %d, P=%d, N=%d)", dtype, head_dim, state_dim);
-  SA_CHECK_ARG(u && A && B && C && delta_raw && length && D && gate && out && yd && h_last && dt &&
+  SA_CHECK_ARG(u && A && B && C && delta_raw && D && gate && out && yd && h_last && dt &&
                    dc && states,
                "sa_ssd_fwd_gated: null tensor pointer");
   SA_CHECK_ARG(sa::aligned16(D) && sa::aligned16(gate) && sa::aligned16(out) && sa::aligned16(yd),

@@ -37,9 +37,7 @@ def _prep(u, A, B, C, delta_raw, delta_bias, h_init, length):
     A32 = as_dtype(A, torch.float32).contiguous()
     bias32 = None if delta_bias is None else as_dtype(delta_bias, torch.float32).contiguous()
     h0 = _f32_aligned(h_init)
-    if length is None:
-        length = torch.full((b,), L, dtype=torch.int64, device=u.device)
-    else:
+    if length is not None:   # None: full rows (the C-ABI's NULL length)
         length = as_dtype(length, torch.int64).contiguous()
     return code, u.contiguous(), A32, B, C, delta_raw, bias32, h0, length
 

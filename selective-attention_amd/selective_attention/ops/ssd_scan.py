@@ -3,7 +3,7 @@
 Drop-in for the reference's SSDScanFn (ops/ssd_scan.py:7-96): a
 torch.autograd.Function with the same forward signature and defaults, the
 same ndim/shape validation (ValueError before any launch), contiguity
-handling, `length` defaulting to the full sequence on the inputs' device,
+handling, an absent `length` meaning the full sequence,
 fp32 outputs y and h_last, and a backward that returns
 (u_grad, A_grad, B_grad, C_grad, delta_raw_grad, delta_bias_grad,
 h_init_grad, None x5).  Caller: SSM.forward (modules/ssm.py:136-139).
@@ -88,8 +88,8 @@ class SSDScanFn(torch.autograd.Function):
 
 def check_scan_args(u, A, B, C, delta_raw, delta_bias, h_init, length):
     """The reference's validation and contiguity handling (ops/ssd_scan.py:38-68):
-    ValueError on a bad ndim / shape before any launch, contiguous copies,
-    `length` defaulting to the full sequence on the inputs' device."""
+    ValueError on a bad ndim / shape before any launch, contiguous copies;
+    an absent `length` means the full sequence."""
     check_ndim(u, 4, name="u")
     check_ndim(A, 1, name="A")
     check_ndim(B, 4, name="B")
@@ -121,7 +121,6 @@ def check_scan_args(u, A, B, C, delta_raw, delta_bias, h_init, length):
     delta_bias = to_contiguous(delta_bias)
     h_init = to_contiguous(h_init)
     length = to_contiguous(length)
-
-    if length is None:
-        length = torch.full((batch_size,), seq_len, dtype=torch.long, device=u.device)
+    # an absent length stays None: the kernels take it as every row full,
+    # where the reference materialises torch.full((batch,), seq_len)
     return u, A, B, C, delta_raw, delta_bias, h_init, length
