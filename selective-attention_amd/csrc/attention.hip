@@ -748,12 +748,37 @@ template <int D, bool BIAS>
 __global__ __launch_bounds__(64, 2) void paged_decode_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ kp, const bf16* __restrict__ vp,
     const int32_t* __restrict__ page_table, const int32_t* __restrict__ seq_lens,
-    const float* __restrict__ key_bias, const int32_t* __restrict__ cum_row,
+    const float* __restrict__ key_bias, int32_t* __restrict__ cum_row,
     float* __restrict__ part_o, float* __restrict__ part_ml, int b, int Hq, int Hkv, int ps,
     int max_pages, int num_pages, int W, float scale_log2) {
   constexpr int DT = D / 16, KS = D / 32;
   const int w = blockIdx.x;
-  const long T = static_cast<long>(Hkv) * cum_row[b];
+  const int lane = threadIdx.x, c = lane & 15, g = lane >> 4;
+  // b <= 64: every wave forms the row plan itself, lane r holding row r's
+  // 64-key tiles and the tiles of the rows before it (cum_row[r]); wave 0
+  // stores cum_row for the merge.  Larger batches read the plan kernel's.
+  const bool lane_plan = b <= 64;
+  int ex_l = 0, tot = 0;
+  if (lane_plan) {
+    const int nb = lane < b ? (decode_row_len(seq_lens, lane, max_pages, ps) + 63) >> 6 : 0;
+    int incl = nb;
+#pragma unroll
+    for (int o2 = 1; o2 < 64; o2 <<= 1) {
+      const int t = __shfl_up(incl, o2, 64);
+      if (lane >= o2) incl += t;
+    }
+    ex_l = incl - nb;
+    tot = __builtin_amdgcn_readlane(incl, 63);
+    if (w == 0 && lane < b) {
+      cum_row[lane + 1] = incl;
+      if (lane == 0) cum_row[0] = 0;
+    }
+  }
+  // cum_row[r] for a wave-uniform r in [0, b]
+  auto crow = [&](int r) -> int {
+    return lane_plan ? (r < 64 ? __builtin_amdgcn_readlane(ex_l, r) : tot) : cum_row[r];
+  };
+  const long T = static_cast<long>(Hkv) * crow(b);
   // with at most T waves every wave gets at least one tile, which keeps the
   // segment ids of one (row, kv head) consecutive
   W = static_cast<int>(min(static_cast<long>(W), T));
@@ -761,7 +786,6 @@ __global__ __launch_bounds__(64, 2) void paged_decode_kernel(
   long gt = decode_wave_begin(w, T, W);
   const long gt_end = decode_wave_begin(w + 1, T, W);
   const int grp = Hq / Hkv;
-  const int lane = threadIdx.x, c = lane & 15, g = lane >> 4;
   const int pshift = ps == 128 ? 7 : 6;  // page size 64 or 128
   const int tshift = pshift - 6;         // log2(64-key tiles per page)
   const unsigned voff = static_cast<unsigned>(2 * (c * ps + 8 * g));
@@ -769,7 +793,9 @@ __global__ __launch_bounds__(64, 2) void paged_decode_kernel(
   // row of the first tile: the largest r with Hkv * cum_row[r] <= gt, by a
   // 64-ary search (cum_row is non-decreasing; invariant: answer in [lo, lo + span))
   int bi = 0;
-  {
+  if (lane_plan) {   // cum_row is non-decreasing in the lane: a prefix of lanes qualifies
+    bi = __popcll(__ballot(lane < b && static_cast<long>(Hkv) * ex_l <= gt)) - 1;
+  } else {
     int lo = 0, span = b;
     while (span > 1) {
       const int step = (span + 63) >> 6;
@@ -784,12 +810,12 @@ __global__ __launch_bounds__(64, 2) void paged_decode_kernel(
   }
 
   while (gt < gt_end) {
-    long rb = static_cast<long>(Hkv) * cum_row[bi];
-    int tb = cum_row[bi + 1] - cum_row[bi];
+    long rb = static_cast<long>(Hkv) * crow(bi);
+    int tb = crow(bi + 1) - crow(bi);
     while (gt >= rb + static_cast<long>(Hkv) * tb) {  // rows with no tiles
       ++bi;
-      rb = static_cast<long>(Hkv) * cum_row[bi];
-      tb = cum_row[bi + 1] - cum_row[bi];
+      rb = static_cast<long>(Hkv) * crow(bi);
+      tb = crow(bi + 1) - crow(bi);
     }
     const int off = static_cast<int>(gt - rb);
     const int kvh = off / tb;
@@ -1063,7 +1089,7 @@ int decode_wave_count(int head_dim, bool bias) {
               : decode_waves(paged_decode_kernel<64, false>, 3);
 }
 
-// plan, stream-K decode and merge on workspace `ws` with W waves
+// plan (more than 64 rows), stream-K decode and merge on workspace `ws` with W waves
 int decode_launch(const void* q, const void* k_pages, const void* v_pages,
                   const int32_t* page_table, const int32_t* seq_lens, const float* key_bias,
                   int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
@@ -1071,7 +1097,7 @@ int decode_launch(const void* q, const void* k_pages, const void* v_pages,
                   int W, hipStream_t s) {
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf(static_cast<float>(head_dim));
   const float sl2 = scale * sa::kLog2e;
-  {
+  if (batch > 64) {   // up to 64 rows the decode waves form the plan themselves
     sa::ProfScope prof_("paged_decode_plan", s);
     hipLaunchKernelGGL(sa::paged_decode_plan_kernel, dim3(1), dim3(1024), 0, s, seq_lens, batch,
                        page_size, max_pages, ws.cum_row);

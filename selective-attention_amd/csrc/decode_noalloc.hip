@@ -73,7 +73,8 @@ extern "C" int sa_paged_decode_fwd_noalloc(int dtype, const void* q, const void*
   sa::DecodeWs ws;
   sa::decode_ws_layout(batch, num_q_heads, num_kv_heads, head_dim, W, base, &ws);
   // every byte the merge reads is written earlier in the same call (cum_row
-  // by the plan kernel, each segment partial by its wave): nothing is cleared
+  // by the plan kernel or, up to 64 rows, by decode wave 0; each segment
+  // partial by its wave): nothing is cleared
   return sa::decode_launch(q, k_pages, v_pages, page_table, seq_lens, key_bias, batch,
                            num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_pages,
                            softmax_scale, o, ws, W, static_cast<hipStream_t>(stream));

@@ -331,7 +331,9 @@ def _run_decode(d, bias=None):
 @pytest.mark.gpu
 @pytest.mark.parametrize("b,Hq,Hkv,D,minl,maxl", [(3, 8, 2, 128, 1, 200), (4, 4, 4, 64, 60, 70),
                                                    (2, 32, 8, 128, 1000, 3000),
-                                                   (5, 16, 1, 128, 1, 1100)])
+                                                   (5, 16, 1, 128, 1, 1100),
+                                                   # more than 64 rows: the separate plan kernel
+                                                   (70, 4, 2, 64, 1, 300)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_paged_decode_parity(b, Hq, Hkv, D, minl, maxl, with_bias):
     print(f"decode b={b} Hq={Hq} Hkv={Hkv} D={D} len=[{minl},{maxl}] bias={with_bias}", flush=True)
