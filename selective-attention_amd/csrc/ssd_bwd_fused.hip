@@ -615,6 +615,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
                 duT[h][pt] = mfma_bf16(load_v8bf(Yl + off), Bf[2 * half + ks], duT[h][pt]);
               }
             state_dB(Yh, ul, ekh[h] * dtk[h], half);
+            __builtin_amdgcn_sched_barrier(0);   // the halves' operand reads stay apart
           }
           // head k's state part is complete: scale by e^{dc_last - dc_sig}; x_B
           const float ek = ekh[h];
