@@ -405,32 +405,57 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 #pragma unroll
   for (int i = 0; i < NK; ++i) o_gc[i] = dma_off<NK * 4, swz_k256>(i, w, lane, act_rs);
   float pdc = 0.f, pdc0 = 0.f;   // dc prefetch of the next target strip (head tid / 64, row tid % 64)
+  // The last launch has no registers to hold the DMA lane offsets through
+  // the kernel (they were spilled): it recomputes them where a stage is
+  // issued, a few integer operations each.
+  auto lane_offsets = [&](int (&gs)[2], int (&gy)[2], int (&gc)[NK]) {
+    if constexpr (last) {
+      const int ln = opaque(lane);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        gs[i] = dma_off<8, swz_s128>(i, w, ln, N);
+        gy[i] = dma_off<8, swz_k128>(i, w, ln, 64);
+      }
+#pragma unroll
+      for (int i = 0; i < NK; ++i) gc[i] = dma_off<NK * 4, swz_k256>(i, w, ln, act_rs);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        gs[i] = o_gs[i];
+        gy[i] = o_gy[i];
+      }
+#pragma unroll
+      for (int i = 0; i < NK; ++i) gc[i] = o_gc[i];
+    }
+  };
   auto issue = [&](int p, int j, int par) {   // par: the stage's buffer
     if (p >= NPASS) return;
     bf16* dst = stg(par);
     const int nst = n_state(p);
+    int gs[2], gy[2], gc[NK];
+    lane_offsets(gs, gy, gc);
     if (j < nst) {
       const int k = p * HS + j;
       if (k < HPG) {
         const bf16* src = dSg + k * (2L * 64 * N);
         bf16* cdst = Cs(state_cpar(j));
-        dma_pre<8>(dst, src, o_gs, w);
-        dma_pre<8>(dst + kPlaneT, src + 64L * N, o_gs, w);
-        dma_pre<8>(cdst, src + 64, o_gs, w);
-        dma_pre<8>(cdst + kPlaneT, src + 64 + 64L * N, o_gs, w);
+        dma_pre<8>(dst, src, gs, w);
+        dma_pre<8>(dst + kPlaneT, src + 64L * N, gs, w);
+        dma_pre<8>(cdst, src + 64, gs, w);
+        dma_pre<8>(cdst + kPlaneT, src + 64 + 64L * N, gs, w);
       }
     } else {
       const int qq = j - nst, Ti = qq / HS, h = qq % HS, T = S + Ti, k = p * HS + h;
       if (k < HPG) {
         const bf16* src = dyg + (static_cast<long>(T) * HPG + k) * (2L * kPlaneT);
-        dma_pre<8>(dst, src, o_gy, w);
-        dma_pre<8>(dst + kPlaneT, src + kPlaneT, o_gy, w);
+        dma_pre<8>(dst, src, gy, w);
+        dma_pre<8>(dst + kPlaneT, src + kPlaneT, gy, w);
       }
       if (h == 0) {
         const int t0 = 64 * T;
         bf16* cdst = Cs((T - S) & 1);
         const bf16* csrc = Cc + static_cast<long>(t0) * act_rs;
-        if (qlim - t0 >= 64) dma_pre<NK * 4>(cdst, csrc, o_gc, w);
+        if (qlim - t0 >= 64) dma_pre<NK * 4>(cdst, csrc, gc, w);
         else dma_tile<NK * 4, swz_k256>(cdst, csrc, act_rs, qlim - t0, w, lane);
         if (tid < HPG * 64) {   // raw: nothing waits for these before the stage's end
           const float* dch = dcc + (tid >> 6) * hstride + t0;
