@@ -38,7 +38,9 @@ const char* sa_last_error(void);
  * its stream.  sa_profile_collect synchronises them, aggregates by kernel
  * name (NUL-separated into names_buf), writes total milliseconds and launch
  * counts, clears the records and returns the number of distinct kernels
- * (-1 on a HIP error).  Not thread-safe.
+ * (-1 on a HIP error).  Safe to call from several host threads (the
+ * records are guarded by one mutex, taken by a launch only while timing is
+ * on); the records of all threads are aggregated together.
  */
 void sa_profile_enable(int on);
 int sa_profile_collect(char* names_buf, int names_len, float* total_ms, int* counts,

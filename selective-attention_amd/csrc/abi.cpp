@@ -5,6 +5,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -28,14 +30,17 @@ int sa_version(void) { return 2; }
 }  // extern "C"
 
 // ---------------------------------------------------------------------------
-// per-kernel event timing (single-threaded use; see prof.h)
+// per-kernel event timing (see prof.h).  Entry points may be called from
+// several host threads: the switch is atomic and the records are guarded by
+// one mutex, which a launch takes only while profiling is on.
 // ---------------------------------------------------------------------------
 namespace {
 struct ProfRec {
   const char* name;
   hipEvent_t a, b;
 };
-bool g_prof_on = false;
+std::atomic<bool> g_prof_on{false};
+std::mutex g_prof_mu;
 std::vector<ProfRec> g_recs;
 std::vector<hipEvent_t> g_free;
 
@@ -53,7 +58,8 @@ hipEvent_t take_event() {
 
 namespace sa {
 int prof_begin(const char* name, hipStream_t s) {
-  if (!g_prof_on) return -1;
+  if (!g_prof_on.load(std::memory_order_relaxed)) return -1;
+  std::lock_guard<std::mutex> lock(g_prof_mu);
   ProfRec r{name, take_event(), take_event()};
   if (!r.a || !r.b) return -1;
   (void)hipEventRecord(r.a, s);
@@ -62,13 +68,14 @@ int prof_begin(const char* name, hipStream_t s) {
 }
 void prof_end(int slot, hipStream_t s) {
   if (slot < 0) return;
+  std::lock_guard<std::mutex> lock(g_prof_mu);
   (void)hipEventRecord(g_recs[slot].b, s);
 }
 }  // namespace sa
 
 extern "C" {
 
-void sa_profile_enable(int on) { g_prof_on = on != 0; }
+void sa_profile_enable(int on) { g_prof_on.store(on != 0, std::memory_order_relaxed); }
 
 // Synchronises the recorded events, aggregates by kernel name and clears the
 // records.  Writes up to max_kernels entries: names (NUL-separated into
@@ -76,6 +83,7 @@ void sa_profile_enable(int on) { g_prof_on = on != 0; }
 // distinct kernels (or -1 on a HIP error).
 int sa_profile_collect(char* names_buf, int names_len, float* total_ms, int* counts,
                        int max_kernels) {
+  std::lock_guard<std::mutex> lock(g_prof_mu);
   std::vector<std::string> names;
   std::vector<float> tot;
   std::vector<int> cnt;
