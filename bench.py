@@ -704,6 +704,7 @@ def cpu_baseline(torch, budget_s):
     # config 3: 8 of the 64 decode rows (their pages copied to the host) + the state update
     rows = 8
     d = workloads.decode_inputs(device="cuda:0")
+    total_tokens = int(d.seq_lens.to("cpu", torch.int64).sum())
     lens = d.seq_lens[:rows].to("cpu", torch.int64)
     ps = d.k_pages.shape[2]
     npg = [int((n + ps - 1) // ps) for n in lens.tolist()]
@@ -729,7 +730,9 @@ def cpu_baseline(torch, budget_s):
 
     ta, ra = _median_time(attn, share / 2)
     ts, rs = _median_time(ssu, share / 2)
-    scale = 64 / rows
+    # the attention's work is proportional to the cached tokens it reads:
+    # scale the sample by the tokens of all 64 rows over those of the sample
+    scale = total_tokens / int(lens.sum())
     return {"value": round(tok1 / t1, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"config 1 fwd+bwd on 1 of 8 batch rows (L={tok1}), fp32 torch restatement "
                       f"(oracle/ssd.py), median of {r1} after 1 warm-up: {t1:.2f} s per row",
@@ -743,7 +746,8 @@ def cpu_baseline(torch, budget_s):
                                    "ssu_us": round(ts * 1e6, 1),
                                    "sample": f"paged GQA attention on rows 0-{rows - 1} "
                                              f"({int(lens.sum())} cached tokens) scaled by "
-                                             f"{scale:g} to 64 rows, plus the whole state update "
+                                             f"{scale:.3f} to the {total_tokens} cached tokens of "
+                                             f"all 64 rows, plus the whole state update "
                                              f"(b64 H32 P64 N128), medians of {ra} / {rs}"},
             }}
 

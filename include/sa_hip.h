@@ -38,9 +38,11 @@ const char* sa_last_error(void);
  * its stream.  sa_profile_collect synchronises them, aggregates by kernel
  * name (NUL-separated into names_buf), writes total milliseconds and launch
  * counts, clears the records and returns the number of distinct kernels
- * (-1 on a HIP error).  Safe to call from several host threads (the
+ * (-1 on a HIP error).  Safe to call from several host threads: the
  * records are guarded by one mutex, taken by a launch only while timing is
- * on); the records of all threads are aggregated together.
+ * on, and a launch's record is published only once both of its events are
+ * recorded, so a collect never sees a launch in progress; the records of
+ * all threads are aggregated together.
  */
 void sa_profile_enable(int on);
 int sa_profile_collect(char* names_buf, int names_len, float* total_ms, int* counts,

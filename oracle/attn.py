@@ -70,6 +70,72 @@ def sparse_attn_varlen(q, k, v, cu_seqlens, block_idx, block_size=64, softmax_sc
     return o
 
 
+def sparse_attn_varlen_blocks(q, k, v, cu_seqlens, block_idx, seqs, heads=None, block_size=64,
+                              softmax_scale=None, key_bias=None, dtype=torch.float64):
+    """sparse_attn_varlen restricted to the sequences `seqs` (indices into
+    cu_seqlens) and the heads `heads` (default all), computed block by block:
+    each query block gathers only its selected key blocks, so the work is
+    the selected (query, key) pairs instead of a dense n x n matrix per
+    sequence.  Same semantics (a repeated id counts once, ids outside the
+    sequence's blocks or after the query block select nothing, the
+    diagonal block is causal, key_bias skips the query's own key).
+    Returns {seq: o (n, len(heads), D)} in `dtype`."""
+    T, H, D = q.shape
+    heads = list(range(H)) if heads is None else list(heads)
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
+    bs = block_size
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    qblk0 = [0]
+    for s in range(len(cu) - 1):
+        qblk0.append(qblk0[-1] + math.ceil((cu[s + 1] - cu[s]) / bs))
+    out = {}
+    for s in seqs:
+        a, b = cu[s], cu[s + 1]
+        n = b - a
+        nb = math.ceil(n / bs)
+        res = torch.zeros((n, len(heads), D), dtype=dtype)
+        if n == 0:
+            out[s] = res
+            continue
+        pad = nb * bs - n
+        qpos = torch.arange(nb * bs).view(nb, bs)                   # query position in the sequence
+        for hi, h in enumerate(heads):
+            rows = block_idx[h, qblk0[s]:qblk0[s] + nb].to(torch.int64)
+            if rows.shape[0] < nb:                                    # missing rows select nothing
+                rows = torch.cat([rows, torch.full((nb - rows.shape[0], rows.shape[1]), -1,
+                                                   dtype=torch.int64)])
+            M = rows.shape[1]
+            ok = (rows >= 0) & (rows < nb) & (rows <= torch.arange(nb)[:, None])
+            # a repeated id counts once: keep the first slot that holds it
+            dup = torch.zeros_like(ok)
+            for m in range(1, M):
+                dup[:, m] = (rows[:, m:m + 1] == rows[:, :m]).any(-1)
+            ok &= ~dup
+            ids = torch.where(ok, rows, 0)
+            qs = torch.nn.functional.pad(q[a:b, h].to(dtype), (0, 0, 0, pad)).view(nb, bs, D)
+            ks = torch.nn.functional.pad(k[a:b, h].to(dtype), (0, 0, 0, pad)).view(nb, bs, D)
+            vs = torch.nn.functional.pad(v[a:b, h].to(dtype), (0, 0, 0, pad)).view(nb, bs, D)
+            kg, vg = ks[ids], vs[ids]                                 # (nb, M, bs, D)
+            kpos = ids[:, :, None] * bs + torch.arange(bs)            # (nb, M, bs)
+            sc = torch.einsum("jqd,jmkd->jqmk", qs, kg) * scale       # (nb, bs, M, bs)
+            if key_bias is not None:
+                kb = torch.nn.functional.pad(key_bias[h, a:b].to(dtype), (0, pad)).view(nb, bs)[ids]
+                own = kpos[:, None, :, :] == qpos[:, :, None, None]
+                sc = sc + torch.where(own, torch.zeros((), dtype=dtype), kb[:, None, :, :])
+            allow = (ok[:, None, :, None] & (kpos[:, None, :, :] <= qpos[:, :, None, None])
+                     & (kpos[:, None, :, :] < n) & (qpos[:, :, None, None] < n))
+            sc = sc.masked_fill(~allow, float("-inf")).reshape(nb, bs, M * bs)
+            m = sc.max(dim=-1, keepdim=True).values
+            p = torch.where(allow.reshape(nb, bs, M * bs),
+                            torch.exp(sc - torch.where(torch.isinf(m), 0.0, m)), 0.0)
+            den = p.sum(-1, keepdim=True)
+            o = torch.einsum("jqk,jkd->jqd", p, vg.reshape(nb, M * bs, D))
+            o = torch.where(den > 0, o / torch.where(den > 0, den, 1.0), 0.0)
+            res[:, hi] = o.reshape(nb * bs, D)[:n]
+        out[s] = res
+    return out
+
+
 def paged_decode_attn(q, k_pages, v_pages, page_table, seq_lens, softmax_scale=None,
                       key_bias=None, dtype=torch.float64):
     """q (b, Hq, D); k_pages (num_pages, Hkv, page_size, D); v_pages
@@ -91,16 +157,15 @@ def paged_decode_attn(q, k_pages, v_pages, page_table, seq_lens, softmax_scale=N
         V = v_pages[pages].to(dtype).transpose(-1, -2)                      # (npg, Hkv, ps, D)
         K = K.permute(1, 0, 2, 3).reshape(Hkv, npg * ps, D)[:, :n]
         V = V.permute(1, 0, 2, 3).reshape(Hkv, npg * ps, D)[:, :n]
-        K = K.repeat_interleave(grp, dim=0)
-        V = V.repeat_interleave(grp, dim=0)
-        sc = torch.einsum("hd,hnd->hn", q[i].to(dtype), K) * scale
+        # query heads h = kv * grp + j read kv head kv: (Hkv, grp, D) against (Hkv, n, D)
+        qg = q[i].to(dtype).view(Hkv, grp, D)
+        sc = torch.matmul(qg, K.transpose(-1, -2)) * scale                 # (Hkv, grp, n)
         if key_bias is not None:
-            kb = key_bias[pages].to(dtype).permute(1, 0, 2).reshape(Hkv, npg * ps)[:, :n]
-            kb = kb.repeat_interleave(grp, dim=0).clone()
+            kb = key_bias[pages].to(dtype).permute(1, 0, 2).reshape(Hkv, npg * ps)[:, :n].clone()
             kb[:, n - 1] = 0.0
-            sc = sc + kb
+            sc = sc + kb[:, None, :]
         p = torch.softmax(sc, dim=-1)
-        o[i] = torch.einsum("hn,hnd->hd", p, V)
+        o[i] = torch.matmul(p, V).reshape(Hq, D)
     return o
 
 

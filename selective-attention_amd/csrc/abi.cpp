@@ -31,8 +31,11 @@ int sa_version(void) { return 2; }
 
 // ---------------------------------------------------------------------------
 // per-kernel event timing (see prof.h).  Entry points may be called from
-// several host threads: the switch is atomic and the records are guarded by
-// one mutex, which a launch takes only while profiling is on.
+// several host threads: the switch is atomic, and the record list and the
+// free events are guarded by one mutex, which a launch takes only while
+// profiling is on.  A launch holds its two events in its own ProfScope and
+// appends the record only once both are recorded, so a collect on another
+// thread never sees (or recycles the events of) a launch in progress.
 // ---------------------------------------------------------------------------
 namespace {
 struct ProfRec {
@@ -44,7 +47,7 @@ std::mutex g_prof_mu;
 std::vector<ProfRec> g_recs;
 std::vector<hipEvent_t> g_free;
 
-hipEvent_t take_event() {
+hipEvent_t take_event() {   // caller holds g_prof_mu
   if (!g_free.empty()) {
     hipEvent_t e = g_free.back();
     g_free.pop_back();
@@ -57,19 +60,27 @@ hipEvent_t take_event() {
 }  // namespace
 
 namespace sa {
-int prof_begin(const char* name, hipStream_t s) {
-  if (!g_prof_on.load(std::memory_order_relaxed)) return -1;
-  std::lock_guard<std::mutex> lock(g_prof_mu);
-  ProfRec r{name, take_event(), take_event()};
-  if (!r.a || !r.b) return -1;
-  (void)hipEventRecord(r.a, s);
-  g_recs.push_back(r);
-  return static_cast<int>(g_recs.size()) - 1;
+void prof_begin(hipStream_t s, hipEvent_t* a, hipEvent_t* b) {
+  *a = *b = nullptr;
+  if (!g_prof_on.load(std::memory_order_relaxed)) return;
+  {
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    hipEvent_t ea = take_event(), eb = take_event();
+    if (!ea || !eb) {
+      if (ea) g_free.push_back(ea);
+      if (eb) g_free.push_back(eb);
+      return;
+    }
+    *a = ea;
+    *b = eb;
+  }
+  (void)hipEventRecord(*a, s);
 }
-void prof_end(int slot, hipStream_t s) {
-  if (slot < 0) return;
+void prof_end(const char* name, hipEvent_t a, hipEvent_t b, hipStream_t s) {
+  if (!a || !b) return;
+  (void)hipEventRecord(b, s);
   std::lock_guard<std::mutex> lock(g_prof_mu);
-  (void)hipEventRecord(g_recs[slot].b, s);
+  g_recs.push_back(ProfRec{name, a, b});
 }
 }  // namespace sa
 

@@ -207,6 +207,11 @@ extern "C" int sa_score_stats(int dtype, const void* q, const void* k, const int
                head_dim);
   SA_CHECK_ARG(!causal || q_len == k_len, "sa_score_stats: causal needs q_len == k_len");
   SA_CHECK_ARG(q && k && out, "sa_score_stats: null tensor pointer");
+  // the same checks for empty and non-empty calls: dtype and head_dim first
+  SA_CHECK_ARG(dtype == sa::kBF16 || dtype == sa::kF32, "sa_score_stats: unsupported dtype %d",
+               dtype);
+  SA_CHECK_ARG(head_dim == 32 || head_dim == 64 || head_dim == 96 || head_dim == 128,
+               "sa_score_stats: head_dim %d not supported (32, 64, 96, 128)", head_dim);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (batch == 0 || q_len == 0 || k_len == 0) {   // no pairs: the reduction writes zeros
     hipLaunchKernelGGL(sa::score_stats_reduce_kernel, dim3(heads), dim3(256), 0, s, nullptr, 0,

@@ -77,17 +77,25 @@ inline BwdWs bwd_layout(const SsdDims& d, size_t mt_bytes) {
   w.per_bh = static_cast<int>((PN + 1023) / 1024);
   const size_t bhc = static_cast<size_t>(d.b) * d.H * d.nc;
   size_t o = 0;
+  // A bf16 shape the fused kernels take may still run the generic ones (the
+  // pointer alignment decides at launch), so for such shapes the region
+  // after dS holds either layout: the generic path's fp32 dCB, or the fused
+  // path's bf16 planes and parked dB part, and is sized for the larger.
   w.fused = mt_bytes == 2 && ssd_bwd_fused_shape_ok(d);
   w.dS = o;        o = al256(o + bhc * PN * 4);
-  // the generic path's fp32 dCB; the fused path keeps dCB^T as bf16 planes
-  w.dCB = o;       o = al256(o + (w.fused ? 0 : static_cast<size_t>(d.b) * d.nc * d.G * d.Lc * d.Lc * 4));
   const size_t bncg = static_cast<size_t>(d.b) * d.nc * d.G;
+  const size_t region = o;
+  // the generic path's fp32 dCB
+  w.dCB = region;
+  const size_t generic_end = al256(region + bncg * d.Lc * d.Lc * 4);
+  // the fused path: dy and dS as hi + lo planes, dCB^T as planes, and the
+  // state part of dB from the first source launch (more than two heads per
+  // group), [b][nc][G][Lc][N] fp32
   w.dyp = o;       o = al256(o + (w.fused ? bhc * d.Lc * 64 * 2 * 2 : 0));
   w.dSp = o;       o = al256(o + (w.fused ? bhc * PN * 2 * 2 : 0));
   w.dcbp = o;      o = al256(o + (w.fused ? bncg * w.ttiles * w.ttiles * 2 * 64 * 64 * 2 : 0));
-  // the state part of dB from the fused backward's first launch (more than
-  // two heads per group), [b][nc][G][Lc][N] fp32
   w.dbpark = o;    o = al256(o + (w.fused && d.H / d.G > 2 ? bncg * d.Lc * d.N * 4 : 0));
+  if (o < generic_end) o = generic_end;
   w.ddt_part = o;  o = al256(o + bhc * w.ptiles * d.Lc * 4);
   w.xB_part = o;   o = al256(o + bhc * w.ntiles * d.Lc * 4);
   w.xC_part = o;   o = al256(o + bhc * w.ntiles * d.Lc * 4);

@@ -237,9 +237,11 @@ class PagedSelectiveAttnCache:
     def page_table(self) -> torch.Tensor:
         """(batch, pages) int32 on the cache's device (at least max_pages columns).
         Columns past a row's pages repeat the row's last page id (0 for a row
-        without pages): the device-side append clamps its column to the
-        table's width, so an append past a row's pages lands in that row's own
-        last page, never in another row's."""
+        without pages, which the decode kernel never reads: its length is 0).
+        The device-side append clamps its column to the table's width, and
+        enter_device_mode gives every row at least one page, so an append past
+        a row's pages lands in that row's own last page, never in another
+        row's."""
         if self._pt_dirty or self._pt is None:
             width = max([self.max_pages] + [len(r) for r in self.rows])
             pt = torch.zeros(self.b, width, dtype=torch.int32)
@@ -308,17 +310,19 @@ class PagedSelectiveAttnCache:
         most `extra_tokens` appends may follow: the table's columns past a row's
         pages repeat its last page, so a row that runs past them overwrites
         slots of its own last page (wrong keys for that row alone, no fault)."""
-        if extra_tokens > 0:
-            fresh = []
-            for i in range(self.b):
-                need = (self.lens[i] + extra_tokens + self.ps - 1) // self.ps
-                while len(self.rows[i]) < need:
-                    pid = self._alloc(fill=False)
-                    self.rows[i].append(pid)
-                    fresh.append(pid)
-            if fresh:   # reset the new pages' gates in one launch
-                self.gate_pages[torch.tensor(fresh, device=self.device)] = float("-inf")
-                self._pt_dirty = True
+        # every row gets at least one page of its own, so that a device-side
+        # append (clamped to the table's width) never writes into page 0 of
+        # another row, even for a row that had no tokens and no pages
+        fresh = []
+        for i in range(self.b):
+            need = max(1, (self.lens[i] + max(extra_tokens, 0) + self.ps - 1) // self.ps)
+            while len(self.rows[i]) < need:
+                pid = self._alloc(fill=False)
+                self.rows[i].append(pid)
+                fresh.append(pid)
+        if fresh:   # reset the new pages' gates in one launch
+            self.gate_pages[torch.tensor(fresh, device=self.device)] = float("-inf")
+            self._pt_dirty = True
         self.page_table()
         self.lens_dev = torch.tensor(self.lens, dtype=torch.int32).to(self.device)
 

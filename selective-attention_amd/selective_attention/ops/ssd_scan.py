@@ -38,19 +38,15 @@ class SSDScanFn(torch.autograd.Function):
         delta_limit: Tuple[float, float] = (0.0, float("inf")),
         is_causal: bool = True,
     ):
-        """
-        Args:
-            u: (batch_size, seq_len, num_heads, head_dim)
-            A: (num_heads,)
-            B, C: (batch_size, seq_len, num_groups, state_dim)
-            delta_raw: (batch_size, seq_len, num_heads)
-            delta_bias: (num_heads,)
-            h_init: (batch_size, num_heads, head_dim, state_dim)
-            length: (batch_size,)
+        """Chunked scan of every (batch row, head) over the sequence.
 
-        Returns:
-            y: (batch_size, seq_len, num_heads, head_dim)
-            h_last: (batch_size, num_heads, head_dim, state_dim)
+        Shapes (b = batch, L = seq_len, H = heads, P = head_dim, G = groups,
+        N = state_dim): u (b, L, H, P); A (H,); B and C (b, L, G, N);
+        delta_raw (b, L, H); delta_bias (H,) or None; h_init (b, H, P, N) or
+        None (zero state); length (b,) int64 or None (every row full).
+
+        Returns (y, h_last): y (b, L, H, P) and the state after the last
+        valid token h_last (b, H, P, N), both fp32.
         """
         u, A, B, C, delta_raw, delta_bias, h_init, length = check_scan_args(
             u, A, B, C, delta_raw, delta_bias, h_init, length)
@@ -88,39 +84,25 @@ class SSDScanFn(torch.autograd.Function):
 
 def check_scan_args(u, A, B, C, delta_raw, delta_bias, h_init, length):
     """The reference's validation and contiguity handling (ops/ssd_scan.py:38-68):
-    ValueError on a bad ndim / shape before any launch, contiguous copies;
-    an absent `length` means the full sequence."""
-    check_ndim(u, 4, name="u")
-    check_ndim(A, 1, name="A")
-    check_ndim(B, 4, name="B")
-    check_ndim(C, 4, name="C")
-    check_ndim(delta_raw, 3, name="delta_raw")
-    check_ndim(delta_bias, 1, name="delta_bias", optional=True)
-    check_ndim(h_init, 4, name="h_init", optional=True)
-    check_ndim(length, 1, name="length", optional=True)
+    first every tensor's ndim, then every shape against the sizes u and B
+    give, each a ValueError raised before any launch, in the reference's
+    order; then contiguous copies where needed.  An absent `length` stays
+    None: the kernels read it as every row full (the reference builds
+    torch.full((batch,), seq_len) on the device instead)."""
+    args = dict(u=u, A=A, B=B, C=C, delta_raw=delta_raw, delta_bias=delta_bias,
+                h_init=h_init, length=length)
+    optional = ("delta_bias", "h_init", "length")
+    ndims = dict(u=4, A=1, B=4, C=4, delta_raw=3, delta_bias=1, h_init=4, length=1)
+    for name, nd in ndims.items():
+        check_ndim(args[name], nd, name=name, optional=name in optional)
 
-    batch_size, seq_len, num_heads, head_dim = u.shape
-    num_groups, state_dim = B.shape[2], B.shape[3]
+    b, L, H, P = u.shape
+    G, N = B.shape[2], B.shape[3]
+    shapes = dict(A=(H,), B=(b, L, G, N), C=(b, L, G, N), delta_raw=(b, L, H),
+                  delta_bias=(H,), h_init=(b, H, P, N), length=(b,))
+    for name, shape in shapes.items():
+        check_shape(args[name], shape, name=name, optional=name in optional)
+    if H % G != 0:
+        raise ValueError(f"num_heads ({H}) must be a multiple of num_groups ({G})")
 
-    check_shape(A, (num_heads,), name="A")
-    check_shape(B, (batch_size, seq_len, num_groups, state_dim), name="B")
-    check_shape(C, (batch_size, seq_len, num_groups, state_dim), name="C")
-    check_shape(delta_raw, (batch_size, seq_len, num_heads), name="delta_raw")
-    check_shape(delta_bias, (num_heads,), name="delta_bias", optional=True)
-    check_shape(h_init, (batch_size, num_heads, head_dim, state_dim), name="h_init",
-                optional=True)
-    check_shape(length, (batch_size,), name="length", optional=True)
-    if num_heads % num_groups != 0:
-        raise ValueError(f"num_heads ({num_heads}) must be a multiple of num_groups ({num_groups})")
-
-    u = to_contiguous(u)
-    A = to_contiguous(A)
-    B = to_contiguous(B)
-    C = to_contiguous(C)
-    delta_raw = to_contiguous(delta_raw)
-    delta_bias = to_contiguous(delta_bias)
-    h_init = to_contiguous(h_init)
-    length = to_contiguous(length)
-    # an absent length stays None: the kernels take it as every row full,
-    # where the reference materialises torch.full((batch,), seq_len)
-    return u, A, B, C, delta_raw, delta_bias, h_init, length
+    return tuple(to_contiguous(args[name]) for name in ndims)

@@ -102,6 +102,30 @@ def test_oracle_decode_bias_spares_newest_key():
     torch.testing.assert_close(out[0, 0], vp[0, 0, :, 1], rtol=1e-10, atol=1e-12)
 
 
+def test_oracle_sparse_blocks_equals_dense_restatement():
+    """The block-gathered sparse oracle (used at config 2's full size) equals
+    the dense one, with a bias, duplicated ids, ids past the query block and
+    past the sequence, -1 padding and a short block_idx."""
+    lens, H, D = [200, 90, 64, 1], 3, 16
+    q, k, v, cu = packed(lens, H, D, seed=12, dtype=F64)
+    g = torch.Generator().manual_seed(13)
+    idx, _, _ = workloads.block_selection(lens, H, 64, 3, g)
+    idx = _with_duplicates(idx, g)
+    idx[0, 1, -1] = 3          # after its query block
+    idx[1, 2, 0] = 9           # outside the sequence
+    bias = torch.randn(H, sum(lens), generator=g, dtype=F64)
+    bias[:, ::5] = float("-inf")
+    for sel, kb in ((idx, bias), (idx[:, :-2], None)):
+        dense = ref.sparse_attn_varlen(q, k, v, cu, sel, key_bias=kb)
+        blk = ref.sparse_attn_varlen_blocks(q, k, v, cu, sel, range(len(lens)), key_bias=kb)
+        for s in range(len(lens)):
+            a, b = int(cu[s]), int(cu[s + 1])
+            torch.testing.assert_close(blk[s], dense[a:b], rtol=1e-12, atol=1e-12)
+    part = ref.sparse_attn_varlen_blocks(q, k, v, cu, idx, [1], heads=[2])
+    torch.testing.assert_close(part[1], ref.sparse_attn_varlen(q, k, v, cu, idx)[200:290, 2:3],
+                               rtol=1e-12, atol=1e-12)
+
+
 # ------------------------------------------------------- workload invariants
 def test_varlen_packing_and_selection_invariants():
     g = torch.Generator().manual_seed(0)
@@ -306,18 +330,20 @@ def test_sparse_attn_short_block_idx_writes_every_row():
 
 @pytest.mark.gpu
 def test_sparse_attn_config2_sample():
-    """Config 2 (T=65536, H16, D128) on the device; two heads of the first
-    three sequences against the oracle, every output finite."""
+    """Config 2 (T=65536, H16, D128, the bench's own inputs) on the device:
+    every head of the first three sequences and of the longest one against
+    the fp64 oracle (block-gathered), every output finite."""
     w = workloads.sparse_attn_inputs()
-    o = _run_sparse(w.q, w.k, w.v, w.cu_seqlens, w.block_idx)
+    o = _run_sparse(w.q, w.k, w.v, w.cu_seqlens, w.block_idx).cpu()
     assert torch.isfinite(o.float()).all()
     cu = w.cu_seqlens
-    T3 = int(cu[3])
-    nq = sum(math.ceil(n / 64) for n in w.lens[:3])
-    for h in (0, 9):
-        exp = ref.sparse_attn_varlen(w.q[:T3, h:h + 1], w.k[:T3, h:h + 1], w.v[:T3, h:h + 1],
-                                     cu[:4], w.block_idx[h:h + 1, :nq])
-        assert_parity(o[:T3, h:h + 1], exp, torch.bfloat16, f"o head {h}")
+    longest = max(range(len(w.lens)), key=lambda s: w.lens[s])
+    seqs = sorted({0, 1, 2, longest})
+    print(f"config 2 sequences {seqs} (lengths {[w.lens[s] for s in seqs]}), 16 heads", flush=True)
+    exp = ref.sparse_attn_varlen_blocks(w.q, w.k, w.v, cu, w.block_idx, seqs)
+    for s in seqs:
+        a, b = int(cu[s]), int(cu[s + 1])
+        assert_parity(o[a:b], exp[s], torch.bfloat16, f"o seq {s}")
 
 
 def _run_decode(d, bias=None):
@@ -384,17 +410,18 @@ def test_paged_decode_empty_rows_and_single_long_row():
 
 
 @pytest.mark.gpu
-def test_paged_decode_config3_sample():
-    """Config 3 (b64, 32q/8kv, D128, len U[1024,32768], 64-token pages) on the
-    device; four rows checked against the oracle."""
+def test_paged_decode_config3_all_rows():
+    """Config 3 (b64, 32q/8kv, D128, len U[1024,32768], 64-token pages) on
+    the device: all 64 rows against the fp64 oracle."""
     d = workloads.decode_inputs(device="cuda")
-    o = _run_decode(d)
+    o = _run_decode(d).cpu()
     assert torch.isfinite(o.float()).all()
-    rows = [0, 17, 40, 63]
-    kp, vp = d.k_pages, d.v_pages
-    exp = ref.paged_decode_attn(d.q[rows].cpu(), kp.cpu(), vp.cpu(), d.page_table[rows].cpu(),
-                                d.seq_lens[rows].cpu())
-    assert_parity(o[rows], exp, torch.bfloat16, "o")
+    kp, vp, table, lens, q = (t.cpu() for t in (d.k_pages, d.v_pages, d.page_table,
+                                                  d.seq_lens, d.q))
+    for r0 in range(0, 64, 16):
+        rows = list(range(r0, r0 + 16))
+        exp = ref.paged_decode_attn(q[rows], kp, vp, table[rows], lens[rows])
+        assert_parity(o[rows], exp, torch.bfloat16, f"o rows {r0}..{r0 + 15}")
 
 
 # ------------------------------------------------- dense varlen attention (modes)

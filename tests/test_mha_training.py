@@ -84,6 +84,141 @@ def test_oracle_train_attn_gate_mutes_a_key_except_on_its_diagonal():
     assert torch.allclose(out[0, 0], w @ v[0, 0], atol=1e-12)
 
 
+def test_oracle_rope_rotate_is_pairwise_rotation():
+    """rope_rotate (modules/rope.py) against its definition: element i and
+    i + D/2 form a pair turned by the angle pos * base^(-i / (D/2)), as the
+    2x2 matrix [[cos, -sin], [sin, cos]] with the angle taken in Python
+    floats.  Position 0 is the identity, pair norms are kept, and the score
+    of two rotated vectors depends only on the difference of positions."""
+    D, L, base = 8, 7, 10000.0
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, L, D, generator=g, dtype=F64)
+    pos = torch.tensor([0, 1, 2, 5, 100, 1000, 8191])
+    got = lm_ref.rope_rotate(x, pos, base)
+    half = D // 2
+    for t in range(L):
+        for i in range(half):
+            a = float(torch.tensor(float(pos[t]), dtype=torch.float32)
+                      * torch.tensor(1.0 / base ** (i / half), dtype=torch.float32))
+            c, s = math.cos(a), math.sin(a)
+            x0, x1 = x[:, t, i], x[:, t, i + half]
+            # the fp32 angle is exact in the oracle; cos/sin of it here in fp64
+            torch.testing.assert_close(got[:, t, i], c * x0 - s * x1, rtol=0, atol=1e-6)
+            torch.testing.assert_close(got[:, t, i + half], s * x0 + c * x1, rtol=0, atol=1e-6)
+    assert torch.equal(got[:, 0], x[:, 0])
+    n_in = x[..., :half] ** 2 + x[..., half:] ** 2
+    n_out = got[..., :half] ** 2 + got[..., half:] ** 2
+    torch.testing.assert_close(n_out, n_in, rtol=1e-12, atol=1e-12)
+    q, k = torch.randn(D, generator=g, dtype=F64), torch.randn(D, generator=g, dtype=F64)
+    # integer positions below 2^24 give exact fp32 angles, so shifting both
+    # positions by the same amount keeps q.k up to the cos / sin rounding
+    def score(m, n):
+        return float((lm_ref.rope_rotate(q[None], torch.tensor([m]), base)
+                      * lm_ref.rope_rotate(k[None], torch.tensor([n]), base)).sum())
+    for m, n in ((5, 2), (40, 37), (300, 297)):
+        assert score(m, n) == pytest.approx(score(3, 0), rel=1e-6, abs=1e-6)
+
+
+def _identity_mha_params(dim, H, gate_out_bias, select_bias=None, cross=False):
+    """Projection weights that are identities (zero biases) and gate
+    projections with zero weight: the composition's attention then acts on
+    the inputs themselves, with constant gates sigmoid(bias)."""
+    eye = torch.eye(dim, dtype=F64)
+    p = {"q_proj.weight": eye.clone(), "k_proj.weight": eye.clone(),
+         "v_proj.weight": eye.clone(), "v_proj.bias": torch.zeros(dim, dtype=F64),
+         "out_proj.weight": eye.clone(), "out_proj.bias": torch.zeros(dim, dtype=F64)}
+    if cross:
+        p["select_gate_proj.weight"] = torch.zeros(H, dim, dtype=F64)
+        p["select_gate_proj.bias"] = select_bias.clone()
+    else:
+        p["gate_proj.weight"] = torch.zeros(H + dim, dim, dtype=F64)
+        p["gate_proj.bias"] = torch.cat([select_bias, gate_out_bias])
+    return p
+
+
+def test_oracle_selective_train_forward_penalty_zero_is_rope_sdpa():
+    """selective_mha_train_forward at penalty 0 with identity projections and
+    constant gates: the output is causal SDPA over the RoPE-rotated heads of
+    x, times sigmoid(out-gate bias) column by column."""
+    b, L, H, hd = 2, 9, 2, 8
+    dim = H * hd
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(b, L, dim, generator=g, dtype=F64)
+    ob = torch.randn(dim, generator=g, dtype=F64)
+    p = _identity_mha_params(dim, H, ob, torch.randn(H, generator=g, dtype=F64))
+    out, _ = lm_ref.selective_mha_train_forward(p, x, None, hd, 0.0)
+    xh = x.view(b, L, H, hd).transpose(1, 2)
+    pos = torch.arange(L)
+    e = F.scaled_dot_product_attention(lm_ref.rope_rotate(xh, pos), lm_ref.rope_rotate(xh, pos),
+                                       xh, is_causal=True)
+    exp = e.transpose(1, 2).reshape(b, L, dim) * torch.sigmoid(ob)
+    torch.testing.assert_close(out, exp, rtol=1e-10, atol=1e-12)
+
+
+def test_oracle_cross_train_penalty_zero_is_masked_sdpa():
+    """cross_mha_train_forward at penalty 0 with identity projections: SDPA
+    of the decoder states over the context, keys past each row's context
+    length masked out; the std is the population std of exactly those
+    scores (brute force)."""
+    b, L, Lc, H, hd = 2, 5, 11, 2, 8
+    dim = H * hd
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(b, L, dim, generator=g, dtype=F64)
+    ctx = torch.randn(b, Lc, dim, generator=g, dtype=F64)
+    lens = torch.tensor([11, 4])
+    p = _identity_mha_params(dim, H, None, torch.randn(H, generator=g, dtype=F64), cross=True)
+    out, std = lm_ref.cross_mha_train_forward(p, x, ctx, lens, hd, 0.0)
+    qh = x.view(b, L, H, hd).transpose(1, 2)
+    kh = ctx.view(b, Lc, H, hd).transpose(1, 2)
+    mask = (torch.arange(Lc)[None, :] < lens[:, None])[:, None, None, :]
+    e = F.scaled_dot_product_attention(qh, kh, kh, attn_mask=mask)
+    torch.testing.assert_close(out, e.transpose(1, 2).reshape(b, L, dim), rtol=1e-10, atol=1e-12)
+    for h in range(H):
+        vals = [float(qh[i, h, t] @ kh[i, h, j]) / math.sqrt(hd)
+                for i in range(b) for t in range(L) for j in range(int(lens[i]))]
+        m = sum(vals) / len(vals)
+        sd = math.sqrt(sum((v - m) ** 2 for v in vals) / len(vals))
+        assert float(std[h]) == pytest.approx(sd, rel=1e-10)
+
+
+def test_oracle_cross_train_key0_exemption_brute_force():
+    """cross_mha_train_forward with a gate: a loop over (row, head, query)
+    adds log(gate_j) * std_h * penalty to every valid key but key 0 and takes
+    the softmax over the keys inside the context length.  A gate near 0 on
+    key 0 leaves its weight untouched; the same gate on another key mutes it."""
+    b, L, Lc, H, hd, pen = 2, 4, 9, 2, 8, 1.3
+    dim = H * hd
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(b, L, dim, generator=g, dtype=F64)
+    ctx = torch.randn(b, Lc, dim, generator=g, dtype=F64)
+    lens = torch.tensor([9, 6])
+    sb = torch.randn(H, generator=g, dtype=F64)
+    p = _identity_mha_params(dim, H, None, sb, cross=True)
+    # per-key gates: a non-zero gate weight on one context feature varies them
+    p["select_gate_proj.weight"][:, 0] = 2.0
+    ctx[:, 0, 0] = -300.0           # key 0: gate ~ e^-600 (exempt anyway)
+    ctx[1, 3, 0] = -300.0           # key 3 of row 1: muted
+    x[..., 0] = 0.0                 # feature 0 drives the gate only, not q.k
+    out, std = lm_ref.cross_mha_train_forward(p, x, ctx, lens, hd, pen)
+    gate = torch.sigmoid(ctx[..., 0:1] * 2.0 + sb)          # (b, Lc, H)
+    for i in range(b):
+        n = int(lens[i])
+        for h in range(H):
+            kh = ctx[i, :, h * hd:(h + 1) * hd]
+            for t in range(L):
+                q = x[i, t, h * hd:(h + 1) * hd]
+                s = [float(q @ kh[j]) / math.sqrt(hd)
+                     + (0.0 if j == 0 else math.log(float(gate[i, j, h])) * float(std[h]) * pen)
+                     for j in range(n)]
+                mx = max(s)
+                w = [math.exp(v - mx) for v in s]
+                z = sum(w)
+                exp = sum(w[j] / z * kh[j] for j in range(n))
+                torch.testing.assert_close(out[i, t, h * hd:(h + 1) * hd], exp, rtol=1e-9, atol=1e-12)
+                if i == 1:
+                    assert w[3] / z < 1e-100 and w[0] / z > 1e-12
+
+
 # ---------------------------------------------------------------- GPU parity
 STATS_CASES = [
     (torch.bfloat16, 2, 3, 200, 64, True, [200, 77]),

@@ -187,6 +187,24 @@ def test_paged_cache_table_padding_stays_in_row():
     assert [int(pt[i, col]) for i in range(3)] == [r[-1] for r in cache.rows]
 
 
+def test_device_mode_gives_empty_rows_their_own_page():
+    """A row with no tokens (and no pages) entering device mode with no extra
+    tokens still gets a page of its own: the device-side append of its next
+    token lands there, never in page 0 of another row."""
+    cache = PagedSelectiveAttnCache(3, 1, 8, max_tokens=200, device="cpu")
+    z = torch.zeros(3, 1, 100, 8)
+    cache.build(z, z, torch.zeros(3, 1, 100), lengths=torch.tensor([100, 0, 30]))
+    assert cache.rows[1] == []
+    cache.enter_device_mode(0)
+    pt = cache.page_table()
+    owned = [set(r) for r in cache.rows]
+    assert all(len(r) >= 1 for r in cache.rows)
+    assert not (owned[0] & owned[1]) and not (owned[1] & owned[2]) and not (owned[0] & owned[2])
+    for i in range(3):
+        assert set(pt[i].tolist()) <= owned[i], f"row {i}: {pt[i].tolist()} vs {cache.rows[i]}"
+    cache.exit_device_mode()
+
+
 # ------------------------------------------------------------- GPU parity
 PREFILL_CASES = {
     # name: (b, H, L, D, lengths, thr, dead_heads)

@@ -142,6 +142,41 @@ def test_ssd_bwd_softplus_far_above_threshold():
         assert_scaled(v, exp[k], f"d{k}")
 
 
+def _misaligned(t):
+    """A contiguous device copy of t that starts 2 bytes into its buffer (a
+    view with a storage offset, as a slice of a larger tensor gives)."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device="cuda")
+    v = buf[1:].view(t.shape)
+    v.copy_(t.cuda())
+    assert v.data_ptr() % 16 != 0
+    return v
+
+
+@pytest.mark.gpu
+def test_ssd_bwd_fused_shape_misaligned_inputs():
+    """A shape the fused kernels take (bf16, P 64, N 128, 4 heads per group)
+    with u, B and C 2 bytes off a 16-byte boundary runs the generic kernels
+    inside the same workspace; every gradient matches the oracle."""
+    from selective_attention.ops import SSDScanFn
+    print("ssd bwd fused shape, misaligned u/B/C", flush=True)
+    x = make_inputs(dtype=torch.bfloat16, b=2, L=256, H=8, P=64, N=128, G=2, lens=[256, 150],
+                    with_h=False)
+    g = torch.Generator().manual_seed(21)
+    dy = torch.randn(2, 256, 8, 64, generator=g)
+    leaves = {k: (_misaligned(x[k]) if k in ("u", "B", "C") else x[k].cuda().clone())
+              for k in ("u", "A", "B", "C", "delta_raw", "delta_bias")}
+    for v in leaves.values():
+        v.requires_grad_(True)
+    y, _ = SSDScanFn.apply(leaves["u"], leaves["A"], leaves["B"], leaves["C"],
+                           leaves["delta_raw"], leaves["delta_bias"], None, x["length"].cuda(),
+                           128, True, (0.0, float("inf")), True)
+    grads = torch.autograd.grad((y,), list(leaves.values()), (dy.cuda(),))
+    torch.cuda.synchronize()
+    exp = ref_grads(x, dy, None, 128)
+    for k, v in zip(leaves, grads):
+        assert_parity(v, exp[k], torch.bfloat16, f"d{k}")
+
+
 @pytest.mark.gpu
 def test_ssd_bwd_fused_deterministic():
     x = make_inputs(b=2, L=256, H=8, P=64, N=128, G=2, dtype=torch.bfloat16, lens=[256, 190])
@@ -196,7 +231,9 @@ def test_ssd_config1_full_batch_rows_equal_single_rows():
     rows are independent and every kernel is deterministic, so rows 0 and 7
     of y, h_last and every per-row gradient equal, bit for bit, a b = 1 run on
     that row alone.  dA is a sum over rows: its b = 8 value equals the sum of
-    the eight b = 1 values to fp32 rounding."""
+    the eight b = 1 values to fp32 rounding.  Row 0 of the bench's own inputs
+    (y, h_last, du, dB, dC, d delta_raw and that row's dA) is checked against
+    the fp64 oracle."""
     print("ssd config1 full batch vs single rows", flush=True)
     from selective_attention.ops import SSDScanFn
     cfg = workloads.SSD_CONFIGS[1]
@@ -225,6 +262,18 @@ def test_ssd_config1_full_batch_rows_equal_single_rows():
         assert torch.equal(h[r:r + 1], h1), f"h_last row {r}"
         for k in ("u", "B", "C", "delta_raw"):
             assert torch.equal(g[k][r:r + 1], g1[k]), f"d{k} row {r}"
+        if r == 0:
+            print("row 0 of the bench inputs vs the fp64 oracle", flush=True)
+            x0 = {k: (w[k][0:1] if k != "A" else w[k]).cpu() for k in names}
+            x0.update(delta_bias=None, h_init=None, length=None)
+            y_ref, h_ref = ref.ssd_scan_forward(x0["u"], x0["A"], x0["B"], x0["C"],
+                                                x0["delta_raw"], None, None, None,
+                                                chunk_size=cfg["chunk"])
+            assert_parity(y1.cpu(), y_ref, torch.bfloat16, "y row 0")
+            assert_parity(h1.cpu(), h_ref, torch.bfloat16, "h_last row 0")
+            exp = ref_grads(x0, w["dy"][0:1].cpu(), None, cfg["chunk"])
+            for k in names:
+                assert_parity(g1[k].cpu(), exp[k], torch.bfloat16, f"d{k} row 0")
     torch.testing.assert_close(g["A"], dA_rows, rtol=1e-5, atol=1e-5 * dA_rows.abs().max().item())
 
 
