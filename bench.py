@@ -79,12 +79,14 @@ def ssd_alg_flops(b, L, H, P, G, N, Lc):
     return 3 * fwd
 
 
-def run_ssd(args, torch):
+def _ssd_step_leg(args, torch, cfg, workload, traffic_file=None):
+    """SSDScanFn forward + backward (autograd.grad for u, A, B, C, delta_raw)
+    at the shapes of cfg, bf16 activations, fp32 state, fp32 y and dy; times
+    the step and every kernel (HIP events on the launch stream)."""
     from selective_attention import workloads
     from selective_attention.ops import SSDScanFn
     from selective_attention.profiling import kernel_timer
 
-    cfg = dict(workloads.SSD_CONFIGS[1])
     dev = torch.device("cuda:0")
     x = workloads.ssd_inputs(**cfg, device=dev, with_dy=True)
     b, L, H, P = x["u"].shape
@@ -118,10 +120,11 @@ def run_ssd(args, torch):
     flops = ssd_alg_flops(b, L, H, P, G, N, Lc)
     achieved = alg / (ms / 1e3) / 1e9
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "ssd_fwd_bwd_config1_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_step")
+    if traffic_file:
+        tpath = os.path.join(ROOT, "profiles", traffic_file)
+        if os.path.exists(tpath):
+            with open(tpath) as f:
+                traffic = json.load(f).get("hbm_bytes_per_step")
     roofline = {
         "bound": "hbm",
         "achieved": round(achieved, 1),
@@ -138,9 +141,43 @@ def run_ssd(args, torch):
         "kernels": kernels,
     }
     return dict(ms=ms, ms_mean=ms_mean, tokens=b * L, roofline=roofline,
-                config={"workload": "ssd_scan_fwd_bwd_config1", "batch": b, "seq_len": L,
+                config={"workload": workload, "batch": b, "seq_len": L,
                         "nheads": H, "headdim": P, "dstate": N, "ngroups": G, "chunk": Lc,
                         "activations": "bf16", "state": "fp32", "y_dtype": "fp32"})
+
+
+def run_ssd(args, torch):
+    from selective_attention import workloads
+    return _ssd_step_leg(args, torch, dict(workloads.SSD_CONFIGS[1]), "ssd_scan_fwd_bwd_config1",
+                         "ssd_fwd_bwd_config1_traffic.json")
+
+
+# SSD fwd+bwd at the SSM shapes of the models: config 4's hybrid LM (d_model
+# 1024, expand 2, head_dim 64, state 128, one group) and the reference's
+# default CausalLMConfig (models/causal_lm.py:11-22: d_model 512, state 64,
+# one group; SSM expand 2, head_dim 64)
+SSD_MODEL_SHAPES = {
+    "config4_ssm": dict(batch=4, seqlen=8192, nheads=32, headdim=64, dstate=128, ngroups=1,
+                        chunk=256, dtype=None),
+    "reference_default_ssm": dict(batch=8, seqlen=4096, nheads=16, headdim=64, dstate=64,
+                                  ngroups=1, chunk=256, dtype=None),
+}
+
+
+def run_ssd_shapes(args, torch):
+    """The headline step at the models' own SSM shapes (see SSD_MODEL_SHAPES)."""
+    out = {}
+    for name, cfg in SSD_MODEL_SHAPES.items():
+        cfg = dict(cfg, dtype=torch.bfloat16)
+        r = _ssd_step_leg(args, torch, cfg, f"ssd_scan_fwd_bwd_{name}")
+        rf = r["roofline"]
+        out[name] = {"ms_per_step": round(r["ms"], 3),
+                     "tokens_per_s": round(r["tokens"] / (r["ms"] / 1e3), 1),
+                     "hbm_frac": rf["frac"], "achieved_gbs": rf["achieved"],
+                     "algorithmic_bytes": rf["algorithmic_bytes"], "mfma_frac": rf["mfma_frac"],
+                     "kernels_per_step_us": {k: v["per_step_us"] for k, v in rf["kernels"].items()},
+                     "config": r["config"]}
+    return out
 
 
 def _time_steps(torch, fn, steps, warmup):
@@ -853,7 +890,8 @@ def main():
         "config": res["config"],
         "roofline": res["roofline"],
     }
-    legs = [("decode", "decode", run_decode), ("sparse", "sparse_attn", run_sparse),
+    legs = [("ssd_shapes", "ssd_model_shapes", run_ssd_shapes),
+            ("decode", "decode", run_decode), ("sparse", "sparse_attn", run_sparse),
             ("ssm_io", "ssm_io", run_ssm_io), ("selective_mha", "selective_mha", run_selective_mha),
             ("causal_lm", "causal_lm", run_causal_lm), ("seq2seq", "seq2seq", run_seq2seq)]
     want = set() if args.ssd_only else (

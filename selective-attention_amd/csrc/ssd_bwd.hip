@@ -61,7 +61,7 @@ __device__ __forceinline__ void frag_col_sums(const float (&v)[2][2][4], float (
 // ---------------------------------------------------------------------------
 struct BwdWs {
   size_t dS, dCB, ddt_part, xB_part, xC_part, rsum, qpart, ddc_part, dA_part, db_part;
-  size_t dyp, dSp, dcbp, dbpark, total;   // bf16 planes and dB partials of the fused path
+  size_t dyp, dSp, dcbp, total;   // bf16 planes of the fused path
   int ptiles, ntiles, ttiles, per_bh;
   bool fused;
 };
@@ -88,13 +88,10 @@ inline BwdWs bwd_layout(const SsdDims& d, size_t mt_bytes) {
   // the generic path's fp32 dCB
   w.dCB = region;
   const size_t generic_end = al256(region + bncg * d.Lc * d.Lc * 4);
-  // the fused path: dy and dS as hi + lo planes, dCB^T as planes, and the
-  // state part of dB from the first source launch (more than two heads per
-  // group), [b][nc][G][Lc][N] fp32
+  // the fused path: dy and dS as hi + lo planes, dCB^T as planes
   w.dyp = o;       o = al256(o + (w.fused ? bhc * d.Lc * 64 * 2 * 2 : 0));
   w.dSp = o;       o = al256(o + (w.fused ? bhc * PN * 2 * 2 : 0));
   w.dcbp = o;      o = al256(o + (w.fused ? bncg * w.ttiles * w.ttiles * 2 * 64 * 64 * 2 : 0));
-  w.dbpark = o;    o = al256(o + (w.fused && d.H / d.G > 2 ? bncg * d.Lc * d.N * 4 : 0));
   if (o < generic_end) o = generic_end;
   w.ddt_part = o;  o = al256(o + bhc * w.ptiles * d.Lc * 4);
   w.xB_part = o;   o = al256(o + bhc * w.ntiles * d.Lc * 4);
@@ -921,7 +918,6 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
   bf16* dyp = reinterpret_cast<bf16*>(ws + w.dyp);
   bf16* dSp = reinterpret_cast<bf16*>(ws + w.dSp);
   bf16* dcbp = reinterpret_cast<bf16*>(ws + w.dcbp);
-  float* dbpark = reinterpret_cast<float*>(ws + w.dbpark);
   // 1. dH_intra -> dS buffer (the fused path also writes dy as hi + lo planes)
   if (fused) {
     if ((rc = launch_dstate_planes(dy, C_, dt, dc, length, dS, dyp, d, s))) return rc;
@@ -940,7 +936,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
   if (fused) {
     // 3-5 fused: du, dB, dC, decay sums
     if ((rc = launch_ssd_bwd_fused(u, Bm, Cm, dyp, dt, dc, states, dSp, length, du_, dB_, dC_,
-                                   dcbp, ddt_part, xB_part, xC_part, qpart, rsum, dbpark, d,
+                                   dcbp, ddt_part, xB_part, xC_part, qpart, rsum, d,
                                    lo >= 0.f, s)))
       return rc;
     ptiles = ntiles = qtiles = 1;

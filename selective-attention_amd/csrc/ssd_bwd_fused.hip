@@ -270,43 +270,40 @@ __device__ __forceinline__ int opaque(int v) {
 // ---------------------------------------------------------------------------
 // source-strip kernel.  One 256-thread block per (b, c, group, source strip S),
 // two blocks per CU.  Wave w owns the source columns sigma = 64 S + 16 w +
-// lane % 16.  The group's heads run in passes (one launch each, in order) of
-// HS = min(HPG, 2) heads: du, x_B, ddt, q, r of those heads.  dB and the dCB
-// planes need every head of the group: a pass that is not the last parks its
-// fp32 share of dCB in the 64 bytes per lane that the last pass overwrites
-// with the hi / lo planes, and the state part of dB from its own heads in a
-// workspace slot of the block; the last pass starts dB from that slot, adds
-// the parked dCB shares back, writes the planes and adds dB's intra part.
-// Passes other than the last hold the source row's B and their heads' u rows
-// in registers for the whole pass.
+// lane % 16.  The block walks the group's heads in passes of HS heads (two,
+// or one for a one-head group): du, x_B, ddt, q, r of those heads.  dB and
+// the dCB planes need every head of the group.  dB^T stays in registers from
+// the first pass to the last (state part of every head, then the intra part
+// in the last pass).  dCB of a target strip is summed over the passes in the
+// 64 bytes per lane that the last pass overwrites with the hi / lo planes: a
+// pass other than the last stores its running fp32 sum there and the next
+// pass adds its share to it (each lane reads back only what it wrote).
+// Passes other than the last hold their heads' u rows in registers; every
+// pass holds the source row's B.
 // ---------------------------------------------------------------------------
-template <int NK, int HPG>
+template <int NK>
 struct SrcSmem {
   static constexpr int N = 32 * NK;
   static constexpr int kStage = 2 * kPlaneT;       // bf16: one head's dy tile or dS n half (hi, lo)
   static constexpr int kC = 64 * N;                // bf16: one C tile
 };
 
-template <int NK, int HPG, int PASS>
+enum SrcMode { kSrcOnly = 0, kSrcFirst = 1, kSrcMiddle = 2, kSrcLast = 3 };
+
+template <int NK, int HS, bool MID>
 __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     const bf16* __restrict__ u, const bf16* __restrict__ Bm, const bf16* __restrict__ Cm,
     const bf16* __restrict__ dyp, const float* __restrict__ dt, const float* __restrict__ dc,
     const bf16* __restrict__ dSp, const int64_t* __restrict__ length, bf16* __restrict__ du,
     bf16* __restrict__ dB, bf16* __restrict__ dcbp, float* __restrict__ ddt_part,
     float* __restrict__ xB_part, float* __restrict__ qpart, float* __restrict__ rpart,
-    float* __restrict__ dbpark, SsdDims d, int mono) {
-  using SM = SrcSmem<NK, HPG>;
+    SsdDims d, int mono) {
+  using SM = SrcSmem<NK>;
   constexpr int N = SM::N;
-  constexpr int HS = HPG < 2 ? HPG : 2;          // heads per pass
-  constexpr int NPASS = (HPG + HS - 1) / HS;
-  constexpr int pass = PASS;
-  constexpr bool last = PASS == NPASS - 1;
-  constexpr int KB = PASS * HS;                  // first head of this pass
-  constexpr int KE = KB + HS < HPG ? KB + HS : HPG;   // one past its last
-  static_assert(PASS < NPASS, "ssd_bwd_src: pass");
   constexpr int NH = N / 64;     // 64-wide n halves of a dS tile
   constexpr int NT = N / 16;     // 16-row n tiles of dB^T
   static_assert(NH == 2, "ssd_bwd_src: state_dim 128");
+  static_assert(HS == 1 || HS == 2, "ssd_bwd_src: one or two heads per pass");
   // Separate LDS objects per stage buffer: with the stage parity a
   // compile-time constant, the compiler sees that the reads of one buffer do
   // not depend on the DMA into the other and inserts no waits for it.
@@ -314,12 +311,14 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   __shared__ __align__(16) bf16 stg1[SM::kStage];
   __shared__ __align__(16) bf16 Cs0[SM::kC];        // [64][N]
   __shared__ __align__(16) bf16 Cs1[SM::kC];
-  __shared__ __align__(16) float dcs[2 * HPG * 64];  // [T parity][head][64] dc (log2)
-  __shared__ __align__(16) float ats[2 * HPG * 64];  // [T parity][head][64] e^{dc - dc_T0}
+  __shared__ __align__(16) float dcs[2 * HS * 64];   // [T parity][head of the pass][64] dc (log2)
+  __shared__ __align__(16) float ats[2 * HS * 64];   // [T parity][head of the pass][64] e^{dc - dc_T0}
   __shared__ __align__(16) float rx[2 * 4 * 64];     // [stage parity][4 waves][64] row sums
   auto stg = [&](int par) -> bf16* { return par ? stg1 : stg0; };
   auto Cs = [&](int par) -> bf16* { return par ? Cs1 : Cs0; };
 
+  const int hpg = d.H / d.G;
+  const int npass = (hpg + HS - 1) / HS;
   const int stiles = d.Lc / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
   const int S = bid % stiles;
@@ -338,7 +337,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   const int w = wave_index();
   const int sl = 16 * w + li;        // this lane's source column within the strip
   const int sig = s0 + sl;           // its chunk position
-  const int h0 = g * HPG;
+  const int h0 = g * hpg;
   const long bhc0 = (static_cast<long>(b) * d.H + h0) * d.nc + c;   // head k: + k nc
   const int hstride = d.nc * d.Lc;
   const long bcg = (static_cast<long>(b) * d.nc + c) * d.G + g;
@@ -356,19 +355,17 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   const int rstride = d.nc * stiles * d.Lc;
 
   if (s0 >= lim) {   // the strip is past the length: zero outputs and partials
-    for (int e = tid; e < 64 * (KE - KB) * 8; e += 256) {
-      const int row = e / ((KE - KB) * 8), col8 = e % ((KE - KB) * 8);
+    for (int e = tid; e < 64 * hpg * 8; e += 256) {
+      const int row = e / (hpg * 8), col8 = e % (hpg * 8);
       if (s0 + row < qlim)
-        *reinterpret_cast<uint4*>(duc + static_cast<unsigned>((s0 + row) * u_rs + KB * 64 + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<uint4*>(duc + static_cast<unsigned>((s0 + row) * u_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
     }
-    if (last) {
-      for (int e = tid; e < 64 * (N / 8); e += 256) {
-        const int row = e / (N / 8), col8 = e % (N / 8);
-        if (s0 + row < qlim)
-          *reinterpret_cast<uint4*>(dBc + static_cast<unsigned>((s0 + row) * act_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
-      }
+    for (int e = tid; e < 64 * (N / 8); e += 256) {
+      const int row = e / (N / 8), col8 = e % (N / 8);
+      if (s0 + row < qlim)
+        *reinterpret_cast<uint4*>(dBc + static_cast<unsigned>((s0 + row) * act_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
     }
-    for (int k = KB; k < KE; ++k) {
+    for (int k = 0; k < hpg; ++k) {
       if (tid < 64) {
         ddtc[k * hstride + s0 + tid] = 0.f;
         xBc[k * hstride + s0 + tid] = 0.f;
@@ -383,123 +380,19 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   const int scl = min(sig, lim - 1);       // clamped source row (a valid address)
   const int ntile = (lim + 63) / 64 - S;   // target strips T = S .. S + ntile - 1
 
-  // Stages of pass p: first one state stage per head p HS + j, its dS n
+  // Stages of a pass: first one state stage per head of the pass, its dS n
   // half 0 in the stage buffer and n half 1 in a C buffer (no C tile is in
   // use before the pair stages); then per target strip T = S + Ti the dy
-  // tile of head p HS + h, h = 0..HS-1 (C_T and the dc tables come with
-  // h == 0).
-  auto n_state = [&](int) { return HS; };
-  // C buffers: strip T's tile goes into buffer (T - S) & 1, and state stage j
-  // takes buffer (HS - j) & 1, a compile-time choice (the last state stage
-  // takes buffer 1, which the first pair stage's tile does not go into)
+  // tile of head h = 0..HS-1 of the pass (C_T and the dc tables come with
+  // h == 0).  C buffers: strip T's tile goes into buffer (T - S) & 1, and
+  // state stage j takes buffer (HS - j) & 1, a compile-time choice (the last
+  // state stage takes buffer 1, which the first pair stage's tile does not
+  // go into).
+  constexpr int nst = HS;
   auto state_cpar = [&](int j) { return (HS - j) & 1; };
-  auto n_stage = [&](int p) { return n_state(p) + HS * ntile; };
-  const bf16* dyg = dyp + (bcg * stiles) * (HPG * 2L * kPlaneT);   // + (T HPG + k) 2 kPlaneT
+  const int n_stage = nst + HS * ntile;
+  const bf16* dyg = dyp + (bcg * stiles) * (static_cast<long>(hpg) * 2 * kPlaneT);   // + (T hpg + k) 2 kPlaneT
   const bf16* dSg = dSp + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (2L * 64 * N);
-  int o_gs[2], o_gy[2], o_gc[NK];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    o_gs[i] = dma_off<8, swz_s128>(i, w, lane, N);
-    o_gy[i] = dma_off<8, swz_k128>(i, w, lane, 64);
-  }
-#pragma unroll
-  for (int i = 0; i < NK; ++i) o_gc[i] = dma_off<NK * 4, swz_k256>(i, w, lane, act_rs);
-  float pdc = 0.f, pdc0 = 0.f;   // dc prefetch of the next target strip (head tid / 64, row tid % 64)
-  // The last launch has no registers to hold the DMA lane offsets through
-  // the kernel (they were spilled): it recomputes them where a stage is
-  // issued, a few integer operations each.
-  auto lane_offsets = [&](int (&gs)[2], int (&gy)[2], int (&gc)[NK]) {
-    if constexpr (last) {
-      const int ln = opaque(lane);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        gs[i] = dma_off<8, swz_s128>(i, w, ln, N);
-        gy[i] = dma_off<8, swz_k128>(i, w, ln, 64);
-      }
-#pragma unroll
-      for (int i = 0; i < NK; ++i) gc[i] = dma_off<NK * 4, swz_k256>(i, w, ln, act_rs);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        gs[i] = o_gs[i];
-        gy[i] = o_gy[i];
-      }
-#pragma unroll
-      for (int i = 0; i < NK; ++i) gc[i] = o_gc[i];
-    }
-  };
-  auto issue = [&](int p, int j, int par) {   // par: the stage's buffer
-    if (p >= NPASS) return;
-    bf16* dst = stg(par);
-    const int nst = n_state(p);
-    int gs[2], gy[2], gc[NK];
-    lane_offsets(gs, gy, gc);
-    if (j < nst) {
-      const int k = p * HS + j;
-      if (k < HPG) {
-        const bf16* src = dSg + k * (2L * 64 * N);
-        bf16* cdst = Cs(state_cpar(j));
-        dma_pre<8>(dst, src, gs, w);
-        dma_pre<8>(dst + kPlaneT, src + 64L * N, gs, w);
-        dma_pre<8>(cdst, src + 64, gs, w);
-        dma_pre<8>(cdst + kPlaneT, src + 64 + 64L * N, gs, w);
-      }
-    } else {
-      const int qq = j - nst, Ti = qq / HS, h = qq % HS, T = S + Ti, k = p * HS + h;
-      if (k < HPG) {
-        const bf16* src = dyg + (static_cast<long>(T) * HPG + k) * (2L * kPlaneT);
-        dma_pre<8>(dst, src, gy, w);
-        dma_pre<8>(dst + kPlaneT, src + kPlaneT, gy, w);
-      }
-      if (h == 0) {
-        const int t0 = 64 * T;
-        bf16* cdst = Cs((T - S) & 1);
-        const bf16* csrc = Cc + static_cast<long>(t0) * act_rs;
-        if (qlim - t0 >= 64) dma_pre<NK * 4>(cdst, csrc, gc, w);
-        else dma_tile<NK * 4, swz_k256>(cdst, csrc, act_rs, qlim - t0, w, lane);
-        if (tid < HPG * 64) {   // raw: nothing waits for these before the stage's end
-          const float* dch = dcc + (tid >> 6) * hstride + t0;
-          pdc = dch[tid & 63];
-          pdc0 = dch[0];
-        }
-      }
-    }
-  };
-  // the next stage after stage j (buffer par) of pass p
-  auto issue_next = [&](int p, int j, int par) {
-    if (j + 1 < n_stage(p)) issue(p, j + 1, par ^ 1);
-  };
-  // end of the stage before stage j of pass p: the dc tables of a new target
-  // strip, then every DMA of the next stage complete and visible
-  auto end_stage = [&](int p, int j) {
-    const int nst = n_state(p);
-    if (j < n_stage(p) && j >= nst && (j - nst) % HS == 0 && tid < HPG * 64) {
-      const int T = S + (j - nst) / HS;
-      dcs[(T & 1) * HPG * 64 + tid] = pdc * kLog2e;
-      ats[(T & 1) * HPG * 64 + tid] = fast_exp2(fminf(pdc * kLog2e - pdc0 * kLog2e, 0.f));
-    }
-    wait_all_mem();
-    __syncthreads();
-  };
-  auto flush_r = [&](int p, int j, int par) {   // the row sums pair stage j left in LDS -> rpart
-    const int qq = j - n_state(p), Ti = qq / HS, k = p * HS + qq % HS;
-    if (tid < 64 && k < HPG) {
-      const float* rr = rx + par * 256;
-      rc[k * rstride + 64 * (S + Ti) + tid] = rr[tid] + rr[64 + tid] + rr[128 + tid] + rr[192 + tid];
-    }
-  };
-
-  // per-lane element offsets of the fragment reads inside a tile (the
-  // swizzle of every row this lane reads depends on lane bits only, so each
-  // read is a precomputed offset plus a compile-time constant)
-  const int rl = 8 * (li >> 2) + (li & 3);   // key_of_row(kt, li) = rl + kro(kt)
-  int o_w[2], o_tr[4], o_c[NK];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) o_w[ks] = toff<8, swz_k128>(rl, 32 * ks + 8 * lg);
-#pragma unroll
-  for (int pt = 0; pt < 4; ++pt) o_tr[pt] = tr_first<8, swz_k128>(8 * lg, 16 * pt, lane);
-#pragma unroll
-  for (int ks = 0; ks < NK; ++ks) o_c[ks] = toff<NK * 4, swz_k256>(rl, 32 * ks + 8 * lg);
 
   // this lane's 64 bytes of the dCB tile (S, Tp): chunk q = 2 ks + (hi, lo)
   // holds dCB[tau = 64 Tp + 32 ks + 8 lg .. + 7][sigma = sig] of that plane.
@@ -513,57 +406,132 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
            (w * 64 + li * 4 + lg) * 8;
   };
 
-  // B of this lane's source row (all N) and u of this pass' heads there are
-  // the same in every stage: a pass other than the last loads them once,
-  // with the first stage, instead of at the start of each stage that uses
-  // them (where each load's latency was exposed).  The last pass has no
-  // registers to spare and loads them per stage.
-  constexpr bool kHold = !last;
-  constexpr bool kHoldB = true;   // B of the source row: every pass
-  const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 8 * lg);
-  v8bf Bh[NK], Uh[HS][2];
-#pragma unroll
-  for (int ks = 0; ks < NK; ++ks) Bh[ks] = kHoldB && sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
-#pragma unroll
-  for (int h = 0; h < HS; ++h) {
-    const int k = pass * HS + h;
-    const bf16* urow = uc + min(k, HPG - 1) * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      Uh[h][ks] = kHold && sv && k < HPG ? load_v8bf(urow + 32 * ks) : zero_v8bf();
-  }
-  // dB^T rows n = 16 nt + 4 lg + r, column sig.  Every pass forms the state
-  // part of its own heads; a pass other than the last parks it (this
-  // thread's 128 bytes of the block's slot) and the last pass starts from
-  // the parked part, so no pass reads another pass' dS tiles.
+  // dB^T rows n = 16 nt + 4 lg + r, column sig: the state part of every head
+  // (every pass), then the intra part (last pass)
   v4f dBT[NT];
-  float4* const park = reinterpret_cast<float4*>(dbpark) + static_cast<long>(bid) * (NT * 256) + tid;
-  if constexpr (last && NPASS > 1) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const float4 v = park[nt * 256];
-      dBT[nt] = v4f{v.x, v.y, v.z, v.w};
-    }
-  } else {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) dBT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
-  }
-  issue(pass, 0, n_state(pass) & 1);   // stage j has buffer parity (j + n_state) & 1
-  wait_all_mem();
-  __syncthreads();
+  for (int nt = 0; nt < NT; ++nt) dBT[nt] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  // Stage buffers alternate: stage j has buffer parity (j + HS) & 1, so a
-  // pair stage's buffer is its head (with one head per pass, its strip's
-  // parity).
-  // Each stage issues its own register loads before the next stage's DMA, so
-  // that waiting for them does not wait for the DMA.
-  {
-    const int nst = n_state(pass);
+  // one pass over heads KB .. KB + HS - 1 (those < hpg)
+  auto run_pass = [&](auto mode_c, const int pass) {
+    constexpr int MODE = decltype(mode_c)::value;
+    constexpr bool last = MODE == kSrcOnly || MODE == kSrcLast;
+    constexpr bool first = MODE == kSrcOnly || MODE == kSrcFirst;
+    const int KB = pass * HS;
+    float pdc = 0.f, pdc0 = 0.f;   // dc prefetch of the next target strip (head tid / 64, row tid % 64)
+    // Values derived from the lane id are recomputed in each pass (and the
+    // DMA lane offsets where a stage is issued, a few integer operations
+    // each) from an opaque copy of it, so that none of them is held in a
+    // register from one pass to the next.
+    const int lnp = opaque(lane);
+    const int lgp = lnp >> 4, lip = lnp & 15;
+    auto lane_offsets = [&](int (&gs)[2], int (&gy)[2], int (&gc)[NK]) {
+      const int ln = opaque(lane);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        gs[i] = dma_off<8, swz_s128>(i, w, ln, N);
+        gy[i] = dma_off<8, swz_k128>(i, w, ln, 64);
+      }
+#pragma unroll
+      for (int i = 0; i < NK; ++i) gc[i] = dma_off<NK * 4, swz_k256>(i, w, ln, act_rs);
+    };
+    // per-lane element offsets of the fragment reads inside a tile (the
+    // swizzle of every row this lane reads depends on lane bits only, so
+    // each read is a precomputed offset plus a compile-time constant)
+    const int rl = 8 * (lip >> 2) + (lip & 3);   // key_of_row(kt, li) = rl + kro(kt)
+    int o_w[2], o_tr[4], o_c[NK];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) o_w[ks] = toff<8, swz_k128>(rl, 32 * ks + 8 * lgp);
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) o_tr[pt] = tr_first<8, swz_k128>(8 * lgp, 16 * pt, lnp);
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) o_c[ks] = toff<NK * 4, swz_k256>(rl, 32 * ks + 8 * lgp);
+    // B of this lane's source row (all N): the same in every stage of the pass
+    const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 8 * lgp);
+    v8bf Bh[NK];
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) Bh[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
+    auto issue = [&](int j, int par) {   // par: the stage's buffer
+      bf16* dst = stg(par);
+      int gs[2], gy[2], gc[NK];
+      lane_offsets(gs, gy, gc);
+      if (j < nst) {
+        const int k = KB + j;
+        if (k < hpg) {
+          const bf16* src = dSg + k * (2L * 64 * N);
+          bf16* cdst = Cs(state_cpar(j));
+          dma_pre<8>(dst, src, gs, w);
+          dma_pre<8>(dst + kPlaneT, src + 64L * N, gs, w);
+          dma_pre<8>(cdst, src + 64, gs, w);
+          dma_pre<8>(cdst + kPlaneT, src + 64 + 64L * N, gs, w);
+        }
+      } else {
+        const int qq = j - nst, Ti = qq / HS, h = qq % HS, T = S + Ti, k = KB + h;
+        if (k < hpg) {
+          const bf16* src = dyg + (static_cast<long>(T) * hpg + k) * (2L * kPlaneT);
+          dma_pre<8>(dst, src, gy, w);
+          dma_pre<8>(dst + kPlaneT, src + kPlaneT, gy, w);
+        }
+        if (h == 0) {
+          const int t0 = 64 * T;
+          bf16* cdst = Cs((T - S) & 1);
+          const bf16* csrc = Cc + static_cast<long>(t0) * act_rs;
+          if (qlim - t0 >= 64) dma_pre<NK * 4>(cdst, csrc, gc, w);
+          else dma_tile<NK * 4, swz_k256>(cdst, csrc, act_rs, qlim - t0, w, lane);
+          if (tid < HS * 64) {   // raw: nothing waits for these before the stage's end
+            const int k2 = min(KB + (tid >> 6), hpg - 1);
+            const float* dch = dcc + k2 * hstride + t0;
+            pdc = dch[tid & 63];
+            pdc0 = dch[0];
+          }
+        }
+      }
+    };
+    // the next stage after stage j (buffer par) of this pass
+    auto issue_next = [&](int j, int par) {
+      if (j + 1 < n_stage) issue(j + 1, par ^ 1);
+    };
+    // end of the stage before stage j: the dc tables of a new target strip,
+    // then every DMA of the next stage complete and visible
+    auto end_stage = [&](int j) {
+      if (j < n_stage && j >= nst && (j - nst) % HS == 0 && tid < HS * 64) {
+        const int T = S + (j - nst) / HS;
+        dcs[(T & 1) * HS * 64 + tid] = pdc * kLog2e;
+        ats[(T & 1) * HS * 64 + tid] = fast_exp2(fminf(pdc * kLog2e - pdc0 * kLog2e, 0.f));
+      }
+      wait_all_mem();
+      __syncthreads();
+    };
+    auto flush_r = [&](int j, int par) {   // the row sums pair stage j left in LDS -> rpart
+      const int qq = j - nst, Ti = qq / HS, k = KB + qq % HS;
+      if (tid < 64 && k < hpg) {
+        const float* rr = rx + par * 256;
+        rc[k * rstride + 64 * (S + Ti) + tid] = rr[tid] + rr[64 + tid] + rr[128 + tid] + rr[192 + tid];
+      }
+    };
+
+    // u rows of this pass' heads: held for the whole pass by the first pass;
+    // the others (which hold the running dCB sum or finish dB) have no
+    // registers to spare and load them per stage
+    constexpr bool kHold = first && !last;
+    v8bf Uh[HS][2];
+#pragma unroll
+    for (int h = 0; h < HS; ++h) {
+      const int k = KB + h;
+      const bf16* urow = uc + min(k, hpg - 1) * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        Uh[h][ks] = kHold && sv && k < hpg ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+    }
+    issue(0, nst & 1);   // stage j has buffer parity (j + nst) & 1
+    wait_all_mem();
+    __syncthreads();
+
     v4f duT[HS][4];   // du^T of this pass' heads: rows p = 16 pt + 4 lg + r, column sig
     float qacc[HS], dtk[HS], dck[HS], ekh[HS];
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
-      const int k = min(pass * HS + h, HPG - 1);
+      const int k = min(KB + h, hpg - 1);
       dck[h] = dcc[k * hstride + scl] * kLog2e;
       dtk[h] = sv ? dtc[k * hstride + scl] : 0.f;
       // e^{min(dc_last - dc_sig, 0)}: the state weight is ekh dt
@@ -603,24 +571,18 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
       };
 #pragma unroll
       for (int h = 0; h < HS; ++h) {
-        const int k = pass * HS + h;
-        const bool kv = k < HPG;
+        const int k = KB + h;
+        const bool kv = k < hpg;
         const int j = h, par = (h + HS) & 1;
-        v8bf Bf[NK], ul[2] = {Uh[h][0], Uh[h][1]};
-#pragma unroll
-        for (int ks = 0; ks < NK; ++ks) Bf[ks] = Bh[ks];
+        v8bf ul[2] = {Uh[h][0], Uh[h][1]};
         uint2 ux[4];    // u of head k at this lane's column, for x_B
         if (kv && !kHold) {
           const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
-          if (!kHoldB) {
-#pragma unroll
-            for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
-          }
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) ul[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
         }
         __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the DMA
-        issue_next(pass, j, par);
+        issue_next(j, par);
         if (kv) {
 #pragma unroll
           for (int half = 0; half < NH; ++half) {
@@ -636,8 +598,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 #pragma unroll
               for (int pt = 0; pt < 4; ++pt) {
                 const int off = o_sd[ks] + 16 * pt * 64;
-                duT[h][pt] = mfma_bf16(load_v8bf(Yh + off), Bf[2 * half + ks], duT[h][pt]);
-                duT[h][pt] = mfma_bf16(load_v8bf(Yl + off), Bf[2 * half + ks], duT[h][pt]);
+                duT[h][pt] = mfma_bf16(load_v8bf(Yh + off), Bh[2 * half + ks], duT[h][pt]);
+                duT[h][pt] = mfma_bf16(load_v8bf(Yl + off), Bh[2 * half + ks], duT[h][pt]);
               }
             state_dB(Yh, ul, ekh[h] * dtk[h], half);
             __builtin_amdgcn_sched_barrier(0);   // the halves' operand reads stay apart
@@ -653,34 +615,31 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
           sx = group_sum(sv ? sx : 0.f) * dtk[h];
           if (lg == 0) xBc[k * hstride + sig] = sx;
         }
-        end_stage(pass, j + 1);
+        end_stage(j + 1);
       }
     }
-    if constexpr (!last) {   // the state part of dB for the last pass
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) park[nt * 256] = make_float4(dBT[nt][0], dBT[nt][1], dBT[nt][2], dBT[nt][3]);
-    }
 
-    // the dCB of target strip Tp: park this pass' share, or (last pass) add
-    // the parked shares, dB^T[n, sig] += sum_t C[t, n] dCB[t, sig] and store
-    // the hi / lo planes
-    // (prev: the parked shares, loaded at the end of the stage before)
+    // the dCB of target strip Tp: store this pass' running sum (fp32, in the
+    // bytes of the planes), or (last pass) finish it: dB^T[n, sig] += sum_t
+    // C[t, n] dCB[t, sig] and store the hi / lo planes
+    // (prev: the running sum of the passes before, loaded at the end of the
+    // stage before)
     auto load_prev = [&](int Tp, float4 (&prev)[4]) {
-      if (last && NPASS > 1) {
+      if constexpr (!first) {
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) prev[kt] = *reinterpret_cast<const float4*>(dcb_at(Tp, kt));
       }
     };
     auto finish_pair = [&](int Tp, v4f (&dCBa)[4], const float4 (&prev)[4]) {
-      if (!last) {
+      if constexpr (!first) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) dCBa[kt] += v4f{prev[kt].x, prev[kt].y, prev[kt].z, prev[kt].w};
+      }
+      if constexpr (!last) {
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
           *reinterpret_cast<float4*>(dcb_at(Tp, kt)) = make_float4(dCBa[kt][0], dCBa[kt][1], dCBa[kt][2], dCBa[kt][3]);
         return;
-      }
-      if (NPASS > 1) {
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) dCBa[kt] += v4f{prev[kt].x, prev[kt].y, prev[kt].z, prev[kt].w};
       }
       const bf16* Cb = Cs((Tp - S) & 1);
       const int ctb = tr_first<NK * 4, swz_k256>(8 * lg, 0, lane);   // column tile 0
@@ -703,7 +662,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
       }
     };
 
-    // ---- pair stages: target strip T = S + Ti, head k = pass HS + h ----
+    // ---- pair stages: target strip T = S + Ti, head k = KB + h ----
     v4f dCBa[4];
     float4 prev[4];
     for (int Ti = 0; Ti < ntile; ++Ti) {
@@ -715,17 +674,11 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 #pragma unroll
       for (int h = 0; h < HS; ++h) {
         const int j = nst + Ti * HS + h;
-        const int k = pass * HS + h;
-        const bool kv = k < HPG;
+        const int k = KB + h;
+        const bool kv = k < hpg;
         const int par = HS == 1 ? (Ti & 1) : h;
         // register loads of this stage, before the next stage's DMA
-        v8bf Bf[NK], uf[2] = {Uh[h][0], Uh[h][1]};
-#pragma unroll
-        for (int ks = 0; ks < NK; ++ks) Bf[ks] = Bh[ks];
-        if (!kHoldB && h == 0) {
-#pragma unroll
-          for (int ks = 0; ks < NK; ++ks) Bf[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
-        }
+        v8bf uf[2] = {Uh[h][0], Uh[h][1]};
         if (!kHold && kv) {
           const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
 #pragma unroll
@@ -738,8 +691,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
           finish_pair(T - 1, dCBa, prev);
           __syncthreads();
         }
-        issue_next(pass, j, par);
-        if (j > nst) flush_r(pass, j - 1, par ^ 1);
+        issue_next(j, par);
+        if (j > nst) flush_r(j - 1, par ^ 1);
         if (HS > 1 && h == 0 && Ti > 0) finish_pair(T - 1, dCBa, prev);
         const bf16* Yh = stg(par);
         const bf16* Yl = Yh + kPlaneT;
@@ -750,12 +703,12 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
             dCBa[kt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < NK; ++ks)
-              CB[kt] = mfma_bf16(load_v8bf(Cb + o_c[ks] + kro(kt) * N), Bf[ks], CB[kt]);
+              CB[kt] = mfma_bf16(load_v8bf(Cb + o_c[ks] + kro(kt) * N), Bh[ks], CB[kt]);
           }
         }
         if (kv) {
-          const float* dcT = dcs + (T & 1) * HPG * 64 + 64 * k;
-          const float* atT = ats + (T & 1) * HPG * 64 + 64 * k;
+          const float* dcT = dcs + (T & 1) * HS * 64 + 64 * h;
+          const float* atT = ats + (T & 1) * HS * 64 + 64 * h;
           const float dk = dck[h], dtv = dtk[h];
           // W[t, sig] = dy[t] . u[sig]
           // the four row tiles' accumulators in turn, one (k step, plane)
@@ -837,21 +790,23 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
             }
           }
         }
-        // the parked dCB shares of this strip, for finish_pair in the next stage
+        // the running dCB sum of the passes before, for finish_pair in the
+        // next stage
         if (h == HS - 1) load_prev(T, prev);
-        end_stage(pass, j + 1);
+        end_stage(j + 1);
       }
     }
-    flush_r(pass, n_stage(pass) - 1, HS == 1 ? ((ntile - 1) & 1) : HS - 1);
+    flush_r(n_stage - 1, HS == 1 ? ((ntile - 1) & 1) : HS - 1);
     finish_pair(S + ntile - 1, dCBa, prev);
-    // every wave is done with the stage buffers: they stage du (stg0) and dB (stg1)
+    // every wave is done with the stage buffers: they stage du (stg0) and,
+    // after the last pass, dB (stg1)
     __syncthreads();
 
     // ---- du, ddt_direct, q of this pass' heads ----
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
-      const int k = pass * HS + h;
-      if (k >= HPG) continue;
+      const int k = KB + h;
+      if (k >= hpg) continue;
       const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
       float sx = 0.f;
 #pragma unroll
@@ -865,19 +820,37 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         qc[k * hstride + sig] = qv;
       }
     }
-  }
-  // row-sum partials of target strips past the length are zero
-  for (int k = KB; k < KE; ++k)
-    for (int t = 64 * (S + ntile) + tid; t < d.Lc; t += 256) rc[k * rstride + t] = 0.f;
-  if (last) {
+    // row-sum partials of target strips past the length are zero
+    for (int k = KB; k < min(KB + HS, hpg); ++k)
+      for (int t = 64 * (S + ntile) + tid; t < d.Lc; t += 256) rc[k * rstride + t] = 0.f;
+    if constexpr (last) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) stage_out8<16>(stg1, sl, 16 * nt + 4 * lg, pack4_bf16(dBT[nt]));
-  }
-  __syncthreads();
+      for (int nt = 0; nt < NT; ++nt) stage_out8<16>(stg1, sl, 16 * nt + 4 * lg, pack4_bf16(dBT[nt]));
+    }
+    __syncthreads();
 #pragma unroll
-  for (int h = 0; h < HS; ++h)
-    if (KB + h < HPG) write_rows<8>(stg0 + h * 4096, duc + (KB + h) * 64 + s0 * u_rs, u_rs, qlim - s0, tid);
-  if (last) write_rows<16>(stg1, dBc + s0 * act_rs, act_rs, qlim - s0, tid);
+    for (int h = 0; h < HS; ++h)
+      if (KB + h < hpg) write_rows<8>(stg0 + h * 4096, duc + (KB + h) * 64 + s0 * u_rs, u_rs, qlim - s0, tid);
+    if constexpr (last) write_rows<16>(stg1, dBc + s0 * act_rs, act_rs, qlim - s0, tid);
+    // the next pass' first DMA goes into these buffers
+    if constexpr (!last) __syncthreads();
+  };
+
+  if constexpr (HS == 1) {
+    run_pass(std::integral_constant<int, kSrcOnly>{}, 0);
+  } else if constexpr (!MID) {
+    if (npass == 1) {
+      run_pass(std::integral_constant<int, kSrcOnly>{}, 0);
+    } else {
+      run_pass(std::integral_constant<int, kSrcFirst>{}, 0);
+      run_pass(std::integral_constant<int, kSrcLast>{}, 1);
+    }
+  } else {
+    run_pass(std::integral_constant<int, kSrcFirst>{}, 0);
+    for (int pass = 1; pass + 1 < npass; ++pass)
+      run_pass(std::integral_constant<int, kSrcMiddle>{}, pass);
+    run_pass(std::integral_constant<int, kSrcLast>{}, npass - 1);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -897,7 +870,7 @@ struct TgtSmem {
   static constexpr size_t bytes = 2 * kStage * 2;
 };
 
-template <int NK, int HPG>
+template <int NK>
 __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
     const bf16* __restrict__ Bm, const bf16* __restrict__ Cm, const bf16* __restrict__ dyp,
     const float* __restrict__ dc, const float* __restrict__ states,
@@ -911,6 +884,7 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
   extern __shared__ __align__(16) unsigned char smem_raw[];
   bf16* stg = reinterpret_cast<bf16*>(smem_raw);   // [2][kStage]
 
+  const int HPG = d.H / d.G;
   const int ttiles = d.Lc / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
   const int half = bid & 1;
@@ -1102,17 +1076,14 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
 // The host pass leaves the stubs of ssd_bwd_src_kernel undefined when it only
 // meets them through a launch (its device lambdas are not substituted there);
 // explicit instantiation makes it emit them.
-#define SA_SRC_INST(HPG, PASS)                                                                   \
-  template __global__ void ssd_bwd_src_kernel<4, HPG, PASS>(                                     \
+#define SA_SRC_INST(HS, MID)                                                                     \
+  template __global__ void ssd_bwd_src_kernel<4, HS, MID>(                                       \
       const bf16*, const bf16*, const bf16*, const bf16*, const float*, const float*,            \
-      const bf16*, const int64_t*, bf16*, bf16*, bf16*, float*, float*, float*, float*, float*,  \
+      const bf16*, const int64_t*, bf16*, bf16*, bf16*, float*, float*, float*, float*,          \
       SsdDims, int);
-SA_SRC_INST(1, 0)
-SA_SRC_INST(2, 0)
-SA_SRC_INST(3, 0)
-SA_SRC_INST(3, 1)
-SA_SRC_INST(4, 0)
-SA_SRC_INST(4, 1)
+SA_SRC_INST(1, false)
+SA_SRC_INST(2, false)
+SA_SRC_INST(2, true)
 #undef SA_SRC_INST
 
 template <typename K>
@@ -1125,34 +1096,32 @@ int raise_smem(K kernel, size_t bytes, const char* who) {
   return 0;
 }
 
-template <int HPG>
-int launch_fused_hpg(const void* u, const void* B, const void* C, const bf16* dyp,
-                     const float* dt, const float* dc, const float* states, const bf16* dSp,
-                     const int64_t* length, void* du, void* dB, void* dC, bf16* dcbp,
-                     float* ddt_part, float* xB_part, float* xC_part, float* qpart, float* rpart,
-                     float* dbpark, const SsdDims& d, bool dt_nonneg, hipStream_t s) {
+int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const bf16* dyp,
+                         const float* dt, const float* dc, const float* states, const bf16* dSp,
+                         const int64_t* length, void* du, void* dB, void* dC, bf16* dcbp,
+                         float* ddt_part, float* xB_part, float* xC_part, float* qpart,
+                         float* rpart, const SsdDims& d, bool dt_nonneg, hipStream_t s) {
   constexpr int NK = 4;
   const long blocks = static_cast<long>(d.b) * d.nc * d.G * (d.Lc / 64);
-  auto src_pass = [&](auto kernel) -> int {
+  {
+    // one launch walks every head of the group (in passes of two heads
+    // inside each block)
     ProfScope prof_("ssd_bwd_src", s);
+    const int hpg = d.H / d.G;
+    auto kernel = hpg == 1 ? ssd_bwd_src_kernel<NK, 1, false>
+                           : hpg <= 4 ? ssd_bwd_src_kernel<NK, 2, false> : ssd_bwd_src_kernel<NK, 2, true>;
     hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), 0, s,
                        static_cast<const bf16*>(u), static_cast<const bf16*>(B),
                        static_cast<const bf16*>(C), dyp, dt, dc, dSp, length,
                        static_cast<bf16*>(du), static_cast<bf16*>(dB), dcbp, ddt_part, xB_part,
-                       qpart, rpart, dbpark, d, dt_nonneg ? 1 : 0);
+                       qpart, rpart, d, dt_nonneg ? 1 : 0);
     SA_CHECK_LAUNCH("ssd_bwd_src");
-    return 0;
-  };
-  // heads in passes of two, one launch each (the last one completes dB and dCB)
-  if (const int rc = src_pass(ssd_bwd_src_kernel<NK, HPG, 0>)) return rc;
-  if constexpr (HPG > 2) {
-    if (const int rc = src_pass(ssd_bwd_src_kernel<NK, HPG, 1>)) return rc;
   }
   {
     const size_t smem = TgtSmem<NK>::bytes;
-    if (const int rc = raise_smem(ssd_bwd_tgt_kernel<NK, HPG>, smem, "ssd_bwd_tgt")) return rc;
+    if (const int rc = raise_smem(ssd_bwd_tgt_kernel<NK>, smem, "ssd_bwd_tgt")) return rc;
     ProfScope prof_("ssd_bwd_tgt", s);
-    hipLaunchKernelGGL((ssd_bwd_tgt_kernel<NK, HPG>), dim3(2 * blocks), dim3(256), smem, s,
+    hipLaunchKernelGGL((ssd_bwd_tgt_kernel<NK>), dim3(2 * blocks), dim3(256), smem, s,
                        static_cast<const bf16*>(B), static_cast<const bf16*>(C), dyp, dc, states,
                        dcbp, length, static_cast<bf16*>(dC), xC_part, d);
     SA_CHECK_LAUNCH("ssd_bwd_tgt");
@@ -1161,28 +1130,13 @@ int launch_fused_hpg(const void* u, const void* B, const void* C, const bf16* dy
 }
 
 bool ssd_bwd_fused_shape_ok(const SsdDims& d) {
-  const int hpg = d.H / d.G;
-  return d.P == 64 && d.N == 128 && d.Lc % 64 == 0 && hpg >= 1 && hpg <= 4;
+  return d.P == 64 && d.N == 128 && d.Lc % 64 == 0 && d.H / d.G >= 1;
 }
 
 bool ssd_bwd_fused_ok(const SsdDims& d, const void* u, const void* B, const void* C,
                       const void* dy) {
   return ssd_bwd_fused_shape_ok(d) && aligned16(u) && aligned16(B) && aligned16(C) &&
          aligned16(dy);
-}
-
-int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const bf16* dyp,
-                         const float* dt, const float* dc, const float* states, const bf16* dSp,
-                         const int64_t* length, void* du, void* dB, void* dC, bf16* dcbp,
-                         float* ddt_part, float* xB_part, float* xC_part, float* qpart,
-                         float* rpart, float* dbpark, const SsdDims& d, bool dt_nonneg,
-                         hipStream_t s) {
-  switch (d.H / d.G) {
-    case 1: return launch_fused_hpg<1>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, dbpark, d, dt_nonneg, s);
-    case 2: return launch_fused_hpg<2>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, dbpark, d, dt_nonneg, s);
-    case 3: return launch_fused_hpg<3>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, dbpark, d, dt_nonneg, s);
-    default: return launch_fused_hpg<4>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp, ddt_part, xB_part, xC_part, qpart, rpart, dbpark, d, dt_nonneg, s);
-  }
 }
 
 }  // namespace sa

@@ -60,7 +60,7 @@ int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const bf16
                          const float* dt, const float* dc, const float* states, const bf16* dSp,
                          const int64_t* length, void* du, void* dB, void* dC, bf16* dcbp,
                          float* ddt_part, float* xB_part, float* xC_part, float* qpart,
-                         float* rpart, float* dbpark, const SsdDims& d, bool dt_nonneg,
+                         float* rpart, const SsdDims& d, bool dt_nonneg,
                          hipStream_t s);
 
 // dH_intra (chunk_outer MODE 1, bf16 dy) that also writes dy as the hi + lo

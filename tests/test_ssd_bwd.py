@@ -71,15 +71,22 @@ def test_ssd_bwd_parity(dtype, name, shape, chunk):
     check(make_inputs(dtype=dtype, **shape), chunk, dtype)
 
 
-# bf16, headdim 64, state 64/128, chunk a multiple of 64, <= 4 heads per group:
-# the fused column / row kernels (every other case runs the generic kernels)
+# bf16, headdim 64, state_dim 128, chunk a multiple of 64 (any number of heads
+# per group): the fused source / target kernels; the N = 64 cases and the
+# p128_n192 case run the generic kernels
 FUSED_CASES = [
     ("hpg1_lens", dict(b=2, L=192, H=2, P=64, N=128, G=2, lens=[192, 77]), 64),
-    ("hpg3_ragged", dict(b=1, L=200, H=3, P=64, N=64, G=1, lens=[171]), 128),
+    ("hpg3_ragged_n64", dict(b=1, L=200, H=3, P=64, N=64, G=1, lens=[171]), 128),
     ("hpg4_partial", dict(b=2, L=320, H=8, P=64, N=128, G=2, lens=[320, 130]), 128),
-    # three heads per group: two source launches, the second with one head (dB parked between them)
+    # three heads per group: two passes, the second with one head
     ("hpg3_n128", dict(b=2, L=256, H=6, P=64, N=128, G=2, lens=[256, 171]), 128),
-    ("zero_len", dict(b=2, L=128, H=4, P=64, N=64, G=1, lens=[0, 65], with_h=False), 64),
+    ("zero_len_n64", dict(b=2, L=128, H=4, P=64, N=64, G=1, lens=[0, 65], with_h=False), 64),
+    ("zero_len_n128", dict(b=2, L=128, H=4, P=64, N=128, G=1, lens=[0, 65], with_h=False), 64),
+    # more than four heads per group: first, middle and last passes in one block
+    ("hpg8_mid", dict(b=1, L=256, H=8, P=64, N=128, G=1, lens=[230]), 128),
+    ("hpg5_odd", dict(b=2, L=192, H=10, P=64, N=128, G=2, lens=[192, 100]), 64),
+    # config 4's SSM shape class: 32 heads in one group, chunk 256
+    ("hpg32_c256", dict(b=1, L=512, H=32, P=64, N=128, G=1, lens=[512]), 256),
     # fused path: a zero-length row next to full and partial ones (every strip
     # of that row takes the kernels' early exits), two heads per group
     ("hpg2_zero_len", dict(b=3, L=192, H=4, P=64, N=128, G=2, lens=[192, 0, 100]), 64),
