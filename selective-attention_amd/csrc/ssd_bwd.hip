@@ -940,7 +940,7 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
                                    lo >= 0.f, s)))
       return rc;
     ptiles = ntiles = qtiles = 1;
-    xctiles = 2;   // x_C: one partial per half of N (ssd_bwd_tgt)
+    xctiles = d.N / 64;   // x_C: one partial per 64 n (ssd_bwd_tgt block)
     rtiles = d.Lc / 64;
   } else {
   // 3. du, ddt_direct

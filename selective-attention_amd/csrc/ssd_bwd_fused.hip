@@ -58,6 +58,11 @@ __host__ __device__ __forceinline__ int swz_k256(int r) {
   return ((r & 3) << 1) | (((r >> 3) & 1) << 3) | ((r >> 4) & 1);
 }
 
+// C (and B) tiles of the source kernel: 256-byte rows at state_dim 128,
+// 128-byte rows at state_dim 64, read through key_of_row row sets and transposed
+template <int NK>
+__host__ __device__ __forceinline__ int swz_c(int r) { return NK == 4 ? swz_k256(r) : swz_k128(r); }
+
 // element offset of (row, col) in a swizzled tile with RC 16-byte chunks per row
 template <int RC, int (*F)(int)>
 __device__ __forceinline__ int toff(int row, int col) {
@@ -302,7 +307,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   constexpr int N = SM::N;
   constexpr int NH = N / 64;     // 64-wide n halves of a dS tile
   constexpr int NT = N / 16;     // 16-row n tiles of dB^T
-  static_assert(NH == 2, "ssd_bwd_src: state_dim 128");
+  static_assert(NH == 1 || NH == 2, "ssd_bwd_src: state_dim 64 or 128");
   static_assert(HS == 1 || HS == 2, "ssd_bwd_src: one or two heads per pass");
   // Separate LDS objects per stage buffer: with the stage parity a
   // compile-time constant, the compiler sees that the reads of one buffer do
@@ -393,6 +398,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   const int n_stage = nst + HS * ntile;
   const bf16* dyg = dyp + (bcg * stiles) * (static_cast<long>(hpg) * 2 * kPlaneT);   // + (T hpg + k) 2 kPlaneT
   const bf16* dSg = dSp + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (2L * 64 * N);
+  constexpr int RCB = N / 8;   // 16-byte chunks of a dB row
 
   // this lane's 64 bytes of the dCB tile (S, Tp): chunk q = 2 ks + (hi, lo)
   // holds dCB[tau = 64 Tp + 32 ks + 8 lg .. + 7][sigma = sig] of that plane.
@@ -433,7 +439,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         gy[i] = dma_off<8, swz_k128>(i, w, ln, 64);
       }
 #pragma unroll
-      for (int i = 0; i < NK; ++i) gc[i] = dma_off<NK * 4, swz_k256>(i, w, ln, act_rs);
+      for (int i = 0; i < NK; ++i) gc[i] = dma_off<NK * 4, swz_c<NK>>(i, w, ln, act_rs);
     };
     // per-lane element offsets of the fragment reads inside a tile (the
     // swizzle of every row this lane reads depends on lane bits only, so
@@ -445,7 +451,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) o_tr[pt] = tr_first<8, swz_k128>(8 * lgp, 16 * pt, lnp);
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks) o_c[ks] = toff<NK * 4, swz_k256>(rl, 32 * ks + 8 * lgp);
+    for (int ks = 0; ks < NK; ++ks) o_c[ks] = toff<NK * 4, swz_c<NK>>(rl, 32 * ks + 8 * lgp);
     // B of this lane's source row (all N): the same in every stage of the pass
     const bf16* brow = Bc + static_cast<unsigned>(scl * act_rs + 8 * lgp);
     v8bf Bh[NK];
@@ -462,8 +468,10 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
           bf16* cdst = Cs(state_cpar(j));
           dma_pre<8>(dst, src, gs, w);
           dma_pre<8>(dst + kPlaneT, src + 64L * N, gs, w);
-          dma_pre<8>(cdst, src + 64, gs, w);
-          dma_pre<8>(cdst + kPlaneT, src + 64 + 64L * N, gs, w);
+          if constexpr (NH == 2) {
+            dma_pre<8>(cdst, src + 64, gs, w);
+            dma_pre<8>(cdst + kPlaneT, src + 64 + 64L * N, gs, w);
+          }
         }
       } else {
         const int qq = j - nst, Ti = qq / HS, h = qq % HS, T = S + Ti, k = KB + h;
@@ -477,7 +485,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
           bf16* cdst = Cs((T - S) & 1);
           const bf16* csrc = Cc + static_cast<long>(t0) * act_rs;
           if (qlim - t0 >= 64) dma_pre<NK * 4>(cdst, csrc, gc, w);
-          else dma_tile<NK * 4, swz_k256>(cdst, csrc, act_rs, qlim - t0, w, lane);
+          else dma_tile<NK * 4, swz_c<NK>>(cdst, csrc, act_rs, qlim - t0, w, lane);
           if (tid < HS * 64) {   // raw: nothing waits for these before the stage's end
             const int k2 = min(KB + (tid >> 6), hpg - 1);
             const float* dch = dcc + k2 * hstride + t0;
@@ -642,7 +650,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         return;
       }
       const bf16* Cb = Cs((Tp - S) & 1);
-      const int ctb = tr_first<NK * 4, swz_k256>(8 * lg, 0, lane);   // column tile 0
+      const int ctb = tr_first<NK * 4, swz_c<NK>>(8 * lg, 0, lane);   // column tile 0
       const int cfx = 16 * (swz_k256(8 * lg + ((lane & 15) >> 2)) >> 1);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
@@ -652,9 +660,14 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         *reinterpret_cast<v8bf*>(dcb_at(Tp, 2 * ks + 1)) = dl;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-          // column tile nt: chunk pair nt of the row, XOR-swizzled
-          const int a0 = ctb - (cfx & 0x70) + (((16 * nt) ^ cfx) & 0x70) + 32 * ks * N;
-          const v8bf a = tr_at(Cb, a0, a0 + 4 * N);
+          v8bf a;
+          if constexpr (NK == 4) {
+            // column tile nt: chunk pair nt of the row, XOR-swizzled
+            const int a0 = ctb - (cfx & 0x70) + (((16 * nt) ^ cfx) & 0x70) + 32 * ks * N;
+            a = tr_at(Cb, a0, a0 + 4 * N);
+          } else {
+            a = tr_frag<8, swz_k128>(Cb, 32 * ks + 8 * lg, 16 * nt, lane);
+          }
           dBT[nt] = mfma_bf16(a, dh, dBT[nt]);
           dBT[nt] = mfma_bf16(a, dl, dBT[nt]);
           if (nt & 1) __builtin_amdgcn_sched_barrier(0);
@@ -825,13 +838,13 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
       for (int t = 64 * (S + ntile) + tid; t < d.Lc; t += 256) rc[k * rstride + t] = 0.f;
     if constexpr (last) {
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) stage_out8<16>(stg1, sl, 16 * nt + 4 * lg, pack4_bf16(dBT[nt]));
+      for (int nt = 0; nt < NT; ++nt) stage_out8<RCB>(stg1, sl, 16 * nt + 4 * lg, pack4_bf16(dBT[nt]));
     }
     __syncthreads();
 #pragma unroll
     for (int h = 0; h < HS; ++h)
       if (KB + h < hpg) write_rows<8>(stg0 + h * 4096, duc + (KB + h) * 64 + s0 * u_rs, u_rs, qlim - s0, tid);
-    if constexpr (last) write_rows<16>(stg1, dBc + s0 * act_rs, act_rs, qlim - s0, tid);
+    if constexpr (last) write_rows<RCB>(stg1, dBc + s0 * act_rs, act_rs, qlim - s0, tid);
     // the next pass' first DMA goes into these buffers
     if constexpr (!last) __syncthreads();
   };
@@ -863,7 +876,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 // ---------------------------------------------------------------------------
 template <int NK>
 struct TgtSmem {
-  static constexpr int NH = 16 * NK;   // n of one half
+  static constexpr int NHALF = NK / 2;   // blocks per target strip (64 n each)
+  static constexpr int NH = 32 * NK / NHALF;   // n of one block
   // a stage: this half of H_in of one head (hi, lo: 2 x 64 x NH) or this
   // half of B_S (64 x NH) + dCB^T (hi, lo: 2 x 64 x 64)
   static constexpr int kStage = 2 * 64 * NH > 64 * NH + 2 * kPlaneT ? 2 * 64 * NH : 64 * NH + 2 * kPlaneT;
@@ -886,9 +900,10 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
 
   const int HPG = d.H / d.G;
   const int ttiles = d.Lc / 64;
+  constexpr int NHALF = SM::NHALF;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int half = bid & 1;
-  int rest = bid >> 1;
+  const int half = NHALF == 2 ? (bid & 1) : 0;
+  int rest = NHALF == 2 ? (bid >> 1) : bid;
   const int T = rest % ttiles;
   rest /= ttiles;
   const int g = rest % d.G;
@@ -914,7 +929,7 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
   const float* Hc = states + ((static_cast<long>(b) * d.nc + c) * d.H + h0) * (64L * N) + n0;
   const float* dcc = dc + bhc0 * d.Lc;
   bf16* dCc = dC + tok0 * act_rs + static_cast<long>(g) * N + n0;
-  float* xCc = xC_part + (bhc0 * 2 + half) * d.Lc;   // head k: + 2 k hstride
+  float* xCc = xC_part + (bhc0 * NHALF + half) * d.Lc;   // head k: + NHALF k hstride
 
   if (t0 >= lim) {
     for (int e = tid; e < 64 * (NH / 8); e += 256) {
@@ -923,7 +938,7 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
         *reinterpret_cast<uint4*>(dCc + static_cast<unsigned>((t0 + row) * act_rs + 8 * col8)) = uint4{0u, 0u, 0u, 0u};
     }
     for (int k = 0; k < HPG; ++k)
-      if (tid < 64) xCc[2 * k * hstride + t0 + tid] = 0.f;
+      if (tid < 64) xCc[NHALF * k * hstride + t0 + tid] = 0.f;
     return;
   }
 
@@ -1037,7 +1052,7 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
         dCT[nt] += X[nt];
       }
       s = group_sum(s);
-      if (lg == 0) xCc[2 * k * hstride + tau] = tau < lim ? s : 0.f;
+      if (lg == 0) xCc[NHALF * k * hstride + tau] = tau < lim ? s : 0.f;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         dyf[ks][0] = dyn[ks][0];
@@ -1076,14 +1091,17 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
 // The host pass leaves the stubs of ssd_bwd_src_kernel undefined when it only
 // meets them through a launch (its device lambdas are not substituted there);
 // explicit instantiation makes it emit them.
-#define SA_SRC_INST(HS, MID)                                                                     \
-  template __global__ void ssd_bwd_src_kernel<4, HS, MID>(                                       \
+#define SA_SRC_INST(NK, HS, MID)                                                                 \
+  template __global__ void ssd_bwd_src_kernel<NK, HS, MID>(                                      \
       const bf16*, const bf16*, const bf16*, const bf16*, const float*, const float*,            \
       const bf16*, const int64_t*, bf16*, bf16*, bf16*, float*, float*, float*, float*,          \
       SsdDims, int);
-SA_SRC_INST(1, false)
-SA_SRC_INST(2, false)
-SA_SRC_INST(2, true)
+SA_SRC_INST(4, 1, false)
+SA_SRC_INST(4, 2, false)
+SA_SRC_INST(4, 2, true)
+SA_SRC_INST(2, 1, false)
+SA_SRC_INST(2, 2, false)
+SA_SRC_INST(2, 2, true)
 #undef SA_SRC_INST
 
 template <typename K>
@@ -1096,12 +1114,12 @@ int raise_smem(K kernel, size_t bytes, const char* who) {
   return 0;
 }
 
-int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const bf16* dyp,
-                         const float* dt, const float* dc, const float* states, const bf16* dSp,
-                         const int64_t* length, void* du, void* dB, void* dC, bf16* dcbp,
-                         float* ddt_part, float* xB_part, float* xC_part, float* qpart,
-                         float* rpart, const SsdDims& d, bool dt_nonneg, hipStream_t s) {
-  constexpr int NK = 4;
+template <int NK>
+int launch_fused_nk(const void* u, const void* B, const void* C, const bf16* dyp,
+                    const float* dt, const float* dc, const float* states, const bf16* dSp,
+                    const int64_t* length, void* du, void* dB, void* dC, bf16* dcbp,
+                    float* ddt_part, float* xB_part, float* xC_part, float* qpart, float* rpart,
+                    const SsdDims& d, bool dt_nonneg, hipStream_t s) {
   const long blocks = static_cast<long>(d.b) * d.nc * d.G * (d.Lc / 64);
   {
     // one launch walks every head of the group (in passes of two heads
@@ -1121,16 +1139,28 @@ int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const bf16
     const size_t smem = TgtSmem<NK>::bytes;
     if (const int rc = raise_smem(ssd_bwd_tgt_kernel<NK>, smem, "ssd_bwd_tgt")) return rc;
     ProfScope prof_("ssd_bwd_tgt", s);
-    hipLaunchKernelGGL((ssd_bwd_tgt_kernel<NK>), dim3(2 * blocks), dim3(256), smem, s,
-                       static_cast<const bf16*>(B), static_cast<const bf16*>(C), dyp, dc, states,
+    hipLaunchKernelGGL((ssd_bwd_tgt_kernel<NK>), dim3(TgtSmem<NK>::NHALF * blocks), dim3(256), smem,
+                       s, static_cast<const bf16*>(B), static_cast<const bf16*>(C), dyp, dc, states,
                        dcbp, length, static_cast<bf16*>(dC), xC_part, d);
     SA_CHECK_LAUNCH("ssd_bwd_tgt");
   }
   return 0;
 }
 
+int launch_ssd_bwd_fused(const void* u, const void* B, const void* C, const bf16* dyp,
+                         const float* dt, const float* dc, const float* states, const bf16* dSp,
+                         const int64_t* length, void* du, void* dB, void* dC, bf16* dcbp,
+                         float* ddt_part, float* xB_part, float* xC_part, float* qpart,
+                         float* rpart, const SsdDims& d, bool dt_nonneg, hipStream_t s) {
+  if (d.N == 64)
+    return launch_fused_nk<2>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp,
+                              ddt_part, xB_part, xC_part, qpart, rpart, d, dt_nonneg, s);
+  return launch_fused_nk<4>(u, B, C, dyp, dt, dc, states, dSp, length, du, dB, dC, dcbp,
+                            ddt_part, xB_part, xC_part, qpart, rpart, d, dt_nonneg, s);
+}
+
 bool ssd_bwd_fused_shape_ok(const SsdDims& d) {
-  return d.P == 64 && d.N == 128 && d.Lc % 64 == 0 && d.H / d.G >= 1;
+  return d.P == 64 && (d.N == 64 || d.N == 128) && d.Lc % 64 == 0 && d.H / d.G >= 1;
 }
 
 bool ssd_bwd_fused_ok(const SsdDims& d, const void* u, const void* B, const void* C,

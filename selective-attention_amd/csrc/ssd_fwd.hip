@@ -929,8 +929,10 @@ int launch_chunk_outer(const void* a, const void* bsrc, const float* dt, const f
 int launch_dstate_planes(const float* dy, const void* C, const float* dt, const float* dc,
                          const int64_t* length, float* out, bf16* dyp, const SsdDims& d,
                          hipStream_t s) {
-  SA_CHECK_ARG(d.P == 64 && d.N == 128 && d.Lc % 64 == 0 && aligned16(dy) && aligned16(C),
-               "launch_dstate_planes: P 64, N 128, chunk %% 64 and aligned operands required");
+  SA_CHECK_ARG(d.P == 64 && (d.N == 64 || d.N == 128) && d.Lc % 64 == 0 && aligned16(dy) &&
+                   aligned16(C),
+               "launch_dstate_planes: P 64, N 64 or 128, chunk %% 64 and aligned operands required");
+  if (d.N == 64) return launch_chunk_outer_bf16_nk<2, 1>(dy, C, dt, dc, length, out, d, s, dyp);
   return launch_chunk_outer_bf16_nk<4, 1>(dy, C, dt, dc, length, out, d, s, dyp);
 }
 
