@@ -294,8 +294,10 @@ struct SrcSmem {
 };
 
 enum SrcMode { kSrcOnly = 0, kSrcFirst = 1, kSrcMiddle = 2, kSrcLast = 3 };
+// pass plans: one pass (at most HS heads), two passes, more than two
+enum SrcPlan { kPlanOne = 0, kPlanTwo = 1, kPlanMany = 2 };
 
-template <int NK, int HS, bool MID>
+template <int NK, int HS, int PLAN>
 __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     const bf16* __restrict__ u, const bf16* __restrict__ Bm, const bf16* __restrict__ Cm,
     const bf16* __restrict__ dyp, const float* __restrict__ dt, const float* __restrict__ dc,
@@ -849,15 +851,13 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     if constexpr (!last) __syncthreads();
   };
 
-  if constexpr (HS == 1) {
+  // one instantiation per pass plan, so that a launch carries only the pass
+  // bodies it runs (each body is 20-25 KB of code)
+  if constexpr (PLAN == kPlanOne) {
     run_pass(std::integral_constant<int, kSrcOnly>{}, 0);
-  } else if constexpr (!MID) {
-    if (npass == 1) {
-      run_pass(std::integral_constant<int, kSrcOnly>{}, 0);
-    } else {
-      run_pass(std::integral_constant<int, kSrcFirst>{}, 0);
-      run_pass(std::integral_constant<int, kSrcLast>{}, 1);
-    }
+  } else if constexpr (PLAN == kPlanTwo) {
+    run_pass(std::integral_constant<int, kSrcFirst>{}, 0);
+    run_pass(std::integral_constant<int, kSrcLast>{}, 1);
   } else {
     run_pass(std::integral_constant<int, kSrcFirst>{}, 0);
     for (int pass = 1; pass + 1 < npass; ++pass)
@@ -1091,17 +1091,19 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
 // The host pass leaves the stubs of ssd_bwd_src_kernel undefined when it only
 // meets them through a launch (its device lambdas are not substituted there);
 // explicit instantiation makes it emit them.
-#define SA_SRC_INST(NK, HS, MID)                                                                 \
-  template __global__ void ssd_bwd_src_kernel<NK, HS, MID>(                                      \
+#define SA_SRC_INST(NK, HS, PLAN)                                                                \
+  template __global__ void ssd_bwd_src_kernel<NK, HS, PLAN>(                                     \
       const bf16*, const bf16*, const bf16*, const bf16*, const float*, const float*,            \
       const bf16*, const int64_t*, bf16*, bf16*, bf16*, float*, float*, float*, float*,          \
       SsdDims, int);
-SA_SRC_INST(4, 1, false)
-SA_SRC_INST(4, 2, false)
-SA_SRC_INST(4, 2, true)
-SA_SRC_INST(2, 1, false)
-SA_SRC_INST(2, 2, false)
-SA_SRC_INST(2, 2, true)
+SA_SRC_INST(4, 1, kPlanOne)
+SA_SRC_INST(4, 2, kPlanOne)
+SA_SRC_INST(4, 2, kPlanTwo)
+SA_SRC_INST(4, 2, kPlanMany)
+SA_SRC_INST(2, 1, kPlanOne)
+SA_SRC_INST(2, 2, kPlanOne)
+SA_SRC_INST(2, 2, kPlanTwo)
+SA_SRC_INST(2, 2, kPlanMany)
 #undef SA_SRC_INST
 
 template <typename K>
@@ -1126,8 +1128,10 @@ int launch_fused_nk(const void* u, const void* B, const void* C, const bf16* dyp
     // inside each block)
     ProfScope prof_("ssd_bwd_src", s);
     const int hpg = d.H / d.G;
-    auto kernel = hpg == 1 ? ssd_bwd_src_kernel<NK, 1, false>
-                           : hpg <= 4 ? ssd_bwd_src_kernel<NK, 2, false> : ssd_bwd_src_kernel<NK, 2, true>;
+    auto kernel = hpg == 1   ? ssd_bwd_src_kernel<NK, 1, kPlanOne>
+                  : hpg <= 2 ? ssd_bwd_src_kernel<NK, 2, kPlanOne>
+                  : hpg <= 4 ? ssd_bwd_src_kernel<NK, 2, kPlanTwo>
+                             : ssd_bwd_src_kernel<NK, 2, kPlanMany>;
     hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), 0, s,
                        static_cast<const bf16*>(u), static_cast<const bf16*>(B),
                        static_cast<const bf16*>(C), dyp, dt, dc, dSp, length,
