@@ -87,6 +87,14 @@ FUSED_CASES = [
     ("hpg5_odd", dict(b=2, L=192, H=10, P=64, N=128, G=2, lens=[192, 100]), 64),
     # config 4's SSM shape class: 32 heads in one group, chunk 256
     ("hpg32_c256", dict(b=1, L=512, H=32, P=64, N=128, G=1, lens=[512]), 256),
+    # the reference default's class: state_dim 64, 16 heads in one group
+    ("n64_hpg16_c256", dict(b=2, L=300, H=16, P=64, N=64, G=1, lens=[300, 201]), 256),
+    # state_dim 64, five heads per group (first, middle and a one-head last pass)
+    ("n64_hpg5", dict(b=1, L=256, H=10, P=64, N=64, G=2, lens=[250]), 128),
+    # chunk 512: up to eight target strips per source strip
+    ("hpg4_c512", dict(b=1, L=700, H=8, P=64, N=128, G=2, lens=[650]), 512),
+    # chunk 192 (three strips), six heads per group
+    ("hpg6_c192", dict(b=2, L=400, H=12, P=64, N=128, G=2, lens=[400, 222]), 192),
     # fused path: a zero-length row next to full and partial ones (every strip
     # of that row takes the kernels' early exits), two heads per group
     ("hpg2_zero_len", dict(b=3, L=192, H=4, P=64, N=128, G=2, lens=[192, 0, 100]), 64),
@@ -185,10 +193,14 @@ def test_ssd_bwd_fused_shape_misaligned_inputs():
 
 
 @pytest.mark.gpu
-def test_ssd_bwd_fused_deterministic():
-    x = make_inputs(b=2, L=256, H=8, P=64, N=128, G=2, dtype=torch.bfloat16, lens=[256, 190])
+@pytest.mark.parametrize("H,G,N", [(8, 2, 128), (12, 1, 128), (6, 1, 64)])
+def test_ssd_bwd_fused_deterministic(H, G, N):
+    """Two, more than two, and state_dim 64 passes: bit-equal reruns (every
+    cross-block sum is a fixed-order partial sum, the running dCB sum is
+    read back by the lane that wrote it)."""
+    x = make_inputs(b=2, L=256, H=H, P=64, N=N, G=G, dtype=torch.bfloat16, lens=[256, 190])
     g = torch.Generator().manual_seed(3)
-    dy = torch.randn(2, 256, 8, 64, generator=g)
+    dy = torch.randn(2, 256, H, 64, generator=g)
     a = gpu_grads(x, dy, None, 128)
     b = gpu_grads(x, dy, None, 128)
     for k in a:
