@@ -117,13 +117,14 @@ def test_ssd_bwd_fused_parity(name, shape, chunk):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("N", [128, 64])
 @pytest.mark.parametrize("softplus,limit", [(False, (-0.02, 0.05)), (True, (-1.0, float("inf")))])
-def test_ssd_bwd_fused_signed_limits(softplus, limit):
+def test_ssd_bwd_fused_signed_limits(softplus, limit, N):
     """Fused bf16 backward on its exact-decay branch (negative lower dt limit;
-    with softplus off some dt are negative)."""
+    with softplus off some dt are negative), state_dim 128 and 64."""
     from tests.test_ssd_fwd import signed_dt_inputs
-    print(f"ssd bwd fused signed softplus={softplus} limit={limit}", flush=True)
-    x = signed_dt_inputs(softplus, b=2, L=256, H=4, P=64, N=128, G=2, lens=[256, 170])
+    print(f"ssd bwd fused signed softplus={softplus} limit={limit} N={N}", flush=True)
+    x = signed_dt_inputs(softplus, b=2, L=256, H=4, P=64, N=N, G=2, lens=[256, 170])
     check(x, 128, torch.bfloat16, softplus, limit)
 
 
@@ -131,6 +132,7 @@ def test_ssd_bwd_fused_signed_limits(softplus, limit):
 @pytest.mark.parametrize("dtype,shape,chunk", [
     (torch.float32, dict(b=2, L=150, H=4, P=24, N=40, G=2, lens=[150, 97]), 32),
     (torch.bfloat16, dict(b=2, L=320, H=8, P=64, N=128, G=2, lens=[320, 130]), 128),
+    (torch.bfloat16, dict(b=2, L=320, H=12, P=64, N=64, G=2, lens=[320, 130]), 128),
 ])
 def test_ssd_bwd_softplus_threshold(dtype, shape, chunk):
     """delta_raw + bias in (20.5, 22) on 3 % of the tokens: d(delta_raw) is
