@@ -44,24 +44,36 @@ namespace sa {
 
 // ---------------------------------------------------------------------------
 // LDS layouts.  Chunk c (16 bytes) of row r is stored at chunk c ^ f(r).
+// The gfx950 LDS does not map banks by the low address bits alone (a
+// 16-byte read of 16 lanes with distinct chunks of a 256-byte span can
+// still conflict, depending on the rows and on the chunks the other lane
+// groups read), so the permutations below were chosen by measurement: for
+// each tile, every XOR permutation of row bits into chunk bits was run on
+// the kernel's own read sets, and these give SQ_LDS_BANK_CONFLICT = 0 for
+// all of them.
 // ---------------------------------------------------------------------------
-// 128-byte rows (64 bf16) read through key_of_row row sets and transposed
+// 128-byte rows (64 bf16) of the target kernel's tiles, read transposed
 __host__ __device__ __forceinline__ int swz_k128(int r) {
   return ((r >> 4) & 1) | (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
 }
-// 128-byte rows read as 16 consecutive rows and transposed
-__host__ __device__ __forceinline__ int swz_s128(int r) {
-  return (((r >> 1) & 1) << 1) | ((r >> 2) & 1) | (((r >> 3) & 1) << 2);
+// 128-byte rows of the source kernel's dy and dS tiles (and C at state_dim
+// 64): read as 16-byte fragments of the key_of_row row sets (dy, C) or of
+// 16 consecutive rows (dS), and transposed (ds_read_b64_tr_b16); rows r and
+// r + 4 share the permutation
+__host__ __device__ __forceinline__ int swz_r128(int r) {
+  return (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
 }
-// 256-byte rows (128 bf16) read through key_of_row row sets and transposed
-__host__ __device__ __forceinline__ int swz_k256(int r) {
-  return ((r & 3) << 1) | (((r >> 3) & 1) << 3) | ((r >> 4) & 1);
+// 256-byte rows (128 bf16) of the source kernel's C tile, read as 16-byte
+// fragments of the key_of_row row sets and transposed; rows r and r + 4
+// share the permutation
+__host__ __device__ __forceinline__ int swz_r256(int r) {
+  return ((r & 1) << 1) | (((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 3);
 }
 
-// C (and B) tiles of the source kernel: 256-byte rows at state_dim 128,
-// 128-byte rows at state_dim 64, read through key_of_row row sets and transposed
+// C tiles of the source kernel: 256-byte rows at state_dim 128, 128-byte
+// rows at state_dim 64
 template <int NK>
-__host__ __device__ __forceinline__ int swz_c(int r) { return NK == 4 ? swz_k256(r) : swz_k128(r); }
+__host__ __device__ __forceinline__ int swz_c(int r) { return NK == 4 ? swz_r256(r) : swz_r128(r); }
 
 // element offset of (row, col) in a swizzled tile with RC 16-byte chunks per row
 template <int RC, int (*F)(int)>
@@ -437,8 +449,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
       const int ln = opaque(lane);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        gs[i] = dma_off<8, swz_s128>(i, w, ln, N);
-        gy[i] = dma_off<8, swz_k128>(i, w, ln, 64);
+        gs[i] = dma_off<8, swz_r128>(i, w, ln, N);
+        gy[i] = dma_off<8, swz_r128>(i, w, ln, 64);
       }
 #pragma unroll
       for (int i = 0; i < NK; ++i) gc[i] = dma_off<NK * 4, swz_c<NK>>(i, w, ln, act_rs);
@@ -449,9 +461,9 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     const int rl = 8 * (lip >> 2) + (lip & 3);   // key_of_row(kt, li) = rl + kro(kt)
     int o_w[2], o_tr[4], o_c[NK];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) o_w[ks] = toff<8, swz_k128>(rl, 32 * ks + 8 * lgp);
+    for (int ks = 0; ks < 2; ++ks) o_w[ks] = toff<8, swz_r128>(rl, 32 * ks + 8 * lgp);
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt) o_tr[pt] = tr_first<8, swz_k128>(8 * lgp, 16 * pt, lnp);
+    for (int pt = 0; pt < 4; ++pt) o_tr[pt] = tr_first<8, swz_r128>(8 * lgp, 16 * pt, lnp);
 #pragma unroll
     for (int ks = 0; ks < NK; ++ks) o_c[ks] = toff<NK * 4, swz_c<NK>>(rl, 32 * ks + 8 * lgp);
     // B of this lane's source row (all N): the same in every stage of the pass
@@ -555,11 +567,11 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     {
       int o_sd[2], o_st[4][2];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) o_sd[ks] = toff<8, swz_s128>(li, 32 * ks + 8 * lg);
+      for (int ks = 0; ks < 2; ++ks) o_sd[ks] = toff<8, swz_r128>(li, 32 * ks + 8 * lg);
 #pragma unroll
       for (int nt4 = 0; nt4 < 4; ++nt4) {
-        o_st[nt4][0] = tr_first<8, swz_s128>(8 * lg, 16 * nt4, lane);
-        o_st[nt4][1] = tr_first<8, swz_s128>(8 * lg + 4, 16 * nt4, lane);
+        o_st[nt4][0] = tr_first<8, swz_r128>(8 * lg, 16 * nt4, lane);
+        o_st[nt4][1] = tr_first<8, swz_r128>(8 * lg + 4, 16 * nt4, lane);
       }
       // dB^T rows of the n half in stage buffer Y from a head's dS, its u row
       // uf at this lane's column and its state weight wk
@@ -653,7 +665,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
       }
       const bf16* Cb = Cs((Tp - S) & 1);
       const int ctb = tr_first<NK * 4, swz_c<NK>>(8 * lg, 0, lane);   // column tile 0
-      const int cfx = 16 * (swz_k256(8 * lg + ((lane & 15) >> 2)) >> 1);
+      const int cfx = 16 * (swz_r256(8 * lg + ((lane & 15) >> 2)) >> 1);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         v8bf dh, dl;
@@ -668,7 +680,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
             const int a0 = ctb - (cfx & 0x70) + (((16 * nt) ^ cfx) & 0x70) + 32 * ks * N;
             a = tr_at(Cb, a0, a0 + 4 * N);
           } else {
-            a = tr_frag<8, swz_k128>(Cb, 32 * ks + 8 * lg, 16 * nt, lane);
+            a = tr_frag<8, swz_r128>(Cb, 32 * ks + 8 * lg, 16 * nt, lane);
           }
           dBT[nt] = mfma_bf16(a, dh, dBT[nt]);
           dBT[nt] = mfma_bf16(a, dl, dBT[nt]);
