@@ -43,31 +43,13 @@
 namespace sa {
 
 // ---------------------------------------------------------------------------
-// LDS layouts.  Chunk c (16 bytes) of row r is stored at chunk c ^ f(r).
-// The gfx950 LDS does not map banks by the low address bits alone (a
-// 16-byte read of 16 lanes with distinct chunks of a 256-byte span can
-// still conflict, depending on the rows and on the chunks the other lane
-// groups read), so the permutations below were chosen by measurement: for
-// each tile, every XOR permutation of row bits into chunk bits was run on
-// the kernel's own read sets, and these give SQ_LDS_BANK_CONFLICT = 0 for
-// all of them.
+// LDS layouts.  Chunk c (16 bytes) of row r is stored at chunk c ^ f(r):
+// swz_r128 / swz_r256 (ssd_common.h) for the source kernel's tiles,
+// swz_k128 for the target kernel's.
 // ---------------------------------------------------------------------------
 // 128-byte rows (64 bf16) of the target kernel's tiles, read transposed
 __host__ __device__ __forceinline__ int swz_k128(int r) {
   return ((r >> 4) & 1) | (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
-}
-// 128-byte rows of the source kernel's dy and dS tiles (and C at state_dim
-// 64): read as 16-byte fragments of the key_of_row row sets (dy, C) or of
-// 16 consecutive rows (dS), and transposed (ds_read_b64_tr_b16); rows r and
-// r + 4 share the permutation
-__host__ __device__ __forceinline__ int swz_r128(int r) {
-  return (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
-}
-// 256-byte rows (128 bf16) of the source kernel's C tile, read as 16-byte
-// fragments of the key_of_row row sets and transposed; rows r and r + 4
-// share the permutation
-__host__ __device__ __forceinline__ int swz_r256(int r) {
-  return ((r & 1) << 1) | (((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 3);
 }
 
 // C tiles of the source kernel: 256-byte rows at state_dim 128, 128-byte

@@ -180,11 +180,14 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
     const void* __restrict__ a_src, const bf16* __restrict__ x_src, const float* __restrict__ dt,
     const float* __restrict__ dc, const int64_t* __restrict__ length, float* __restrict__ out,
     bf16* __restrict__ dyp, SsdDims d) {
-  constexpr int N = 32 * NK, LDX = N + 8, LDA = 64 + 8;
+  constexpr int N = 32 * NK;
+  using TA = LdsTile<64>;                  // the scaled operand's planes
+  using TX = LdsTile<N>;                   // the B or C tile
+  constexpr int PLA = 64 * TA::kLd;        // elements per plane
   constexpr int NPL = 2;                   // hi + lo planes of the scaled operand
   constexpr int NTW = N / 64;              // 16-wide n tiles per wave
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* sm = reinterpret_cast<bf16*>(smem_raw);   // As [NPL][64][LDA], Xs [64][LDX]
+  bf16* sm = reinterpret_cast<bf16*>(smem_raw);   // As [NPL][64 rows], Xs [64 rows]
 
   const int ptiles = d.P / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -249,7 +252,7 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
     };
     auto commit_tile = [&]() __attribute__((always_inline)) {
       bf16* As = sm;
-      bf16* Xs = As + NPL * 64 * LDA;
+      bf16* Xs = As + NPL * PLA;
       if constexpr (MODE == 0) {
         // w * u is fp32 (dt up to z > 20 makes it large): hi + lo planes keep
         // the chunk states near fp32, which the backward's dC, dA and
@@ -265,9 +268,9 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
             r[j] = pack_bf16x2(v0, v1);
             rl[j] = pack_bf16x2(v0 - bf16lo_to_f32(r[j]), v1 - bf16hi_to_f32(r[j]));
           }
-          *reinterpret_cast<uint4*>(As + row * LDA + 8 * (e & 7)) = uint4{r[0], r[1], r[2], r[3]};
-          *reinterpret_cast<uint4*>(As + 64 * LDA + row * LDA + 8 * (e & 7)) =
-              uint4{rl[0], rl[1], rl[2], rl[3]};
+          const int ao = TA::off(row, 8 * (e & 7));
+          *reinterpret_cast<uint4*>(As + ao) = uint4{r[0], r[1], r[2], r[3]};
+          *reinterpret_cast<uint4*>(As + PLA + ao) = uint4{rl[0], rl[1], rl[2], rl[3]};
         }
       } else {
         const int row = tid >> 2, c0 = 16 * (tid & 3);
@@ -308,14 +311,13 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
             lo[2 * i + j] = pack_bf16x2(v[2 * j] - bf16lo_to_f32(hh), v[2 * j + 1] - bf16hi_to_f32(hh));
           }
         }
-        uint4* ph = reinterpret_cast<uint4*>(As + row * LDA + c0);
-        uint4* pl = reinterpret_cast<uint4*>(As + 64 * LDA + row * LDA + c0);
-        ph[0] = uint4{hi[0], hi[1], hi[2], hi[3]};
-        ph[1] = uint4{hi[4], hi[5], hi[6], hi[7]};
-        pl[0] = uint4{lo[0], lo[1], lo[2], lo[3]};
-        pl[1] = uint4{lo[4], lo[5], lo[6], lo[7]};
+        const int ao0 = TA::off(row, c0), ao1 = TA::off(row, c0 + 8);
+        *reinterpret_cast<uint4*>(As + ao0) = uint4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<uint4*>(As + ao1) = uint4{hi[4], hi[5], hi[6], hi[7]};
+        *reinterpret_cast<uint4*>(As + PLA + ao0) = uint4{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<uint4*>(As + PLA + ao1) = uint4{lo[4], lo[5], lo[6], lo[7]};
       }
-      px.commit(Xs, LDX, tid);
+      commit_lds(px, Xs, tid);
     };
 
     const int ntt = (klim + 63) / 64;
@@ -326,7 +328,7 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
       const bool has_next = tt + 1 < ntt;
       if (has_next) load_tile(tt + 1);
       const bf16* As = sm;
-      const bf16* Xs = As + NPL * 64 * LDA;
+      const bf16* Xs = As + NPL * PLA;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         v8bf bop[4][NPL];
@@ -334,10 +336,10 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
         for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
           for (int pl = 0; pl < NPL; ++pl)
-            bop[pt][pl] = lds_tr8(As + pl * 64 * LDA + (32 * ks + 8 * lg) * LDA + 16 * pt, LDA, lane);
+            bop[pt][pl] = tile_tr8<64>(As + pl * PLA, 32 * ks + 8 * lg, 16 * pt, lane);
 #pragma unroll
         for (int i = 0; i < NTW; ++i) {
-          const v8bf a = lds_tr8(Xs + (32 * ks + 8 * lg) * LDX + 16 * (NTW * w + i), LDX, lane);
+          const v8bf a = tile_tr8<N>(Xs, 32 * ks + 8 * lg, 16 * (NTW * w + i), lane);
 #pragma unroll
           for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
@@ -535,9 +537,12 @@ struct GateOut {
 };
 
 // bf16 elements of the chunk-scan region that holds the HC heads' U tiles
-// ([HC][64][72]) and, after the sigma loop, one H_in tile ([64][N + 8])
-constexpr int chunk_scan_ureg(int NK, int HC) {
-  return HC * 64 * 72 > 64 * (32 * NK + 8) ? HC * 64 * 72 : 64 * (32 * NK + 8);
+// (HC LdsTile<64> tiles) and, after the sigma loop, one H_in tile
+// (LdsTile<N>, 64 rows)
+template <int NK, int HC>
+constexpr int chunk_scan_ureg() {
+  constexpr int u = HC * 64 * LdsTile<64>::kLd, hn = 64 * LdsTile<32 * NK>::kLd;
+  return u > hn ? u : hn;
 }
 
 // ---------------------------------------------------------------------------
@@ -561,12 +566,14 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
     const float* __restrict__ dt, const float* __restrict__ dc, const float* __restrict__ states,
     float* __restrict__ y, GateOut go, SsdDims d, int mono) {
   constexpr int N = 32 * NK;
-  constexpr int LDN = N + 8, LDU = 64 + 8;
+  using TB = LdsTile<N>;    // B sigma tile and H_in tile: 64 rows of N
+  using TU = LdsTile<64>;   // U tiles: 64 sigma rows of 64 p
+  constexpr int PLU = 64 * TU::kLd;
   constexpr int HQ = N / 16;   // float4 of an H tile per thread (64 x N fp32 / 256 threads)
-  constexpr int UREG = chunk_scan_ureg(NK, HC);   // bf16 of the U tiles / H_in tile region
+  constexpr int UREG = chunk_scan_ureg<NK, HC>();   // bf16 of the U tiles / H_in tile region
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  bf16* Bs = reinterpret_cast<bf16*>(smem_raw);  // [64][LDN]     B rows of the sigma tile
-  bf16* Us = Bs + 64 * LDN;                      // [HC][64][LDU] U rows per head; later H_in tile
+  bf16* Bs = reinterpret_cast<bf16*>(smem_raw);  // B rows of the sigma tile (TB)
+  bf16* Us = Bs + 64 * TB::kLd;                  // [HC] U rows per head (TU); later the H_in tile (TB)
   float* tab = reinterpret_cast<float*>(Us + UREG);   // [HC][64] e^{dc_t0 - dc_sig} dt_sig
   float* dcd = tab + HC * 64;                                 // [HC][64] dc_sig (log2)
   float* dtd = dcd + HC * 64;                                 // [HC][64] dt_sig (0 past qlim)
@@ -659,14 +666,14 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
     for (int i = 0; i < NK; ++i) {
       const int e = tid + 256 * i;
       const int row = e / (4 * NK), c8 = e % (4 * NK);
-      *reinterpret_cast<uint4*>(Bs + row * LDN + 8 * c8) = pb[i];
+      *reinterpret_cast<uint4*>(Bs + TB::off(row, 8 * c8)) = pb[i];
     }
 #pragma unroll
     for (int k = 0; k < HC; ++k)
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int e = tid + 256 * i;
-        *reinterpret_cast<uint4*>(Us + k * 64 * LDU + (e >> 3) * LDU + 8 * (e & 7)) = pu[k][i];
+        *reinterpret_cast<uint4*>(Us + k * PLU + TU::off(e >> 3, 8 * (e & 7))) = pu[k][i];
       }
     if (tid < HC * 64) {
       dcd[tid] = pdc;
@@ -676,7 +683,7 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
   };
 
   // H_in staging for the state contribution (one head per stage, bf16 in the U tiles' space)
-  bf16* Hs = Us;   // [64][LDN] bf16, in the U tiles' region
+  bf16* Hs = Us;   // 64 rows of N bf16 (TB), in the U tiles' region
   float4 ph[HQ];
   auto load_h = [&](int k) {
     const float* Hb = states + (((static_cast<long>(b) * d.nc + c) * d.H + h0 + k) * d.P + p0) * N;
@@ -693,7 +700,7 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
     for (int i = 0; i < HQ; ++i) {
       const int e = tid + 256 * i;
       const int row = e / (N / 4), c4 = e % (N / 4);
-      *reinterpret_cast<uint2*>(Hs + row * LDN + 4 * c4) =
+      *reinterpret_cast<uint2*>(Hs + TB::off(row, 4 * c4)) =
           uint2{pack_bf16x2(ph[i].x, ph[i].y), pack_bf16x2(ph[i].z, ph[i].w)};
     }
   };
@@ -715,13 +722,13 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
     // MFMA runs, and consecutive MFMAs go to different accumulators
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) cbt[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-    v8bf bnx = load_v8bf(Bs + key_of_row(0, cl) * LDN + 8 * lg);
+    v8bf bnx = load_v8bf(Bs + TB::off(key_of_row(0, cl), 8 * lg));
 #pragma unroll
     for (int i = 0; i < 4 * NK; ++i) {
       const int ks = i / 4, kt = i % 4;
       const v8bf bf = bnx;
       if (i + 1 < 4 * NK)
-        bnx = load_v8bf(Bs + key_of_row((i + 1) % 4, cl) * LDN + 8 * lg + 32 * ((i + 1) / 4));
+        bnx = load_v8bf(Bs + TB::off(key_of_row((i + 1) % 4, cl), 8 * lg + 32 * ((i + 1) / 4)));
       __builtin_amdgcn_sched_barrier(0);
       cbt[kt] = mfma_bf16(bf, Cw[ks], cbt[kt]);
     }
@@ -746,13 +753,13 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
           }
         }
       }
-      const bf16* ut = Us + k * 64 * LDU;
+      const bf16* ut = Us + k * PLU;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const v8bf pbk = pack_p(sk[2 * ks], sk[2 * ks + 1]);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-          acc[k][t] = mfma_bf16(lds_tr8(ut + (32 * ks + 8 * lg) * LDU + 16 * t, LDU, lane), pbk, acc[k][t]);
+          acc[k][t] = mfma_bf16(tile_tr8<64>(ut, 32 * ks + 8 * lg, 16 * t, lane), pbk, acc[k][t]);
       }
     }
   };
@@ -784,13 +791,13 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
       v4f st[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) st[t] = v4f{0.f, 0.f, 0.f, 0.f};
-      v8bf hnx = load_v8bf(Hs + cl * LDN + 8 * lg);
+      v8bf hnx = load_v8bf(Hs + TB::off(cl, 8 * lg));
 #pragma unroll
       for (int i = 0; i < 4 * NK; ++i) {
         const int ks = i / 4, t = i % 4;
         const v8bf hf = hnx;
         if (i + 1 < 4 * NK)
-          hnx = load_v8bf(Hs + (16 * ((i + 1) % 4) + cl) * LDN + 8 * lg + 32 * ((i + 1) / 4));
+          hnx = load_v8bf(Hs + TB::off(16 * ((i + 1) % 4) + cl, 8 * lg + 32 * ((i + 1) / 4)));
         __builtin_amdgcn_sched_barrier(0);
         st[t] = mfma_bf16(hf, Cw[ks], st[t]);
       }
@@ -809,6 +816,8 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
     // rows out, 16 bytes per lane (stored from the fragments, one
     // instruction wrote 64 bytes of each of 16 rows)
     float* ys = reinterpret_cast<float*>(smem_raw);
+    static_assert(2 * 64 * 64 * sizeof(float) <= sizeof(bf16) * (64 * TB::kLd + UREG),
+                  "chunk_scan_fwd: the y staging fits in the tile region");
     const int rl = 16 * w + cl;
 #pragma unroll
     for (int r2 = 0; r2 < (HC + 1) / 2; ++r2) {
@@ -890,7 +899,7 @@ int launch_chunk_outer_bf16_nk(const void* a, const void* x, const float* dt, co
                                const int64_t* length, float* out, const SsdDims& d, hipStream_t s,
                                bf16* dyp = nullptr) {
   const long blocks = static_cast<long>(d.P / 64) * d.H * d.nc * d.b;
-  const size_t smem = sizeof(bf16) * (2 * 64 * 72 + 64 * (32 * NK + 8));
+  const size_t smem = sizeof(bf16) * 64 * (2 * LdsTile<64>::kLd + LdsTile<32 * NK>::kLd);
   if (smem > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(chunk_outer_bf16_kernel<NK, MODE>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
@@ -981,7 +990,7 @@ int launch_chunk_scan_bf16_nk(const void* u, const void* B, const void* C, const
   const int nhc = (hpg + HC - 1) / HC;
   const long blocks = static_cast<long>((d.Lc + 63) / 64) * ((d.P + 63) / 64) * nhc * d.G *
                       d.nc * d.b;
-  const size_t smem = sizeof(bf16) * (64 * (32 * NK + 8) + chunk_scan_ureg(NK, HC)) +
+  const size_t smem = sizeof(bf16) * (64 * LdsTile<32 * NK>::kLd + chunk_scan_ureg<NK, HC>()) +
                       sizeof(float) * HC * 192;
   auto run = [&](auto kernel, const char* name) -> int {
     if (smem > 64 * 1024) {
