@@ -98,48 +98,12 @@ __device__ __forceinline__ int v_swz(int r) {
   else return (((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 1) | ((r >> 4) & 1);
 }
 
-// LDS DMA written as instructions the compiler does not interpret: it then
-// inserts no waits of its own for them (it cannot tell which LDS bytes a DMA
-// writes, and would otherwise hold every LDS read until all DMA in flight had
-// landed); the kernel waits with explicit vmcnt and barriers.  Each lane's
-// data goes to LDS byte address lds + 16 lane (4 lane for the dword form),
-// from base + off (off in bytes).  m0 carries the LDS address; nothing else
-// in the kernels that use these relies on m0.
-//
-// lds_addr: the LDS byte address of a generic pointer into LDS, as a
-// wave-uniform value (the DMA helpers take it through readfirstlane, which
-// costs nothing where it already sits in a scalar register).  A generic LDS address is the shared aperture in the
-// high half and the LDS offset in the low half, so the low 32 bits are the
-// address (no address-space cast, whose null check costs a 64-bit compare
-// and select per use).  Kernels take it once per stage, outside their loops.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
-}
-__device__ __forceinline__ void dma_lds16(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
-               "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
-}
-__device__ __forceinline__ void dma_lds4(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base),
-               "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
 // p[i] for a wave-uniform i through the constant address space: a scalar
 // load, counted by lgkmcnt rather than the vector memory counter
 __device__ __forceinline__ int32_t load_uniform(const int32_t* p, int i) {
   typedef const __attribute__((address_space(4))) int32_t cint;
   return ((cint*)p)[__builtin_amdgcn_readfirstlane(i)];
 }
-
-// s_waitcnt immediate: vmcnt(N), expcnt and lgkmcnt not waited for
-template <int N>
-constexpr int vm_wait() {
-  return (N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14);
-}
-constexpr int kLgkmWait0 = 0xF | (7 << 4) | (3 << 14);   // lgkmcnt(0) only
 
 // Online softmax with a lazy reference.  s[kt][i] holds log2-domain scores of
 // this lane's keys for query column lane & 15 (-inf where masked).  The

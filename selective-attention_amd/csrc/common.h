@@ -257,6 +257,42 @@ __device__ __forceinline__ v8bf lds_tr8(const bf16* x, int ld, int lane) {
   return __builtin_bit_cast(v8bf, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// LDS DMA written as instructions the compiler does not interpret: it then
+// inserts no waits of its own for them (it cannot tell which LDS bytes a DMA
+// writes, and would otherwise hold every LDS read until all DMA in flight had
+// landed); the kernel waits with explicit vmcnt and barriers.  Each lane's
+// data goes to LDS byte address lds + 16 lane (4 lane for the dword form),
+// from base + off (off in bytes).  m0 carries the LDS address; nothing else
+// in the kernels that use these relies on m0.
+//
+// lds_addr: the LDS byte address of a generic pointer into LDS, as a
+// wave-uniform value (the DMA helpers take it through readfirstlane, which
+// costs nothing where it already sits in a scalar register).  A generic LDS address is the shared aperture in the
+// high half and the LDS offset in the low half, so the low 32 bits are the
+// address (no address-space cast, whose null check costs a 64-bit compare
+// and select per use).  Kernels take it once per stage, outside their loops.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
+}
+__device__ __forceinline__ void dma_lds16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
+               "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_lds4(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base),
+               "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt immediate: vmcnt(N), expcnt and lgkmcnt not waited for
+template <int N>
+constexpr int vm_wait() {
+  return (N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14);
+}
+constexpr int kLgkmWait0 = 0xF | (7 << 4) | (3 << 14);   // lgkmcnt(0) only
+
 // key (within a 64-key tile) held by MFMA row c of score tile kt
 __device__ __forceinline__ int key_of_row(int kt, int c) {
   return 32 * (kt >> 1) + 8 * (c >> 2) + 4 * (kt & 1) + (c & 3);

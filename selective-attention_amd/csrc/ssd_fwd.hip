@@ -361,6 +361,188 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// chunk states and state passing in one kernel (forward, bf16, P and N
+// multiples of 64):
+//   S_c[p][n] = sum_t u[t,p] w_t B[t,n],  w_t = e^{min(dc_last - dc_t, 0)} dt_t
+//   states[c] = H_c,  H_{c+1} = e^{dc_last(c)} H_c + S_c,  H_0 = h_init or 0,
+//   h_last = H_nc
+// One block per (b, head, 64-wide p tile, 64-wide n block), 4 waves: wave w
+// accumulates S_c^T[n][p] for the block's n columns 16 w .. 16 w + 15 and its
+// 64 p, and holds H_c in the same fragment layout (lane: n = n0 + 16 w +
+// 4 lg + r, p = p0 + 16 pt + li).  The block walks every 64-token t tile of
+// every chunk in order, so the chunk states never leave the chip.
+// A tile's raw u and B rows and its dc, dt go from HBM straight into one of
+// three LDS stages (global_load_lds, issued three tiles ahead and waited for
+// with explicit counts); each step then scales u by w_t and splits it into
+// hi + lo planes (w u is fp32) for the MFMAs, which read B from the stage.
+// The products and their order are chunk_outer_bf16_kernel<., 0>'s and the
+// update is state_passing_fwd_kernel's.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
+    const bf16* __restrict__ u, const bf16* __restrict__ Bm, const float* __restrict__ dt,
+    const float* __restrict__ dc, const float* __restrict__ h_init, float* __restrict__ states,
+    float* __restrict__ h_last, SsdDims d) {
+  using TL = LdsTile<64>;
+  constexpr int PL = 64 * TL::kLd;            // bf16 per 64 x 64 tile
+  constexpr int NS = 3;                        // DMA stages
+  constexpr int kStage = 2 * PL + 4 * 128;     // bf16: u tile, B tile (+PL), 4 x 64 fp32 row values (+2 PL)
+  __shared__ __align__(16) bf16 As[2 * PL];   // hi, lo planes of (w u)[t][p]
+  __shared__ __align__(16) bf16 stg[NS * kStage];
+
+  const int ptiles = d.P / 64, nblk = d.N / 64;
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  int rest = bid;
+  const int nb = rest % nblk;
+  rest /= nblk;
+  const int pti = rest % ptiles;
+  rest /= ptiles;
+  const int h = rest % d.H;
+  const int b = rest / d.H;
+  const int p0 = 64 * pti, n0 = 64 * nb;
+  const int g = h / (d.H / d.G);
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int a_rs = d.H * d.P, x_rs = d.G * d.N;
+  const long PN = static_cast<long>(d.P) * d.N;
+  const long bh = static_cast<long>(b) * d.H + h;
+  // this lane's element offset inside a [P][N] state: + 16 pt N
+  const int eo = (p0 + li) * d.N + n0 + 16 * w + 4 * lg;
+
+  v4f H[4], S[4];
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) {
+    S[pt] = v4f{0.f, 0.f, 0.f, 0.f};
+    H[pt] = v4f{0.f, 0.f, 0.f, 0.f};
+    if (h_init) {
+      const float4 v = *reinterpret_cast<const float4*>(h_init + bh * PN + eo + 16 * pt * d.N);
+      H[pt] = v4f{v.x, v.y, v.z, v.w};
+    }
+  }
+
+  // the initial state has arrived before the loop, whose waits count DMA only
+  __builtin_amdgcn_s_waitcnt(vm_wait<0>());
+
+  // t tiles: every chunk but the last has tpc, the last ntt_last
+  const int tpc = (d.Lc + 63) / 64;
+  const int qlast = d.L - (d.nc - 1) * d.Lc;
+  const int ntiles = (d.nc - 1) * tpc + (qlast + 63) / 64;
+
+  // DMA instruction i (0, 1) of this wave fills tile bytes 1024 (2 w + i) +
+  // 16 lane: row pos / 8, stored chunk pos % 8, which holds logical chunk
+  // (pos % 8) ^ swz_r128(row) (the LdsTile<64> layout)
+  int drow[2], dcol[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int pos = 64 * (2 * w + i) + lane;
+    drow[i] = pos >> 3;
+    dcol[i] = 8 * ((pos & 7) ^ swz_r128(pos >> 3));
+  }
+  const uint32_t lds_st = lds_addr(stg), lds_wave = static_cast<uint32_t>(2 * w) << 10;
+  // tile gt into stage st: 2 + 2 sixteen-byte and 1 four-byte DMA per wave
+  // (wave 0 brings the tile's dc, wave 1 its dt, wave 2 64 copies of the
+  // chunk's last dc, wave 3 a spare copy of dt, so that every wave counts
+  // the same number per tile).  Rows past the chunk repeat its last (their
+  // scale is 0).
+  auto issue = [&](int gt, int st) __attribute__((always_inline)) {
+    const int c = gt / tpc, tt = gt - c * tpc;
+    const int t0 = 64 * tt;
+    const int qv = min(64, min(d.Lc, d.L - c * d.Lc) - t0);
+    const long tok = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc + t0;
+    const bf16* ub = u + tok * a_rs + h * d.P + p0;
+    const bf16* xb = Bm + tok * x_rs + static_cast<long>(g) * d.N + n0;
+    const uint32_t base = lds_st + static_cast<uint32_t>(st * kStage * 2);   // bytes
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = min(drow[i], qv - 1);
+      dma_lds16(ub, 2u * static_cast<uint32_t>(r * a_rs + dcol[i]), base + lds_wave + (i << 10));
+      dma_lds16(xb, 2u * static_cast<uint32_t>(r * x_rs + dcol[i]), base + 2 * PL + lds_wave + (i << 10));
+    }
+    const long crow = (bh * d.nc + c) * d.Lc;
+    const float* rv = w == 2 ? dc + crow + d.Lc - 1 : ((w & 1) ? dt : dc) + crow + t0;
+    const uint32_t ro = w == 2 ? 0u : 4u * static_cast<uint32_t>(min(lane, qv - 1));
+    dma_lds4(rv, ro, base + 4 * PL + 256 * w);
+  };
+
+  issue(0, 0);
+  issue(min(1, ntiles - 1), 1);
+  issue(min(2, ntiles - 1), 2);
+  for (int gt = 0; gt < ntiles; ++gt) {
+    const int st = gt % NS;
+    const bf16* sb = stg + st * kStage;
+    const int c = gt / tpc, tt = gt - c * tpc;
+    const int qlim = min(d.Lc, d.L - c * d.Lc);
+    // tile gt has landed (two later tiles, 5 DMAs each, may still be in flight)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(vm_wait<10>());
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (tt == 0) {   // the chunk's entry state
+      float* o = states + (static_cast<long>(b) * d.nc + c) * d.H * PN + static_cast<long>(h) * PN + eo;
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt)
+        *reinterpret_cast<float4*>(o + 16 * pt * d.N) = make_float4(H[pt][0], H[pt][1], H[pt][2], H[pt][3]);
+    }
+    // w u as hi + lo planes
+    {
+      const float* rdc = reinterpret_cast<const float*>(sb + 2 * PL);   // dc, dt, dc_last: 64 fp32 each
+      const float* rdt = rdc + 64;
+      const float dcl = rdc[128] * kLog2e;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid + 256 * i, row = e >> 3;
+        const int ao = TL::off(row, 8 * (e & 7));
+        const uint4 q = *reinterpret_cast<const uint4*>(sb + ao);
+        const float sc = 64 * tt + row < qlim
+                             ? fast_exp2(fminf(dcl - rdc[row] * kLog2e, 0.f)) * rdt[row] : 0.f;
+        const uint32_t v[4] = {q.x, q.y, q.z, q.w};
+        uint32_t r[4], rl[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float v0 = bf16lo_to_f32(v[j]) * sc, v1 = bf16hi_to_f32(v[j]) * sc;
+          r[j] = pack_bf16x2(v0, v1);
+          rl[j] = pack_bf16x2(v0 - bf16lo_to_f32(r[j]), v1 - bf16hi_to_f32(r[j]));
+        }
+        *reinterpret_cast<uint4*>(As + ao) = uint4{r[0], r[1], r[2], r[3]};
+        *reinterpret_cast<uint4*>(As + PL + ao) = uint4{rl[0], rl[1], rl[2], rl[3]};
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      v8bf bop[4][2];
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) bop[pt][pl] = tile_tr8<64>(As + pl * PL, 32 * ks + 8 * lg, 16 * pt, lane);
+      const v8bf a = tile_tr8<64>(sb + PL, 32 * ks + 8 * lg, 16 * w, lane);
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) S[pt] = mfma_bf16(a, bop[pt][pl], S[pt]);
+    }
+    if (tt == (qlim + 63) / 64 - 1) {   // the chunk's last tile: pass the state on
+      const float sc = expf(reinterpret_cast<const float*>(sb + 2 * PL)[128]);
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) H[pt][r] = sc * H[pt][r] + S[pt][r];
+        S[pt] = v4f{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    // every wave is done with the stage and the planes: refill the stage
+    // (the last tile again past the end, so that every step waits the same)
+    __syncthreads();
+    issue(min(gt + NS, ntiles - 1), st);
+  }
+  // drain the surplus DMA before the block ends
+  __builtin_amdgcn_s_waitcnt(vm_wait<0>());
+  float* o = h_last + bh * PN + eo;
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt)
+    *reinterpret_cast<float4*>(o + 16 * pt * d.N) = make_float4(H[pt][0], H[pt][1], H[pt][2], H[pt][3]);
+}
+
+// ---------------------------------------------------------------------------
 // state passing (forward): sequential over chunks, parallel over (b, h, P*N).
 // Loads of a group of chunks are issued together before the dependent math.
 // ---------------------------------------------------------------------------
@@ -945,6 +1127,25 @@ int launch_dstate_planes(const float* dy, const void* C, const float* dt, const 
   return launch_chunk_outer_bf16_nk<4, 1>(dy, C, dt, dc, length, out, d, s, dyp);
 }
 
+// chunk states and state passing in one kernel: bf16 u and B, head_dim and
+// state_dim multiples of 64, 16-byte aligned operands
+bool chunk_state_pass_ok(const SsdDims& d, const void* u, const void* B, const float* h_init,
+                         const float* states, const float* h_last) {
+  return d.P % 64 == 0 && d.N % 64 == 0 && aligned16(u) && aligned16(B) &&
+         (!h_init || aligned16(h_init)) && aligned16(states) && aligned16(h_last);
+}
+int launch_chunk_state_pass(const void* u, const void* B, const float* dt, const float* dc,
+                            const float* h_init, float* states, float* h_last, const SsdDims& d,
+                            hipStream_t s) {
+  const long blocks = static_cast<long>(d.b) * d.H * (d.P / 64) * (d.N / 64);
+  ProfScope prof_("chunk_state_pass_fwd", s);
+  hipLaunchKernelGGL(chunk_state_pass_kernel, dim3(blocks), dim3(256), 0, s,
+                     static_cast<const bf16*>(u), static_cast<const bf16*>(B), dt, dc, h_init,
+                     states, h_last, d);
+  SA_CHECK_LAUNCH("chunk_state_pass");
+  return 0;
+}
+
 int launch_state_passing_fwd(float* states, const float* h_init, float* h_last, const float* dc,
                              const SsdDims& d, hipStream_t s) {
   const long PN = static_cast<long>(d.P) * d.N;
@@ -1042,8 +1243,12 @@ int ssd_fwd_impl(const void* u, const float* A, const void* B, const void* C,
   SA_CHECK_ARG(!go || fast, "sa_ssd_fwd_gated: the fused epilogue needs the bf16 fast path "
                "(state_dim a multiple of 32, <= 256; head_dim a multiple of 8; 16-byte aligned)");
   if ((rc = launch_chunk_cumsum<T>(delta_raw, A, bias, length, dt, dc, d, sp, lo, hi, s))) return rc;
-  if ((rc = launch_chunk_outer<MT, T, T, 0>(u, B, dt, dc, length, states, d, s))) return rc;
-  if ((rc = launch_state_passing_fwd(states, h_init, h_last, dc, d, s))) return rc;
+  if (sizeof(T) == 2 && chunk_state_pass_ok(d, u, B, h_init, states, h_last)) {
+    if ((rc = launch_chunk_state_pass(u, B, dt, dc, h_init, states, h_last, d, s))) return rc;
+  } else {
+    if ((rc = launch_chunk_outer<MT, T, T, 0>(u, B, dt, dc, length, states, d, s))) return rc;
+    if ((rc = launch_state_passing_fwd(states, h_init, h_last, dc, d, s))) return rc;
+  }
   if (fast) return launch_chunk_scan_bf16(u, B, C, dt, dc, states, y, d, lo >= 0.f ? 1 : 0, go, s);
   return launch_chunk_scan<MT, T>(u, B, C, dt, dc, states, y, d, s);
 }

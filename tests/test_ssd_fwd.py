@@ -300,3 +300,31 @@ def test_ssd_short_chunk_ignores_stale_lds(chunk):
         assert_parity(h, h_ref, torch.float32, "h_last")
         for gname, gv in zip(("du", "dB", "dC", "ddelta_raw"), grads):
             assert torch.isfinite(gv).all(), f"{gname}: non-finite values"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,chunk", [
+    # chunk 96: each chunk is one full and one 32-row t tile; ragged lengths
+    (dict(b=2, L=300, H=4, P=64, N=128, G=2, lens=[300, 95]), 96),
+    # two p tiles, three n blocks, the last chunk partial
+    (dict(b=1, L=600, H=2, P=128, N=192, G=1), 256),
+    # no initial state, state_dim 64
+    (dict(b=2, L=256, H=4, P=64, N=64, G=1, with_h=False), 64),
+])
+def test_ssd_fwd_chunk_states_near_fp32(shape, chunk):
+    """The chunk entry states and h_last of the bf16 path (chunk states and
+    state passing in one kernel, w u as hi + lo planes) against the oracle's
+    at 1e-4 of their scale, and dt, dc at the fp32 bound."""
+    from selective_attention.kernels.ssd_scan import ssd_scan_forward
+    print(f"ssd fwd chunk states {shape} chunk={chunk}", flush=True)
+    x = make_inputs(dtype=torch.bfloat16, **shape)
+    xd = to_dev(x)
+    _, h, (dt, dc, st) = ssd_scan_forward(xd["u"], xd["A"], xd["B"], xd["C"], xd["delta_raw"],
+                                          xd["delta_bias"], xd["h_init"], xd["length"], chunk,
+                                          return_saved=True)
+    torch.cuda.synchronize()
+    _, h_ref, it = ref.ssd_scan_forward(**x, chunk_size=chunk, return_intermediates=True)
+    assert_parity(dt, it["dt"], torch.float32, "dt")
+    assert_parity(dc, it["dc"], torch.float32, "dc")
+    assert_scaled(st, it["H_in"], "states", frac=1e-4)
+    assert_scaled(h, h_ref, "h_last", frac=1e-4)
