@@ -55,6 +55,14 @@ struct LdsTile {
     else return r * kLd + col;
   }
 };
+// transposed read at precomputed element offsets: off0 addresses this lane's
+// row k0 + (lane & 15) / 4, off1 the row 4 further on (see tile_tr8)
+__device__ __forceinline__ v8bf tile_tr8_at(const bf16* t, int off0, int off1) {
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(t + off0));
+  const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(t + off1));
+  return __builtin_bit_cast(v8bf, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
 // a BfTile's registers (64 rows of 32 NK bf16) into an LdsTile<32 NK>
 template <int NK, int NTHR>
 __device__ __forceinline__ void commit_lds(const BfTile<NK, NTHR>& t, bf16* dst, int tid) {

@@ -373,10 +373,12 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
 // every chunk in order, so the chunk states never leave the chip.
 // A tile's raw u and B rows and its dc, dt go from HBM straight into one of
 // three LDS stages (global_load_lds, issued three tiles ahead and waited for
-// with explicit counts); each step then scales u by w_t and splits it into
-// hi + lo planes (w u is fp32) for the MFMAs, which read B from the stage.
-// The products and their order are chunk_outer_bf16_kernel<., 0>'s and the
-// update is state_passing_fwd_kernel's.
+// with explicit counts).  Step g runs tile g's MFMAs (w u as hi + lo planes,
+// B from the stage) while the waves scale tile g + 1's u by w_t and split it
+// into its planes in place (w u is fp32), so that the split's latency does
+// not sit between a tile's arrival and its MFMAs.  The products and their
+// order are chunk_outer_bf16_kernel<., 0>'s and the update is
+// state_passing_fwd_kernel's.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
     const bf16* __restrict__ u, const bf16* __restrict__ Bm, const float* __restrict__ dt,
@@ -385,8 +387,10 @@ __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
   using TL = LdsTile<64>;
   constexpr int PL = 64 * TL::kLd;            // bf16 per 64 x 64 tile
   constexpr int NS = 3;                        // DMA stages
-  constexpr int kStage = 2 * PL + 4 * 128;     // bf16: u tile, B tile (+PL), 4 x 64 fp32 row values (+2 PL)
-  __shared__ __align__(16) bf16 As[2 * PL];   // hi, lo planes of (w u)[t][p]
+  constexpr int kDma = 5;                      // DMA instructions per wave per tile
+  // stage (bf16): u tile, then its hi plane in place; lo plane (+PL); B tile
+  // (+2 PL); 4 x 64 fp32 row values (+3 PL): dc, dt, the chunk's last dc
+  constexpr int kStage = 3 * PL + 4 * 128;
   __shared__ __align__(16) bf16 stg[NS * kStage];
 
   const int ptiles = d.P / 64, nblk = d.N / 64;
@@ -418,110 +422,169 @@ __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
       H[pt] = v4f{v.x, v.y, v.z, v.w};
     }
   }
-
-  // the initial state has arrived before the loop, whose waits count DMA only
+  // the initial state has arrived before the loop, whose waits count DMA
+  // and the state stores only
   __builtin_amdgcn_s_waitcnt(vm_wait<0>());
 
-  // t tiles: every chunk but the last has tpc, the last ntt_last
+  // t tiles: every chunk but the last has tpc, the last ntt_last; walkers
+  // hold (chunk, t tile in it, tiles in the chunk) and advance without division
   const int tpc = (d.Lc + 63) / 64;
   const int qlast = d.L - (d.nc - 1) * d.Lc;
-  const int ntiles = (d.nc - 1) * tpc + (qlast + 63) / 64;
+  const int ntt_last = (qlast + 63) / 64;
+  const int ntiles = (d.nc - 1) * tpc + ntt_last;
+  struct Walk {
+    int c, tt, ntt;
+  };
+  auto adv = [&](Walk& x) __attribute__((always_inline)) {
+    if (++x.tt == x.ntt) {
+      x.tt = 0;
+      ++x.c;
+      x.ntt = x.c == d.nc - 1 ? ntt_last : tpc;
+    }
+  };
+  auto rows_of = [&](const Walk& x) { return min(64, min(d.Lc, d.L - x.c * d.Lc) - 64 * x.tt); };
+
+  // per-lane LDS element offsets, the same in every stage: transposed reads
+  // of the planes (rows 8 lg + (li / 4) and + 4 of k step 0, columns 16 pt +
+  // 4 (li % 4); k step 1 is 32 rows = 2048 elements on) and of B (columns
+  // 16 w + 4 (li % 4)), and the two u chunks this thread splits
+  int o_b[4][2], o_x[2], ao[2];
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) o_b[pt][hh] = TL::off(8 * lg + 4 * hh + (li >> 2), 16 * pt + 4 * (li & 3));
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) o_x[hh] = TL::off(8 * lg + 4 * hh + (li >> 2), 16 * w + 4 * (li & 3));
+#pragma unroll
+  for (int i = 0; i < 2; ++i) ao[i] = TL::off((tid + 256 * i) >> 3, 8 * ((tid + 256 * i) & 7));
 
   // DMA instruction i (0, 1) of this wave fills tile bytes 1024 (2 w + i) +
-  // 16 lane: row pos / 8, stored chunk pos % 8, which holds logical chunk
-  // (pos % 8) ^ swz_r128(row) (the LdsTile<64> layout)
+  // 16 lane: row pos / 8 with pos = 64 (2 w + i) + lane, stored chunk pos %
+  // 8, which holds logical chunk (pos % 8) ^ swz_r128(row) (the LdsTile<64>
+  // layout); lane byte offsets of a full tile's u and B rows
   int drow[2], dcol[2];
+  uint32_t du[2], dx[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int pos = 64 * (2 * w + i) + lane;
     drow[i] = pos >> 3;
     dcol[i] = 8 * ((pos & 7) ^ swz_r128(pos >> 3));
+    du[i] = 2u * static_cast<uint32_t>(drow[i] * a_rs + dcol[i]);
+    dx[i] = 2u * static_cast<uint32_t>(drow[i] * x_rs + dcol[i]);
   }
   const uint32_t lds_st = lds_addr(stg), lds_wave = static_cast<uint32_t>(2 * w) << 10;
-  // tile gt into stage st: 2 + 2 sixteen-byte and 1 four-byte DMA per wave
+  // tile x into stage st: 2 + 2 sixteen-byte and 1 four-byte DMA per wave
   // (wave 0 brings the tile's dc, wave 1 its dt, wave 2 64 copies of the
   // chunk's last dc, wave 3 a spare copy of dt, so that every wave counts
   // the same number per tile).  Rows past the chunk repeat its last (their
   // scale is 0).
-  auto issue = [&](int gt, int st) __attribute__((always_inline)) {
-    const int c = gt / tpc, tt = gt - c * tpc;
-    const int t0 = 64 * tt;
-    const int qv = min(64, min(d.Lc, d.L - c * d.Lc) - t0);
-    const long tok = static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc + t0;
+  auto issue = [&](const Walk& x, int st) __attribute__((always_inline)) {
+    const int t0 = 64 * x.tt, qv = rows_of(x);
+    const long tok = static_cast<long>(b) * d.L + static_cast<long>(x.c) * d.Lc + t0;
     const bf16* ub = u + tok * a_rs + h * d.P + p0;
     const bf16* xb = Bm + tok * x_rs + static_cast<long>(g) * d.N + n0;
     const uint32_t base = lds_st + static_cast<uint32_t>(st * kStage * 2);   // bytes
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int r = min(drow[i], qv - 1);
-      dma_lds16(ub, 2u * static_cast<uint32_t>(r * a_rs + dcol[i]), base + lds_wave + (i << 10));
-      dma_lds16(xb, 2u * static_cast<uint32_t>(r * x_rs + dcol[i]), base + 2 * PL + lds_wave + (i << 10));
+      uint32_t ou = du[i], ox = dx[i];
+      if (qv < 64) {
+        const int r = min(drow[i], qv - 1);
+        ou = 2u * static_cast<uint32_t>(r * a_rs + dcol[i]);
+        ox = 2u * static_cast<uint32_t>(r * x_rs + dcol[i]);
+      }
+      dma_lds16(ub, ou, base + lds_wave + (i << 10));
+      dma_lds16(xb, ox, base + 4 * PL + lds_wave + (i << 10));
     }
-    const long crow = (bh * d.nc + c) * d.Lc;
+    const long crow = (bh * d.nc + x.c) * d.Lc;
     const float* rv = w == 2 ? dc + crow + d.Lc - 1 : ((w & 1) ? dt : dc) + crow + t0;
     const uint32_t ro = w == 2 ? 0u : 4u * static_cast<uint32_t>(min(lane, qv - 1));
-    dma_lds4(rv, ro, base + 4 * PL + 256 * w);
+    dma_lds4(rv, ro, base + 6 * PL + 256 * w);
+  };
+  // tile x's u in stage ST -> (w u) hi plane in place, lo plane at +PL
+  auto split = [&](const Walk& x, auto stc) __attribute__((always_inline)) {
+    bf16* sb = stg + decltype(stc)::value * kStage;
+    const int qv = rows_of(x);
+    const float* rdc = reinterpret_cast<const float*>(sb + 3 * PL);
+    const float* rdt = rdc + 64;
+    const float dcl = rdc[128] * kLog2e;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = (tid + 256 * i) >> 3;
+      const uint4 q = *reinterpret_cast<const uint4*>(sb + ao[i]);
+      const float sc = row < qv ? fast_exp2(fminf(dcl - rdc[row] * kLog2e, 0.f)) * rdt[row] : 0.f;
+      const uint32_t v[4] = {q.x, q.y, q.z, q.w};
+      uint32_t r[4], rl[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float v0 = bf16lo_to_f32(v[j]) * sc, v1 = bf16hi_to_f32(v[j]) * sc;
+        r[j] = pack_bf16x2(v0, v1);
+        rl[j] = pack_bf16x2(v0 - bf16lo_to_f32(r[j]), v1 - bf16hi_to_f32(r[j]));
+      }
+      *reinterpret_cast<uint4*>(sb + ao[i]) = uint4{r[0], r[1], r[2], r[3]};
+      *reinterpret_cast<uint4*>(sb + PL + ao[i]) = uint4{rl[0], rl[1], rl[2], rl[3]};
+    }
   };
 
-  issue(0, 0);
-  issue(min(1, ntiles - 1), 1);
-  issue(min(2, ntiles - 1), 2);
-  for (int gt = 0; gt < ntiles; ++gt) {
-    const int st = gt % NS;
-    const bf16* sb = stg + st * kStage;
-    const int c = gt / tpc, tt = gt - c * tpc;
-    const int qlim = min(d.Lc, d.L - c * d.Lc);
-    // tile gt has landed (two later tiles, 5 DMAs each, may still be in flight)
+  // prologue: tiles 0, 1, 2 (the last again past the end) into stages 0..2
+  Walk wi{0, 0, d.nc == 1 ? ntt_last : tpc};
+  int gi = 0;   // tile index of wi
+  auto adv_issue = [&]() __attribute__((always_inline)) {
+    if (gi + 1 < ntiles) {
+      adv(wi);
+      ++gi;
+    }
+  };
+  issue(wi, 0);
+  adv_issue();
+  issue(wi, 1);
+  adv_issue();
+  issue(wi, 2);
+  adv_issue();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(vm_wait<2 * kDma>());
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  Walk wc{0, 0, d.nc == 1 ? ntt_last : tpc};   // the tile computed
+  Walk wsp = wc;                               // the tile split (one ahead)
+  split(wsp, std::integral_constant<int, 0>{});
+  adv(wsp);
+  bool stored = false;   // the step before stored a state (4 stores per wave)
+  int gt = 0;
+  // step gt (its stage ST = gt % NS, a compile-time value in the unrolled loop)
+  auto step = [&](auto stc) __attribute__((always_inline)) {
+    constexpr int ST = decltype(stc)::value;
+    const bf16* sb = stg + ST * kStage;
+    // tile gt + 1 has landed (tile gt + 2, and the state stores of the step
+    // before, may still be in flight); tile gt's planes are visible
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(vm_wait<10>());
+    if (stored) __builtin_amdgcn_s_waitcnt(vm_wait<kDma + 4>());
+    else __builtin_amdgcn_s_waitcnt(vm_wait<kDma>());
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (tt == 0) {   // the chunk's entry state
-      float* o = states + (static_cast<long>(b) * d.nc + c) * d.H * PN + static_cast<long>(h) * PN + eo;
+    stored = wc.tt == 0;
+    if (stored) {   // the chunk's entry state
+      float* o = states + (static_cast<long>(b) * d.nc + wc.c) * d.H * PN + static_cast<long>(h) * PN + eo;
 #pragma unroll
       for (int pt = 0; pt < 4; ++pt)
         *reinterpret_cast<float4*>(o + 16 * pt * d.N) = make_float4(H[pt][0], H[pt][1], H[pt][2], H[pt][3]);
     }
-    // w u as hi + lo planes
-    {
-      const float* rdc = reinterpret_cast<const float*>(sb + 2 * PL);   // dc, dt, dc_last: 64 fp32 each
-      const float* rdt = rdc + 64;
-      const float dcl = rdc[128] * kLog2e;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int e = tid + 256 * i, row = e >> 3;
-        const int ao = TL::off(row, 8 * (e & 7));
-        const uint4 q = *reinterpret_cast<const uint4*>(sb + ao);
-        const float sc = 64 * tt + row < qlim
-                             ? fast_exp2(fminf(dcl - rdc[row] * kLog2e, 0.f)) * rdt[row] : 0.f;
-        const uint32_t v[4] = {q.x, q.y, q.z, q.w};
-        uint32_t r[4], rl[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float v0 = bf16lo_to_f32(v[j]) * sc, v1 = bf16hi_to_f32(v[j]) * sc;
-          r[j] = pack_bf16x2(v0, v1);
-          rl[j] = pack_bf16x2(v0 - bf16lo_to_f32(r[j]), v1 - bf16hi_to_f32(r[j]));
-        }
-        *reinterpret_cast<uint4*>(As + ao) = uint4{r[0], r[1], r[2], r[3]};
-        *reinterpret_cast<uint4*>(As + PL + ao) = uint4{rl[0], rl[1], rl[2], rl[3]};
-      }
-    }
-    __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       v8bf bop[4][2];
 #pragma unroll
       for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl) bop[pt][pl] = tile_tr8<64>(As + pl * PL, 32 * ks + 8 * lg, 16 * pt, lane);
-      const v8bf a = tile_tr8<64>(sb + PL, 32 * ks + 8 * lg, 16 * w, lane);
+        for (int pl = 0; pl < 2; ++pl)
+          bop[pt][pl] = tile_tr8_at(sb + pl * PL + 2048 * ks, o_b[pt][0], o_b[pt][1]);
+      const v8bf a = tile_tr8_at(sb + 2 * PL + 2048 * ks, o_x[0], o_x[1]);
 #pragma unroll
       for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
         for (int pl = 0; pl < 2; ++pl) S[pt] = mfma_bf16(a, bop[pt][pl], S[pt]);
     }
-    if (tt == (qlim + 63) / 64 - 1) {   // the chunk's last tile: pass the state on
-      const float sc = expf(reinterpret_cast<const float*>(sb + 2 * PL)[128]);
+    if (gt + 1 < ntiles) split(wsp, std::integral_constant<int, (ST + 1) % NS>{});
+    if (wc.tt == wc.ntt - 1) {   // the chunk's last tile: pass the state on
+      const float sc = expf(reinterpret_cast<const float*>(sb + 3 * PL)[128]);
 #pragma unroll
       for (int pt = 0; pt < 4; ++pt) {
 #pragma unroll
@@ -529,10 +592,22 @@ __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
         S[pt] = v4f{0.f, 0.f, 0.f, 0.f};
       }
     }
-    // every wave is done with the stage and the planes: refill the stage
-    // (the last tile again past the end, so that every step waits the same)
+    // every wave is done with the stage, and tile gt + 1's planes are
+    // written: refill the stage (the last tile again past the end, so that
+    // every step waits the same)
     __syncthreads();
-    issue(min(gt + NS, ntiles - 1), st);
+    issue(wi, ST);
+    adv_issue();
+    adv(wc);
+    adv(wsp);
+    ++gt;
+  };
+  while (gt < ntiles) {
+    step(std::integral_constant<int, 0>{});
+    if (gt >= ntiles) break;
+    step(std::integral_constant<int, 1>{});
+    if (gt >= ntiles) break;
+    step(std::integral_constant<int, 2>{});
   }
   // drain the surplus DMA before the block ends
   __builtin_amdgcn_s_waitcnt(vm_wait<0>());
