@@ -1202,12 +1202,33 @@ int launch_dstate_planes(const float* dy, const void* C, const float* dt, const 
   return launch_chunk_outer_bf16_nk<4, 1>(dy, C, dt, dc, length, out, d, s, dyp);
 }
 
+// compute units of the current device (cached per device; 256 if unknown)
+int device_cus() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      return 256;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
 // chunk states and state passing in one kernel: bf16 u and B, head_dim and
-// state_dim multiples of 64, 16-byte aligned operands
+// state_dim multiples of 64, 16-byte aligned operands, and at least two
+// blocks per CU.  Its blocks walk every chunk in order, so it wins only
+// while every CU holds two of them (config 1: 512 blocks of 64 t tiles,
+// 108 us against 127 for the two kernels); with fewer, longer walks it
+// loses (config 4's SSM shape, 256 blocks of 128 tiles: 154 against ~127 us;
+// the reference default, 128 blocks: 80 us).
 bool chunk_state_pass_ok(const SsdDims& d, const void* u, const void* B, const float* h_init,
                          const float* states, const float* h_last) {
+  const long blocks = static_cast<long>(d.b) * d.H * (d.P / 64) * (d.N / 64);
   return d.P % 64 == 0 && d.N % 64 == 0 && aligned16(u) && aligned16(B) &&
-         (!h_init || aligned16(h_init)) && aligned16(states) && aligned16(h_last);
+         (!h_init || aligned16(h_init)) && aligned16(states) && aligned16(h_last) &&
+         blocks >= 2L * device_cus();
 }
 int launch_chunk_state_pass(const void* u, const void* B, const float* dt, const float* dc,
                             const float* h_init, float* states, float* h_last, const SsdDims& d,

@@ -303,6 +303,48 @@ def test_ssd_short_chunk_ignores_stale_lds(chunk):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("N,chunk,lens", [(128, 96, [300, 95, 300]), (64, 256, [300, 1, 212])])
+def test_ssd_fwd_chunk_state_pass_equals_two_kernels(N, chunk, lens):
+    """With at least two blocks per CU (b H (P / 64) (N / 64) >= 2 CUs) the
+    chunk states and state passing run as one kernel; a single batch row
+    (fewer blocks) runs chunk_outer_bf16 + state_passing_fwd.  Every row's
+    entry states, h_last, dt and dc are bit-equal between the two, and the
+    one-kernel states match the oracle's at 1e-4 of their scale."""
+    from selective_attention.kernels.ssd_scan import ssd_scan_forward
+    from selective_attention.profiling import kernel_timer
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    H = 128
+    b = max(3, -(-2 * cus // (H * (N // 64))))
+    lens = (lens * b)[:b]
+    print(f"ssd fwd one-kernel chunk states: b={b} H={H} N={N} chunk={chunk} cus={cus}", flush=True)
+    x = make_inputs(dtype=torch.bfloat16, b=b, L=300, H=H, P=64, N=N, G=4, lens=lens)
+
+    def run(xs):
+        xd = to_dev(xs)
+        with kernel_timer() as kt:
+            _, h, (dt, dc, st) = ssd_scan_forward(xd["u"], xd["A"], xd["B"], xd["C"], xd["delta_raw"],
+                                                  xd["delta_bias"], xd["h_init"], xd["length"],
+                                                  chunk, return_saved=True)
+            torch.cuda.synchronize()
+        return (h, dt, dc, st), kt.stats
+
+    full, kfull = run(x)
+    assert "chunk_state_pass_fwd" in kfull and "state_passing_fwd" not in kfull, sorted(kfull)
+    for r in (0, b - 1):
+        xr = {k: (v[r:r + 1] if isinstance(v, torch.Tensor) and k not in ("A", "delta_bias") else v)
+              for k, v in x.items()}
+        one, kone = run(xr)
+        assert "state_passing_fwd" in kone and "chunk_state_pass_fwd" not in kone, sorted(kone)
+        for name, a, o in zip(("h_last", "dt", "dc", "states"), full, one):
+            assert torch.equal(a[r:r + 1], o), f"row {r}: {name} differs from the two-kernel path"
+    xs = {k: (v[:2] if isinstance(v, torch.Tensor) and k not in ("A", "delta_bias") else v)
+          for k, v in x.items()}
+    _, h_ref, it = ref.ssd_scan_forward(**xs, chunk_size=chunk, return_intermediates=True)
+    assert_scaled(full[3][:2], it["H_in"], "states", frac=1e-4)
+    assert_scaled(full[0][:2], h_ref, "h_last", frac=1e-4)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("shape,chunk", [
     # chunk 96: each chunk is one full and one 32-row t tile; ragged lengths
     (dict(b=2, L=300, H=4, P=64, N=128, G=2, lens=[300, 95]), 96),
