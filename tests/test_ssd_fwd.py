@@ -354,9 +354,10 @@ def test_ssd_fwd_chunk_state_pass_equals_two_kernels(N, chunk, lens):
     (dict(b=2, L=256, H=4, P=64, N=64, G=1, with_h=False), 64),
 ])
 def test_ssd_fwd_chunk_states_near_fp32(shape, chunk):
-    """The chunk entry states and h_last of the bf16 path (chunk states and
-    state passing in one kernel, w u as hi + lo planes) against the oracle's
-    at 1e-4 of their scale, and dt, dc at the fp32 bound."""
+    """The chunk entry states and h_last of the bf16 path at shapes with few
+    blocks (chunk_outer_bf16 + state_passing_fwd, w u as hi + lo planes)
+    against the oracle's at 1e-4 of their scale, and dt, dc at the fp32
+    bound."""
     from selective_attention.kernels.ssd_scan import ssd_scan_forward
     print(f"ssd fwd chunk states {shape} chunk={chunk}", flush=True)
     x = make_inputs(dtype=torch.bfloat16, **shape)
