@@ -958,7 +958,9 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
   // registers); then S = j - HPG = 0..T: this half of B_S and dCB^T of (S, T) by DMA
   const int nstage = HPG + T + 1;
   float4 ph[4];   // H prefetch: row tid / 4, columns n0 + 16 (tid % 4) .. +15
+  float dce_n;    // dc of this lane's row for the prefetched head
   auto load_h = [&](int k) {
+    dce_n = dcc[k * hstride + tcl];
     const float* src = Hc + k * (64L * N) + (tid >> 2) * N + 16 * (tid & 3);
 #pragma unroll
     for (int i = 0; i < 4; ++i) ph[i] = *reinterpret_cast<const float4*>(src + 4 * i);
@@ -981,17 +983,36 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
       *reinterpret_cast<uint4*>(dst + 64 * NH + off) = uint4{lo[0], lo[1], lo[2], lo[3]};
     }
   };
-  int o_dcb[2];
+  // The intra stages' DMA goes through dma_lds16, which the compiler does not
+  // see as an LDS write: with the builtin it held every stage's first LDS
+  // read until the next stage's DMA (issued just before) had landed, so no
+  // load overlapped any compute.  The end-of-stage wait and barrier order
+  // the DMA before the next stage's reads.  Lane offsets in bytes: B tile
+  // row brow[i], swizzled column bcol[i]; the dCB planes in lane order.
+  int brow[2], bcol[2];
+  uint32_t o_bt[2], o_dcb[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) o_dcb[i] = dcb_lane_off(i, w, lane);
+  for (int i = 0; i < 2; ++i) {
+    const int pos = (w * 2 + i) * 64 + lane;
+    brow[i] = pos >> 3;
+    bcol[i] = 8 * ((pos & 7) ^ (swz_k128(brow[i]) & 7));
+    o_bt[i] = 2u * static_cast<uint32_t>(brow[i] * act_rs + bcol[i]);
+    o_dcb[i] = 2u * static_cast<uint32_t>(dcb_lane_off(i, w, lane));
+  }
+  const uint32_t lds_st = lds_addr(stg), lds_wave = static_cast<uint32_t>(2 * w) << 10;
   auto issue_intra = [&](int jj) {
     const int S = jj - HPG;
-    bf16* dst = stg + (jj & 1) * SM::kStage;
-    dma_tile<8, swz_k128>(dst, Bc + static_cast<long>(64 * S) * act_rs, act_rs,
-                          min(64, qlim - 64 * S), w, lane);
+    const uint32_t base = lds_st + static_cast<uint32_t>((jj & 1) * SM::kStage * 2);
+    const int qv = min(64, qlim - 64 * S);   // rows past it repeat row qv - 1
+    const bf16* bsrc = Bc + static_cast<long>(64 * S) * act_rs;
     const bf16* src = dcbp + ((bcg * ttiles + S) * ttiles + T) * (2L * kPlaneT);
-    dma_pre<8>(dst + 64 * NH, src, o_dcb, w);
-    dma_pre<8>(dst + 64 * NH + kPlaneT, src + 2048, o_dcb, w);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t ob = qv < 64 ? 2u * static_cast<uint32_t>(min(brow[i], qv - 1) * act_rs + bcol[i]) : o_bt[i];
+      dma_lds16(bsrc, ob, base + lds_wave + (i << 10));
+      dma_lds16(src, o_dcb[i], base + 2 * 64 * NH + lds_wave + (i << 10));
+      dma_lds16(src, o_dcb[i] + 4096u, base + 2 * (64 * NH + kPlaneT) + lds_wave + (i << 10));
+    }
   };
 
   v4f dCT[NTH];   // dC^T rows n = n0 + 16 nt + 4 lg + r, column tau
@@ -1002,10 +1023,23 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
   for (int ks = 0; ks < 2; ++ks) dyn[ks][0] = dyn[ks][1] = zero_v8bf();
   load_h(0);
   load_dy(0, dyf);
+  float dce = dce_n;
   commit_h(0);
+  // The loads before the loop land here (the empty asm statements take their
+  // values).  Left to itself the compiler sinks them into the first stage,
+  // and its waits for them inside the loop also hold every stage's prefetch.
+  asm volatile("" : "+v"(dce));
+#pragma unroll
+  for (int nt = 0; nt < NTH; ++nt) asm volatile("" : "+v"(cv[nt]));
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) asm volatile("" : "+v"(dyf[ks][0]), "+v"(dyf[ks][1]));
   __syncthreads();
 
+  // x_C of head j is stored at the start of stage j + 1, before that stage's
+  // loads, so that the end-of-stage wait does not wait for the store
+  float xs = 0.f;
   for (int j = 0; j < nstage; ++j) {
+    if (j >= 1 && j - 1 < HPG && lg == 0) xCc[NHALF * (j - 1) * hstride + tau] = tau < lim ? xs : 0.f;
     if (j + 1 < HPG) {
       load_h(j + 1);
       load_dy(j + 1, dyn);
@@ -1015,7 +1049,6 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
     const bf16* Sg = stg + (j & 1) * SM::kStage;
     if (j < HPG) {
       // X^T[n, tau] = sum_p H[p, n] dy[tau, p]; dC^T += e^{dc_tau} X^T; x_C
-      const int k = j;
       v4f X[NTH];
 #pragma unroll
       for (int nt = 0; nt < NTH; ++nt) X[nt] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -1037,7 +1070,7 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
           X[nt] = mfma_bf16(hh, dyf[ks][1], X[nt]);
         }
       }
-      const float e = fast_exp2(dcc[k * hstride + tcl] * kLog2e);
+      const float e = fast_exp2(dce * kLog2e);
       float s = 0.f;
 #pragma unroll
       for (int nt = 0; nt < NTH; ++nt) {
@@ -1045,13 +1078,13 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
         s += dot4_bf16(X[nt], cv[nt]);
         dCT[nt] += X[nt];
       }
-      s = group_sum(s);
-      if (lg == 0) xCc[NHALF * k * hstride + tau] = tau < lim ? s : 0.f;
+      xs = group_sum(s);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         dyf[ks][0] = dyn[ks][0];
         dyf[ks][1] = dyn[ks][1];
       }
+      dce = dce_n;
     } else {
       // dC^T[n, tau] += sum_sig B[sig, n] dCB[tau, sig]
       const bf16* Bt = Sg;
