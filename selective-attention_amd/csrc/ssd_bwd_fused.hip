@@ -127,6 +127,29 @@ __device__ __forceinline__ int dma_off_w8(int i, int w, int lane, int grs) {
   return row * grs + 8 * (pc ^ (F(row) & (RC - 1)));
 }
 
+// The same copies through dma_lds16 (common.h), which the compiler does not
+// see as LDS writes, so it holds no LDS access or load use for them; the
+// kernel orders them with its own waits.  lds: the tile's LDS byte address.
+template <int RC>
+__device__ __forceinline__ void dma_pre_op(uint32_t lds, const bf16* g, const int (&off)[RC / 4], int w) {
+#pragma unroll
+  for (int i = 0; i < RC / 4; ++i)
+    dma_lds16(g, 2u * static_cast<uint32_t>(off[i]), lds + (static_cast<uint32_t>(w * (RC / 4) + i) << 10));
+}
+template <int RC, int (*F)(int)>
+__device__ __forceinline__ void dma_tile_op(uint32_t lds, const bf16* g, int grs, int rows_valid,
+                                            int w, int lane) {
+#pragma unroll
+  for (int i = 0; i < RC / 4; ++i) {
+    const int inst = w * (RC / 4) + i;
+    const int pos = inst * 64 + lane;
+    const int row = pos / RC, pc = pos % RC;
+    const int gr = row < rows_valid ? row : rows_valid - 1;
+    dma_lds16(g, 2u * static_cast<uint32_t>(gr * grs + 8 * (pc ^ (F(row) & (RC - 1)))),
+              lds + (static_cast<uint32_t>(inst) << 10));
+  }
+}
+
 // Lane offset (elements) for DMA instruction i of wave w into a swz_k128
 // [sigma][tau] plane of a dCB tile.  The source kernel stores a tile in lane
 // order: dCB[tau = 8 c .. 8 c + 7][sigma] of plane p (hi, lo), c = 4 ks + lg,
@@ -305,9 +328,10 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   constexpr int NT = N / 16;     // 16-row n tiles of dB^T
   static_assert(NH == 1 || NH == 2, "ssd_bwd_src: state_dim 64 or 128");
   static_assert(HS == 1 || HS == 2, "ssd_bwd_src: one or two heads per pass");
-  // Separate LDS objects per stage buffer: with the stage parity a
-  // compile-time constant, the compiler sees that the reads of one buffer do
-  // not depend on the DMA into the other and inserts no waits for it.
+  // One LDS object per stage buffer.  The DMA into them goes through
+  // dma_lds16, which the compiler does not see as an LDS write (with the
+  // builtin it held LDS accesses and load uses inside a stage until the next
+  // stage's DMA had landed); end_stage's wait and barrier order it.
   __shared__ __align__(16) bf16 stg0[SM::kStage];   // [hi, lo][64][64]
   __shared__ __align__(16) bf16 stg1[SM::kStage];
   __shared__ __align__(16) bf16 Cs0[SM::kC];        // [64][N]
@@ -317,6 +341,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   __shared__ __align__(16) float rx[2 * 4 * 64];     // [stage parity][4 waves][64] row sums
   auto stg = [&](int par) -> bf16* { return par ? stg1 : stg0; };
   auto Cs = [&](int par) -> bf16* { return par ? Cs1 : Cs0; };
+  const uint32_t l_stg0 = lds_addr(stg0), l_stg1 = lds_addr(stg1);
+  const uint32_t l_cs0 = lds_addr(Cs0), l_cs1 = lds_addr(Cs1);
 
   const int hpg = d.H / d.G;
   const int npass = (hpg + HS - 1) / HS;
@@ -454,34 +480,34 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 #pragma unroll
     for (int ks = 0; ks < NK; ++ks) Bh[ks] = sv ? load_v8bf(brow + 32 * ks) : zero_v8bf();
     auto issue = [&](int j, int par) {   // par: the stage's buffer
-      bf16* dst = stg(par);
+      const uint32_t dst = par ? l_stg1 : l_stg0;
       int gs[2], gy[2], gc[NK];
       lane_offsets(gs, gy, gc);
       if (j < nst) {
         const int k = KB + j;
         if (k < hpg) {
           const bf16* src = dSg + k * (2L * 64 * N);
-          bf16* cdst = Cs(state_cpar(j));
-          dma_pre<8>(dst, src, gs, w);
-          dma_pre<8>(dst + kPlaneT, src + 64L * N, gs, w);
+          const uint32_t cdst = state_cpar(j) ? l_cs1 : l_cs0;
+          dma_pre_op<8>(dst, src, gs, w);
+          dma_pre_op<8>(dst + 2 * kPlaneT, src + 64L * N, gs, w);
           if constexpr (NH == 2) {
-            dma_pre<8>(cdst, src + 64, gs, w);
-            dma_pre<8>(cdst + kPlaneT, src + 64 + 64L * N, gs, w);
+            dma_pre_op<8>(cdst, src + 64, gs, w);
+            dma_pre_op<8>(cdst + 2 * kPlaneT, src + 64 + 64L * N, gs, w);
           }
         }
       } else {
         const int qq = j - nst, Ti = qq / HS, h = qq % HS, T = S + Ti, k = KB + h;
         if (k < hpg) {
           const bf16* src = dyg + (static_cast<long>(T) * hpg + k) * (2L * kPlaneT);
-          dma_pre<8>(dst, src, gy, w);
-          dma_pre<8>(dst + kPlaneT, src + kPlaneT, gy, w);
+          dma_pre_op<8>(dst, src, gy, w);
+          dma_pre_op<8>(dst + 2 * kPlaneT, src + kPlaneT, gy, w);
         }
         if (h == 0) {
           const int t0 = 64 * T;
-          bf16* cdst = Cs((T - S) & 1);
+          const uint32_t cdst = ((T - S) & 1) ? l_cs1 : l_cs0;
           const bf16* csrc = Cc + static_cast<long>(t0) * act_rs;
-          if (qlim - t0 >= 64) dma_pre<NK * 4>(cdst, csrc, gc, w);
-          else dma_tile<NK * 4, swz_c<NK>>(cdst, csrc, act_rs, qlim - t0, w, lane);
+          if (qlim - t0 >= 64) dma_pre_op<NK * 4>(cdst, csrc, gc, w);
+          else dma_tile_op<NK * 4, swz_c<NK>>(cdst, csrc, act_rs, qlim - t0, w, lane);
           if (tid < HS * 64) {   // raw: nothing waits for these before the stage's end
             const int k2 = min(KB + (tid >> 6), hpg - 1);
             const float* dch = dcc + k2 * hstride + t0;
