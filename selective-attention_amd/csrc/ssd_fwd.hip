@@ -216,18 +216,21 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
     const int a_rs = d.H * d.P, x_rs = d.G * N;
     const bf16* xc = x_src + tok0 * x_rs + static_cast<long>(g) * N;
     const float dcl = dc[crow + d.Lc - 1] * kLog2e;
-    auto row_scale = [&](int t) __attribute__((always_inline)) {   // scale of row t (0 past klim)
-      const int tc = min(t, klim - 1);
-      float sc;
-      if constexpr (MODE == 0) sc = fast_exp2(fminf(dcl - dc[crow + tc] * kLog2e, 0.f)) * dt[crow + tc];
-      else sc = fast_exp2(dc[crow + tc] * kLog2e);
-      return t < klim ? sc : 0.f;
-    };
-    // prefetch registers
-    int slot_tile = 0;   // tile index held by the prefetch registers (dy planes)
+    // Prefetch registers.  A row's dc (and dt) are loaded with the tile and
+    // turned into its scale only at the commit: a use at load time would
+    // make the compiler wait there for the whole prefetch (loads complete in
+    // order), before the current tile's MFMAs.
+    int slot_tile = 0;   // tile index held by the prefetch registers
     uint4 pa0[MODE == 0 ? 2 : 1];
     float4 pa1[MODE == 1 ? 4 : 1];
-    float psc[2];
+    float pdc[2], pdt[2];   // dc, dt of the rows (clamped to klim - 1)
+    // scale of row t of the held tile from its dc, dt (0 past klim)
+    auto row_scale = [&](int t, float dcv, float dtv) __attribute__((always_inline)) {
+      float sc;
+      if constexpr (MODE == 0) sc = fast_exp2(fminf(dcl - dcv * kLog2e, 0.f)) * dtv;
+      else sc = fast_exp2(dcv * kLog2e);
+      return t < klim ? sc : 0.f;
+    };
     BfTile<NK, 256> px;
     auto load_tile = [&](int tt) __attribute__((always_inline)) {
       const int t0 = 64 * tt, kv = min(64, klim - t0);
@@ -238,7 +241,9 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
         for (int i = 0; i < 2; ++i) {
           const int e = tid + 256 * i, row = e >> 3;
           pa0[i] = *reinterpret_cast<const uint4*>(ac + static_cast<unsigned>((t0 + min(row, kv - 1)) * a_rs + 8 * (e & 7)));
-          psc[i] = row_scale(t0 + row);
+          const int tc = min(t0 + row, klim - 1);
+          pdc[i] = dc[crow + tc];
+          pdt[i] = dt[crow + tc];
         }
       } else {
         const float* ac = static_cast<const float*>(a_src) + tok0 * a_rs + h * d.P + p0;
@@ -246,7 +251,7 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
         const float* pp = ac + static_cast<unsigned>((t0 + min(row, kv - 1)) * a_rs + 16 * (tid & 3));
 #pragma unroll
         for (int i = 0; i < 4; ++i) pa1[i] = *reinterpret_cast<const float4*>(pp + 4 * i);
-        psc[0] = row_scale(t0 + row);
+        pdc[0] = dc[crow + min(t0 + row, klim - 1)];
       }
       px.load(xc + static_cast<long>(t0) * x_rs, x_rs, kv, tid);
     };
@@ -260,11 +265,12 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int e = tid + 256 * i, row = e >> 3;
+          const float sc = row_scale(64 * slot_tile + row, pdc[i], pdt[i]);
           const uint32_t q[4] = {pa0[i].x, pa0[i].y, pa0[i].z, pa0[i].w};
           uint32_t r[4], rl[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float v0 = bf16lo_to_f32(q[j]) * psc[i], v1 = bf16hi_to_f32(q[j]) * psc[i];
+            const float v0 = bf16lo_to_f32(q[j]) * sc, v1 = bf16hi_to_f32(q[j]) * sc;
             r[j] = pack_bf16x2(v0, v1);
             rl[j] = pack_bf16x2(v0 - bf16lo_to_f32(r[j]), v1 - bf16hi_to_f32(r[j]));
           }
@@ -274,8 +280,31 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
         }
       } else {
         const int row = tid >> 2, c0 = 16 * (tid & 3);
+        const float sc = row_scale(64 * slot_tile + row, pdc[0], 0.f);
+        uint32_t hi[8], lo[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v[4] = {pa1[i].x * sc, pa1[i].y * sc, pa1[i].z * sc, pa1[i].w * sc};
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const uint32_t hh = pack_bf16x2(v[2 * j], v[2 * j + 1]);
+            hi[2 * i + j] = hh;
+            lo[2 * i + j] = pack_bf16x2(v[2 * j] - bf16lo_to_f32(hh), v[2 * j + 1] - bf16hi_to_f32(hh));
+          }
+        }
+        const int ao0 = TA::off(row, c0), ao1 = TA::off(row, c0 + 8);
+        *reinterpret_cast<uint4*>(As + ao0) = uint4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<uint4*>(As + ao1) = uint4{hi[4], hi[5], hi[6], hi[7]};
+        *reinterpret_cast<uint4*>(As + PLA + ao0) = uint4{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<uint4*>(As + PLA + ao1) = uint4{lo[4], lo[5], lo[6], lo[7]};
+      }
+      commit_lds(px, Xs, tid);
+      if constexpr (MODE == 1) {
         if (dyp) {
-          // the unscaled tile rows as planes (zero rows past the length)
+          // the unscaled tile rows as planes (zero rows past the length),
+          // stored after the tile's loads are used: the compiler would
+          // otherwise wait for these stores before those uses
+          const int row = tid >> 2, c0 = 16 * (tid & 3);
           const int tt = slot_tile;
           const bool in = 64 * tt + row < klim;
           uint32_t uh[8], ul[8];
@@ -300,24 +329,7 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
           pl[0] = uint4{ul[0], ul[1], ul[2], ul[3]};
           pl[1] = uint4{ul[4], ul[5], ul[6], ul[7]};
         }
-        uint32_t hi[8], lo[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float v[4] = {pa1[i].x * psc[0], pa1[i].y * psc[0], pa1[i].z * psc[0], pa1[i].w * psc[0]};
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const uint32_t hh = pack_bf16x2(v[2 * j], v[2 * j + 1]);
-            hi[2 * i + j] = hh;
-            lo[2 * i + j] = pack_bf16x2(v[2 * j] - bf16lo_to_f32(hh), v[2 * j + 1] - bf16hi_to_f32(hh));
-          }
-        }
-        const int ao0 = TA::off(row, c0), ao1 = TA::off(row, c0 + 8);
-        *reinterpret_cast<uint4*>(As + ao0) = uint4{hi[0], hi[1], hi[2], hi[3]};
-        *reinterpret_cast<uint4*>(As + ao1) = uint4{hi[4], hi[5], hi[6], hi[7]};
-        *reinterpret_cast<uint4*>(As + PLA + ao0) = uint4{lo[0], lo[1], lo[2], lo[3]};
-        *reinterpret_cast<uint4*>(As + PLA + ao1) = uint4{lo[4], lo[5], lo[6], lo[7]};
       }
-      commit_lds(px, Xs, tid);
     };
 
     const int ntt = (klim + 63) / 64;
