@@ -540,18 +540,39 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
       }
     };
 
-    // u rows of this pass' heads: held for the whole pass by the first pass;
-    // the others (which hold the running dCB sum or finish dB) have no
-    // registers to spare and load them per stage
+    // u rows of this pass' heads: held for the whole pass by the first pass.
+    // The others (which hold the running dCB sum or finish dB) have no
+    // registers to spare: they hold the u row of one head (un), the one the
+    // next stage needs (stages walk the pass' heads in turn, starting with
+    // KB), reloaded in each stage once that stage's last use of it is done,
+    // so that no stage waits on a load (which would also wait for the DMA
+    // issued before it).  Rows past the length are zeroed where used.  A
+    // stage of an absent head (KB + h >= hpg, only h = 1 with KB = hpg - 1)
+    // loads nothing: un then holds head hpg - 1 = KB, what the next stage
+    // (head KB) needs.
     constexpr bool kHold = first && !last;
     v8bf Uh[HS][2];
+    v8bf un[2];
+    auto load_un = [&](int h) {   // u row of head KB + h (clamped to a valid head)
+      const bf16* urow = uc + min(KB + h, hpg - 1) * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
 #pragma unroll
-    for (int h = 0; h < HS; ++h) {
-      const int k = KB + h;
-      const bf16* urow = uc + min(k, hpg - 1) * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
+      for (int ks = 0; ks < 2; ++ks) un[ks] = load_v8bf(urow + 32 * ks);
+    };
+    auto use_un = [&](v8bf (&f)[2]) {
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        Uh[h][ks] = kHold && sv && k < hpg ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+      for (int ks = 0; ks < 2; ++ks) f[ks] = sv ? un[ks] : zero_v8bf();
+    };
+    if constexpr (kHold) {
+#pragma unroll
+      for (int h = 0; h < HS; ++h) {
+        const int k = KB + h;
+        const bf16* urow = uc + min(k, hpg - 1) * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          Uh[h][ks] = sv && k < hpg ? load_v8bf(urow + 32 * ks) : zero_v8bf();
+      }
+    } else {
+      load_un(0);
     }
     issue(0, nst & 1);   // stage j has buffer parity (j + nst) & 1
     wait_all_mem();
@@ -606,12 +627,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         const int j = h, par = (h + HS) & 1;
         v8bf ul[2] = {Uh[h][0], Uh[h][1]};
         uint2 ux[4];    // u of head k at this lane's column, for x_B
-        if (kv && !kHold) {
-          const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) ul[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
-        }
-        __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the DMA
+        if constexpr (!kHold) use_un(ul);
         issue_next(j, par);
         if (kv) {
 #pragma unroll
@@ -632,6 +648,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
                 duT[h][pt] = mfma_bf16(load_v8bf(Yl + off), Bh[2 * half + ks], duT[h][pt]);
               }
             state_dB(Yh, ul, ekh[h] * dtk[h], half);
+            // the next stage's u row (the next head of the pass)
+            if (!kHold && half == NH - 1) load_un((h + 1) % HS);
             __builtin_amdgcn_sched_barrier(0);   // the halves' operand reads stay apart
           }
           // head k's state part is complete: scale by e^{dc_last - dc_sig}; x_B
@@ -712,14 +730,8 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         const int k = KB + h;
         const bool kv = k < hpg;
         const int par = HS == 1 ? (Ti & 1) : h;
-        // register loads of this stage, before the next stage's DMA
         v8bf uf[2] = {Uh[h][0], Uh[h][1]};
-        if (!kHold && kv) {
-          const bf16* urow = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 8 * lg);
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) uf[ks] = sv ? load_v8bf(urow + 32 * ks) : zero_v8bf();
-        }
-        __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the DMA
+        if constexpr (!kHold) use_un(uf);
         // with one head per pass, the next stage brings the C tile of strip
         // T + 1 into the buffer finish_pair(T - 1) reads: finish it first
         if (HS == 1 && Ti > 0) {
@@ -762,6 +774,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
             for (int kt = 0; kt < 4; ++kt) W[kt] = mfma_bf16(f[kt], uf[ks], W[kt]);
             __builtin_amdgcn_sched_barrier(0);   // bound the operand reads in flight
           }
+          if constexpr (!kHold) load_un((h + 1) % HS);   // the next stage's u row
           // decay and masks: dCB += W', M = W' o CB (q: column sums, r: row sums); W <- L
           float m[16];
           float qs = 0.f;
