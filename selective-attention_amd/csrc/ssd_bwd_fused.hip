@@ -574,6 +574,18 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     } else {
       load_un(0);
     }
+    // this pass' dc and dt at the source row and dc at the chunk end: loaded
+    // ahead of the first stage's DMA and landed by its wait (a load used in
+    // a stage waits for the DMA issued before it as well)
+    float dcr[HS], dtr[HS], dcl[HS];
+#pragma unroll
+    for (int h = 0; h < HS; ++h) {
+      const int k = min(KB + h, hpg - 1);
+      dcr[h] = dcc[k * hstride + scl];
+      dtr[h] = dtc[k * hstride + scl];
+      dcl[h] = dcc[k * hstride + d.Lc - 1];
+    }
+    asm volatile("" ::: "memory");   // the loads stay ahead of the wait
     issue(0, nst & 1);   // stage j has buffer parity (j + nst) & 1
     wait_all_mem();
     __syncthreads();
@@ -582,11 +594,10 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     float qacc[HS], dtk[HS], dck[HS], ekh[HS];
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
-      const int k = min(KB + h, hpg - 1);
-      dck[h] = dcc[k * hstride + scl] * kLog2e;
-      dtk[h] = sv ? dtc[k * hstride + scl] : 0.f;
+      dck[h] = dcr[h] * kLog2e;
+      dtk[h] = sv ? dtr[h] : 0.f;
       // e^{min(dc_last - dc_sig, 0)}: the state weight is ekh dt
-      ekh[h] = fast_exp2(fminf(dcc[k * hstride + d.Lc - 1] * kLog2e - dck[h], 0.f));
+      ekh[h] = fast_exp2(fminf(dcl[h] * kLog2e - dck[h], 0.f));
       qacc[h] = 0.f;
 #pragma unroll
       for (int pt = 0; pt < 4; ++pt) duT[h][pt] = v4f{0.f, 0.f, 0.f, 0.f};
