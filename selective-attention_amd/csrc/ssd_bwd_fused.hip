@@ -63,25 +63,6 @@ __device__ __forceinline__ int toff(int row, int col) {
   return row * (RC * 8) + 8 * ((col >> 3) ^ (F(row) & (RC - 1))) + (col & 7);
 }
 
-// 64 rows x RC chunks of bf16 from global (row stride grs elements; rows past
-// rows_valid repeat row rows_valid - 1) into a swizzled LDS tile; the 4 waves
-// of the block share the copy, one 1 KB DMA instruction per 64 chunks
-template <int RC, int (*F)(int)>
-__device__ __forceinline__ void dma_tile(bf16* lds, const bf16* g, long grs, int rows_valid,
-                                         int w, int lane) {
-  constexpr int NI = RC;          // 64 * RC chunks / 64 per instruction
-  constexpr int PW = NI / 4;
-#pragma unroll
-  for (int i = 0; i < PW; ++i) {
-    const int inst = w * PW + i;
-    const int pos = inst * 64 + lane;
-    const int row = pos / RC, pc = pos % RC;
-    const int gr = row < rows_valid ? row : rows_valid - 1;
-    __builtin_amdgcn_global_load_lds(g + gr * grs + 8 * (pc ^ (F(row) & (RC - 1))),
-                                     lds + inst * 512, 16, 0, 0);
-  }
-}
-
 // lane offset (elements, row stride grs) of DMA instruction i of wave w for a
 // 64-row swizzled tile with RC chunks per row
 template <int RC, int (*F)(int)>
@@ -91,45 +72,12 @@ __device__ __forceinline__ int dma_off(int i, int w, int lane, int grs) {
   const int row = pos / RC, pc = pos % RC;
   return row * grs + 8 * (pc ^ (F(row) & (RC - 1)));
 }
-// the tile copy of dma_tile with precomputed lane offsets (full tiles)
-template <int RC>
-__device__ __forceinline__ void dma_pre(bf16* lds, const bf16* g, const int (&off)[RC / 4], int w) {
-#pragma unroll
-  for (int i = 0; i < RC / 4; ++i)
-    __builtin_amdgcn_global_load_lds(g + static_cast<unsigned>(off[i]), lds + (w * (RC / 4) + i) * 512, 16, 0, 0);
-}
-
-// the same for a tile copied by 8 waves (RC / 8 instructions each)
-template <int RC>
-__device__ __forceinline__ void dma_pre_w8(bf16* lds, const bf16* g, const int (&off)[RC / 8], int w) {
-#pragma unroll
-  for (int i = 0; i < RC / 8; ++i)
-    __builtin_amdgcn_global_load_lds(g + static_cast<unsigned>(off[i]), lds + (w * (RC / 8) + i) * 512, 16, 0, 0);
-}
-// 8-wave copy of a partial tile: rows past rows_valid repeat row rows_valid - 1
-template <int RC, int (*F)(int)>
-__device__ __forceinline__ void dma_part_w8(bf16* lds, const bf16* g, long grs, int rows_valid,
-                                            int w, int lane) {
-#pragma unroll
-  for (int i = 0; i < RC / 8; ++i) {
-    const int inst = w * (RC / 8) + i, pos = inst * 64 + lane;
-    const int row = pos / RC, pc = pos % RC;
-    const int gr = row < rows_valid ? row : rows_valid - 1;
-    __builtin_amdgcn_global_load_lds(g + gr * grs + 8 * (pc ^ (F(row) & (RC - 1))),
-                                     lds + inst * 512, 16, 0, 0);
-  }
-}
-// lane offset of 8-wave DMA instruction i of wave w (RC chunks per row)
-template <int RC, int (*F)(int)>
-__device__ __forceinline__ int dma_off_w8(int i, int w, int lane, int grs) {
-  const int inst = w * (RC / 8) + i, pos = inst * 64 + lane;
-  const int row = pos / RC, pc = pos % RC;
-  return row * grs + 8 * (pc ^ (F(row) & (RC - 1)));
-}
-
-// The same copies through dma_lds16 (common.h), which the compiler does not
-// see as LDS writes, so it holds no LDS access or load use for them; the
-// kernel orders them with its own waits.  lds: the tile's LDS byte address.
+// Tile copies into LDS through dma_lds16 (common.h), which the compiler does
+// not see as LDS writes, so it holds no LDS access or load use for them; the
+// kernels order them with their own waits.  lds: the tile's LDS byte
+// address; the 4 waves of a block share a copy, one 1 KB DMA instruction per
+// 64 chunks.  dma_pre_op: a full 64-row tile from per-lane element offsets
+// (dma_off); dma_tile_op: rows past rows_valid repeat row rows_valid - 1.
 template <int RC>
 __device__ __forceinline__ void dma_pre_op(uint32_t lds, const bf16* g, const int (&off)[RC / 4], int w) {
 #pragma unroll
