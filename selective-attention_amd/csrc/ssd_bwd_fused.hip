@@ -526,12 +526,16 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
     // ahead of the first stage's DMA and landed by its wait (a load used in
     // a stage waits for the DMA issued before it as well)
     float dcr[HS], dtr[HS], dcl[HS];
+    uint2 uxh[HS][4];   // u of head KB + h at this lane's column, for x_B
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
       const int k = min(KB + h, hpg - 1);
       dcr[h] = dcc[k * hstride + scl];
       dtr[h] = dtc[k * hstride + scl];
       dcl[h] = dcc[k * hstride + d.Lc - 1];
+      const bf16* urow4 = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) uxh[h][pt] = *reinterpret_cast<const uint2*>(urow4 + 16 * pt);
     }
     asm volatile("" ::: "memory");   // the loads stay ahead of the wait
     issue(0, nst & 1);   // stage j has buffer parity (j + nst) & 1
@@ -585,17 +589,11 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
         const bool kv = k < hpg;
         const int j = h, par = (h + HS) & 1;
         v8bf ul[2] = {Uh[h][0], Uh[h][1]};
-        uint2 ux[4];    // u of head k at this lane's column, for x_B
         if constexpr (!kHold) use_un(ul);
         issue_next(j, par);
         if (kv) {
 #pragma unroll
           for (int half = 0; half < NH; ++half) {
-            if (half == NH - 1) {   // read under the last half's MFMAs
-              const bf16* urow4 = uc + k * 64 + static_cast<unsigned>(scl * u_rs + 4 * lg);
-#pragma unroll
-              for (int pt = 0; pt < 4; ++pt) ux[pt] = *reinterpret_cast<const uint2*>(urow4 + 16 * pt);
-            }
             const bf16* Yh = half ? Cs(state_cpar(j)) : stg(par);
             const bf16* Yl = Yh + kPlaneT;
 #pragma unroll
@@ -617,7 +615,7 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
 #pragma unroll
           for (int pt = 0; pt < 4; ++pt) {
             duT[h][pt] *= ek;
-            sx += dot4_bf16(duT[h][pt], ux[pt]);
+            sx += dot4_bf16(duT[h][pt], uxh[h][pt]);
           }
           sx = group_sum(sv ? sx : 0.f) * dtk[h];
           if (lg == 0) xBc[k * hstride + sig] = sx;
