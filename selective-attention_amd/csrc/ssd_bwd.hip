@@ -736,7 +736,24 @@ __device__ __forceinline__ float block_sum(float v, float* wtot) {
   return s;
 }
 
-template <typename T>
+// sum over k < n of base[k * stride], added in order k = 0, 1, ...: the
+// first M loads are issued together (clamped to a valid k) before any is
+// used; a loop that adds each load before the next is issued waits a memory
+// round trip per term
+template <int M>
+__device__ __forceinline__ float sum_parts(const float* base, long stride, int n) {   // n >= 1
+  float v[M];
+#pragma unroll
+  for (int k = 0; k < M; ++k) v[k] = base[static_cast<long>(min(k, n - 1)) * stride];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < M; ++k) s += k < n ? v[k] : 0.f;
+  for (int k = M; k < n; ++k) s += base[static_cast<long>(k) * stride];
+  return s;
+}
+
+// PER: positions per thread, (Lc + 255) / 256
+template <typename T, int PER>
 __global__ __launch_bounds__(256) void chunk_cumsum_bwd_kernel(
     const T* __restrict__ delta_raw, const float* __restrict__ A,
     const float* __restrict__ delta_bias, const int64_t* __restrict__ length,
@@ -755,44 +772,43 @@ __global__ __launch_bounds__(256) void chunk_cumsum_bwd_kernel(
   const int len = seq_limit(length, b, d.L);
   const int lim = chunk_limit(len, c, d.Lc);
   const int qlim = min(d.Lc, d.L - c * d.Lc);
-  const int per = (d.Lc + 255) / 256;
-  const int tb = threadIdx.x * per;
+  const int tb = threadIdx.x * PER;
 
   // every global load is issued here, ahead of the block reductions (a
   // barrier orders memory, so loads placed after one wait for it)
   float ddc = 0.f;
   for (int k = threadIdx.x; k < per_bh; k += 256) ddc += ddc_part[bhc * per_bh + k];
-  float qr[4], xb[4], xc[4], zv[4], dtv[4], ddtd[4];
+  // loads from clamped (valid) positions, unconditionally, so that they are
+  // all in flight together; positions past Lc, qlim or lim are masked after
+  float qr[PER], xb[PER], xc[PER], zv[PER], dtv[PER], ddtd[PER];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    qr[j] = xb[j] = xc[j] = zv[j] = dtv[j] = ddtd[j] = 0.f;
+  for (int j = 0; j < PER; ++j) {
     const int t = tb + j;
-    if (j < per && t < d.Lc) {
-      float q = 0.f, x1 = 0.f, x2 = 0.f;
-      for (int k = 0; k < ttiles; ++k) q += qpart[(bhc * ttiles + k) * d.Lc + t];
-      for (int k = 0; k < ntiles; ++k) x1 += xB_part[(bhc * ntiles + k) * d.Lc + t];
-      for (int k = 0; k < xctiles; ++k) x2 += xC_part[(bhc * xctiles + k) * d.Lc + t];
-      // row sums: partials of the source tiles k <= t / 64 (rtiles == 1: complete)
-      float r = 0.f;
-      for (int k = 0; k < rtiles && 64 * k <= t; ++k) r += rsum[(bhc * rtiles + k) * d.Lc + t];
-      qr[j] = q - r;
-      xb[j] = t < lim - 1 ? x1 : 0.f;
-      xc[j] = t < lim ? x2 : 0.f;
-      if (t < lim) {
-        const long off = (static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc + t) * d.H + h;
-        zv[j] = load_f32(delta_raw + off);
-        dtv[j] = dt[crow + t];
-        for (int k = 0; k < ptiles; ++k) ddtd[j] += ddt_part[(bhc * ptiles + k) * d.Lc + t];
-      }
-    }
+    const int tl = min(t, d.Lc - 1), tq = min(t, qlim - 1);
+    const float q = sum_parts<4>(qpart + bhc * ttiles * d.Lc + tl, d.Lc, ttiles);
+    const float x1 = sum_parts<2>(xB_part + bhc * ntiles * d.Lc + tl, d.Lc, ntiles);
+    const float x2 = sum_parts<2>(xC_part + bhc * xctiles * d.Lc + tl, d.Lc, xctiles);
+    // row sums: partials of the source tiles k <= t / 64 (rtiles == 1: complete)
+    const float r = sum_parts<4>(rsum + bhc * rtiles * d.Lc + tl, d.Lc, min(rtiles, tl / 64 + 1));
+    const long off = (static_cast<long>(b) * d.L + static_cast<long>(c) * d.Lc + tq) * d.H + h;
+    const float z = load_f32(delta_raw + off);
+    const float dtt = dt[crow + tl];
+    const float dd = sum_parts<2>(ddt_part + bhc * ptiles * d.Lc + tl, d.Lc, ptiles);
+    const bool tv = t < d.Lc, tin = tv && t < lim;
+    qr[j] = tv ? q - r : 0.f;
+    xb[j] = tv && t < lim - 1 ? x1 : 0.f;
+    xc[j] = tin ? x2 : 0.f;
+    zv[j] = tin ? z : 0.f;
+    dtv[j] = tin ? dtt : 0.f;
+    ddtd[j] = tin ? dd : 0.f;
   }
   // ddc_last of this chunk (sum of the state-passing partials)
   ddc = block_sum(ddc, wtot);
   if (!has_init && c == 0) ddc = 0.f;
   float sqr = 0.f, sxb = 0.f, sxc = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (j < per && tb + j == d.Lc - 1) xc[j] += ddc;
+  for (int j = 0; j < PER; ++j) {
+    if (tb + j == d.Lc - 1) xc[j] += ddc;
     sqr += qr[j];
     sxb += xb[j];
     sxc += xc[j];
@@ -805,9 +821,9 @@ __global__ __launch_bounds__(256) void chunk_cumsum_bwd_kernel(
   float rq = eq, rb = eb, rc = ec;
   float dA_loc = 0.f, db_loc = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int t = tb + j;
-    if (j < per && t < d.Lc) {
+    if (t < d.Lc) {
       const float dA_intra = rq, dA_B = rb, dA_C = tc - rc;  // exclusive, exclusive, suffix
       rq += qr[j];
       rb += xb[j];
@@ -978,7 +994,12 @@ int ssd_bwd_impl(const void* u_, const float* A, const void* B_, const void* C_,
   {
     const long blocks = bnc * d.H;
     ProfScope prof_("chunk_cumsum_bwd", s);
-    hipLaunchKernelGGL(chunk_cumsum_bwd_kernel<T>, dim3(blocks), dim3(256), 0, s,
+    const int per = (d.Lc + 255) / 256;   // 1..4: chunk sizes are validated to [1, 1024]
+    auto kernel = per <= 1 ? chunk_cumsum_bwd_kernel<T, 1>
+                  : per == 2 ? chunk_cumsum_bwd_kernel<T, 2>
+                  : per == 3 ? chunk_cumsum_bwd_kernel<T, 3>
+                             : chunk_cumsum_bwd_kernel<T, 4>;
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), 0, s,
                        static_cast<const T*>(delta_raw_), A, bias, length, dt, ddt_part, xB_part,
                        xC_part, rsum, qpart, ddc_part, static_cast<T*>(ddelta_), dA_part, db_part,
                        d, ptiles, ntiles, xctiles, qtiles, rtiles, w.per_bh, has_init, sp, lo, hi);
