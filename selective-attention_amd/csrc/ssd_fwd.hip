@@ -523,7 +523,11 @@ __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
     for (int i = 0; i < 2; ++i) {
       const int row = (tid + 256 * i) >> 3;
       const uint4 q = *reinterpret_cast<const uint4*>(sb + ao[i]);
-      const float sc = row < qv ? fast_exp2(fminf(dcl - rdc[row] * kLog2e, 0.f)) * rdt[row] : 0.f;
+      // rows past the chunk hold copies of its last row (finite): the scale is
+      // computed in every lane and masked by a select, not a branch
+      float sc = fast_exp2(fminf(dcl - rdc[row] * kLog2e, 0.f)) * rdt[row];
+      asm volatile("" : "+v"(sc));
+      sc = row < qv ? sc : 0.f;
       const uint32_t v[4] = {q.x, q.y, q.z, q.w};
       uint32_t r[4], rl[4];
 #pragma unroll
@@ -900,7 +904,11 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
   // ---- sigma-tile staging (registers -> LDS) ----
   uint4 pb[NK];
   uint4 pu[HC][2];
+  // raw dc / dt of the tile: the scaling and masking wait for commit_tile,
+  // since arithmetic on a value right after its load waits for every load
+  // issued before it (the tile's whole prefetch)
   float pdc = 0.f, pdt = 0.f, pdc0 = 0.f;
+  bool pdt_ok = false;
   auto load_tile = [&](int s) {
     const int s0 = 64 * s, sv = min(64, qlim - s0);
 #pragma unroll
@@ -924,10 +932,10 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
     {
       const int k = tid >> 6, sig = s0 + (tid & 63);
       const float* dch = dc + crow0 + min(k, nh - 1) * hrow;
-      pdc = dch[min(sig, d.Lc - 1)] * kLog2e;
-      pdc0 = dch[t0] * kLog2e;
+      pdc = dch[min(sig, d.Lc - 1)];
+      pdc0 = dch[t0];
       pdt = dt[crow0 + min(k, nh - 1) * hrow + min(sig, d.Lc - 1)];
-      if (sig >= qlim || k >= nh) pdt = 0.f;
+      pdt_ok = sig < qlim && k < nh;
     }
   };
   auto commit_tile = [&]() {
@@ -944,10 +952,14 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
         const int e = tid + 256 * i;
         *reinterpret_cast<uint4*>(Us + k * PLU + TU::off(e >> 3, 8 * (e & 7))) = pu[k][i];
       }
-    if (tid < HC * 64) {
-      dcd[tid] = pdc;
-      dtd[tid] = pdt;
-      tab[tid] = pdt * fast_exp2(fminf(pdc0 - pdc, 0.f));
+    // with four heads every thread writes (a compile-time true condition:
+    // under a runtime one the compiler moved the dc / dt loads of load_tile
+    // into this branch, after the tile's MFMAs)
+    if (HC * 64 >= 256 || tid < HC * 64) {
+      const float c = pdc * kLog2e, t = pdt_ok ? pdt : 0.f;
+      dcd[tid] = c;
+      dtd[tid] = t;
+      tab[tid] = t * fast_exp2(fminf(pdc0 * kLog2e - c, 0.f));
     }
   };
 
@@ -961,26 +973,30 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
       const int e = tid + 256 * i;
       const int row = e / (N / 4), c4 = e % (N / 4);
       ph[i] = *reinterpret_cast<const float4*>(Hb + static_cast<unsigned>(min(row, d.P - p0 - 1) * N + 4 * c4));
-      if (p0 + row >= d.P) ph[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
+  // rows past P are zeroed here, not in load_h: a select right after the load
+  // would wait for it there, before the MFMAs it is meant to overlap
   auto commit_h = [&]() {
 #pragma unroll
     for (int i = 0; i < HQ; ++i) {
       const int e = tid + 256 * i;
       const int row = e / (N / 4), c4 = e % (N / 4);
-      *reinterpret_cast<uint2*>(Hs + TB::off(row, 4 * c4)) =
-          uint2{pack_bf16x2(ph[i].x, ph[i].y), pack_bf16x2(ph[i].z, ph[i].w)};
+      const uint2 v = uint2{pack_bf16x2(ph[i].x, ph[i].y), pack_bf16x2(ph[i].z, ph[i].w)};
+      *reinterpret_cast<uint2*>(Hs + TB::off(row, 4 * c4)) = p0 + row < d.P ? v : uint2{0u, 0u};
     }
   };
   load_tile(0);
   commit_tile();
   __syncthreads();
   // one sigma tile: C.B^T, decay, Y^T += U^T S^T for every head
-  auto sigma_tile = [&](int s, bool diag) __attribute__((always_inline)) {
+  // DIAG and FACT are compile-time, so that the decay of a tile is straight-line
+  // code (a runtime choice per element row put a branch and an LDS wait
+  // around every four products)
+  auto sigma_tile = [&](int s, auto diag_c, auto fact_c) __attribute__((always_inline)) {
+    constexpr bool DIAG = decltype(diag_c)::value, FACT = decltype(fact_c)::value;
     const int s0 = 64 * s;
-    const bool fact = mono && !diag;
-    if (mono && diag) {
+    if (DIAG && mono) {
 #pragma unroll
       for (int k = 0; k < HC; ++k)
 #pragma unroll
@@ -1001,14 +1017,14 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
       __builtin_amdgcn_sched_barrier(0);
       cbt[kt] = mfma_bf16(bf, Cw[ks], cbt[kt]);
     }
+    // every head slot runs, also past nh: its U tile and dt are zero
 #pragma unroll
     for (int k = 0; k < HC; ++k) {
-      if (k >= nh) break;
       v4f sk[4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         const int tb = 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1);   // 4 consecutive sigma rows
-        if (fact) {
+        if constexpr (FACT) {
           const float4 tq = *reinterpret_cast<const float4*>(tab + k * 64 + tb);
           sk[kt] = cbt[kt] * v4f{tq.x, tq.y, tq.z, tq.w};
         } else {
@@ -1017,8 +1033,15 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
           const float dv[4] = {dq.x, dq.y, dq.z, dq.w}, tv[4] = {tq.x, tq.y, tq.z, tq.w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float e = fast_exp2(fminf(dct[k] - dv[i], 0.f)) * tv[i];
-            sk[kt][i] = s0 + tb + i <= tau ? cbt[kt][i] * e : 0.f;
+            float e = fast_exp2(fminf(dct[k] - dv[i], 0.f)) * tv[i];
+            if constexpr (DIAG) {
+              // e computed in every lane (the compiler would otherwise branch
+              // around it per element) and the mask taken as a select
+              asm volatile("" : "+v"(e));
+              sk[kt][i] = s0 + tb + i <= tau ? cbt[kt][i] * e : 0.f;
+            } else {
+              sk[kt][i] = cbt[kt][i] * e;   // sigma < t0 <= tau
+            }
           }
         }
       }
@@ -1032,18 +1055,22 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
       }
     }
   };
-  for (int s = 0; s < ti; ++s) {
-    load_tile(s + 1);
-    sigma_tile(s, false);
-    __syncthreads();  // every wave is done with this tile
-    commit_tile();
-    __syncthreads();
-  }
+  auto below_diag = [&](auto fact_c) __attribute__((always_inline)) {
+    for (int s = 0; s < ti; ++s) {
+      load_tile(s + 1);
+      sigma_tile(s, std::false_type{}, fact_c);
+      __syncthreads();  // every wave is done with this tile
+      commit_tile();
+      __syncthreads();
+    }
+  };
+  if (mono) below_diag(std::true_type{});
+  else below_diag(std::false_type{});
   // the diagonal tile prefetches the first head's H_in instead (when its
   // registers fit beside the tile's: state_dim <= 192)
   constexpr bool kEarlyH = NK <= 6;
   if constexpr (kEarlyH) load_h(0);
-  sigma_tile(ti, true);
+  sigma_tile(ti, std::true_type{}, std::false_type{});
   __syncthreads();
   if constexpr (!kEarlyH) load_h(0);
 
