@@ -1074,7 +1074,20 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
   __syncthreads();
   if constexpr (!kEarlyH) load_h(0);
 
-  // ---- state contribution exp(dc_tau) * H_in . C^T, one head per stage, then the store ----
+  // ---- state contribution exp(dc_tau) * H_in . C^T, one head per stage ----
+  // Without the gate epilogue, the y rows of head k leave through LDS as soon
+  // as its state part is added, so that their stores overlap the next head's
+  // stage: lane pieces in at 16-byte chunk c ^ (row % 16) of [64 rows][64 p]
+  // fp32, then whole 256-byte rows out, 16 bytes per lane (stored from the
+  // fragments, one instruction wrote 64 bytes of each of 16 rows).  The
+  // staging is the B tile's space when that holds 16 KB, else the U region
+  // past the H_in tile; either is disjoint from H_in.
+  constexpr int kHsBytes = static_cast<int>(sizeof(bf16)) * 64 * TB::kLd;
+  constexpr int kYsOff = kHsBytes >= 64 * 64 * 4 ? 0 : 2 * kHsBytes;
+  static_assert(kYsOff + 64 * 64 * 4 <= static_cast<int>(sizeof(bf16)) * (64 * TB::kLd + UREG),
+                "chunk_scan_fwd: the y staging fits in the tile region");
+  float* ys = reinterpret_cast<float*>(smem_raw + kYsOff);
+  const int rl = 16 * w + cl;
   commit_h();
   __syncthreads();
 #pragma unroll
@@ -1100,54 +1113,38 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[k][t] += st[t] * e;
     }
-    if (more) {
+    if constexpr (!GATED) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        *reinterpret_cast<float4*>(ys + rl * 64 + 4 * ((4 * t + lg) ^ (rl & 15))) =
+            make_float4(acc[k][t][0], acc[k][t][1], acc[k][t][2], acc[k][t][3]);
+      __syncthreads();   // head k's rows staged; every wave is done with its H_in tile
+      if (more) commit_h();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e2 = tid + 256 * i, r = e2 >> 4, ch = e2 & 15;
+        if (t0 + r < qlim && p0 + 4 * ch < d.P)
+          *reinterpret_cast<float4*>(y + (tok0 + t0 + r) * u_rs + static_cast<long>(h0 + k) * d.P + p0 + 4 * ch) =
+              *reinterpret_cast<const float4*>(ys + r * 64 + 4 * (ch ^ (r & 15)));
+      }
+      if (more) __syncthreads();   // the next H_in tile is in; the staging is free
+    } else if (more) {
       __syncthreads();
       commit_h();
       __syncthreads();
     }
   }
-  if constexpr (!GATED) {
-    // y leaves through LDS, two heads per round: lane pieces in at 16-byte
-    // chunk c ^ (row % 16) of [2][64 rows][64 p] fp32, then whole 256-byte
-    // rows out, 16 bytes per lane (stored from the fragments, one
-    // instruction wrote 64 bytes of each of 16 rows)
-    float* ys = reinterpret_cast<float*>(smem_raw);
-    static_assert(2 * 64 * 64 * sizeof(float) <= sizeof(bf16) * (64 * TB::kLd + UREG),
-                  "chunk_scan_fwd: the y staging fits in the tile region");
-    const int rl = 16 * w + cl;
+  if constexpr (GATED) {
+    if (tau < qlim) {
+      // SSM epilogue: yd = y + D u, out = yd silu(gate) (bf16; y itself is not stored)
 #pragma unroll
-    for (int r2 = 0; r2 < (HC + 1) / 2; ++r2) {
-      __syncthreads();   // every wave is done with the LDS (last stage, previous round)
+      for (int k = 0; k < HC; ++k) {
+        if (k >= nh) break;
+        const long row = (tok0 + tau) * u_rs + static_cast<long>(h0 + k) * d.P;
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const int k = 2 * r2 + s2;
-        if (k >= HC) break;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          *reinterpret_cast<float4*>(ys + s2 * 4096 + rl * 64 + 4 * ((4 * t + lg) ^ (rl & 15))) =
-              make_float4(acc[k][t][0], acc[k][t][1], acc[k][t][2], acc[k][t][3]);
-      }
-      __syncthreads();
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int e = tid + 256 * i, s2 = e >> 10, r = (e >> 4) & 63, ch = e & 15;
-        const int k = 2 * r2 + s2;
-        if (k < nh && t0 + r < qlim && p0 + 4 * ch < d.P)
-          *reinterpret_cast<float4*>(y + (tok0 + t0 + r) * u_rs + static_cast<long>(h0 + k) * d.P + p0 + 4 * ch) =
-              *reinterpret_cast<const float4*>(ys + s2 * 4096 + r * 64 + 4 * (ch ^ (r & 15)));
-      }
-    }
-  } else if (tau < qlim) {
-#pragma unroll
-    for (int k = 0; k < HC; ++k) {
-      if (k >= nh) break;
-      const long row = (tok0 + tau) * u_rs + static_cast<long>(h0 + k) * d.P;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int p = p0 + 16 * t + 4 * lg;
-        if (p >= d.P) continue;
-        if constexpr (GATED) {
-          // SSM epilogue: yd = y + D u, out = yd silu(gate) (bf16; y itself is not stored)
+        for (int t = 0; t < 4; ++t) {
+          const int p = p0 + 16 * t + 4 * lg;
+          if (p >= d.P) continue;
           const uint2 uq = *reinterpret_cast<const uint2*>(u + row + p);
           const uint2 gq = *reinterpret_cast<const uint2*>(go.gate + row + p);
           const float4 dq = *reinterpret_cast<const float4*>(go.D + (h0 + k) * d.P + p);
