@@ -158,6 +158,17 @@ __global__ __launch_bounds__(256) void chunk_outer_kernel(
       }
 }
 
+// Two bf16 values (one 32-bit word) times sc, as hi + lo bf16 pairs: hi =
+// bf16(x sc), lo = bf16(x sc - hi) with the residual from one fused
+// multiply-add.  Written out, so that the chunk-state kernels that must agree
+// bit for bit (chunk_outer_bf16_kernel<., 0>, chunk_state_pass_kernel) do
+// not depend on where the compiler contracts a multiply and a subtract.
+__device__ __forceinline__ void split_scaled(uint32_t v, float sc, uint32_t& hi, uint32_t& lo) {
+  const float x0 = bf16lo_to_f32(v), x1 = bf16hi_to_f32(v);
+  hi = pack_bf16x2(x0 * sc, x1 * sc);
+  lo = pack_bf16x2(__builtin_fmaf(x0, sc, -bf16lo_to_f32(hi)), __builtin_fmaf(x1, sc, -bf16hi_to_f32(hi)));
+}
+
 // ---------------------------------------------------------------------------
 // chunk outer products, bf16 fast path (P and N multiples of 64):
 //   MODE 0: states[p][n] = sum_t u[t,p] w_t B[t,n],  w_t = e^{min(dc_last - dc_t, 0)} dt_t
@@ -227,7 +238,9 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
     // scale of row t of the held tile from its dc, dt (0 past klim)
     auto row_scale = [&](int t, float dcv, float dtv) __attribute__((always_inline)) {
       float sc;
-      if constexpr (MODE == 0) sc = fast_exp2(fminf(dcl - dcv * kLog2e, 0.f)) * dtv;
+      // (the fused multiply-add written out: chunk_state_pass_kernel forms the
+      // same argument, and the two must agree bit for bit)
+      if constexpr (MODE == 0) sc = fast_exp2(fminf(__builtin_fmaf(dcv, -kLog2e, dcl), 0.f)) * dtv;
       else sc = fast_exp2(dcv * kLog2e);
       return t < klim ? sc : 0.f;
     };
@@ -269,11 +282,7 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
           const uint32_t q[4] = {pa0[i].x, pa0[i].y, pa0[i].z, pa0[i].w};
           uint32_t r[4], rl[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float v0 = bf16lo_to_f32(q[j]) * sc, v1 = bf16hi_to_f32(q[j]) * sc;
-            r[j] = pack_bf16x2(v0, v1);
-            rl[j] = pack_bf16x2(v0 - bf16lo_to_f32(r[j]), v1 - bf16hi_to_f32(r[j]));
-          }
+          for (int j = 0; j < 4; ++j) split_scaled(q[j], sc, r[j], rl[j]);
           const int ao = TA::off(row, 8 * (e & 7));
           *reinterpret_cast<uint4*>(As + ao) = uint4{r[0], r[1], r[2], r[3]};
           *reinterpret_cast<uint4*>(As + PLA + ao) = uint4{rl[0], rl[1], rl[2], rl[3]};
@@ -378,34 +387,45 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
 //   S_c[p][n] = sum_t u[t,p] w_t B[t,n],  w_t = e^{min(dc_last - dc_t, 0)} dt_t
 //   states[c] = H_c,  H_{c+1} = e^{dc_last(c)} H_c + S_c,  H_0 = h_init or 0,
 //   h_last = H_nc
-// One block per (b, head, 64-wide p tile, 64-wide n block), 4 waves: wave w
-// accumulates S_c^T[n][p] for the block's n columns 16 w .. 16 w + 15 and its
-// 64 p, and holds H_c in the same fragment layout (lane: n = n0 + 16 w +
-// 4 lg + r, p = p0 + 16 pt + li).  The block walks every 64-token t tile of
-// every chunk in order, so the chunk states never leave the chip.
+// One block per (b, head, 64-wide p tile, 64 NB-wide n block), 4 NB waves:
+// wave w accumulates S_c^T[n][p] for the block's n columns 16 w .. 16 w + 15
+// and its 64 p, and holds H_c in the same fragment layout (lane: n = n0 +
+// 16 w + 4 lg + r, p = p0 + 16 pt + li).  The block walks every 64-token t
+// tile of every chunk in order, so the chunk states never leave the chip.
+// With NB = 2 (state_dim a multiple of 128) one 512-thread block covers 128
+// n: each u tile is brought in and split once for both halves, half the
+// split work per thread (one block per CU instead of two of 64 n).
 // A tile's raw u and B rows and its dc, dt go from HBM straight into one of
-// three LDS stages (global_load_lds, issued three tiles ahead and waited for
-// with explicit counts).  Step g runs tile g's MFMAs (w u as hi + lo planes,
+// NS LDS stages (global_load_lds, issued NS tiles ahead and waited for with
+// explicit counts; three stages at NB = 1, four at NB = 2).  Step g runs tile g's MFMAs (w u as hi + lo planes,
 // B from the stage) while the waves scale tile g + 1's u by w_t and split it
 // into its planes in place (w u is fp32), so that the split's latency does
 // not sit between a tile's arrival and its MFMAs.  The products and their
 // order are chunk_outer_bf16_kernel<., 0>'s and the update is
 // state_passing_fwd_kernel's.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
+template <int NB>
+__global__ __launch_bounds__(256 * NB, 2 / NB) void chunk_state_pass_kernel(
     const bf16* __restrict__ u, const bf16* __restrict__ Bm, const float* __restrict__ dt,
     const float* __restrict__ dc, const float* __restrict__ h_init, float* __restrict__ states,
     float* __restrict__ h_last, SsdDims d) {
-  using TL = LdsTile<64>;
-  constexpr int PL = 64 * TL::kLd;            // bf16 per 64 x 64 tile
-  constexpr int NS = 3;                        // DMA stages
-  constexpr int kDma = 5;                      // DMA instructions per wave per tile
+  using TL = LdsTile<64>;                      // u tile and its planes
+  using TB = LdsTile<64 * NB>;                 // B tile: 64 rows of the block's 64 NB n
+  constexpr int NT = 256 * NB;                 // threads
+  constexpr int NW = 4 * NB;                   // waves
+  constexpr int PL = 64 * TL::kLd;             // bf16 per 64 x 64 plane
+  constexpr int XL = 64 * TB::kLd;             // bf16 of the B tile
+  constexpr int NS = NB == 2 ? 4 : 3;          // DMA stages (four fit beside one 512-thread block)
+  constexpr int UI = 2 / NB;                   // u DMA instructions per wave per tile
+  constexpr int BI = 2;                        // B DMA instructions per wave per tile
+  constexpr int kDma = UI + BI + 1;            // DMA instructions per wave per tile
   // stage (bf16): u tile, then its hi plane in place; lo plane (+PL); B tile
-  // (+2 PL); 4 x 64 fp32 row values (+3 PL): dc, dt, the chunk's last dc
-  constexpr int kStage = 3 * PL + 4 * 128;
+  // (+2 PL); NW x 64 fp32 row values (+2 PL + XL): dc, dt, 64 copies of the
+  // chunk's last dc, spare copies of dt
+  constexpr int kStage = 2 * PL + XL + NW * 128;
   __shared__ __align__(16) bf16 stg[NS * kStage];
 
-  const int ptiles = d.P / 64, nblk = d.N / 64;
+  const int ptiles = d.P / 64, nblk = d.N / (64 * NB);
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
   int rest = bid;
   const int nb = rest % nblk;
@@ -414,7 +434,7 @@ __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
   rest /= ptiles;
   const int h = rest % d.H;
   const int b = rest / d.H;
-  const int p0 = 64 * pti, n0 = 64 * nb;
+  const int p0 = 64 * pti, n0 = 64 * NB * nb;
   const int g = h / (d.H / d.G);
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -458,36 +478,45 @@ __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
 
   // per-lane LDS element offsets, the same in every stage: transposed reads
   // of the planes (rows 8 lg + (li / 4) and + 4 of k step 0, columns 16 pt +
-  // 4 (li % 4); k step 1 is 32 rows = 2048 elements on) and of B (columns
-  // 16 w + 4 (li % 4)), and the two u chunks this thread splits
-  int o_b[4][2], o_x[2], ao[2];
+  // 4 (li % 4); k step 1 is 32 rows on) and of B (columns 16 w + 4 (li %
+  // 4)), and the u chunks this thread splits
+  int o_b[4][2], o_x[2], ao[UI];
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) o_b[pt][hh] = TL::off(8 * lg + 4 * hh + (li >> 2), 16 * pt + 4 * (li & 3));
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) o_x[hh] = TL::off(8 * lg + 4 * hh + (li >> 2), 16 * w + 4 * (li & 3));
+  for (int hh = 0; hh < 2; ++hh) o_x[hh] = TB::off(8 * lg + 4 * hh + (li >> 2), 16 * w + 4 * (li & 3));
 #pragma unroll
-  for (int i = 0; i < 2; ++i) ao[i] = TL::off((tid + 256 * i) >> 3, 8 * ((tid + 256 * i) & 7));
+  for (int i = 0; i < UI; ++i) ao[i] = TL::off((tid + NT * i) >> 3, 8 * ((tid + NT * i) & 7));
 
-  // DMA instruction i (0, 1) of this wave fills tile bytes 1024 (2 w + i) +
-  // 16 lane: row pos / 8 with pos = 64 (2 w + i) + lane, stored chunk pos %
-  // 8, which holds logical chunk (pos % 8) ^ swz_r128(row) (the LdsTile<64>
-  // layout); lane byte offsets of a full tile's u and B rows
-  int drow[2], dcol[2];
-  uint32_t du[2], dx[2];
+  // u DMA instruction i of this wave fills plane bytes 1024 (UI w + i) + 16
+  // lane: row pos / 8 with pos = 64 (UI w + i) + lane, stored chunk pos % 8,
+  // which holds logical chunk (pos % 8) ^ swz_r128(row) (the LdsTile<64>
+  // layout); B instruction i fills tile bytes 1024 (BI w + i) + 16 lane, 8 NB
+  // chunks per row (the LdsTile<64 NB> layout).  Lane byte offsets of a full
+  // tile's u and B rows:
+  int urow[UI], ucol[UI], xrow[BI], xcol[BI];
+  uint32_t du[UI], dx[BI];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int pos = 64 * (2 * w + i) + lane;
-    drow[i] = pos >> 3;
-    dcol[i] = 8 * ((pos & 7) ^ swz_r128(pos >> 3));
-    du[i] = 2u * static_cast<uint32_t>(drow[i] * a_rs + dcol[i]);
-    dx[i] = 2u * static_cast<uint32_t>(drow[i] * x_rs + dcol[i]);
+  for (int i = 0; i < UI; ++i) {
+    const int pos = 64 * (UI * w + i) + lane;
+    urow[i] = pos >> 3;
+    ucol[i] = 8 * ((pos & 7) ^ swz_r128(pos >> 3));
+    du[i] = 2u * static_cast<uint32_t>(urow[i] * a_rs + ucol[i]);
   }
-  const uint32_t lds_st = lds_addr(stg), lds_wave = static_cast<uint32_t>(2 * w) << 10;
-  // tile x into stage st: 2 + 2 sixteen-byte and 1 four-byte DMA per wave
+#pragma unroll
+  for (int i = 0; i < BI; ++i) {
+    const int pos = 64 * (BI * w + i) + lane;
+    constexpr int RC = 8 * NB;   // 16-byte chunks per B row
+    xrow[i] = pos / RC;
+    xcol[i] = 8 * ((pos % RC) ^ (NB == 1 ? swz_r128(pos / RC) : swz_r256(pos / RC)));
+    dx[i] = 2u * static_cast<uint32_t>(xrow[i] * x_rs + xcol[i]);
+  }
+  const uint32_t lds_st = lds_addr(stg);
+  // tile x into stage st: UI + BI sixteen-byte and 1 four-byte DMA per wave
   // (wave 0 brings the tile's dc, wave 1 its dt, wave 2 64 copies of the
-  // chunk's last dc, wave 3 a spare copy of dt, so that every wave counts
+  // chunk's last dc, the others spare copies of dt, so that every wave counts
   // the same number per tile).  Rows past the chunk repeat its last (their
   // scale is 0).
   auto issue = [&](const Walk& x, int st) __attribute__((always_inline)) {
@@ -497,51 +526,50 @@ __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
     const bf16* xb = Bm + tok * x_rs + static_cast<long>(g) * d.N + n0;
     const uint32_t base = lds_st + static_cast<uint32_t>(st * kStage * 2);   // bytes
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      uint32_t ou = du[i], ox = dx[i];
-      if (qv < 64) {
-        const int r = min(drow[i], qv - 1);
-        ou = 2u * static_cast<uint32_t>(r * a_rs + dcol[i]);
-        ox = 2u * static_cast<uint32_t>(r * x_rs + dcol[i]);
-      }
-      dma_lds16(ub, ou, base + lds_wave + (i << 10));
-      dma_lds16(xb, ox, base + 4 * PL + lds_wave + (i << 10));
+    for (int i = 0; i < UI; ++i) {
+      uint32_t ou = du[i];
+      if (qv < 64) ou = 2u * static_cast<uint32_t>(min(urow[i], qv - 1) * a_rs + ucol[i]);
+      dma_lds16(ub, ou, base + (static_cast<uint32_t>(UI * w + i) << 10));
+    }
+#pragma unroll
+    for (int i = 0; i < BI; ++i) {
+      uint32_t ox = dx[i];
+      if (qv < 64) ox = 2u * static_cast<uint32_t>(min(xrow[i], qv - 1) * x_rs + xcol[i]);
+      dma_lds16(xb, ox, base + 4 * PL + (static_cast<uint32_t>(BI * w + i) << 10));
     }
     const long crow = (bh * d.nc + x.c) * d.Lc;
-    const float* rv = w == 2 ? dc + crow + d.Lc - 1 : ((w & 1) ? dt : dc) + crow + t0;
+    const float* rv = w == 2 ? dc + crow + d.Lc - 1 : ((w == 0) ? dc : dt) + crow + t0;
     const uint32_t ro = w == 2 ? 0u : 4u * static_cast<uint32_t>(min(lane, qv - 1));
-    dma_lds4(rv, ro, base + 6 * PL + 256 * w);
+    dma_lds4(rv, ro, base + 4 * PL + 2 * XL + 256 * w);
   };
   // tile x's u in stage ST -> (w u) hi plane in place, lo plane at +PL
   auto split = [&](const Walk& x, auto stc) __attribute__((always_inline)) {
     bf16* sb = stg + decltype(stc)::value * kStage;
     const int qv = rows_of(x);
-    const float* rdc = reinterpret_cast<const float*>(sb + 3 * PL);
+    const float* rdc = reinterpret_cast<const float*>(sb + 2 * PL + XL);
     const float* rdt = rdc + 64;
     const float dcl = rdc[128] * kLog2e;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int row = (tid + 256 * i) >> 3;
+    for (int i = 0; i < UI; ++i) {
+      const int row = (tid + NT * i) >> 3;
       const uint4 q = *reinterpret_cast<const uint4*>(sb + ao[i]);
       // rows past the chunk hold copies of its last row (finite): the scale is
       // computed in every lane and masked by a select, not a branch
-      float sc = fast_exp2(fminf(dcl - rdc[row] * kLog2e, 0.f)) * rdt[row];
+      // (the argument's fused multiply-add written out, as chunk_outer_bf16_kernel
+      // forms it: where the compiler contracts would otherwise differ)
+      float sc = fast_exp2(fminf(__builtin_fmaf(rdc[row], -kLog2e, dcl), 0.f)) * rdt[row];
       asm volatile("" : "+v"(sc));
       sc = row < qv ? sc : 0.f;
       const uint32_t v[4] = {q.x, q.y, q.z, q.w};
       uint32_t r[4], rl[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float v0 = bf16lo_to_f32(v[j]) * sc, v1 = bf16hi_to_f32(v[j]) * sc;
-        r[j] = pack_bf16x2(v0, v1);
-        rl[j] = pack_bf16x2(v0 - bf16lo_to_f32(r[j]), v1 - bf16hi_to_f32(r[j]));
-      }
+      for (int j = 0; j < 4; ++j) split_scaled(v[j], sc, r[j], rl[j]);
       *reinterpret_cast<uint4*>(sb + ao[i]) = uint4{r[0], r[1], r[2], r[3]};
       *reinterpret_cast<uint4*>(sb + PL + ao[i]) = uint4{rl[0], rl[1], rl[2], rl[3]};
     }
   };
 
-  // prologue: tiles 0, 1, 2 (the last again past the end) into stages 0..2
+  // prologue: tiles 0 .. NS - 1 (the last again past the end) into stages 0 .. NS - 1
   Walk wi{0, 0, d.nc == 1 ? ntt_last : tpc};
   int gi = 0;   // tile index of wi
   auto adv_issue = [&]() __attribute__((always_inline)) {
@@ -550,14 +578,13 @@ __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
       ++gi;
     }
   };
-  issue(wi, 0);
-  adv_issue();
-  issue(wi, 1);
-  adv_issue();
-  issue(wi, 2);
-  adv_issue();
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    issue(wi, st);
+    adv_issue();
+  }
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(vm_wait<2 * kDma>());
+  __builtin_amdgcn_s_waitcnt(vm_wait<(NS - 1) * kDma>());
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   Walk wc{0, 0, d.nc == 1 ? ntt_last : tpc};   // the tile computed
@@ -570,11 +597,12 @@ __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
   auto step = [&](auto stc) __attribute__((always_inline)) {
     constexpr int ST = decltype(stc)::value;
     const bf16* sb = stg + ST * kStage;
-    // tile gt + 1 has landed (tile gt + 2, and the state stores of the step
-    // before, may still be in flight); tile gt's planes are visible
+    // tile gt + 1 has landed (tiles gt + 2 .. gt + NS - 1, and the state
+    // stores of the step before, may still be in flight); tile gt's planes
+    // are visible
     asm volatile("" ::: "memory");
-    if (stored) __builtin_amdgcn_s_waitcnt(vm_wait<kDma + 4>());
-    else __builtin_amdgcn_s_waitcnt(vm_wait<kDma>());
+    if (stored) __builtin_amdgcn_s_waitcnt(vm_wait<(NS - 2) * kDma + 4>());
+    else __builtin_amdgcn_s_waitcnt(vm_wait<(NS - 2) * kDma>());
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     stored = wc.tt == 0;
@@ -591,8 +619,8 @@ __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
       for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
         for (int pl = 0; pl < 2; ++pl)
-          bop[pt][pl] = tile_tr8_at(sb + pl * PL + 2048 * ks, o_b[pt][0], o_b[pt][1]);
-      const v8bf a = tile_tr8_at(sb + 2 * PL + 2048 * ks, o_x[0], o_x[1]);
+          bop[pt][pl] = tile_tr8_at(sb + pl * PL + 32 * TL::kLd * ks, o_b[pt][0], o_b[pt][1]);
+      const v8bf a = tile_tr8_at(sb + 2 * PL + 32 * TB::kLd * ks, o_x[0], o_x[1]);
 #pragma unroll
       for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
@@ -600,7 +628,7 @@ __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
     }
     if (gt + 1 < ntiles) split(wsp, std::integral_constant<int, (ST + 1) % NS>{});
     if (wc.tt == wc.ntt - 1) {   // the chunk's last tile: pass the state on
-      const float sc = expf(reinterpret_cast<const float*>(sb + 3 * PL)[128]);
+      const float sc = expf(reinterpret_cast<const float*>(sb + 2 * PL + XL)[128]);
 #pragma unroll
       for (int pt = 0; pt < 4; ++pt) {
 #pragma unroll
@@ -624,6 +652,10 @@ __global__ __launch_bounds__(256, 2) void chunk_state_pass_kernel(
     step(std::integral_constant<int, 1>{});
     if (gt >= ntiles) break;
     step(std::integral_constant<int, 2>{});
+    if constexpr (NS == 4) {
+      if (gt >= ntiles) break;
+      step(std::integral_constant<int, 3 % NS>{});
+    }
   }
   // drain the surplus DMA before the block ends
   __builtin_amdgcn_s_waitcnt(vm_wait<0>());
@@ -1259,21 +1291,35 @@ int device_cus() {
 // 108 us against 127 for the two kernels); with fewer, longer walks it
 // loses (config 4's SSM shape, 256 blocks of 128 tiles: 154 against ~127 us;
 // the reference default, 128 blocks: 80 us).
+// n blocks of 128 (one 512-thread block per CU) where state_dim allows,
+// else of 64 (two 256-thread blocks per CU); 0: the fused kernel does not fit
+static int chunk_state_pass_nb(const SsdDims& d) {
+  if (d.P % 64 != 0 || d.N % 64 != 0) return 0;
+  const long bhp = static_cast<long>(d.b) * d.H * (d.P / 64);
+  if (d.N % 128 == 0 && bhp * (d.N / 128) >= device_cus()) return 2;
+  if (bhp * (d.N / 64) >= 2L * device_cus()) return 1;
+  return 0;
+}
 bool chunk_state_pass_ok(const SsdDims& d, const void* u, const void* B, const float* h_init,
                          const float* states, const float* h_last) {
-  const long blocks = static_cast<long>(d.b) * d.H * (d.P / 64) * (d.N / 64);
-  return d.P % 64 == 0 && d.N % 64 == 0 && aligned16(u) && aligned16(B) &&
-         (!h_init || aligned16(h_init)) && aligned16(states) && aligned16(h_last) &&
-         blocks >= 2L * device_cus();
+  return chunk_state_pass_nb(d) > 0 && aligned16(u) && aligned16(B) &&
+         (!h_init || aligned16(h_init)) && aligned16(states) && aligned16(h_last);
 }
 int launch_chunk_state_pass(const void* u, const void* B, const float* dt, const float* dc,
                             const float* h_init, float* states, float* h_last, const SsdDims& d,
                             hipStream_t s) {
-  const long blocks = static_cast<long>(d.b) * d.H * (d.P / 64) * (d.N / 64);
+  const int nb = chunk_state_pass_nb(d);
+  SA_CHECK_ARG(nb > 0, "chunk_state_pass: shape not covered");
+  const long blocks = static_cast<long>(d.b) * d.H * (d.P / 64) * (d.N / (64 * nb));
   ProfScope prof_("chunk_state_pass_fwd", s);
-  hipLaunchKernelGGL(chunk_state_pass_kernel, dim3(blocks), dim3(256), 0, s,
-                     static_cast<const bf16*>(u), static_cast<const bf16*>(B), dt, dc, h_init,
-                     states, h_last, d);
+  if (nb == 2)
+    hipLaunchKernelGGL(chunk_state_pass_kernel<2>, dim3(blocks), dim3(512), 0, s,
+                       static_cast<const bf16*>(u), static_cast<const bf16*>(B), dt, dc, h_init,
+                       states, h_last, d);
+  else
+    hipLaunchKernelGGL(chunk_state_pass_kernel<1>, dim3(blocks), dim3(256), 0, s,
+                       static_cast<const bf16*>(u), static_cast<const bf16*>(B), dt, dc, h_init,
+                       states, h_last, d);
   SA_CHECK_LAUNCH("chunk_state_pass");
   return 0;
 }
