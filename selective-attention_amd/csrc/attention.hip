@@ -191,7 +191,10 @@ __global__ __launch_bounds__(256, (attn_blocks_per_cu<D, MODE, SEL>())) void spa
   // grid_qblk >= the query blocks of the packing: surplus ids find no sequence
   // and exit; a query block past the rows of block_idx has no selection
   const int h = lid / grid_qblk;
-  const int gq = lid - h * grid_qblk;
+  // a head's query blocks from the last to the first: in causal modes a
+  // block's work grows with its position in the sequence, so the longest
+  // go first and each launch round ends on short ones
+  const int gq = grid_qblk - 1 - (lid - h * grid_qblk);
   const int tid = threadIdx.x, lane = tid & 63;
   // locate the query block's sequence (q blocks are numbered sequence by
   // sequence): 64 sequences per step, one per lane, a prefix sum of their

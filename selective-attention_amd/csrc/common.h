@@ -355,6 +355,25 @@ __device__ __forceinline__ int xcd_swizzle(int bid, int nblocks) {
   return xcd * per + slot;
 }
 
+// Block order for launches whose blocks come in groups of nk with unequal
+// work (member k of a group walks nk - k tiles, say).  Blocks that share an
+// XCD (consecutive ids after xcd_swizzle) are taken in windows of one XCD's
+// resident blocks (32 CUs x 2 blocks = 64 on MI355X): a window holds
+// max(1, 64 / nk) whole groups and issues member 0 of each of its groups
+// first, then member 1, and so on.  Each resident round then ends on the
+// short members, and a group's members still run within one window of each
+// other (what they share stays in L2).  bid in [0, nblocks), nblocks a
+// multiple of nk; returns the member k and the group index.
+__device__ __forceinline__ void xcd_window_order(int bid, int nblocks, int nk, int& k, int& grp) {
+  constexpr int kResidentPerXcd = 64;
+  const int wg = max(1, kResidentPerXcd / nk);        // groups per window
+  const int ngrp = nblocks / nk;
+  const int win = bid / (wg * nk), inw = bid - win * (wg * nk);
+  const int wsz = min(wg, ngrp - win * wg);           // the last window may be short
+  k = inw / wsz;
+  grp = win * wg + (inw - k * wsz);
+}
+
 }  // namespace sa
 
 // host-side error plumbing shared by every entry point (defined in abi.cpp)

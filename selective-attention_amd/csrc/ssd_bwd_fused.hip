@@ -296,8 +296,12 @@ __global__ __launch_bounds__(256, 2) void ssd_bwd_src_kernel(
   const int npass = (hpg + HS - 1) / HS;
   const int stiles = d.Lc / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int S = bid % stiles;
-  int rest = bid / stiles;
+  // strip S walks stiles - S target strips: longest first in each window of
+  // one XCD's resident blocks, so that launch rounds end on short blocks
+  // while a tile's strips still run close together in time (its dy and C
+  // tiles are read by every strip from L2)
+  int S, rest;
+  xcd_window_order(bid, gridDim.x, stiles, S, rest);
   const int g = rest % d.G;
   rest /= d.G;
   const int c = rest % d.nc;

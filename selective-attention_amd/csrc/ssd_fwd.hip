@@ -888,8 +888,11 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_fwd_bf16_kernel(
   const int ttiles = (d.Lc + 63) / 64, ptiles = (d.P + 63) / 64;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
   int rest = bid;
-  const int ti = rest % ttiles;
-  rest /= ttiles;
+  // tau tile ti walks ti + 1 sigma tiles: longest first in each window of one
+  // XCD's resident blocks (the launch rounds end on short blocks)
+  int ti;
+  xcd_window_order(bid, gridDim.x, ttiles, ti, rest);
+  ti = ttiles - 1 - ti;
   const int pti = rest % ptiles;
   rest /= ptiles;
   const int hc = rest % nhc;

@@ -71,9 +71,9 @@ def test_ssd_bwd_parity(dtype, name, shape, chunk):
     check(make_inputs(dtype=dtype, **shape), chunk, dtype)
 
 
-# bf16, headdim 64, state_dim 128, chunk a multiple of 64 (any number of heads
-# per group): the fused source / target kernels; the N = 64 cases and the
-# p128_n192 case run the generic kernels
+# bf16, headdim 64, state_dim 64 or 128, chunk a multiple of 64 (any number of
+# heads per group): the fused source / target kernels; the p128_n192 case
+# (headdim 128) runs the generic kernels
 FUSED_CASES = [
     ("hpg1_lens", dict(b=2, L=192, H=2, P=64, N=128, G=2, lens=[192, 77]), 64),
     ("hpg3_ragged_n64", dict(b=1, L=200, H=3, P=64, N=64, G=1, lens=[171]), 128),
