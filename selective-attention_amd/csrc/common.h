@@ -363,9 +363,10 @@ __device__ __forceinline__ int xcd_swizzle(int bid, int nblocks) {
 // first, then member 1, and so on.  Each resident round then ends on the
 // short members, and a group's members still run within one window of each
 // other (what they share stays in L2).  bid in [0, nblocks), nblocks a
-// multiple of nk; returns the member k and the group index.
+// multiple of nk; returns the member k and the group index.  Kernels that
+// run three blocks per CU pass their own resident count.
+template <int kResidentPerXcd = 64>
 __device__ __forceinline__ void xcd_window_order(int bid, int nblocks, int nk, int& k, int& grp) {
-  constexpr int kResidentPerXcd = 64;
   const int wg = max(1, kResidentPerXcd / nk);        // groups per window
   const int ngrp = nblocks / nk;
   const int win = bid / (wg * nk), inw = bid - win * (wg * nk);

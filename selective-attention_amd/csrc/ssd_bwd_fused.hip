@@ -898,8 +898,12 @@ __global__ __launch_bounds__(256, 3) void ssd_bwd_tgt_kernel(
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
   const int half = NHALF == 2 ? (bid & 1) : 0;
   int rest = NHALF == 2 ? (bid >> 1) : bid;
-  const int T = rest % ttiles;
-  rest /= ttiles;
+  // target strip T walks T + 1 source strips: longest first in windows of one
+  // XCD's resident blocks (three per CU, the two halves of a tile adjacent:
+  // 48 tile pairs)
+  int T;
+  xcd_window_order<48>(rest, gridDim.x / NHALF, ttiles, T, rest);
+  T = ttiles - 1 - T;
   const int g = rest % d.G;
   rest /= d.G;
   const int c = rest % d.nc;
