@@ -104,6 +104,11 @@ FUSED_CASES = [
     # one head per group at chunk 256: single-head source launches over
     # every start strip S (odd ones included) and up to four target strips
     ("hpg1_c256", dict(b=2, L=512, H=2, P=64, N=128, G=2, lens=[512, 333]), 256),
+    # 75 (b, chunk, group) groups at chunk 256: the longest-first block order
+    # runs several full windows of one XCD's resident blocks and a partial
+    # last one (source kernel and chunk scan 16 groups per window, target
+    # kernel 12), with the last chunk 76 rows long
+    ("windows_partial", dict(b=3, L=1100, H=10, P=64, N=128, G=5, lens=[1100, 700, 1033]), 256),
     # two P tiles, three N slices: bf16 chunk-state / dH_intra kernels, generic column / row kernels
     ("p128_n192", dict(b=2, L=600, H=2, P=128, N=192, G=1, lens=[600, 389]), 256),
 ]

@@ -223,6 +223,9 @@ FAST_CASES = [
     ("p128_n192_c256", dict(b=2, L=600, H=2, P=128, N=192, G=1, lens=[600, 517]), 256),
     # state_dim 256: two heads per block, the second head chunk partial
     ("n256_hpg3", dict(b=1, L=160, H=3, P=64, N=256, G=1, lens=[150]), 64),
+    # 75 groups of four tau tiles: the longest-first block order over several
+    # full windows of one XCD's resident blocks and a partial last one
+    ("windows_partial", dict(b=3, L=1100, H=10, P=64, N=128, G=5, lens=[1100, 700, 1033]), 256),
 ]
 
 
