@@ -292,6 +292,11 @@ constexpr int vm_wait() {
   return (N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14);
 }
 constexpr int kLgkmWait0 = 0xF | (7 << 4) | (3 << 14);   // lgkmcnt(0) only
+// vmcnt(N) and lgkmcnt(0): the wave's LDS accesses are complete as well
+template <int N>
+constexpr int vm_lgkm_wait() {
+  return (N & 15) | (7 << 4) | ((N >> 4) << 14);
+}
 
 // key (within a 64-key tile) held by MFMA row c of score tile kt
 __device__ __forceinline__ int key_of_row(int kt, int c) {

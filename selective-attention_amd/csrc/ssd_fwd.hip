@@ -396,8 +396,10 @@ __global__ __launch_bounds__(256, 3) void chunk_outer_bf16_kernel(
 // n: each u tile is brought in and split once for both halves, half the
 // split work per thread (one block per CU instead of two of 64 n).
 // A tile's raw u and B rows and its dc, dt go from HBM straight into one of
-// NS LDS stages (global_load_lds, issued NS tiles ahead and waited for with
-// explicit counts; three stages at NB = 1, four at NB = 2).  Step g runs tile g's MFMAs (w u as hi + lo planes,
+// NS LDS stages (global_load_lds, issued NS - 1 tiles ahead and waited for
+// with explicit counts; three stages at NB = 1, four at NB = 2).  Step g
+// refills, after its MFMAs, the stage step g - 1 consumed (every wave is past
+// it at step g's barrier), so a step has one barrier.  Step g runs tile g's MFMAs (w u as hi + lo planes,
 // B from the stage) while the waves scale tile g + 1's u by w_t and split it
 // into its planes in place (w u is fp32), so that the split's latency does
 // not sit between a tile's arrival and its MFMAs.  The products and their
@@ -569,7 +571,7 @@ __global__ __launch_bounds__(256 * NB, 2 / NB) void chunk_state_pass_kernel(
     }
   };
 
-  // prologue: tiles 0 .. NS - 1 (the last again past the end) into stages 0 .. NS - 1
+  // prologue: tiles 0 .. NS - 2 (the last again past the end) into stages 0 .. NS - 2
   Walk wi{0, 0, d.nc == 1 ? ntt_last : tpc};
   int gi = 0;   // tile index of wi
   auto adv_issue = [&]() __attribute__((always_inline)) {
@@ -579,12 +581,12 @@ __global__ __launch_bounds__(256 * NB, 2 / NB) void chunk_state_pass_kernel(
     }
   };
 #pragma unroll
-  for (int st = 0; st < NS; ++st) {
+  for (int st = 0; st < NS - 1; ++st) {
     issue(wi, st);
     adv_issue();
   }
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(vm_wait<(NS - 1) * kDma>());
+  __builtin_amdgcn_s_waitcnt(vm_wait<(NS - 2) * kDma>());
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   Walk wc{0, 0, d.nc == 1 ? ntt_last : tpc};   // the tile computed
@@ -597,12 +599,14 @@ __global__ __launch_bounds__(256 * NB, 2 / NB) void chunk_state_pass_kernel(
   auto step = [&](auto stc) __attribute__((always_inline)) {
     constexpr int ST = decltype(stc)::value;
     const bf16* sb = stg + ST * kStage;
-    // tile gt + 1 has landed (tiles gt + 2 .. gt + NS - 1, and the state
-    // stores of the step before, may still be in flight); tile gt's planes
-    // are visible
+    // tile gt + 1 has landed (tiles gt + 2 .. gt + NS - 2 may still be in
+    // flight, and with NS >= 4 the state stores of step gt - 1, which follow
+    // tile gt + 1's DMA; with NS = 3 they precede it); tile gt's planes are
+    // visible: the waits take lgkmcnt(0) too, since this barrier is the
+    // step's only one and follows the split's LDS writes of step gt - 1
     asm volatile("" ::: "memory");
-    if (stored) __builtin_amdgcn_s_waitcnt(vm_wait<(NS - 2) * kDma + 4>());
-    else __builtin_amdgcn_s_waitcnt(vm_wait<(NS - 2) * kDma>());
+    if (NS >= 4 && stored) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait<(NS - 3) * kDma + (NS >= 4 ? 4 : 0)>());
+    else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait<(NS - 3) * kDma>());
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     stored = wc.tt == 0;
@@ -636,11 +640,10 @@ __global__ __launch_bounds__(256 * NB, 2 / NB) void chunk_state_pass_kernel(
         S[pt] = v4f{0.f, 0.f, 0.f, 0.f};
       }
     }
-    // every wave is done with the stage, and tile gt + 1's planes are
-    // written: refill the stage (the last tile again past the end, so that
-    // every step waits the same)
-    __syncthreads();
-    issue(wi, ST);
+    // refill the stage step gt - 1 consumed with tile gt + NS - 1 (the last
+    // tile again past the end, so that every step waits the same): every wave
+    // passed this step's barrier after its last use of that stage
+    issue(wi, (ST + NS - 1) % NS);
     adv_issue();
     adv(wc);
     adv(wsp);
